@@ -1,0 +1,385 @@
+/*
+ * splatx_hip.h — the C ABI of the MI355X (gfx950) backend for the splatx 3DGS training step.
+ *
+ * Pure C (C99, POD structs, int32 status codes) so that a Swift module map, a C++ adapter, or
+ * Python ctypes can bind it directly. Every entry point replaces one virtual op of the reference
+ * operator boundary `splatx::KernelBackend`
+ * (Sources/SplatXCore/include/splatx/KernelBackend.h:396-509) or one method of the resident
+ * `splatx::TrainStepExecutor` (KernelBackend.h:386-392). Struct fields keep the reference field
+ * names (which are the gsplat kernel argument names) and their meaning.
+ *
+ * Ownership (mirrors KernelBackend.h): inputs are borrowed host pointers valid for the duration of
+ * the call; outputs are caller-allocated host buffers of the documented sizes. Ops that are
+ * in-place in the reference (fused_adam, mcmc_perturb_positions) are in-place here.
+ * Calls are blocking and not thread-safe per backend (KernelBackend.h threading contract:
+ * one backend per process, calls commit and wait).
+ *
+ * Errors: every function returns SXH_OK or an error code; the message of the last failing call on
+ * the calling thread is available from sxh_last_error(). The codes map onto the reference's
+ * exception types (Validate.h:23 std::invalid_argument; MetalBackend.cpp:52-54 std::runtime_error).
+ */
+#ifndef SPLATX_HIP_H
+#define SPLATX_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SXH_ABI_VERSION 1
+
+/* Status codes. */
+enum {
+    SXH_OK = 0,
+    SXH_ERR_INVALID_ARGUMENT = 1, /* reference: std::invalid_argument (Validate.h:23) */
+    SXH_ERR_RUNTIME = 2,          /* reference: std::runtime_error (device, allocation, unsupported camera) */
+    SXH_ERR_CAPACITY = 3          /* output capacity too small: required size is reported, nothing written */
+};
+
+/* ------------------------------------------------------------------------------------------ */
+/* Backend lifetime                                                                           */
+/* ------------------------------------------------------------------------------------------ */
+
+typedef struct sxh_backend sxh_backend;
+
+/* Replaces make_metal_backend(void* device, const MetalBackendDesc&) (MetalBackend.h:38-57).
+ * device_ordinal selects the HIP device. */
+int32_t sxh_backend_create(int32_t device_ordinal, sxh_backend** out);
+void sxh_backend_destroy(sxh_backend* b);
+/* Replaces KernelBackend::name() (KernelBackend.h:399). */
+const char* sxh_backend_name(const sxh_backend* b);
+/* Message of the last failing call on this thread ("" if none). */
+const char* sxh_last_error(void);
+int32_t sxh_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------ */
+/* fused_adam — KernelBackend::fused_adam (KernelBackend.h:404), AdamInputs (:18-27)          */
+/* In place, no bias correction, eps outside sqrt(v), valid[g]==0 skips param and moments.    */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    float* param;           /* [n_elems] in/out */
+    const float* grad;      /* [n_elems] */
+    float* exp_avg;         /* [n_elems] in/out */
+    float* exp_avg_sq;      /* [n_elems] in/out */
+    const uint8_t* valid;   /* [n_gauss] 0/1, may be NULL */
+    int64_t n_elems;        /* N*D */
+    int64_t n_gauss;        /* N */
+    float lr, b1, b2, eps;
+} sxh_adam_inputs;
+int32_t sxh_fused_adam(sxh_backend* b, const sxh_adam_inputs* in);
+
+/* ------------------------------------------------------------------------------------------ */
+/* projection_fused_fwd / _bwd — KernelBackend.h:407-413, ProjectionFusedInputs (:31-45),      */
+/* ProjectionFusedOutputs (:47-54), ProjectionFusedGradsIn (:57-66), ProjectionFusedGrads      */
+/* (:68-74). PINHOLE only (camera_model must be 0; anything else is SXH_ERR_RUNTIME, as the    */
+/* reference's runtime_error at Validate.h:51-55).                                            */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    const float* means;      /* [N,3] world */
+    const float* covars;     /* [N,6] triu (c00,c01,c02,c11,c12,c22); NULL selects quats+scales */
+    const float* quats;      /* [N,4] (w,x,y,z), unnormalized */
+    const float* scales;     /* [N,3] linear */
+    const float* opacities;  /* [N] post-sigmoid, may be NULL (fwd only: opacity-aware radius) */
+    const float* viewmats;   /* [C,16] world->cam row-major */
+    const float* Ks;         /* [C,9] row-major */
+    int64_t N, C;
+    int32_t width, height;
+    float eps2d, near_plane, far_plane, radius_clip;
+    uint32_t camera_model;   /* 0 = PINHOLE */
+    uint8_t calc_compensations;
+} sxh_projection_inputs;
+
+/* Caller-allocated. Culled slots: radii = 0, compensations = 0, other outputs unspecified
+ * (this implementation writes 0 there). */
+typedef struct {
+    int32_t* radii;          /* [C,N,2] */
+    float* means2d;          /* [C,N,2] */
+    float* depths;           /* [C,N] */
+    float* conics;           /* [C,N,3] */
+    float* compensations;    /* [C,N], required iff calc_compensations */
+} sxh_projection_outputs;
+
+typedef struct {
+    const int32_t* radii;          /* [C,N,2] fwd output */
+    const float* conics;           /* [C,N,3] fwd output */
+    const float* compensations;    /* [C,N] fwd output, required iff v_compensations != NULL */
+    const float* v_means2d;        /* [C,N,2] */
+    const float* v_depths;         /* [C,N] */
+    const float* v_conics;         /* [C,N,3] */
+    const float* v_compensations;  /* [C,N] or NULL */
+    uint8_t viewmats_grad;
+} sxh_projection_grads_in;
+
+typedef struct {
+    float* v_means;     /* [N,3] */
+    float* v_covars;    /* [N,6]  covars path only (else may be NULL) */
+    float* v_quats;     /* [N,4]  quats/scales path only */
+    float* v_scales;    /* [N,3]  quats/scales path only */
+    float* v_viewmats;  /* [C,16] only when viewmats_grad */
+} sxh_projection_grads;
+
+int32_t sxh_projection_fused_fwd(sxh_backend* b, const sxh_projection_inputs* in,
+                                 sxh_projection_outputs* out);
+int32_t sxh_projection_fused_bwd(sxh_backend* b, const sxh_projection_inputs* in,
+                                 const sxh_projection_grads_in* gin, sxh_projection_grads* out);
+
+/* ------------------------------------------------------------------------------------------ */
+/* sh_fwd / sh_bwd — KernelBackend.h:414-419, ShInputs (:77-86), ShOutputs/ShGrads (:88-95)   */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    const float* dirs;       /* [B*N,3] unnormalized */
+    const float* coeffs;     /* [N,K,D] */
+    const uint8_t* masks;    /* [B*N] 0/1 or NULL; masked elements are left unwritten */
+    uint32_t degrees_to_use; /* 0..4 */
+    int64_t B, N, K;
+    uint32_t D;
+    uint8_t compute_v_dirs;  /* bwd only */
+} sxh_sh_inputs;
+int32_t sxh_sh_fwd(sxh_backend* b, const sxh_sh_inputs* in, float* colors /* [B*N,D] */);
+int32_t sxh_sh_bwd(sxh_backend* b, const sxh_sh_inputs* in, const float* v_colors /* [B*N,D] */,
+                   float* v_coeffs /* [N,K,D] */, float* v_dirs /* [B*N,3] or NULL */);
+
+/* ------------------------------------------------------------------------------------------ */
+/* isect_tiles — KernelBackend.h:420-422, IsectTilesInputs (:106-115), IsectTilesOutputs       */
+/* (:121-128). conics+opacities given -> AccuTile; both NULL -> AABB.                         */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    const float* means2d;    /* [I,N,2] */
+    const int32_t* radii;    /* [I,N,2] */
+    const float* depths;     /* [I,N] */
+    const float* conics;     /* [I,N,3] (AccuTile) or NULL */
+    const float* opacities;  /* [I,N] (AccuTile) or NULL */
+    int64_t I, N;
+    uint32_t tile_size, tile_width, tile_height;
+} sxh_isect_inputs;
+
+typedef struct {
+    int32_t* tiles_per_gauss; /* [I,N] caller-allocated */
+    uint64_t* isect_ids;      /* [capacity] raw emit order */
+    int32_t* flatten_ids;     /* [capacity] */
+    int64_t capacity;         /* in: size of isect_ids/flatten_ids */
+    int64_t n_isects;         /* out (also on SXH_ERR_CAPACITY) */
+    uint32_t tile_n_bits;     /* out */
+    uint32_t image_n_bits;    /* out */
+} sxh_isect_outputs;
+int32_t sxh_isect_tiles(sxh_backend* b, const sxh_isect_inputs* in, sxh_isect_outputs* out);
+
+/* prefix_scan_i64 — KernelBackend.h:428-430: int32 -> inclusive int64 cumsum. */
+int32_t sxh_prefix_scan_i64(sxh_backend* b, const int32_t* in, int64_t n, int64_t* out);
+
+/* sort_isect — KernelBackend.h:435-437, SortIsectInputs (:143-148): stable ascending sort of
+ * (u64 key, i32 value) on key bits [0, key_n_bits). */
+typedef struct {
+    const uint64_t* keys;
+    const int32_t* values;
+    int64_t n;
+    uint32_t key_n_bits;
+} sxh_sort_inputs;
+int32_t sxh_sort_isect(sxh_backend* b, const sxh_sort_inputs* in, uint64_t* keys_sorted,
+                       int32_t* values_sorted);
+
+/* isect_offset_encode — KernelBackend.h:441-443, IsectOffsetInputs (:161-166). */
+typedef struct {
+    const uint64_t* isect_ids; /* [n_isects] sorted */
+    int64_t n_isects;
+    int64_t I;
+    uint32_t tile_width, tile_height;
+} sxh_offset_inputs;
+int32_t sxh_isect_offset_encode(sxh_backend* b, const sxh_offset_inputs* in,
+                                int32_t* offsets /* [I*tile_height*tile_width] */);
+
+/* ------------------------------------------------------------------------------------------ */
+/* rasterize_fwd / _bwd — KernelBackend.h:450-461, RasterizeFwdInputs (:175-188),              */
+/* RasterizeFwdOutputs (:195-199), RasterizeBwdGradsIn (:207-213), RasterizeBwdGrads (:220-226) */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    const float* means2d;         /* [I,N,2] */
+    const float* conics;          /* [I,N,3] */
+    const float* colors;          /* [I,N,3] */
+    const float* opacities;       /* [I,N] */
+    const float* backgrounds;     /* [I,3] or NULL */
+    const uint8_t* masks;         /* [I,TH,TW] or NULL */
+    const int32_t* isect_offsets; /* [I,TH,TW] */
+    const int32_t* flatten_ids;   /* [n_isects] sorted */
+    int64_t I, N, n_isects;
+    uint32_t image_width, image_height;
+    uint32_t tile_size, tile_width, tile_height;
+} sxh_raster_inputs;
+
+typedef struct {
+    float* render_colors;  /* [I,H,W,3] */
+    float* render_alphas;  /* [I,H,W,1] */
+    int32_t* last_ids;     /* [I,H,W] */
+} sxh_raster_outputs;
+
+typedef struct {
+    const float* render_alphas;
+    const int32_t* last_ids;
+    const float* v_render_colors;  /* [I,H,W,3] */
+    const float* v_render_alphas;  /* [I,H,W,1] */
+    uint8_t absgrad;
+} sxh_raster_grads_in;
+
+typedef struct {
+    float* v_means2d;      /* [I,N,2] */
+    float* v_conics;       /* [I,N,3] */
+    float* v_colors;       /* [I,N,3] */
+    float* v_opacities;    /* [I,N] */
+    float* v_means2d_abs;  /* [I,N,2] only when absgrad (else may be NULL) */
+} sxh_raster_grads;
+
+int32_t sxh_rasterize_fwd(sxh_backend* b, const sxh_raster_inputs* in, sxh_raster_outputs* out);
+int32_t sxh_rasterize_bwd(sxh_backend* b, const sxh_raster_inputs* in,
+                          const sxh_raster_grads_in* gin, sxh_raster_grads* out);
+
+/* ------------------------------------------------------------------------------------------ */
+/* RNG — rng_normal_f32 / rng_philox_u32 (KernelBackend.h:466-474), RngNormalInputs (:234-238) */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    uint64_t seed;
+    uint64_t offset;
+    int64_t count;
+} sxh_rng_inputs;
+int32_t sxh_rng_normal_f32(sxh_backend* b, const sxh_rng_inputs* in, float* out /* [count] */);
+int32_t sxh_rng_philox_u32(sxh_backend* b, const sxh_rng_inputs* in, uint32_t* out /* [count] */);
+
+/* ------------------------------------------------------------------------------------------ */
+/* MCMC — mcmc_relocation (KernelBackend.h:478-480, RelocationInputs :246-254) and             */
+/* mcmc_perturb_positions (:483-485, PerturbInputs :265-275).                                 */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    const float* opacities;  /* [N] post-sigmoid */
+    const float* scales;     /* [N,3] linear */
+    const int32_t* ratios;   /* [N] in 1..n_max */
+    const float* binoms;     /* [n_max*n_max] */
+    int64_t N;
+    int32_t n_max;
+    float min_opacity;
+} sxh_relocation_inputs;
+int32_t sxh_mcmc_relocation(sxh_backend* b, const sxh_relocation_inputs* in,
+                            float* new_opacities /* [N] */, float* new_scales /* [N,3] */);
+
+typedef struct {
+    float* positions;              /* [N,3] in/out */
+    const float* quats;            /* [N,4] */
+    const float* scales_log;       /* [N,3] */
+    const float* opacities_logit;  /* [N] */
+    const float* noise;            /* [N,3] */
+    int64_t N;
+    float noise_scale, t, k;
+} sxh_perturb_inputs;
+int32_t sxh_mcmc_perturb_positions(sxh_backend* b, const sxh_perturb_inputs* in);
+
+/* Host helper: make_binoms_lut (CpuKernels.h:166) — out has n_max*n_max floats. */
+int32_t sxh_make_binoms_lut(int32_t n_max, float* out);
+
+/* ------------------------------------------------------------------------------------------ */
+/* SSIM — ssim_fwd / ssim_bwd (KernelBackend.h:491-501), SsimInputs (:283-291),               */
+/* SsimFwdOutputs (:299-305), SsimGradsIn (:313-318). Layout [I,H,W,C], valid padding.        */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct {
+    const float* img1;  /* [I,H,W,C] render */
+    const float* img2;  /* [I,H,W,C] GT */
+    int64_t I, H, W, C;
+    uint8_t need_coeffs;
+} sxh_ssim_inputs;
+
+typedef struct {
+    double ssim;         /* out: mean of the map, f64 sum in ascending index order */
+    float* ssim_map;     /* [I,H-10,W-10,C] */
+    float* coeff_mu;     /* same shape, only when need_coeffs */
+    float* coeff_sigma;
+    float* coeff_cross;
+} sxh_ssim_outputs;
+
+typedef struct {
+    const float* coeff_mu;
+    const float* coeff_sigma;
+    const float* coeff_cross;
+    float v_loss;
+} sxh_ssim_grads_in;
+
+int32_t sxh_ssim_fwd(sxh_backend* b, const sxh_ssim_inputs* in, sxh_ssim_outputs* out);
+int32_t sxh_ssim_bwd(sxh_backend* b, const sxh_ssim_inputs* in, const sxh_ssim_grads_in* gin,
+                     float* v_img1 /* [I,H,W,C] */);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Resident train-step executor — TrainStepExecutor (KernelBackend.h:386-392) created by       */
+/* KernelBackend::make_train_step_executor (:505-508); TrainStepExecutorDesc (:338-346),       */
+/* ResidentParamSync (:354-359), ResidentStepInputs (:361-378), ResidentStepOutputs (:380-384) */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct sxh_executor sxh_executor;
+
+enum { SXH_ISECT_ACCUTILE = 0, SXH_ISECT_AABB = 1 };
+
+typedef struct {
+    int64_t arena_rows;    /* parameter rows (MCMC cap_max) — never reallocated */
+    int32_t sh_degree;     /* 0..3 */
+    float eps2d, near_plane, far_plane, radius_clip;
+    float b1, b2, eps;
+    float ssim_weight;     /* lambda; 0 bypasses SSIM */
+    uint8_t antialiased;
+    uint8_t isect_mode;    /* SXH_ISECT_ACCUTILE (the reference step) or SXH_ISECT_AABB */
+} sxh_exec_desc;
+
+/* Group order: 0 means[3], 1 quats[4], 2 scales[3] (log), 3 opacities[1] (logit), 4 sh0[3],
+ * 5 shN[(K-1)*3] (NULL when sh_degree == 0). */
+typedef struct {
+    float* params[6];
+    float* exp_avg[6];
+    float* exp_avg_sq[6];
+    int64_t rows;
+} sxh_param_sync;
+
+typedef struct {
+    const float* viewmat;     /* [16] world->cam row-major */
+    const float* K;           /* [9] */
+    int32_t width, height;
+    const float* gt_rgb;      /* [H,W,3] host, or NULL when gt_index >= 0 or forward_only */
+    int32_t gt_index;         /* >= 0: use the device-resident GT cache entry (sxh_exec_set_gt_cache) */
+    int64_t count;            /* alive rows <= arena_rows */
+    uint32_t degrees_to_use;
+    float lr[6];
+    float opacity_reg_w, scale_reg_w;
+    uint8_t forward_only;
+    uint8_t inject_noise;
+    uint64_t noise_seed, noise_offset;
+    float noise_scale;
+} sxh_step_inputs;
+
+typedef struct {
+    float loss;              /* 0 when forward_only */
+    int64_t n_isects;        /* the sync-point readback */
+    int64_t n_visible;       /* Gaussians with radii > 0 (device counter) */
+    float* render_colors;    /* in: [H,W,3] host buffer to fill, or NULL for no readback */
+} sxh_step_outputs;
+
+int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor** out);
+void sxh_exec_destroy(sxh_executor* e);
+/* TrainStepExecutor::upload_params / download_params. */
+int32_t sxh_exec_upload(sxh_executor* e, const sxh_param_sync* s);
+int32_t sxh_exec_download(sxh_executor* e, const sxh_param_sync* s);
+/* TrainStepExecutor::step: two host sync points (n_isects, loss). */
+int32_t sxh_exec_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out);
+/* Device-resident GT cache: n_images images of [height,width,3] floats, uploaded once. */
+int32_t sxh_exec_set_gt_cache(sxh_executor* e, const float* images, int32_t n_images,
+                              int32_t width, int32_t height);
+/* Renders the current parameters into GT cache entry `index` (synthetic-target helper). */
+int32_t sxh_exec_render_to_gt_cache(sxh_executor* e, const sxh_step_inputs* in, int32_t index);
+
+/* Per-kernel timing of the last step (HIP events on the executor's stream), enabled by
+ * sxh_exec_set_profiling(e, 1). Names are stable strings; times are milliseconds. */
+typedef struct {
+    int32_t n;
+    const char* names[32];
+    float ms[32];
+} sxh_exec_timing;
+int32_t sxh_exec_set_profiling(sxh_executor* e, int32_t enable);
+int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* SPLATX_HIP_H */

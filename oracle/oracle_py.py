@@ -1,0 +1,140 @@
+"""ctypes access to the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the checker
+or the timed CPU baseline. `Oracle(libm=False)` uses the deterministic transcendental layer shared
+with the device code; `Oracle(libm=True)` uses glibc exactly like the reference CPU code;
+`Reference()` calls the reference's own CpuKernels.cpp built under oracle/_ref (when present).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+sys.path.insert(0, os.path.join(REPO, "splatx-metal_amd", "python"))
+
+import splatx_hip as sh  # noqa: E402  (struct layouts of include/splatx_hip.h)
+
+
+class StepArgs(C.Structure):
+    _fields_ = [("params", sh.fp * 6), ("exp_avg", sh.fp * 6), ("exp_avg_sq", sh.fp * 6),
+                ("count", C.c_int64), ("sh_degree", C.c_int32), ("viewmat", sh.fp), ("K", sh.fp),
+                ("width", C.c_int32), ("height", C.c_int32), ("gt_rgb", sh.fp),
+                ("degrees_to_use", C.c_uint32), ("lr", C.c_float * 6), ("opacity_reg_w", C.c_float),
+                ("scale_reg_w", C.c_float), ("eps2d", C.c_float), ("near_plane", C.c_float),
+                ("far_plane", C.c_float), ("radius_clip", C.c_float), ("b1", C.c_float),
+                ("b2", C.c_float), ("eps", C.c_float), ("ssim_weight", C.c_float),
+                ("antialiased", C.c_uint8), ("isect_mode", C.c_uint8), ("forward_only", C.c_uint8),
+                ("inject_noise", C.c_uint8), ("noise_seed", C.c_uint64), ("noise_offset", C.c_uint64),
+                ("noise_scale", C.c_float), ("loss", C.c_float), ("n_isects", C.c_int64),
+                ("n_visible", C.c_int64), ("render_colors", sh.fp), ("stage_ms", C.c_double * 16)]
+
+
+def lib_path(libm: bool) -> str:
+    return os.path.join(HERE, "liboracle_libm.so" if libm else "liboracle.so")
+
+
+class Oracle(sh.Ops):
+    def __init__(self, libm: bool = False):
+        p = lib_path(libm)
+        if not os.path.exists(p):
+            raise RuntimeError(f"oracle not built: {p}")
+        lib = C.CDLL(p)
+        super().__init__(lib, "sxo_")
+        self.libm = libm
+
+    def make_binoms_lut(self, n_max=51):
+        out = np.zeros(n_max * n_max, np.float32)
+        self._call("make_binoms_lut", n_max, sh.ptr(out))
+        return out
+
+    def quat_scale_to_covar(self, quats, scales):
+        q, s = sh.f32(quats), sh.f32(scales)
+        out = np.zeros((q.shape[0], 3, 3), np.float32)
+        self._call("quat_scale_to_covar", sh.ptr(q), sh.ptr(s), q.shape[0], sh.ptr(out))
+        return out
+
+    def _arr(self, name, x, *extra):
+        x = sh.f32(x)
+        outs = [np.zeros_like(x) for _ in range(2 if name == "sincosf_array" else 1)]
+        f = getattr(self.lib, "sxo_" + name)
+        f.restype = None
+        f(sh.ptr(x), *[sh.ptr(sh.f32(e)) for e in extra], *[sh.ptr(o) for o in outs], C.c_int64(x.size))
+        return outs if len(outs) > 1 else outs[0]
+
+    def logf(self, x):
+        return self._arr("logf_array", x)
+
+    def expf(self, x):
+        return self._arr("expf_array", x)
+
+    def expf_fast(self, x):
+        return self._arr("expf_fast_array", x)
+
+    def powf(self, x, p):
+        return self._arr("powf_array", x, p)
+
+    def sincosf(self, x):
+        return self._arr("sincosf_array", x)
+
+    def train_step(self, params, exp_avg, exp_avg_sq, count, sh_degree, viewmat, K, width, height,
+                   gt_rgb, degrees_to_use, lr, opacity_reg_w=0.0, scale_reg_w=0.0, eps2d=0.3,
+                   near_plane=0.01, far_plane=1e10, radius_clip=0.0, b1=0.9, b2=0.999, eps=1e-15,
+                   ssim_weight=0.2, antialiased=False, isect_mode=sh.SXH_ISECT_ACCUTILE,
+                   forward_only=False, inject_noise=False, noise_seed=0, noise_offset=0,
+                   noise_scale=0.0, want_render=True):
+        a = StepArgs()
+        for g in range(6):
+            a.params[g] = sh.ptr(params[g]) if params[g] is not None and params[g].size else None
+            a.exp_avg[g] = sh.ptr(exp_avg[g]) if exp_avg[g] is not None and exp_avg[g].size else None
+            a.exp_avg_sq[g] = sh.ptr(exp_avg_sq[g]) if exp_avg_sq[g] is not None and exp_avg_sq[g].size else None
+        keep = [sh.f32(viewmat), sh.f32(K), sh.f32(gt_rgb)]
+        render = np.zeros((height, width, 3), np.float32) if want_render else None
+        a.count, a.sh_degree = count, sh_degree
+        a.viewmat, a.K, a.gt_rgb = sh.ptr(keep[0]), sh.ptr(keep[1]), sh.ptr(keep[2])
+        a.width, a.height, a.degrees_to_use = width, height, degrees_to_use
+        for g in range(6):
+            a.lr[g] = lr[g]
+        a.opacity_reg_w, a.scale_reg_w = opacity_reg_w, scale_reg_w
+        a.eps2d, a.near_plane, a.far_plane, a.radius_clip = eps2d, near_plane, far_plane, radius_clip
+        a.b1, a.b2, a.eps, a.ssim_weight = b1, b2, eps, ssim_weight
+        a.antialiased, a.isect_mode = int(bool(antialiased)), isect_mode
+        a.forward_only, a.inject_noise = int(bool(forward_only)), int(bool(inject_noise))
+        a.noise_seed, a.noise_offset, a.noise_scale = noise_seed, noise_offset, noise_scale
+        a.render_colors = sh.ptr(render)
+        self._call("train_step", C.byref(a))
+        stage_fn = self.lib.sxo_stage_name
+        stage_fn.restype = C.c_char_p
+        stages = {stage_fn(i).decode(): a.stage_ms[i] for i in range(16)}
+        return dict(loss=float(a.loss), n_isects=int(a.n_isects), n_visible=int(a.n_visible),
+                    render_colors=render, stage_ms=stages)
+
+
+class Reference(sh.Ops):
+    """The reference's own CPU kernels (oracle/_ref/libsx_ref.so, built from /root/reference)."""
+
+    PATH = os.path.join(HERE, "_ref", "libsx_ref.so")
+
+    def __init__(self):
+        if not os.path.exists(self.PATH):
+            raise RuntimeError("oracle/_ref not built (reference tree absent)")
+        super().__init__(C.CDLL(self.PATH), "sxr_")
+
+    def quat_scale_to_covar(self, quats, scales):
+        q, s = sh.f32(quats), sh.f32(scales)
+        out = np.zeros((q.shape[0], 3, 3), np.float32)
+        self._call("quat_scale_to_covar", sh.ptr(q), sh.ptr(s), q.shape[0], sh.ptr(out))
+        return out
+
+    def make_binoms_lut(self, n_max=51):
+        out = np.zeros(n_max * n_max, np.float32)
+        self._call("make_binoms_lut", n_max, sh.ptr(out))
+        return out
+
+    @staticmethod
+    def available() -> bool:
+        return os.path.exists(Reference.PATH)

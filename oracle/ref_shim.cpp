@@ -1,0 +1,201 @@
+// ref_shim.cpp — C entry points over the reference's own CPU kernels (TEST INFRASTRUCTURE ONLY).
+//
+// Compiled by oracle/Makefile together with Sources/SplatXCore/CpuKernels.cpp and Math.cpp taken
+// in place from the reference tree, into oracle/_ref/libsx_ref.so. It converts the C structs of
+// include/splatx_hip.h to the reference's KernelBackend.h structs and calls the reference's
+// functions unchanged, so tests can cross-check the oracle restatement against the real thing.
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "splatx/CpuKernels.h"
+#include "splatx/KernelBackend.h"
+#include "splatx/Math.h"
+#include "splatx_hip.h"
+
+namespace {
+thread_local std::string g_err;
+struct CapacityError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+template <class F>
+int32_t guarded(F&& f) {
+    try {
+        f();
+        return SXH_OK;
+    } catch (const std::invalid_argument& e) {
+        g_err = e.what();
+        return SXH_ERR_INVALID_ARGUMENT;
+    } catch (const CapacityError& e) {
+        g_err = e.what();
+        return SXH_ERR_CAPACITY;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return SXH_ERR_RUNTIME;
+    }
+}
+template <class T>
+void put(T* dst, const std::vector<T>& v) {
+    if (dst && !v.empty()) std::memcpy(dst, v.data(), v.size() * sizeof(T));
+}
+} // namespace
+
+extern "C" {
+
+const char* sxr_last_error(void) { return g_err.c_str(); }
+
+int32_t sxr_fused_adam(const sxh_adam_inputs* in) {
+    return guarded([&] {
+        splatx::AdamInputs a;
+        a.param = in->param; a.grad = in->grad; a.exp_avg = in->exp_avg;
+        a.exp_avg_sq = in->exp_avg_sq; a.valid = in->valid; a.n_elems = in->n_elems;
+        a.n_gauss = in->n_gauss; a.lr = in->lr; a.b1 = in->b1; a.b2 = in->b2; a.eps = in->eps;
+        splatx::fused_adam_cpu(a);
+    });
+}
+
+int32_t sxr_projection_fused_fwd(const sxh_projection_inputs* in, sxh_projection_outputs* out) {
+    return guarded([&] {
+        splatx::ProjectionFusedInputs p;
+        p.means = in->means; p.covars = in->covars; p.quats = in->quats; p.scales = in->scales;
+        p.opacities = in->opacities; p.viewmats = in->viewmats; p.Ks = in->Ks; p.N = in->N;
+        p.C = in->C; p.width = in->width; p.height = in->height; p.eps2d = in->eps2d;
+        p.near_plane = in->near_plane; p.far_plane = in->far_plane; p.radius_clip = in->radius_clip;
+        p.camera_model = in->camera_model; p.calc_compensations = in->calc_compensations != 0;
+        const splatx::ProjectionFusedOutputs o = splatx::projection_fused_fwd_cpu(p);
+        put(out->radii, o.radii);
+        put(out->means2d, o.means2d);
+        put(out->depths, o.depths);
+        put(out->conics, o.conics);
+        if (in->calc_compensations) put(out->compensations, o.compensations);
+    });
+}
+
+int32_t sxr_sh_fwd(const sxh_sh_inputs* in, float* colors) {
+    return guarded([&] {
+        splatx::ShInputs s;
+        s.dirs = in->dirs; s.coeffs = in->coeffs; s.masks = in->masks;
+        s.degrees_to_use = in->degrees_to_use; s.B = in->B; s.N = in->N; s.K = in->K; s.D = in->D;
+        put(colors, splatx::sh_fwd_cpu(s).colors);
+    });
+}
+
+int32_t sxr_isect_tiles(const sxh_isect_inputs* in, sxh_isect_outputs* out) {
+    return guarded([&] {
+        splatx::IsectTilesInputs i;
+        i.means2d = in->means2d; i.radii = in->radii; i.depths = in->depths; i.conics = in->conics;
+        i.opacities = in->opacities; i.I = in->I; i.N = in->N; i.tile_size = in->tile_size;
+        i.tile_width = in->tile_width; i.tile_height = in->tile_height;
+        const splatx::IsectTilesOutputs o = splatx::isect_tiles_cpu(i);
+        put(out->tiles_per_gauss, o.tiles_per_gauss);
+        out->n_isects = o.n_isects;
+        out->tile_n_bits = o.tile_n_bits;
+        out->image_n_bits = o.image_n_bits;
+        if (out->capacity < o.n_isects) throw CapacityError("capacity too small");
+        put(out->isect_ids, o.isect_ids);
+        put(out->flatten_ids, o.flatten_ids);
+    });
+}
+
+int32_t sxr_sort_isect(const sxh_sort_inputs* in, uint64_t* keys_sorted, int32_t* values_sorted) {
+    return guarded([&] {
+        splatx::SortIsectInputs s;
+        s.keys = in->keys; s.values = in->values; s.n = in->n; s.key_n_bits = in->key_n_bits;
+        const splatx::SortIsectOutputs o = splatx::sort_isect_cpu(s);
+        put(keys_sorted, o.keys_sorted);
+        put(values_sorted, o.values_sorted);
+    });
+}
+
+int32_t sxr_isect_offset_encode(const sxh_offset_inputs* in, int32_t* offsets) {
+    return guarded([&] {
+        splatx::IsectOffsetInputs i;
+        i.isect_ids = in->isect_ids; i.n_isects = in->n_isects; i.I = in->I;
+        i.tile_width = in->tile_width; i.tile_height = in->tile_height;
+        put(offsets, splatx::isect_offset_encode_cpu(i));
+    });
+}
+
+int32_t sxr_rasterize_fwd(const sxh_raster_inputs* in, sxh_raster_outputs* out) {
+    return guarded([&] {
+        splatx::RasterizeFwdInputs r;
+        r.means2d = in->means2d; r.conics = in->conics; r.colors = in->colors;
+        r.opacities = in->opacities; r.backgrounds = in->backgrounds; r.masks = in->masks;
+        r.isect_offsets = in->isect_offsets; r.flatten_ids = in->flatten_ids; r.I = in->I;
+        r.N = in->N; r.n_isects = in->n_isects; r.image_width = in->image_width;
+        r.image_height = in->image_height; r.tile_size = in->tile_size;
+        r.tile_width = in->tile_width; r.tile_height = in->tile_height;
+        const splatx::RasterizeFwdOutputs o = splatx::rasterize_fwd_cpu(r);
+        put(out->render_colors, o.render_colors);
+        put(out->render_alphas, o.render_alphas);
+        put(out->last_ids, o.last_ids);
+    });
+}
+
+int32_t sxr_rng_normal_f32(const sxh_rng_inputs* in, float* out) {
+    return guarded([&] {
+        splatx::RngNormalInputs r;
+        r.seed = in->seed; r.offset = in->offset; r.count = in->count;
+        put(out, splatx::rng_normal_f32_cpu(r));
+    });
+}
+
+int32_t sxr_rng_philox_u32(const sxh_rng_inputs* in, uint32_t* out) {
+    return guarded([&] {
+        splatx::RngNormalInputs r;
+        r.seed = in->seed; r.offset = in->offset; r.count = in->count;
+        put(out, splatx::rng_philox_u32_cpu(r));
+    });
+}
+
+int32_t sxr_make_binoms_lut(int32_t n_max, float* out) {
+    return guarded([&] { put(out, splatx::make_binoms_lut(n_max)); });
+}
+
+int32_t sxr_mcmc_relocation(const sxh_relocation_inputs* in, float* new_op, float* new_sc) {
+    return guarded([&] {
+        splatx::RelocationInputs r;
+        r.opacities = in->opacities; r.scales = in->scales; r.ratios = in->ratios;
+        r.binoms = in->binoms; r.N = in->N; r.n_max = in->n_max; r.min_opacity = in->min_opacity;
+        const splatx::RelocationOutputs o = splatx::mcmc_relocation_cpu(r);
+        put(new_op, o.new_opacities);
+        put(new_sc, o.new_scales);
+    });
+}
+
+int32_t sxr_mcmc_perturb_positions(const sxh_perturb_inputs* in) {
+    return guarded([&] {
+        splatx::PerturbInputs p;
+        p.positions = in->positions; p.quats = in->quats; p.scales_log = in->scales_log;
+        p.opacities_logit = in->opacities_logit; p.noise = in->noise; p.N = in->N;
+        p.noise_scale = in->noise_scale; p.t = in->t; p.k = in->k;
+        splatx::mcmc_perturb_positions_cpu(p);
+    });
+}
+
+int32_t sxr_ssim_fwd(const sxh_ssim_inputs* in, sxh_ssim_outputs* out) {
+    return guarded([&] {
+        splatx::SsimInputs s;
+        s.img1 = in->img1; s.img2 = in->img2; s.I = in->I; s.H = in->H; s.W = in->W; s.C = in->C;
+        s.need_coeffs = in->need_coeffs != 0;
+        const splatx::SsimFwdOutputs o = splatx::ssim_fwd_cpu(s);
+        out->ssim = o.ssim;
+        put(out->ssim_map, o.ssim_map);
+        if (in->need_coeffs) {
+            put(out->coeff_mu, o.coeff_mu);
+            put(out->coeff_sigma, o.coeff_sigma);
+            put(out->coeff_cross, o.coeff_cross);
+        }
+    });
+}
+
+int32_t sxr_quat_scale_to_covar(const float* quats, const float* scales, int64_t n, float* out) {
+    return guarded([&] {
+        for (int64_t i = 0; i < n; i++) {
+            const splatx::Mat3 c = splatx::quat_scale_to_covar(quats + i * 4, scales + i * 3);
+            std::memcpy(out + i * 9, c.m, sizeof(c.m));
+        }
+    });
+}
+
+} // extern "C"
