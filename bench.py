@@ -1,0 +1,196 @@
+"""Benchmark of the resident 3DGS training step on one MI355X (BASELINE.json metric).
+
+Workload (the headline): N = 1,000,000 Gaussians, SH degree 3, 1297x840
+pinhole (fx = fy = 1150, principal point centred), means x,y ~ U[-4,4], z ~ U[1.5,20],
+log-scales ~ N(ln 0.01, 0.7), AccuTile intersection, loss 0.8 L1 + 0.2 (1 - SSIM), fused Adam.
+Every step uses its own seeded camera pose (rotation <= 5 deg, translation <= 0.2); its target is
+the render of a second seeded scene from that pose, held in the device-resident GT cache.
+A step = graph of kernels from preprocess to Adam with its two host syncs (n_isects, loss).
+
+Prints one JSON line. `roofline` is for the kernel with the largest share of GPU time in the timed
+region (HIP events on the executor's stream); `cpu_baseline` times the CPU oracle (this repo's
+single-threaded restatement of the reference CPU path plus its own backward) on one full step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "splatx-metal_amd", "python"))
+
+import scene  # noqa: E402
+import splatx_hip as sh  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, n_passes: int) -> float:
+    """Minimum HBM bytes one launch of `name` must move (per-unit figures stated in DESIGN.md)."""
+    pd = 3 + 4 + 3 + 1 + 3 + (sh_k - 1) * 3  # parameter floats per Gaussian (59 at SH3)
+    if name == "preprocess":
+        # params of every Gaussian (44 B) + SH coefficients of visible ones; writes radii+count (12 B),
+        # and for visible ones the 48-B splat record and the zeroed 48-B gradient record
+        return 44.0 * n + 4.0 * 3 * sh_k * v + 12.0 * n + 96.0 * v
+    if name == "postprocess":
+        # visible: read params, both moments, grads (36 B) and conic/comp/meta (20 B); write params+moments
+        return 4.0 * (n - v) + v * (4.0 * pd * 3 + 36 + 20 + 4.0 * pd * 3)
+    if name == "raster_fwd":
+        return i * (4 + 36) + px * 20.0
+    if name == "raster_bwd":
+        return i * (4 + 36 + 36) + px * (4 + 4 + 12)
+    if name == "sort":
+        return i * 36.0 * n_passes
+    if name == "emit":
+        return v * 28.0 + n * 8.0 + i * 12.0
+    if name == "offsets":
+        return i * 8.0 + 4.0 * (px / 256.0)
+    if name == "scan":
+        return n * 12.0
+    if name == "ssim_fwd":
+        return px * 3 * (4 + 4) + (px * 3) * 16.0
+    if name == "ssim_bwd_l1":
+        return px * 3 * (4 + 4) + (px * 3) * 12.0 + px * 3 * 4.0
+    return 0.0
+
+
+def cpu_baseline(sc, pose, gt, lr) -> dict:
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle_py
+
+    orc = oracle_py.Oracle(libm=False)
+    p, m, v = scene.copy_state(sc)
+    t0 = time.perf_counter()
+    r = orc.train_step(p, m, v, sc.n, sc.sh_degree, pose, sc.K, sc.width, sc.height, gt, sc.sh_degree, lr,
+                       ssim_weight=0.2, want_render=False)
+    dt = (time.perf_counter() - t0) * 1000.0
+    return {"value": round(dt, 1), "unit": "ms/iter", "cores": 1, "kind": "port",
+            "sample": "one full fwd+bwd+Adam step of the same config-3 workload (N=1M, SH3, 1297x840, AccuTile, "
+                      "SSIM) by the single-threaded CPU oracle", "n_isects": r["n_isects"],
+            "stages_ms": {k: round(x, 1) for k, x in r["stage_ms"].items() if x > 0}}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the step has no multi-GPU "
+              f"path — run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    sc, cfg = scene.config_scene(args.config, seed=0)
+    tgt, _ = scene.config_scene(args.config, seed=1)
+    n_poses = args.steps + args.warmup
+    rng = np.random.Generator(np.random.PCG64(1234))
+    poses = [scene.jittered_view(rng) for _ in range(n_poses)]
+    lr = list(sc.lr)
+    isect = sh.SXH_ISECT_ACCUTILE if cfg["isect"] == "accutile" else sh.SXH_ISECT_AABB
+    aa = bool(cfg.get("antialiased", False))
+
+    b = sh.Backend(0)
+    ex = b.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
+                                    antialiased=aa, isect_mode=isect)
+    # targets: the second scene rendered from every pose into the device GT cache
+    ex.set_gt_cache(np.zeros((n_poses, sc.height, sc.width, 3), np.float32))
+    tp, tm, tv = scene.copy_state(tgt)
+    ex.upload_params(tp, tm, tv, sc.n)
+    base = scene.step_kwargs(sc)
+    gt_first = None
+    for k in range(n_poses):
+        ex.render_to_gt_cache(k, **dict(base, viewmat=poses[k]))
+        if k == args.warmup:  # host copy of the first timed target, for the CPU baseline
+            gt_first = ex.step(want_render=True, forward_only=True, **dict(base, viewmat=poses[k]))["render_colors"]
+    p, m, v = scene.copy_state(sc)
+    ex.upload_params(p, m, v, sc.n)
+
+    # pre-built step arguments (no host work inside the timed loop beyond the step itself)
+    steps = []
+    for k in range(n_poses):
+        s_in, keep = ex.make_step_inputs(**dict(base, viewmat=poses[k]), gt_index=k)
+        steps.append((s_in, keep))
+    out = sh.StepOutputs()
+    for k in range(args.warmup):
+        rc = ex.step_raw(steps[k][0], out)
+        assert rc == 0, b.lib.sxh_last_error()
+
+    ex.set_profiling(True)
+    totals = {}
+    n_isects, n_vis, losses = [], [], []
+    t0 = time.perf_counter()
+    for k in range(args.warmup, n_poses):
+        rc = ex.step_raw(steps[k][0], out)
+        if rc != 0:
+            raise RuntimeError(b.lib.sxh_last_error())
+        for name, ms in ex.get_timing().items():
+            totals[name] = totals.get(name, 0.0) + ms
+        n_isects.append(out.n_isects)
+        n_vis.append(out.n_visible)
+        losses.append(out.loss)
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1000.0 / args.steps
+    avg = {k: x / args.steps for k, x in totals.items()}
+
+    I, V = float(np.mean(n_isects)), float(np.mean(n_vis))
+    px = sc.width * sc.height
+    sh_k = (sc.sh_degree + 1) ** 2
+    tiles = ((sc.width + 15) // 16) * ((sc.height + 15) // 16)
+    n_passes = (32 + int(tiles - 1).bit_length() + 7) // 8
+    kernel_names = [k for k in avg if not k.startswith("host_")]
+    per_kernel = {}
+    for k in kernel_names:
+        by = algorithmic_bytes(k, sc.n, V, I, px, sh_k, n_passes)
+        per_kernel[k] = {"ms": round(avg[k], 4), "alg_GB": round(by / 1e9, 4),
+                         "GBps": round(by / 1e9 / (avg[k] / 1e3), 1) if by > 0 and avg[k] > 0 else None}
+    dom = max(kernel_names, key=lambda k: avg[k])
+    dom_bytes = algorithmic_bytes(dom, sc.n, V, I, px, sh_k, n_passes)
+    achieved = dom_bytes / 1e9 / (avg[dom] / 1e3)
+    step_bytes = sum(algorithmic_bytes(k, sc.n, V, I, px, sh_k, n_passes) for k in kernel_names)
+
+    res = {
+        "metric": "train-step ms/iter (fwd+bwd+Adam) at N=1M, 1297x840; % HBM roofline",
+        "value": round(ms_per_step, 4),
+        "unit": "ms/iter",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded generator of BASELINE.json configs; target = second seeded scene rendered per pose)",
+        "config": {"workload": f"config {args.config}: N={sc.n}, SH{sc.sh_degree}, {sc.width}x{sc.height}, "
+                               f"fx=fy={cfg['fx']}, {cfg['isect']} isect, ssim_weight={cfg['ssim']}, "
+                               f"pose jittered per step", "gaussians": sc.n, "width": sc.width,
+                   "height": sc.height, "sh_degree": sc.sh_degree, "parallelism": "single GPU"},
+        "gaussians_per_s": round(sc.n / (ms_per_step / 1e3), 1),
+        "mean_n_isects": round(I, 1),
+        "mean_visible": round(V, 1),
+        "final_loss": round(float(losses[-1]), 6),
+        "step_alg_GB": round(step_bytes / 1e9, 4),
+        "step_hbm_roofline_frac": round(step_bytes / 1e9 / (ms_per_step / 1e3) / HBM_PEAK_GBS, 5),
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "kernels": per_kernel,
+        "host_waits_ms": {k: round(avg[k], 4) for k in avg if k.startswith("host_")},
+    }
+    ex.close()
+    b.close()
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(sc, poses[args.warmup], gt_first, lr)
+        res["cpu_baseline"]["cores_available"] = os.cpu_count()
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,468 @@
+// executor.cpp — the device-resident train-step executor (TrainStepExecutor, KernelBackend.h:386-392;
+// the reference's MetalTrainStepExecutor, MetalBackend.cpp:1628-2460).
+//
+// One HIP stream. A step is: preprocess -> int64 scan -> [sync 1: n_isects readback, isect buffers
+// grow 1.5x when needed] -> emit -> radix sort -> offsets -> raster fwd -> SSIM fwd -> SSIM bwd
+// fused with the L1 gradient -> raster bwd -> postprocess (bwd chain + Adam + noise) -> device loss
+// reduction -> [sync 2: loss readback]. Parameters, moments and the GT cache stay in HBM; the
+// arena is sized once for arena_rows and never reallocated.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "splatx_hip.h"
+#include "sx_host.h"
+#include "sx_kernels.h"
+#include "sx_step.h"
+
+using namespace sxh;
+
+namespace {
+
+struct PinnedHost {
+    void* p = nullptr;
+    explicit PinnedHost(size_t bytes) { SXH_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault)); }
+    ~PinnedHost() {
+        if (p) (void)hipHostFree(p);
+    }
+    PinnedHost(const PinnedHost&) = delete;
+    PinnedHost& operator=(const PinnedHost&) = delete;
+};
+
+constexpr int kMaxEvents = 32;
+
+} // namespace
+
+struct sxh_executor {
+    sxh_backend* b = nullptr;
+    sxh_exec_desc d{};
+    int n_coeffs = 1;
+    int dims[6] = {3, 4, 3, 1, 3, 0};
+    int rows = 0;
+    DevBuf<float> p[6], m[6], v[6];
+    DevBuf<float4> splats, grads;
+    DevBuf<int32_t> radii, tiles;
+    DevBuf<int64_t> cum;
+    DevBuf<uint8_t> scan_scratch;
+    DevBuf<unsigned long long> n_vis;
+    // intersections (grow 1.5x, reused)
+    size_t isect_cap = 0;
+    DevBuf<uint64_t> keys_a, keys_b;
+    DevBuf<int32_t> vals_a, vals_b;
+    DevBuf<uint8_t> sort_scratch;
+    // image-sized buffers
+    size_t img_px = 0, img_tiles = 0, img_map = 0;
+    DevBuf<int32_t> offsets, last_ids;
+    DevBuf<float> render, alpha, v_render, v_alpha_zero, gt_stage;
+    DevBuf<float> ssim_map, cmu, csg, ccr;
+    DevBuf<double> ssim_part, l1_part;
+    DevBuf<float> loss_dev;
+    // GT cache
+    DevBuf<float> gt_cache;
+    int gt_n = 0, gt_w = 0, gt_h = 0;
+    DevBuf<float> staging;
+    PinnedHost host_small{64};
+    // profiling
+    bool prof = false;
+    hipEvent_t ev[kMaxEvents] = {};
+    const char* ev_name[kMaxEvents] = {};
+    int n_ev = 0;
+    sxh_exec_timing timing{};
+    double sync_ms[2] = {0, 0};
+
+    sxk::Arena arena() {
+        sxk::Arena A{};
+        for (int g = 0; g < 6; g++) {
+            A.p[g] = p[g].p;
+            A.m[g] = m[g].p;
+            A.v[g] = v[g].p;
+        }
+        A.rows = rows;
+        return A;
+    }
+
+    void mark(const char* name) {
+        if (!prof || n_ev >= kMaxEvents) return;
+        SXH_HIP(hipEventRecord(ev[n_ev], b->stream));
+        ev_name[n_ev++] = name;
+    }
+
+    void ensure_isect(size_t n) {
+        if (n <= isect_cap) return;
+        const size_t cap = std::max<size_t>(n + n / 2, 1 << 16);
+        keys_a.alloc(cap);
+        keys_b.alloc(cap);
+        vals_a.alloc(cap);
+        vals_b.alloc(cap);
+        sort_scratch.alloc(sxk::sort_scratch_bytes(static_cast<int64_t>(cap)));
+        isect_cap = cap;
+    }
+
+    void ensure_image(int W, int H, bool use_ssim) {
+        const size_t px = static_cast<size_t>(W) * H;
+        const size_t tiles_n = static_cast<size_t>((W + 15) / 16) * ((H + 15) / 16);
+        const size_t map_n = use_ssim ? static_cast<size_t>(H - 10) * (W - 10) * 3 : 0;
+        if (px > img_px) {
+            render.alloc(px * 3);
+            alpha.alloc(px);
+            last_ids.alloc(px);
+            v_render.alloc(px * 3);
+            v_alpha_zero.alloc(px);
+            SXH_HIP(hipMemsetAsync(v_alpha_zero.p, 0, px * sizeof(float), b->stream));
+            gt_stage.alloc(px * 3);
+            img_px = px;
+        }
+        // one f64 partial per workgroup of the loss kernels (exact counts of their grids)
+        const size_t l1_blocks = std::max<size_t>(sxk::step_ssim_bwd_blocks(H, W),
+                                                  sxk::step_l1_blocks(static_cast<int64_t>(px) * 3));
+        if (l1_blocks > l1_part.n) l1_part.alloc(l1_blocks);
+        if (tiles_n > img_tiles) {
+            offsets.alloc(tiles_n);
+            img_tiles = tiles_n;
+        }
+        if (use_ssim) {
+            if (map_n > img_map) {
+                ssim_map.alloc(map_n);
+                cmu.alloc(map_n);
+                csg.alloc(map_n);
+                ccr.alloc(map_n);
+                img_map = map_n;
+            }
+            const size_t ss_blocks = static_cast<size_t>(sxk::ssim_fwd_blocks(1, H, W, 3));
+            if (ss_blocks > ssim_part.n) ssim_part.alloc(ss_blocks);
+        }
+    }
+};
+
+extern "C" {
+
+int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor** out) {
+    return guarded([&] {
+        if (!b || !desc || !out) invalid("TrainStepExecutor", "null argument");
+        // MetalBackend.cpp:1632-1641
+        if (desc->arena_rows < 1) invalid("TrainStepExecutor", "arena_rows must be >= 1");
+        if (desc->sh_degree < 0 || desc->sh_degree > 3) invalid("TrainStepExecutor", "sh_degree must be in [0,3]");
+        if (!(desc->ssim_weight >= 0.0f && desc->ssim_weight <= 1.0f))
+            invalid("TrainStepExecutor", "ssim_weight must be in [0,1]");
+        if (desc->isect_mode != SXH_ISECT_ACCUTILE && desc->isect_mode != SXH_ISECT_AABB)
+            invalid("TrainStepExecutor", "isect_mode must be ACCUTILE or AABB");
+        const int64_t K = static_cast<int64_t>(desc->sh_degree + 1) * (desc->sh_degree + 1);
+        if (desc->arena_rows * K * 3 > INT32_MAX) invalid("TrainStepExecutor", "arena_rows*K*3 exceeds int32");
+        SXH_HIP(hipSetDevice(b->device));
+        auto* e = new sxh_executor();
+        try {
+            e->b = b;
+            e->d = *desc;
+            e->n_coeffs = static_cast<int>(K);
+            e->dims[5] = static_cast<int>((K - 1) * 3);
+            e->rows = static_cast<int>(desc->arena_rows);
+            const size_t R = static_cast<size_t>(e->rows);
+            for (int g = 0; g < 6; g++) {
+                if (e->dims[g] == 0) continue;
+                const size_t n = R * e->dims[g];
+                e->p[g].alloc(n);
+                e->m[g].alloc(n);
+                e->v[g].alloc(n);
+                SXH_HIP(hipMemsetAsync(e->p[g].p, 0, n * 4, b->stream));
+                SXH_HIP(hipMemsetAsync(e->m[g].p, 0, n * 4, b->stream));
+                SXH_HIP(hipMemsetAsync(e->v[g].p, 0, n * 4, b->stream));
+            }
+            e->splats.alloc(R * 3);
+            e->grads.alloc(R * 3);
+            e->radii.alloc(R * 2);
+            e->tiles.alloc(R);
+            e->cum.alloc(R);
+            e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
+            e->n_vis.alloc(1);
+            e->loss_dev.alloc(1);
+            e->staging.alloc(R * 45);
+            e->ensure_isect(1 << 16);
+            for (int k = 0; k < kMaxEvents; k++) SXH_HIP(hipEventCreate(&e->ev[k]));
+            SXH_HIP(hipStreamSynchronize(b->stream));
+        } catch (...) {
+            delete e;
+            throw;
+        }
+        *out = e;
+    });
+}
+
+void sxh_exec_destroy(sxh_executor* e) {
+    if (!e) return;
+    (void)hipStreamSynchronize(e->b->stream);
+    for (int k = 0; k < kMaxEvents; k++)
+        if (e->ev[k]) (void)hipEventDestroy(e->ev[k]);
+    delete e;
+}
+
+static void sync_params(sxh_executor* e, const sxh_param_sync* s, bool up) {
+    if (!s) invalid("TrainStepExecutor", "null sync");
+    if (s->rows < 0 || s->rows > e->rows) invalid("TrainStepExecutor", "sync rows out of [0, arena_rows]");
+    const int rows = static_cast<int>(s->rows);
+    if (rows == 0) return;
+    hipStream_t st = e->b->stream;
+    for (int g = 0; g < 6; g++) {
+        const int dim = e->dims[g];
+        if (dim == 0) continue;
+        float* host[3] = {s->params[g], s->exp_avg[g], s->exp_avg_sq[g]};
+        DevBuf<float>* dev[3] = {&e->p[g], &e->m[g], &e->v[g]};
+        for (int k = 0; k < 3; k++) {
+            if (!host[k]) invalid("TrainStepExecutor", "null parameter/moment pointer for group " + std::to_string(g));
+            const size_t n = static_cast<size_t>(rows) * dim;
+            if (up) {
+                SXH_HIP(hipMemcpyAsync(e->staging.p, host[k], n * 4, hipMemcpyHostToDevice, st));
+                sxk::aos_to_soa(e->staging.p, dev[k]->p, rows, dim, e->rows, st);
+            } else {
+                sxk::soa_to_aos(dev[k]->p, e->staging.p, rows, dim, e->rows, st);
+                SXH_HIP(hipMemcpyAsync(host[k], e->staging.p, n * 4, hipMemcpyDeviceToHost, st));
+            }
+            SXH_HIP(hipStreamSynchronize(st));  // staging is reused
+        }
+    }
+}
+
+int32_t sxh_exec_upload(sxh_executor* e, const sxh_param_sync* s) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor", "null executor");
+        SXH_HIP(hipSetDevice(e->b->device));
+        sync_params(e, s, true);
+    });
+}
+
+int32_t sxh_exec_download(sxh_executor* e, const sxh_param_sync* s) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor", "null executor");
+        SXH_HIP(hipSetDevice(e->b->device));
+        sync_params(e, s, false);
+    });
+}
+
+int32_t sxh_exec_set_gt_cache(sxh_executor* e, const float* images, int32_t n, int32_t width, int32_t height) {
+    return guarded([&] {
+        if (!e || !images) invalid("TrainStepExecutor", "null argument");
+        if (n < 1 || width < 1 || height < 1) invalid("TrainStepExecutor", "bad GT cache shape");
+        SXH_HIP(hipSetDevice(e->b->device));
+        const size_t per = static_cast<size_t>(width) * height * 3;
+        e->gt_cache.alloc(per * n);
+        SXH_HIP(hipMemcpyAsync(e->gt_cache.p, images, per * n * 4, hipMemcpyHostToDevice, e->b->stream));
+        SXH_HIP(hipStreamSynchronize(e->b->stream));
+        e->gt_n = n;
+        e->gt_w = width;
+        e->gt_h = height;
+    });
+}
+
+int32_t sxh_exec_set_profiling(sxh_executor* e, int32_t enable) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor", "null executor");
+        e->prof = enable != 0;
+    });
+}
+
+int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out) {
+    return guarded([&] {
+        if (!e || !out) invalid("TrainStepExecutor", "null argument");
+        *out = e->timing;
+    });
+}
+
+// The step proper. `gt_override` (device) replaces the GT source when not null.
+static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out, float* render_to_dev) {
+    const char* what = "TrainStepExecutor::step";
+    if (!in || !out) invalid(what, "null inputs/outputs");
+    // MetalBackend.cpp:1697-1711
+    if (in->count < 1 || in->count > e->rows) invalid(what, "count out of [1, arena_rows]");
+    if (in->width < 1 || in->height < 1) invalid(what, "width/height must be positive");
+    if (!in->viewmat || !in->K) invalid(what, "null viewmat/K");
+    const bool fwd_only = in->forward_only != 0;
+    const bool use_gt_cache = in->gt_index >= 0;
+    if (!fwd_only && !use_gt_cache && !in->gt_rgb) invalid(what, "null gt_rgb");
+    if (use_gt_cache && !fwd_only) {
+        if (in->gt_index >= e->gt_n) invalid(what, "gt_index out of range");
+        if (in->width != e->gt_w || in->height != e->gt_h) invalid(what, "GT cache image size mismatch");
+    }
+    const bool use_ssim = e->d.ssim_weight > 0.0f && !fwd_only;
+    if (use_ssim && (in->height < 11 || in->width < 11)) invalid(what, "ssim requires H, W >= 11");
+    if (in->degrees_to_use > static_cast<uint32_t>(e->d.sh_degree)) invalid(what, "degrees_to_use > sh_degree");
+
+    hipStream_t s = e->b->stream;
+    const int W = in->width, H = in->height;
+    const int tw = (W + 15) / 16, th = (H + 15) / 16;
+    const size_t HW = static_cast<size_t>(W) * H;
+    const size_t n_px = HW * 3;
+    const size_t map_n = use_ssim ? static_cast<size_t>(H - 10) * (W - 10) * 3 : 0;
+    e->ensure_image(W, H, use_ssim);
+    e->n_ev = 0;
+
+    sxk::StepConst c{};
+    std::memcpy(c.vm, in->viewmat, sizeof(c.vm));
+    std::memcpy(c.K, in->K, sizeof(c.K));
+    c.width = W;
+    c.height = H;
+    c.count = static_cast<int>(in->count);
+    c.n_coeffs = e->n_coeffs;
+    c.degree = in->degrees_to_use;
+    c.eps2d = e->d.eps2d;
+    c.near_plane = e->d.near_plane;
+    c.far_plane = e->d.far_plane;
+    c.radius_clip = e->d.radius_clip;
+    c.aa = e->d.antialiased ? 1 : 0;
+    c.accutile = e->d.isect_mode == SXH_ISECT_ACCUTILE ? 1 : 0;
+    c.tile_width = tw;
+    c.tile_height = th;
+    c.tile_n_bits = sx::bits_for_count(static_cast<int64_t>(tw) * th);
+    for (int g = 0; g < 6; g++) c.lr[g] = in->lr[g];
+    c.b1 = e->d.b1;
+    c.b2 = e->d.b2;
+    c.eps = e->d.eps;
+    c.opacity_reg_w = in->opacity_reg_w;
+    c.scale_reg_w = in->scale_reg_w;
+    c.inject_noise = (in->inject_noise && !fwd_only) ? 1 : 0;
+    c.noise_seed = in->noise_seed;
+    c.noise_offset = in->noise_offset;
+    c.noise_scale = in->noise_scale;
+    const sxk::Arena A = e->arena();
+
+    // ---- segment A: preprocess + scan ------------------------------------------------------------
+    e->mark("start");
+    SXH_HIP(hipMemsetAsync(e->n_vis.p, 0, sizeof(unsigned long long), s));
+    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->grads.p, e->n_vis.p, s);
+    e->mark("preprocess");
+    sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s);
+    e->mark("scan");
+    int64_t* hs = static_cast<int64_t*>(e->host_small.p);
+    SXH_HIP(hipMemcpyAsync(&hs[0], e->cum.p + (c.count - 1), 8, hipMemcpyDeviceToHost, s));
+    SXH_HIP(hipMemcpyAsync(&hs[1], e->n_vis.p, 8, hipMemcpyDeviceToHost, s));
+    SXH_HIP(hipGetLastError());
+    // ---- sync 1: n_isects (MetalBackend.cpp:1849-1858) --------------------------------------------
+    auto t0 = std::chrono::steady_clock::now();
+    SXH_HIP(hipStreamSynchronize(s));
+    e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    const int64_t n_isects = hs[0];
+    out->n_isects = n_isects;
+    out->n_visible = hs[1];
+    validate_n_isects_readback(n_isects, what);
+    e->ensure_isect(static_cast<size_t>(n_isects));
+    e->mark("sync1");
+
+    // ---- segment B ---------------------------------------------------------------------------------
+    int32_t* flat = e->vals_a.p;
+    if (n_isects > 0) {
+        sxk::step_emit(c, e->splats.p, e->radii.p, e->cum.p, e->keys_a.p, e->vals_a.p, s);
+        e->mark("emit");
+        const int which = sxk::radix_sort(e->keys_a.p, e->vals_a.p, e->keys_b.p, e->vals_b.p, n_isects,
+                                          32 + c.tile_n_bits, e->sort_scratch.p, s);
+        e->mark("sort");
+        const uint64_t* keys = which ? e->keys_b.p : e->keys_a.p;
+        flat = which ? e->vals_b.p : e->vals_a.p;
+        sxk::offset_encode(keys, n_isects, 1, tw * th, c.tile_n_bits, e->offsets.p, s);
+        e->mark("offsets");
+    } else {
+        SXH_HIP(hipMemsetAsync(e->offsets.p, 0, static_cast<size_t>(tw) * th * 4, s));
+    }
+    sxk::RasterArgs ra{};
+    ra.splats = e->splats.p;
+    ra.offsets = e->offsets.p;
+    ra.flatten_ids = flat;
+    ra.I = 1;
+    ra.width = W;
+    ra.height = H;
+    ra.tile_width = tw;
+    ra.tile_height = th;
+    ra.n_isects = static_cast<int32_t>(n_isects);
+    sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
+    e->mark("raster_fwd");
+    float* hloss = reinterpret_cast<float*>(&hs[2]);
+    *hloss = 0.0f;
+    if (!fwd_only) {
+        const float* gt = nullptr;
+        if (use_gt_cache) gt = e->gt_cache.p + static_cast<size_t>(in->gt_index) * n_px;
+        else {
+            SXH_HIP(hipMemcpyAsync(e->gt_stage.p, in->gt_rgb, n_px * 4, hipMemcpyHostToDevice, s));
+            gt = e->gt_stage.p;
+        }
+        int n_l1 = 0, n_ss = 0;
+        if (use_ssim) {
+            n_ss = sxk::ssim_fwd_blocks(1, H, W, 3);
+            sxk::ssim_fwd(e->render.p, gt, 1, H, W, 3, 1, e->ssim_map.p, e->cmu.p, e->csg.p, e->ccr.p,
+                          e->ssim_part.p, s);
+            e->mark("ssim_fwd");
+            const float G = static_cast<float>(-static_cast<double>(e->d.ssim_weight) / static_cast<double>(map_n));
+            n_l1 = sxk::step_ssim_bwd_blocks(H, W);
+            sxk::step_ssim_bwd_l1(e->render.p, gt, e->cmu.p, e->csg.p, e->ccr.p, H, W, G, 1.0f - e->d.ssim_weight,
+                                  1.0f / static_cast<float>(n_px), e->v_render.p, e->l1_part.p, s);
+            e->mark("ssim_bwd_l1");
+        } else {
+            n_l1 = sxk::step_l1_blocks(static_cast<int64_t>(n_px));
+            sxk::step_l1_grad(e->render.p, gt, static_cast<int64_t>(n_px), e->v_render.p, e->l1_part.p, n_l1, s);
+            e->mark("l1_grad");
+        }
+        if (n_isects > 0) {
+            sxk::RasterBwdGrads gg{nullptr, nullptr, nullptr, nullptr, nullptr, e->grads.p};
+            sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
+            e->mark("raster_bwd");
+        }
+        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, s);
+        e->mark("postprocess");
+        sxk::step_loss_final(e->l1_part.p, n_l1, e->ssim_part.p, n_ss, static_cast<double>(n_px),
+                             static_cast<double>(map_n), e->d.ssim_weight, use_ssim ? 1 : 0, e->loss_dev.p, s);
+        e->mark("loss");
+        SXH_HIP(hipMemcpyAsync(hloss, e->loss_dev.p, 4, hipMemcpyDeviceToHost, s));
+    }
+    if (render_to_dev)
+        SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
+    if (out->render_colors)
+        SXH_HIP(hipMemcpyAsync(out->render_colors, e->render.p, n_px * 4, hipMemcpyDeviceToHost, s));
+    SXH_HIP(hipGetLastError());
+    // ---- sync 2: loss (MetalBackend.cpp:2241-2261) ----------------------------------------------------
+    t0 = std::chrono::steady_clock::now();
+    SXH_HIP(hipStreamSynchronize(s));
+    e->sync_ms[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    out->loss = fwd_only ? 0.0f : *hloss;
+    if (e->prof) {
+        sxh_exec_timing& t = e->timing;
+        t.n = 0;
+        for (int k = 1; k < e->n_ev && t.n < 30; k++) {
+            float ms = 0.f;
+            if (std::strcmp(e->ev_name[k], "sync1") == 0) continue;  // host wait, reported below
+            const int prev = (std::strcmp(e->ev_name[k - 1], "sync1") == 0 && k >= 2) ? k - 1 : k - 1;
+            SXH_HIP(hipEventElapsedTime(&ms, e->ev[prev], e->ev[k]));
+            t.names[t.n] = e->ev_name[k];
+            t.ms[t.n++] = ms;
+        }
+        t.names[t.n] = "host_sync1_wait";
+        t.ms[t.n++] = static_cast<float>(e->sync_ms[0]);
+        t.names[t.n] = "host_sync2_wait";
+        t.ms[t.n++] = static_cast<float>(e->sync_ms[1]);
+    }
+}
+
+int32_t sxh_exec_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor::step", "null executor");
+        SXH_HIP(hipSetDevice(e->b->device));
+        run_step(e, in, out, nullptr);
+    });
+}
+
+int32_t sxh_exec_render_to_gt_cache(sxh_executor* e, const sxh_step_inputs* in, int32_t index) {
+    return guarded([&] {
+        if (!e || !in) invalid("TrainStepExecutor", "null argument");
+        if (index < 0 || index >= e->gt_n) invalid("TrainStepExecutor", "GT cache index out of range");
+        if (in->width != e->gt_w || in->height != e->gt_h) invalid("TrainStepExecutor", "GT cache image size mismatch");
+        SXH_HIP(hipSetDevice(e->b->device));
+        sxh_step_inputs f = *in;
+        f.forward_only = 1;
+        sxh_step_outputs o{};
+        const size_t n_px = static_cast<size_t>(in->width) * in->height * 3;
+        run_step(e, &f, &o, e->gt_cache.p + static_cast<size_t>(index) * n_px);
+        SXH_HIP(hipStreamSynchronize(e->b->stream));
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,123 @@
+// sx_kernels.h — host-side launchers of the gfx950 kernels (one stream argument each).
+// Every pointer is a device pointer. Launchers perform no allocation and no synchronization.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sxk {
+
+// ---- elementwise / Adam -------------------------------------------------------------------
+void adam(float* param, const float* grad, float* m, float* v, const uint8_t* valid, int64_t n_elems,
+          int64_t D, float lr, float b1, float b2, float eps, hipStream_t s);
+
+// ---- projection ---------------------------------------------------------------------------
+struct ProjArgs {
+    const float* means;
+    const float* covars;   // [N,6] or null
+    const float* quats;    // [N,4]
+    const float* scales;   // [N,3]
+    const float* opacities;
+    const float* viewmats; // [C,16]
+    const float* Ks;       // [C,9]
+    int N, C, width, height;
+    float eps2d, near_plane, far_plane, radius_clip;
+    int calc_comp;
+};
+void projection_fwd(const ProjArgs& a, int32_t* radii, float* means2d, float* depths, float* conics,
+                    float* comps, hipStream_t s);
+struct ProjBwdArgs {
+    const int32_t* radii;
+    const float* conics;
+    const float* comps;
+    const float* v_means2d;
+    const float* v_depths;
+    const float* v_conics;
+    const float* v_comps;  // or null
+    int viewmats_grad;
+};
+// v_* outputs must be zeroed by the caller (accumulated atomically when C > 1).
+void projection_bwd(const ProjArgs& a, const ProjBwdArgs& g, float* v_means, float* v_covars,
+                    float* v_quats, float* v_scales, float* v_viewmats, hipStream_t s);
+
+// ---- SH -------------------------------------------------------------------------------------
+void sh_fwd(const float* dirs, const float* coeffs, const uint8_t* masks, uint32_t degree, int B, int N,
+            int K, int D, float* colors, hipStream_t s);
+// v_coeffs / v_dirs zeroed by the caller.
+void sh_bwd(const float* dirs, const float* coeffs, const uint8_t* masks, uint32_t degree, int B, int N,
+            int K, int D, const float* v_colors, float* v_coeffs, float* v_dirs, hipStream_t s);
+
+// ---- intersection / scan / sort / offsets ---------------------------------------------------
+struct IsectArgs {
+    const float* means2d;
+    const int32_t* radii;
+    const float* depths;
+    const float* conics;     // null -> AABB
+    const float* opacities;  // null -> AABB
+    int I, N;
+    int tile_size, tile_width, tile_height;
+    uint32_t tile_n_bits;
+};
+void isect_count(const IsectArgs& a, int32_t* tiles_per_gauss, hipStream_t s);
+void isect_emit(const IsectArgs& a, const int64_t* cum, uint64_t* keys, int32_t* vals, hipStream_t s);
+
+// inclusive int32 -> int64 scan; scratch needs scan_scratch_bytes(n) bytes.
+size_t scan_scratch_bytes(int64_t n);
+void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s);
+
+// Stable LSD radix sort of (u64 key, i32 value) on bits [0, key_bits). Result lands in
+// keys_a/vals_a when the pass count is even, else in keys_b/vals_b; returns 0 or 1 accordingly.
+size_t sort_scratch_bytes(int64_t n);
+int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n,
+               uint32_t key_bits, void* scratch, hipStream_t s);
+
+// offsets[I*n_tiles] from sorted keys; n_isects > 0.
+void offset_encode(const uint64_t* keys, int64_t n_isects, int I, int n_tiles, uint32_t tile_n_bits,
+                   int32_t* offsets, hipStream_t s);
+
+// ---- raster ---------------------------------------------------------------------------------
+// Packed per-Gaussian record consumed by the rasterizer: 3 x float4
+// {x, y, opacity, 0}, {conic a, b, c, 0}, {r, g, b, 0}.
+void pack_splats(const float* means2d, const float* conics, const float* colors, const float* opacities,
+                 int n, float4* splats, hipStream_t s);
+struct RasterArgs {
+    const float4* splats;
+    const int32_t* offsets;
+    const int32_t* flatten_ids;
+    const float* backgrounds;  // [I,3] or null
+    const uint8_t* masks;      // [I,n_tiles] or null
+    int I, width, height, tile_width, tile_height;
+    int32_t n_isects;
+};
+void raster_fwd(const RasterArgs& a, float* render_colors, float* render_alphas, int32_t* last_ids,
+                hipStream_t s);
+// Gradient outputs zeroed by the caller; packed as 3 x float4 per Gaussian when `packed_grads`
+// is set (v_xy.x, v_xy.y, v_op, _ | v_conic a,b,c, _ | v_rgb, _), else SoA pointers are used.
+struct RasterBwdGrads {
+    float* v_means2d;
+    float* v_conics;
+    float* v_colors;
+    float* v_opacities;
+    float* v_means2d_abs;
+    float4* packed;  // when set: the resident-step record layout (3 x float4 per Gaussian)
+};
+void raster_bwd(const RasterArgs& a, const float* render_alphas, const int32_t* last_ids,
+                const float* v_render_colors, const float* v_render_alphas, const RasterBwdGrads& g,
+                hipStream_t s);
+
+// ---- SSIM -----------------------------------------------------------------------------------
+void ssim_fwd(const float* img1, const float* img2, int I, int H, int W, int C, int need_coeffs,
+              float* map, float* cmu, float* csg, float* ccr, double* block_sums, hipStream_t s);
+int ssim_fwd_blocks(int I, int H, int W, int C);
+void ssim_bwd(const float* img1, const float* img2, const float* cmu, const float* csg, const float* ccr,
+              int I, int H, int W, int C, float G, float* v_img1, hipStream_t s);
+
+// ---- RNG / MCMC -----------------------------------------------------------------------------
+void rng_philox_u32(uint64_t seed, uint64_t offset, int64_t count, uint32_t* out, hipStream_t s);
+void rng_normal_f32(uint64_t seed, uint64_t offset, int64_t count, float* out, hipStream_t s);
+void mcmc_relocation(const float* opac, const float* scales, const int32_t* ratios, const float* binoms,
+                     int N, int n_max, float min_opacity, float* new_op, float* new_sc, hipStream_t s);
+void mcmc_perturb(float* positions, const float* quats, const float* scales_log, const float* logits,
+                  const float* noise, int N, float noise_scale, float t, float k, hipStream_t s);
+
+} // namespace sxk

@@ -1,0 +1,69 @@
+// sx_step.h — launchers of the fused resident-step kernels (k_step.hip).
+//
+// Device arena layout (MI355X-first): every parameter group and both Adam moments are stored
+// coefficient-major (SoA), element j of row i at [j * rows + i], so each per-Gaussian thread's
+// reads and writes are fully coalesced 256-byte wave accesses. The host sync format of the
+// reference (row-major [rows][dim], KernelBackend.h:348-359) is converted on upload/download.
+// Per-Gaussian intermediates are packed in three float4 records:
+//   splat[3i+0] = {mean2d.x, mean2d.y, opacity used by isect/raster, depth}
+//   splat[3i+1] = {conic a, b, c, compensation}
+//   splat[3i+2] = {r, g, b, meta bits: 1 = visible, 2/4/8 = relu mask of r/g/b}
+//   grads[3i+0] = {v_mean2d.x, v_mean2d.y, v_opacity, 0}, grads[3i+1] = {v_conic a,b,c, 0},
+//   grads[3i+2] = {v_rgb, 0} (raster backward accumulates here atomically)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sxk {
+
+struct Arena {
+    float* p[6];
+    float* m[6];
+    float* v[6];
+    int rows;  // arena stride
+};
+
+struct StepConst {
+    float vm[16];
+    float K[9];
+    int width, height;
+    int count;
+    int n_coeffs;  // (sh_degree+1)^2 of the arena
+    uint32_t degree;
+    float eps2d, near_plane, far_plane, radius_clip;
+    int aa;
+    int accutile;
+    int tile_width, tile_height;
+    uint32_t tile_n_bits;
+    float lr[6];
+    float b1, b2, eps;
+    float opacity_reg_w, scale_reg_w;
+    int inject_noise;
+    uint64_t noise_seed, noise_offset;
+    float noise_scale;
+};
+
+void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
+                     float4* grads, unsigned long long* n_visible, hipStream_t s);
+void step_emit(const StepConst& c, const float4* splats, const int32_t* radii, const int64_t* cum,
+               uint64_t* keys, int32_t* vals, hipStream_t s);
+void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
+                      hipStream_t s);
+// Noise only (the forward-only path never calls it; a training step fuses it into postprocess).
+// L1 gradient without SSIM: v_render = sign(render - gt) / n, per-block f64 sums of |render - gt|.
+void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_render, double* partials,
+                  int n_blocks, hipStream_t s);
+int step_l1_blocks(int64_t n);
+// SSIM backward fused with the L1 gradient: v_render = w_l1 * sign(d)/n + G*(...), plus |d| sums.
+void step_ssim_bwd_l1(const float* render, const float* gt, const float* cmu, const float* csg,
+                      const float* ccr, int H, int W, float G, float w_l1, float g_l1, float* v_render,
+                      double* l1_partials, hipStream_t s);
+int step_ssim_bwd_blocks(int H, int W);
+// loss = (1-lam) * float(l1_sum / n_px) + lam * (1 - float(ssim_sum / M)) (or the L1 alone)
+void step_loss_final(const double* l1_partials, int n_l1, const double* ssim_partials, int n_ssim,
+                     double n_px, double M, float lam, int use_ssim, float* loss_out, hipStream_t s);
+void aos_to_soa(const float* aos, float* soa, int rows, int dim, int stride, hipStream_t s);
+void soa_to_aos(const float* soa, float* aos, int rows, int dim, int stride, hipStream_t s);
+
+} // namespace sxk

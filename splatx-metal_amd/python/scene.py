@@ -1,0 +1,122 @@
+"""Synthetic scenes and cameras of the benchmark configurations (BASELINE.json `configs`).
+
+All randomness is numpy PCG64 with explicit seeds, so the GPU executor and the CPU oracle get
+byte-identical inputs. Parameter groups follow the reference order (KernelBackend.h:348-353):
+0 means[N,3], 1 quats[N,4] (w,x,y,z), 2 log-scales[N,3], 3 opacity logits[N], 4 sh0[N,3],
+5 shN[N,(K-1)*3].
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import numpy as np
+
+# TrainConfig defaults (Sources/SplatXCore/include/splatx/Trainer.h:211-218)
+LR_MEANS, LR_SCALES, LR_QUATS, LR_OPAC, LR_SH0, LR_SHN = 1.6e-4, 5e-3, 1e-3, 5e-2, 2.5e-3, 2.5e-3 / 20.0
+
+
+@dataclasses.dataclass
+class Scene:
+    n: int
+    sh_degree: int
+    params: list
+    width: int
+    height: int
+    viewmat: np.ndarray
+    K: np.ndarray
+    gt: np.ndarray | None = None
+    lr: tuple = (LR_MEANS, LR_QUATS, LR_SCALES, LR_OPAC, LR_SH0, LR_SHN)
+
+
+def group_dims(sh_degree: int):
+    return [3, 4, 3, 1, 3, ((sh_degree + 1) ** 2 - 1) * 3]
+
+
+def make_params(n, sh_degree, seed, xy=2.0, z=(2.0, 10.0), log_scale_mu=math.log(0.02), log_scale_sd=0.5,
+                dc_sd=0.5, rest_sd=0.05, tie_frac=0.0):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    means = np.empty((n, 3), np.float32)
+    means[:, 0] = rng.uniform(-xy, xy, n)
+    means[:, 1] = rng.uniform(-xy, xy, n)
+    means[:, 2] = rng.uniform(z[0], z[1], n)
+    if tie_frac > 0:  # a share of means with one identical depth (stable-sort stress)
+        k = int(n * tie_frac)
+        means[:k, 2] = np.float32(0.5 * (z[0] + z[1]))
+    q = rng.standard_normal((n, 4)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    log_s = rng.normal(log_scale_mu, log_scale_sd, (n, 3)).astype(np.float32)
+    logit = rng.standard_normal(n).astype(np.float32)
+    sh0 = rng.normal(0.0, dc_sd, (n, 3)).astype(np.float32)
+    K = (sh_degree + 1) ** 2
+    shN = rng.normal(0.0, rest_sd, (n, (K - 1) * 3)).astype(np.float32)
+    return [means, q.astype(np.float32), log_s, logit, sh0, shN]
+
+
+def pinhole(fx, fy, cx, cy):
+    return np.array([[fx, 0, cx], [0, fy, cy], [0, 0, 1]], np.float32)
+
+
+def identity_view():
+    return np.eye(4, dtype=np.float32)
+
+
+def jittered_view(rng, max_deg=5.0, max_t=0.2):
+    """World->camera matrix: rotation by <= max_deg about a random axis, translation <= max_t."""
+    axis = rng.standard_normal(3)
+    axis /= np.linalg.norm(axis)
+    ang = math.radians(rng.uniform(-max_deg, max_deg))
+    Kx = np.array([[0, -axis[2], axis[1]], [axis[2], 0, -axis[0]], [-axis[1], axis[0], 0]])
+    R = np.eye(3) + math.sin(ang) * Kx + (1 - math.cos(ang)) * Kx @ Kx
+    t = rng.standard_normal(3)
+    t = t / np.linalg.norm(t) * rng.uniform(0, max_t)
+    V = np.eye(4)
+    V[:3, :3] = R
+    V[:3, 3] = t
+    return V.astype(np.float32)
+
+
+def make_scene(n=10000, sh_degree=0, width=256, height=256, fx=230.0, seed=0, gt="uniform", **kw) -> Scene:
+    """Config-1 style scene (x,y ~ U[-2,2], z ~ U[2,10], log-scales ~ N(ln 0.02, 0.5)) with a camera at
+    the origin looking +z and a seeded U[0,1] target image."""
+    params = make_params(n, sh_degree, seed, **kw)
+    sc = Scene(n=n, sh_degree=sh_degree, params=params, width=width, height=height, viewmat=identity_view(),
+               K=pinhole(fx, fx, width / 2.0, height / 2.0))
+    if gt == "uniform":
+        rng = np.random.Generator(np.random.PCG64(seed + 1000))
+        sc.gt = rng.uniform(0.0, 1.0, (height, width, 3)).astype(np.float32)
+    return sc
+
+
+CONFIGS = {
+    # BASELINE.json configs[0..4]
+    1: dict(n=10_000, sh_degree=0, width=256, height=256, fx=230.0, isect="aabb", ssim=0.0, target="uniform"),
+    2: dict(n=100_000, sh_degree=3, width=800, height=800, fx=720.0, isect="aabb", ssim=0.2, target="scene"),
+    3: dict(n=1_000_000, sh_degree=3, width=1297, height=840, fx=1150.0, isect="accutile", ssim=0.2,
+            target="scene", xy=4.0, z=(1.5, 20.0), log_scale_mu=math.log(0.01), log_scale_sd=0.7),
+    5: dict(n=2_000_000, sh_degree=3, width=1920, height=1080, fx=1600.0, isect="accutile", ssim=0.2,
+            target="scene", xy=3.0, z=(2.0, 4.0), log_scale_mu=math.log(0.08), log_scale_sd=0.5, tie_frac=0.1,
+            antialiased=True),
+}
+
+
+def config_scene(cfg_id: int, seed: int = 0) -> tuple[Scene, dict]:
+    c = dict(CONFIGS[cfg_id])
+    kw = {k: c.pop(k) for k in ("xy", "z", "log_scale_mu", "log_scale_sd", "tie_frac") if k in c}
+    n, deg, w, h, fx = c["n"], c["sh_degree"], c["width"], c["height"], c["fx"]
+    params = make_params(n, deg, seed, **kw)
+    sc = Scene(n=n, sh_degree=deg, params=params, width=w, height=h, viewmat=identity_view(),
+               K=pinhole(fx, fx, w / 2.0, h / 2.0))
+    return sc, c
+
+
+def copy_state(sc: Scene):
+    p = [x.copy() for x in sc.params]
+    m = [np.zeros_like(x) for x in sc.params]
+    v = [np.zeros_like(x) for x in sc.params]
+    return p, m, v
+
+
+def step_kwargs(sc: Scene, degrees_to_use=None):
+    return dict(viewmat=sc.viewmat, K=sc.K, width=sc.width, height=sc.height, count=sc.n,
+                degrees_to_use=sc.sh_degree if degrees_to_use is None else degrees_to_use, lr=list(sc.lr))

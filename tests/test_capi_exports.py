@@ -1,0 +1,38 @@
+"""The C-ABI library loads and exports every entry point include/splatx_hip.h declares (no GPU use)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "splatx_hip.h")
+LIB = os.path.join(REPO, "splatx-metal_amd", "build", "libsplatx_hip.so")
+
+
+def declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(sxh_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_header_is_pure_c():
+    txt = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    for bad in ("class ", "template", "namespace", "std::", "#include <hip", "torch"):
+        assert bad not in txt.replace('extern "C"', "")
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(LIB):
+        pytest.fail("library not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(LIB)
+    names = declared()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_without_gpu():
+    lib = ctypes.CDLL(LIB)
+    lib.sxh_abi_version.restype = ctypes.c_int32
+    assert lib.sxh_abi_version() == 1

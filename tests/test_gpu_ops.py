@@ -1,0 +1,270 @@
+"""gfx950 backend (through the C ABI) against the golden fixtures and the CPU oracle.
+
+Bar: bit-exact for integer, key and index outputs and for every deterministic forward
+(projection, SH, isect, scan, sort, offsets, raster fwd, SSIM, Adam, RNG, relocation, perturb —
+the device code follows the oracle's operation order with the same transcendental layer);
+gradients whose device accumulation order differs (raster bwd atomics, float SH/projection VJPs vs
+the oracle's double accumulation) are held to rel_l2 <= 1e-4 (north star: rel 1e-4 for gradients).
+"""
+import hashlib
+
+import numpy as np
+import pytest
+
+import golden_checks as gc
+import inputs
+import splatx_hip as sh
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = [gc.check_adam, gc.check_projection_fwd, gc.check_projection_bwd, gc.check_sh, gc.check_isect_sort_offsets,
+          gc.check_raster_fwd, gc.check_raster_bwd, gc.check_ssim, gc.check_relocation, gc.check_perturb,
+          gc.check_rng]
+
+
+@pytest.mark.parametrize("check", GOLDEN, ids=lambda c: c.__name__)
+def test_gpu_goldens(gpu, check):
+    check(gpu)
+
+
+def same_bits(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    if a.dtype.kind == "f":
+        return np.array_equal(a.view(np.uint32 if a.dtype == np.float32 else np.uint64),
+                              b.view(np.uint32 if b.dtype == np.float32 else np.uint64))
+    return np.array_equal(a, b)
+
+
+def rel_l2(a, e):
+    a = np.asarray(a, np.float64).ravel()
+    e = np.asarray(e, np.float64).ravel()
+    den = np.sqrt((e * e).sum())
+    return float(np.sqrt(((a - e) ** 2).sum()) / den) if den > 0 else float(np.sqrt(((a - e) ** 2).sum()))
+
+
+# ---- projection ----------------------------------------------------------------------------
+PROJ_CASES = [dict(), dict(aa=True), dict(covars=True, n=1500), dict(C=3), dict(opacities=False),
+              dict(C=2, aa=True, n=2500)]
+
+
+@pytest.mark.parametrize("case", PROJ_CASES, ids=str)
+def test_projection_fwd_bitexact(gpu, oracle, case):
+    kw = inputs.proj_kwargs(seed=11, **case)
+    g = gpu.projection_fused_fwd(**kw)
+    o = oracle.projection_fused_fwd(**kw)
+    v = gc.valid_mask(o["radii"])
+    assert 0 < v.sum() < v.size
+    for k in ("radii", "means2d", "depths", "conics"):
+        assert same_bits(g[k], o[k]), k
+    if kw["calc_compensations"]:
+        assert same_bits(g["compensations"], o["compensations"])
+
+
+@pytest.mark.parametrize("case", [dict(), dict(aa=True), dict(covars=True, n=1500), dict(C=3)], ids=str)
+def test_projection_bwd_close(gpu, oracle, case):
+    kw = inputs.proj_kwargs(seed=12, **case)
+    f = oracle.projection_fused_fwd(**kw)
+    r = inputs.rng(5)
+    CN = f["depths"].size
+    v = gc.valid_mask(f["radii"]).reshape(f["depths"].shape)
+    gin = dict(radii=f["radii"], conics=f["conics"],
+               v_means2d=(r.standard_normal(f["means2d"].shape) * v[..., None]).astype(np.float32),
+               v_depths=(r.standard_normal(f["depths"].shape) * v).astype(np.float32),
+               v_conics=(r.standard_normal(f["conics"].shape) * v[..., None]).astype(np.float32),
+               viewmats_grad=True)
+    if kw["calc_compensations"]:
+        gin["compensations"] = f["compensations"]
+        gin["v_compensations"] = (r.standard_normal(CN) * v.ravel()).astype(np.float32).reshape(f["depths"].shape)
+    a = gpu.projection_fused_bwd(**gin, **kw)
+    b = oracle.projection_fused_bwd(**gin, **kw)
+    for k in ("v_means", "v_covars", "v_quats", "v_scales", "v_viewmats"):
+        if b[k] is not None:
+            assert rel_l2(a[k], b[k]) <= 1e-4, (k, rel_l2(a[k], b[k]))
+
+
+# ---- SH --------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("deg,K,B", [(0, 1, 1), (1, 4, 1), (2, 9, 1), (3, 16, 1), (3, 16, 2), (4, 25, 1), (2, 16, 1)])
+def test_sh_fwd_bitexact_bwd_close(gpu, oracle, deg, K, B):
+    r = inputs.rng(deg * 10 + K + B)
+    N = 3000
+    dirs = r.standard_normal((B * N, 3)).astype(np.float32)
+    coeffs = r.standard_normal((N, K, 3)).astype(np.float32)
+    masks = (r.uniform(0, 1, B * N) > 0.3).astype(np.uint8)
+    a = gpu.sh_fwd(dirs, coeffs, deg, masks=masks, B=B)
+    b = oracle.sh_fwd(dirs, coeffs, deg, masks=masks, B=B)
+    assert same_bits(a, b)
+    vc = r.standard_normal((B * N, 3)).astype(np.float32)
+    ga = gpu.sh_bwd(dirs, coeffs, deg, vc, masks=masks, B=B)
+    gb = oracle.sh_bwd(dirs, coeffs, deg, vc, masks=masks, B=B)
+    assert rel_l2(ga["v_coeffs"], gb["v_coeffs"]) <= 1e-5
+    if deg > 0:
+        assert rel_l2(ga["v_dirs"], gb["v_dirs"]) <= 1e-5
+
+
+# ---- intersection / scan / sort / offsets ----------------------------------------------------------
+@pytest.mark.parametrize("accu,I", [(True, 1), (False, 1), (True, 2), (False, 2)])
+def test_isect_bitexact(gpu, oracle, accu, I):
+    kw = inputs.isect_kwargs(oracle, n=5000, seed=21 + I, accutile=accu, I=I)
+    a = gpu.isect_tiles(**kw)
+    b = oracle.isect_tiles(**kw)
+    assert a["n_isects"] == b["n_isects"] > 0
+    for k in ("tiles_per_gauss", "isect_ids", "flatten_ids"):
+        assert np.array_equal(a[k], b[k]), k
+
+
+@pytest.mark.parametrize("n", [1, 7, 255, 256, 4095, 4096, 4097, 100_000, 1_000_003])
+def test_scan_exact(gpu, n):
+    r = inputs.rng(n)
+    x = r.integers(0, 3000, n).astype(np.int32)
+    if n > 10:
+        x[r.integers(0, n, 3)] = 2_000_000_000  # int64 promotion
+    assert np.array_equal(gpu.prefix_scan_i64(x), np.cumsum(x.astype(np.int64)))
+
+
+@pytest.mark.parametrize("n", [0, 1, 255, 256, 1023, 1024, 4095, 4096, 4097, 65_537, 300_001])
+@pytest.mark.parametrize("bits", [4, 13, 36, 45, 64])
+def test_sort_matches_stable_sort(gpu, n, bits):
+    keys, vals = inputs.sort_inputs(n, bits, seed=n + bits)
+    ks, vs = gpu.sort_isect(keys, vals, bits)
+    rk, rv = inputs.stable_sort_ref(keys, vals)
+    assert np.array_equal(ks, rk) and np.array_equal(vs, rv)
+
+
+def test_sort_3m_with_ties_and_determinism(gpu):
+    keys, vals = inputs.sort_inputs(3_000_000, 45, seed=3)
+    rk, rv = inputs.stable_sort_ref(keys, vals)
+    digests = set()
+    for _ in range(5):
+        ks, vs = gpu.sort_isect(keys, vals, 45)
+        assert np.array_equal(ks, rk) and np.array_equal(vs, rv)
+        digests.add(hashlib.sha1(ks.tobytes() + vs.tobytes()).hexdigest())
+    assert len(digests) == 1
+
+
+def test_offsets_doc_example_and_edges(gpu, oracle):
+    # IsectTests/ScanTests doc example: tile ids [1,1,1,3,3] over 6 tiles -> [0,0,3,3,5,5]
+    ids = (np.array([1, 1, 1, 3, 3], np.uint64) << np.uint64(32))
+    assert list(gpu.isect_offset_encode(ids, 1, 6, 1)) == [0, 0, 3, 3, 5, 5]
+    assert list(gpu.isect_offset_encode(np.zeros(0, np.uint64), 1, 6, 1)) == [0] * 6
+    kw = inputs.isect_kwargs(oracle, n=4000, seed=31, I=2)
+    it = oracle.isect_tiles(**kw)
+    ks, _ = oracle.sort_isect(it["isect_ids"], it["flatten_ids"], 32 + it["tile_n_bits"] + it["image_n_bits"])
+    a = gpu.isect_offset_encode(ks, 2, kw["tile_width"], kw["tile_height"])
+    b = oracle.isect_offset_encode(ks, 2, kw["tile_width"], kw["tile_height"])
+    assert np.array_equal(a, b)
+
+
+# ---- raster ----------------------------------------------------------------------------------------------
+RASTER_CASES = [dict(), dict(backgrounds=True), dict(masks=True, backgrounds=True), dict(I=2), dict(accutile=False),
+                dict(n=12000, width=333, height=171)]
+
+
+@pytest.mark.parametrize("case", RASTER_CASES, ids=str)
+def test_raster_fwd_bitexact_bwd_close(gpu, oracle, case):
+    kw = inputs.raster_kwargs(oracle, seed=41, **case)
+    a = gpu.rasterize_fwd(**kw)
+    b = oracle.rasterize_fwd(**kw)
+    for k in ("render_colors", "render_alphas", "last_ids"):
+        assert same_bits(a[k], b[k]), k
+    a2 = gpu.rasterize_fwd(**kw)
+    assert same_bits(a2["render_colors"], a["render_colors"])  # run-to-run determinism
+    r = inputs.rng(9)
+    gin = dict(render_alphas=b["render_alphas"], last_ids=b["last_ids"],
+               v_render_colors=r.standard_normal(b["render_colors"].shape).astype(np.float32),
+               v_render_alphas=r.standard_normal(b["render_alphas"].shape).astype(np.float32))
+    ga = gpu.rasterize_bwd(absgrad=True, **gin, **kw)
+    gb = oracle.rasterize_bwd(absgrad=True, **gin, **kw)
+    for k in ("v_means2d", "v_conics", "v_colors", "v_opacities", "v_means2d_abs"):
+        assert rel_l2(ga[k], gb[k]) <= 1e-4, (k, rel_l2(ga[k], gb[k]))
+    gc2 = gpu.rasterize_bwd(absgrad=True, **gin, **kw)  # self-consistency of the atomic path
+    for k in ("v_means2d", "v_conics", "v_colors", "v_opacities"):
+        assert rel_l2(gc2[k], ga[k]) <= 1e-5
+
+
+def test_raster_empty_and_background(gpu, oracle):
+    kw = inputs.raster_kwargs(oracle, seed=43, backgrounds=True)
+    kw["n_isects"] = 0
+    kw["flatten_ids"] = np.zeros(0, np.int32)
+    kw["isect_offsets"] = np.zeros_like(kw["isect_offsets"])
+    a = gpu.rasterize_fwd(**kw)
+    b = oracle.rasterize_fwd(**kw)
+    assert same_bits(a["render_colors"], b["render_colors"])
+    assert np.allclose(a["render_colors"][0], kw["backgrounds"][0])
+
+
+# ---- SSIM -------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(1, 24, 24, 3), (1, 37, 53, 3), (2, 16, 40, 1), (1, 200, 301, 3)])
+def test_ssim_bitexact(gpu, oracle, shape):
+    r = inputs.rng(sum(shape))
+    x = r.uniform(0, 1, shape).astype(np.float32)
+    y = np.clip(x * 0.9 + r.normal(0, 0.05, shape), 0, 1).astype(np.float32)
+    a = gpu.ssim_fwd(x, y, need_coeffs=True)
+    b = oracle.ssim_fwd(x, y, need_coeffs=True)
+    for k in ("ssim_map", "coeff_mu", "coeff_sigma", "coeff_cross"):
+        assert same_bits(a[k], b[k]), k
+    assert a["ssim"] == b["ssim"]
+    va = gpu.ssim_bwd(x, y, a["coeff_mu"], a["coeff_sigma"], a["coeff_cross"], 0.2)
+    vb = oracle.ssim_bwd(x, y, b["coeff_mu"], b["coeff_sigma"], b["coeff_cross"], 0.2)
+    assert same_bits(va, vb)
+
+
+# ---- Adam / RNG / MCMC -------------------------------------------------------------------------------------
+def test_adam_bitexact(gpu, oracle):
+    r = inputs.rng(3)
+    N, D = 50_000, 7
+    p, g = r.standard_normal((N, D)).astype(np.float32), r.standard_normal((N, D)).astype(np.float32)
+    m, v = r.standard_normal((N, D)).astype(np.float32), np.abs(r.standard_normal((N, D))).astype(np.float32)
+    valid = (r.uniform(0, 1, N) > 0.4).astype(np.uint8)
+    outs = []
+    for ops in (gpu, oracle):
+        pp, mm, vv = p.copy(), m.copy(), v.copy()
+        ops.fused_adam(pp, g, mm, vv, valid, N, 1e-3, 0.9, 0.999, 1e-15)
+        outs.append((pp, mm, vv))
+    for x, y in zip(*outs):
+        assert same_bits(x, y)
+
+
+def test_rng_bitexact(gpu, oracle):
+    for seed, off, count in ((0, 0, 4), (0xDEADBEEFCAFEF00D, 7, 1021), (0x853C49E6748FEA9B, 2**33 + 5, 100_003)):
+        assert np.array_equal(gpu.rng_philox_u32(seed, off, count), oracle.rng_philox_u32(seed, off, count))
+        assert same_bits(gpu.rng_normal_f32(seed, off, count), oracle.rng_normal_f32(seed, off, count))
+    z = gpu.rng_normal_f32(1, 0, 1_000_000)
+    assert abs(z.mean()) < 5e-3 and abs(z.std() - 1) < 5e-3
+
+
+def test_relocation_and_perturb_bitexact(gpu, oracle):
+    r = inputs.rng(4)
+    N = 5000
+    op = r.uniform(0.001, 0.999, N).astype(np.float32)
+    sc = np.exp(r.normal(-3, 1, (N, 3))).astype(np.float32)
+    ratios = r.integers(1, 52, N).astype(np.int32)
+    binoms = oracle.make_binoms_lut(51)
+    assert same_bits(gpu.make_binoms_lut(51), binoms)
+    a = gpu.mcmc_relocation(op, sc, ratios, binoms)
+    b = oracle.mcmc_relocation(op, sc, ratios, binoms)
+    assert same_bits(a[0], b[0]) and same_bits(a[1], b[1])
+    pos = r.standard_normal((N, 3)).astype(np.float32)
+    args = (r.standard_normal((N, 4)).astype(np.float32), r.normal(-3, 1, (N, 3)).astype(np.float32),
+            r.standard_normal(N).astype(np.float32), r.standard_normal((N, 3)).astype(np.float32))
+    pa, pb = pos.copy(), pos.copy()
+    gpu.mcmc_perturb_positions(pa, *args, 0.05)
+    oracle.mcmc_perturb_positions(pb, *args, 0.05)
+    assert same_bits(pa, pb)
+
+
+# ---- error contract (Validate.h) -----------------------------------------------------------------------
+def test_validation_errors(gpu):
+    kw = inputs.proj_kwargs(n=10)
+    with pytest.raises(sh.SxRuntimeError):
+        gpu.projection_fused_fwd(**dict(kw, camera_model=1))
+    with pytest.raises(sh.SxInvalidArgument):
+        gpu.sort_isect(np.zeros(4, np.uint64), np.zeros(4, np.int32), 65)
+    with pytest.raises(sh.SxInvalidArgument):
+        gpu.sh_fwd(np.zeros((4, 3), np.float32), np.zeros((4, 4, 3), np.float32), 2)
+    with pytest.raises(sh.SxInvalidArgument):
+        gpu.mcmc_relocation(np.full(3, 0.5, np.float32), np.ones((3, 3), np.float32), np.array([1, 0, 2], np.int32),
+                            gpu.make_binoms_lut(51))
+    x = np.zeros((1, 10, 20, 3), np.float32)
+    with pytest.raises(sh.SxInvalidArgument):
+        gpu.ssim_fwd(x, x)
