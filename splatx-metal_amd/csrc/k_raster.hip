@@ -7,8 +7,9 @@
 // the CPU reference's order (CpuKernels.cpp:821-849) and the deterministic exp of sx_fmath.h, so
 // colors/alphas/last_ids are bit-identical to the CPU oracle; the workgroup exits as soon as all
 // its pixels are done.
-// Backward: back-to-front walk recovering T by division, per-wave reduction of the nine gradient
-// components through cross-lane shuffles, one set of float atomics per wave and Gaussian.
+// Backward: back-to-front walk recovering T by division; the nine gradient components of each
+// (Gaussian, wave) are summed over the wave with DPP row operations, the four waves of the tile are
+// combined in LDS once per batch, and one set of float atomics per (tile, Gaussian) is issued.
 #include <hip/hip_runtime.h>
 
 #include "sx_dev.h"
@@ -35,9 +36,18 @@ __device__ __forceinline__ PixelEval eval_weight(float ca, float cb, float cc, f
     return e;
 }
 
+__device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx, float dy) {
+    return 0.5f * (ca * dx * dx + cc * dy * dy) + cb * dx * dy;
+}
+
+// Largest sigma for which opacity * exp(-sigma) can still reach the 1/255 alpha threshold, plus a
+// 0.01 margin: any pair with sigma above it is invalid in the exact evaluation too (its alpha is at
+// most e^-0.01/255), so skipping its exp leaves every result bit-identical.
+__device__ __forceinline__ float sigma_cutoff(float opac) { return __logf(opac * 255.0f) + 0.01f; }
+
 __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __restrict__ out_rgb,
                                                          float* __restrict__ out_alpha, int32_t* __restrict__ out_last) {
-    __shared__ float4 s_xyo[kThreads];
+    __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
     __shared__ float4 s_con[kThreads];
     __shared__ float4 s_rgb[kThreads];
     const int n_tiles = a.tile_width * a.tile_height;
@@ -71,7 +81,9 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
         const int32_t idx = bstart + tid;
         if (idx < range_end) {
             const int32_t g = a.flatten_ids[idx];
-            s_xyo[tid] = a.splats[(size_t)g * 3];
+            float4 xyo = a.splats[(size_t)g * 3];
+            xyo.w = sigma_cutoff(xyo.z);
+            s_xyo[tid] = xyo;
             s_con[tid] = a.splats[(size_t)g * 3 + 1];
             s_rgb[tid] = a.splats[(size_t)g * 3 + 2];
         }
@@ -81,7 +93,10 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             for (int t = 0; t < cnt; t++) {
                 const float4 xyo = s_xyo[t];
                 const float4 con = s_con[t];
-                const PixelEval e = eval_weight(con.x, con.y, con.z, xyo.x - px, xyo.y - py, xyo.z);
+                const float dx = xyo.x - px, dy = xyo.y - py;
+                const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
+                if (sigma > xyo.w) continue;  // provably below the alpha threshold
+                const PixelEval e = eval_weight(con.x, con.y, con.z, dx, dy, xyo.z);
                 if (!e.valid) continue;
                 const float next_T = T * (1.0f - e.alpha);
                 if (next_T <= sx::kTransmittanceThreshold) {
@@ -106,20 +121,43 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     out_last[pix] = cur;
 }
 
+// ---- 64-lane sums through DPP (gfx9 data-parallel primitives) -----------------------------------
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+// Sum over the wave; the total is exact in lane 63 (other lanes hold partial sums).
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v += dpp_f<0xB1, 0xF>(v);   // quad_perm(1,0,3,2): pairs
+    v += dpp_f<0x4E, 0xF>(v);   // quad_perm(2,3,0,1): quads
+    v += dpp_f<0x141, 0xF>(v);  // row_half_mirror: 8 lanes
+    v += dpp_f<0x140, 0xF>(v);  // row_mirror: 16-lane row
+    v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+constexpr int kGrads = 9;  // v_xy(2), v_opacity, v_conic(3), v_rgb(3)
+
+template <bool ABSGRAD>
 __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const float* __restrict__ ralpha,
                                                          const int32_t* __restrict__ last_ids,
                                                          const float* __restrict__ v_rc, const float* __restrict__ v_ra,
                                                          RasterBwdGrads g) {
-    __shared__ float4 s_xyo[kThreads];
+    constexpr int NV = ABSGRAD ? kGrads + 2 : kGrads;
+    __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
     __shared__ float4 s_con[kThreads];
     __shared__ float4 s_rgb[kThreads];
     __shared__ int32_t s_id[kThreads];
+    __shared__ float s_part[kThreads / 64][NV][kThreads];  // per-wave sums, Gaussian-minor
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
     const int tile = blockIdx.x % n_tiles;
     if (a.masks && a.masks[(size_t)img * n_tiles + tile] == 0) return;  // uniform
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const bool lane63 = (tid & 63) == 63;
     const int px_i = tx * 16 + (tid & 15), py_i = ty * 16 + (tid >> 4);
     const bool inside = px_i < a.width && py_i < a.height;
     const size_t pix = inside ? (size_t)img * a.height * a.width + (size_t)py_i * a.width + px_i
@@ -137,7 +175,6 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     const float va = v_ra[pix];
     const float bg_dot = bg ? (bg[0] * vc0 + bg[1] * vc1 + bg[2] * vc2) : 0.f;
     const int32_t wave_bin_final = sxd::wave_max_i(bin_final);
-    const bool absgrad = g.v_means2d_abs != nullptr;
     const int32_t num = range_end - range_start;
     const int num_batches = (num + kThreads - 1) / kThreads;
     for (int b = 0; b < num_batches; b++) {
@@ -148,92 +185,114 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
         if (idx >= range_start) {
             const int32_t gid = a.flatten_ids[idx];
             s_id[tid] = gid;
-            s_xyo[tid] = a.splats[(size_t)gid * 3];
+            float4 xyo = a.splats[(size_t)gid * 3];
+            xyo.w = sigma_cutoff(xyo.z);
+            s_xyo[tid] = xyo;
             s_con[tid] = a.splats[(size_t)gid * 3 + 1];
             s_rgb[tid] = a.splats[(size_t)gid * 3 + 2];
         }
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; w++)
+#pragma unroll
+            for (int k = 0; k < NV; k++) s_part[w][k][tid] = 0.f;
         __syncthreads();
         for (int t = max(0, batch_end - wave_bin_final); t < batch_size; t++) {
-            bool valid = inside && (batch_end - t) <= bin_final;
-            float4 xyo = make_float4(0.f, 0.f, 0.f, 0.f), con = xyo;
-            PixelEval e{0.f, 0.f, 0.f, false};
-            float dx = 0.f, dy = 0.f;
-            if (valid) {
-                xyo = s_xyo[t];
-                con = s_con[t];
-                dx = xyo.x - px;
-                dy = xyo.y - py;
-                e = eval_weight(con.x, con.y, con.z, dx, dy, xyo.z);
-                valid = e.valid;
-            }
-            if (!__any(valid)) continue;  // wave-uniform
+            const float4 xyo = s_xyo[t];
+            const float4 con = s_con[t];
+            const float dx = xyo.x - px, dy = xyo.y - py;
+            const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
+            bool valid = inside && (batch_end - t) <= bin_final && !(sigma > xyo.w);
+            if (!__any(valid)) continue;  // wave-uniform, before any exp
             float g_r = 0.f, g_g = 0.f, g_b = 0.f, g_ca = 0.f, g_cb = 0.f, g_cc = 0.f, g_x = 0.f, g_y = 0.f,
                   g_o = 0.f, g_ax = 0.f, g_ay = 0.f;
             if (valid) {
-                const float ra = 1.0f / sxd::smax(sx::kMinOneMinusAlpha, 1.0f - e.alpha);
-                T *= ra;
-                const float fac = e.alpha * T;
-                const float4 c = s_rgb[t];
-                g_r = fac * vc0;
-                g_g = fac * vc1;
-                g_b = fac * vc2;
-                float v_alpha = (c.x * T - b0 * ra) * vc0 + (c.y * T - b1 * ra) * vc1 + (c.z * T - b2 * ra) * vc2;
-                v_alpha += T_final * ra * va;
-                if (bg) v_alpha += -T_final * ra * bg_dot;
-                const float opac = xyo.z;
-                if (opac * e.vis <= sx::kMaxAlpha) {
-                    const float v_sigma = -opac * e.vis * v_alpha;
-                    g_ca = 0.5f * v_sigma * dx * dx;
-                    g_cb = v_sigma * dx * dy;
-                    g_cc = 0.5f * v_sigma * dy * dy;
-                    g_x = v_sigma * (con.x * dx + con.y * dy);
-                    g_y = v_sigma * (con.y * dx + con.z * dy);
-                    g_ax = fabsf(g_x);
-                    g_ay = fabsf(g_y);
-                    g_o = e.vis * v_alpha;
+                const PixelEval e = eval_weight(con.x, con.y, con.z, dx, dy, xyo.z);
+                if (e.valid) {
+                    const float ra = 1.0f / sxd::smax(sx::kMinOneMinusAlpha, 1.0f - e.alpha);
+                    T *= ra;
+                    const float fac = e.alpha * T;
+                    const float4 c = s_rgb[t];
+                    g_r = fac * vc0;
+                    g_g = fac * vc1;
+                    g_b = fac * vc2;
+                    float v_alpha = (c.x * T - b0 * ra) * vc0 + (c.y * T - b1 * ra) * vc1 + (c.z * T - b2 * ra) * vc2;
+                    v_alpha += T_final * ra * va;
+                    if (bg) v_alpha += -T_final * ra * bg_dot;
+                    const float opac = xyo.z;
+                    if (opac * e.vis <= sx::kMaxAlpha) {
+                        const float v_sigma = -opac * e.vis * v_alpha;
+                        g_ca = 0.5f * v_sigma * dx * dx;
+                        g_cb = v_sigma * dx * dy;
+                        g_cc = 0.5f * v_sigma * dy * dy;
+                        g_x = v_sigma * (con.x * dx + con.y * dy);
+                        g_y = v_sigma * (con.y * dx + con.z * dy);
+                        if (ABSGRAD) {
+                            g_ax = fabsf(g_x);
+                            g_ay = fabsf(g_y);
+                        }
+                        g_o = e.vis * v_alpha;
+                    }
+                    b0 += c.x * fac;
+                    b1 += c.y * fac;
+                    b2 += c.z * fac;
                 }
-                b0 += c.x * fac;
-                b1 += c.y * fac;
-                b2 += c.z * fac;
             }
-            g_r = sxd::wave_sum(g_r);
-            g_g = sxd::wave_sum(g_g);
-            g_b = sxd::wave_sum(g_b);
-            g_ca = sxd::wave_sum(g_ca);
-            g_cb = sxd::wave_sum(g_cb);
-            g_cc = sxd::wave_sum(g_cc);
-            g_x = sxd::wave_sum(g_x);
-            g_y = sxd::wave_sum(g_y);
-            g_o = sxd::wave_sum(g_o);
-            if (absgrad) {
-                g_ax = sxd::wave_sum(g_ax);
-                g_ay = sxd::wave_sum(g_ay);
+            const float s0 = wave_sum_lane63(g_x), s1 = wave_sum_lane63(g_y), s2 = wave_sum_lane63(g_o);
+            const float s3 = wave_sum_lane63(g_ca), s4 = wave_sum_lane63(g_cb), s5 = wave_sum_lane63(g_cc);
+            const float s6 = wave_sum_lane63(g_r), s7 = wave_sum_lane63(g_g), s8 = wave_sum_lane63(g_b);
+            float s9 = 0.f, s10 = 0.f;
+            if (ABSGRAD) {
+                s9 = wave_sum_lane63(g_ax);
+                s10 = wave_sum_lane63(g_ay);
             }
-            if (sxd::lane_id() == 0 && g.packed) {
-                float* rec = reinterpret_cast<float*>(g.packed + (size_t)s_id[t] * 3);
-                atomicAdd(&rec[0], g_x);
-                atomicAdd(&rec[1], g_y);
-                atomicAdd(&rec[2], g_o);
-                atomicAdd(&rec[4], g_ca);
-                atomicAdd(&rec[5], g_cb);
-                atomicAdd(&rec[6], g_cc);
-                atomicAdd(&rec[8], g_r);
-                atomicAdd(&rec[9], g_g);
-                atomicAdd(&rec[10], g_b);
-            } else if (sxd::lane_id() == 0) {
-                const int32_t gid = s_id[t];
-                atomicAdd(&g.v_colors[(size_t)gid * 3], g_r);
-                atomicAdd(&g.v_colors[(size_t)gid * 3 + 1], g_g);
-                atomicAdd(&g.v_colors[(size_t)gid * 3 + 2], g_b);
-                atomicAdd(&g.v_conics[(size_t)gid * 3], g_ca);
-                atomicAdd(&g.v_conics[(size_t)gid * 3 + 1], g_cb);
-                atomicAdd(&g.v_conics[(size_t)gid * 3 + 2], g_cc);
-                atomicAdd(&g.v_means2d[(size_t)gid * 2], g_x);
-                atomicAdd(&g.v_means2d[(size_t)gid * 2 + 1], g_y);
-                atomicAdd(&g.v_opacities[gid], g_o);
-                if (absgrad) {
-                    atomicAdd(&g.v_means2d_abs[(size_t)gid * 2], g_ax);
-                    atomicAdd(&g.v_means2d_abs[(size_t)gid * 2 + 1], g_ay);
+            if (lane63) {
+                float* p = &s_part[wave][0][t];
+                p[0 * kThreads] = s0; p[1 * kThreads] = s1; p[2 * kThreads] = s2;
+                p[3 * kThreads] = s3; p[4 * kThreads] = s4; p[5 * kThreads] = s5;
+                p[6 * kThreads] = s6; p[7 * kThreads] = s7; p[8 * kThreads] = s8;
+                if (ABSGRAD) {
+                    p[9 * kThreads] = s9;
+                    p[10 * kThreads] = s10;
+                }
+            }
+        }
+        __syncthreads();
+        // one thread per Gaussian of the batch: combine the four waves, then one atomic per component
+        if (tid < batch_size) {
+            float v[NV];
+            bool any = false;
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                v[k] = s_part[0][k][tid] + s_part[1][k][tid] + s_part[2][k][tid] + s_part[3][k][tid];
+                any |= v[k] != 0.f;
+            }
+            if (any) {
+                const int32_t gid = s_id[tid];
+                if (g.packed) {
+                    float* rec = reinterpret_cast<float*>(g.packed + (size_t)gid * 3);
+                    atomicAdd(&rec[0], v[0]);
+                    atomicAdd(&rec[1], v[1]);
+                    atomicAdd(&rec[2], v[2]);
+                    atomicAdd(&rec[4], v[3]);
+                    atomicAdd(&rec[5], v[4]);
+                    atomicAdd(&rec[6], v[5]);
+                    atomicAdd(&rec[8], v[6]);
+                    atomicAdd(&rec[9], v[7]);
+                    atomicAdd(&rec[10], v[8]);
+                } else {
+                    atomicAdd(&g.v_means2d[(size_t)gid * 2], v[0]);
+                    atomicAdd(&g.v_means2d[(size_t)gid * 2 + 1], v[1]);
+                    atomicAdd(&g.v_opacities[gid], v[2]);
+                    atomicAdd(&g.v_conics[(size_t)gid * 3], v[3]);
+                    atomicAdd(&g.v_conics[(size_t)gid * 3 + 1], v[4]);
+                    atomicAdd(&g.v_conics[(size_t)gid * 3 + 2], v[5]);
+                    atomicAdd(&g.v_colors[(size_t)gid * 3], v[6]);
+                    atomicAdd(&g.v_colors[(size_t)gid * 3 + 1], v[7]);
+                    atomicAdd(&g.v_colors[(size_t)gid * 3 + 2], v[8]);
+                    if (ABSGRAD) {
+                        atomicAdd(&g.v_means2d_abs[(size_t)gid * 2], v[9]);
+                        atomicAdd(&g.v_means2d_abs[(size_t)gid * 2 + 1], v[10]);
+                    }
                 }
             }
         }
@@ -252,7 +311,10 @@ void raster_bwd(const RasterArgs& a, const float* ralpha, const int32_t* last_id
                 const float* v_ra, const RasterBwdGrads& g, hipStream_t s) {
     const int blocks = a.I * a.tile_width * a.tile_height;
     if (blocks <= 0 || a.n_isects <= 0) return;
-    hipLaunchKernelGGL(k_raster_bwd, dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc, v_ra, g);
+    if (g.v_means2d_abs)
+        hipLaunchKernelGGL(k_raster_bwd<true>, dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc, v_ra, g);
+    else
+        hipLaunchKernelGGL(k_raster_bwd<false>, dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc, v_ra, g);
 }
 
 } // namespace sxk
