@@ -65,14 +65,54 @@ def cpu_baseline(sc, pose, gt, lr) -> dict:
 
     orc = oracle_py.Oracle(libm=False)
     p, m, v = scene.copy_state(sc)
+    n_steps = 2
+    stages = {}
     t0 = time.perf_counter()
-    r = orc.train_step(p, m, v, sc.n, sc.sh_degree, pose, sc.K, sc.width, sc.height, gt, sc.sh_degree, lr,
-                       ssim_weight=0.2, want_render=False)
-    dt = (time.perf_counter() - t0) * 1000.0
+    for _ in range(n_steps):
+        r = orc.train_step(p, m, v, sc.n, sc.sh_degree, pose, sc.K, sc.width, sc.height, gt, sc.sh_degree, lr,
+                           ssim_weight=0.2, want_render=False)
+        for k, x in r["stage_ms"].items():
+            stages[k] = stages.get(k, 0.0) + x / n_steps
+    dt = (time.perf_counter() - t0) * 1000.0 / n_steps
     return {"value": round(dt, 1), "unit": "ms/iter", "cores": 1, "kind": "port",
-            "sample": "one full fwd+bwd+Adam step of the same config-3 workload (N=1M, SH3, 1297x840, AccuTile, "
-                      "SSIM) by the single-threaded CPU oracle", "n_isects": r["n_isects"],
-            "stages_ms": {k: round(x, 1) for k, x in r["stage_ms"].items() if x > 0}}
+            "sample": f"{n_steps} consecutive full fwd+bwd+Adam steps of the same config-3 workload (N=1M, SH3, "
+                      "1297x840, AccuTile, SSIM; first timed pose and its target) by the single-threaded CPU oracle",
+            "n_isects": r["n_isects"], "stages_ms": {k: round(x, 1) for k, x in stages.items() if x > 0}}
+
+
+def calibrate_copy(mib: int, reps: int = 4) -> None:
+    """Device-to-device copies of a known size (the runtime's copy kernel), as the yardstick that scales
+    the FETCH_SIZE / WRITE_SIZE counters of a `rocprofv3 --pmc` run into HBM bytes."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = mib << 20
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    for p in (a, b):
+        if hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(n)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    if hip.hipMemset(a, 1, ctypes.c_size_t(n)) != 0:
+        raise RuntimeError("hipMemset failed")
+    for _ in range(reps):
+        if hip.hipMemcpy(b, a, ctypes.c_size_t(n), 3) != 0:  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+    print(json.dumps({"calibrate_copy_bytes": n, "reps": reps}), flush=True)
+
+
+def load_traffic(kernel: str, cfg: int):
+    """HBM bytes per launch of `kernel`, as measured by the counter runs recorded in profiles/traffic.json
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel yardstick); None if not recorded."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    k = rec.get("kernels", {}).get(kernel)
+    if k is None or rec.get("config") != cfg:
+        return None
+    return k["hbm_bytes"]
 
 
 def main():
@@ -82,11 +122,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run device copies of MIB MiB (yardstick for the HBM byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the step has no multi-GPU "
               f"path — run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy > 0:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     sc, cfg = scene.config_scene(args.config, seed=0)
     tgt, _ = scene.config_scene(args.config, seed=1)
@@ -180,7 +225,8 @@ def main():
         "step_alg_GB": round(step_bytes / 1e9, 4),
         "step_hbm_roofline_frac": round(step_bytes / 1e9 / (ms_per_step / 1e3) / HBM_PEAK_GBS, 5),
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic(dom, args.config), "alg_bytes": round(dom_bytes)},
         "kernels": per_kernel,
         "host_waits_ms": {k: round(avg[k], 4) for k in avg if k.startswith("host_")},
     }
