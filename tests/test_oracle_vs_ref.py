@@ -1,0 +1,183 @@
+"""The oracle's restatement against the reference's own CPU code (oracle/_ref), on seeded inputs.
+
+oracle/_ref/libsx_ref.so is Sources/SplatXCore/CpuKernels.cpp + Math.cpp compiled in place from the
+reference tree (oracle/Makefile, target `ref`); it exists only where the reference tree does, so
+these tests skip elsewhere. The glibc build of the oracle (liboracle_libm.so) must agree with it
+bit for bit on every forward op the reference implements on the CPU (CpuBackend.cpp:6-51); the
+deterministic-transcendental build (liboracle.so, the one the GPU is compared with) must agree on
+every integer output and to within a few float ulps elsewhere.
+"""
+import numpy as np
+import pytest
+
+import inputs
+
+pytestmark = pytest.mark.filterwarnings("ignore::RuntimeWarning")
+
+
+def same_bits(a, b):
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype
+    return np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def close(a, b, rtol=2e-6, atol=1e-7):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    np.testing.assert_allclose(a, b, rtol=rtol, atol=atol)
+
+
+PROJ_CASES = [dict(seed=1), dict(seed=2, aa=True), dict(seed=3, covars=True, n=500),
+              dict(seed=4, C=2, aa=True), dict(seed=5, opacities=False)]
+
+
+@pytest.mark.parametrize("case", PROJ_CASES, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_projection_fwd(reference, oracle_libm, oracle, case):
+    kw = inputs.proj_kwargs(**case)
+    r = reference.projection_fused_fwd(**kw)
+    o = oracle_libm.projection_fused_fwd(**kw)
+    s = oracle.projection_fused_fwd(**kw)
+    valid = r["radii"][..., 0] > 0
+    assert valid.sum() > 50
+    assert same_bits(o["radii"], r["radii"])
+    for k in ("means2d", "depths", "conics", "compensations"):
+        if r[k] is None:
+            continue
+        assert same_bits(o[k][valid], r[k][valid]), k
+    # deterministic transcendentals: radii may differ only where a radius sits on an integer edge
+    assert (s["radii"] != r["radii"]).any(axis=-1).mean() < 1e-3
+    both = valid & (s["radii"][..., 0] > 0)
+    for k in ("means2d", "depths", "conics", "compensations"):
+        if r[k] is not None:
+            close(s[k][both], r[k][both], rtol=1e-5, atol=1e-6)
+
+
+def test_quat_scale_to_covar(reference, oracle_libm):
+    r = inputs.rng(11)
+    q = r.standard_normal((2000, 4)).astype(np.float32)
+    s = np.exp(r.normal(-2.0, 1.0, (2000, 3))).astype(np.float32)
+    assert same_bits(oracle_libm.quat_scale_to_covar(q, s), reference.quat_scale_to_covar(q, s))
+
+
+@pytest.mark.parametrize("deg", [0, 1, 2, 3, 4])
+def test_sh_fwd(reference, oracle_libm, oracle, deg):
+    r = inputs.rng(20 + deg)
+    n, K = 3000, 25 if deg == 4 else 16
+    dirs = r.standard_normal((n, 3)).astype(np.float32)
+    coeffs = r.normal(0, 0.5, (n, K, 3)).astype(np.float32)
+    masks = (r.uniform(size=n) > 0.1).astype(np.uint8)
+    ref = reference.sh_fwd(dirs, coeffs, deg, masks=masks)
+    assert same_bits(oracle_libm.sh_fwd(dirs, coeffs, deg, masks=masks), ref)
+    assert same_bits(oracle.sh_fwd(dirs, coeffs, deg, masks=masks), ref)  # no transcendentals in SH
+
+
+@pytest.mark.parametrize("accutile", [True, False])
+@pytest.mark.parametrize("I", [1, 2])
+def test_isect_sort_offsets(reference, oracle_libm, accutile, I):
+    kw = inputs.isect_kwargs(oracle_libm, n=3000, seed=30 + I, accutile=accutile, I=I)
+    r = reference.isect_tiles(**kw)
+    o = oracle_libm.isect_tiles(**kw)
+    assert r["n_isects"] > 1000
+    for k in ("tiles_per_gauss", "isect_ids", "flatten_ids"):
+        assert same_bits(o[k], r[k]), k
+    assert (o["tile_n_bits"], o["image_n_bits"]) == (r["tile_n_bits"], r["image_n_bits"])
+    bits = 32 + r["tile_n_bits"] + r["image_n_bits"]
+    rk, rv = reference.sort_isect(r["isect_ids"], r["flatten_ids"], bits)
+    ok, ov = oracle_libm.sort_isect(r["isect_ids"], r["flatten_ids"], bits)
+    assert same_bits(ok, rk) and same_bits(ov, rv)
+    ro = reference.isect_offset_encode(rk, I, kw["tile_width"], kw["tile_height"])
+    oo = oracle_libm.isect_offset_encode(rk, I, kw["tile_width"], kw["tile_height"])
+    assert same_bits(oo, ro)
+
+
+def test_isect_with_deterministic_exp_matches(reference, oracle):
+    """AccuTile uses log/sqrt of the opacity level set: the sx build must give the same tile sets."""
+    kw = inputs.isect_kwargs(oracle, n=3000, seed=41, accutile=True)
+    r = reference.isect_tiles(**kw)
+    s = oracle.isect_tiles(**kw)
+    assert np.mean(s["tiles_per_gauss"] != r["tiles_per_gauss"]) < 1e-3
+
+
+@pytest.mark.parametrize("bg,masks", [(False, False), (True, False), (True, True)])
+def test_rasterize_fwd(reference, oracle_libm, bg, masks):
+    kw = inputs.raster_kwargs(oracle_libm, n=2500, seed=50, backgrounds=bg, masks=masks)
+    r = reference.rasterize_fwd(**kw)
+    o = oracle_libm.rasterize_fwd(**kw)
+    assert r["render_alphas"].max() > 0.5
+    for k in ("render_colors", "render_alphas", "last_ids"):
+        assert same_bits(o[k], r[k]), k
+
+
+def test_rasterize_fwd_deterministic_exp_close(reference, oracle):
+    kw = inputs.raster_kwargs(oracle, n=2500, seed=51)
+    r = reference.rasterize_fwd(**kw)
+    s = oracle.rasterize_fwd(**kw)
+    close(s["render_colors"], r["render_colors"], rtol=1e-5, atol=1e-6)
+    assert np.mean(s["last_ids"] != r["last_ids"]) < 1e-3
+
+
+def test_ssim_fwd(reference, oracle_libm):
+    r = inputs.rng(60)
+    a = r.uniform(0, 1, (1, 40, 53, 3)).astype(np.float32)
+    b = np.clip(a + r.normal(0, 0.1, a.shape), 0, 1).astype(np.float32)
+    ref = reference.ssim_fwd(a, b, need_coeffs=True)
+    o = oracle_libm.ssim_fwd(a, b, need_coeffs=True)
+    assert o["ssim"] == ref["ssim"]
+    for k in ("ssim_map", "coeff_mu", "coeff_sigma", "coeff_cross"):
+        assert same_bits(o[k], ref[k]), k
+
+
+def test_adam(reference, oracle_libm):
+    r = inputs.rng(70)
+    n, d = 5000, 3
+    p0 = r.standard_normal((n, d)).astype(np.float32)
+    g = r.standard_normal((n, d)).astype(np.float32)
+    m0 = r.normal(0, 0.1, (n, d)).astype(np.float32)
+    v0 = r.uniform(0, 0.1, (n, d)).astype(np.float32)
+    valid = (r.uniform(size=n) > 0.3).astype(np.uint8)
+    outs = []
+    for ops in (reference, oracle_libm):
+        p, m, v = p0.copy(), m0.copy(), v0.copy()
+        ops.fused_adam(p, g, m, v, valid, n, 1e-3, eps=1e-15)
+        outs.append((p, m, v))
+    for a, b in zip(*outs):
+        assert same_bits(a, b)
+
+
+def test_rng(reference, oracle_libm, oracle):
+    for seed, off in ((0, 0), (42, 7), (2**40 + 3, 2**33 + 1)):
+        ru = reference.rng_philox_u32(seed, off, 4099)
+        assert same_bits(oracle.rng_philox_u32(seed, off, 4099), ru)
+        rn = reference.rng_normal_f32(seed, off, 4099)
+        assert same_bits(oracle_libm.rng_normal_f32(seed, off, 4099), rn)
+        close(oracle.rng_normal_f32(seed, off, 4099), rn, rtol=1e-6, atol=1e-6)
+
+
+def test_relocation_and_lut(reference, oracle_libm):
+    lut = reference.make_binoms_lut(51)
+    assert same_bits(oracle_libm.make_binoms_lut(51), lut)
+    r = inputs.rng(80)
+    n = 3000
+    op = r.uniform(0.001, 0.999, n).astype(np.float32)
+    sc = np.exp(r.normal(-3, 1, (n, 3))).astype(np.float32)
+    ratios = r.integers(1, 52, n).astype(np.int32)
+    ro, rs = reference.mcmc_relocation(op, sc, ratios, lut)
+    oo, os_ = oracle_libm.mcmc_relocation(op, sc, ratios, lut)
+    assert same_bits(oo, ro) and same_bits(os_, rs)
+
+
+def test_perturb(reference, oracle_libm, oracle):
+    r = inputs.rng(90)
+    n = 3000
+    pos = r.standard_normal((n, 3)).astype(np.float32)
+    q = r.standard_normal((n, 4)).astype(np.float32)
+    sl = r.normal(-3, 1, (n, 3)).astype(np.float32)
+    lo = r.normal(0, 3, n).astype(np.float32)
+    nz = r.standard_normal((n, 3)).astype(np.float32)
+    outs = []
+    for ops in (reference, oracle_libm, oracle):
+        p = pos.copy()
+        ops.mcmc_perturb_positions(p, q, sl, lo, nz, 0.01)
+        outs.append(p)
+    assert same_bits(outs[1], outs[0])
+    close(outs[2], outs[0], rtol=1e-6, atol=1e-7)
