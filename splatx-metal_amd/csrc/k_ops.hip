@@ -188,11 +188,14 @@ __global__ void __launch_bounds__(kBlock) k_sh_fwd(const float* __restrict__ dir
         colors[(size_t)elem * D + c] = sxd::sh_color(degree, dx, dy, dz, [&](int k) { return cf[k * D + c]; });
 }
 
+// DEG is the degree used (compile time, so the basis stays in registers)
+template <int DEG>
 __global__ void __launch_bounds__(kBlock) k_sh_bwd(const float* __restrict__ dirs, const float* __restrict__ coeffs,
-                                                   const uint8_t* __restrict__ masks, uint32_t degree, int BN, int N,
+                                                   const uint8_t* __restrict__ masks, int BN, int N,
                                                    int K, int D, const float* __restrict__ v_colors,
                                                    float* __restrict__ v_coeffs, float* __restrict__ v_dirs,
                                                    int atomic_coeffs) {
+    constexpr uint32_t degree = DEG;
     const int elem = blockIdx.x * kBlock + threadIdx.x;
     if (elem >= BN) return;
     if (masks && masks[elem] == 0) return;
@@ -201,10 +204,11 @@ __global__ void __launch_bounds__(kBlock) k_sh_bwd(const float* __restrict__ dir
     float* vcf = v_coeffs + (size_t)gid * K * D;
     sxd::ShBasis b;
     sxd::sh_basis(degree, dirs[elem * 3], dirs[elem * 3 + 1], dirs[elem * 3 + 2], b);
-    const int nb = (static_cast<int>(degree) + 1) * (static_cast<int>(degree) + 1);
+    constexpr int nb = (DEG + 1) * (DEG + 1);
     float vx = 0.f, vy = 0.f, vz = 0.f;
     for (int c = 0; c < D; c++) {
         const float vc = v_colors[(size_t)elem * D + c];
+#pragma unroll
         for (int k = 0; k < nb; k++) {
             const float val = b.Y[k] * vc;
             if (atomic_coeffs) atomicAdd(&vcf[k * D + c], val);
@@ -479,8 +483,15 @@ void sh_bwd(const float* dirs, const float* coeffs, const uint8_t* masks, uint32
             int D, const float* v_colors, float* v_coeffs, float* v_dirs, hipStream_t s) {
     const int BN = B * N;
     if (BN <= 0) return;
-    hipLaunchKernelGGL(k_sh_bwd, dim3(grid_for(BN)), dim3(kBlock), 0, s, dirs, coeffs, masks, degree, BN, N, K, D,
-                       v_colors, v_coeffs, v_dirs, B > 1 ? 1 : 0);
+    const dim3 grid(grid_for(BN)), block(kBlock);
+    const int at = B > 1 ? 1 : 0;
+    switch (degree) {
+        case 0: hipLaunchKernelGGL(k_sh_bwd<0>, grid, block, 0, s, dirs, coeffs, masks, BN, N, K, D, v_colors, v_coeffs, v_dirs, at); break;
+        case 1: hipLaunchKernelGGL(k_sh_bwd<1>, grid, block, 0, s, dirs, coeffs, masks, BN, N, K, D, v_colors, v_coeffs, v_dirs, at); break;
+        case 2: hipLaunchKernelGGL(k_sh_bwd<2>, grid, block, 0, s, dirs, coeffs, masks, BN, N, K, D, v_colors, v_coeffs, v_dirs, at); break;
+        case 3: hipLaunchKernelGGL(k_sh_bwd<3>, grid, block, 0, s, dirs, coeffs, masks, BN, N, K, D, v_colors, v_coeffs, v_dirs, at); break;
+        default: hipLaunchKernelGGL(k_sh_bwd<4>, grid, block, 0, s, dirs, coeffs, masks, BN, N, K, D, v_colors, v_coeffs, v_dirs, at); break;
+    }
 }
 
 void isect_count(const IsectArgs& a, int32_t* tiles, hipStream_t s) {

@@ -7,9 +7,11 @@
 // the CPU reference's order (CpuKernels.cpp:821-849) and the deterministic exp of sx_fmath.h, so
 // colors/alphas/last_ids are bit-identical to the CPU oracle; the workgroup exits as soon as all
 // its pixels are done.
-// Backward: back-to-front walk recovering T by division; the nine gradient components of each
-// (Gaussian, wave) are summed over the wave with DPP row operations, the four waves of the tile are
-// combined in LDS once per batch, and one set of float atomics per (tile, Gaussian) is issued.
+// Backward: back-to-front walk recovering T by division. Contributing Gaussians are taken four at a
+// time; their nine gradient components are summed over the wave with one transposed reduction
+// (gfx950 v_permlane32_swap / v_permlane16_swap folds, then DPP within 16-lane rows), the four waves
+// of the tile add their sums into LDS, and one set of float atomics per (tile, Gaussian) is issued
+// after each batch.
 #include <hip/hip_runtime.h>
 
 #include "sx_dev.h"
@@ -121,20 +123,35 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     out_last[pix] = cur;
 }
 
-// ---- 64-lane sums through DPP (gfx9 data-parallel primitives) -----------------------------------
-template <int CTRL, int ROW_MASK>
+// ---- wave reductions -----------------------------------------------------------------------------
+template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-// Sum over the wave; the total is exact in lane 63 (other lanes hold partial sums).
-__device__ __forceinline__ float wave_sum_lane63(float v) {
-    v += dpp_f<0xB1, 0xF>(v);   // quad_perm(1,0,3,2): pairs
-    v += dpp_f<0x4E, 0xF>(v);   // quad_perm(2,3,0,1): quads
-    v += dpp_f<0x141, 0xF>(v);  // row_half_mirror: 8 lanes
-    v += dpp_f<0x140, 0xF>(v);  // row_mirror: 16-lane row
-    v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-    v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+// Sum over each 16-lane row; every lane of the row ends with the row total.
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm(1,0,3,2): pairs
+    v += dpp_f<0x4E>(v);   // quad_perm(2,3,0,1): quads
+    v += dpp_f<0x141>(v);  // row_half_mirror: 8 lanes
+    v += dpp_f<0x140>(v);  // row_mirror: the 16-lane row
     return v;
+}
+// v_permlane32_swap exchanges lanes 32-63 of `a` with lanes 0-31 of `b`; the sum of the two results
+// holds a's 32-lane half sums in lanes 0-31 and b's in lanes 32-63.
+__device__ __forceinline__ float fold32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// v_permlane16_swap exchanges the odd 16-lane rows of `a` with the even rows of `b`; after the sum,
+// row 0 holds a's row-0 + row-1 partials, row 1 b's, row 2 a's rows 2 + 3, row 3 b's.
+__device__ __forceinline__ float fold16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Four per-lane values (one per Gaussian slot A..D) reduced over the 64 lanes in 10 instructions: the
+// result's row 0 holds the total of A, row 1 of C, row 2 of B, row 3 of D (every lane of the row).
+__device__ __forceinline__ float wave_sum4(float a, float b, float c, float d) {
+    return row_sum16(fold16(fold32(a, b), fold32(c, d)));
 }
 
 constexpr int kGrads = 9;  // v_xy(2), v_opacity, v_conic(3), v_rgb(3)
@@ -149,15 +166,15 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     __shared__ float4 s_con[kThreads];
     __shared__ float4 s_rgb[kThreads];
     __shared__ int32_t s_id[kThreads];
-    __shared__ float s_part[kThreads / 64][NV][kThreads];  // per-wave sums, Gaussian-minor
+    __shared__ float4 s_part4[NV * kThreads / 4];  // per-tile sums [k][t], the four waves add into it
+    float* s_part = reinterpret_cast<float*>(s_part4);
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
     const int tile = blockIdx.x % n_tiles;
     if (a.masks && a.masks[(size_t)img * n_tiles + tile] == 0) return;  // uniform
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const bool lane63 = (tid & 63) == 63;
+    const int lane = tid & 63;
     const int px_i = tx * 16 + (tid & 15), py_i = ty * 16 + (tid >> 4);
     const bool inside = px_i < a.width && py_i < a.height;
     const size_t pix = inside ? (size_t)img * a.height * a.width + (size_t)py_i * a.width + px_i
@@ -177,6 +194,9 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     const int32_t wave_bin_final = sxd::wave_max_i(bin_final);
     const int32_t num = range_end - range_start;
     const int num_batches = (num + kThreads - 1) / kThreads;
+    // row r of a wave_sum4 result belongs to slot A=0, C=2, B=1, D=3 for r = 0..3
+    const int row = lane >> 4;
+    const int row_slot = row == 0 ? 0 : row == 1 ? 2 : row == 2 ? 1 : 3;
     for (int b = 0; b < num_batches; b++) {
         __syncthreads();
         const int32_t batch_end = range_end - 1 - kThreads * b;
@@ -192,78 +212,103 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
             s_rgb[tid] = a.splats[(size_t)gid * 3 + 2];
         }
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; w++)
-#pragma unroll
-            for (int k = 0; k < NV; k++) s_part[w][k][tid] = 0.f;
+        for (int j = tid; j < NV * kThreads / 4; j += kThreads) s_part4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         __syncthreads();
-        for (int t = max(0, batch_end - wave_bin_final); t < batch_size; t++) {
+
+        // first batch-local index >= t where some lane of this wave has a contributing pair (uniform)
+        auto next_active = [&](int t) -> int {
+            for (; t < batch_size; t++) {
+                const float4 xyo = s_xyo[t];
+                const float4 con = s_con[t];
+                const float sigma = sigma_of(con.x, con.y, con.z, xyo.x - px, xyo.y - py);
+                const bool valid = inside && (batch_end - t) <= bin_final && !(sigma > xyo.w);
+                if (__any(valid)) break;
+            }
+            return t;
+        };
+        // this lane's gradient terms for batch-local Gaussian t; advances T and the back-sums
+        auto grads_of = [&](int t, float* gv) {
+#pragma unroll
+            for (int k = 0; k < NV; k++) gv[k] = 0.f;
             const float4 xyo = s_xyo[t];
             const float4 con = s_con[t];
             const float dx = xyo.x - px, dy = xyo.y - py;
             const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
-            bool valid = inside && (batch_end - t) <= bin_final && !(sigma > xyo.w);
-            if (!__any(valid)) continue;  // wave-uniform, before any exp
-            float g_r = 0.f, g_g = 0.f, g_b = 0.f, g_ca = 0.f, g_cb = 0.f, g_cc = 0.f, g_x = 0.f, g_y = 0.f,
-                  g_o = 0.f, g_ax = 0.f, g_ay = 0.f;
-            if (valid) {
-                const PixelEval e = eval_weight(con.x, con.y, con.z, dx, dy, xyo.z);
-                if (e.valid) {
-                    const float ra = 1.0f / sxd::smax(sx::kMinOneMinusAlpha, 1.0f - e.alpha);
-                    T *= ra;
-                    const float fac = e.alpha * T;
-                    const float4 c = s_rgb[t];
-                    g_r = fac * vc0;
-                    g_g = fac * vc1;
-                    g_b = fac * vc2;
-                    float v_alpha = (c.x * T - b0 * ra) * vc0 + (c.y * T - b1 * ra) * vc1 + (c.z * T - b2 * ra) * vc2;
-                    v_alpha += T_final * ra * va;
-                    if (bg) v_alpha += -T_final * ra * bg_dot;
-                    const float opac = xyo.z;
-                    if (opac * e.vis <= sx::kMaxAlpha) {
-                        const float v_sigma = -opac * e.vis * v_alpha;
-                        g_ca = 0.5f * v_sigma * dx * dx;
-                        g_cb = v_sigma * dx * dy;
-                        g_cc = 0.5f * v_sigma * dy * dy;
-                        g_x = v_sigma * (con.x * dx + con.y * dy);
-                        g_y = v_sigma * (con.y * dx + con.z * dy);
-                        if (ABSGRAD) {
-                            g_ax = fabsf(g_x);
-                            g_ay = fabsf(g_y);
-                        }
-                        g_o = e.vis * v_alpha;
-                    }
-                    b0 += c.x * fac;
-                    b1 += c.y * fac;
-                    b2 += c.z * fac;
-                }
-            }
-            const float s0 = wave_sum_lane63(g_x), s1 = wave_sum_lane63(g_y), s2 = wave_sum_lane63(g_o);
-            const float s3 = wave_sum_lane63(g_ca), s4 = wave_sum_lane63(g_cb), s5 = wave_sum_lane63(g_cc);
-            const float s6 = wave_sum_lane63(g_r), s7 = wave_sum_lane63(g_g), s8 = wave_sum_lane63(g_b);
-            float s9 = 0.f, s10 = 0.f;
-            if (ABSGRAD) {
-                s9 = wave_sum_lane63(g_ax);
-                s10 = wave_sum_lane63(g_ay);
-            }
-            if (lane63) {
-                float* p = &s_part[wave][0][t];
-                p[0 * kThreads] = s0; p[1 * kThreads] = s1; p[2 * kThreads] = s2;
-                p[3 * kThreads] = s3; p[4 * kThreads] = s4; p[5 * kThreads] = s5;
-                p[6 * kThreads] = s6; p[7 * kThreads] = s7; p[8 * kThreads] = s8;
+            if (!(inside && (batch_end - t) <= bin_final && !(sigma > xyo.w))) return;
+            const PixelEval e = eval_weight(con.x, con.y, con.z, dx, dy, xyo.z);
+            if (!e.valid) return;
+            // hardware reciprocal (1 ulp): the backward is compared at a relative tolerance, and
+            // an IEEE division costs ~10 instructions per pair
+            const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - e.alpha));
+            T *= ra;
+            const float fac = e.alpha * T;
+            const float4 c = s_rgb[t];
+            gv[6] = fac * vc0;
+            gv[7] = fac * vc1;
+            gv[8] = fac * vc2;
+            float v_alpha = (c.x * T - b0 * ra) * vc0 + (c.y * T - b1 * ra) * vc1 + (c.z * T - b2 * ra) * vc2;
+            v_alpha += T_final * ra * va;
+            if (bg) v_alpha += -T_final * ra * bg_dot;
+            const float opac = xyo.z;
+            if (opac * e.vis <= sx::kMaxAlpha) {
+                const float v_sigma = -opac * e.vis * v_alpha;
+                gv[3] = 0.5f * v_sigma * dx * dx;
+                gv[4] = v_sigma * dx * dy;
+                gv[5] = 0.5f * v_sigma * dy * dy;
+                gv[0] = v_sigma * (con.x * dx + con.y * dy);
+                gv[1] = v_sigma * (con.y * dx + con.z * dy);
                 if (ABSGRAD) {
-                    p[9 * kThreads] = s9;
-                    p[10 * kThreads] = s10;
+                    gv[9] = fabsf(gv[0]);
+                    gv[10] = fabsf(gv[1]);
                 }
+                gv[2] = e.vis * v_alpha;
             }
+            b0 += c.x * fac;
+            b1 += c.y * fac;
+            b2 += c.z * fac;
+        };
+
+        int t = max(0, batch_end - wave_bin_final);
+        while (true) {
+            // up to four contributing Gaussians, in order, then one transposed reduction for all four
+            float gA[NV], gB[NV], gC[NV], gD[NV];
+            const int tA = next_active(t);
+            if (tA >= batch_size) break;
+            grads_of(tA, gA);
+            const int tB = next_active(tA + 1);
+            if (tB < batch_size) grads_of(tB, gB);
+            else
+#pragma unroll
+                for (int k = 0; k < NV; k++) gB[k] = 0.f;
+            const int tC = tB < batch_size ? next_active(tB + 1) : batch_size;
+            if (tC < batch_size) grads_of(tC, gC);
+            else
+#pragma unroll
+                for (int k = 0; k < NV; k++) gC[k] = 0.f;
+            const int tD = tC < batch_size ? next_active(tC + 1) : batch_size;
+            if (tD < batch_size) grads_of(tD, gD);
+            else
+#pragma unroll
+                for (int k = 0; k < NV; k++) gD[k] = 0.f;
+            const int t_row = row_slot == 0 ? tA : row_slot == 1 ? tB : row_slot == 2 ? tC : tD;
+            const bool writer = (lane & 15) == 0 && t_row < batch_size;
+            float* dst = s_part + t_row;
+#pragma unroll
+            for (int k = 0; k < NV; k++) {
+                const float v = wave_sum4(gA[k], gB[k], gC[k], gD[k]);
+                if (writer) atomicAdd(&dst[k * kThreads], v);  // LDS add: the four waves of the tile
+            }
+            if (tD >= batch_size) break;
+            t = tD + 1;
         }
         __syncthreads();
-        // one thread per Gaussian of the batch: combine the four waves, then one atomic per component
+        // one thread per Gaussian of the batch: one global atomic per gradient component
         if (tid < batch_size) {
             float v[NV];
             bool any = false;
 #pragma unroll
             for (int k = 0; k < NV; k++) {
-                v[k] = s_part[0][k][tid] + s_part[1][k][tid] + s_part[2][k][tid] + s_part[3][k][tid];
+                v[k] = s_part[k * kThreads + tid];
                 any |= v[k] != 0.f;
             }
             if (any) {

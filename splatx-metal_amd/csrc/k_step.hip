@@ -12,6 +12,8 @@
 // forward is bit-identical to the CPU oracle's host-path step.
 #include <hip/hip_runtime.h>
 
+#include <stdexcept>
+
 #include "sx_dev_bwd.h"
 #include "sx_philox.h"
 #include "sx_step.h"
@@ -129,6 +131,9 @@ __global__ void __launch_bounds__(kBlock) k_emit(StepConst c, const float4* __re
     }
 }
 
+// NC = the arena's SH coefficient count (1, 4, 9 or 16), a compile-time bound so that the SH basis and
+// its partials stay in registers
+template <int NC>
 __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, const float4* __restrict__ splats,
                                                         const float4* __restrict__ grads) {
     const int i = blockIdx.x * kBlock + threadIdx.x;
@@ -154,7 +159,8 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         sxd::sh_basis(c.degree, mw[0] - cp[0], mw[1] - cp[1], mw[2] - cp[2], b);
         const int nb = (static_cast<int>(c.degree) + 1) * (static_cast<int>(c.degree) + 1);
         float vx = 0.f, vy = 0.f, vz = 0.f;
-        for (int k = 0; k < c.n_coeffs; k++) {
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
 #pragma unroll
             for (int ch = 0; ch < 3; ch++) {
                 const int grp = k == 0 ? 4 : 5;
@@ -231,7 +237,10 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         for (int k = 0; k < 3; k++) {
             const uint32_t n = n0 + k;
             const uint32_t t = n >> 2;
-            nz[k] = (t == t0) ? z0[n & 3u] : z1[n & 3u];
+            const uint32_t j = n & 3u;  // register selects (a dynamic array index would go to scratch)
+            const float a = j == 0 ? z0[0] : j == 1 ? z0[1] : j == 2 ? z0[2] : z0[3];
+            const float b = j == 0 ? z1[0] : j == 1 ? z1[1] : j == 2 ? z1[2] : z1[3];
+            nz[k] = (t == t0) ? a : b;
         }
         sxd::perturb_one(mw, q, sl, logit, nz, c.noise_scale, 0.005f, 100.0f);
 #pragma unroll
@@ -259,7 +268,16 @@ __global__ void __launch_bounds__(kBlock) k_l1(const float* __restrict__ render,
 
 __device__ double block_sum_fixed(const double* __restrict__ p, int n, double* s_red) {
     double acc = 0.0;
-    for (int k = threadIdx.x; k < n; k += kBlock) acc += p[k];
+    int k = threadIdx.x;
+    // eight independent loads in flight, summed in the same (ascending) order as the plain loop
+    for (; k + 7 * kBlock < n; k += 8 * kBlock) {
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = p[k + j * kBlock];
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc += v[j];
+    }
+    for (; k < n; k += kBlock) acc += p[k];
     s_red[threadIdx.x] = acc;
     __syncthreads();
     for (int o = kBlock / 2; o > 0; o >>= 1) {
@@ -316,7 +334,14 @@ void step_emit(const StepConst& c, const float4* splats, const int32_t* radii, c
 
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads, hipStream_t s) {
     if (c.count <= 0) return;
-    hipLaunchKernelGGL(k_postprocess, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, A, splats, grads);
+    const dim3 grid(grid_for(c.count)), block(kBlock);
+    switch (c.n_coeffs) {
+        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads); break;
+        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads); break;
+        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads); break;
+        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads); break;
+        default: throw std::invalid_argument("postprocess: SH coefficient count must be 1, 4, 9 or 16");
+    }
 }
 
 int step_l1_blocks(int64_t n) { return static_cast<int>(std::min<int64_t>(1024, grid_for(n))); }
