@@ -50,6 +50,7 @@ struct sxh_executor {
     DevBuf<int64_t> cum;
     DevBuf<uint8_t> scan_scratch;
     DevBuf<unsigned long long> n_vis;
+    DevBuf<uint32_t> vis_part;
     // intersections (grow 1.5x, reused)
     size_t isect_cap = 0;
     DevBuf<uint64_t> keys_a, keys_b;
@@ -179,6 +180,7 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->cum.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
             e->n_vis.alloc(1);
+            e->vis_part.alloc(static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
             e->loss_dev.alloc(1);
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
@@ -330,8 +332,7 @@ static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_output
 
     // ---- segment A: preprocess + scan ------------------------------------------------------------
     e->mark("start");
-    SXH_HIP(hipMemsetAsync(e->n_vis.p, 0, sizeof(unsigned long long), s));
-    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->grads.p, e->n_vis.p, s);
+    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->grads.p, e->vis_part.p, e->n_vis.p, s);
     e->mark("preprocess");
     sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s);
     e->mark("scan");

@@ -22,20 +22,27 @@ namespace {
 
 constexpr int kThreads = 256;
 
-struct PixelEval {
-    float vis, alpha, sigma;
-    bool valid;
-};
-
-// eval_gaussian_weight (KernelCommon.h:75-96 contract; CpuKernels.cpp:753-760 forms)
-__device__ __forceinline__ PixelEval eval_weight(float ca, float cb, float cc, float dx, float dy, float opac) {
-    PixelEval e;
-    e.sigma = 0.5f * (ca * dx * dx + cc * dy * dy) + cb * dx * dy;
-    e.vis = sxm::expf_fast(-e.sigma);
-    const float oa = opac * e.vis;
-    e.alpha = sxd::smin(sx::kMaxAlpha, oa);
-    e.valid = !(e.sigma < 0.f || e.alpha < sx::kAlphaThreshold);
-    return e;
+// sxm::expf_fast(-sigma) without its range branches: identical for sigma in [0, 86] (no overflow,
+// no subnormal scaling); `cut` is the Gaussian's sigma cutoff, wave-uniform, and only an opacity
+// above ~1e35 pushes it past that range, in which case the general function is used.
+__device__ __forceinline__ float exp_neg(float sigma, float cut) {
+    const float cut_u = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cut)));  // uniform branch
+    if (__builtin_expect(cut_u > 86.0f, 0)) return sxm::expf_fast(-sigma);
+    const float x = -sigma;
+    const float kf = __builtin_rintf(x * 1.44269502f);
+    float r = __builtin_fmaf(kf, -0.693145751953125f, x);
+    r = __builtin_fmaf(kf, -1.42860677e-06f, r);
+    float p = 2.48015873e-05f;
+    p = __builtin_fmaf(p, r, 1.98412698e-04f);
+    p = __builtin_fmaf(p, r, 1.38888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int k = static_cast<int>(kf);
+    return p * __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
 }
 
 __device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx, float dy) {
@@ -98,14 +105,15 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
                 const float dx = xyo.x - px, dy = xyo.y - py;
                 const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
                 if (sigma > xyo.w) continue;  // provably below the alpha threshold
-                const PixelEval e = eval_weight(con.x, con.y, con.z, dx, dy, xyo.z);
-                if (!e.valid) continue;
-                const float next_T = T * (1.0f - e.alpha);
+                const float vis = exp_neg(sigma, xyo.w);
+                const float alpha = sxd::smin(sx::kMaxAlpha, xyo.z * vis);
+                if (sigma < 0.f || alpha < sx::kAlphaThreshold) continue;
+                const float next_T = T * (1.0f - alpha);
                 if (next_T <= sx::kTransmittanceThreshold) {
                     done = true;
                     break;
                 }
-                const float w = e.alpha * T;
+                const float w = alpha * T;
                 const float4 c = s_rgb[t];
                 r0 = __builtin_fmaf(c.x, w, r0);
                 r1 = __builtin_fmaf(c.y, w, r1);
@@ -215,54 +223,62 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
         for (int j = tid; j < NV * kThreads / 4; j += kThreads) s_part4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         __syncthreads();
 
-        // first batch-local index >= t where some lane of this wave has a contributing pair (uniform)
-        auto next_active = [&](int t) -> int {
-            for (; t < batch_size; t++) {
-                const float4 xyo = s_xyo[t];
-                const float4 con = s_con[t];
-                const float sigma = sigma_of(con.x, con.y, con.z, xyo.x - px, xyo.y - py);
-                const bool valid = inside && (batch_end - t) <= bin_final && !(sigma > xyo.w);
-                if (__any(valid)) break;
-            }
-            return t;
+        // A candidate: the first batch-local Gaussian at or after t with a lane of this wave inside
+        // its sigma cutoff and before the lane's last contributor (t is wave-uniform), with this
+        // lane's offsets, sigma and the Gaussian's record kept for its gradient.
+        struct Cand {
+            int t;
+            bool valid;
+            float dx, dy, sigma;
+            float4 xyo, con;
         };
-        // this lane's gradient terms for batch-local Gaussian t; advances T and the back-sums
-        auto grads_of = [&](int t, float* gv) {
-#pragma unroll
-            for (int k = 0; k < NV; k++) gv[k] = 0.f;
-            const float4 xyo = s_xyo[t];
-            const float4 con = s_con[t];
-            const float dx = xyo.x - px, dy = xyo.y - py;
-            const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
-            if (!(inside && (batch_end - t) <= bin_final && !(sigma > xyo.w))) return;
-            const PixelEval e = eval_weight(con.x, con.y, con.z, dx, dy, xyo.z);
-            if (!e.valid) return;
-            // hardware reciprocal (1 ulp): the backward is compared at a relative tolerance, and
-            // an IEEE division costs ~10 instructions per pair
-            const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - e.alpha));
+        auto next_active = [&](int t, Cand& q) {
+            for (; t < batch_size; t++) {
+                q.xyo = s_xyo[t];
+                q.con = s_con[t];
+                q.dx = q.xyo.x - px;
+                q.dy = q.xyo.y - py;
+                q.sigma = sigma_of(q.con.x, q.con.y, q.con.z, q.dx, q.dy);
+                q.valid = inside && (batch_end - t) <= bin_final && !(q.sigma > q.xyo.w);
+                if (__any(q.valid)) break;
+            }
+            q.t = t;
+        };
+        // this lane's gradient terms for the candidate, without branches: a pair that does not
+        // contribute gets alpha = 0, so T (times 1/(1 - 0) = 1), the back-sums and every term are
+        // left unchanged / zero
+        auto grads_of = [&](const Cand& q, float* gv) {
+            const float opac = q.xyo.z;
+            const float vis_raw = exp_neg(q.sigma, q.xyo.w);
+            const float oa = opac * vis_raw;
+            const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
+            const bool ok = q.valid && !(q.sigma < 0.f || alpha_raw < sx::kAlphaThreshold);
+            const float alpha = ok ? alpha_raw : 0.0f;
+            // hardware reciprocal (1 ulp; exact for 1): the backward is compared at a relative
+            // tolerance, and an IEEE division costs ~10 instructions per pair
+            const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - alpha));
             T *= ra;
-            const float fac = e.alpha * T;
-            const float4 c = s_rgb[t];
+            const float fac = alpha * T;
+            const float4 c = s_rgb[q.t];
             gv[6] = fac * vc0;
             gv[7] = fac * vc1;
             gv[8] = fac * vc2;
             float v_alpha = (c.x * T - b0 * ra) * vc0 + (c.y * T - b1 * ra) * vc1 + (c.z * T - b2 * ra) * vc2;
             v_alpha += T_final * ra * va;
             if (bg) v_alpha += -T_final * ra * bg_dot;
-            const float opac = xyo.z;
-            if (opac * e.vis <= sx::kMaxAlpha) {
-                const float v_sigma = -opac * e.vis * v_alpha;
-                gv[3] = 0.5f * v_sigma * dx * dx;
-                gv[4] = v_sigma * dx * dy;
-                gv[5] = 0.5f * v_sigma * dy * dy;
-                gv[0] = v_sigma * (con.x * dx + con.y * dy);
-                gv[1] = v_sigma * (con.y * dx + con.z * dy);
-                if (ABSGRAD) {
-                    gv[9] = fabsf(gv[0]);
-                    gv[10] = fabsf(gv[1]);
-                }
-                gv[2] = e.vis * v_alpha;
+            const float vis = (ok && oa <= sx::kMaxAlpha) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
+            const float v_sigma = -opac * vis * v_alpha;
+            const float dx = q.dx, dy = q.dy;
+            gv[3] = 0.5f * v_sigma * dx * dx;
+            gv[4] = v_sigma * dx * dy;
+            gv[5] = 0.5f * v_sigma * dy * dy;
+            gv[0] = v_sigma * (q.con.x * dx + q.con.y * dy);
+            gv[1] = v_sigma * (q.con.y * dx + q.con.z * dy);
+            if (ABSGRAD) {
+                gv[9] = fabsf(gv[0]);
+                gv[10] = fabsf(gv[1]);
             }
+            gv[2] = vis * v_alpha;
             b0 += c.x * fac;
             b1 += c.y * fac;
             b2 += c.z * fac;
@@ -272,21 +288,26 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
         while (true) {
             // up to four contributing Gaussians, in order, then one transposed reduction for all four
             float gA[NV], gB[NV], gC[NV], gD[NV];
-            const int tA = next_active(t);
+            Cand q;
+            next_active(t, q);
+            const int tA = q.t;
             if (tA >= batch_size) break;
-            grads_of(tA, gA);
-            const int tB = next_active(tA + 1);
-            if (tB < batch_size) grads_of(tB, gB);
+            grads_of(q, gA);
+            next_active(tA + 1, q);
+            const int tB = q.t;
+            if (tB < batch_size) grads_of(q, gB);
             else
 #pragma unroll
                 for (int k = 0; k < NV; k++) gB[k] = 0.f;
-            const int tC = tB < batch_size ? next_active(tB + 1) : batch_size;
-            if (tC < batch_size) grads_of(tC, gC);
+            if (tB < batch_size) next_active(tB + 1, q);
+            const int tC = tB < batch_size ? q.t : batch_size;
+            if (tC < batch_size) grads_of(q, gC);
             else
 #pragma unroll
                 for (int k = 0; k < NV; k++) gC[k] = 0.f;
-            const int tD = tC < batch_size ? next_active(tC + 1) : batch_size;
-            if (tD < batch_size) grads_of(tD, gD);
+            if (tC < batch_size) next_active(tC + 1, q);
+            const int tD = tC < batch_size ? q.t : batch_size;
+            if (tD < batch_size) grads_of(q, gD);
             else
 #pragma unroll
                 for (int k = 0; k < NV; k++) gD[k] = 0.f;

@@ -33,20 +33,29 @@ __device__ __forceinline__ void campos_of(const float* vm, float* cp) {
 
 __device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + sxm::expf_(-x)); }
 
-__device__ __forceinline__ void adam_elem(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
-                                          size_t idx, float g, float lr, float b1, float b2, float eps) {
-    float mm = m[idx], vv = v[idx];
+// Adam of one element whose parameter and moments were already loaded (CpuKernels.cpp:127-144 arithmetic);
+// returns the updated parameter
+__device__ __forceinline__ float adam_update(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
+                                             size_t idx, float p0, float mm, float vv, float g, float lr, float b1,
+                                             float b2, float eps) {
     mm = b1 * mm + (1.0f - b1) * g;
     vv = b2 * vv + (1.0f - b2) * g * g;
-    p[idx] += -lr * mm / (__builtin_sqrtf(vv) + eps);
+    const float p1 = p0 + -lr * mm / (__builtin_sqrtf(vv) + eps);
+    p[idx] = p1;
     m[idx] = mm;
     v[idx] = vv;
+    return p1;
 }
 
+
+// NC = the arena's SH coefficient count (1, 4, 9 or 16): the coefficients of a visible Gaussian are
+// loaded into registers in one burst before the evaluation
+template <int NC>
 __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, float4* __restrict__ splats,
                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
                                                        float4* __restrict__ grads,
-                                                       unsigned long long* __restrict__ n_visible) {
+                                                       uint32_t* __restrict__ vis_part) {
+    __shared__ uint32_t s_vis[kBlock / 64];
     const int i = blockIdx.x * kBlock + threadIdx.x;
     bool vis = false;
     if (i < c.count) {
@@ -72,11 +81,16 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
             const float dx = mw[0] - cp[0], dy = mw[1] - cp[1], dz = mw[2] - cp[2];
             float col[3];
             meta = 1u;
+            const int nb = (static_cast<int>(c.degree) + 1) * (static_cast<int>(c.degree) + 1);
+            float co[NC][3];
+#pragma unroll
+            for (int k = 0; k < NC; k++)
+#pragma unroll
+                for (int ch = 0; ch < 3; ch++)
+                    co[k][ch] = k >= nb ? 0.0f : k == 0 ? A.p[4][ch * R + i] : A.p[5][((k - 1) * 3 + ch) * R + i];
 #pragma unroll
             for (int ch = 0; ch < 3; ch++) {
-                const float raw = sxd::sh_color(c.degree, dx, dy, dz, [&](int k) {
-                    return k == 0 ? A.p[4][ch * R + i] : A.p[5][((k - 1) * 3 + ch) * R + i];
-                });
+                const float raw = sxd::sh_color(c.degree, dx, dy, dz, [&](int k) { return co[k][ch]; });
                 const float pre = raw + 0.5f;
                 if (pre > 0.0f) meta |= 2u << ch;
                 col[ch] = (pre < 0.0f) ? 0.0f : pre;
@@ -101,8 +115,31 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
         }
         tiles[i] = cnt;
     }
+    // visible count per block (one plain store; a single global counter would serialize every wave)
     const unsigned long long bal = __ballot(vis);
-    if (sxd::lane_id() == 0 && bal) atomicAdd(n_visible, static_cast<unsigned long long>(__popcll(bal)));
+    if (sxd::lane_id() == 0) s_vis[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; w++) t += s_vis[w];
+        vis_part[blockIdx.x] = t;
+    }
+}
+
+// sum of the per-block visible counts (one block)
+__global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict__ part, int n,
+                                                      unsigned long long* __restrict__ out) {
+    __shared__ unsigned long long s_red[kBlock];
+    unsigned long long acc = 0;
+    for (int k = threadIdx.x; k < n; k += kBlock) acc += part[k];
+    s_red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = kBlock / 2; o > 0; o >>= 1) {
+        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = s_red[0];
 }
 
 __global__ void __launch_bounds__(kBlock) k_emit(StepConst c, const float4* __restrict__ splats,
@@ -152,29 +189,72 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         const float4 s1 = splats[3 * (size_t)i + 1];
         // relu mask (train_relu_mask_apply)
         const float vrgb[3] = {(meta & 2u) ? g2.x : 0.0f, (meta & 4u) ? g2.y : 0.0f, (meta & 8u) ? g2.z : 0.0f};
-        // SH backward streamed into Adam of sh0 / shN (coefficients read before their update)
+        // moments of means, quats, scales and opacity, requested now and used at the end
+        float m0[3], v0[3], m1[4], v1[4], m2[3], v2[3];
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            m0[k] = A.m[0][k * R + i];
+            v0[k] = A.v[0][k * R + i];
+            m2[k] = A.m[2][k * R + i];
+            v2[k] = A.v[2][k * R + i];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            m1[k] = A.m[1][k * R + i];
+            v1[k] = A.v[1][k * R + i];
+        }
+        const float m3 = A.m[3][i], v3 = A.v[3][i];
+        // SH backward fused with Adam of sh0 / shN. Loads are issued in bursts (all coefficients,
+        // then the moments chunk by chunk) so that a wave has many requests in flight instead of one
+        // load-update-store round trip per coefficient.
         float cp[3];
         campos_of(c.vm, cp);
         sxd::ShBasis b;
         sxd::sh_basis(c.degree, mw[0] - cp[0], mw[1] - cp[1], mw[2] - cp[2], b);
         const int nb = (static_cast<int>(c.degree) + 1) * (static_cast<int>(c.degree) + 1);
+        float co[NC][3];
+#pragma unroll
+        for (int k = 0; k < NC; k++)
+#pragma unroll
+            for (int ch = 0; ch < 3; ch++)
+                co[k][ch] = k == 0 ? A.p[4][(size_t)ch * R + i] : A.p[5][(size_t)((k - 1) * 3 + ch) * R + i];
         float vx = 0.f, vy = 0.f, vz = 0.f;
 #pragma unroll
-        for (int k = 0; k < NC; k++) {
+        for (int k = 0; k < NC; k++)
 #pragma unroll
-            for (int ch = 0; ch < 3; ch++) {
-                const int grp = k == 0 ? 4 : 5;
-                const size_t idx = (k == 0 ? (size_t)ch : (size_t)((k - 1) * 3 + ch)) * R + i;
-                float gval = 0.f;
+            for (int ch = 0; ch < 3; ch++)
                 if (k < nb) {
-                    const float co = A.p[grp][idx];
-                    gval = b.Y[k] * vrgb[ch];
-                    vx += vrgb[ch] * (b.dX[k] * co);
-                    vy += vrgb[ch] * (b.dY[k] * co);
-                    vz += vrgb[ch] * (b.dZ[k] * co);
+                    vx += vrgb[ch] * (b.dX[k] * co[k][ch]);
+                    vy += vrgb[ch] * (b.dY[k] * co[k][ch]);
+                    vz += vrgb[ch] * (b.dZ[k] * co[k][ch]);
                 }
-                adam_elem(A.p[grp], A.m[grp], A.v[grp], idx, gval, c.lr[grp], c.b1, c.b2, c.eps);
-            }
+        constexpr int KC = NC < 4 ? NC : 4;  // coefficients per moment burst
+#pragma unroll
+        for (int k0 = 0; k0 < NC; k0 += KC) {
+            float mm[KC][3], vv[KC][3];
+#pragma unroll
+            for (int dk = 0; dk < KC; dk++)
+#pragma unroll
+                for (int ch = 0; ch < 3; ch++) {
+                    const int k = k0 + dk;
+                    if (k >= NC) continue;  // last chunk of NC = 9 is partial
+                    const int grp = k == 0 ? 4 : 5;
+                    const size_t idx = (k == 0 ? (size_t)ch : (size_t)((k - 1) * 3 + ch)) * R + i;
+                    mm[dk][ch] = A.m[grp][idx];
+                    vv[dk][ch] = A.v[grp][idx];
+                }
+#pragma unroll
+            for (int dk = 0; dk < KC; dk++)
+#pragma unroll
+                for (int ch = 0; ch < 3; ch++) {
+                    const int k = k0 + dk;
+                    if (k >= NC) continue;
+                    const int grp = k == 0 ? 4 : 5;
+                    const size_t idx = (k == 0 ? (size_t)ch : (size_t)((k - 1) * 3 + ch)) * R + i;
+                    const float g = k < nb ? b.Y[k] * vrgb[ch] : 0.0f;
+                    adam_update(A.p[grp], A.m[grp], A.v[grp], idx, co[k][ch], mm[dk][ch], vv[dk][ch], g, c.lr[grp],
+                                c.b1, c.b2, c.eps);
+                }
         }
         float vdir[3] = {0.f, 0.f, 0.f};
         if (c.degree >= 1) sxd::sh_dir_vjp(b, vx, vy, vz, vdir);
@@ -209,21 +289,18 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         if (c.opacity_reg_w > 0.0f) vlog += c.opacity_reg_w * opac * (1.0f - opac);
         // Adam of means, quats, scales, opacities
 #pragma unroll
-        for (int k = 0; k < 3; k++) adam_elem(A.p[0], A.m[0], A.v[0], k * R + i, vm_[k], c.lr[0], c.b1, c.b2, c.eps);
+        // (the updated values stay in registers for the noise step below)
+        for (int k = 0; k < 3; k++)
+            mw[k] = adam_update(A.p[0], A.m[0], A.v[0], k * R + i, mw[k], m0[k], v0[k], vm_[k], c.lr[0], c.b1, c.b2,
+                                c.eps);
 #pragma unroll
-        for (int k = 0; k < 4; k++) adam_elem(A.p[1], A.m[1], A.v[1], k * R + i, vq[k], c.lr[1], c.b1, c.b2, c.eps);
+        for (int k = 0; k < 4; k++)
+            q[k] = adam_update(A.p[1], A.m[1], A.v[1], k * R + i, q[k], m1[k], v1[k], vq[k], c.lr[1], c.b1, c.b2, c.eps);
 #pragma unroll
-        for (int k = 0; k < 3; k++) adam_elem(A.p[2], A.m[2], A.v[2], k * R + i, vsl[k], c.lr[2], c.b1, c.b2, c.eps);
-        adam_elem(A.p[3], A.m[3], A.v[3], i, vlog, c.lr[3], c.b1, c.b2, c.eps);
-        if (c.inject_noise) {
-#pragma unroll
-            for (int k = 0; k < 3; k++) mw[k] = A.p[0][k * R + i];
-#pragma unroll
-            for (int k = 0; k < 4; k++) q[k] = A.p[1][k * R + i];
-#pragma unroll
-            for (int k = 0; k < 3; k++) sl[k] = A.p[2][k * R + i];
-            logit = A.p[3][i];
-        }
+        for (int k = 0; k < 3; k++)
+            sl[k] = adam_update(A.p[2], A.m[2], A.v[2], k * R + i, sl[k], m2[k], v2[k], vsl[k], c.lr[2], c.b1, c.b2,
+                                c.eps);
+        logit = adam_update(A.p[3], A.m[3], A.v[3], i, logit, m3, v3, vlog, c.lr[3], c.b1, c.b2, c.eps);
     }
     if (c.inject_noise) {
         // normals 3i..3i+2 of the Philox stream (seed, offset): blocks t = n / 4
@@ -320,11 +397,20 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 } // namespace
 
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles, float4* grads,
-                     unsigned long long* n_visible, hipStream_t s) {
+                     uint32_t* vis_part, unsigned long long* n_visible, hipStream_t s) {
     if (c.count <= 0) return;
-    hipLaunchKernelGGL(k_preprocess, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, A, splats, radii, tiles, grads,
-                       n_visible);
+    const dim3 grid(grid_for(c.count)), block(kBlock);
+    switch (c.n_coeffs) {
+        case 1: hipLaunchKernelGGL(k_preprocess<1>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
+        case 4: hipLaunchKernelGGL(k_preprocess<4>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
+        case 9: hipLaunchKernelGGL(k_preprocess<9>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
+        case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
+        default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
+    }
+    hipLaunchKernelGGL(k_count_sum, dim3(1), dim3(kBlock), 0, s, vis_part, static_cast<int>(grid.x), n_visible);
 }
+
+int step_preprocess_blocks(int64_t count) { return grid_for(count); }
 
 void step_emit(const StepConst& c, const float4* splats, const int32_t* radii, const int64_t* cum, uint64_t* keys,
                int32_t* vals, hipStream_t s) {

@@ -45,7 +45,9 @@ struct StepConst {
 };
 
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
-                     float4* grads, unsigned long long* n_visible, hipStream_t s);
+                     float4* grads, uint32_t* vis_part, unsigned long long* n_visible, hipStream_t s);
+// size of the per-block visible-count scratch of step_preprocess
+int step_preprocess_blocks(int64_t count);
 void step_emit(const StepConst& c, const float4* splats, const int32_t* radii, const int64_t* cum,
                uint64_t* keys, int32_t* vals, hipStream_t s);
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
