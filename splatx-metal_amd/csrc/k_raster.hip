@@ -54,16 +54,70 @@ __device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx
 // most e^-0.01/255), so skipping its exp leaves every result bit-identical.
 __device__ __forceinline__ float sigma_cutoff(float opac) { return __logf(opac * 255.0f) + 0.01f; }
 
+// Which of the tile's four waves (pixel rows y0 + 4w .. y0 + 4w + 3) the Gaussian's cutoff set
+// {sigma <= cut} can reach: for a positive-definite conic the set's y half-extent is
+// sqrt(2 cut a / det). Conservative: the extent gets a relative and an absolute margin far above
+// float rounding of sigma, and every degenerate, nearly degenerate or non-finite case keeps all
+// four waves.
+__device__ __forceinline__ uint32_t wave_rows_mask(float4 xyo, float4 con, int y0) {
+    const float a = con.x, b = con.y, c = con.z, cut = xyo.w;
+    if (cut == -__builtin_inff()) return 0u;  // opacity 0: no pixel passes
+    const float det = a * c - b * b;
+    const bool finite = __builtin_isfinite(a) && __builtin_isfinite(b) && __builtin_isfinite(c) &&
+                        __builtin_isfinite(cut) && __builtin_fabsf(xyo.x) < 1e18f && __builtin_fabsf(xyo.y) < 1e18f;
+    if (!finite || !(a > 0.f) || !(det > 1e-4f * a * c)) return 0xFu;
+    if (cut < 0.f) return 0u;  // sigma >= 0 everywhere for a positive-definite conic
+    const float ry = __builtin_sqrtf(2.0f * cut * a / det) * 1.001f + 0.01f;
+    const float lo = xyo.y - ry, hi = xyo.y + ry;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const float r0 = static_cast<float>(y0 + 4 * w) + 0.5f, r1 = r0 + 3.0f;
+        if (hi >= r0 && lo <= r1) m |= 1u << w;
+    }
+    return m;
+}
+
+// Per-wave Gaussian lists of a batch: s_list[w][0 .. s_len[w]) = the batch-local indices t (in
+// increasing order) whose mask has bit w. All 256 threads call it; thread t passes Gaussian t's mask
+// (0 for slots past the batch). Ends with a barrier.
+__device__ __forceinline__ void build_wave_lists(uint32_t m, uint8_t (*s_list)[kThreads], int (*s_wc)[4],
+                                                 int* s_len) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int pos[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const unsigned long long bal = __ballot((m >> w) & 1u);
+        pos[w] = __popcll(bal & below);
+        if (lane == 0) s_wc[w][wave] = __popcll(bal);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        int off = 0;
+#pragma unroll
+        for (int sw = 0; sw < 4; sw++) off += sw < wave ? s_wc[w][sw] : 0;
+        if ((m >> w) & 1u) s_list[w][off + pos[w]] = static_cast<uint8_t>(tid);
+        if (tid == 0) s_len[w] = s_wc[w][0] + s_wc[w][1] + s_wc[w][2] + s_wc[w][3];
+    }
+    __syncthreads();
+}
+
 __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __restrict__ out_rgb,
                                                          float* __restrict__ out_alpha, int32_t* __restrict__ out_last) {
     __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
     __shared__ float4 s_con[kThreads];
     __shared__ float4 s_rgb[kThreads];
+    __shared__ uint8_t s_list[4][kThreads];
+    __shared__ int s_wc[4][4];
+    __shared__ int s_len[4];
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
     const int tile = blockIdx.x % n_tiles;
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
+    const int wave = tid >> 6;
     const int px_i = tx * 16 + (tid & 15), py_i = ty * 16 + (tid >> 4);
     const bool inside = px_i < a.width && py_i < a.height;
     const size_t pix = (size_t)img * a.height * a.width + (size_t)py_i * a.width + px_i;
@@ -88,18 +142,22 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     for (int32_t bstart = range_start; bstart < range_end; bstart += kThreads) {
         if (__syncthreads_count(done) == kThreads) break;  // also the barrier before LDS reuse
         const int32_t idx = bstart + tid;
+        uint32_t wm = 0u;
         if (idx < range_end) {
             const int32_t g = a.flatten_ids[idx];
             float4 xyo = a.splats[(size_t)g * 3];
             xyo.w = sigma_cutoff(xyo.z);
+            const float4 con = a.splats[(size_t)g * 3 + 1];
             s_xyo[tid] = xyo;
-            s_con[tid] = a.splats[(size_t)g * 3 + 1];
+            s_con[tid] = con;
             s_rgb[tid] = a.splats[(size_t)g * 3 + 2];
+            wm = wave_rows_mask(xyo, con, ty * 16);
         }
-        __syncthreads();
-        const int cnt = min(kThreads, range_end - bstart);
+        build_wave_lists(wm, s_list, s_wc, s_len);
         if (!done) {
-            for (int t = 0; t < cnt; t++) {
+            const int len = s_len[wave];
+            for (int j = 0; j < len; j++) {
+                const int t = s_list[wave][j];
                 const float4 xyo = s_xyo[t];
                 const float4 con = s_con[t];
                 const float dx = xyo.x - px, dy = xyo.y - py;
