@@ -353,6 +353,7 @@ typedef struct {
     int64_t n_isects;        /* the sync-point readback */
     int64_t n_visible;       /* Gaussians with radii > 0 (device counter) */
     float* render_colors;    /* in: [H,W,3] host buffer to fill, or NULL for no readback */
+    uint32_t sort_key_bits;  /* out: significant bits of the step's sort keys (tile bits + compressed depth) */
 } sxh_step_outputs;
 
 int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor** out);

@@ -179,8 +179,8 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->tiles.alloc(R);
             e->cum.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
-            e->n_vis.alloc(1);
-            e->vis_part.alloc(static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
+            e->n_vis.alloc(2);
+            e->vis_part.alloc(3 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
             e->loss_dev.alloc(1);
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
@@ -338,7 +338,7 @@ static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_output
     e->mark("scan");
     int64_t* hs = static_cast<int64_t*>(e->host_small.p);
     SXH_HIP(hipMemcpyAsync(&hs[0], e->cum.p + (c.count - 1), 8, hipMemcpyDeviceToHost, s));
-    SXH_HIP(hipMemcpyAsync(&hs[1], e->n_vis.p, 8, hipMemcpyDeviceToHost, s));
+    SXH_HIP(hipMemcpyAsync(&hs[1], e->n_vis.p, 16, hipMemcpyDeviceToHost, s));  // count, depth-bit range
     SXH_HIP(hipGetLastError());
     // ---- sync 1: n_isects (MetalBackend.cpp:1849-1858) --------------------------------------------
     auto t0 = std::chrono::steady_clock::now();
@@ -346,22 +346,37 @@ static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_output
     e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     const int64_t n_isects = hs[0];
     out->n_isects = n_isects;
+    out->sort_key_bits = 0;
     out->n_visible = hs[1];
     validate_n_isects_readback(n_isects, what);
     e->ensure_isect(static_cast<size_t>(n_isects));
     e->mark("sync1");
+    // sort keys: the depth bits of the visible Gaussians span [lo, hi]; storing depth - lo in just
+    // enough bits keeps the (tile, depth) order and usually saves a radix pass
+    {
+        const uint64_t range = static_cast<uint64_t>(hs[2]);
+        const uint32_t lo = static_cast<uint32_t>(range), hi = static_cast<uint32_t>(range >> 32);
+        c.key_depth_bits = 32;
+        c.key_depth_base = 0;
+        if (out->n_visible > 0 && hi >= lo) {
+            const uint32_t span = hi - lo;
+            c.key_depth_bits = span ? 32u - static_cast<uint32_t>(__builtin_clz(span)) : 0u;
+            c.key_depth_base = lo;
+        }
+    }
 
     // ---- segment B ---------------------------------------------------------------------------------
     int32_t* flat = e->vals_a.p;
     if (n_isects > 0) {
         sxk::step_emit(c, e->splats.p, e->radii.p, e->cum.p, e->keys_a.p, e->vals_a.p, s);
         e->mark("emit");
+        out->sort_key_bits = c.key_depth_bits + c.tile_n_bits;
         const int which = sxk::radix_sort(e->keys_a.p, e->vals_a.p, e->keys_b.p, e->vals_b.p, n_isects,
-                                          32 + c.tile_n_bits, e->sort_scratch.p, s);
+                                          out->sort_key_bits, e->sort_scratch.p, s);
         e->mark("sort");
         const uint64_t* keys = which ? e->keys_b.p : e->keys_a.p;
         flat = which ? e->vals_b.p : e->vals_a.p;
-        sxk::offset_encode(keys, n_isects, 1, tw * th, c.tile_n_bits, e->offsets.p, s);
+        sxk::offset_encode(keys, n_isects, 1, tw * th, c.tile_n_bits, e->offsets.p, s, c.key_depth_bits);
         e->mark("offsets");
     } else {
         SXH_HIP(hipMemsetAsync(e->offsets.p, 0, static_cast<size_t>(tw) * th * 4, s));
@@ -378,7 +393,7 @@ static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_output
     ra.n_isects = static_cast<int32_t>(n_isects);
     sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
     e->mark("raster_fwd");
-    float* hloss = reinterpret_cast<float*>(&hs[2]);
+    float* hloss = reinterpret_cast<float*>(&hs[3]);
     *hloss = 0.0f;
     if (!fwd_only) {
         const float* gt = nullptr;

@@ -357,12 +357,13 @@ __global__ void __launch_bounds__(kBlock) k_scan_tiles(const int32_t* __restrict
 // offset encode — IntersectTile.metal:310-335 contract (one thread per sorted intersection).
 // ------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(kBlock) k_offsets(const uint64_t* __restrict__ keys, int64_t n, int64_t total,
-                                                    int n_tiles, uint32_t tile_n_bits, int32_t* __restrict__ off) {
+                                                    int n_tiles, uint32_t tile_n_bits, int32_t* __restrict__ off,
+                                                    uint32_t key_shift) {
     const int64_t idx = blockIdx.x * (int64_t)kBlock + threadIdx.x;
     if (idx >= n) return;
     const uint64_t tile_mask = (static_cast<uint64_t>(1) << tile_n_bits) - 1;
     auto flat_tile = [&](uint64_t key) {
-        const uint64_t id = key >> 32;
+        const uint64_t id = key >> key_shift;
         return static_cast<int64_t>(id >> tile_n_bits) * n_tiles + static_cast<int64_t>(id & tile_mask);
     };
     const int64_t cur = flat_tile(keys[idx]);
@@ -371,7 +372,7 @@ __global__ void __launch_bounds__(kBlock) k_offsets(const uint64_t* __restrict__
     if (idx == n - 1)
         for (int64_t i = cur + 1; i < total; i++) off[i] = static_cast<int32_t>(n);
     if (idx > 0) {
-        if ((keys[idx - 1] >> 32) == (keys[idx] >> 32)) return;
+        if ((keys[idx - 1] >> key_shift) == (keys[idx] >> key_shift)) return;
         const int64_t prev = flat_tile(keys[idx - 1]);
         for (int64_t i = prev + 1; i <= cur; i++) off[i] = static_cast<int32_t>(idx);
     }
@@ -517,10 +518,10 @@ void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hip
 }
 
 void offset_encode(const uint64_t* keys, int64_t n, int I, int n_tiles, uint32_t tile_n_bits, int32_t* off,
-                   hipStream_t s) {
+                   hipStream_t s, uint32_t key_shift) {
     if (n <= 0) return;
     hipLaunchKernelGGL(k_offsets, dim3(grid_for(n)), dim3(kBlock), 0, s, keys, n, (int64_t)I * n_tiles, n_tiles,
-                       tile_n_bits, off);
+                       tile_n_bits, off, key_shift);
 }
 
 void pack_splats(const float* m2, const float* cn, const float* col, const float* op, int n, float4* sp,

@@ -252,11 +252,12 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     const float px = static_cast<float>(px_i) + 0.5f, py = static_cast<float>(py_i) + 0.5f;
     const float T_final = 1.0f - ralpha[pix];
     float T = T_final;
-    float b0 = 0.f, b1 = 0.f, b2 = 0.f;
+    float bdot = 0.f;  // <accumulated back colour, v_render> (the back-sum dotted with v_render)
     const int32_t bin_final = inside ? last_ids[pix] : -1;
     const float vc0 = v_rc[pix * 3], vc1 = v_rc[pix * 3 + 1], vc2 = v_rc[pix * 3 + 2];
     const float va = v_ra[pix];
     const float bg_dot = bg ? (bg[0] * vc0 + bg[1] * vc1 + bg[2] * vc2) : 0.f;
+    const float tva = T_final * (va - bg_dot);  // the alpha and background terms of every v_alpha, over ra
     const int32_t wave_bin_final = sxd::wave_max_i(bin_final);
     const int32_t num = range_end - range_start;
     const int num_batches = (num + kThreads - 1) / kThreads;
@@ -321,9 +322,10 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
             gv[6] = fac * vc0;
             gv[7] = fac * vc1;
             gv[8] = fac * vc2;
-            float v_alpha = (c.x * T - b0 * ra) * vc0 + (c.y * T - b1 * ra) * vc1 + (c.z * T - b2 * ra) * vc2;
-            v_alpha += T_final * ra * va;
-            if (bg) v_alpha += -T_final * ra * bg_dot;
+            // v_alpha = sum_c (c_c T - b_c ra) vc_c + T_final ra (va - <bg, vc>), with the back-sum kept
+            // as its dot product with v_render
+            const float cvc = c.x * vc0 + c.y * vc1 + c.z * vc2;
+            const float v_alpha = T * cvc + ra * (tva - bdot);
             const float vis = (ok && oa <= sx::kMaxAlpha) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
             const float v_sigma = -opac * vis * v_alpha;
             const float dx = q.dx, dy = q.dy;
@@ -337,9 +339,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
                 gv[10] = fabsf(gv[1]);
             }
             gv[2] = vis * v_alpha;
-            b0 += c.x * fac;
-            b1 += c.y * fac;
-            b2 += c.z * fac;
+            bdot += fac * cvc;
         };
 
         int t = max(0, batch_end - wave_bin_final);

@@ -3,11 +3,12 @@
 // Contract: KernelBackend.h:130-148 / sort_isect (ascending unsigned key, stable, only bits
 // [0, key_bits) significant). Design: 8-bit digits, so a 45-bit isect key needs 6 passes (the
 // reference's 4-bit digits need 12). Each pass is three launches with no inter-workgroup waiting:
-//   1. per-tile digit histogram (LDS counters)        -> hist[digit][tile]
-//   2. exclusive scan of hist in digit-major order     -> global start of (digit, tile)
-//   3. stable scatter: each 64-lane wave ranks its keys per digit with 8 ballots (lanes with an
-//      identical digit form one match mask), waves are ordered through LDS counts, rounds keep
-//      input order, so equal digits keep their relative order.
+//   1. per-tile digit histogram (LDS counters)        -> hist[digit][tile], plus the digit totals
+//   2. one workgroup per digit scans its row of hist   -> global start of (digit, tile)
+//   3. stable scatter: each 64-lane wave ranks the keys of its quarter of the tile per digit with 8
+//      ballots (lanes with an identical digit form one match mask) and per-wave LDS offsets, so
+//      equal digits keep their relative order; the tile is reordered in LDS first so that the
+//      global writes of each digit's run are contiguous.
 #include <hip/hip_runtime.h>
 
 #include "sx_kernels.h"
@@ -21,8 +22,11 @@ constexpr int kRounds = 16;
 constexpr int kTile = kThreads * kRounds;  // 4096 keys per workgroup
 constexpr int kBins = 256;
 
+// Per-tile digit histogram -> hist[digit][tile]; the tile's counts are also added to the pass's
+// digit totals (zeroed by k_zero_totals before the first pass).
 __global__ void __launch_bounds__(kThreads) k_hist(const uint64_t* __restrict__ keys, int64_t n, int shift,
-                                                   uint32_t* __restrict__ hist, int n_tiles) {
+                                                   uint32_t* __restrict__ hist, int n_tiles,
+                                                   uint32_t* __restrict__ totals) {
     __shared__ uint32_t h[kBins];
     h[threadIdx.x] = 0;
     __syncthreads();
@@ -33,12 +37,14 @@ __global__ void __launch_bounds__(kThreads) k_hist(const uint64_t* __restrict__ 
         if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & 0xFF], 1u);
     }
     __syncthreads();
-    hist[(size_t)threadIdx.x * n_tiles + blockIdx.x] = h[threadIdx.x];
+    const uint32_t c = h[threadIdx.x];
+    hist[(size_t)threadIdx.x * n_tiles + blockIdx.x] = c;
+    if (c) atomicAdd(&totals[threadIdx.x], c);
 }
 
-// Exclusive scan of a u32 array in two launches (block sums, then per-block prefix + local scan).
-constexpr int kScanItems = 16;
-constexpr int kScanTile = kThreads * kScanItems;
+__global__ void __launch_bounds__(kThreads) k_zero_totals(uint32_t* __restrict__ totals, int n) {
+    for (int i = threadIdx.x; i < n; i += kThreads) totals[i] = 0;
+}
 
 __device__ inline uint32_t block_excl_scan_u32(uint32_t v, uint32_t* s_wave, uint32_t* total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -61,68 +67,101 @@ __device__ inline uint32_t block_excl_scan_u32(uint32_t v, uint32_t* s_wave, uin
     return pre + x - v;
 }
 
-__global__ void __launch_bounds__(kThreads) k_u32_sums(const uint32_t* __restrict__ in, int64_t n,
-                                                       uint32_t* __restrict__ sums) {
+// One workgroup per digit d: hist[d][t] <- (keys of digits < d) + (keys of digit d in tiles < t),
+// the global output start of tile t's run of digit d.
+__global__ void __launch_bounds__(kThreads) k_scan_digit(uint32_t* __restrict__ hist, int n_tiles,
+                                                         const uint32_t* __restrict__ totals) {
     __shared__ uint32_t s_wave[kWaves];
-    const int64_t base = (int64_t)blockIdx.x * kScanTile;
-    uint32_t acc = 0;
-    for (int i = 0; i < kScanItems; i++) {
-        const int64_t idx = base + i * kThreads + threadIdx.x;
-        if (idx < n) acc += in[idx];
-    }
-    uint32_t tot = 0;
-    block_excl_scan_u32(acc, s_wave, &tot);
-    if (threadIdx.x == 0) sums[blockIdx.x] = tot;
-}
-
-__global__ void __launch_bounds__(kThreads) k_u32_scan(uint32_t* __restrict__ data, int64_t n,
-                                                       const uint32_t* __restrict__ sums) {
-    __shared__ uint32_t s_wave[kWaves];
-    __shared__ uint32_t s_prefix;
-    uint32_t p = 0;
-    for (int b = threadIdx.x; b < static_cast<int>(blockIdx.x); b += kThreads) p += sums[b];
-    uint32_t ptot = 0;
-    block_excl_scan_u32(p, s_wave, &ptot);
-    if (threadIdx.x == 0) s_prefix = ptot;
+    const int d = blockIdx.x, tid = threadIdx.x;
+    uint32_t all = 0;
+    const uint32_t before = block_excl_scan_u32(totals[tid], s_wave, &all);
+    __shared__ uint32_t s_base;
+    if (tid == d) s_base = before;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
-    uint32_t v[kScanItems];
-    uint32_t acc = 0;
+    uint32_t carry = s_base;
+    uint32_t* row = hist + (size_t)d * n_tiles;
+    constexpr int kItems = 4;
+    for (int c0 = 0; c0 < n_tiles; c0 += kThreads * kItems) {
+        const int i0 = c0 + tid * kItems;
+        uint32_t v[kItems], sum = 0;
 #pragma unroll
-    for (int i = 0; i < kScanItems; i++) {
-        v[i] = (base + i < n) ? data[base + i] : 0u;
-        acc += v[i];
-    }
-    uint32_t run = block_excl_scan_u32(acc, s_wave, nullptr) + s_prefix;
+        for (int j = 0; j < kItems; j++) {
+            v[j] = i0 + j < n_tiles ? row[i0 + j] : 0u;
+            sum += v[j];
+        }
+        uint32_t chunk = 0;
+        uint32_t run = block_excl_scan_u32(sum, s_wave, &chunk) + carry;
 #pragma unroll
-    for (int i = 0; i < kScanItems; i++) {
-        if (base + i < n) data[base + i] = run;
-        run += v[i];
+        for (int j = 0; j < kItems; j++) {
+            if (i0 + j < n_tiles) row[i0 + j] = run;
+            run += v[j];
+        }
+        carry += chunk;
     }
 }
 
+// Stable scatter of one tile of 4096 keys. Wave w owns the contiguous quarter [1024 w, 1024 w + 1024)
+// of the tile and walks it in 16 rounds of 64 keys; ranks among equal digits come from 64-lane
+// match masks (8 ballots), so within the tile the order is (wave, round, lane) = input order. The
+// tile is reordered by digit in LDS and then written out run by run: consecutive threads store
+// consecutive addresses of one digit's output range.
 __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict__ kin, const int32_t* __restrict__ vin,
                                                       uint64_t* __restrict__ kout, int32_t* __restrict__ vout,
                                                       int64_t n, int shift, const uint32_t* __restrict__ hist,
                                                       int n_tiles) {
-    __shared__ uint32_t s_off[kBins];
-    __shared__ uint32_t s_cnt[kWaves][kBins];
+    constexpr int kPerWave = kTile / kWaves;  // 1024
+    __shared__ uint64_t s_k[kTile];
+    __shared__ int32_t s_v[kTile];
+    __shared__ uint32_t s_gstart[kBins];  // global start of this tile's run of each digit
+    __shared__ uint32_t s_lstart[kBins];  // local (in-tile) start of each digit's run
+    __shared__ uint32_t s_woff[kWaves][kBins];  // per wave: next local slot of each digit
+    __shared__ uint32_t s_wave[kWaves];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    s_off[tid] = hist[(size_t)tid * n_tiles + blockIdx.x];
-    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int64_t base = (int64_t)blockIdx.x * kTile;
-    for (int r = 0; r < kRounds; r++) {
-        const int64_t round_base = base + r * kThreads;
-        if (round_base >= n) break;  // uniform across the workgroup
+    const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
+    s_gstart[tid] = hist[(size_t)tid * n_tiles + blockIdx.x];
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) s_cnt[w][tid] = 0;
-        __syncthreads();
-        const int64_t idx = round_base + tid;
-        const bool valid = idx < n;
-        const uint64_t key = valid ? kin[idx] : 0ull;
-        const int32_t val = valid ? vin[idx] : 0;
-        const uint32_t digit = static_cast<uint32_t>((key >> shift) & 0xFF);
+    for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
+    __syncthreads();
+    uint64_t key[kRounds];
+    int32_t val[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+        const int i = wave * kPerWave + r * 64 + lane;
+        key[r] = i < tile_n ? kin[base + i] : 0ull;
+        val[r] = i < tile_n ? vin[base + i] : 0;
+    }
+    // per-wave digit histograms
+#pragma unroll
+    for (int r = 0; r < kRounds; r++)
+        if (wave * kPerWave + r * 64 + lane < tile_n) atomicAdd(&s_woff[wave][(key[r] >> shift) & 0xFF], 1u);
+    __syncthreads();
+    {
+        // thread = digit: the digit's in-tile start, then each wave's start inside the digit's run
+        uint32_t c[kWaves], tot = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            c[w] = s_woff[w][tid];
+            tot += c[w];
+        }
+        uint32_t all = 0;
+        uint32_t run = block_excl_scan_u32(tot, s_wave, &all);
+        s_lstart[tid] = run;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            s_woff[w][tid] = run;
+            run += c[w];
+        }
+    }
+    __syncthreads();
+    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint32_t* woff = s_woff[wave];
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+        if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
+        const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
+        const uint32_t digit = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
         uint64_t match = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 8; b++) {
@@ -131,20 +170,23 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
             match &= bit ? bal : ~bal;
         }
         const uint32_t rank = static_cast<uint32_t>(__popcll(match & lanes_below));
-        if (valid && rank == 0) s_cnt[wave][digit] = static_cast<uint32_t>(__popcll(match));
-        __syncthreads();
+        uint32_t pos = 0;
         if (valid) {
-            uint32_t pos = s_off[digit] + rank;
-            for (int w = 0; w < wave; w++) pos += s_cnt[w][digit];
-            kout[pos] = key;
-            vout[pos] = val;
+            pos = woff[digit] + rank;
+            s_k[pos] = key[r];
+            s_v[pos] = val[r];
         }
-        __syncthreads();
-        uint32_t add = 0;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) add += s_cnt[w][tid];
-        s_off[tid] += add;
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();  // every lane has read woff[] before it is advanced
+        if (valid && rank == 0) woff[digit] += static_cast<uint32_t>(__popcll(match));
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    for (int p = tid; p < tile_n; p += kThreads) {
+        const uint64_t k = s_k[p];
+        const uint32_t d = static_cast<uint32_t>((k >> shift) & 0xFF);
+        const uint32_t g = s_gstart[d] + (static_cast<uint32_t>(p) - s_lstart[d]);
+        kout[g] = k;
+        vout[g] = s_v[p];
     }
 }
 
@@ -152,11 +194,12 @@ int tiles_for(int64_t n) { return static_cast<int>((n + kTile - 1) / kTile); }
 
 } // namespace
 
+constexpr int kMaxPasses = 8;
+
 size_t sort_scratch_bytes(int64_t n) {
     const int64_t tiles = std::max<int64_t>(1, tiles_for(n));
     const int64_t hist = tiles * kBins;
-    const int64_t sums = (hist + kScanTile - 1) / kScanTile;
-    return sizeof(uint32_t) * static_cast<size_t>(hist + sums + 64);
+    return sizeof(uint32_t) * static_cast<size_t>(hist + kMaxPasses * kBins + 64);
 }
 
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
@@ -165,18 +208,17 @@ int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* val
     const int tiles = tiles_for(n);
     uint32_t* hist = static_cast<uint32_t*>(scratch);
     const int64_t hist_n = (int64_t)tiles * kBins;
-    uint32_t* sums = hist + hist_n;
-    const int scan_blocks = static_cast<int>((hist_n + kScanTile - 1) / kScanTile);
+    uint32_t* totals = hist + hist_n;
     const int passes = static_cast<int>((key_bits + 7) / 8);
+    hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins);
     uint64_t* kin = keys_a;
     int32_t* vin = vals_a;
     uint64_t* kout = keys_b;
     int32_t* vout = vals_b;
     for (int p = 0; p < passes; p++) {
         const int shift = 8 * p;
-        hipLaunchKernelGGL(k_hist, dim3(tiles), dim3(kThreads), 0, s, kin, n, shift, hist, tiles);
-        hipLaunchKernelGGL(k_u32_sums, dim3(scan_blocks), dim3(kThreads), 0, s, hist, hist_n, sums);
-        hipLaunchKernelGGL(k_u32_scan, dim3(scan_blocks), dim3(kThreads), 0, s, hist, hist_n, sums);
+        hipLaunchKernelGGL(k_hist, dim3(tiles), dim3(kThreads), 0, s, kin, n, shift, hist, tiles, totals + p * kBins);
+        hipLaunchKernelGGL(k_scan_digit, dim3(kBins), dim3(kThreads), 0, s, hist, tiles, totals + p * kBins);
         hipLaunchKernelGGL(k_scatter, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, hist,
                            tiles);
         std::swap(kin, kout);

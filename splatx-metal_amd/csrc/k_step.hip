@@ -55,7 +55,8 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
                                                        float4* __restrict__ grads,
                                                        uint32_t* __restrict__ vis_part) {
-    __shared__ uint32_t s_vis[kBlock / 64];
+    __shared__ uint32_t s_vis[kBlock / 64], s_dmin[kBlock / 64], s_dmax[kBlock / 64];
+    uint32_t dbits_min = 0xFFFFFFFFu, dbits_max = 0u;
     const int i = blockIdx.x * kBlock + threadIdx.x;
     bool vis = false;
     if (i < c.count) {
@@ -104,6 +105,8 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
                 cnt = (r.max_y - r.min_y) * (r.max_x - r.min_x);
             }
             splats[3 * (size_t)i] = make_float4(o.m2x, o.m2y, op_used, o.depth);
+            dbits_min = __float_as_uint(o.depth);
+            dbits_max = dbits_min;
             splats[3 * (size_t)i + 1] = make_float4(o.ca, o.cb, o.cc, o.comp);
             splats[3 * (size_t)i + 2] = make_float4(col[0], col[1], col[2], __uint_as_float(meta));
             const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -115,31 +118,63 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
         }
         tiles[i] = cnt;
     }
-    // visible count per block (one plain store; a single global counter would serialize every wave)
+    // visible count and depth-bit range per block (plain stores; a single global counter would
+    // serialize every wave)
     const unsigned long long bal = __ballot(vis);
-    if (sxd::lane_id() == 0) s_vis[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        dbits_min = min(dbits_min, static_cast<uint32_t>(__shfl_xor(static_cast<int>(dbits_min), o, 64)));
+        dbits_max = max(dbits_max, static_cast<uint32_t>(__shfl_xor(static_cast<int>(dbits_max), o, 64)));
+    }
+    if (sxd::lane_id() == 0) {
+        s_vis[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal));
+        s_dmin[threadIdx.x >> 6] = dbits_min;
+        s_dmax[threadIdx.x >> 6] = dbits_max;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t t = 0;
+        uint32_t t = 0, lo = 0xFFFFFFFFu, hi = 0u;
 #pragma unroll
-        for (int w = 0; w < kBlock / 64; w++) t += s_vis[w];
-        vis_part[blockIdx.x] = t;
+        for (int w = 0; w < kBlock / 64; w++) {
+            t += s_vis[w];
+            lo = min(lo, s_dmin[w]);
+            hi = max(hi, s_dmax[w]);
+        }
+        vis_part[3 * blockIdx.x] = t;
+        vis_part[3 * blockIdx.x + 1] = lo;
+        vis_part[3 * blockIdx.x + 2] = hi;
     }
 }
 
-// sum of the per-block visible counts (one block)
+// sum of the per-block visible counts and the overall depth-bit range (one block); out = {u64 count,
+// u32 min, u32 max}
 __global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict__ part, int n,
                                                       unsigned long long* __restrict__ out) {
     __shared__ unsigned long long s_red[kBlock];
+    __shared__ uint32_t s_lo[kBlock], s_hi[kBlock];
     unsigned long long acc = 0;
-    for (int k = threadIdx.x; k < n; k += kBlock) acc += part[k];
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+    for (int k = threadIdx.x; k < n; k += kBlock) {
+        acc += part[3 * k];
+        lo = min(lo, part[3 * k + 1]);
+        hi = max(hi, part[3 * k + 2]);
+    }
     s_red[threadIdx.x] = acc;
+    s_lo[threadIdx.x] = lo;
+    s_hi[threadIdx.x] = hi;
     __syncthreads();
     for (int o = kBlock / 2; o > 0; o >>= 1) {
-        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
+        if (threadIdx.x < o) {
+            s_red[threadIdx.x] += s_red[threadIdx.x + o];
+            s_lo[threadIdx.x] = min(s_lo[threadIdx.x], s_lo[threadIdx.x + o]);
+            s_hi[threadIdx.x] = max(s_hi[threadIdx.x], s_hi[threadIdx.x + o]);
+        }
         __syncthreads();
     }
-    if (threadIdx.x == 0) out[0] = s_red[0];
+    if (threadIdx.x == 0) {
+        out[0] = s_red[0];
+        out[1] = (static_cast<unsigned long long>(s_hi[0]) << 32) | s_lo[0];
+    }
 }
 
 __global__ void __launch_bounds__(kBlock) k_emit(StepConst c, const float4* __restrict__ splats,
@@ -150,10 +185,10 @@ __global__ void __launch_bounds__(kBlock) k_emit(StepConst c, const float4* __re
     if (!(radii[2 * i] > 0 && radii[2 * i + 1] > 0)) return;
     const float4 s0 = splats[3 * (size_t)i];
     const float4 s1 = splats[3 * (size_t)i + 1];
-    const uint64_t depth_enc = static_cast<uint64_t>(__float_as_uint(s0.w));
+    const uint64_t depth_enc = static_cast<uint64_t>(__float_as_uint(s0.w) - c.key_depth_base);
     int64_t cur = i == 0 ? 0 : cum[i - 1];
     auto emit = [&](int32_t tile) {
-        keys[cur] = (static_cast<uint64_t>(static_cast<uint32_t>(tile)) << 32) | depth_enc;
+        keys[cur] = (static_cast<uint64_t>(static_cast<uint32_t>(tile)) << c.key_depth_bits) | depth_enc;
         vals[cur] = i;
         ++cur;
     };

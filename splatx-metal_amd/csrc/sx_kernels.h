@@ -72,8 +72,9 @@ int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* val
                uint32_t key_bits, void* scratch, hipStream_t s);
 
 // offsets[I*n_tiles] from sorted keys; n_isects > 0.
+// key_shift: position of the (image, tile) id in the key (32 for the isect_tiles encoding)
 void offset_encode(const uint64_t* keys, int64_t n_isects, int I, int n_tiles, uint32_t tile_n_bits,
-                   int32_t* offsets, hipStream_t s);
+                   int32_t* offsets, hipStream_t s, uint32_t key_shift = 32);
 
 // ---- raster ---------------------------------------------------------------------------------
 // Packed per-Gaussian record consumed by the rasterizer: 3 x float4

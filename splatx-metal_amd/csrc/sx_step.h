@@ -36,6 +36,9 @@ struct StepConst {
     int accutile;
     int tile_width, tile_height;
     uint32_t tile_n_bits;
+    // executor sort keys: tile << key_depth_bits | (depth bits - key_depth_base), the depth range of
+    // the visible Gaussians compressed to key_depth_bits (order-preserving for positive depths)
+    uint32_t key_depth_bits, key_depth_base;
     float lr[6];
     float b1, b2, eps;
     float opacity_reg_w, scale_reg_w;
@@ -44,9 +47,11 @@ struct StepConst {
     float noise_scale;
 };
 
+// vis_part: 3 u32 per block (visible count, min and max depth bits); out_vis: {u64 visible count,
+// u32 min depth bits, u32 max depth bits} of the visible Gaussians
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
-                     float4* grads, uint32_t* vis_part, unsigned long long* n_visible, hipStream_t s);
-// size of the per-block visible-count scratch of step_preprocess
+                     float4* grads, uint32_t* vis_part, unsigned long long* out_vis, hipStream_t s);
+// number of blocks of step_preprocess (vis_part holds 3 u32 per block)
 int step_preprocess_blocks(int64_t count);
 void step_emit(const StepConst& c, const float4* splats, const int32_t* radii, const int64_t* cum,
                uint64_t* keys, int32_t* vals, hipStream_t s);

@@ -176,7 +176,7 @@ class StepInputs(C.Structure):
 
 class StepOutputs(C.Structure):
     _fields_ = [("loss", C.c_float), ("n_isects", C.c_int64), ("n_visible", C.c_int64),
-                ("render_colors", fp)]
+                ("render_colors", fp), ("sort_key_bits", C.c_uint32)]
 
 
 class ExecTiming(C.Structure):
