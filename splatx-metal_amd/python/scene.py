@@ -95,7 +95,7 @@ CONFIGS = {
     3: dict(n=1_000_000, sh_degree=3, width=1297, height=840, fx=1150.0, isect="accutile", ssim=0.2,
             target="scene", xy=4.0, z=(1.5, 20.0), log_scale_mu=math.log(0.01), log_scale_sd=0.7),
     5: dict(n=2_000_000, sh_degree=3, width=1920, height=1080, fx=1600.0, isect="accutile", ssim=0.2,
-            target="scene", xy=3.0, z=(2.0, 4.0), log_scale_mu=math.log(0.08), log_scale_sd=0.5, tie_frac=0.1,
+            target="scene", xy=2.8, z=(2.0, 4.0), log_scale_mu=math.log(0.08), log_scale_sd=0.5, tie_frac=0.1,
             antialiased=True),
 }
 
