@@ -22,8 +22,21 @@ constexpr int kRounds = 16;
 constexpr int kTile = kThreads * kRounds;  // 4096 keys per workgroup
 constexpr int kBins = 256;
 
+// Lanes of the wave whose 8-bit digit equals this lane's (among lanes where `valid`), from 8 ballots.
+__device__ __forceinline__ uint64_t digit_match(uint32_t digit, bool valid) {
+    uint64_t match = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const bool bit = (digit >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        match &= bit ? bal : ~bal;
+    }
+    return match;
+}
+
 // Per-tile digit histogram -> hist[digit][tile]; the tile's counts are also added to the pass's
-// digit totals (zeroed by k_zero_totals before the first pass).
+// digit totals (zeroed by k_zero_totals before the first pass). Equal digits of a wave are counted
+// by one leader lane (match masks), so concentrated digits cost no LDS atomic contention.
 __global__ void __launch_bounds__(kThreads) k_hist(const uint64_t* __restrict__ keys, int64_t n, int shift,
                                                    uint32_t* __restrict__ hist, int n_tiles,
                                                    uint32_t* __restrict__ totals) {
@@ -31,10 +44,20 @@ __global__ void __launch_bounds__(kThreads) k_hist(const uint64_t* __restrict__ 
     h[threadIdx.x] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * kTile;
-#pragma unroll 4
+    const int lane = threadIdx.x & 63;
+    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint64_t key[kRounds];
+#pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const int64_t idx = base + r * kThreads + threadIdx.x;
-        if (idx < n) atomicAdd(&h[(keys[idx] >> shift) & 0xFF], 1u);
+        key[r] = idx < n ? keys[idx] : 0ull;
+    }
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+        const bool valid = base + r * kThreads + threadIdx.x < n;
+        const uint32_t d = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint64_t match = digit_match(d, valid);
+        if (valid && (match & lanes_below) == 0) atomicAdd(&h[d], static_cast<uint32_t>(__popcll(match)));
     }
     __syncthreads();
     const uint32_t c = h[threadIdx.x];
@@ -132,10 +155,24 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
         key[r] = i < tile_n ? kin[base + i] : 0ull;
         val[r] = i < tile_n ? vin[base + i] : 0;
     }
-    // per-wave digit histograms
+    // per-wave digit histograms: one leader lane per distinct digit of a round; the ranks among
+    // equal digits (and the leaders' counts) are kept for the placement below
+    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint8_t rank[kRounds];
+    uint8_t cnt[kRounds];  // 0 unless this lane leads its digit group (then popcount - 1, fits 0..63)
 #pragma unroll
-    for (int r = 0; r < kRounds; r++)
-        if (wave * kPerWave + r * 64 + lane < tile_n) atomicAdd(&s_woff[wave][(key[r] >> shift) & 0xFF], 1u);
+    for (int r = 0; r < kRounds; r++) {
+        const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
+        const uint32_t d = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint64_t match = digit_match(d, valid);
+        rank[r] = static_cast<uint8_t>(__popcll(match & lanes_below));
+        cnt[r] = 0;
+        if (valid && rank[r] == 0) {
+            const uint32_t c = static_cast<uint32_t>(__popcll(match));
+            cnt[r] = static_cast<uint8_t>(c - 1);
+            s_woff[wave][d] += c;  // only this wave writes its row, one leader per digit
+        }
+    }
     __syncthreads();
     {
         // thread = digit: the digit's in-tile start, then each wave's start inside the digit's run
@@ -155,29 +192,19 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
         }
     }
     __syncthreads();
-    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     uint32_t* woff = s_woff[wave];
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
         const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
         const uint32_t digit = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
-        uint64_t match = __ballot(valid);
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
-            const bool bit = (digit >> b) & 1u;
-            const uint64_t bal = __ballot(bit);
-            match &= bit ? bal : ~bal;
-        }
-        const uint32_t rank = static_cast<uint32_t>(__popcll(match & lanes_below));
-        uint32_t pos = 0;
         if (valid) {
-            pos = woff[digit] + rank;
+            const uint32_t pos = woff[digit] + rank[r];
             s_k[pos] = key[r];
             s_v[pos] = val[r];
         }
         __builtin_amdgcn_wave_barrier();  // every lane has read woff[] before it is advanced
-        if (valid && rank == 0) woff[digit] += static_cast<uint32_t>(__popcll(match));
+        if (valid && rank[r] == 0) woff[digit] += static_cast<uint32_t>(cnt[r]) + 1u;
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
