@@ -60,7 +60,7 @@ struct sxh_executor {
     size_t img_px = 0, img_tiles = 0, img_map = 0;
     DevBuf<int32_t> offsets, last_ids;
     DevBuf<float> render, alpha, v_render, v_alpha_zero, gt_stage;
-    DevBuf<float> ssim_map, cmu, csg, ccr;
+    DevBuf<float> cmu, csg, ccr;  // SSIM coefficient maps (the map itself is only summed)
     DevBuf<double> ssim_part, l1_part;
     DevBuf<float> loss_dev;
     // GT cache
@@ -128,7 +128,6 @@ struct sxh_executor {
         }
         if (use_ssim) {
             if (map_n > img_map) {
-                ssim_map.alloc(map_n);
                 cmu.alloc(map_n);
                 csg.alloc(map_n);
                 ccr.alloc(map_n);
@@ -405,7 +404,7 @@ static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_output
         int n_l1 = 0, n_ss = 0;
         if (use_ssim) {
             n_ss = sxk::ssim_fwd_blocks(1, H, W, 3);
-            sxk::ssim_fwd(e->render.p, gt, 1, H, W, 3, 1, e->ssim_map.p, e->cmu.p, e->csg.p, e->ccr.p,
+            sxk::ssim_fwd(e->render.p, gt, 1, H, W, 3, 1, nullptr, e->cmu.p, e->csg.p, e->ccr.p,
                           e->ssim_part.p, s);
             e->mark("ssim_fwd");
             const float G = static_cast<float>(-static_cast<double>(e->d.ssim_weight) / static_cast<double>(map_n));

@@ -116,15 +116,11 @@ __global__ void __launch_bounds__(256) k_ssim_fwd(const float* __restrict__ img1
     }
 }
 
-// FUSE_L1: the resident step's loss gradient — v = w_l1 * sign(x - y) * g_l1 + G*(...), and one
-// f64 partial sum of |x - y| per workgroup (TrainStep.metal:143-155 combination, Trainer.cpp:330-345).
-template <bool FUSE_L1>
-__global__ void __launch_bounds__(256) k_ssim_bwd_t(const float* __restrict__ img1, const float* __restrict__ img2,
-                                                    const float* __restrict__ cmu, const float* __restrict__ csg,
-                                                    const float* __restrict__ ccr, int H, int W, int C, float G,
-                                                    float* __restrict__ v_img1, float w_l1, float g_l1,
-                                                    double* __restrict__ l1_partials) {
-    __shared__ double s_red[256];
+// Any channel count: one workgroup per (tile, channel).
+__global__ void __launch_bounds__(256) k_ssim_bwd(const float* __restrict__ img1, const float* __restrict__ img2,
+                                                  const float* __restrict__ cmu, const float* __restrict__ csg,
+                                                  const float* __restrict__ ccr, int H, int W, int C, float G,
+                                                  float* __restrict__ v_img1) {
     __shared__ float d[3][A][A + 1];
     __shared__ float h[3][A][T + 1];
     const int mh = H - 10, mw = W - 10;
@@ -162,7 +158,6 @@ __global__ void __launch_bounds__(256) k_ssim_bwd_t(const float* __restrict__ im
     }
     __syncthreads();
     const int qy = oy + threadIdx.y, qx = ox + threadIdx.x;
-    double l1 = 0.0;
     if (qy < H && qx < W) {
         float c1 = 0.f, c2 = 0.f, c3 = 0.f;
 #pragma unroll
@@ -175,15 +170,204 @@ __global__ void __launch_bounds__(256) k_ssim_bwd_t(const float* __restrict__ im
         }
         const size_t q = ihwc(img, qy, qx, ch, H, W, C);
         const float x = img1[q], y = img2[q];
+        v_img1[q] = G * (c1 + 2.f * x * c2 + y * c3);
+    }
+}
+
+// Three-channel variants (the training images): one workgroup per 16x16 tile covers all three
+// channels, so every global load and store touches whole interleaved pixels (coalesced), and each
+// channel's passes run exactly as above (same tap order, same results).
+constexpr int C3 = 3;
+
+__global__ void __launch_bounds__(256) k_ssim_fwd3(const float* __restrict__ img1, const float* __restrict__ img2,
+                                                   int H, int W, int need_coeffs, float* __restrict__ map,
+                                                   float* __restrict__ cmu, float* __restrict__ csg,
+                                                   float* __restrict__ ccr, double* __restrict__ block_sums) {
+    __shared__ float sx[C3][A][A + 1];
+    __shared__ float sy[C3][A][A + 1];
+    __shared__ float h[5][A][T + 1];
+    __shared__ double s_red[256];
+    const int mh = H - 10, mw = W - 10;
+    const int img = blockIdx.z;
+    const int oy = blockIdx.y * T, ox = blockIdx.x * T;
+    const int tid = threadIdx.y * T + threadIdx.x;
+    for (int k = tid; k < A * A * C3; k += 256) {
+        const int ay = k / (A * C3), rem = k % (A * C3);
+        const int ax = rem / C3, c = rem % C3;
+        const int y = oy + ay, x = ox + ax;
+        float a = 0.f, b = 0.f;
+        if (y < H && x < W) {
+            const size_t off = ihwc(img, y, x, c, H, W, C3);
+            a = img1[off];
+            b = img2[off];
+        }
+        sx[c][ay][ax] = a;
+        sy[c][ay][ax] = b;
+    }
+    const int my = oy + threadIdx.y, mx = ox + threadIdx.x;
+    const bool out = my < mh && mx < mw;
+    float S_[C3], cm_[C3], cs_[C3], cc_[C3];
+    double contrib = 0.0;
+#pragma unroll
+    for (int c = 0; c < C3; c++) {
+        __syncthreads();  // loads done / previous channel's vertical pass done with h
+        for (int k = tid; k < A * T; k += 256) {
+            const int r = k / T, cx = k % T;
+            float m1 = 0.f, m2 = 0.f, e11 = 0.f, e22 = 0.f, e12 = 0.f;
+#pragma unroll
+            for (int u = 0; u < 11; u++) {
+                const float w = c_taps[u];
+                const float x = sx[c][r][cx + u], g = sy[c][r][cx + u];
+                m1 = __builtin_fmaf(w, x, m1);
+                m2 = __builtin_fmaf(w, g, m2);
+                e11 = __builtin_fmaf(w * x, x, e11);
+                e22 = __builtin_fmaf(w * g, g, e22);
+                e12 = __builtin_fmaf(w * x, g, e12);
+            }
+            h[0][r][cx] = m1;
+            h[1][r][cx] = m2;
+            h[2][r][cx] = e11;
+            h[3][r][cx] = e22;
+            h[4][r][cx] = e12;
+        }
+        __syncthreads();
+        S_[c] = cm_[c] = cs_[c] = cc_[c] = 0.f;
+        if (out) {
+            float mu1 = 0.f, mu2 = 0.f, e11 = 0.f, e22 = 0.f, e12 = 0.f;
+#pragma unroll
+            for (int v = 0; v < 11; v++) {
+                const float w = c_taps[v];
+                const int r = threadIdx.y + v;
+                mu1 = __builtin_fmaf(w, h[0][r][threadIdx.x], mu1);
+                mu2 = __builtin_fmaf(w, h[1][r][threadIdx.x], mu2);
+                e11 = __builtin_fmaf(w, h[2][r][threadIdx.x], e11);
+                e22 = __builtin_fmaf(w, h[3][r][threadIdx.x], e22);
+                e12 = __builtin_fmaf(w, h[4][r][threadIdx.x], e12);
+            }
+            const float sigma1 = __builtin_fmaf(-mu1, mu1, e11);
+            const float sigma2 = __builtin_fmaf(-mu2, mu2, e22);
+            const float sigma12 = __builtin_fmaf(-mu1, mu2, e12);
+            const float A1 = 2.f * mu1 * mu2 + sx::kSsimC1;
+            const float B1 = mu1 * mu1 + mu2 * mu2 + sx::kSsimC1;
+            const float A2 = 2.f * sigma12 + sx::kSsimC2;
+            const float B2 = sigma1 + sigma2 + sx::kSsimC2;
+            const float denom = B1 * B2;
+            const float S = (A1 * A2) / denom;
+            S_[c] = S;
+            contrib += static_cast<double>(S);
+            const float dS_dmu1 = 2.f * (mu2 * A2 / denom - mu1 * S / B1);
+            const float dS_dsigma1 = -S / B2;
+            const float dS_dsigma12 = 2.f * A1 / denom;
+            cm_[c] = dS_dmu1 - 2.f * mu1 * dS_dsigma1 - mu2 * dS_dsigma12;
+            cs_[c] = dS_dsigma1;
+            cc_[c] = dS_dsigma12;
+        }
+    }
+    if (out) {
+        const size_t mo = ihwc(img, my, mx, 0, mh, mw, C3);
+#pragma unroll
+        for (int c = 0; c < C3; c++) {
+            if (map) map[mo + c] = S_[c];
+            if (need_coeffs) {
+                cmu[mo + c] = cm_[c];
+                csg[mo + c] = cs_[c];
+                ccr[mo + c] = cc_[c];
+            }
+        }
+    }
+    if (block_sums) {  // fixed-shape tree: deterministic
+        s_red[tid] = contrib;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) s_red[tid] += s_red[tid + o];
+            __syncthreads();
+        }
+        if (tid == 0) block_sums[((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = s_red[0];
+    }
+}
+
+// FUSE_L1: the resident step's loss gradient — v = w_l1 * sign(x - y) * g_l1 + G*(...), and one
+// f64 partial sum of |x - y| per workgroup (TrainStep.metal:143-155 combination, Trainer.cpp:330-345).
+template <bool FUSE_L1>
+__global__ void __launch_bounds__(256) k_ssim_bwd3(const float* __restrict__ img1, const float* __restrict__ img2,
+                                                   const float* __restrict__ cmu, const float* __restrict__ csg,
+                                                   const float* __restrict__ ccr, int H, int W, float G,
+                                                   float* __restrict__ v_img1, float w_l1, float g_l1,
+                                                   double* __restrict__ l1_partials) {
+    __shared__ double s_red[256];
+    __shared__ float d[3][C3][A][A + 1];
+    __shared__ float h[3][A][T + 1];
+    const int mh = H - 10, mw = W - 10;
+    const int img = blockIdx.z;
+    const int oy = blockIdx.y * T, ox = blockIdx.x * T;
+    const int tid = threadIdx.y * T + threadIdx.x;
+    for (int k = tid; k < A * A * C3; k += 256) {
+        const int ay = k / (A * C3), rem = k % (A * C3);
+        const int ax = rem / C3, c = rem % C3;
+        const int y = oy + ay - 10, x = ox + ax - 10;
+        float a = 0.f, b = 0.f, e = 0.f;
+        if (y >= 0 && y < mh && x >= 0 && x < mw) {
+            const size_t off = ihwc(img, y, x, c, mh, mw, C3);
+            a = cmu[off];
+            b = csg[off];
+            e = ccr[off];
+        }
+        d[0][c][ay][ax] = a;
+        d[1][c][ay][ax] = b;
+        d[2][c][ay][ax] = e;
+    }
+    const int qy = oy + threadIdx.y, qx = ox + threadIdx.x;
+    const bool in = qy < H && qx < W;
+    const size_t q0 = ihwc(img, in ? qy : 0, in ? qx : 0, 0, H, W, C3);
+    float xs[C3], ys[C3];
+#pragma unroll
+    for (int c = 0; c < C3; c++) {
+        xs[c] = in ? img1[q0 + c] : 0.f;
+        ys[c] = in ? img2[q0 + c] : 0.f;
+    }
+    float vout[C3];
+    double l1 = 0.0;
+#pragma unroll
+    for (int c = 0; c < C3; c++) {
+        __syncthreads();
+        for (int k = tid; k < A * T; k += 256) {
+            const int r = k / T, cx = k % T;
+            float s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+            for (int u = 0; u < 11; u++) {
+                const float w = c_taps[u];
+                s1 = __builtin_fmaf(w, d[0][c][r][cx + u], s1);
+                s2 = __builtin_fmaf(w, d[1][c][r][cx + u], s2);
+                s3 = __builtin_fmaf(w, d[2][c][r][cx + u], s3);
+            }
+            h[0][r][cx] = s1;
+            h[1][r][cx] = s2;
+            h[2][r][cx] = s3;
+        }
+        __syncthreads();
+        float c1 = 0.f, c2 = 0.f, c3 = 0.f;
+#pragma unroll
+        for (int v = 0; v < 11; v++) {
+            const float w = c_taps[v];
+            const int r = threadIdx.y + v;
+            c1 = __builtin_fmaf(w, h[0][r][threadIdx.x], c1);
+            c2 = __builtin_fmaf(w, h[1][r][threadIdx.x], c2);
+            c3 = __builtin_fmaf(w, h[2][r][threadIdx.x], c3);
+        }
+        const float x = xs[c], y = ys[c];
         const float vd = G * (c1 + 2.f * x * c2 + y * c3);
         if (FUSE_L1) {
-            const float d = x - y;
-            const float base = d > 0.0f ? g_l1 : (d < 0.0f ? -g_l1 : 0.0f);
-            v_img1[q] = w_l1 * base + vd;
-            l1 = fabs(static_cast<double>(d));
+            const float dd = x - y;
+            const float base = dd > 0.0f ? g_l1 : (dd < 0.0f ? -g_l1 : 0.0f);
+            vout[c] = w_l1 * base + vd;
+            if (in) l1 += fabs(static_cast<double>(dd));
         } else {
-            v_img1[q] = vd;
+            vout[c] = vd;
         }
+    }
+    if (in) {
+#pragma unroll
+        for (int c = 0; c < C3; c++) v_img1[q0 + c] = vout[c];
     }
     if (FUSE_L1) {
         s_red[tid] = l1;
@@ -200,13 +384,19 @@ __global__ void __launch_bounds__(256) k_ssim_bwd_t(const float* __restrict__ im
 
 int ssim_fwd_blocks(int I, int H, int W, int C) {
     const int mh = H - 10, mw = W - 10;
-    return ((mw + T - 1) / T) * ((mh + T - 1) / T) * I * C;
+    return ((mw + T - 1) / T) * ((mh + T - 1) / T) * I * (C == C3 ? 1 : C);
 }
 
 void ssim_fwd(const float* img1, const float* img2, int I, int H, int W, int C, int need_coeffs, float* map,
               float* cmu, float* csg, float* ccr, double* block_sums, hipStream_t s) {
     const int mh = H - 10, mw = W - 10;
     if (mh <= 0 || mw <= 0) return;
+    if (C == C3) {
+        dim3 grid((mw + T - 1) / T, (mh + T - 1) / T, I);
+        hipLaunchKernelGGL(k_ssim_fwd3, grid, dim3(T, T), 0, s, img1, img2, H, W, need_coeffs, map, cmu, csg, ccr,
+                           block_sums);
+        return;
+    }
     dim3 grid((mw + T - 1) / T, (mh + T - 1) / T, I * C);
     hipLaunchKernelGGL(k_ssim_fwd, grid, dim3(T, T), 0, s, img1, img2, H, W, C, need_coeffs, map, cmu, csg, ccr,
                        block_sums);
@@ -214,18 +404,23 @@ void ssim_fwd(const float* img1, const float* img2, int I, int H, int W, int C, 
 
 void ssim_bwd(const float* img1, const float* img2, const float* cmu, const float* csg, const float* ccr, int I,
               int H, int W, int C, float G, float* v_img1, hipStream_t s) {
+    if (C == C3) {
+        dim3 grid((W + T - 1) / T, (H + T - 1) / T, I);
+        hipLaunchKernelGGL(k_ssim_bwd3<false>, grid, dim3(T, T), 0, s, img1, img2, cmu, csg, ccr, H, W, G, v_img1,
+                           0.f, 0.f, nullptr);
+        return;
+    }
     dim3 grid((W + T - 1) / T, (H + T - 1) / T, I * C);
-    hipLaunchKernelGGL(k_ssim_bwd_t<false>, grid, dim3(T, T), 0, s, img1, img2, cmu, csg, ccr, H, W, C, G, v_img1,
-                       0.f, 0.f, nullptr);
+    hipLaunchKernelGGL(k_ssim_bwd, grid, dim3(T, T), 0, s, img1, img2, cmu, csg, ccr, H, W, C, G, v_img1);
 }
 
-int step_ssim_bwd_blocks(int H, int W) { return ((W + T - 1) / T) * ((H + T - 1) / T) * 3; }
+int step_ssim_bwd_blocks(int H, int W) { return ((W + T - 1) / T) * ((H + T - 1) / T); }
 
 void step_ssim_bwd_l1(const float* render, const float* gt, const float* cmu, const float* csg, const float* ccr,
                       int H, int W, float G, float w_l1, float g_l1, float* v_render, double* l1_partials,
                       hipStream_t s) {
-    dim3 grid((W + T - 1) / T, (H + T - 1) / T, 3);
-    hipLaunchKernelGGL(k_ssim_bwd_t<true>, grid, dim3(T, T), 0, s, render, gt, cmu, csg, ccr, H, W, 3, G, v_render,
+    dim3 grid((W + T - 1) / T, (H + T - 1) / T, 1);
+    hipLaunchKernelGGL(k_ssim_bwd3<true>, grid, dim3(T, T), 0, s, render, gt, cmu, csg, ccr, H, W, G, v_render,
                        w_l1, g_l1, l1_partials);
 }
 

@@ -194,7 +194,8 @@ def test_raster_empty_and_background(gpu, oracle):
 
 
 # ---- SSIM -------------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("shape", [(1, 24, 24, 3), (1, 37, 53, 3), (2, 16, 40, 1), (1, 200, 301, 3)])
+@pytest.mark.parametrize("shape", [(1, 24, 24, 3), (1, 37, 53, 3), (2, 16, 40, 1), (1, 200, 301, 3), (2, 30, 41, 3),
+                                   (1, 19, 27, 4)])
 def test_ssim_bitexact(gpu, oracle, shape):
     r = inputs.rng(sum(shape))
     x = r.uniform(0, 1, shape).astype(np.float32)
