@@ -369,6 +369,62 @@ int32_t sxh_exec_set_gt_cache(sxh_executor* e, const float* images, int32_t n_im
 /* Renders the current parameters into GT cache entry `index` (synthetic-target helper). */
 int32_t sxh_exec_render_to_gt_cache(sxh_executor* e, const sxh_step_inputs* in, int32_t index);
 
+/* ------------------------------------------------------------------------------------------ */
+/* MCMC refine on the device — replaces the host orchestration Trainer::mcmc_refine           */
+/* (Trainer.cpp:1273-1280) = mcmc_relocate (:1284-1338) + mcmc_add (:1342-1395) with          */
+/* mcmc_zero_adam_rows (:1422-1435) and the helpers multinomial_with_replacement (:1199-1218) */
+/* and run_relocation_for (:1231-1258), plus the noise tail mcmc_inject_noise (:1400-1418)    */
+/* that step_resident runs after a refine (:960-967). The reference downloads and re-uploads  */
+/* the whole arena for this (sync_host_for_mutation, :911-914); here it runs in place in HBM. */
+/* ------------------------------------------------------------------------------------------ */
+
+/* The multinomial engine, std::mt19937_64 (Trainer.h:495 mcmc_rng_), in libstdc++'s layout:  */
+/* x[312] state words and p, the index of the next word to temper (p == 312: the next draw    */
+/* twists first). A standard textual state (the 312 most recent words, as libc++ writes it)   */
+/* is x = those words with p = 312.                                                            */
+typedef struct {
+    uint64_t x[312];
+    uint32_t p;
+} sxh_mt64_state;
+
+/* std::mt19937_64::seed(seed) (Trainer.cpp:713). Host only. */
+int32_t sxh_mt64_seed(uint64_t seed, sxh_mt64_state* out);
+
+typedef struct {
+    int64_t count;           /* live rows before the refine (cloud_.count) */
+    int64_t cap_max;         /* growth cap, <= arena_rows (McmcOptions::cap_max, Trainer.h:190) */
+    float min_opacity;       /* dead = sigmoid(logit) <= min_opacity, in (0,1) (Trainer.h:191) */
+    int32_t n_max;           /* ratio clamp of the relocation (kMcmcNMax = 51) */
+    const float* binoms;     /* [n_max*n_max] host LUT (sxh_make_binoms_lut) */
+    sxh_mt64_state* rng;     /* in/out: advanced by exactly the draws the reference makes */
+    uint8_t inject_noise;    /* after the refine: mcmc_inject_noise over the new count */
+    uint64_t noise_seed, noise_offset;
+    float noise_scale;
+} sxh_refine_inputs;
+
+typedef struct {
+    int64_t count;           /* out: live rows after the refine */
+    int64_t n_relocated;     /* out: McmcRefineResult.relocated_dead.size() */
+    int64_t n_added;         /* out: McmcRefineResult.added_src.size() */
+    /* Optional (NULL = not wanted) copies of McmcRefineResult (Trainer.h:414-420), each with
+     * `capacity` entries; SXH_ERR_CAPACITY before any mutation when a wanted list would not fit. */
+    int64_t* relocated_dead;
+    int64_t* relocation_src;
+    int64_t* added_src;
+    int64_t capacity;
+} sxh_refine_outputs;
+
+/* Errors follow the reference: NaN weights or a zero weight sum (multinomial, :1205-1209) and a
+ * non-positive new scale (:1318-1319) fail before that phase mutates anything. */
+int32_t sxh_exec_mcmc_refine(sxh_executor* e, const sxh_refine_inputs* in, sxh_refine_outputs* out);
+
+/* The refine's two sequential primitives on the device, exposed for verification like the other
+ * ops: the multinomial's running f64 sum of float weights (Trainer.cpp:1202-1208: acc +=
+ * double(w[i]), left to right; out[i] = the sum after w[i]), and `n` raw 64-bit draws of the
+ * engine (advancing `st`). */
+int32_t sxh_running_sum_f64(sxh_backend* b, const float* w, int64_t n, double* out /* [n] */);
+int32_t sxh_mt64_draw(sxh_backend* b, sxh_mt64_state* st, int64_t n, uint64_t* out /* [n] */);
+
 /* Per-kernel timing of the last step (HIP events on the executor's stream), enabled by
  * sxh_exec_set_profiling(e, 1). Names are stable strings; times are milliseconds. */
 typedef struct {

@@ -3,7 +3,8 @@
 Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the checker
 or the timed CPU baseline. `Oracle(libm=False)` uses the deterministic transcendental layer shared
 with the device code; `Oracle(libm=True)` uses glibc exactly like the reference CPU code;
-`Reference()` calls the reference's own CpuKernels.cpp built under oracle/_ref (when present).
+`Reference()` calls the reference's own CPU code (CpuKernels.cpp, and the Trainer on the CPU
+backend for the MCMC refine) built under oracle/_ref (when present).
 """
 from __future__ import annotations
 
@@ -32,6 +33,27 @@ class StepArgs(C.Structure):
                 ("inject_noise", C.c_uint8), ("noise_seed", C.c_uint64), ("noise_offset", C.c_uint64),
                 ("noise_scale", C.c_float), ("loss", C.c_float), ("n_isects", C.c_int64),
                 ("n_visible", C.c_int64), ("render_colors", sh.fp), ("stage_ms", C.c_double * 16)]
+
+
+class RefineArgs(C.Structure):
+    _fields_ = [("params", sh.fp * 6), ("exp_avg", sh.fp * 6), ("exp_avg_sq", sh.fp * 6), ("count", C.c_int64),
+                ("cap_max", C.c_int64), ("sh_degree", C.c_int32), ("min_opacity", C.c_float), ("n_max", C.c_int32),
+                ("binoms", sh.fp), ("rng", C.POINTER(sh.MtState)), ("new_count", C.c_int64),
+                ("n_relocated", C.c_int64), ("n_added", C.c_int64), ("relocated_dead", sh.i64p),
+                ("relocation_src", sh.i64p), ("added_src", sh.i64p), ("capacity", C.c_int64)]
+
+
+class RefCase(C.Structure):
+    _fields_ = [("params", sh.fp * 6), ("exp_avg", sh.fp * 6), ("exp_avg_sq", sh.fp * 6), ("count", C.c_int64),
+                ("cap_max", C.c_int64), ("sh_degree", C.c_int32), ("min_opacity", C.c_float), ("seed", C.c_uint64),
+                ("n_refine", C.c_int32), ("out_params", sh.fp * 6), ("out_exp_avg", sh.fp * 6),
+                ("out_exp_avg_sq", sh.fp * 6), ("counts", sh.i64p), ("n_relocated", sh.i64p), ("n_added", sh.i64p),
+                ("relocated_dead", sh.i64p), ("relocation_src", sh.i64p), ("added_src", sh.i64p),
+                ("capacity", C.c_int64), ("rng_out", C.POINTER(sh.MtState))]
+
+
+def _ptr_or_null(a):
+    return sh.ptr(a) if a is not None and a.size else None
 
 
 def lib_path(libm: bool) -> str:
@@ -113,6 +135,45 @@ class Oracle(sh.Ops):
         return dict(loss=float(a.loss), n_isects=int(a.n_isects), n_visible=int(a.n_visible),
                     render_colors=render, stage_ms=stages)
 
+    def mt64_seed(self, seed):
+        st = sh.MtState()
+        self._call("mt64_seed", C.c_uint64(seed), C.byref(st))
+        return st
+
+    def mt64_draw(self, st, n):
+        out = np.zeros(n, np.uint64)
+        self._call("mt64_draw", C.byref(st), C.c_int64(n), sh.ptr(out))
+        return out
+
+    def running_sum_f64(self, w):
+        w = sh.f32(w)
+        out = np.zeros(w.size, np.float64)
+        f = self.lib.sxo_running_sum_f64
+        f.restype = C.c_int32
+        f(sh.ptr(w), C.c_int64(w.size), out.ctypes.data_as(C.POINTER(C.c_double)))
+        return out
+
+    def mcmc_refine(self, params, exp_avg, exp_avg_sq, count, cap_max, sh_degree, rng, binoms, min_opacity=0.005,
+                    n_max=51, want_lists=True):
+        """Trainer::mcmc_refine on AoS arena arrays [rows, dim] in place; `rng` (MtState) advanced in place."""
+        a = RefineArgs()
+        for g in range(6):
+            a.params[g] = _ptr_or_null(params[g])
+            a.exp_avg[g] = _ptr_or_null(exp_avg[g])
+            a.exp_avg_sq[g] = _ptr_or_null(exp_avg_sq[g])
+        keep = sh.f32(binoms)
+        a.count, a.cap_max, a.sh_degree, a.min_opacity, a.n_max = count, cap_max, sh_degree, min_opacity, n_max
+        a.binoms, a.rng = sh.ptr(keep), C.pointer(rng)
+        lists = None
+        if want_lists:
+            cap = params[3].shape[0]
+            lists = [np.zeros(cap, np.int64) for _ in range(3)]
+            a.relocated_dead, a.relocation_src, a.added_src = (sh.ptr(x) for x in lists)
+            a.capacity = cap
+        self._call("mcmc_refine", C.byref(a))
+        o = sh.RefineOutputs(a.new_count, a.n_relocated, a.n_added)
+        return sh.refine_lists(o, lists)
+
 
 class Reference(sh.Ops):
     """The reference's own CPU kernels (oracle/_ref/libsx_ref.so, built from /root/reference)."""
@@ -134,6 +195,39 @@ class Reference(sh.Ops):
         out = np.zeros(n_max * n_max, np.float32)
         self._call("make_binoms_lut", n_max, sh.ptr(out))
         return out
+
+    def trainer_mcmc_refine(self, params, exp_avg, exp_avg_sq, count, cap_max, sh_degree, seed, n_refine,
+                            min_opacity=0.005):
+        """The reference's Trainer (CPU backend, MCMC on) after n_refine calls of mcmc_refine.
+
+        params: count-row AoS arrays; exp_avg / exp_avg_sq: cap_max-row arrays. Returns cap_max-row
+        arrays, the count and list sizes after every refine, the last refine's lists and the
+        engine state."""
+        c = RefCase()
+        dims = sh.GROUP_DIMS(sh_degree)
+        outs = [[np.zeros((cap_max, d), np.float32) for d in dims] for _ in range(3)]
+        keep = [[sh.f32(x) for x in grp] for grp in (params, exp_avg, exp_avg_sq)]
+        for g in range(6):
+            c.params[g] = _ptr_or_null(keep[0][g])
+            c.exp_avg[g] = _ptr_or_null(keep[1][g])
+            c.exp_avg_sq[g] = _ptr_or_null(keep[2][g])
+            c.out_params[g] = _ptr_or_null(outs[0][g])
+            c.out_exp_avg[g] = _ptr_or_null(outs[1][g])
+            c.out_exp_avg_sq[g] = _ptr_or_null(outs[2][g])
+        c.count, c.cap_max, c.sh_degree, c.min_opacity, c.seed, c.n_refine = (count, cap_max, sh_degree, min_opacity,
+                                                                              seed, n_refine)
+        per = [np.zeros(n_refine, np.int64) for _ in range(3)]
+        c.counts, c.n_relocated, c.n_added = (sh.ptr(x) for x in per)
+        lists = [np.zeros(cap_max, np.int64) for _ in range(3)]
+        c.relocated_dead, c.relocation_src, c.added_src = (sh.ptr(x) for x in lists)
+        c.capacity = cap_max
+        st = sh.MtState()
+        c.rng_out = C.pointer(st)
+        self._call("trainer_mcmc_refine", C.byref(c))
+        nr, na = int(per[1][-1]), int(per[2][-1])
+        return dict(params=outs[0], exp_avg=outs[1], exp_avg_sq=outs[2], counts=per[0], n_relocated=per[1],
+                    n_added=per[2], relocated_dead=lists[0][:nr], relocation_src=lists[1][:nr],
+                    added_src=lists[2][:na], rng=st)
 
     @staticmethod
     def available() -> bool:

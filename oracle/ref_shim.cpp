@@ -1,17 +1,49 @@
-// ref_shim.cpp — C entry points over the reference's own CPU kernels (TEST INFRASTRUCTURE ONLY).
+// ref_shim.cpp — C entry points over the reference's own CPU code (TEST INFRASTRUCTURE ONLY).
 //
-// Compiled by oracle/Makefile together with Sources/SplatXCore/CpuKernels.cpp and Math.cpp taken
-// in place from the reference tree, into oracle/_ref/libsx_ref.so. It converts the C structs of
-// include/splatx_hip.h to the reference's KernelBackend.h structs and calls the reference's
-// functions unchanged, so tests can cross-check the oracle restatement against the real thing.
+// Compiled by oracle/Makefile together with Sources/SplatXCore/{CpuKernels,Math,CpuBackend,Trainer,
+// Checkpoint}.cpp taken in place from the reference tree, into oracle/_ref/libsx_ref.so. It
+// converts the C structs of include/splatx_hip.h to the reference's KernelBackend.h structs and
+// calls the reference's functions unchanged (for the MCMC refine: a reference Trainer on the
+// reference CPU backend), so tests can cross-check the oracle restatement against the real thing.
 #include <cstring>
+#include <memory>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 
+#include "splatx/Checkpoint.h"
 #include "splatx/CpuKernels.h"
 #include "splatx/KernelBackend.h"
 #include "splatx/Math.h"
+#include "splatx/Trainer.h"
 #include "splatx_hip.h"
+
+extern "C" {
+/* One reference Trainer with MCMC on (CPU backend): n_refine calls of Trainer::mcmc_refine on a
+ * cloud of `count` rows and cap_max-row Adam moments. Outputs are cap_max-row arrays. */
+typedef struct {
+    const float* params[6];   /* [count, dim] */
+    const float* exp_avg[6];  /* [cap_max, dim] */
+    const float* exp_avg_sq[6];
+    int64_t count, cap_max;
+    int32_t sh_degree;
+    float min_opacity;
+    uint64_t seed;
+    int32_t n_refine;
+    /* outputs */
+    float* out_params[6];     /* [cap_max, dim] */
+    float* out_exp_avg[6];
+    float* out_exp_avg_sq[6];
+    int64_t* counts;          /* [n_refine] count after each refine */
+    int64_t* n_relocated;     /* [n_refine] */
+    int64_t* n_added;         /* [n_refine] */
+    int64_t* relocated_dead;  /* last refine's lists, `capacity` entries each */
+    int64_t* relocation_src;
+    int64_t* added_src;
+    int64_t capacity;
+    sxh_mt64_state* rng_out;  /* the engine after the last refine (its checkpoint text) */
+} sxr_refine_case;
+}
 
 namespace {
 thread_local std::string g_err;
@@ -195,6 +227,65 @@ int32_t sxr_quat_scale_to_covar(const float* quats, const float* scales, int64_t
             const splatx::Mat3 c = splatx::quat_scale_to_covar(quats + i * 4, scales + i * 3);
             std::memcpy(out + i * 9, c.m, sizeof(c.m));
         }
+    });
+}
+
+int32_t sxr_trainer_mcmc_refine(sxr_refine_case* c) {
+    return guarded([&] {
+        auto cpu = splatx::make_cpu_backend();
+        splatx::SplatCloud cloud;
+        cloud.count = c->count;
+        cloud.sh_degree = c->sh_degree;
+        std::vector<float>* vs[6] = {&cloud.means, &cloud.quats, &cloud.scales,
+                                     &cloud.opacities, &cloud.sh0, &cloud.shN};
+        const int64_t dims[6] = {3, 4, 3, 1, 3, static_cast<int64_t>(cloud.sh_rest_coeffs()) * 3};
+        for (int g = 0; g < 6; g++) vs[g]->assign(c->params[g], c->params[g] + c->count * dims[g]);
+        splatx::TrainConfig cfg;
+        cfg.total_iters = 1000;
+        cfg.mcmc.enabled = true;
+        cfg.mcmc.cap_max = c->cap_max;
+        cfg.mcmc.min_opacity = c->min_opacity;
+        cfg.mcmc.seed = c->seed;
+        splatx::Trainer tr(*cpu, std::move(cloud), cfg);
+        const splatx::Trainer::ParamGroup groups[6] = {
+            splatx::Trainer::ParamGroup::Means, splatx::Trainer::ParamGroup::Quats,
+            splatx::Trainer::ParamGroup::Scales, splatx::Trainer::ParamGroup::Opacities,
+            splatx::Trainer::ParamGroup::Sh0, splatx::Trainer::ParamGroup::ShN};
+        for (int g = 0; g < 6; g++) {
+            splatx::AdamState& st = tr.adam_state(groups[g]);
+            st.exp_avg.assign(c->exp_avg[g], c->exp_avg[g] + c->cap_max * dims[g]);
+            st.exp_avg_sq.assign(c->exp_avg_sq[g], c->exp_avg_sq[g] + c->cap_max * dims[g]);
+        }
+        splatx::Trainer::McmcRefineResult last;
+        for (int r = 0; r < c->n_refine; r++) {
+            last = tr.mcmc_refine();
+            c->counts[r] = tr.splat_count();
+            c->n_relocated[r] = static_cast<int64_t>(last.relocated_dead.size());
+            c->n_added[r] = static_cast<int64_t>(last.added_src.size());
+        }
+        const splatx::SplatCloud& out = tr.cloud();
+        const std::vector<float>* os[6] = {&out.means, &out.quats, &out.scales,
+                                           &out.opacities, &out.sh0, &out.shN};
+        for (int g = 0; g < 6; g++) {
+            put(c->out_params[g], *os[g]);
+            const splatx::AdamState& st = tr.adam_state(groups[g]);
+            put(c->out_exp_avg[g], st.exp_avg);
+            put(c->out_exp_avg_sq[g], st.exp_avg_sq);
+        }
+        const auto put_list = [&](int64_t* dst, const std::vector<int64_t>& v) {
+            if (!dst) return;
+            if (static_cast<int64_t>(v.size()) > c->capacity) throw CapacityError("refine list capacity");
+            put(dst, v);
+        };
+        put_list(c->relocated_dead, last.relocated_dead);
+        put_list(c->relocation_src, last.relocation_src);
+        put_list(c->added_src, last.added_src);
+        // the engine state as the reference serializes it into a checkpoint (Trainer.cpp:1500-1510)
+        const splatx::TrainerCheckpoint ck = tr.make_checkpoint(0);
+        std::istringstream is(ck.mcmc_rng_state);
+        for (int i = 0; i < 312; i++) is >> c->rng_out->x[i];
+        is >> c->rng_out->p;
+        if (!is) throw std::runtime_error("unexpected mt19937_64 text layout");
     });
 }
 

@@ -15,6 +15,9 @@
 #include <cmath>
 #include <cstring>
 #include <numeric>
+#include <random>
+#include <sstream>
+#include <unordered_map>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -1790,6 +1793,207 @@ extern "C" int32_t sxo_train_step(sxo_step_args* a) {
                                   0.005f, 100.0f};
             check(sxo_mcmc_perturb_positions(&pi));
             a->stage_ms[15] += ms_since(t0);
+        }
+    });
+}
+
+// ------------------------------------------------------------------------------------------
+// MCMC refine — Trainer::mcmc_refine (Trainer.cpp:1273-1280): mcmc_relocate (:1284-1338) then
+// mcmc_add (:1342-1395), with multinomial_with_replacement (:1199-1218), run_relocation_for
+// (:1231-1258) and mcmc_zero_adam_rows (:1422-1435), on host AoS arrays of arena rows (the
+// reference's cap_max arena, :686-709). The engine is std::mt19937_64 itself; its state crosses
+// the C boundary in libstdc++'s text layout (312 words, then the position).
+// ------------------------------------------------------------------------------------------
+namespace {
+
+std::mt19937_64 mt_from(const sxh_mt64_state& st) {
+    std::ostringstream os;
+    for (int i = 0; i < 312; i++) os << st.x[i] << ' ';
+    os << st.p;
+    std::istringstream is(os.str());
+    std::mt19937_64 g;
+    is >> g;
+    if (!is) throw std::invalid_argument("mcmc_refine: malformed rng state");
+    return g;
+}
+
+void mt_to(const std::mt19937_64& g, sxh_mt64_state* st) {
+    std::ostringstream os;
+    os << g;
+    std::istringstream is(os.str());
+    for (int i = 0; i < 312; i++) is >> st->x[i];
+    is >> st->p;
+}
+
+float sigmoid_o(float x) { return 1.0f / (1.0f + o_exp(-x)); }  // Trainer.cpp:430
+
+float logit_o(float p) {  // Trainer.cpp:432-436
+    if (!(p > 0.0f && p < 1.0f)) throw std::invalid_argument("logit_f32: p must be in (0,1)");
+    return o_log(p / (1.0f - p));
+}
+
+// Trainer.cpp:1199-1218
+std::vector<int64_t> multinomial_o(const float* w, int64_t n_w, int64_t n_samples, std::mt19937_64& rng) {
+    std::vector<double> cdf(static_cast<size_t>(n_w));
+    double acc = 0.0;
+    for (int64_t i = 0; i < n_w; i++) {
+        if (!(w[i] >= 0.0f)) throw std::invalid_argument("multinomial: weights must be >= 0 and finite");
+        acc += static_cast<double>(w[i]);
+        cdf[static_cast<size_t>(i)] = acc;
+    }
+    if (!(acc > 0.0)) throw std::invalid_argument("multinomial: weight sum must be > 0");
+    std::vector<int64_t> out(static_cast<size_t>(n_samples));
+    for (int64_t j = 0; j < n_samples; j++) {
+        const double u = static_cast<double>(rng() >> 11) * 0x1.0p-53 * acc;
+        const int64_t idx = std::upper_bound(cdf.begin(), cdf.end(), u) - cdf.begin();
+        out[static_cast<size_t>(j)] = std::min(idx, n_w - 1);
+    }
+    return out;
+}
+
+struct RefineArrays {
+    float* p[6];
+    float* m[6];
+    float* v[6];
+    int64_t dim[6];
+};
+
+// Trainer.cpp:1231-1258 (gather + bincount ratios + the relocation op), then the source
+// opacity / scale writes of :1310-1321 (or :1367-1377)
+void relocate_sources(RefineArrays& a, const std::vector<float>& op_act, const std::vector<int64_t>& sampled,
+                      const float* binoms, int32_t n_max, float min_opacity, const char* what) {
+    const int64_t n = static_cast<int64_t>(sampled.size());
+    std::unordered_map<int64_t, int32_t> counts;
+    for (int64_t s : sampled) counts[s]++;
+    std::vector<float> g_op(static_cast<size_t>(n)), g_sc(static_cast<size_t>(n) * 3);
+    std::vector<int32_t> ratios(static_cast<size_t>(n));
+    for (int64_t j = 0; j < n; j++) {
+        const int64_t s = sampled[static_cast<size_t>(j)];
+        g_op[static_cast<size_t>(j)] = op_act[static_cast<size_t>(s)];
+        for (int k = 0; k < 3; k++) g_sc[static_cast<size_t>(j) * 3 + k] = o_exp(a.p[2][s * 3 + k]);
+        ratios[static_cast<size_t>(j)] = std::min(counts[s] + 1, n_max);
+    }
+    std::vector<float> new_op(static_cast<size_t>(n)), new_sc(static_cast<size_t>(n) * 3);
+    sxh_relocation_inputs rin{g_op.data(), g_sc.data(), ratios.data(), binoms, n, n_max, min_opacity};
+    if (sxo_mcmc_relocation(&rin, new_op.data(), new_sc.data()) != SXH_OK) throw std::runtime_error(g_err);
+    for (int64_t j = 0; j < n; j++) {
+        const int64_t s = sampled[static_cast<size_t>(j)];
+        a.p[3][s] = logit_o(new_op[static_cast<size_t>(j)]);
+        for (int k = 0; k < 3; k++) {
+            const float ns = new_sc[static_cast<size_t>(j) * 3 + k];
+            if (!(ns > 0.0f)) throw std::logic_error(std::string(what) + ": non-positive new_scale");
+            a.p[2][s * 3 + k] = o_log(ns);
+        }
+    }
+}
+
+void copy_row(RefineArrays& a, int64_t dst, int64_t src) {  // Trainer.cpp:1223-1225 over all groups
+    for (int g = 0; g < 6; g++)
+        for (int64_t k = 0; k < a.dim[g]; k++) a.p[g][dst * a.dim[g] + k] = a.p[g][src * a.dim[g] + k];
+}
+
+void zero_moments(RefineArrays& a, int64_t row) {  // Trainer.cpp:1422-1435
+    for (int g = 0; g < 6; g++)
+        for (int64_t k = 0; k < a.dim[g]; k++) {
+            a.m[g][row * a.dim[g] + k] = 0.0f;
+            a.v[g][row * a.dim[g] + k] = 0.0f;
+        }
+}
+
+}  // namespace
+
+// std::mt19937_64(seed) itself, in the C layout
+extern "C" int32_t sxo_mt64_seed(uint64_t seed, sxh_mt64_state* out) {
+    return guarded([&] {
+        std::mt19937_64 g(seed);
+        mt_to(g, out);
+    });
+}
+
+// n raw draws of std::mt19937_64 from a state (advances the state)
+extern "C" int32_t sxo_mt64_draw(sxh_mt64_state* st, int64_t n, uint64_t* out) {
+    return guarded([&] {
+        std::mt19937_64 g = mt_from(*st);
+        for (int64_t i = 0; i < n; i++) out[i] = g();
+        mt_to(g, st);
+    });
+}
+
+// the multinomial's running f64 sum (Trainer.cpp:1202-1208), left to right
+extern "C" int32_t sxo_running_sum_f64(const float* w, int64_t n, double* out) {
+    return guarded([&] {
+        double acc = 0.0;
+        for (int64_t i = 0; i < n; i++) {
+            acc += static_cast<double>(w[i]);
+            out[i] = acc;
+        }
+    });
+}
+
+extern "C" int32_t sxo_mcmc_refine(sxo_refine_args* r) {
+    return guarded([&] {
+        const char* what = "mcmc_refine";
+        if (!r || !r->rng || !r->binoms) invalid(what, "null argument");
+        if (r->count < 1 || r->cap_max < r->count) invalid(what, "bad count / cap_max");
+        const int64_t K3 = static_cast<int64_t>((r->sh_degree + 1) * (r->sh_degree + 1) - 1) * 3;
+        RefineArrays a{};
+        const int64_t dims[6] = {3, 4, 3, 1, 3, K3};
+        for (int g = 0; g < 6; g++) {
+            a.p[g] = r->params[g];
+            a.m[g] = r->exp_avg[g];
+            a.v[g] = r->exp_avg_sq[g];
+            a.dim[g] = dims[g];
+        }
+        std::mt19937_64 rng = mt_from(*r->rng);
+        r->new_count = r->count;
+        r->n_relocated = 0;
+        r->n_added = 0;
+        struct SaveRng {  // the engine state is handed back even when a phase throws
+            std::mt19937_64& g;
+            sxh_mt64_state* st;
+            ~SaveRng() { mt_to(g, st); }
+        } save{rng, r->rng};
+
+        // relocate (Trainer.cpp:1284-1338)
+        {
+            const int64_t N = r->count;
+            std::vector<float> op_act(static_cast<size_t>(N));
+            for (int64_t i = 0; i < N; i++) op_act[static_cast<size_t>(i)] = sigmoid_o(a.p[3][i]);
+            std::vector<int64_t> dead, alive;
+            for (int64_t i = 0; i < N; i++) (op_act[static_cast<size_t>(i)] <= r->min_opacity ? dead : alive).push_back(i);
+            if (!dead.empty() && !alive.empty()) {
+                std::vector<float> probs(alive.size());
+                for (size_t j = 0; j < alive.size(); j++) probs[j] = op_act[static_cast<size_t>(alive[j])];
+                const std::vector<int64_t> local = multinomial_o(probs.data(), static_cast<int64_t>(alive.size()),
+                                                                 static_cast<int64_t>(dead.size()), rng);
+                std::vector<int64_t> sampled(dead.size());
+                for (size_t j = 0; j < dead.size(); j++) sampled[j] = alive[static_cast<size_t>(local[j])];
+                relocate_sources(a, op_act, sampled, r->binoms, r->n_max, r->min_opacity, "Trainer::mcmc_relocate");
+                for (size_t j = 0; j < dead.size(); j++) copy_row(a, dead[j], sampled[j]);
+                for (int64_t s : sampled) zero_moments(a, s);
+                r->n_relocated = static_cast<int64_t>(dead.size());
+                if (r->relocated_dead && r->capacity >= r->n_relocated)
+                    std::copy(dead.begin(), dead.end(), r->relocated_dead);
+                if (r->relocation_src && r->capacity >= r->n_relocated)
+                    std::copy(sampled.begin(), sampled.end(), r->relocation_src);
+            }
+        }
+        // add (Trainer.cpp:1342-1395)
+        {
+            const int64_t N = r->count;
+            const int64_t target = std::min(r->cap_max, (N * 21 + 19) / 20);
+            const int64_t n_add = target - N;
+            if (n_add > 0) {
+                std::vector<float> op_act(static_cast<size_t>(N));
+                for (int64_t i = 0; i < N; i++) op_act[static_cast<size_t>(i)] = sigmoid_o(a.p[3][i]);
+                const std::vector<int64_t> sampled = multinomial_o(op_act.data(), N, n_add, rng);
+                relocate_sources(a, op_act, sampled, r->binoms, r->n_max, r->min_opacity, "Trainer::mcmc_add");
+                for (int64_t j = 0; j < n_add; j++) copy_row(a, N + j, sampled[static_cast<size_t>(j)]);
+                for (int64_t j = 0; j < n_add; j++) zero_moments(a, N + j);
+                r->n_added = n_add;
+                r->new_count = N + n_add;
+                if (r->added_src && r->capacity >= n_add) std::copy(sampled.begin(), sampled.end(), r->added_src);
+            }
         }
     });
 }

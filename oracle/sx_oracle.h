@@ -91,6 +91,31 @@ typedef struct {
 } sxo_step_args;
 
 int32_t sxo_train_step(sxo_step_args* a);
+
+/* Trainer::mcmc_refine (Trainer.cpp:1273-1435) on host AoS arrays of arena rows, in place. */
+typedef struct {
+    float* params[6];
+    float* exp_avg[6];
+    float* exp_avg_sq[6];
+    int64_t count, cap_max;
+    int32_t sh_degree;
+    float min_opacity;
+    int32_t n_max;
+    const float* binoms;
+    sxh_mt64_state* rng; /* in/out */
+    /* outputs */
+    int64_t new_count, n_relocated, n_added;
+    int64_t* relocated_dead; /* optional, `capacity` entries each */
+    int64_t* relocation_src;
+    int64_t* added_src;
+    int64_t capacity;
+} sxo_refine_args;
+int32_t sxo_mcmc_refine(sxo_refine_args* r);
+/* std::mt19937_64 helpers: the seeded state, n raw draws (advancing the state). */
+int32_t sxo_mt64_seed(uint64_t seed, sxh_mt64_state* out);
+int32_t sxo_mt64_draw(sxh_mt64_state* st, int64_t n, uint64_t* out);
+/* The left-to-right f64 running sum of float weights. */
+int32_t sxo_running_sum_f64(const float* w, int64_t n, double* out);
 const char* sxo_stage_name(int32_t i);
 
 #ifdef __cplusplus

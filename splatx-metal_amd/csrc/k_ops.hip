@@ -417,21 +417,8 @@ __global__ void __launch_bounds__(kBlock) k_relocation(const float* __restrict__
                                                        float* __restrict__ new_sc) {
     const int idx = blockIdx.x * kBlock + threadIdx.x;
     if (idx >= N) return;
-    const int n_idx = ratios[idx];
-    const float old_op = opac[idx];
-    float nop = 1.0f - sxm::powf_(1.0f - old_op, 1.0f / static_cast<float>(n_idx));
-    nop = sxd::smin(sxd::smax(nop, min_opacity), 1.0f - 1.1920928955078125e-07f);
-    new_op[idx] = nop;
-    float denom = 0.0f;
-    for (int i = 1; i <= n_idx; i++)
-        for (int k = 0; k <= i - 1; k++) {
-            const float bin = binoms[(i - 1) * n_max + k];
-            const float sign = (k & 1) ? -1.0f : 1.0f;
-            const float term = (sign / __builtin_sqrtf(static_cast<float>(k + 1))) *
-                               sxm::powf_(nop, static_cast<float>(k + 1));
-            denom += bin * term;
-        }
-    const float coeff = old_op / denom;
+    float coeff;
+    new_op[idx] = relocation_one(opac[idx], ratios[idx], binoms, n_max, min_opacity, &coeff);
     for (int i = 0; i < 3; i++) new_sc[idx * 3 + i] = coeff * sc[idx * 3 + i];
 }
 

@@ -173,6 +173,26 @@ __device__ __forceinline__ void quat_scale_vjp(const float* q, const float* s, c
 }
 
 
+// Eq.9 relocation of one source (CpuKernels.cpp:924-960 forms: clamp first, then the (i,k)
+// ascending sum) — shared by the per-op kernel and the device refine. Returns the new opacity and
+// the factor that scales the linear scales.
+__device__ __forceinline__ float relocation_one(float old_op, int n_idx, const float* __restrict__ binoms, int n_max,
+                                                float min_opacity, float* coeff) {
+    float nop = 1.0f - sxm::powf_(1.0f - old_op, 1.0f / static_cast<float>(n_idx));
+    nop = smin(smax(nop, min_opacity), 1.0f - 1.1920928955078125e-07f);
+    float denom = 0.0f;
+    for (int i = 1; i <= n_idx; i++)
+        for (int k = 0; k <= i - 1; k++) {
+            const float bin = binoms[(i - 1) * n_max + k];
+            const float sign = (k & 1) ? -1.0f : 1.0f;
+            const float term = (sign / __builtin_sqrtf(static_cast<float>(k + 1))) *
+                               sxm::powf_(nop, static_cast<float>(k + 1));
+            denom += bin * term;
+        }
+    *coeff = old_op / denom;
+    return nop;
+}
+
 // Perturbation of one Gaussian (CpuKernels.cpp:969-1008 forms) — shared with the fused step.
 __device__ __forceinline__ void perturb_one(float* pos, const float* q, const float* slog, float logit, const float* nz,
                             float noise_scale, float tt, float kk) {

@@ -1,0 +1,140 @@
+// sx_exec.h — the device-resident executor object (TrainStepExecutor state), shared by the step
+// (executor.cpp) and the device MCMC refine (refine.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstddef>
+
+#include "splatx_hip.h"
+#include "sx_host.h"
+#include "sx_kernels.h"
+#include "sx_step.h"
+
+namespace sxh_detail {
+
+struct PinnedHost {
+    void* p = nullptr;
+    explicit PinnedHost(size_t bytes) { SXH_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault)); }
+    ~PinnedHost() {
+        if (p) (void)hipHostFree(p);
+    }
+    PinnedHost(const PinnedHost&) = delete;
+    PinnedHost& operator=(const PinnedHost&) = delete;
+};
+
+constexpr int kMaxEvents = 32;
+
+} // namespace sxh_detail
+
+using sxh_detail::PinnedHost;
+using sxh_detail::kMaxEvents;
+
+struct sxh_executor {
+    sxh_backend* b = nullptr;
+    sxh_exec_desc d{};
+    int n_coeffs = 1;
+    int dims[6] = {3, 4, 3, 1, 3, 0};
+    int rows = 0;
+    sxh::DevBuf<float> p[6], m[6], v[6];
+    sxh::DevBuf<float4> splats, grads;
+    sxh::DevBuf<int32_t> radii, tiles;
+    sxh::DevBuf<int64_t> cum;
+    sxh::DevBuf<uint8_t> scan_scratch;
+    sxh::DevBuf<unsigned long long> n_vis;
+    sxh::DevBuf<uint32_t> vis_part;
+    // intersections (grow 1.5x, reused)
+    size_t isect_cap = 0;
+    sxh::DevBuf<uint64_t> keys_a, keys_b;
+    sxh::DevBuf<int32_t> vals_a, vals_b;
+    sxh::DevBuf<uint8_t> sort_scratch;
+    // image-sized buffers
+    size_t img_px = 0, img_tiles = 0, img_map = 0;
+    sxh::DevBuf<int32_t> offsets, last_ids;
+    sxh::DevBuf<float> render, alpha, v_render, v_alpha_zero, gt_stage;
+    sxh::DevBuf<float> cmu, csg, ccr;  // SSIM coefficient maps (the map itself is only summed)
+    sxh::DevBuf<double> ssim_part, l1_part;
+    sxh::DevBuf<float> loss_dev;
+    // GT cache
+    sxh::DevBuf<float> gt_cache;
+    int gt_n = 0, gt_w = 0, gt_h = 0;
+    sxh::DevBuf<float> staging;
+    PinnedHost host_small{64};
+    // device MCMC refine (allocated on the first refine, arena-sized)
+    sxh::DevBuf<float> mc_op_act, mc_new_logit, mc_new_log_scale, mc_binoms;
+    sxh::DevBuf<int32_t> mc_dead, mc_alive, mc_sampled;
+    sxh::DevBuf<uint32_t> mc_counts, mc_err;
+    sxh::DevBuf<double> mc_cdf, mc_total;
+    sxh::DevBuf<uint64_t> mc_raw, mc_mt;
+    // profiling
+    bool prof = false;
+    hipEvent_t ev[kMaxEvents] = {};
+    const char* ev_name[kMaxEvents] = {};
+    int n_ev = 0;
+    sxh_exec_timing timing{};
+    double sync_ms[2] = {0, 0};
+
+    sxk::Arena arena() {
+        sxk::Arena A{};
+        for (int g = 0; g < 6; g++) {
+            A.p[g] = p[g].p;
+            A.m[g] = m[g].p;
+            A.v[g] = v[g].p;
+        }
+        A.rows = rows;
+        return A;
+    }
+
+    void mark(const char* name) {
+        if (!prof || n_ev >= kMaxEvents) return;
+        SXH_HIP(hipEventRecord(ev[n_ev], b->stream));
+        ev_name[n_ev++] = name;
+    }
+
+    void ensure_isect(size_t n) {
+        if (n <= isect_cap) return;
+        const size_t cap = std::max<size_t>(n + n / 2, 1 << 16);
+        keys_a.alloc(cap);
+        keys_b.alloc(cap);
+        vals_a.alloc(cap);
+        vals_b.alloc(cap);
+        sort_scratch.alloc(sxk::sort_scratch_bytes(static_cast<int64_t>(cap)));
+        isect_cap = cap;
+    }
+
+    void ensure_image(int W, int H, bool use_ssim) {
+        const size_t px = static_cast<size_t>(W) * H;
+        const size_t tiles_n = static_cast<size_t>((W + 15) / 16) * ((H + 15) / 16);
+        const size_t map_n = use_ssim ? static_cast<size_t>(H - 10) * (W - 10) * 3 : 0;
+        if (px > img_px) {
+            render.alloc(px * 3);
+            alpha.alloc(px);
+            last_ids.alloc(px);
+            v_render.alloc(px * 3);
+            v_alpha_zero.alloc(px);
+            SXH_HIP(hipMemsetAsync(v_alpha_zero.p, 0, px * sizeof(float), b->stream));
+            gt_stage.alloc(px * 3);
+            img_px = px;
+        }
+        // one f64 partial per workgroup of the loss kernels (exact counts of their grids)
+        const size_t l1_blocks = std::max<size_t>(sxk::step_ssim_bwd_blocks(H, W),
+                                                  sxk::step_l1_blocks(static_cast<int64_t>(px) * 3));
+        if (l1_blocks > l1_part.n) l1_part.alloc(l1_blocks);
+        if (tiles_n > img_tiles) {
+            offsets.alloc(tiles_n);
+            img_tiles = tiles_n;
+        }
+        if (use_ssim) {
+            if (map_n > img_map) {
+                cmu.alloc(map_n);
+                csg.alloc(map_n);
+                ccr.alloc(map_n);
+                img_map = map_n;
+            }
+            const size_t ss_blocks = static_cast<size_t>(sxk::ssim_fwd_blocks(1, H, W, 3));
+            if (ss_blocks > ssim_part.n) ssim_part.alloc(ss_blocks);
+        }
+    }
+};
+

@@ -34,7 +34,7 @@ def group_dims(sh_degree: int):
 
 
 def make_params(n, sh_degree, seed, xy=2.0, z=(2.0, 10.0), log_scale_mu=math.log(0.02), log_scale_sd=0.5,
-                dc_sd=0.5, rest_sd=0.05, tie_frac=0.0):
+                dc_sd=0.5, rest_sd=0.05, tie_frac=0.0, logit_sd=1.0):
     rng = np.random.Generator(np.random.PCG64(seed))
     means = np.empty((n, 3), np.float32)
     means[:, 0] = rng.uniform(-xy, xy, n)
@@ -46,7 +46,7 @@ def make_params(n, sh_degree, seed, xy=2.0, z=(2.0, 10.0), log_scale_mu=math.log
     q = rng.standard_normal((n, 4)).astype(np.float32)
     q /= np.linalg.norm(q, axis=1, keepdims=True)
     log_s = rng.normal(log_scale_mu, log_scale_sd, (n, 3)).astype(np.float32)
-    logit = rng.standard_normal(n).astype(np.float32)
+    logit = (rng.standard_normal(n) * logit_sd).astype(np.float32)
     sh0 = rng.normal(0.0, dc_sd, (n, 3)).astype(np.float32)
     K = (sh_degree + 1) ** 2
     shN = rng.normal(0.0, rest_sd, (n, (K - 1) * 3)).astype(np.float32)
@@ -94,6 +94,12 @@ CONFIGS = {
     2: dict(n=100_000, sh_degree=3, width=800, height=800, fx=720.0, isect="aabb", ssim=0.2, target="scene"),
     3: dict(n=1_000_000, sh_degree=3, width=1297, height=840, fx=1150.0, isect="accutile", ssim=0.2,
             target="scene", xy=4.0, z=(1.5, 20.0), log_scale_mu=math.log(0.01), log_scale_sd=0.7),
+    # MCMC at scale: 3M live rows in a 4M arena; logits ~ N(0, 3.2^2) put ~5% of the rows at or
+    # below the dead threshold sigmoid(logit) <= 0.005 (logit <= -5.29), i.e. the 5% lowest
+    # opacities relocate; opacity and scale regularization 1e-2 each
+    4: dict(n=3_000_000, cap_max=4_000_000, sh_degree=3, width=1297, height=840, fx=1150.0, isect="accutile",
+            ssim=0.2, target="scene", xy=4.0, z=(1.5, 20.0), log_scale_mu=math.log(0.01), log_scale_sd=0.7,
+            logit_sd=3.2, opacity_reg=1e-2, scale_reg=1e-2, min_opacity=0.005),
     5: dict(n=2_000_000, sh_degree=3, width=1920, height=1080, fx=1600.0, isect="accutile", ssim=0.2,
             target="scene", xy=2.8, z=(2.0, 4.0), log_scale_mu=math.log(0.08), log_scale_sd=0.5, tie_frac=0.1,
             antialiased=True),
@@ -102,7 +108,7 @@ CONFIGS = {
 
 def config_scene(cfg_id: int, seed: int = 0) -> tuple[Scene, dict]:
     c = dict(CONFIGS[cfg_id])
-    kw = {k: c.pop(k) for k in ("xy", "z", "log_scale_mu", "log_scale_sd", "tie_frac") if k in c}
+    kw = {k: c.pop(k) for k in ("xy", "z", "log_scale_mu", "log_scale_sd", "tie_frac", "logit_sd") if k in c}
     n, deg, w, h, fx = c["n"], c["sh_degree"], c["width"], c["height"], c["fx"]
     params = make_params(n, deg, seed, **kw)
     sc = Scene(n=n, sh_degree=deg, params=params, width=w, height=h, viewmat=identity_view(),

@@ -179,6 +179,39 @@ class StepOutputs(C.Structure):
                 ("render_colors", fp), ("sort_key_bits", C.c_uint32)]
 
 
+class MtState(C.Structure):
+    """std::mt19937_64 in libstdc++'s layout: 312 words and the next-word position."""
+    _fields_ = [("x", C.c_uint64 * 312), ("p", C.c_uint32)]
+
+    def copy(self) -> "MtState":
+        c = MtState()
+        C.memmove(C.byref(c), C.byref(self), C.sizeof(MtState))
+        return c
+
+    def equals(self, other: "MtState") -> bool:
+        return self.p == other.p and list(self.x) == list(other.x)
+
+
+class RefineInputs(C.Structure):
+    _fields_ = [("count", C.c_int64), ("cap_max", C.c_int64), ("min_opacity", C.c_float), ("n_max", C.c_int32),
+                ("binoms", fp), ("rng", C.POINTER(MtState)), ("inject_noise", C.c_uint8),
+                ("noise_seed", C.c_uint64), ("noise_offset", C.c_uint64), ("noise_scale", C.c_float)]
+
+
+class RefineOutputs(C.Structure):
+    _fields_ = [("count", C.c_int64), ("n_relocated", C.c_int64), ("n_added", C.c_int64),
+                ("relocated_dead", i64p), ("relocation_src", i64p), ("added_src", i64p), ("capacity", C.c_int64)]
+
+
+def refine_lists(out: RefineOutputs, lists) -> dict:
+    r = dict(count=int(out.count), n_relocated=int(out.n_relocated), n_added=int(out.n_added))
+    if lists is not None:
+        r["relocated_dead"] = lists[0][:out.n_relocated].copy()
+        r["relocation_src"] = lists[1][:out.n_relocated].copy()
+        r["added_src"] = lists[2][:out.n_added].copy()
+    return r
+
+
 class ExecTiming(C.Structure):
     _fields_ = [("n", C.c_int32), ("names", C.c_char_p * 32), ("ms", C.c_float * 32)]
 
@@ -481,6 +514,29 @@ class Backend(Ops):
     def make_train_step_executor(self, **desc) -> "Executor":
         return Executor(self, **desc)
 
+    def running_sum_f64(self, w):
+        """The multinomial's left-to-right f64 running sum on the device (sxh_running_sum_f64)."""
+        w = f32(w).ravel()
+        out = np.zeros(w.size, np.float64)
+        self._call("running_sum_f64", ptr(w), C.c_int64(w.size), out.ctypes.data_as(C.POINTER(C.c_double)))
+        return out
+
+    def mt64_draw(self, st: MtState, n: int):
+        """n draws of std::mt19937_64 on the device (sxh_mt64_draw); `st` advanced in place."""
+        out = np.zeros(n, np.uint64)
+        self._call("mt64_draw", C.byref(st), C.c_int64(n), ptr(out))
+        return out
+
+    def mt64_seed(self, seed: int) -> MtState:
+        """std::mt19937_64(seed) state (sxh_mt64_seed)."""
+        st = MtState()
+        f = self.lib.sxh_mt64_seed
+        f.restype = C.c_int32
+        f.argtypes = [C.c_uint64, C.POINTER(MtState)]
+        if f(seed, C.byref(st)) != SXH_OK:
+            raise SxInvalidArgument(self.lib.sxh_last_error().decode())
+        return st
+
 
 GROUP_DIMS = lambda sh_degree: [3, 4, 3, 1, 3, ((sh_degree + 1) ** 2 - 1) * 3]
 
@@ -503,7 +559,8 @@ class Executor:
         self._check(self.lib.sxh_exec_create(backend.handle, C.byref(d), C.byref(h)))
         self.h = h
         for n in ("sxh_exec_upload", "sxh_exec_download", "sxh_exec_step", "sxh_exec_set_gt_cache",
-                  "sxh_exec_render_to_gt_cache", "sxh_exec_set_profiling", "sxh_exec_get_timing"):
+                  "sxh_exec_render_to_gt_cache", "sxh_exec_set_profiling", "sxh_exec_get_timing",
+                  "sxh_exec_mcmc_refine"):
             getattr(self.lib, n).restype = C.c_int32
         self.lib.sxh_exec_destroy.argtypes = [C.c_void_p]
 
@@ -512,6 +569,8 @@ class Executor:
             msg = self.lib.sxh_last_error().decode(errors="replace")
             if rc == SXH_ERR_INVALID_ARGUMENT:
                 raise SxInvalidArgument(msg)
+            if rc == SXH_ERR_CAPACITY:
+                raise SxCapacityError(msg)
             raise SxRuntimeError(msg)
 
     def close(self):
@@ -565,6 +624,22 @@ class Executor:
     def render_to_gt_cache(self, index, **kw):
         s, keep = self.make_step_inputs(**kw)
         self._check(self.lib.sxh_exec_render_to_gt_cache(self.h, C.byref(s), index))
+
+    def mcmc_refine(self, count, cap_max, rng: MtState, binoms, min_opacity=0.005, n_max=51, inject_noise=False,
+                    noise_seed=0, noise_offset=0, noise_scale=0.0, want_lists=False, capacity=None):
+        """Trainer::mcmc_refine on the arena (sxh_exec_mcmc_refine); `rng` is advanced in place."""
+        binoms = f32(binoms)
+        i = RefineInputs(count, cap_max, min_opacity, n_max, ptr(binoms), C.pointer(rng), int(bool(inject_noise)),
+                         noise_seed, noise_offset, noise_scale)
+        lists = None
+        o = RefineOutputs()
+        if want_lists:
+            cap = self.arena_rows if capacity is None else capacity
+            lists = [np.zeros(max(cap, 1), np.int64) for _ in range(3)]
+            o.relocated_dead, o.relocation_src, o.added_src = (ptr(a) for a in lists)
+            o.capacity = cap
+        self._check(self.lib.sxh_exec_mcmc_refine(self.h, C.byref(i), C.byref(o)))
+        return refine_lists(o, lists)
 
     def set_profiling(self, enable: bool):
         self._check(self.lib.sxh_exec_set_profiling(self.h, int(bool(enable))))

@@ -99,3 +99,24 @@ def sort_inputs(n, key_bits, seed=0, ties=True):
 def stable_sort_ref(keys, vals):
     order = np.argsort(keys, kind="stable")
     return keys[order], vals[order]
+
+
+def make_cloud(n, cap, sh_degree, seed, logit_mu=-1.0, logit_sd=3.0, moments=True):
+    """Arena arrays [cap, dim] (rows >= n zero), seeded: ~5% dead at the default logit spread."""
+    r = np.random.default_rng(seed)
+    dims = scene.group_dims(sh_degree)
+    p = [np.zeros((cap, d), np.float32) for d in dims]
+    p[0][:n] = r.normal(0, 2, (n, 3))
+    p[1][:n] = r.normal(0, 1, (n, 4))
+    p[2][:n] = r.normal(np.log(0.01), 0.7, (n, 3))
+    p[3][:n, 0] = r.normal(logit_mu, logit_sd, n)
+    p[4][:n] = r.normal(0, 0.5, (n, 3))
+    if dims[5]:
+        p[5][:n] = r.normal(0, 0.05, (n, dims[5]))
+    m = [np.zeros((cap, d), np.float32) for d in dims]
+    v = [np.zeros((cap, d), np.float32) for d in dims]
+    if moments:
+        for g in range(6):
+            m[g][:n] = r.normal(0, 1e-3, (n, dims[g]))
+            v[g][:n] = np.abs(r.normal(0, 1e-6, (n, dims[g])))
+    return p, m, v
