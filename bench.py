@@ -135,6 +135,8 @@ def main():
 
     sc, cfg = scene.config_scene(args.config, seed=0)
     tgt, _ = scene.config_scene(args.config, seed=1)
+    mcmc = "cap_max" in cfg  # config 4: MCMC arena, a device refine after every step
+    arena = cfg.get("cap_max", sc.n)
     n_poses = args.steps + args.warmup
     rng = np.random.Generator(np.random.PCG64(1234))
     poses = [scene.jittered_view(rng) for _ in range(n_poses)]
@@ -143,7 +145,7 @@ def main():
     aa = bool(cfg.get("antialiased", False))
 
     b = sh.Backend(0)
-    ex = b.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
+    ex = b.make_train_step_executor(arena_rows=arena, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
                                     antialiased=aa, isect_mode=isect)
     # targets: the second scene rendered from every pose into the device GT cache
     ex.set_gt_cache(np.zeros((n_poses, sc.height, sc.width, 3), np.float32))
@@ -156,23 +158,40 @@ def main():
         if k == args.warmup:  # host copy of the first timed target, for the CPU baseline
             gt_first = ex.step(want_render=True, forward_only=True, **dict(base, viewmat=poses[k]))["render_colors"]
     p, m, v = scene.copy_state(sc)
-    ex.upload_params(p, m, v, sc.n)
+    if mcmc:  # the arena beyond the live rows starts at zero (Trainer.cpp:686-709)
+        p, m, v = ([np.concatenate([x.reshape(sc.n, -1), np.zeros((arena - sc.n, x.reshape(sc.n, -1).shape[1]),
+                                                                  np.float32)]) for x in grp] for grp in (p, m, v))
+    ex.upload_params(p, m, v, arena)
 
     # pre-built step arguments (no host work inside the timed loop beyond the step itself)
-    steps = []
-    for k in range(n_poses):
-        s_in, keep = ex.make_step_inputs(**dict(base, viewmat=poses[k]), gt_index=k)
-        steps.append((s_in, keep))
+    count = sc.n
+
+    def step_inputs(k, count):
+        extra = {}
+        if mcmc:  # Trainer.cpp:920-935: regularization weights over the live count; no noise on refine steps
+            extra = dict(count=count, opacity_reg_w=cfg["opacity_reg"] / count,
+                         scale_reg_w=cfg["scale_reg"] / (3 * count))
+        return ex.make_step_inputs(**dict(base, viewmat=poses[k], **extra), gt_index=k)
+
+    steps = [step_inputs(k, count) for k in range(n_poses)]
     out = sh.StepOutputs()
     for k in range(args.warmup):
         rc = ex.step_raw(steps[k][0], out)
         assert rc == 0, b.lib.sxh_last_error()
+
+    refine_ms, counts = [], []
+    if mcmc:
+        binoms = b.make_binoms_lut(51)
+        rng_state = b.mt64_seed(42)
+        noise_lr = 5e5  # McmcOptions::noise_lr (Trainer.h:195); noise_scale = lr_means * noise_lr
 
     ex.set_profiling(True)
     totals = {}
     n_isects, n_vis, losses, passes = [], [], [], []
     t0 = time.perf_counter()
     for k in range(args.warmup, n_poses):
+        if mcmc and count != sc.n:
+            steps[k] = step_inputs(k, count)
         rc = ex.step_raw(steps[k][0], out)
         if rc != 0:
             raise RuntimeError(b.lib.sxh_last_error())
@@ -182,6 +201,13 @@ def main():
         n_vis.append(out.n_visible)
         passes.append((out.sort_key_bits + 7) // 8)
         losses.append(out.loss)
+        if mcmc:  # the refine step of Trainer::step_resident (Trainer.cpp:957-967): refine, then noise
+            tr = time.perf_counter()
+            r = ex.mcmc_refine(count, arena, rng_state, binoms, min_opacity=cfg["min_opacity"], inject_noise=True,
+                               noise_seed=42, noise_offset=k, noise_scale=lr[0] * noise_lr)
+            refine_ms.append((time.perf_counter() - tr) * 1000.0)
+            count = r["count"]
+            counts.append(count)
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
     avg = {k: x / args.steps for k, x in totals.items()}
@@ -231,6 +257,13 @@ def main():
         "kernels": per_kernel,
         "host_waits_ms": {k: round(avg[k], 4) for k in avg if k.startswith("host_")},
     }
+    if mcmc:
+        res["config"]["workload"] = (f"config 4: {sc.n} live of a {arena}-row arena, SH{sc.sh_degree}, "
+                                     f"{sc.width}x{sc.height}, AccuTile, SSIM, opacity/scale reg 1e-2; every step "
+                                     f"is a refine step (step, device MCMC refine, noise)")
+        res["mcmc"] = {"refine_ms_mean": round(float(np.mean(refine_ms)), 3),
+                       "refine_ms_median": round(float(np.median(refine_ms)), 3),
+                       "count_first": int(counts[0]), "count_last": int(counts[-1])}
     ex.close()
     b.close()
     if not args.no_cpu_baseline:

@@ -5,8 +5,8 @@
 //   k_mc_activate   sigmoid_f32 of every live logit (Trainer.cpp:430, 455-459) + dead flags
 //                   (:1288-1291) + NaN detection for the multinomial's weight check (:1205-1206)
 //   k_mc_compact    stable dead / alive index lists from an int64 scan of the flags
-//   k_mc_cdf        the multinomial's running f64 sum (:1202-1208), bit-identical to the
-//                   left-to-right accumulation but computed by a whole workgroup (see below)
+//   k_cdf_*         the multinomial's running f64 sum (:1202-1208), bit-identical to the
+//                   left-to-right accumulation but computed as a scan (see below)
 //   k_mc_mt_gen     std::mt19937_64 words: the 312-word twist in LDS, one workgroup
 //   k_mc_search     u = (r >> 11) * 2^-53 * acc, upper_bound on the cdf, clamp (:1211-1216),
 //                   source index and bincount (:1238-1240)
@@ -60,13 +60,24 @@ __global__ void __launch_bounds__(kBlock) k_mc_compact(const int32_t* __restrict
 // RN(a*u + w) = (a + r)*u, where w = q*u + f (0 <= f < u) and r = q below the half-ulp, q + 1
 // above it, and at an exact half the choice that leaves a + r even. So each element is a map on
 // the parity of a: non-tie elements add r and flip parity by r's low bit, ties add q or q + 1 and
-// leave a even. These maps compose associatively, so a workgroup scans 8192 of them at a time;
-// the first element whose sum leaves the binade (a >= 2^53) is recomputed with a plain f64 add,
-// and the scan restarts after it in the new binade. The result equals the sequential loop bit for
-// bit; there are only as many restarts as binades crossed (about 20-40 for millions of weights).
-constexpr int kCdfThreads = 1024;
-constexpr int kCdfPer = 8;
-constexpr int kCdfChunk = kCdfThreads * kCdfPer;
+// leave a even. These maps compose associatively, which makes the left-to-right sum a scan:
+//   A  chunk sums (4096 weights per workgroup, any order: only used to predict)
+//   B  predicted binade of every chunk from the approximate prefix, or "uncertain" near a power of 2
+//   C  per chunk, the composed map of its weights in the predicted binade
+//   D  one workgroup walks the chunks in order with the exact running sum: a chunk whose start lies
+//      in the predicted binade and whose composed map keeps a < 2^53 advances in O(1); any other
+//      chunk (the first, those that cross a binade, wrong predictions) is summed by the whole
+//      workgroup element-exactly, restarting after each element that leaves the binade
+//   E  per chunk not summed in D, the exact start value + an in-chunk scan of the maps -> cdf.
+// The result equals the sequential loop bit for bit whatever the predictions were (D checks them);
+// they only decide how many chunks take the slow path (those that cross one of the 20-40 binades).
+constexpr int kCdfChunk = 4096;
+constexpr int kCdfBlock = 256;
+constexpr int kCdfPerT = kCdfChunk / kCdfBlock;  // 16
+constexpr int kWalkThreads = 512;
+constexpr int kWalkPer = kCdfChunk / kWalkThreads;  // 4
+constexpr int kWalkTile = kWalkThreads;  // chunk records staged in LDS at a time (one per thread)
+constexpr int kUncertain = -100000;
 constexpr uint64_t kSat = 1ull << 62;
 constexpr uint64_t kTwo53 = 1ull << 53;
 constexpr int64_t kNone = INT64_MAX;
@@ -135,125 +146,394 @@ __device__ __forceinline__ ParMap pm_shfl_up(const ParMap& v, int delta) {
     return r;
 }
 
-__global__ void __launch_bounds__(kCdfThreads) k_mc_cdf(const float* __restrict__ w_all,
-                                                        const int32_t* __restrict__ gather, int64_t n,
-                                                        double* __restrict__ cdf, double* __restrict__ total,
-                                                        uint32_t* __restrict__ err) {
-    __shared__ ParMap s_wave[kCdfThreads / 64];
-    __shared__ unsigned long long s_cross;
-    __shared__ double s_next;
+__device__ __forceinline__ int exponent_of(double s) {
+    return static_cast<int>((static_cast<uint64_t>(__double_as_longlong(s)) >> 52) & 0x7ffu) - 1023;
+}
+__device__ __forceinline__ uint64_t units_of(double s) {  // s / ulp(s) for a normal s
+    const uint64_t sb = static_cast<uint64_t>(__double_as_longlong(s));
+    return (sb & ((1ull << 52) - 1u)) | (1ull << 52);
+}
+__device__ __forceinline__ double ulp_of_binade(int E) {
+    return __longlong_as_double(static_cast<long long>(static_cast<uint64_t>(E - 52 + 1023) << 52));
+}
+
+__device__ __forceinline__ float load_w(const float* __restrict__ w_all, const int32_t* __restrict__ gather,
+                                        int64_t i) {
+    return w_all[gather ? gather[i] : i];
+}
+
+// Ordered exclusive scan of one map per thread over a workgroup of NT threads; returns the
+// composition of the maps of all lower threads and sets `all` to the workgroup's total.
+template <int NT>
+__device__ __forceinline__ ParMap wg_exclusive_scan(ParMap x, ParMap* s_wave, ParMap& all) {
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    double s = 0.0;  // running sum before element `start` (uniform)
-    int64_t start = 0;
-    bool bad = false;
-    while (start < n) {
-        if (t == 0) s_cross = static_cast<unsigned long long>(kNone);
-        const int64_t base = start + static_cast<int64_t>(t) * kCdfPer;
-        const int64_t chunk_end = start + kCdfChunk < n ? start + kCdfChunk : n;
-        float w[kCdfPer];
 #pragma unroll
-        for (int j = 0; j < kCdfPer; j++) {
-            const int64_t i = base + j;
-            w[j] = 0.0f;
-            if (i < chunk_end) {
-                w[j] = w_all[gather ? gather[i] : i];
-                bad |= !(w[j] >= 0.0f);
-            }
+    for (int off = 1; off < 64; off <<= 1) {
+        const ParMap y = pm_shfl_up(x, off);
+        if (lane >= off) x = pm_compose(y, x);
+    }
+    const ParMap lanes_before = pm_shfl_up(x, 1);
+    if (lane == 63) s_wave[wv] = x;
+    __syncthreads();
+    ParMap pre = pm_identity();
+    all = pm_identity();
+#pragma unroll
+    for (int k = 0; k < NT / 64; k++) {
+        if (k < wv) pre = pm_compose(pre, s_wave[k]);
+        all = pm_compose(all, s_wave[k]);
+    }
+    if (lane > 0) pre = pm_compose(pre, lanes_before);
+    return pre;
+}
+
+// A: chunk sums in f64 (any order) + the NaN check of the multinomial
+__global__ void __launch_bounds__(kCdfBlock) k_cdf_chunk_sum(const float* __restrict__ w_all,
+                                                             const int32_t* __restrict__ gather, int64_t n,
+                                                             double* __restrict__ chunk_sum,
+                                                             uint32_t* __restrict__ err) {
+    __shared__ double s_red[kCdfBlock / 64];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kCdfChunk;
+    double acc = 0.0;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < kCdfPerT; j++) {
+        const int64_t i = base + j * kCdfBlock + threadIdx.x;
+        if (i < n) {
+            const float w = load_w(w_all, gather, i);
+            bad |= !(w >= 0.0f);
+            acc += static_cast<double>(w);
         }
+    }
+    if (bad) atomicOr(err, kMcErrWeights);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+#pragma unroll
+        for (int k = 0; k < kCdfBlock / 64; k++) t += s_red[k];
+        chunk_sum[blockIdx.x] = t;
+    }
+}
+
+// B: approximate prefix of the chunk sums -> predicted binade of each chunk (kUncertain when the
+// chunk's approximate range comes within a relative 2^-20 of a power of two, or starts at 0)
+__global__ void __launch_bounds__(kWalkThreads) k_cdf_predict(const double* __restrict__ chunk_sum, int n_chunks,
+                                                              int32_t* __restrict__ chunk_E) {
+    __shared__ double s_v[kWalkThreads];
+    double carry = 0.0;
+    for (int tile = 0; tile < n_chunks; tile += kWalkThreads) {
+        const int c = tile + static_cast<int>(threadIdx.x);
+        const double v = c < n_chunks ? chunk_sum[c] : 0.0;
+        s_v[threadIdx.x] = v;
+        __syncthreads();
+        for (int off = 1; off < kWalkThreads; off <<= 1) {  // inclusive Hillis-Steele scan
+            const double y = threadIdx.x >= static_cast<unsigned>(off) ? s_v[threadIdx.x - off] : 0.0;
+            __syncthreads();
+            s_v[threadIdx.x] += y;
+            __syncthreads();
+        }
+        const double incl = carry + s_v[threadIdx.x];
+        const double excl = incl - v;
+        if (c < n_chunks) {
+            const double lo = excl * (1.0 - 0x1.0p-20), hi = incl * (1.0 + 0x1.0p-20);
+            const int Elo = exponent_of(lo), Ehi = exponent_of(hi);
+            chunk_E[c] = (excl > 0.0 && Elo == Ehi) ? Elo : kUncertain;
+        }
+        carry += s_v[kWalkThreads - 1];
+        __syncthreads();
+    }
+}
+
+// C: composed map of each chunk in its predicted binade
+__global__ void __launch_bounds__(kCdfBlock) k_cdf_chunk_map(const float* __restrict__ w_all,
+                                                             const int32_t* __restrict__ gather, int64_t n,
+                                                             const int32_t* __restrict__ chunk_E,
+                                                             uint64_t* __restrict__ map_d0,
+                                                             uint64_t* __restrict__ map_d1,
+                                                             uint32_t* __restrict__ map_o) {
+    __shared__ ParMap s_wave[kCdfBlock / 64];
+    const int E = chunk_E[blockIdx.x];
+    if (E == kUncertain) return;  // uniform over the workgroup
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kCdfChunk + static_cast<int64_t>(threadIdx.x) * kCdfPerT;
+    ParMap acc = pm_identity();
+#pragma unroll
+    for (int j = 0; j < kCdfPerT; j++) {
+        const int64_t i = base + j;
+        if (i < n) acc = pm_compose(acc, pm_of(load_w(w_all, gather, i), E));
+    }
+    ParMap all;
+    (void)wg_exclusive_scan<kCdfBlock>(acc, s_wave, all);
+    if (threadIdx.x == 0) {
+        map_d0[blockIdx.x] = all.d0;
+        map_d1[blockIdx.x] = all.d1;
+        map_o[blockIdx.x] = all.o;
+    }
+}
+
+// The element-exact sum of [begin, end) by the whole walk workgroup, starting from the exact s;
+// writes cdf[begin, end) and returns the sum after end - 1. Uniform call (contains barriers).
+__device__ double cdf_range_exact(const float* __restrict__ w_all, const int32_t* __restrict__ gather,
+                                  int64_t begin, int64_t end, double s, double* __restrict__ cdf,
+                                  ParMap* s_wave, unsigned long long* s_cross, double* s_next) {
+    const int t = threadIdx.x;
+    int64_t start = begin;
+    while (start < end) {
+        __syncthreads();
+        if (t == 0) *s_cross = static_cast<unsigned long long>(kNone);
+        const int64_t base = start + static_cast<int64_t>(t) * kWalkPer;
+        float w[kWalkPer];
+#pragma unroll
+        for (int j = 0; j < kWalkPer; j++) w[j] = base + j < end ? load_w(w_all, gather, base + j) : 0.0f;
         if (s == 0.0) {
             // leading zero weights: the sum stays 0; the first positive weight is the sum itself
             __syncthreads();
+            int64_t first = kNone;
 #pragma unroll
-            for (int j = 0; j < kCdfPer; j++)
-                if (base + j < chunk_end && w[j] > 0.0f) {
-                    atomicMin(&s_cross, static_cast<unsigned long long>(base + j));
-                    break;
-                }
+            for (int j = kWalkPer - 1; j >= 0; j--)
+                if (base + j < end && w[j] > 0.0f) first = base + j;
+            if (first != kNone) atomicMin(s_cross, static_cast<unsigned long long>(first));
             __syncthreads();
-            const int64_t c = static_cast<int64_t>(s_cross);
+            const int64_t c = static_cast<int64_t>(*s_cross);
 #pragma unroll
-            for (int j = 0; j < kCdfPer; j++) {
+            for (int j = 0; j < kWalkPer; j++) {
                 const int64_t i = base + j;
-                if (i < chunk_end && i < c) cdf[i] = 0.0;
+                if (i < end && i < c) cdf[i] = 0.0;
                 if (i == c) {
                     cdf[i] = static_cast<double>(w[j]);
-                    s_next = static_cast<double>(w[j]);
+                    *s_next = static_cast<double>(w[j]);
                 }
             }
             __syncthreads();
             if (c != kNone) {
-                s = s_next;
+                s = *s_next;
                 start = c + 1;
             } else {
-                start = chunk_end;
+                start = end;  // every weight of the range is zero; the range covers all threads' loads
             }
-            __syncthreads();
             continue;
         }
-        const uint64_t sb = static_cast<uint64_t>(__double_as_longlong(s));
-        const int E = static_cast<int>((sb >> 52) & 0x7ffu) - 1023;
-        const uint64_t a0 = (sb & ((1ull << 52) - 1u)) | (1ull << 52);
+        const int E = exponent_of(s);
+        const uint64_t a0 = units_of(s);
         const uint32_t p0 = static_cast<uint32_t>(a0 & 1u);
-        const double u = __longlong_as_double(static_cast<long long>(static_cast<uint64_t>(E - 52 + 1023) << 52));
-        ParMap loc[kCdfPer];
+        const double u = ulp_of_binade(E);
+        ParMap loc[kWalkPer];
         ParMap acc = pm_identity();
 #pragma unroll
-        for (int j = 0; j < kCdfPer; j++) {
+        for (int j = 0; j < kWalkPer; j++) {
             acc = pm_compose(acc, pm_of(w[j], E));
             loc[j] = acc;
         }
-        ParMap x = acc;
+        ParMap all;
+        const ParMap pre = wg_exclusive_scan<kWalkThreads>(acc, s_wave, all);
+        uint64_t a[kWalkPer];
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const ParMap y = pm_shfl_up(x, off);
-            if (lane >= off) x = pm_compose(y, x);
-        }
-        if (lane == 63) s_wave[wv] = x;
-        const ParMap lanes_before = pm_shfl_up(x, 1);
-        __syncthreads();
-        ParMap pre = pm_identity();
-        for (int k = 0; k < wv; k++) pre = pm_compose(pre, s_wave[k]);
-        if (lane > 0) pre = pm_compose(pre, lanes_before);
-        uint64_t a[kCdfPer];
-#pragma unroll
-        for (int j = 0; j < kCdfPer; j++) {
+        for (int j = 0; j < kWalkPer; j++) {
             const ParMap T = pm_compose(pre, loc[j]);
             a[j] = a0 + (p0 ? T.d1 : T.d0);
         }
+        int64_t first = kNone;
 #pragma unroll
-        for (int j = 0; j < kCdfPer; j++)
-            if (base + j < chunk_end && a[j] >= kTwo53) {
-                atomicMin(&s_cross, static_cast<unsigned long long>(base + j));
-                break;
-            }
+        for (int j = kWalkPer - 1; j >= 0; j--)
+            if (base + j < end && a[j] >= kTwo53) first = base + j;
+        if (first != kNone) atomicMin(s_cross, static_cast<unsigned long long>(first));
         __syncthreads();
-        const int64_t c = static_cast<int64_t>(s_cross);
+        const int64_t c = static_cast<int64_t>(*s_cross);
+        const int64_t stop = start + kWalkThreads * kWalkPer < end ? start + kWalkThreads * kWalkPer : end;
 #pragma unroll
-        for (int j = 0; j < kCdfPer; j++) {
+        for (int j = 0; j < kWalkPer; j++) {
             const int64_t i = base + j;
-            if (i < chunk_end && i < c) cdf[i] = static_cast<double>(a[j]) * u;
+            if (i < stop && i < c) cdf[i] = static_cast<double>(a[j]) * u;
             if (i == c) {
                 // the element that leaves the binade: a plain f64 add on the exact previous sum
                 const uint64_t a_prev = j > 0 ? a[j > 0 ? j - 1 : 0] : a0 + (p0 ? pre.d1 : pre.d0);
                 const double sc = static_cast<double>(a_prev) * u + static_cast<double>(w[j]);
                 cdf[i] = sc;
-                s_next = sc;
+                *s_next = sc;
             }
         }
         if (c == kNone) {
-            ParMap all = pm_identity();
-            for (int k = 0; k < kCdfThreads / 64; k++) all = pm_compose(all, s_wave[k]);
             s = static_cast<double>(a0 + (p0 ? all.d1 : all.d0)) * u;
-            start = chunk_end;
+            start = stop;
         } else {
             __syncthreads();
-            s = s_next;
+            s = *s_next;
             start = c + 1;
         }
+    }
+    __syncthreads();
+    return s;
+}
+
+// One element of the segmented scan over a tile of chunk maps: segments are runs of chunks that
+// share a predicted binade; `head` is the index of the segment's first chunk.
+struct SegMap {
+    ParMap m;
+    uint32_t flag;  // a segment starts at this element (or within the combined range)
+    int head;
+};
+
+__device__ __forceinline__ SegMap seg_combine(const SegMap& A, const SegMap& B) {  // A earlier
+    const ParMap c = pm_compose(A.m, B.m);
+    const bool b = B.flag != 0u;  // selects, not a branch: keeps the struct in registers
+    SegMap r;
+    r.m.d0 = b ? B.m.d0 : c.d0;
+    r.m.d1 = b ? B.m.d1 : c.d1;
+    r.m.o = b ? B.m.o : c.o;
+    r.flag = A.flag | B.flag;
+    r.head = b ? B.head : A.head;
+    return r;
+}
+
+__device__ __forceinline__ SegMap seg_shfl_up(const SegMap& v, int delta) {
+    SegMap r;
+    r.m = pm_shfl_up(v.m, delta);
+    r.flag = __shfl_up(v.flag, delta, 64);
+    r.head = __shfl_up(v.head, delta, 64);
+    return r;
+}
+
+// D: the ordered walk over the chunks with the exact running sum. Per tile of kWalkTile chunks, a
+// segmented scan composes the maps of each run of chunks predicted in one binade; the walk then
+// advances a whole run in O(1) when the exact sum at its head lies in that binade and the run's
+// total keeps a < 2^53 (so every chunk of it does), writing the runs' chunk start values in
+// parallel. Otherwise it goes chunk by chunk, summing element-exactly where a chunk's own map
+// cannot be applied.
+__global__ void __launch_bounds__(kWalkThreads) k_cdf_walk(const float* __restrict__ w_all,
+                                                           const int32_t* __restrict__ gather, int64_t n,
+                                                           int n_chunks, const int32_t* __restrict__ chunk_E,
+                                                           const uint64_t* __restrict__ map_d0,
+                                                           const uint64_t* __restrict__ map_d1,
+                                                           const uint32_t* __restrict__ map_o,
+                                                           double* __restrict__ chunk_start,
+                                                           uint32_t* __restrict__ walked, double* __restrict__ cdf,
+                                                           double* __restrict__ total) {
+    static_assert(kWalkTile == kWalkThreads, "one chunk record per thread");
+    __shared__ int32_t sE[kWalkTile];
+    __shared__ uint64_t sd0[kWalkTile], sd1[kWalkTile];  // each chunk's own map (parity-indexed increments)
+    __shared__ uint64_t pd0[kWalkTile], pd1[kWalkTile];  // inclusive prefix from the segment head
+    __shared__ uint8_t s_head[kWalkTile];
+    __shared__ int32_t s_seg_end[kWalkTile];             // at a head: one past the segment's last chunk
+    __shared__ SegMap s_segw[kWalkThreads / 64];
+    __shared__ ParMap s_wave[kWalkThreads / 64];
+    __shared__ unsigned long long s_cross;
+    __shared__ double s_next;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    double s = 0.0;  // uniform
+    for (int tile = 0; tile < n_chunks; tile += kWalkTile) {
         __syncthreads();
+        const int cnt = n_chunks - tile < kWalkTile ? n_chunks - tile : kWalkTile;
+        int E = kUncertain;
+        ParMap m = pm_identity();
+        if (t < cnt) {
+            E = chunk_E[tile + t];
+            if (E != kUncertain) m = ParMap{map_d0[tile + t], map_d1[tile + t], map_o[tile + t]};
+        }
+        sE[t] = E;
+        sd0[t] = m.d0;
+        sd1[t] = m.d1;
+        __syncthreads();
+        const uint32_t head = (t == 0 || t >= cnt || E == kUncertain || sE[t - 1] == kUncertain || sE[t - 1] != E)
+                                  ? 1u : 0u;
+        s_head[t] = static_cast<uint8_t>(head);
+        SegMap x{m, head, head ? t : -1};
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const SegMap y = seg_shfl_up(x, off);
+            if (lane >= off) x = seg_combine(y, x);
+        }
+        if (lane == 63) s_segw[wv] = x;
+        __syncthreads();
+        SegMap pre{pm_identity(), 0u, -1};
+#pragma unroll
+        for (int k = 0; k < kWalkThreads / 64; k++)
+            if (k < wv) pre = seg_combine(pre, s_segw[k]);
+        const SegMap incl = seg_combine(pre, x);
+        pd0[t] = incl.m.d0;
+        pd1[t] = incl.m.d1;
+        const bool last_of_segment = (t == cnt - 1) || (t + 1 < cnt && s_head[t + 1]);
+        if (t < cnt && last_of_segment) s_seg_end[incl.head] = t + 1;
+        __syncthreads();
+        int k = 0;
+        while (k < cnt) {  // uniform
+            const int c = tile + k;
+            const int Ek = sE[k];
+            if (Ek != kUncertain && s > 0.0 && exponent_of(s) == Ek) {
+                const uint64_t a0 = units_of(s);
+                const bool p1 = (a0 & 1u) != 0;
+                const double u = ulp_of_binade(Ek);
+                if (s_head[k]) {
+                    const int j_end = s_seg_end[k];
+                    const uint64_t a_end = a0 + (p1 ? pd1[j_end - 1] : pd0[j_end - 1]);
+                    if (a_end < kTwo53) {
+                        for (int j = k + t; j < j_end; j += kWalkThreads) {
+                            const uint64_t aj = j == k ? a0 : a0 + (p1 ? pd1[j - 1] : pd0[j - 1]);
+                            chunk_start[tile + j] = static_cast<double>(aj) * u;
+                            walked[tile + j] = 0u;
+                        }
+                        s = static_cast<double>(a_end) * u;
+                        k = j_end;
+                        continue;
+                    }
+                }
+                const uint64_t a = a0 + (p1 ? sd1[k] : sd0[k]);
+                if (a < kTwo53) {
+                    if (t == 0) {
+                        chunk_start[c] = s;
+                        walked[c] = 0u;
+                    }
+                    s = static_cast<double>(a) * u;
+                    k++;
+                    continue;
+                }
+            }
+            if (t == 0) {
+                chunk_start[c] = s;
+                walked[c] = 1u;
+            }
+            const int64_t b = static_cast<int64_t>(c) * kCdfChunk;
+            const int64_t e = b + kCdfChunk < n ? b + kCdfChunk : n;
+            s = cdf_range_exact(w_all, gather, b, e, s, cdf, s_wave, &s_cross, &s_next);
+            k++;
+        }
     }
     if (t == 0) *total = s;
-    if (bad) atomicOr(err, kMcErrWeights);
+}
+
+// E: the cdf of every chunk the walk advanced in O(1)
+__global__ void __launch_bounds__(kCdfBlock) k_cdf_write(const float* __restrict__ w_all,
+                                                         const int32_t* __restrict__ gather, int64_t n,
+                                                         const int32_t* __restrict__ chunk_E,
+                                                         const double* __restrict__ chunk_start,
+                                                         const uint32_t* __restrict__ walked,
+                                                         double* __restrict__ cdf) {
+    __shared__ ParMap s_wave[kCdfBlock / 64];
+    if (walked[blockIdx.x]) return;  // uniform
+    const int E = chunk_E[blockIdx.x];
+    const double s = chunk_start[blockIdx.x];
+    const uint64_t a0 = units_of(s);
+    const uint32_t p0 = static_cast<uint32_t>(a0 & 1u);
+    const double u = ulp_of_binade(E);
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kCdfChunk + static_cast<int64_t>(threadIdx.x) * kCdfPerT;
+    ParMap loc[kCdfPerT];
+    ParMap acc = pm_identity();
+#pragma unroll
+    for (int j = 0; j < kCdfPerT; j++) {
+        const int64_t i = base + j;
+        if (i < n) acc = pm_compose(acc, pm_of(load_w(w_all, gather, i), E));
+        loc[j] = acc;
+    }
+    ParMap all;
+    const ParMap pre = wg_exclusive_scan<kCdfBlock>(acc, s_wave, all);
+#pragma unroll
+    for (int j = 0; j < kCdfPerT; j++) {
+        const int64_t i = base + j;
+        if (i < n) {
+            const ParMap T = pm_compose(pre, loc[j]);
+            cdf[i] = static_cast<double>(a0 + (p0 ? T.d1 : T.d0)) * u;
+        }
+    }
 }
 
 // ---- std::mt19937_64 ----------------------------------------------------------------------------
@@ -499,9 +779,32 @@ void mc_compact(const int32_t* dead, const int64_t* cum, int n, int32_t* dead_li
     hipLaunchKernelGGL(k_mc_compact, dim3(grid_for(n)), dim3(kBlock), 0, s, dead, cum, n, dead_list, alive_list);
 }
 
+size_t mc_cdf_scratch_bytes(int64_t n) {
+    const size_t nc = static_cast<size_t>((n + kCdfChunk - 1) / kCdfChunk);
+    return nc * (8 + 4 + 8 + 8 + 4 + 8 + 4) + 256;
+}
+
 void mc_cdf(const float* w, const int32_t* gather, int64_t n, double* cdf, double* total, uint32_t* err,
-            hipStream_t s) {
-    hipLaunchKernelGGL(k_mc_cdf, dim3(1), dim3(kCdfThreads), 0, s, w, gather, n, cdf, total, err);
+            void* scratch, hipStream_t s) {
+    const int nc = static_cast<int>((n + kCdfChunk - 1) / kCdfChunk);
+    // scratch layout: 8-byte arrays first, then the 4-byte ones
+    double* chunk_sum = static_cast<double*>(scratch);
+    double* chunk_start = chunk_sum + nc;
+    uint64_t* d0 = reinterpret_cast<uint64_t*>(chunk_start + nc);
+    uint64_t* d1 = d0 + nc;
+    int32_t* chunk_E = reinterpret_cast<int32_t*>(d1 + nc);
+    uint32_t* o = reinterpret_cast<uint32_t*>(chunk_E + nc);
+    uint32_t* walked = o + nc;
+    if (nc > 0) {
+        hipLaunchKernelGGL(k_cdf_chunk_sum, dim3(nc), dim3(kCdfBlock), 0, s, w, gather, n, chunk_sum, err);
+        hipLaunchKernelGGL(k_cdf_predict, dim3(1), dim3(kWalkThreads), 0, s, chunk_sum, nc, chunk_E);
+        hipLaunchKernelGGL(k_cdf_chunk_map, dim3(nc), dim3(kCdfBlock), 0, s, w, gather, n, chunk_E, d0, d1, o);
+    }
+    hipLaunchKernelGGL(k_cdf_walk, dim3(1), dim3(kWalkThreads), 0, s, w, gather, n, nc, chunk_E, d0, d1, o,
+                       chunk_start, walked, cdf, total);
+    if (nc > 0)
+        hipLaunchKernelGGL(k_cdf_write, dim3(nc), dim3(kCdfBlock), 0, s, w, gather, n, chunk_E, chunk_start, walked,
+                           cdf);
 }
 
 void mc_mt_gen(uint64_t* state, int64_t n_out, uint64_t* raw, hipStream_t s) {

@@ -44,6 +44,7 @@ void ensure_refine_buffers(sxh_executor* e, int n_max) {
         e->mc_counts.alloc(R);
         e->mc_cdf.alloc(R);
         e->mc_raw.alloc(R);
+        e->mc_cdf_scratch.alloc(sxk::mc_cdf_scratch_bytes(static_cast<int64_t>(R)));
     }
     if (!e->mc_err.p) e->mc_err.alloc(1);
     if (!e->mc_total.p) e->mc_total.alloc(1);
@@ -92,7 +93,7 @@ void draw_and_relocate(Ctx& c, const sxh_refine_inputs* in, const int32_t* gathe
     sxh_executor* e = c.e;
     hipStream_t s = c.s;
     c.clear_err();
-    sxk::mc_cdf(e->mc_op_act.p, gather, n_w, e->mc_cdf.p, e->mc_total.p, e->mc_err.p, s);
+    sxk::mc_cdf(e->mc_op_act.p, gather, n_w, e->mc_cdf.p, e->mc_total.p, e->mc_err.p, e->mc_cdf_scratch.p, s);
     c.read_err_and_total(true);
     if (c.hb->err & sxk::kMcErrWeights) invalid("multinomial", "weights must be >= 0 and finite");
     if (!(c.hb->total > 0.0)) invalid("multinomial", "weight sum must be > 0");
@@ -138,8 +139,9 @@ int32_t sxh_running_sum_f64(sxh_backend* b, const float* w, int64_t n, double* o
         auto dw = upload(w, static_cast<size_t>(n), b->stream);
         DevBuf<double> cdf(static_cast<size_t>(n)), total(1);
         DevBuf<uint32_t> err(1);
+        DevBuf<uint8_t> scratch(sxk::mc_cdf_scratch_bytes(n));
         sxk::fill_u32(err.p, 0u, 1, b->stream);
-        sxk::mc_cdf(dw.p, nullptr, n, cdf.p, total.p, err.p, b->stream);
+        sxk::mc_cdf(dw.p, nullptr, n, cdf.p, total.p, err.p, scratch.p, b->stream);
         SXH_HIP(hipGetLastError());
         uint32_t herr = 0;
         SXH_HIP(hipMemcpyAsync(&herr, err.p, 4, hipMemcpyDeviceToHost, b->stream));

@@ -67,6 +67,7 @@ struct sxh_executor {
     sxh::DevBuf<uint32_t> mc_counts, mc_err;
     sxh::DevBuf<double> mc_cdf, mc_total;
     sxh::DevBuf<uint64_t> mc_raw, mc_mt;
+    sxh::DevBuf<uint8_t> mc_cdf_scratch;
     // profiling
     bool prof = false;
     hipEvent_t ev[kMaxEvents] = {};

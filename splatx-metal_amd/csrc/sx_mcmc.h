@@ -21,9 +21,11 @@ void mc_activate(const float* logits, int n, float min_opacity, float* op_act, i
 // stable dead / alive lists from cum = inclusive int64 scan of dead
 void mc_compact(const int32_t* dead, const int64_t* cum, int n, int32_t* dead_list, int32_t* alive_list,
                 hipStream_t s);
-// cdf[i] = the left-to-right f64 running sum of w[gather[i]] (w[i] when gather is null); total = cdf[n-1]
+// cdf[i] = the left-to-right f64 running sum of w[gather[i]] (w[i] when gather is null); total = the
+// sum (0 when n == 0); scratch: mc_cdf_scratch_bytes(n) bytes, 8-byte aligned
+size_t mc_cdf_scratch_bytes(int64_t n);
 void mc_cdf(const float* w, const int32_t* gather, int64_t n, double* cdf, double* total, uint32_t* err,
-            hipStream_t s);
+            void* scratch, hipStream_t s);
 // state: 312 words + the position word; raw = the next n_out untempered words
 void mc_mt_gen(uint64_t* state, int64_t n_out, uint64_t* raw, hipStream_t s);
 // multinomial draws over cdf[0, n_w): sampled[j] = gather[idx] (idx when gather is null), counts[src]++
