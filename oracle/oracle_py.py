@@ -52,6 +52,17 @@ class RefCase(C.Structure):
                 ("capacity", C.c_int64), ("rng_out", C.POINTER(sh.MtState))]
 
 
+class HipTrainCase(C.Structure):
+    _fields_ = [("params", sh.fp * 6), ("count", C.c_int64), ("sh_degree", C.c_int32), ("viewmat", sh.fp),
+                ("K", sh.fp), ("width", C.c_int32), ("height", C.c_int32), ("gt_rgb", sh.fp), ("steps", C.c_int32),
+                ("total_iters", C.c_int32), ("lr", C.c_float * 6), ("ssim_weight", C.c_float),
+                ("opacity_reg", C.c_float), ("scale_reg", C.c_float), ("antialiased", C.c_uint8),
+                ("resident", C.c_uint8), ("mcmc", C.c_uint8), ("cap_max", C.c_int64), ("seed", C.c_uint64),
+                ("refine_start_ratio", C.c_float), ("refine_stop_ratio", C.c_float),
+                ("refine_every_ratio", C.c_float), ("out_params", sh.fp * 6), ("losses", sh.fp),
+                ("n_isects", sh.i64p), ("render0", sh.fp), ("out_count", C.c_int64), ("n_refined", C.c_int32)]
+
+
 def _ptr_or_null(a):
     return sh.ptr(a) if a is not None and a.size else None
 
@@ -232,3 +243,54 @@ class Reference(sh.Ops):
     @staticmethod
     def available() -> bool:
         return os.path.exists(Reference.PATH)
+
+
+class ReferenceTrainerOnHip:
+    """The reference's Trainer (Trainer.cpp, unchanged) on this repository's backend through the C++
+    KernelBackend adapter: oracle/_ref/libsx_ref_hip.so. Needs a GPU at run time."""
+
+    PATH = os.path.join(HERE, "_ref", "libsx_ref_hip.so")
+
+    def __init__(self):
+        if not os.path.exists(self.PATH):
+            raise RuntimeError("oracle/_ref/libsx_ref_hip.so not built (reference tree absent)")
+        self.lib = C.CDLL(self.PATH)
+        self.lib.sxr_hip_trainer_run.restype = C.c_int32
+        self.lib.sxr_hip_last_error.restype = C.c_char_p
+
+    @staticmethod
+    def available() -> bool:
+        return os.path.exists(ReferenceTrainerOnHip.PATH)
+
+    def run(self, params, count, sh_degree, viewmat, K, width, height, gt, steps, lr, total_iters=100,
+            ssim_weight=0.2, opacity_reg=0.0, scale_reg=0.0, antialiased=False, resident=True, mcmc=False,
+            cap_max=0, seed=42, refine_start_ratio=0.0, refine_stop_ratio=1.0, refine_every_ratio=0.02):
+        c = HipTrainCase()
+        keep = [sh.f32(x).reshape(count, -1) for x in params]
+        for g in range(6):
+            c.params[g] = _ptr_or_null(keep[g])
+        rows = cap_max if mcmc else count
+        dims = sh.GROUP_DIMS(sh_degree)
+        outs = [np.zeros((rows, d), np.float32) for d in dims]
+        for g in range(6):
+            c.out_params[g] = _ptr_or_null(outs[g])
+        vm, KK, gg = sh.f32(viewmat), sh.f32(K), sh.f32(gt)
+        c.count, c.sh_degree, c.viewmat, c.K, c.width, c.height = count, sh_degree, sh.ptr(vm), sh.ptr(KK), width, height
+        c.gt_rgb, c.steps, c.total_iters = sh.ptr(gg), steps, total_iters
+        for g in range(6):
+            c.lr[g] = lr[g]
+        c.ssim_weight, c.opacity_reg, c.scale_reg = ssim_weight, opacity_reg, scale_reg
+        c.antialiased, c.resident, c.mcmc = int(bool(antialiased)), int(bool(resident)), int(bool(mcmc))
+        c.cap_max, c.seed = cap_max, seed
+        c.refine_start_ratio, c.refine_stop_ratio, c.refine_every_ratio = (refine_start_ratio, refine_stop_ratio,
+                                                                           refine_every_ratio)
+        losses = np.zeros(steps, np.float32)
+        n_isects = np.zeros(steps, np.int64)
+        render0 = np.zeros((height, width, 3), np.float32)
+        c.losses, c.n_isects, c.render0 = sh.ptr(losses), sh.ptr(n_isects), sh.ptr(render0)
+        rc = self.lib.sxr_hip_trainer_run(C.byref(c))
+        if rc != sh.SXH_OK:
+            msg = self.lib.sxr_hip_last_error().decode(errors="replace")
+            raise (sh.SxInvalidArgument if rc == sh.SXH_ERR_INVALID_ARGUMENT else sh.SxRuntimeError)(msg)
+        return dict(params=outs, losses=losses, n_isects=n_isects, render0=render0, count=int(c.out_count),
+                    n_refined=int(c.n_refined))

@@ -1,0 +1,116 @@
+// ref_trainer_hip.cpp — the reference's own Trainer driving this repository's backend (TEST
+// INFRASTRUCTURE ONLY).
+//
+// Compiled by oracle/Makefile (target `ref`) with Sources/SplatXCore/{Trainer,CpuKernels,Math}.cpp
+// taken in place from the reference tree and splatx-metal_amd/host/hip_kernel_backend.cpp (the
+// C++ KernelBackend adapter over the C ABI), linked against splatx-metal_amd/build/libsplatx_hip.so,
+// into oracle/_ref/libsx_ref_hip.so. The Trainer code is the reference's, unchanged: it is the
+// caller a maintainer would point at make_hip_backend, so a run here exercises the drop-in
+// boundary end to end — the host path through the per-op virtuals, the resident path through
+// make_train_step_executor, the MCMC refine through the executor's download/upload.
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "hip_kernel_backend.h"
+#include "splatx/KernelBackend.h"
+#include "splatx/Trainer.h"
+#include "splatx_hip.h"
+
+namespace {
+thread_local std::string g_err;
+}
+
+extern "C" {
+
+typedef struct {
+    const float* params[6];  /* [count, dim] */
+    int64_t count;
+    int32_t sh_degree;
+    const float* viewmat;    /* [16] */
+    const float* K;          /* [9] */
+    int32_t width, height;
+    const float* gt_rgb;     /* [H,W,3] */
+    int32_t steps, total_iters;
+    float lr[6];             /* means, quats, scales, opacities, sh0, shN */
+    float ssim_weight, opacity_reg, scale_reg;
+    uint8_t antialiased, resident, mcmc;
+    int64_t cap_max;
+    uint64_t seed;
+    float refine_start_ratio, refine_stop_ratio, refine_every_ratio;
+    /* outputs */
+    float* out_params[6];    /* [rows, dim] with rows = cap_max when mcmc else count */
+    float* losses;           /* [steps] */
+    int64_t* n_isects;       /* [steps] */
+    float* render0;          /* [H,W,3]: the first step's render */
+    int64_t out_count;
+    int32_t n_refined;
+} sxr_hip_train_case;
+
+const char* sxr_hip_last_error(void) { return g_err.c_str(); }
+
+int32_t sxr_hip_trainer_run(sxr_hip_train_case* c) {
+    try {
+        auto backend = splatx::make_hip_backend({});
+        splatx::SplatCloud cloud;
+        cloud.count = c->count;
+        cloud.sh_degree = c->sh_degree;
+        std::vector<float>* vs[6] = {&cloud.means, &cloud.quats, &cloud.scales,
+                                     &cloud.opacities, &cloud.sh0, &cloud.shN};
+        const int64_t dims[6] = {3, 4, 3, 1, 3, static_cast<int64_t>(cloud.sh_rest_coeffs()) * 3};
+        for (int g = 0; g < 6; g++) vs[g]->assign(c->params[g], c->params[g] + c->count * dims[g]);
+        splatx::TrainConfig cfg;
+        cfg.total_iters = c->total_iters;
+        cfg.lr_means = c->lr[0];
+        cfg.lr_quats = c->lr[1];
+        cfg.lr_scales = c->lr[2];
+        cfg.lr_opacities = c->lr[3];
+        cfg.lr_sh0 = c->lr[4];
+        cfg.lr_shN = c->lr[5];
+        cfg.ssim_weight = c->ssim_weight;
+        cfg.opacity_reg = c->opacity_reg;
+        cfg.scale_reg = c->scale_reg;
+        cfg.antialiased = c->antialiased != 0;
+        cfg.resident = c->resident != 0;
+        if (c->mcmc) {
+            cfg.mcmc.enabled = true;
+            cfg.mcmc.cap_max = c->cap_max;
+            cfg.mcmc.seed = c->seed;
+            cfg.mcmc.refine_start_ratio = c->refine_start_ratio;
+            cfg.mcmc.refine_stop_ratio = c->refine_stop_ratio;
+            cfg.mcmc.refine_every_ratio = c->refine_every_ratio;
+        }
+        splatx::Trainer tr(*backend, std::move(cloud), cfg);
+        splatx::TrainingCamera cam;
+        std::memcpy(cam.viewmat, c->viewmat, sizeof(cam.viewmat));
+        std::memcpy(cam.K, c->K, sizeof(cam.K));
+        cam.width = c->width;
+        cam.height = c->height;
+        c->n_refined = 0;
+        for (int it = 0; it < c->steps; it++) {
+            const splatx::TrainStepResult r = tr.step(cam, c->gt_rgb, it);
+            c->losses[it] = r.loss;
+            c->n_isects[it] = r.n_isects;
+            if (r.mcmc_refined) c->n_refined++;
+            if (it == 0 && c->render0 && !r.render_colors.empty())
+                std::memcpy(c->render0, r.render_colors.data(), r.render_colors.size() * sizeof(float));
+        }
+        const splatx::SplatCloud& out = tr.cloud();
+        c->out_count = out.count;
+        const std::vector<float>* os[6] = {&out.means, &out.quats, &out.scales, &out.opacities, &out.sh0, &out.shN};
+        for (int g = 0; g < 6; g++)
+            if (c->out_params[g] && !os[g]->empty())
+                std::memcpy(c->out_params[g], os[g]->data(), os[g]->size() * sizeof(float));
+        return SXH_OK;
+    } catch (const std::invalid_argument& e) {
+        g_err = e.what();
+        return SXH_ERR_INVALID_ARGUMENT;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return SXH_ERR_RUNTIME;
+    }
+}
+
+} // extern "C"

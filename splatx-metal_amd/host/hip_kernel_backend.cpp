@@ -5,6 +5,9 @@
 // everything else, MetalBackend.cpp:52-54).
 #include "hip_kernel_backend.h"
 
+#include <cmath>
+#include <locale>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 
@@ -133,6 +136,8 @@ public:
         out.n_isects = o.n_isects;
         return out;
     }
+
+    sxh_executor* handle() const { return e_; }
 
 private:
     static sxh_param_sync to_c(const ResidentParamSync& s) {
@@ -386,6 +391,83 @@ private:
 };
 
 } // namespace
+
+namespace {
+
+// The engine's state through its text form (the C++ standard's stream operators): libstdc++ writes
+// its 312 words and the position (313 numbers), libc++ the 312 most recent words (then p = 312).
+sxh_mt64_state mt_state_of(const std::mt19937_64& g) {
+    std::ostringstream os;
+    os.imbue(std::locale::classic());
+    os << g;
+    std::istringstream is(os.str());
+    is.imbue(std::locale::classic());
+    std::vector<uint64_t> v;
+    uint64_t x;
+    while (is >> x) v.push_back(x);
+    if (v.size() != 312 && v.size() != 313) throw std::runtime_error("hip_mcmc_refine: unknown mt19937_64 text layout");
+    sxh_mt64_state st{};
+    for (int i = 0; i < 312; i++) st.x[i] = v[static_cast<size_t>(i)];
+    st.p = v.size() == 313 ? static_cast<uint32_t>(v[312]) : 312u;
+    return st;
+}
+
+void mt_state_to(const sxh_mt64_state& st, std::mt19937_64& g) {
+    std::ostringstream probe;
+    probe.imbue(std::locale::classic());
+    probe << g;
+    std::istringstream count_is(probe.str());
+    size_t n = 0;
+    for (uint64_t x; count_is >> x;) n++;
+    std::ostringstream os;
+    os.imbue(std::locale::classic());
+    for (int i = 0; i < 312; i++) os << st.x[i] << (i + 1 < 312 ? " " : "");
+    if (n == 313) os << ' ' << st.p;
+    else if (st.p != 312)  // this library's text form holds no position
+        throw std::runtime_error("hip_mcmc_refine: engine position not expressible in this C++ library's text form");
+    std::istringstream is(os.str());
+    is.imbue(std::locale::classic());
+    is >> g;
+    if (!is) throw std::runtime_error("hip_mcmc_refine: engine state rejected");
+}
+
+} // namespace
+
+HipMcmcRefineResult hip_mcmc_refine(TrainStepExecutor& exec, std::mt19937_64& rng, const HipMcmcRefineInputs& in) {
+    auto* hx = dynamic_cast<HipTrainStepExecutor*>(&exec);
+    if (!hx) throw std::invalid_argument("hip_mcmc_refine: executor was not made by make_hip_backend");
+    if (!in.binoms) throw std::invalid_argument("hip_mcmc_refine: null binoms");
+    sxh_mt64_state st = mt_state_of(rng);
+    sxh_refine_inputs c{};
+    c.count = in.count;
+    c.cap_max = in.cap_max;
+    c.min_opacity = in.min_opacity;
+    c.n_max = static_cast<int32_t>(std::lround(std::sqrt(static_cast<double>(in.binoms->size()))));
+    c.binoms = in.binoms->data();
+    c.rng = &st;
+    c.inject_noise = in.inject_noise ? 1 : 0;
+    c.noise_seed = in.noise_seed;
+    c.noise_offset = in.noise_offset;
+    c.noise_scale = in.noise_scale;
+    HipMcmcRefineResult r;
+    const size_t cap = sz(in.cap_max);
+    r.relocated_dead.resize(cap);
+    r.relocation_src.resize(cap);
+    r.added_src.resize(cap);
+    sxh_refine_outputs o{};
+    o.relocated_dead = data_or_null(r.relocated_dead);
+    o.relocation_src = data_or_null(r.relocation_src);
+    o.added_src = data_or_null(r.added_src);
+    o.capacity = in.cap_max;
+    const int32_t rc = sxh_exec_mcmc_refine(hx->handle(), &c, &o);
+    mt_state_to(st, rng);  // the engine advanced by the draws made, also when a phase failed
+    check(rc);
+    r.count = o.count;
+    r.relocated_dead.resize(sz(o.n_relocated));
+    r.relocation_src.resize(sz(o.n_relocated));
+    r.added_src.resize(sz(o.n_added));
+    return r;
+}
 
 std::unique_ptr<KernelBackend> make_hip_backend(const HipBackendDesc& desc) {
     return std::make_unique<HipKernelBackend>(desc.device_ordinal);

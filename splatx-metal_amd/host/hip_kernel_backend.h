@@ -6,7 +6,10 @@
 // TrainC.cpp:552 and the tests' shared backend; Trainer (Trainer.cpp:668) takes the result unchanged.
 #pragma once
 
+#include <cstdint>
 #include <memory>
+#include <random>
+#include <vector>
 
 #include "splatx/KernelBackend.h"
 
@@ -19,5 +22,25 @@ struct HipBackendDesc {
 // Creates the HIP backend on one GPU. Failure (no device, library/ABI mismatch) raises
 // std::runtime_error, as make_metal_backend does (MetalBackend.h:43-46).
 std::unique_ptr<KernelBackend> make_hip_backend(const HipBackendDesc& desc = {});
+
+// MCMC refine on the device arena of a resident executor made by make_hip_backend: what
+// Trainer::step_resident does on a refine step (Trainer.cpp:957-967: mcmc_refine, then
+// mcmc_inject_noise over the new count) without sync_host_for_mutation's download and the next
+// step's re-upload (Trainer.cpp:911-914). `rng` is the Trainer's multinomial engine (mcmc_rng_);
+// it is advanced by exactly the draws the host path makes. Errors as Trainer::mcmc_refine.
+struct HipMcmcRefineInputs {
+    int64_t count = 0;                        // cloud_.count
+    int64_t cap_max = 0;                      // McmcOptions::cap_max
+    float min_opacity = 0.005f;               // McmcOptions::min_opacity
+    const std::vector<float>* binoms = nullptr;  // Trainer::binoms_ (make_binoms_lut(51))
+    bool inject_noise = false;                // the post-refine noise (Trainer.cpp:966)
+    uint64_t noise_seed = 0, noise_offset = 0;
+    float noise_scale = 0.f;
+};
+struct HipMcmcRefineResult {
+    int64_t count = 0;  // the new cloud_.count
+    std::vector<int64_t> relocated_dead, relocation_src, added_src;  // Trainer::McmcRefineResult
+};
+HipMcmcRefineResult hip_mcmc_refine(TrainStepExecutor& exec, std::mt19937_64& rng, const HipMcmcRefineInputs& in);
 
 } // namespace splatx
