@@ -63,6 +63,13 @@ class HipTrainCase(C.Structure):
                 ("n_isects", sh.i64p), ("render0", sh.fp), ("out_count", C.c_int64), ("n_refined", C.c_int32)]
 
 
+class HipRefineCase(C.Structure):
+    _fields_ = [("params", sh.fp * 6), ("exp_avg", sh.fp * 6), ("exp_avg_sq", sh.fp * 6), ("count", C.c_int64),
+                ("cap_max", C.c_int64), ("sh_degree", C.c_int32), ("n_refine", C.c_int32), ("seed", C.c_uint64),
+                ("binoms", sh.fp), ("counts", sh.i64p), ("last_lists", sh.i64p), ("last_sizes", C.c_int64 * 3),
+                ("rng_out", C.POINTER(sh.MtState))]
+
+
 def _ptr_or_null(a):
     return sh.ptr(a) if a is not None and a.size else None
 
@@ -261,6 +268,28 @@ class ReferenceTrainerOnHip:
     @staticmethod
     def available() -> bool:
         return os.path.exists(ReferenceTrainerOnHip.PATH)
+
+    def adapter_refine(self, params, exp_avg, exp_avg_sq, count, cap_max, sh_degree, seed, n_refine, binoms):
+        """hip_mcmc_refine through the C++ adapter; arrays ([cap_max, dim]) are updated in place."""
+        c = HipRefineCase()
+        for g in range(6):
+            c.params[g] = _ptr_or_null(params[g])
+            c.exp_avg[g] = _ptr_or_null(exp_avg[g])
+            c.exp_avg_sq[g] = _ptr_or_null(exp_avg_sq[g])
+        keep = sh.f32(binoms)
+        c.count, c.cap_max, c.sh_degree, c.n_refine, c.seed, c.binoms = (count, cap_max, sh_degree, n_refine, seed,
+                                                                        sh.ptr(keep))
+        counts = np.zeros(n_refine, np.int64)
+        lists = np.zeros((3, cap_max), np.int64)
+        st = sh.MtState()
+        c.counts, c.last_lists, c.rng_out = sh.ptr(counts), sh.ptr(lists), C.pointer(st)
+        self.lib.sxr_hip_adapter_refine.restype = C.c_int32
+        rc = self.lib.sxr_hip_adapter_refine(C.byref(c))
+        if rc != sh.SXH_OK:
+            raise sh.SxRuntimeError(self.lib.sxr_hip_last_error().decode(errors="replace"))
+        sizes = list(c.last_sizes)
+        return dict(counts=counts, relocated_dead=lists[0][:sizes[0]], relocation_src=lists[1][:sizes[1]],
+                    added_src=lists[2][:sizes[2]], rng=st)
 
     def run(self, params, count, sh_degree, viewmat, K, width, height, gt, steps, lr, total_iters=100,
             ssim_weight=0.2, opacity_reg=0.0, scale_reg=0.0, antialiased=False, resident=True, mcmc=False,

@@ -10,6 +10,8 @@
 // make_train_step_executor, the MCMC refine through the executor's download/upload.
 #include <cstring>
 #include <memory>
+#include <random>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -103,6 +105,71 @@ int32_t sxr_hip_trainer_run(sxr_hip_train_case* c) {
         for (int g = 0; g < 6; g++)
             if (c->out_params[g] && !os[g]->empty())
                 std::memcpy(c->out_params[g], os[g]->data(), os[g]->size() * sizeof(float));
+        return SXH_OK;
+    } catch (const std::invalid_argument& e) {
+        g_err = e.what();
+        return SXH_ERR_INVALID_ARGUMENT;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return SXH_ERR_RUNTIME;
+    }
+}
+
+/* hip_mcmc_refine (the adapter's device refine) on an executor made through the adapter: params
+ * and moments ([rows, dim], rows = cap_max) are uploaded, n_refine refines run from
+ * std::mt19937_64(seed), everything is downloaded back in place; rng_out = the engine after. */
+typedef struct {
+    float* params[6];
+    float* exp_avg[6];
+    float* exp_avg_sq[6];
+    int64_t count, cap_max;
+    int32_t sh_degree, n_refine;
+    uint64_t seed;
+    const float* binoms;     /* [51*51] */
+    int64_t* counts;         /* [n_refine] */
+    int64_t* last_lists;     /* [3, cap_max]: relocated_dead, relocation_src, added_src of the last refine */
+    int64_t last_sizes[3];
+    sxh_mt64_state* rng_out;
+} sxr_hip_refine_case;
+
+int32_t sxr_hip_adapter_refine(sxr_hip_refine_case* c) {
+    try {
+        auto backend = splatx::make_hip_backend({});
+        splatx::TrainStepExecutorDesc d;
+        d.arena_rows = c->cap_max;
+        d.sh_degree = c->sh_degree;
+        auto exec = backend->make_train_step_executor(d);
+        if (!exec) throw std::runtime_error("no executor");
+        splatx::ResidentParamSync sync;
+        sync.rows = c->cap_max;
+        for (int g = 0; g < 6; g++) {
+            sync.params[g] = c->params[g];
+            sync.exp_avg[g] = c->exp_avg[g];
+            sync.exp_avg_sq[g] = c->exp_avg_sq[g];
+        }
+        exec->upload_params(sync);
+        std::mt19937_64 rng(c->seed);
+        const std::vector<float> binoms(c->binoms, c->binoms + 51 * 51);
+        splatx::HipMcmcRefineInputs in;
+        in.count = c->count;
+        in.cap_max = c->cap_max;
+        in.binoms = &binoms;
+        for (int r = 0; r < c->n_refine; r++) {
+            const splatx::HipMcmcRefineResult res = splatx::hip_mcmc_refine(*exec, rng, in);
+            in.count = res.count;
+            c->counts[r] = res.count;
+            const std::vector<int64_t>* ls[3] = {&res.relocated_dead, &res.relocation_src, &res.added_src};
+            for (int k = 0; k < 3; k++) {
+                c->last_sizes[k] = static_cast<int64_t>(ls[k]->size());
+                std::memcpy(c->last_lists + k * c->cap_max, ls[k]->data(), ls[k]->size() * sizeof(int64_t));
+            }
+        }
+        exec->download_params(sync);
+        std::ostringstream os;
+        os << rng;
+        std::istringstream is(os.str());
+        for (int i = 0; i < 312; i++) is >> c->rng_out->x[i];
+        is >> c->rng_out->p;
         return SXH_OK;
     } catch (const std::invalid_argument& e) {
         g_err = e.what();

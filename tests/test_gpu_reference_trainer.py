@@ -73,3 +73,26 @@ def test_reference_trainer_mcmc_resident_on_hip(ref_hip):
     # the first steps precede any refine: the two paths agree there as in the contrast test
     assert r["n_isects"][0] == h["n_isects"][0]
     assert abs(float(h["losses"][0]) - float(r["losses"][0])) <= 1e-6 + 1e-4 * abs(float(h["losses"][0]))
+
+
+def test_adapter_hip_mcmc_refine_matches_oracle(ref_hip, oracle):
+    """splatx::hip_mcmc_refine (the C++ adapter's device refine, std::mt19937_64 exchanged through
+    its text form) over three refines equals the oracle's refine chain bit for bit."""
+    from inputs import make_cloud
+    n, cap, deg = 3000, 3400, 2
+    p, m, v = make_cloud(n, cap, deg, 21)
+    binoms = oracle.make_binoms_lut(51)
+    dp, dm, dv = [x.copy() for x in p], [x.copy() for x in m], [x.copy() for x in v]
+    got = ref_hip.adapter_refine(dp, dm, dv, n, cap, deg, seed=42, n_refine=3, binoms=binoms)
+    rng = oracle.mt64_seed(42)
+    count = n
+    for k in range(3):
+        res = oracle.mcmc_refine(p, m, v, count, cap, deg, rng, binoms)
+        count = res["count"]
+        assert got["counts"][k] == count
+    for key in ("relocated_dead", "relocation_src", "added_src"):
+        assert np.array_equal(got[key], res[key]), key
+    assert got["rng"].equals(rng)
+    for a, b in ((dp, p), (dm, m), (dv, v)):
+        for g in range(6):
+            assert np.array_equal(a[g].view(np.uint32), b[g].view(np.uint32)), g
