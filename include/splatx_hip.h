@@ -425,6 +425,80 @@ int32_t sxh_exec_mcmc_refine(sxh_executor* e, const sxh_refine_inputs* in, sxh_r
 int32_t sxh_running_sum_f64(sxh_backend* b, const float* w, int64_t n, double* out /* [n] */);
 int32_t sxh_mt64_draw(sxh_backend* b, sxh_mt64_state* st, int64_t n, uint64_t* out /* [n] */);
 
+/* ------------------------------------------------------------------------------------------ */
+/* Data formats either side of the step: the INRIA PLY export with its filter (PlyIO.h:20-51),  */
+/* SXCK checkpoints (Checkpoint.h:11-147; Trainer::make_checkpoint / restore_checkpoint,        */
+/* Trainer.cpp:1450-1570) and forward-only render sessions (splatx_train_c.h:604-682). The      */
+/* filter, the compaction and the packing of PLY rows and checkpoint tensors run on the device  */
+/* arena; only the packed bytes cross PCIe.                                                     */
+/* ------------------------------------------------------------------------------------------ */
+
+/* ExportFilterStats (PlyIO.h:43-48). */
+typedef struct {
+    int64_t input, removed_nonfinite, removed_low_opacity, kept;
+} sxh_export_stats;
+
+/* filter_cloud_for_export (PlyIO.h:49-51) + write_inria_ply (:20) of the executor's live rows
+ * [0, count): rows with a non-finite parameter and rows with sigmoid(opacity) <= min_opacity are
+ * dropped; f_rest is zero-padded to 45 coefficients when 0 < K < 15 and pad_sh_full is set. */
+int32_t sxh_exec_export_ply(sxh_executor* e, int64_t count, float min_opacity, uint8_t pad_sh_full,
+                            const char* path, sxh_export_stats* stats /* may be NULL */);
+
+/* read_inria_ply (PlyIO.h:21), host only: with params == NULL it reports count and sh_degree;
+ * then params[6] = AoS arrays of [count, dim] in group order (shN NULL when the degree is 0). */
+int32_t sxh_ply_read(const char* path, int64_t* count, int32_t* sh_degree, float* const* params);
+
+/* CheckpointConfig (Checkpoint.h:86-97). */
+typedef struct {
+    int32_t sh_degree, factor, test_split, total_iters;
+    uint8_t mcmc_enabled, antialiased;
+    int64_t cap_max;
+    uint64_t mcmc_seed;
+    float scene_scale, ssim_weight;
+} sxh_checkpoint_config;
+
+/* CheckpointHeader (Checkpoint.h:133-139). */
+typedef struct {
+    sxh_checkpoint_config config;
+    int32_t iter;
+    int64_t alive_count;
+    uint8_t fp16;
+    uint32_t version;
+} sxh_checkpoint_header;
+
+/* verify_checkpoint_config (Checkpoint.h:117): SXH_ERR_RUNTIME naming the first mismatching field. */
+int32_t sxh_checkpoint_verify_config(const sxh_checkpoint_config* saved, const sxh_checkpoint_config* current);
+/* load_checkpoint_header (Checkpoint.h:140), host only. */
+int32_t sxh_checkpoint_read_header(const char* path, sxh_checkpoint_header* out);
+/* make_checkpoint + save_checkpoint_file (Trainer.cpp:1465-1511, Checkpoint.h:121): rows [0, count)
+ * of the parameters and both moments, fp32 verbatim or fp16 (half, clamped to +-65504; exp_avg_sq
+ * stored as sqrt), written atomically (temp file, fsync, rename, directory fsync). rng_state is the
+ * multinomial engine's text form (NULL or "" without MCMC). */
+int32_t sxh_exec_save_checkpoint(sxh_executor* e, const sxh_checkpoint_config* config, int32_t iter,
+                                 int64_t count, const char* rng_state, uint8_t fp16, const char* path);
+/* load_checkpoint_file + restore_checkpoint (Checkpoint.h:122, Trainer.cpp:1513-1570): the file's
+ * fingerprint is verified against `current` (skipped when NULL), rows [0, alive_count) of the arena
+ * are restored (fp16: exp_avg_sq squared back, exp_avg zeroed where exp_avg_sq decoded to 0), rows
+ * beyond are zeroed; `out` gets the header, rng_state (capacity bytes, NUL-terminated) the engine
+ * text. A file that does not fit the arena is rejected before any device write. */
+int32_t sxh_exec_load_checkpoint(sxh_executor* e, const char* path, const sxh_checkpoint_config* current,
+                                 sxh_checkpoint_header* out, char* rng_state, int64_t rng_capacity);
+
+/* Render sessions (sx_render_session_open / _frame / _close, splatx_train_c.h:604-682): a PLY is
+ * read and uploaded once; each frame is the resident forward at the cloud's SH degree (as
+ * Trainer::render, Trainer.cpp:1133-1151), quantized to RGBA8 on the device (NaN and v <= 0 -> 0,
+ * v > 1 -> 1, round-to-nearest-even of 255 v, alpha 255). */
+typedef struct sxh_render_session sxh_render_session;
+typedef struct {
+    const char* ply_path;
+    int32_t antialiased;
+    int32_t sh_degree;  /* 0: the PLY's degree; 1..3: an upper bound (above the PLY's degree is an error) */
+} sxh_render_session_args;
+int32_t sxh_render_session_open(sxh_backend* b, const sxh_render_session_args* args, sxh_render_session** out);
+int32_t sxh_render_session_frame(sxh_render_session* s, const float* viewmat, float fx, float fy, float cx, float cy,
+                                 int32_t width, int32_t height, uint8_t* out_rgba /* [height*width*4] */);
+void sxh_render_session_close(sxh_render_session* s);
+
 /* Per-kernel timing of the last step (HIP events on the executor's stream), enabled by
  * sxh_exec_set_profiling(e, 1). Names are stable strings; times are milliseconds. */
 typedef struct {

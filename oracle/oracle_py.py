@@ -63,6 +63,14 @@ class HipTrainCase(C.Structure):
                 ("n_isects", sh.i64p), ("render0", sh.fp), ("out_count", C.c_int64), ("n_refined", C.c_int32)]
 
 
+class RefCloudIn(C.Structure):
+    _fields_ = [("params", sh.fp * 6), ("count", C.c_int64), ("sh_degree", C.c_int32)]
+
+
+class RefCloudOut(C.Structure):
+    _fields_ = [("params", sh.fp * 6), ("count", C.c_int64), ("sh_degree", C.c_int32)]
+
+
 class HipRefineCase(C.Structure):
     _fields_ = [("params", sh.fp * 6), ("exp_avg", sh.fp * 6), ("exp_avg_sq", sh.fp * 6), ("count", C.c_int64),
                 ("cap_max", C.c_int64), ("sh_degree", C.c_int32), ("n_refine", C.c_int32), ("seed", C.c_uint64),
@@ -246,6 +254,67 @@ class Reference(sh.Ops):
         return dict(params=outs[0], exp_avg=outs[1], exp_avg_sq=outs[2], counts=per[0], n_relocated=per[1],
                     n_added=per[2], relocated_dead=lists[0][:nr], relocation_src=lists[1][:nr],
                     added_src=lists[2][:na], rng=st)
+
+    # -- formats (PlyIO.cpp, Checkpoint.cpp) ----------------------------------------------------
+    @staticmethod
+    def _cloud_in(params, count, sh_degree):
+        keep = [sh.f32(x).reshape(count, -1) if x is not None and count > 0 else None for x in params]
+        c = RefCloudIn()
+        for g in range(6):
+            c.params[g] = _ptr_or_null(keep[g]) if keep[g] is not None else None
+        c.count, c.sh_degree = count, sh_degree
+        return c, keep
+
+    def export_ply(self, params, count, sh_degree, path, min_opacity=0.005, pad_sh_full=True):
+        c, keep = self._cloud_in(params, count, sh_degree)
+        st = sh.ExportStats()
+        self._call("export_ply", C.byref(c), C.c_float(min_opacity), int(bool(pad_sh_full)), path.encode(),
+                   C.byref(st))
+        return st.as_dict()
+
+    def read_ply(self, path, capacity):
+        o = RefCloudOut()
+        outs = [np.zeros((capacity, d), np.float32) for d in sh.GROUP_DIMS(3)]
+        for g in range(6):
+            o.params[g] = sh.ptr(outs[g])
+        o.count = capacity
+        self._call("read_ply", path.encode(), C.byref(o))
+        n, deg = int(o.count), int(o.sh_degree)
+        dims = sh.GROUP_DIMS(deg)
+        return dict(count=n, sh_degree=deg,
+                    params=[outs[g].ravel()[: n * dims[g]].reshape(n, dims[g]) for g in range(6)])
+
+    def save_checkpoint(self, config, iter, params, exp_avg, exp_avg_sq, count, sh_degree, path, rng_state=None,
+                        fp16=False):
+        c, keep = self._cloud_in(params, count, sh_degree)
+        mk = [sh.f32(x).reshape(count, -1) for x in exp_avg]
+        vk = [sh.f32(x).reshape(count, -1) for x in exp_avg_sq]
+        m = (sh.fp * 6)(*[_ptr_or_null(x) for x in mk])
+        v = (sh.fp * 6)(*[_ptr_or_null(x) for x in vk])
+        self._call("save_checkpoint", C.byref(config), iter, C.byref(c), m, v,
+                   rng_state.encode() if rng_state else None, int(bool(fp16)), path.encode())
+
+    def load_checkpoint(self, path, capacity):
+        h = sh.CkptHeader()
+        o = RefCloudOut()
+        dims = sh.GROUP_DIMS(3)
+        outs = [np.zeros((capacity, d), np.float32) for d in dims]
+        ms = [np.zeros((capacity, d), np.float32) for d in dims]
+        vs = [np.zeros((capacity, d), np.float32) for d in dims]
+        for g in range(6):
+            o.params[g] = sh.ptr(outs[g])
+        o.count = capacity
+        buf = C.create_string_buffer(1 << 16)
+        self._call("load_checkpoint", path.encode(), C.byref(h), C.byref(o), (sh.fp * 6)(*[sh.ptr(x) for x in ms]),
+                   (sh.fp * 6)(*[sh.ptr(x) for x in vs]), buf, C.c_int64(1 << 16))
+        n, deg = int(o.count), int(o.sh_degree)
+        dd = sh.GROUP_DIMS(deg)
+        cut = lambda arrs: [arrs[g].ravel()[: n * dd[g]].reshape(n, dd[g]) for g in range(6)]
+        return dict(header=h.as_dict(), params=cut(outs), exp_avg=cut(ms), exp_avg_sq=cut(vs),
+                    rng_state=buf.value.decode())
+
+    def checkpoint_verify_config(self, saved, current):
+        self._call("checkpoint_verify_config", C.byref(saved), C.byref(current))
 
     @staticmethod
     def available() -> bool:

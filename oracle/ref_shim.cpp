@@ -15,6 +15,7 @@
 #include "splatx/CpuKernels.h"
 #include "splatx/KernelBackend.h"
 #include "splatx/Math.h"
+#include "splatx/PlyIO.h"
 #include "splatx/Trainer.h"
 #include "splatx_hip.h"
 
@@ -43,6 +44,18 @@ typedef struct {
     int64_t capacity;
     sxh_mt64_state* rng_out;  /* the engine after the last refine (its checkpoint text) */
 } sxr_refine_case;
+
+/* A cloud as AoS group arrays of `count` rows (shN NULL at degree 0). */
+typedef struct {
+    const float* params[6];
+    int64_t count;
+    int32_t sh_degree;
+} sxr_cloud_in;
+typedef struct {
+    float* params[6];
+    int64_t count;      /* in: capacity rows, out: rows */
+    int32_t sh_degree;  /* out */
+} sxr_cloud_out;
 }
 
 namespace {
@@ -228,6 +241,120 @@ int32_t sxr_quat_scale_to_covar(const float* quats, const float* scales, int64_t
             std::memcpy(out + i * 9, c.m, sizeof(c.m));
         }
     });
+}
+
+namespace {
+splatx::SplatCloud cloud_from(const sxr_cloud_in* c) {
+    splatx::SplatCloud cl;
+    cl.count = c->count;
+    cl.sh_degree = c->sh_degree;
+    std::vector<float>* vs[6] = {&cl.means, &cl.quats, &cl.scales, &cl.opacities, &cl.sh0, &cl.shN};
+    const int64_t dims[6] = {3, 4, 3, 1, 3, static_cast<int64_t>(cl.sh_rest_coeffs()) * 3};
+    for (int g = 0; g < 6; g++)
+        if (dims[g]) vs[g]->assign(c->params[g], c->params[g] + c->count * dims[g]);
+    return cl;
+}
+void cloud_to(const splatx::SplatCloud& cl, sxr_cloud_out* o) {
+    if (cl.count > o->count) throw CapacityError("cloud capacity");
+    o->count = cl.count;
+    o->sh_degree = cl.sh_degree;
+    const std::vector<float>* vs[6] = {&cl.means, &cl.quats, &cl.scales, &cl.opacities, &cl.sh0, &cl.shN};
+    for (int g = 0; g < 6; g++)
+        if (o->params[g]) put(o->params[g], *vs[g]);
+}
+splatx::CheckpointConfig config_from(const sxh_checkpoint_config* c) {
+    splatx::CheckpointConfig k;
+    k.sh_degree = c->sh_degree;
+    k.factor = c->factor;
+    k.test_split = c->test_split;
+    k.total_iters = c->total_iters;
+    k.mcmc_enabled = c->mcmc_enabled;
+    k.antialiased = c->antialiased;
+    k.cap_max = c->cap_max;
+    k.mcmc_seed = c->mcmc_seed;
+    k.scene_scale = c->scene_scale;
+    k.ssim_weight = c->ssim_weight;
+    return k;
+}
+}  // namespace
+
+/* filter_cloud_for_export + write_inria_ply (PlyIO.h:20-51) */
+int32_t sxr_export_ply(const sxr_cloud_in* c, float min_opacity, uint8_t pad_sh_full, const char* path,
+                       sxh_export_stats* stats) {
+    return guarded([&] {
+        splatx::ExportFilterStats st;
+        const splatx::SplatCloud f = splatx::filter_cloud_for_export(cloud_from(c), min_opacity, &st);
+        splatx::write_inria_ply(f, path, pad_sh_full != 0);
+        if (stats) {
+            stats->input = st.input;
+            stats->removed_nonfinite = st.removed_nonfinite;
+            stats->removed_low_opacity = st.removed_low_opacity;
+            stats->kept = st.kept;
+        }
+    });
+}
+
+/* read_inria_ply */
+int32_t sxr_read_ply(const char* path, sxr_cloud_out* o) {
+    return guarded([&] { cloud_to(splatx::read_inria_ply(path), o); });
+}
+
+/* TrainerCheckpoint of count rows -> save_checkpoint_file */
+int32_t sxr_save_checkpoint(const sxh_checkpoint_config* cfg, int32_t iter, const sxr_cloud_in* c,
+                            const float* const* exp_avg, const float* const* exp_avg_sq, const char* rng_state,
+                            uint8_t fp16, const char* path) {
+    return guarded([&] {
+        splatx::TrainerCheckpoint ck;
+        ck.config = config_from(cfg);
+        ck.iter = iter;
+        ck.cloud = cloud_from(c);
+        const int64_t dims[6] = {3, 4, 3, 1, 3, static_cast<int64_t>(ck.cloud.sh_rest_coeffs()) * 3};
+        for (int g = 0; g < 6; g++) {
+            const int64_t n = c->count * dims[g];
+            if (n) {
+                ck.moments[g].exp_avg.assign(exp_avg[g], exp_avg[g] + n);
+                ck.moments[g].exp_avg_sq.assign(exp_avg_sq[g], exp_avg_sq[g] + n);
+            }
+        }
+        ck.mcmc_rng_state = rng_state ? rng_state : "";
+        splatx::save_checkpoint_file(ck, path, fp16 != 0);
+    });
+}
+
+/* load_checkpoint_file: the header, the cloud and the moments of count rows, the engine text */
+int32_t sxr_load_checkpoint(const char* path, sxh_checkpoint_header* h, sxr_cloud_out* o, float* const* exp_avg,
+                            float* const* exp_avg_sq, char* rng_state, int64_t rng_capacity) {
+    return guarded([&] {
+        const splatx::TrainerCheckpoint ck = splatx::load_checkpoint_file(path);
+        const splatx::CheckpointHeader hh = splatx::load_checkpoint_header(path);
+        h->config.sh_degree = hh.config.sh_degree;
+        h->config.factor = hh.config.factor;
+        h->config.test_split = hh.config.test_split;
+        h->config.total_iters = hh.config.total_iters;
+        h->config.mcmc_enabled = hh.config.mcmc_enabled;
+        h->config.antialiased = hh.config.antialiased;
+        h->config.cap_max = hh.config.cap_max;
+        h->config.mcmc_seed = hh.config.mcmc_seed;
+        h->config.scene_scale = hh.config.scene_scale;
+        h->config.ssim_weight = hh.config.ssim_weight;
+        h->iter = hh.iter;
+        h->alive_count = hh.alive_count;
+        h->fp16 = hh.fp16 ? 1 : 0;
+        h->version = hh.version;
+        cloud_to(ck.cloud, o);
+        for (int g = 0; g < 6; g++) {
+            if (exp_avg && exp_avg[g]) put(exp_avg[g], ck.moments[g].exp_avg);
+            if (exp_avg_sq && exp_avg_sq[g]) put(exp_avg_sq[g], ck.moments[g].exp_avg_sq);
+        }
+        if (rng_state) {
+            if (static_cast<int64_t>(ck.mcmc_rng_state.size()) + 1 > rng_capacity) throw CapacityError("rng capacity");
+            std::memcpy(rng_state, ck.mcmc_rng_state.c_str(), ck.mcmc_rng_state.size() + 1);
+        }
+    });
+}
+
+int32_t sxr_checkpoint_verify_config(const sxh_checkpoint_config* saved, const sxh_checkpoint_config* current) {
+    return guarded([&] { splatx::verify_checkpoint_config(config_from(saved), config_from(current)); });
 }
 
 int32_t sxr_trainer_mcmc_refine(sxr_refine_case* c) {

@@ -156,8 +156,10 @@ int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out) {
     });
 }
 
-// The step proper. `gt_override` (device) replaces the GT source when not null.
-static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out, float* render_to_dev) {
+} // extern "C"
+
+// The step proper. `render_to_dev` (device), when not null, receives a copy of the render.
+void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out, float* render_to_dev) {
     const char* what = "TrainStepExecutor::step";
     if (!in || !out) invalid(what, "null inputs/outputs");
     // MetalBackend.cpp:1697-1711
@@ -341,11 +343,13 @@ static void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_output
     }
 }
 
+extern "C" {
+
 int32_t sxh_exec_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out) {
     return guarded([&] {
         if (!e) invalid("TrainStepExecutor::step", "null executor");
         SXH_HIP(hipSetDevice(e->b->device));
-        run_step(e, in, out, nullptr);
+        sxh_detail::run_step(e, in, out, nullptr);
     });
 }
 
@@ -359,7 +363,7 @@ int32_t sxh_exec_render_to_gt_cache(sxh_executor* e, const sxh_step_inputs* in, 
         f.forward_only = 1;
         sxh_step_outputs o{};
         const size_t n_px = static_cast<size_t>(in->width) * in->height * 3;
-        run_step(e, &f, &o, e->gt_cache.p + static_cast<size_t>(index) * n_px);
+        sxh_detail::run_step(e, &f, &o, e->gt_cache.p + static_cast<size_t>(index) * n_px);
         SXH_HIP(hipStreamSynchronize(e->b->stream));
     });
 }

@@ -139,3 +139,8 @@ struct sxh_executor {
     }
 };
 
+namespace sxh_detail {
+// One training (or forward-only) step of the executor; render_to_dev, when not null, receives a
+// device copy of the render. Defined in executor.cpp.
+void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out, float* render_to_dev);
+}  // namespace sxh_detail

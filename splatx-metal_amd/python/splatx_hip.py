@@ -212,6 +212,111 @@ def refine_lists(out: RefineOutputs, lists) -> dict:
     return r
 
 
+class ExportStats(C.Structure):
+    _fields_ = [("input", C.c_int64), ("removed_nonfinite", C.c_int64), ("removed_low_opacity", C.c_int64),
+                ("kept", C.c_int64)]
+
+    def as_dict(self):
+        return {k: int(getattr(self, k)) for k, _ in self._fields_}
+
+
+class CkptConfig(C.Structure):
+    _fields_ = [("sh_degree", C.c_int32), ("factor", C.c_int32), ("test_split", C.c_int32), ("total_iters", C.c_int32),
+                ("mcmc_enabled", C.c_uint8), ("antialiased", C.c_uint8), ("cap_max", C.c_int64),
+                ("mcmc_seed", C.c_uint64), ("scene_scale", C.c_float), ("ssim_weight", C.c_float)]
+
+    @staticmethod
+    def make(**kw):
+        c = CkptConfig()
+        c.scene_scale = 1.0
+        for k, v in kw.items():
+            setattr(c, k, v)
+        return c
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class CkptHeader(C.Structure):
+    _fields_ = [("config", CkptConfig), ("iter", C.c_int32), ("alive_count", C.c_int64), ("fp16", C.c_uint8),
+                ("version", C.c_uint32)]
+
+    def as_dict(self):
+        return dict(config=self.config.as_dict(), iter=int(self.iter), alive_count=int(self.alive_count),
+                    fp16=int(self.fp16), version=int(self.version))
+
+
+class RenderSessionArgs(C.Structure):
+    _fields_ = [("ply_path", C.c_char_p), ("antialiased", C.c_int32), ("sh_degree", C.c_int32)]
+
+
+def _raise(lib, rc):
+    if rc != SXH_OK:
+        msg = lib.sxh_last_error().decode(errors="replace")
+        if rc == SXH_ERR_INVALID_ARGUMENT:
+            raise SxInvalidArgument(msg)
+        if rc == SXH_ERR_CAPACITY:
+            raise SxCapacityError(msg)
+        raise SxRuntimeError(msg)
+
+
+def ply_read(path, lib=None):
+    """read_inria_ply (sxh_ply_read): dict(count, sh_degree, params = 6 AoS arrays)."""
+    lib = lib or load_library()
+    lib.sxh_last_error.restype = C.c_char_p
+    f = lib.sxh_ply_read
+    f.restype = C.c_int32
+    n, deg = C.c_int64(), C.c_int32()
+    _raise(lib, f(path.encode(), C.byref(n), C.byref(deg), None))
+    dims = GROUP_DIMS(deg.value)
+    params = [np.zeros((n.value, d), np.float32) for d in dims]
+    arr = (fp * 6)(*[ptr(x) if x.size else None for x in params])
+    _raise(lib, f(path.encode(), C.byref(n), C.byref(deg), arr))
+    return dict(count=n.value, sh_degree=deg.value, params=params)
+
+
+def checkpoint_read_header(path, lib=None):
+    lib = lib or load_library()
+    lib.sxh_last_error.restype = C.c_char_p
+    h = CkptHeader()
+    lib.sxh_checkpoint_read_header.restype = C.c_int32
+    _raise(lib, lib.sxh_checkpoint_read_header(path.encode(), C.byref(h)))
+    return h.as_dict()
+
+
+def checkpoint_verify_config(saved: CkptConfig, current: CkptConfig, lib=None):
+    lib = lib or load_library()
+    lib.sxh_last_error.restype = C.c_char_p
+    lib.sxh_checkpoint_verify_config.restype = C.c_int32
+    _raise(lib, lib.sxh_checkpoint_verify_config(C.byref(saved), C.byref(current)))
+
+
+class RenderSession:
+    """sx_render_session_* (splatx_train_c.h:604-682) over sxh_render_session_*."""
+
+    def __init__(self, backend, ply_path, antialiased=False, sh_degree=0):
+        self.lib = backend.lib
+        self.h = C.c_void_p()
+        self._path = ply_path.encode()
+        a = RenderSessionArgs(self._path, int(bool(antialiased)), sh_degree)
+        self.lib.sxh_render_session_open.restype = C.c_int32
+        _raise(self.lib, self.lib.sxh_render_session_open(backend.handle, C.byref(a), C.byref(self.h)))
+        self.lib.sxh_render_session_frame.restype = C.c_int32
+        self.lib.sxh_render_session_close.argtypes = [C.c_void_p]
+
+    def frame(self, viewmat, fx, fy, cx, cy, width, height):
+        vm = f32(viewmat)
+        out = np.zeros((height, width, 4), np.uint8)
+        _raise(self.lib, self.lib.sxh_render_session_frame(self.h, ptr(vm), C.c_float(fx), C.c_float(fy), C.c_float(cx),
+                                                          C.c_float(cy), width, height, ptr(out)))
+        return out
+
+    def close(self):
+        if self.h is not None and self.h.value is not None:
+            self.lib.sxh_render_session_close(self.h)
+        self.h = None
+
+
 class ExecTiming(C.Structure):
     _fields_ = [("n", C.c_int32), ("names", C.c_char_p * 32), ("ms", C.c_float * 32)]
 
@@ -527,6 +632,9 @@ class Backend(Ops):
         self._call("mt64_draw", C.byref(st), C.c_int64(n), ptr(out))
         return out
 
+    def render_session(self, ply_path, antialiased=False, sh_degree=0) -> "RenderSession":
+        return RenderSession(self, ply_path, antialiased, sh_degree)
+
     def mt64_seed(self, seed: int) -> MtState:
         """std::mt19937_64(seed) state (sxh_mt64_seed)."""
         st = MtState()
@@ -640,6 +748,32 @@ class Executor:
             o.capacity = cap
         self._check(self.lib.sxh_exec_mcmc_refine(self.h, C.byref(i), C.byref(o)))
         return refine_lists(o, lists)
+
+    def export_ply(self, count, path, min_opacity=0.005, pad_sh_full=True):
+        """filter_cloud_for_export + write_inria_ply of the live rows (sxh_exec_export_ply)."""
+        st = ExportStats()
+        f = self.lib.sxh_exec_export_ply
+        f.restype = C.c_int32
+        self._check(f(self.h, C.c_int64(count), C.c_float(min_opacity), int(bool(pad_sh_full)), path.encode(),
+                      C.byref(st)))
+        return st.as_dict()
+
+    def save_checkpoint(self, config: CkptConfig, iter, count, path, rng_state=None, fp16=False):
+        f = self.lib.sxh_exec_save_checkpoint
+        f.restype = C.c_int32
+        rng = rng_state.encode() if rng_state else None
+        self._check(f(self.h, C.byref(config), iter, C.c_int64(count), rng, int(bool(fp16)), path.encode()))
+
+    def load_checkpoint(self, path, current: CkptConfig = None, rng_capacity=1 << 16):
+        f = self.lib.sxh_exec_load_checkpoint
+        f.restype = C.c_int32
+        h = CkptHeader()
+        buf = C.create_string_buffer(rng_capacity)
+        self._check(f(self.h, path.encode(), C.byref(current) if current is not None else None, C.byref(h), buf,
+                      C.c_int64(rng_capacity)))
+        d = h.as_dict()
+        d["rng_state"] = buf.value.decode()
+        return d
 
     def set_profiling(self, enable: bool):
         self._check(self.lib.sxh_exec_set_profiling(self.h, int(bool(enable))))
