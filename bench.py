@@ -101,6 +101,55 @@ def calibrate_copy(mib: int, reps: int = 4) -> None:
     print(json.dumps({"calibrate_copy_bytes": n, "reps": reps}), flush=True)
 
 
+def bench_formats(cfg_id: int) -> None:
+    """Wall-clock ms of the data formats on the config's scene (files under $TMPDIR): the device export filter +
+    INRIA PLY write, SXCK checkpoint save and load (fp32 and fp16, with fsync), and render-session frames."""
+    import tempfile
+
+    sc, cfg = scene.config_scene(cfg_id, seed=0)
+    b = sh.Backend(0)
+    ex = b.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree)
+    p, m, v = scene.copy_state(sc)
+    ex.upload_params(p, m, v, sc.n)
+    d = tempfile.mkdtemp(prefix="splatx_formats_")
+    out = {"workload": f"config {cfg_id}: N={sc.n}, SH{sc.sh_degree}", "ms": {}, "bytes": {}}
+
+    def timed(name, fn, reps=3):
+        best = None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            dt = (time.perf_counter() - t0) * 1000.0
+            best = dt if best is None else min(best, dt)
+        out["ms"][name] = round(best, 2)
+
+    ply = os.path.join(d, "c.ply")
+    timed("export_ply", lambda: ex.export_ply(sc.n, ply))
+    out["bytes"]["ply"] = os.path.getsize(ply)
+    ck = sh.CkptConfig.make(sh_degree=sc.sh_degree, total_iters=30000)
+    for fp16 in (False, True):
+        path = os.path.join(d, f"c{16 if fp16 else 32}.sxck")
+        timed(f"save_checkpoint_fp{16 if fp16 else 32}", lambda: ex.save_checkpoint(ck, 100, sc.n, path, fp16=fp16))
+        timed(f"load_checkpoint_fp{16 if fp16 else 32}", lambda: ex.load_checkpoint(path, current=ck))
+        out["bytes"][f"checkpoint_fp{16 if fp16 else 32}"] = os.path.getsize(path)
+    ex.close()
+    sess = b.render_session(ply)
+    rng = np.random.Generator(np.random.PCG64(7))
+    views = [scene.jittered_view(rng) for _ in range(20)]
+    K = sc.K
+    sess.frame(views[0], K[0, 0], K[1, 1], K[0, 2], K[1, 2], sc.width, sc.height)
+    t0 = time.perf_counter()
+    for vm in views:
+        sess.frame(vm, K[0, 0], K[1, 1], K[0, 2], K[1, 2], sc.width, sc.height)
+    out["ms"]["render_session_frame"] = round((time.perf_counter() - t0) * 1000.0 / len(views), 3)
+    sess.close()
+    b.close()
+    for f in os.listdir(d):
+        os.remove(os.path.join(d, f))
+    os.rmdir(d)
+    print(json.dumps(out), flush=True)
+
+
 def load_traffic(kernel: str, cfg: int):
     """HBM bytes per launch of `kernel`, as measured by the counter runs recorded in profiles/traffic.json
     (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel yardstick); None if not recorded."""
@@ -122,6 +171,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--formats", action="store_true",
+                    help="time the formats either side of the step (PLY export, checkpoint save/load, render-session "
+                         "frames) on the config's arena instead of the training step, and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run device copies of MIB MiB (yardstick for the HBM byte counters) and exit")
     args = ap.parse_args()
@@ -131,6 +183,10 @@ def main():
         sys.exit(2)
     if args.calibrate_copy > 0:
         calibrate_copy(args.calibrate_copy)
+        return
+
+    if args.formats:
+        bench_formats(args.config)
         return
 
     sc, cfg = scene.config_scene(args.config, seed=0)

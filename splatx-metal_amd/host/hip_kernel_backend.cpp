@@ -433,6 +433,12 @@ void mt_state_to(const sxh_mt64_state& st, std::mt19937_64& g) {
 
 } // namespace
 
+sxh_executor* hip_executor_handle(TrainStepExecutor& exec) {
+    auto* hx = dynamic_cast<HipTrainStepExecutor*>(&exec);
+    if (!hx) throw std::invalid_argument("hip_executor_handle: executor was not made by make_hip_backend");
+    return hx->handle();
+}
+
 HipMcmcRefineResult hip_mcmc_refine(TrainStepExecutor& exec, std::mt19937_64& rng, const HipMcmcRefineInputs& in) {
     auto* hx = dynamic_cast<HipTrainStepExecutor*>(&exec);
     if (!hx) throw std::invalid_argument("hip_mcmc_refine: executor was not made by make_hip_backend");

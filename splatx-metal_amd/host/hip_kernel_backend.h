@@ -44,3 +44,14 @@ struct HipMcmcRefineResult {
 HipMcmcRefineResult hip_mcmc_refine(TrainStepExecutor& exec, std::mt19937_64& rng, const HipMcmcRefineInputs& in);
 
 } // namespace splatx
+
+struct sxh_executor;
+
+namespace splatx {
+
+// The C handle of a resident executor made by make_hip_backend, for the device-side data formats
+// of include/splatx_hip.h (sxh_exec_export_ply, sxh_exec_save_checkpoint, sxh_exec_load_checkpoint)
+// that read or write its arena in place; std::invalid_argument for any other executor.
+sxh_executor* hip_executor_handle(TrainStepExecutor& exec);
+
+} // namespace splatx
