@@ -276,6 +276,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     ra.tile_width = tw;
     ra.tile_height = th;
     ra.n_isects = static_cast<int32_t>(n_isects);
+    sxk::raster_tile_order(e->offsets.p, tw * th, n_isects, e->tile_order.p, s);
+    ra.tile_order = e->tile_order.p;
     sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
     e->mark("raster_fwd");
     float* hloss = reinterpret_cast<float*>(&hs[3]);

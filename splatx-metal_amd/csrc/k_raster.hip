@@ -114,7 +114,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     __shared__ int s_len[4];
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
-    const int tile = blockIdx.x % n_tiles;
+    const int tile = a.tile_order ? a.tile_order[blockIdx.x % n_tiles] : static_cast<int>(blockIdx.x % n_tiles);
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -236,7 +236,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     float* s_part = reinterpret_cast<float*>(s_part4);
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
-    const int tile = blockIdx.x % n_tiles;
+    const int tile = a.tile_order ? a.tile_order[blockIdx.x % n_tiles] : static_cast<int>(blockIdx.x % n_tiles);
     if (a.masks && a.masks[(size_t)img * n_tiles + tile] == 0) return;  // uniform
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
@@ -424,6 +424,48 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
 }
 
 } // namespace
+
+namespace {
+// Counting sort of the tiles by descending intersection count (256 buckets of width w, w the
+// smallest power of two with max_count < 256 w), one workgroup.
+__global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__ offsets, int n_tiles,
+                                                     int64_t n_isects, int32_t* __restrict__ order) {
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_max;
+    const int t0 = threadIdx.x;
+    if (t0 < 256) s_hist[t0] = 0;
+    if (t0 == 0) s_max = 0;
+    __syncthreads();
+    auto count_of = [&](int t) -> uint32_t {
+        const int64_t e = t + 1 < n_tiles ? offsets[t + 1] : n_isects;
+        return static_cast<uint32_t>(e - offsets[t]);
+    };
+    for (int t = t0; t < n_tiles; t += 1024) atomicMax(&s_max, count_of(t));
+    __syncthreads();
+    int shift = 0;
+    while ((s_max >> shift) >= 256u) shift++;
+    for (int t = t0; t < n_tiles; t += 1024) atomicAdd(&s_hist[255u - (count_of(t) >> shift)], 1u);
+    __syncthreads();
+    if (t0 == 0) {  // exclusive prefix over 256 buckets
+        uint32_t run = 0;
+        for (int b = 0; b < 256; b++) {
+            const uint32_t c = s_hist[b];
+            s_hist[b] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int t = t0; t < n_tiles; t += 1024) {
+        const uint32_t pos = atomicAdd(&s_hist[255u - (count_of(t) >> shift)], 1u);
+        order[pos] = t;
+    }
+}
+}  // namespace
+
+void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s) {
+    if (n_tiles <= 0) return;
+    hipLaunchKernelGGL(k_tile_order, dim3(1), dim3(1024), 0, s, offsets, n_tiles, n_isects, order);
+}
 
 void raster_fwd(const RasterArgs& a, float* rgb, float* alpha, int32_t* last, hipStream_t s) {
     const int blocks = a.I * a.tile_width * a.tile_height;

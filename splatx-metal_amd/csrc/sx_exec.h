@@ -51,7 +51,7 @@ struct sxh_executor {
     sxh::DevBuf<uint8_t> sort_scratch;
     // image-sized buffers
     size_t img_px = 0, img_tiles = 0, img_map = 0;
-    sxh::DevBuf<int32_t> offsets, last_ids;
+    sxh::DevBuf<int32_t> offsets, last_ids, tile_order;
     sxh::DevBuf<float> render, alpha, v_render, v_alpha_zero, gt_stage;
     sxh::DevBuf<float> cmu, csg, ccr;  // SSIM coefficient maps (the map itself is only summed)
     sxh::DevBuf<double> ssim_part, l1_part;
@@ -124,6 +124,7 @@ struct sxh_executor {
         if (l1_blocks > l1_part.n) l1_part.alloc(l1_blocks);
         if (tiles_n > img_tiles) {
             offsets.alloc(tiles_n);
+            tile_order.alloc(tiles_n);
             img_tiles = tiles_n;
         }
         if (use_ssim) {

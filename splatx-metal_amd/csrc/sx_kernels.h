@@ -89,7 +89,13 @@ struct RasterArgs {
     const uint8_t* masks;      // [I,n_tiles] or null
     int I, width, height, tile_width, tile_height;
     int32_t n_isects;
+    // optional (I == 1): workgroup b renders tile tile_order[b] — heaviest tiles first, so the
+    // last workgroups to start are the short ones; null = tile b
+    const int32_t* tile_order;
 };
+// tile_order for raster_fwd/raster_bwd: the n_tiles tile ids by descending intersection count
+// (counting sort on 256 buckets of the count; order within a bucket unspecified)
+void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s);
 void raster_fwd(const RasterArgs& a, float* render_colors, float* render_alphas, int32_t* last_ids,
                 hipStream_t s);
 // Gradient outputs zeroed by the caller; packed as 3 x float4 per Gaussian when `packed_grads`
