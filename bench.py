@@ -45,7 +45,9 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, n_p
     if name == "raster_bwd":
         return i * (4 + 36 + 36) + px * (4 + 4 + 12)
     if name == "sort":
-        return i * 36.0 * n_passes
+        # onesweep: one read of the keys for all digit histograms (8 B), then per pass one read and
+        # one write of (key, value) (24 B)
+        return i * (8.0 + 24.0 * n_passes)
     if name == "emit":
         return v * 28.0 + n * 8.0 + i * 12.0
     if name == "offsets":

@@ -317,6 +317,10 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         e->mark("loss");
         SXH_HIP(hipMemcpyAsync(hloss, e->loss_dev.p, 4, hipMemcpyDeviceToHost, s));
     }
+    uint32_t* hsort = reinterpret_cast<uint32_t*>(&hs[4]);
+    *hsort = 0;
+    if (n_isects > 0)
+        SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p, n_isects), 4, hipMemcpyDeviceToHost, s));
     if (render_to_dev)
         SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
     if (out->render_colors)
@@ -327,6 +331,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     SXH_HIP(hipStreamSynchronize(s));
     e->sync_ms[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     out->loss = fwd_only ? 0.0f : *hloss;
+    if (*hsort) throw std::runtime_error(std::string(what) + ": radix sort look-back did not complete");
     if (e->prof) {
         sxh_exec_timing& t = e->timing;
         t.n = 0;

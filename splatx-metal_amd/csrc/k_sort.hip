@@ -2,7 +2,10 @@
 //
 // Contract: KernelBackend.h:130-148 / sort_isect (ascending unsigned key, stable, only bits
 // [0, key_bits) significant). Design: 8-bit digits, so a 45-bit isect key needs 6 passes (the
-// reference's 4-bit digits need 12). Each pass is three launches with no inter-workgroup waiting:
+// reference's 4-bit digits need 12). Below 2^30 keys the passes run onesweep (see k_os_pass): the
+// digit histograms of all passes come from one read of the keys, and each pass is one launch
+// whose tiles chain their digit prefixes by look-back. The fallback is three launches per pass
+// with no inter-workgroup waiting:
 //   1. per-tile digit histogram (LDS counters)        -> hist[digit][tile], plus the digit totals
 //   2. one workgroup per digit scans its row of hist   -> global start of (digit, tile)
 //   3. stable scatter: each 64-lane wave ranks the keys of its quarter of the tile per digit with 8
@@ -21,6 +24,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kRounds = 16;
 constexpr int kTile = kThreads * kRounds;  // 4096 keys per workgroup
 constexpr int kBins = 256;
+constexpr int kMaxPassesOs = 8;
 
 // Lanes of the wave whose 8-bit digit equals this lane's (among lanes where `valid`), from 8 ballots.
 __device__ __forceinline__ uint64_t digit_match(uint32_t digit, bool valid) {
@@ -217,6 +221,216 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
     }
 }
 
+// ---- onesweep: one launch per pass (digit histograms of every pass from one read up front) ----
+// Tile t of a pass publishes its digit counts to status[t][d] as soon as it has ranked its keys
+// (flag AGG), then looks back over its predecessors' words, adding counts until it meets an
+// inclusive prefix (flag INC), and publishes its own inclusive prefix. Tiles take their index from
+// an atomic counter in the order they start, so every tile a tile waits on has already started and
+// publishes without waiting itself: the look-back always ends. A bounded spin turns a broken
+// invariant into an error flag instead of a hang.
+constexpr uint32_t kFlagAgg = 1u << 30;
+constexpr uint32_t kFlagInc = 2u << 30;
+constexpr uint32_t kValMask = (1u << 30) - 1u;
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr int kLook = 8;  // predecessor words per look-back round trip
+
+__device__ __forceinline__ uint32_t ld_status(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_status(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Digit histograms of passes [0, passes) -> totals[p][d]; clears the first pass's status words and
+// the per-pass tile counters. Grid-stride over 4096-key chunks. A wave whose 64 digits agree (the
+// tile bits of neighbouring keys) adds once; otherwise each lane adds 1 (spread digits, few
+// collisions): cheaper than match masks here, where no ranks are needed.
+__global__ void __launch_bounds__(kThreads) k_os_hist(const uint64_t* __restrict__ keys, int64_t n, int passes,
+                                                      uint32_t* __restrict__ totals, uint32_t* __restrict__ status0,
+                                                      int64_t status_words, uint32_t* __restrict__ counters) {
+    __shared__ uint32_t h[kMaxPassesOs][kBins];
+    for (int p = 0; p < kMaxPassesOs; p++) h[p][threadIdx.x] = 0;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < status_words; i += (int64_t)gridDim.x * kThreads)
+        status0[i] = 0u;
+    if (blockIdx.x == 0 && threadIdx.x <= kMaxPassesOs) counters[threadIdx.x] = 0u;  // + the error word after them
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int64_t chunks = (n + kTile - 1) / kTile;
+    for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const int64_t base = c * kTile;
+        uint64_t key[kRounds];  // the whole chunk in flight before any counting
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const int64_t idx = base + r * kThreads + threadIdx.x;
+            key[r] = idx < n ? keys[idx] : 0ull;
+        }
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const bool valid = base + r * kThreads + threadIdx.x < n;
+            for (int p = 0; p < passes; p++) {
+                const uint32_t d = static_cast<uint32_t>((key[r] >> (8 * p)) & 0xFF);
+                const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
+                if (__all(valid && d == d0)) {  // one digit for the whole wave: one add
+                    if (lane == 0) atomicAdd(&h[p][d0], 64u);
+                } else if (valid) {
+                    atomicAdd(&h[p][d], 1u);  // spread digits: lanes mostly hit distinct counters
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int p = 0; p < passes; p++) {
+        const uint32_t v = h[p][threadIdx.x];
+        if (v) atomicAdd(&totals[p * kBins + threadIdx.x], v);
+    }
+}
+
+// totals[p][d] -> base[p][d] = keys of digits < d (exclusive scan per pass); totals left as is
+__global__ void __launch_bounds__(kThreads) k_os_scan(const uint32_t* __restrict__ totals, int passes,
+                                                      uint32_t* __restrict__ base) {
+    __shared__ uint32_t s_wave[kWaves];
+    for (int p = 0; p < passes; p++) {
+        uint32_t all = 0;
+        base[p * kBins + threadIdx.x] = block_excl_scan_u32(totals[p * kBins + threadIdx.x], s_wave, &all);
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) k_os_pass(const uint64_t* __restrict__ kin, const int32_t* __restrict__ vin,
+                                                      uint64_t* __restrict__ kout, int32_t* __restrict__ vout,
+                                                      int64_t n, int shift, const uint32_t* __restrict__ digit_base,
+                                                      uint32_t* __restrict__ status, uint32_t* __restrict__ status_next,
+                                                      uint32_t* __restrict__ counter, uint32_t* __restrict__ err) {
+    constexpr int kPerWave = kTile / kWaves;  // 1024
+    __shared__ uint64_t s_k[kTile];
+    __shared__ int32_t s_v[kTile];
+    __shared__ uint32_t s_gstart[kBins];
+    __shared__ uint32_t s_lstart[kBins];
+    __shared__ uint32_t s_woff[kWaves][kBins];
+    __shared__ uint32_t s_wave[kWaves];
+    __shared__ uint32_t s_tile;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_tile = atomicAdd(counter, 1u);
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
+    __syncthreads();
+    const uint32_t tile = s_tile;
+    const int64_t base = (int64_t)tile * kTile;
+    const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
+    uint64_t key[kRounds];
+    int32_t val[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+        const int i = wave * kPerWave + r * 64 + lane;
+        key[r] = i < tile_n ? kin[base + i] : 0ull;
+        val[r] = i < tile_n ? vin[base + i] : 0;
+    }
+    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint8_t rank[kRounds];
+    uint8_t cnt[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+        const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
+        const uint32_t d = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint64_t match = digit_match(d, valid);
+        rank[r] = static_cast<uint8_t>(__popcll(match & lanes_below));
+        cnt[r] = 0;
+        if (valid && rank[r] == 0) {
+            const uint32_t c = static_cast<uint32_t>(__popcll(match));
+            cnt[r] = static_cast<uint8_t>(c - 1);
+            s_woff[wave][d] += c;
+        }
+    }
+    __syncthreads();
+    uint32_t tile_count;
+    {
+        uint32_t c[kWaves], tot = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            c[w] = s_woff[w][tid];
+            tot += c[w];
+        }
+        tile_count = tot;
+        uint32_t all = 0;
+        uint32_t run = block_excl_scan_u32(tot, s_wave, &all);
+        s_lstart[tid] = run;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            s_woff[w][tid] = run;
+            run += c[w];
+        }
+    }
+    // publish this tile's digit counts now; the look-back for the prefixes of the tiles before it
+    // waits until the tile has been reordered in LDS, which gives them time to finish theirs
+    uint32_t* my = status + (size_t)tile * kBins + tid;
+    st_status(my, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
+    __syncthreads();
+    uint32_t* woff = s_woff[wave];
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+        if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
+        const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
+        const uint32_t digit = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        if (valid) {
+            const uint32_t pos = woff[digit] + rank[r];
+            s_k[pos] = key[r];
+            s_v[pos] = val[r];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (valid && rank[r] == 0) woff[digit] += static_cast<uint32_t>(cnt[r]) + 1u;
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    // look back (thread = digit): kLook predecessors' words per round trip, newest first, adding
+    // counts until an inclusive prefix; then publish this tile's inclusive prefix
+    uint32_t excl = 0;
+    if (tile > 0) {
+        int64_t j = (int64_t)tile - 1;
+        uint32_t spins = 0;
+        while (j >= 0) {
+            uint32_t w[kLook];
+#pragma unroll
+            for (int q = 0; q < kLook; q++) w[q] = j - q >= 0 ? ld_status(status + (size_t)(j - q) * kBins + tid) : kFlagInc;
+            int adv = kLook;  // predecessors consumed this round
+            bool done = false;
+#pragma unroll
+            for (int q = 0; q < kLook; q++) {
+                if (!done && adv == kLook) {
+                    const uint32_t f = w[q] & ~kValMask;
+                    if (f == 0u) {
+                        adv = q;  // not published yet: retry from this tile
+                    } else {
+                        if (j - q >= 0) excl += w[q] & kValMask;
+                        if (f == kFlagInc) done = true;
+                    }
+                }
+            }
+            if (done) break;
+            j -= adv;
+            if (adv == 0) {
+                if (++spins > kSpinLimit) {
+                    atomicOr(err, 1u);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        st_status(my, kFlagInc | (excl + tile_count));
+    }
+    s_gstart[tid] = digit_base[tid] + excl;
+    if (status_next) status_next[(size_t)tile * kBins + tid] = 0u;
+    __syncthreads();
+    for (int p = tid; p < tile_n; p += kThreads) {
+        const uint64_t k = s_k[p];
+        const uint32_t d = static_cast<uint32_t>((k >> shift) & 0xFF);
+        const uint32_t g = s_gstart[d] + (static_cast<uint32_t>(p) - s_lstart[d]);
+        if (g < n) {  // always, unless the look-back gave up (err set): then no write lands out of range
+            kout[g] = k;
+            vout[g] = s_v[p];
+        }
+    }
+}
+
 int tiles_for(int64_t n) { return static_cast<int>((n + kTile - 1) / kTile); }
 
 } // namespace
@@ -225,23 +439,48 @@ constexpr int kMaxPasses = 8;
 
 size_t sort_scratch_bytes(int64_t n) {
     const int64_t tiles = std::max<int64_t>(1, tiles_for(n));
-    const int64_t hist = tiles * kBins;
-    return sizeof(uint32_t) * static_cast<size_t>(hist + kMaxPasses * kBins + 64);
+    const int64_t hist = tiles * kBins;  // per-pass histogram (three-launch path) or one status buffer (onesweep)
+    // hist/status A, status B, totals [8][256], bases [8][256], counters [8], error word, padding
+    return sizeof(uint32_t) * static_cast<size_t>(2 * hist + 2 * kMaxPasses * kBins + 64);
+}
+
+uint32_t* sort_error_flag(void* scratch, int64_t n) {
+    const int64_t hist_n = (int64_t)std::max(1, tiles_for(n)) * kBins;
+    return static_cast<uint32_t*>(scratch) + 2 * hist_n + 2 * kMaxPasses * kBins + kMaxPasses;
 }
 
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
                void* scratch, hipStream_t s) {
     if (n <= 0 || key_bits == 0) return 0;
-    const int tiles = tiles_for(n);
+    const int tiles = std::max(1, tiles_for(n));
+    const int passes = static_cast<int>((key_bits + 7) / 8);
     uint32_t* hist = static_cast<uint32_t*>(scratch);
     const int64_t hist_n = (int64_t)tiles * kBins;
-    uint32_t* totals = hist + hist_n;
-    const int passes = static_cast<int>((key_bits + 7) / 8);
-    hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins);
+    uint32_t* status_b = hist + hist_n;
+    uint32_t* totals = status_b + hist_n;
+    uint32_t* bases = totals + kMaxPasses * kBins;
+    uint32_t* counters = bases + kMaxPasses * kBins;
+    uint32_t* err = counters + kMaxPasses;  // zeroed with the counters by k_os_hist
     uint64_t* kin = keys_a;
     int32_t* vin = vals_a;
     uint64_t* kout = keys_b;
     int32_t* vout = vals_b;
+    hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins);
+    if (n < (int64_t{1} << 30)) {  // onesweep: counts and prefixes fit the 30-bit status words
+        const int hist_blocks = std::min(tiles, 2048);
+        hipLaunchKernelGGL(k_os_hist, dim3(hist_blocks), dim3(kThreads), 0, s, kin, n, passes, totals, hist, hist_n,
+                           counters);
+        hipLaunchKernelGGL(k_os_scan, dim3(1), dim3(kThreads), 0, s, totals, passes, bases);
+        uint32_t* st[2] = {hist, status_b};
+        for (int p = 0; p < passes; p++) {
+            uint32_t* next = p + 1 < passes ? st[(p + 1) & 1] : nullptr;
+            hipLaunchKernelGGL(k_os_pass, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, 8 * p,
+                               bases + p * kBins, st[p & 1], next, counters + p, err);
+            std::swap(kin, kout);
+            std::swap(vin, vout);
+        }
+        return (passes & 1) ? 1 : 0;
+    }
     for (int p = 0; p < passes; p++) {
         const int shift = 8 * p;
         hipLaunchKernelGGL(k_hist, dim3(tiles), dim3(kThreads), 0, s, kin, n, shift, hist, tiles, totals + p * kBins);

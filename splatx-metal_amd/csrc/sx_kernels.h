@@ -70,6 +70,9 @@ void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hip
 size_t sort_scratch_bytes(int64_t n);
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n,
                uint32_t key_bits, void* scratch, hipStream_t s);
+// device word in the sort's scratch that a sort of n keys sets non-zero when a tile's look-back
+// gave up (a broken invariant, never expected); read it after the sort
+uint32_t* sort_error_flag(void* scratch, int64_t n);
 
 // offsets[I*n_tiles] from sorted keys; n_isects > 0.
 // key_shift: position of the (image, tile) id in the key (32 for the isect_tiles encoding)
