@@ -30,9 +30,12 @@ import splatx_hip as sh  # noqa: E402
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 
 
-def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, n_passes: int) -> float:
-    """Minimum HBM bytes one launch of `name` must move (per-unit figures stated in DESIGN.md)."""
+def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, shape: dict) -> float:
+    """Minimum HBM bytes one launch of `name` must move (per-unit figures stated in DESIGN.md). shape:
+    depth_passes / tile_passes (radix passes of the depth sort over n keys and of the tile sort over the
+    i intersections) and key_b (bytes of a tile id: 2 up to 2^16 tiles, else 4)."""
     pd = 3 + 4 + 3 + 1 + 3 + (sh_k - 1) * 3  # parameter floats per Gaussian (59 at SH3)
+    kb = shape["key_b"]
     if name == "preprocess":
         # params of every Gaussian (44 B) + SH coefficients of visible ones; writes radii+count (12 B),
         # and for visible ones the 48-B splat record and the zeroed 48-B gradient record
@@ -44,16 +47,22 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, n_p
         return i * (4 + 36) + px * 20.0
     if name == "raster_bwd":
         return i * (4 + 36 + 36) + px * (4 + 4 + 12)
-    if name == "sort":
-        # onesweep: one read of the keys for all digit histograms (8 B), then per pass one read and
-        # one write of (key, value) (24 B)
-        return i * (8.0 + 24.0 * n_passes)
-    if name == "emit":
-        return v * 28.0 + n * 8.0 + i * 12.0
-    if name == "offsets":
-        return i * 8.0 + 4.0 * (px / 256.0)
+    if name == "depth_sort":
+        # keys: tile counts (4 B) and the depths of the visible (4 B) in, (key, index) out (8 B); then the
+        # onesweep sort of n (u32, i32) pairs: one histogram read (4 B), per pass a read and a write (16 B)
+        return n * (4.0 + 8.0) + 4.0 * v + n * (4.0 + 16.0 * shape["depth_passes"])
     if name == "scan":
-        return n * 12.0
+        # tile counts gathered through the depth order: order (4 B) + count (4 B) in, offset (8 B) out
+        return n * 16.0
+    if name == "emit":
+        # order (4 B) and offset (8 B) per position, the 32-B conic/mean record of the visible, and the
+        # (tile id, index) entries out
+        return n * 12.0 + v * 32.0 + i * (kb + 4.0)
+    if name == "sort":
+        # tile sort: one histogram read of the ids, per pass a read and a write of (id, index)
+        return i * (kb + 2.0 * (kb + 4.0) * shape["tile_passes"])
+    if name == "offsets":
+        return 4.0 * (px / 256.0)
     if name == "ssim_fwd":
         return px * 3 * (4 + 4) + (px * 3) * 16.0
     if name == "ssim_bwd_l1":
@@ -232,6 +241,8 @@ def main():
         return ex.make_step_inputs(**dict(base, viewmat=poses[k], **extra), gt_index=k)
 
     steps = [step_inputs(k, count) for k in range(n_poses)]
+    n_tiles = ((sc.width + 15) // 16) * ((sc.height + 15) // 16)
+    tile_bits = int(n_tiles - 1).bit_length()  # the tile id's bits (bits_for_count)
     out = sh.StepOutputs()
     for k in range(args.warmup):
         rc = ex.step_raw(steps[k][0], out)
@@ -257,7 +268,7 @@ def main():
             totals[name] = totals.get(name, 0.0) + ms
         n_isects.append(out.n_isects)
         n_vis.append(out.n_visible)
-        passes.append((out.sort_key_bits + 7) // 8)
+        passes.append(((out.sort_key_bits - tile_bits) + 7) // 8)  # depth sort passes
         losses.append(out.loss)
         if mcmc:  # the refine step of Trainer::step_resident (Trainer.cpp:957-967): refine, then noise
             tr = time.perf_counter()
@@ -273,17 +284,18 @@ def main():
     I, V = float(np.mean(n_isects)), float(np.mean(n_vis))
     px = sc.width * sc.height
     sh_k = (sc.sh_degree + 1) ** 2
-    n_passes = float(np.mean(passes))  # radix passes actually run (depth range compressed into the key)
+    shape = {"depth_passes": float(np.mean(passes)), "tile_passes": (tile_bits + 7) // 8,
+             "key_b": 2 if tile_bits <= 16 else 4}
     kernel_names = [k for k in avg if not k.startswith("host_")]
     per_kernel = {}
     for k in kernel_names:
-        by = algorithmic_bytes(k, sc.n, V, I, px, sh_k, n_passes)
+        by = algorithmic_bytes(k, sc.n, V, I, px, sh_k, shape)
         per_kernel[k] = {"ms": round(avg[k], 4), "alg_GB": round(by / 1e9, 4),
                          "GBps": round(by / 1e9 / (avg[k] / 1e3), 1) if by > 0 and avg[k] > 0 else None}
     dom = max(kernel_names, key=lambda k: avg[k])
-    dom_bytes = algorithmic_bytes(dom, sc.n, V, I, px, sh_k, n_passes)
+    dom_bytes = algorithmic_bytes(dom, sc.n, V, I, px, sh_k, shape)
     achieved = dom_bytes / 1e9 / (avg[dom] / 1e3)
-    step_bytes = sum(algorithmic_bytes(k, sc.n, V, I, px, sh_k, n_passes) for k in kernel_names)
+    step_bytes = sum(algorithmic_bytes(k, sc.n, V, I, px, sh_k, shape) for k in kernel_names)
 
     res = {
         "metric": "train-step ms/iter (fwd+bwd+Adam) at N=1M, 1297x840; % HBM roofline",
@@ -305,7 +317,7 @@ def main():
         "gaussians_per_s": round(sc.n / (ms_per_step / 1e3), 1),
         "mean_n_isects": round(I, 1),
         "mean_visible": round(V, 1),
-        "sort_passes": round(n_passes, 2),
+        "sort_passes": {"depth": round(shape["depth_passes"], 2), "tile": shape["tile_passes"]},
         "final_loss": round(float(losses[-1]), 6),
         "step_alg_GB": round(step_bytes / 1e9, 4),
         "step_hbm_roofline_frac": round(step_bytes / 1e9 / (ms_per_step / 1e3) / HBM_PEAK_GBS, 5),

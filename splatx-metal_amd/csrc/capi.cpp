@@ -369,7 +369,7 @@ int32_t sxh_sort_isect(sxh_backend* b, const sxh_sort_inputs* in, uint64_t* keys
         DevBuf<uint8_t> scratch(sxk::sort_scratch_bytes(in->n));
         const int which = sxk::radix_sort(ka.p, va.p, kb.p, vb.p, in->n, in->key_n_bits, scratch.p, s);
         uint32_t sort_err = 0;
-        SXH_HIP(hipMemcpyAsync(&sort_err, sxk::sort_error_flag(scratch.p, in->n), 4, hipMemcpyDeviceToHost, s));
+        SXH_HIP(hipMemcpyAsync(&sort_err, sxk::sort_error_flag(scratch.p), 4, hipMemcpyDeviceToHost, s));
         SXH_HIP(hipStreamSynchronize(s));
         if (sort_err) throw std::runtime_error("sort_isect: radix sort look-back did not complete");
         SXH_HIP(hipGetLastError());

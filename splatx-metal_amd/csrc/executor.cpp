@@ -62,8 +62,12 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->tiles.alloc(R);
             e->cum.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
-            e->n_vis.alloc(2);
-            e->vis_part.alloc(3 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
+            e->dkey_a.alloc(R);
+            e->dkey_b.alloc(R);
+            e->order_a.alloc(R);
+            e->order_b.alloc(R);
+            e->n_vis.alloc(3);
+            e->vis_part.alloc(4 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
             e->loss_dev.alloc(1);
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
@@ -180,6 +184,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     hipStream_t s = e->b->stream;
     const int W = in->width, H = in->height;
     const int tw = (W + 15) / 16, th = (H + 15) / 16;
+    // per-block tile-count sums of the preprocess are 32-bit: 256 Gaussians x at most tw * th tiles
+    if (static_cast<int64_t>(tw) * th > (int64_t{1} << 23)) invalid(what, "image too large (over 2^23 tiles)");
     const size_t HW = static_cast<size_t>(W) * H;
     const size_t n_px = HW * 3;
     const size_t map_n = use_ssim ? static_cast<size_t>(H - 10) * (W - 10) * 3 : 0;
@@ -219,27 +225,25 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     e->mark("start");
     sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->grads.p, e->vis_part.p, e->n_vis.p, s);
     e->mark("preprocess");
-    sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s);
-    e->mark("scan");
     int64_t* hs = static_cast<int64_t*>(e->host_small.p);
-    SXH_HIP(hipMemcpyAsync(&hs[0], e->cum.p + (c.count - 1), 8, hipMemcpyDeviceToHost, s));
-    SXH_HIP(hipMemcpyAsync(&hs[1], e->n_vis.p, 16, hipMemcpyDeviceToHost, s));  // count, depth-bit range
+    // visible count, depth-bit range, intersection total
+    SXH_HIP(hipMemcpyAsync(&hs[0], e->n_vis.p, 24, hipMemcpyDeviceToHost, s));
     SXH_HIP(hipGetLastError());
     // ---- sync 1: n_isects (MetalBackend.cpp:1849-1858) --------------------------------------------
     auto t0 = std::chrono::steady_clock::now();
     SXH_HIP(hipStreamSynchronize(s));
     e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    const int64_t n_isects = hs[0];
+    const int64_t n_isects = hs[2];
     out->n_isects = n_isects;
     out->sort_key_bits = 0;
-    out->n_visible = hs[1];
+    out->n_visible = hs[0];
     validate_n_isects_readback(n_isects, what);
     e->ensure_isect(static_cast<size_t>(n_isects));
     e->mark("sync1");
-    // sort keys: the depth bits of the visible Gaussians span [lo, hi]; storing depth - lo in just
-    // enough bits keeps the (tile, depth) order and usually saves a radix pass
+    // depth keys: the depth bits of the visible Gaussians span [lo, hi]; storing depth - lo in just
+    // enough bits keeps the order and usually saves a radix pass
     {
-        const uint64_t range = static_cast<uint64_t>(hs[2]);
+        const uint64_t range = static_cast<uint64_t>(hs[1]);
         const uint32_t lo = static_cast<uint32_t>(range), hi = static_cast<uint32_t>(range >> 32);
         c.key_depth_bits = 32;
         c.key_depth_base = 0;
@@ -251,17 +255,40 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     }
 
     // ---- segment B ---------------------------------------------------------------------------------
+    // intersections depth first (the Gaussians sorted by depth, tile ids emitted in that order, a
+    // stable sort on the tile bits): the order of the reference's (tile | depth) key sort
     int32_t* flat = e->vals_a.p;
     if (n_isects > 0) {
-        sxk::step_emit(c, e->splats.p, e->radii.p, e->cum.p, e->keys_a.p, e->vals_a.p, s);
-        e->mark("emit");
         out->sort_key_bits = c.key_depth_bits + c.tile_n_bits;
-        const int which = sxk::radix_sort(e->keys_a.p, e->vals_a.p, e->keys_b.p, e->vals_b.p, n_isects,
-                                          out->sort_key_bits, e->sort_scratch.p, s);
-        e->mark("sort");
-        const uint64_t* keys = which ? e->keys_b.p : e->keys_a.p;
-        flat = which ? e->vals_b.p : e->vals_a.p;
-        sxk::offset_encode(keys, n_isects, 1, tw * th, c.tile_n_bits, e->offsets.p, s, c.key_depth_bits);
+        sxk::step_depth_keys(c, e->splats.p, e->tiles.p, e->dkey_a.p, e->order_a.p, s);
+        const int wd = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, c.count,
+                                       c.key_depth_bits, e->sort_scratch.p, s, true);
+        const int32_t* order = wd ? e->order_b.p : e->order_a.p;
+        e->mark("depth_sort");
+        sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s, order);
+        e->mark("scan");
+        const int n_tiles = tw * th;
+        if (c.tile_n_bits <= 16) {
+            uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
+            uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->vals_a.p, s);
+            e->mark("emit");
+            const int which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_isects, c.tile_n_bits,
+                                              e->sort_scratch.p, s, false);
+            e->mark("sort");
+            flat = which ? e->vals_b.p : e->vals_a.p;
+            sxk::step_tile_offsets(which ? kb : ka, n_isects, n_tiles, e->offsets.p, s);
+        } else {
+            uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
+            uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->vals_a.p, s);
+            e->mark("emit");
+            const int which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_isects, c.tile_n_bits,
+                                              e->sort_scratch.p, s, false);
+            e->mark("sort");
+            flat = which ? e->vals_b.p : e->vals_a.p;
+            sxk::step_tile_offsets(which ? kb : ka, n_isects, n_tiles, e->offsets.p, s);
+        }
         e->mark("offsets");
     } else {
         SXH_HIP(hipMemsetAsync(e->offsets.p, 0, static_cast<size_t>(tw) * th * 4, s));
@@ -320,7 +347,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     uint32_t* hsort = reinterpret_cast<uint32_t*>(&hs[4]);
     *hsort = 0;
     if (n_isects > 0)
-        SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p, n_isects), 4, hipMemcpyDeviceToHost, s));
+        SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p), 4, hipMemcpyDeviceToHost, s));
     if (render_to_dev)
         SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
     if (out->render_colors)

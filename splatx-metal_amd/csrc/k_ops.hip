@@ -310,7 +310,8 @@ __device__ inline int64_t block_exclusive_scan_i64(int64_t v, int64_t* s_wave, i
     return wave_prefix + x - v;
 }
 
-__global__ void __launch_bounds__(kBlock) k_scan_sums(const int32_t* __restrict__ in, int64_t n,
+__global__ void __launch_bounds__(kBlock) k_scan_sums(const int32_t* __restrict__ in,
+                                                      const int32_t* __restrict__ gather, int64_t n,
                                                       int64_t* __restrict__ sums) {
     __shared__ int64_t s_wave[kBlock / 64];
     const int64_t base = blockIdx.x * (int64_t)kScanTile;
@@ -318,14 +319,15 @@ __global__ void __launch_bounds__(kBlock) k_scan_sums(const int32_t* __restrict_
 #pragma unroll
     for (int i = 0; i < kScanItems; i++) {
         const int64_t idx = base + i * kBlock + threadIdx.x;
-        if (idx < n) acc += in[idx];
+        if (idx < n) acc += in[gather ? static_cast<int64_t>(gather[idx]) : idx];
     }
     int64_t tot = 0;
     block_exclusive_scan_i64(acc, s_wave, &tot);
     if (threadIdx.x == 0) sums[blockIdx.x] = tot;
 }
 
-__global__ void __launch_bounds__(kBlock) k_scan_tiles(const int32_t* __restrict__ in, int64_t n,
+__global__ void __launch_bounds__(kBlock) k_scan_tiles(const int32_t* __restrict__ in,
+                                                       const int32_t* __restrict__ gather, int64_t n,
                                                        const int64_t* __restrict__ sums, int64_t* __restrict__ out) {
     __shared__ int64_t s_wave[kBlock / 64];
     __shared__ int64_t s_prefix;
@@ -342,7 +344,7 @@ __global__ void __launch_bounds__(kBlock) k_scan_tiles(const int32_t* __restrict
     int64_t acc = 0;
 #pragma unroll
     for (int i = 0; i < kScanItems; i++) {
-        v[i] = (base + i < n) ? in[base + i] : 0;
+        v[i] = (base + i < n) ? in[gather ? static_cast<int64_t>(gather[base + i]) : base + i] : 0;
         acc += v[i];
     }
     int64_t run = block_exclusive_scan_i64(acc, s_wave, nullptr) + s_prefix;
@@ -496,12 +498,12 @@ void isect_emit(const IsectArgs& a, const int64_t* cum, uint64_t* keys, int32_t*
 
 size_t scan_scratch_bytes(int64_t n) { return sizeof(int64_t) * (size_t)std::max<int64_t>(1, grid_for(n, kScanTile)); }
 
-void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s) {
+void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s, const int32_t* gather) {
     if (n <= 0) return;
     const int nb = grid_for(n, kScanTile);
     int64_t* sums = static_cast<int64_t*>(scratch);
-    hipLaunchKernelGGL(k_scan_sums, dim3(nb), dim3(kBlock), 0, s, in, n, sums);
-    hipLaunchKernelGGL(k_scan_tiles, dim3(nb), dim3(kBlock), 0, s, in, n, sums, out);
+    hipLaunchKernelGGL(k_scan_sums, dim3(nb), dim3(kBlock), 0, s, in, gather, n, sums);
+    hipLaunchKernelGGL(k_scan_tiles, dim3(nb), dim3(kBlock), 0, s, in, gather, n, sums, out);
 }
 
 void offset_encode(const uint64_t* keys, int64_t n, int I, int n_tiles, uint32_t tile_n_bits, int32_t* off,

@@ -1,8 +1,10 @@
-// k_sort.hip — stable LSD radix sort of (u64 key, i32 value) pairs for gfx950.
+// k_sort.hip — stable LSD radix sort of (key, i32 value) pairs for gfx950, keys u64 (the isect
+// keys of sort_isect), u32 (depths) or u16 (tile ids).
 //
 // Contract: KernelBackend.h:130-148 / sort_isect (ascending unsigned key, stable, only bits
-// [0, key_bits) significant). Design: 8-bit digits, so a 45-bit isect key needs 6 passes (the
-// reference's 4-bit digits need 12). Below 2^30 keys the passes run onesweep (see k_os_pass): the
+// [0, key_bits) significant). Design: digits of at most 8 bits, the key bits spread evenly over the
+// fewest passes, so a 45-bit isect key needs 6 passes (the reference's 4-bit digits need 12) and a
+// 13-bit tile id two passes of 7 and 6 bits. Below 2^30 keys the passes run onesweep (see k_os_pass): the
 // digit histograms of all passes come from one read of the keys, and each pass is one launch
 // whose tiles chain their digit prefixes by look-back. The fallback is three launches per pass
 // with no inter-workgroup waiting:
@@ -26,6 +28,13 @@ constexpr int kTile = kThreads * kRounds;  // 4096 keys per workgroup
 constexpr int kBins = 256;
 constexpr int kMaxPassesOs = 8;
 
+// Pass p of a sort on bits [0, key_bits) with digits of `dbits` bits covers bits [p dbits, p dbits +
+// width), the last pass only what is left of key_bits (bits above key_bits never count).
+__host__ __device__ inline uint32_t digit_mask(int p, int dbits, uint32_t key_bits) {
+    const int width = min(dbits, static_cast<int>(key_bits) - p * dbits);
+    return (1u << width) - 1u;
+}
+
 // Lanes of the wave whose 8-bit digit equals this lane's (among lanes where `valid`), from 8 ballots.
 __device__ __forceinline__ uint64_t digit_match(uint32_t digit, bool valid) {
     uint64_t match = __ballot(valid);
@@ -41,7 +50,8 @@ __device__ __forceinline__ uint64_t digit_match(uint32_t digit, bool valid) {
 // Per-tile digit histogram -> hist[digit][tile]; the tile's counts are also added to the pass's
 // digit totals (zeroed by k_zero_totals before the first pass). Equal digits of a wave are counted
 // by one leader lane (match masks), so concentrated digits cost no LDS atomic contention.
-__global__ void __launch_bounds__(kThreads) k_hist(const uint64_t* __restrict__ keys, int64_t n, int shift,
+template <class K>
+__global__ void __launch_bounds__(kThreads) k_hist(const K* __restrict__ keys, int64_t n, int shift, uint32_t mask,
                                                    uint32_t* __restrict__ hist, int n_tiles,
                                                    uint32_t* __restrict__ totals) {
     __shared__ uint32_t h[kBins];
@@ -50,16 +60,16 @@ __global__ void __launch_bounds__(kThreads) k_hist(const uint64_t* __restrict__ 
     const int64_t base = (int64_t)blockIdx.x * kTile;
     const int lane = threadIdx.x & 63;
     const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    uint64_t key[kRounds];
+    K key[kRounds];
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const int64_t idx = base + r * kThreads + threadIdx.x;
-        key[r] = idx < n ? keys[idx] : 0ull;
+        key[r] = idx < n ? keys[idx] : K(0);
     }
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const bool valid = base + r * kThreads + threadIdx.x < n;
-        const uint32_t d = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint32_t d = static_cast<uint32_t>(key[r] >> shift) & mask;
         const uint64_t match = digit_match(d, valid);
         if (valid && (match & lanes_below) == 0) atomicAdd(&h[d], static_cast<uint32_t>(__popcll(match)));
     }
@@ -69,8 +79,10 @@ __global__ void __launch_bounds__(kThreads) k_hist(const uint64_t* __restrict__ 
     if (c) atomicAdd(&totals[threadIdx.x], c);
 }
 
-__global__ void __launch_bounds__(kThreads) k_zero_totals(uint32_t* __restrict__ totals, int n) {
+__global__ void __launch_bounds__(kThreads) k_zero_totals(uint32_t* __restrict__ totals, int n,
+                                                          uint32_t* __restrict__ err) {
     for (int i = threadIdx.x; i < n; i += kThreads) totals[i] = 0;
+    if (err && threadIdx.x == 0) *err = 0u;
 }
 
 __device__ inline uint32_t block_excl_scan_u32(uint32_t v, uint32_t* s_wave, uint32_t* total) {
@@ -132,12 +144,13 @@ __global__ void __launch_bounds__(kThreads) k_scan_digit(uint32_t* __restrict__ 
 // match masks (8 ballots), so within the tile the order is (wave, round, lane) = input order. The
 // tile is reordered by digit in LDS and then written out run by run: consecutive threads store
 // consecutive addresses of one digit's output range.
-__global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict__ kin, const int32_t* __restrict__ vin,
-                                                      uint64_t* __restrict__ kout, int32_t* __restrict__ vout,
-                                                      int64_t n, int shift, const uint32_t* __restrict__ hist,
+template <class K>
+__global__ void __launch_bounds__(kThreads) k_scatter(const K* __restrict__ kin, const int32_t* __restrict__ vin,
+                                                      K* __restrict__ kout, int32_t* __restrict__ vout,
+                                                      int64_t n, int shift, uint32_t mask, const uint32_t* __restrict__ hist,
                                                       int n_tiles) {
     constexpr int kPerWave = kTile / kWaves;  // 1024
-    __shared__ uint64_t s_k[kTile];
+    __shared__ K s_k[kTile];
     __shared__ int32_t s_v[kTile];
     __shared__ uint32_t s_gstart[kBins];  // global start of this tile's run of each digit
     __shared__ uint32_t s_lstart[kBins];  // local (in-tile) start of each digit's run
@@ -151,12 +164,12 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
 #pragma unroll
     for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
     __syncthreads();
-    uint64_t key[kRounds];
+    K key[kRounds];
     int32_t val[kRounds];
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const int i = wave * kPerWave + r * 64 + lane;
-        key[r] = i < tile_n ? kin[base + i] : 0ull;
+        key[r] = i < tile_n ? kin[base + i] : K(0);
         val[r] = i < tile_n ? vin[base + i] : 0;
     }
     // per-wave digit histograms: one leader lane per distinct digit of a round; the ranks among
@@ -167,7 +180,7 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
-        const uint32_t d = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint32_t d = static_cast<uint32_t>(key[r] >> shift) & mask;
         const uint64_t match = digit_match(d, valid);
         rank[r] = static_cast<uint8_t>(__popcll(match & lanes_below));
         cnt[r] = 0;
@@ -201,7 +214,7 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
     for (int r = 0; r < kRounds; r++) {
         if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
         const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
-        const uint32_t digit = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint32_t digit = static_cast<uint32_t>(key[r] >> shift) & mask;
         if (valid) {
             const uint32_t pos = woff[digit] + rank[r];
             s_k[pos] = key[r];
@@ -213,8 +226,8 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const uint64_t* __restrict
     }
     __syncthreads();
     for (int p = tid; p < tile_n; p += kThreads) {
-        const uint64_t k = s_k[p];
-        const uint32_t d = static_cast<uint32_t>((k >> shift) & 0xFF);
+        const K k = s_k[p];
+        const uint32_t d = static_cast<uint32_t>(k >> shift) & mask;
         const uint32_t g = s_gstart[d] + (static_cast<uint32_t>(p) - s_lstart[d]);
         kout[g] = k;
         vout[g] = s_v[p];
@@ -245,30 +258,31 @@ __device__ __forceinline__ void st_status(uint32_t* p, uint32_t v) {
 // the per-pass tile counters. Grid-stride over 4096-key chunks. A wave whose 64 digits agree (the
 // tile bits of neighbouring keys) adds once; otherwise each lane adds 1 (spread digits, few
 // collisions): cheaper than match masks here, where no ranks are needed.
-__global__ void __launch_bounds__(kThreads) k_os_hist(const uint64_t* __restrict__ keys, int64_t n, int passes,
+template <class K>
+__global__ void __launch_bounds__(kThreads) k_os_hist(const K* __restrict__ keys, int64_t n, int passes, int dbits, uint32_t key_bits,
                                                       uint32_t* __restrict__ totals, uint32_t* __restrict__ status0,
                                                       int64_t status_words, uint32_t* __restrict__ counters) {
     __shared__ uint32_t h[kMaxPassesOs][kBins];
     for (int p = 0; p < kMaxPassesOs; p++) h[p][threadIdx.x] = 0;
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < status_words; i += (int64_t)gridDim.x * kThreads)
         status0[i] = 0u;
-    if (blockIdx.x == 0 && threadIdx.x <= kMaxPassesOs) counters[threadIdx.x] = 0u;  // + the error word after them
+    if (blockIdx.x == 0 && threadIdx.x < kMaxPassesOs) counters[threadIdx.x] = 0u;
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int64_t chunks = (n + kTile - 1) / kTile;
     for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
         const int64_t base = c * kTile;
-        uint64_t key[kRounds];  // the whole chunk in flight before any counting
+        K key[kRounds];  // the whole chunk in flight before any counting
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
             const int64_t idx = base + r * kThreads + threadIdx.x;
-            key[r] = idx < n ? keys[idx] : 0ull;
+            key[r] = idx < n ? keys[idx] : K(0);
         }
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
             const bool valid = base + r * kThreads + threadIdx.x < n;
             for (int p = 0; p < passes; p++) {
-                const uint32_t d = static_cast<uint32_t>((key[r] >> (8 * p)) & 0xFF);
+                const uint32_t d = static_cast<uint32_t>(key[r] >> (dbits * p)) & digit_mask(p, dbits, key_bits);
                 const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
                 if (__all(valid && d == d0)) {  // one digit for the whole wave: one add
                     if (lane == 0) atomicAdd(&h[p][d0], 64u);
@@ -295,13 +309,14 @@ __global__ void __launch_bounds__(kThreads) k_os_scan(const uint32_t* __restrict
     }
 }
 
-__global__ void __launch_bounds__(kThreads) k_os_pass(const uint64_t* __restrict__ kin, const int32_t* __restrict__ vin,
-                                                      uint64_t* __restrict__ kout, int32_t* __restrict__ vout,
-                                                      int64_t n, int shift, const uint32_t* __restrict__ digit_base,
+template <class K>
+__global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin, const int32_t* __restrict__ vin,
+                                                      K* __restrict__ kout, int32_t* __restrict__ vout,
+                                                      int64_t n, int shift, uint32_t mask, const uint32_t* __restrict__ digit_base,
                                                       uint32_t* __restrict__ status, uint32_t* __restrict__ status_next,
                                                       uint32_t* __restrict__ counter, uint32_t* __restrict__ err) {
     constexpr int kPerWave = kTile / kWaves;  // 1024
-    __shared__ uint64_t s_k[kTile];
+    __shared__ K s_k[kTile];
     __shared__ int32_t s_v[kTile];
     __shared__ uint32_t s_gstart[kBins];
     __shared__ uint32_t s_lstart[kBins];
@@ -317,12 +332,12 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const uint64_t* __restrict
     const uint32_t tile = s_tile;
     const int64_t base = (int64_t)tile * kTile;
     const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
-    uint64_t key[kRounds];
+    K key[kRounds];
     int32_t val[kRounds];
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const int i = wave * kPerWave + r * 64 + lane;
-        key[r] = i < tile_n ? kin[base + i] : 0ull;
+        key[r] = i < tile_n ? kin[base + i] : K(0);
         val[r] = i < tile_n ? vin[base + i] : 0;
     }
     const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -331,7 +346,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const uint64_t* __restrict
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
-        const uint32_t d = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint32_t d = static_cast<uint32_t>(key[r] >> shift) & mask;
         const uint64_t match = digit_match(d, valid);
         rank[r] = static_cast<uint8_t>(__popcll(match & lanes_below));
         cnt[r] = 0;
@@ -370,7 +385,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const uint64_t* __restrict
     for (int r = 0; r < kRounds; r++) {
         if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
         const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
-        const uint32_t digit = static_cast<uint32_t>((key[r] >> shift) & 0xFF);
+        const uint32_t digit = static_cast<uint32_t>(key[r] >> shift) & mask;
         if (valid) {
             const uint32_t pos = woff[digit] + rank[r];
             s_k[pos] = key[r];
@@ -421,8 +436,8 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const uint64_t* __restrict
     if (status_next) status_next[(size_t)tile * kBins + tid] = 0u;
     __syncthreads();
     for (int p = tid; p < tile_n; p += kThreads) {
-        const uint64_t k = s_k[p];
-        const uint32_t d = static_cast<uint32_t>((k >> shift) & 0xFF);
+        const K k = s_k[p];
+        const uint32_t d = static_cast<uint32_t>(k >> shift) & mask;
         const uint32_t g = s_gstart[d] + (static_cast<uint32_t>(p) - s_lstart[d]);
         if (g < n) {  // always, unless the look-back gave up (err set): then no write lands out of range
             kout[g] = k;
@@ -433,64 +448,91 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const uint64_t* __restrict
 
 int tiles_for(int64_t n) { return static_cast<int>((n + kTile - 1) / kTile); }
 
-} // namespace
-
 constexpr int kMaxPasses = 8;
+// scratch layout: a fixed header (digit totals and bases of up to 8 passes, the per-pass tile
+// counters, the error word) and then two tiles x 256 word buffers (the three-launch path's
+// histogram, or the onesweep status words of alternate passes)
+constexpr int kHeaderWords = 2 * kMaxPasses * kBins + 64;
 
-size_t sort_scratch_bytes(int64_t n) {
-    const int64_t tiles = std::max<int64_t>(1, tiles_for(n));
-    const int64_t hist = tiles * kBins;  // per-pass histogram (three-launch path) or one status buffer (onesweep)
-    // hist/status A, status B, totals [8][256], bases [8][256], counters [8], error word, padding
-    return sizeof(uint32_t) * static_cast<size_t>(2 * hist + 2 * kMaxPasses * kBins + 64);
-}
-
-uint32_t* sort_error_flag(void* scratch, int64_t n) {
-    const int64_t hist_n = (int64_t)std::max(1, tiles_for(n)) * kBins;
-    return static_cast<uint32_t*>(scratch) + 2 * hist_n + 2 * kMaxPasses * kBins + kMaxPasses;
-}
-
-int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-               void* scratch, hipStream_t s) {
-    if (n <= 0 || key_bits == 0) return 0;
-    const int tiles = std::max(1, tiles_for(n));
-    const int passes = static_cast<int>((key_bits + 7) / 8);
-    uint32_t* hist = static_cast<uint32_t*>(scratch);
-    const int64_t hist_n = (int64_t)tiles * kBins;
-    uint32_t* status_b = hist + hist_n;
-    uint32_t* totals = status_b + hist_n;
+template <class K>
+int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
+                 void* scratch, bool clear_err, hipStream_t s) {
+    uint32_t* totals = static_cast<uint32_t*>(scratch);
     uint32_t* bases = totals + kMaxPasses * kBins;
     uint32_t* counters = bases + kMaxPasses * kBins;
-    uint32_t* err = counters + kMaxPasses;  // zeroed with the counters by k_os_hist
-    uint64_t* kin = keys_a;
+    uint32_t* err = counters + kMaxPasses;
+    key_bits = std::min<uint32_t>(key_bits, 8 * sizeof(K));
+    // fewest 8-bit-or-narrower passes, the bits spread evenly over them: a 13-bit tile id sorts as 7 + 6
+    // bits (longer runs per digit in each tile's writes than 8 + 5)
+    const int passes = static_cast<int>((key_bits + 7) / 8);
+    const int dbits = passes ? static_cast<int>((key_bits + passes - 1) / passes) : 0;
+    if (n <= 0 || passes == 0) {
+        if (clear_err) hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, 0, err);
+        return 0;
+    }
+    const int tiles = std::max(1, tiles_for(n));
+    const int64_t hist_n = (int64_t)tiles * kBins;
+    uint32_t* hist = totals + kHeaderWords;
+    uint32_t* status_b = hist + hist_n;
+    K* kin = keys_a;
     int32_t* vin = vals_a;
-    uint64_t* kout = keys_b;
+    K* kout = keys_b;
     int32_t* vout = vals_b;
-    hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins);
+    hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins,
+                       clear_err ? err : nullptr);
     if (n < (int64_t{1} << 30)) {  // onesweep: counts and prefixes fit the 30-bit status words
         const int hist_blocks = std::min(tiles, 2048);
-        hipLaunchKernelGGL(k_os_hist, dim3(hist_blocks), dim3(kThreads), 0, s, kin, n, passes, totals, hist, hist_n,
-                           counters);
+        hipLaunchKernelGGL(k_os_hist<K>, dim3(hist_blocks), dim3(kThreads), 0, s, kin, n, passes, dbits, key_bits,
+                           totals, hist, hist_n, counters);
         hipLaunchKernelGGL(k_os_scan, dim3(1), dim3(kThreads), 0, s, totals, passes, bases);
         uint32_t* st[2] = {hist, status_b};
         for (int p = 0; p < passes; p++) {
             uint32_t* next = p + 1 < passes ? st[(p + 1) & 1] : nullptr;
-            hipLaunchKernelGGL(k_os_pass, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, 8 * p,
-                               bases + p * kBins, st[p & 1], next, counters + p, err);
+            hipLaunchKernelGGL(k_os_pass<K>, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, dbits * p,
+                               digit_mask(p, dbits, key_bits), bases + p * kBins, st[p & 1], next, counters + p, err);
             std::swap(kin, kout);
             std::swap(vin, vout);
         }
         return (passes & 1) ? 1 : 0;
     }
     for (int p = 0; p < passes; p++) {
-        const int shift = 8 * p;
-        hipLaunchKernelGGL(k_hist, dim3(tiles), dim3(kThreads), 0, s, kin, n, shift, hist, tiles, totals + p * kBins);
+        const int shift = dbits * p;
+        const uint32_t mask = digit_mask(p, dbits, key_bits);
+        hipLaunchKernelGGL(k_hist<K>, dim3(tiles), dim3(kThreads), 0, s, kin, n, shift, mask, hist, tiles,
+                           totals + p * kBins);
         hipLaunchKernelGGL(k_scan_digit, dim3(kBins), dim3(kThreads), 0, s, hist, tiles, totals + p * kBins);
-        hipLaunchKernelGGL(k_scatter, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, hist,
-                           tiles);
+        hipLaunchKernelGGL(k_scatter<K>, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, mask,
+                           hist, tiles);
         std::swap(kin, kout);
         std::swap(vin, vout);
     }
     return (passes & 1) ? 1 : 0;
+}
+
+} // namespace
+
+size_t sort_scratch_bytes(int64_t n) {
+    const int64_t tiles = std::max<int64_t>(1, tiles_for(n));
+    return sizeof(uint32_t) * static_cast<size_t>(kHeaderWords + 2 * tiles * kBins);
+}
+
+uint32_t* sort_error_flag(void* scratch) {
+    return static_cast<uint32_t*>(scratch) + 2 * kMaxPasses * kBins + kMaxPasses;
+}
+
+int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
+               void* scratch, hipStream_t s, bool clear_err) {
+    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s);
+}
+
+int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
+               void* scratch, hipStream_t s, bool clear_err) {
+    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s);
+}
+
+int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
+               void* scratch, hipStream_t s, bool clear_err) {
+    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s);
 }
 
 } // namespace sxk

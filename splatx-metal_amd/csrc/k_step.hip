@@ -55,8 +55,9 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
                                                        float4* __restrict__ grads,
                                                        uint32_t* __restrict__ vis_part) {
-    __shared__ uint32_t s_vis[kBlock / 64], s_dmin[kBlock / 64], s_dmax[kBlock / 64];
+    __shared__ uint32_t s_vis[kBlock / 64], s_dmin[kBlock / 64], s_dmax[kBlock / 64], s_isect[kBlock / 64];
     uint32_t dbits_min = 0xFFFFFFFFu, dbits_max = 0u;
+    uint32_t n_tiles_sum = 0;  // this lane's tile count; summed per block below
     const int i = blockIdx.x * kBlock + threadIdx.x;
     bool vis = false;
     if (i < c.count) {
@@ -117,6 +118,7 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
             splats[3 * (size_t)i + 2] = make_float4(0.f, 0.f, 0.f, __uint_as_float(0u));
         }
         tiles[i] = cnt;
+        n_tiles_sum = static_cast<uint32_t>(cnt);
     }
     // visible count and depth-bit range per block (plain stores; a single global counter would
     // serialize every wave)
@@ -125,47 +127,54 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
     for (int o = 32; o > 0; o >>= 1) {
         dbits_min = min(dbits_min, static_cast<uint32_t>(__shfl_xor(static_cast<int>(dbits_min), o, 64)));
         dbits_max = max(dbits_max, static_cast<uint32_t>(__shfl_xor(static_cast<int>(dbits_max), o, 64)));
+        n_tiles_sum += static_cast<uint32_t>(__shfl_xor(static_cast<int>(n_tiles_sum), o, 64));
     }
     if (sxd::lane_id() == 0) {
         s_vis[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal));
         s_dmin[threadIdx.x >> 6] = dbits_min;
         s_dmax[threadIdx.x >> 6] = dbits_max;
+        s_isect[threadIdx.x >> 6] = n_tiles_sum;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t t = 0, lo = 0xFFFFFFFFu, hi = 0u;
+        uint32_t t = 0, lo = 0xFFFFFFFFu, hi = 0u, isect = 0u;
 #pragma unroll
         for (int w = 0; w < kBlock / 64; w++) {
             t += s_vis[w];
             lo = min(lo, s_dmin[w]);
             hi = max(hi, s_dmax[w]);
+            isect += s_isect[w];
         }
-        vis_part[3 * blockIdx.x] = t;
-        vis_part[3 * blockIdx.x + 1] = lo;
-        vis_part[3 * blockIdx.x + 2] = hi;
+        vis_part[4 * blockIdx.x] = t;
+        vis_part[4 * blockIdx.x + 1] = lo;
+        vis_part[4 * blockIdx.x + 2] = hi;
+        vis_part[4 * blockIdx.x + 3] = isect;
     }
 }
 
-// sum of the per-block visible counts and the overall depth-bit range (one block); out = {u64 count,
-// u32 min, u32 max}
+// sum of the per-block visible counts, the overall depth-bit range and the intersection total (one
+// block); out = {u64 visible count, u32 min | u32 max << 32, u64 intersections}
 __global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict__ part, int n,
                                                       unsigned long long* __restrict__ out) {
-    __shared__ unsigned long long s_red[kBlock];
+    __shared__ unsigned long long s_red[kBlock], s_isect[kBlock];
     __shared__ uint32_t s_lo[kBlock], s_hi[kBlock];
-    unsigned long long acc = 0;
+    unsigned long long acc = 0, isect = 0;
     uint32_t lo = 0xFFFFFFFFu, hi = 0u;
     for (int k = threadIdx.x; k < n; k += kBlock) {
-        acc += part[3 * k];
-        lo = min(lo, part[3 * k + 1]);
-        hi = max(hi, part[3 * k + 2]);
+        acc += part[4 * k];
+        lo = min(lo, part[4 * k + 1]);
+        hi = max(hi, part[4 * k + 2]);
+        isect += part[4 * k + 3];
     }
     s_red[threadIdx.x] = acc;
+    s_isect[threadIdx.x] = isect;
     s_lo[threadIdx.x] = lo;
     s_hi[threadIdx.x] = hi;
     __syncthreads();
     for (int o = kBlock / 2; o > 0; o >>= 1) {
         if (threadIdx.x < o) {
             s_red[threadIdx.x] += s_red[threadIdx.x + o];
+            s_isect[threadIdx.x] += s_isect[threadIdx.x + o];
             s_lo[threadIdx.x] = min(s_lo[threadIdx.x], s_lo[threadIdx.x + o]);
             s_hi[threadIdx.x] = max(s_hi[threadIdx.x], s_hi[threadIdx.x + o]);
         }
@@ -174,33 +183,196 @@ __global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict
     if (threadIdx.x == 0) {
         out[0] = s_red[0];
         out[1] = (static_cast<unsigned long long>(s_hi[0]) << 32) | s_lo[0];
+        out[2] = s_isect[0];
     }
 }
 
-__global__ void __launch_bounds__(kBlock) k_emit(StepConst c, const float4* __restrict__ splats,
-                                                 const int32_t* __restrict__ radii, const int64_t* __restrict__ cum,
-                                                 uint64_t* __restrict__ keys, int32_t* __restrict__ vals) {
+// Depth-first intersection order. The reference's (tile << depth_bits | depth) keys, sorted stably
+// over emit order (Gaussian index, then the Gaussian's own tile order), put each tile's entries in
+// (depth, index) order. Here the Gaussians that emit are sorted stably by depth once (a few million
+// 32-bit keys), then emit only their tile ids in that order, and a stable sort on the tile bits
+// alone finishes the job: within a tile the order is the depth order, ties by index — the same
+// permutation, for two radix passes over the intersections instead of five or six.
+
+// depth sort keys: depth bits - key_depth_base for Gaussians with tiles, 0 for the rest (which
+// emit nothing, so their place in the order does not matter); values = Gaussian index
+__global__ void __launch_bounds__(kBlock) k_depth_keys(StepConst c, const float4* __restrict__ splats,
+                                                       const int32_t* __restrict__ tiles,
+                                                       uint32_t* __restrict__ keys, int32_t* __restrict__ vals) {
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= c.count) return;
-    if (!(radii[2 * i] > 0 && radii[2 * i + 1] > 0)) return;
-    const float4 s0 = splats[3 * (size_t)i];
-    const float4 s1 = splats[3 * (size_t)i + 1];
-    const uint64_t depth_enc = static_cast<uint64_t>(__float_as_uint(s0.w) - c.key_depth_base);
-    int64_t cur = i == 0 ? 0 : cum[i - 1];
-    auto emit = [&](int32_t tile) {
-        keys[cur] = (static_cast<uint64_t>(static_cast<uint32_t>(tile)) << c.key_depth_bits) | depth_enc;
-        vals[cur] = i;
-        ++cur;
-    };
-    if (c.accutile) {
-        sxd::accutile<true>(s1.x, s1.y, s1.z, s0.z, s0.x, s0.y, 16.0f, c.tile_width, c.tile_height, emit);
-    } else {
-        const sxd::TileRect r = sxd::aabb_rect(s0.x, s0.y, static_cast<float>(radii[2 * i]),
-                                               static_cast<float>(radii[2 * i + 1]), 16.0f, c.tile_width,
-                                               c.tile_height);
-        for (int32_t y = r.min_y; y < r.max_y; y++)
-            for (int32_t x = r.min_x; x < r.max_x; x++) emit(y * c.tile_width + x);
+    keys[i] = tiles[i] > 0 ? __float_as_uint(splats[3 * (size_t)i].w) - c.key_depth_base : 0u;
+    vals[i] = i;
+}
+
+// Thread per position j of the depth order: Gaussian g = order[j] owns the output range
+// [cum[j-1], cum[j]) and fills it with its tile ids in the reference's emit order, value g. Tile
+// counts are heavy-tailed, so a Gaussian with few tiles writes them from its own lane, and the
+// others are taken one at a time by the whole wave: lane l evaluates line u0 + l of the sweep (its
+// cuts are a function of the line alone; the sweep's carried state is rebuilt with shuffles), a
+// wave scan of the line lengths places the lines, and lane e then writes entry e — consecutive
+// lanes on consecutive addresses, with no lane waiting on the longest Gaussian of its wave.
+constexpr int kEmitLaneMax = 64;  // tiles a Gaussian may have to be emitted by its own lane
+
+__device__ __forceinline__ float2 shfl_f2(sxd::F2 v, int src) {
+    return make_float2(__shfl(v.x, src, 64), __shfl(v.y, src, 64));
+}
+
+// The lanes of the wave hold lines u0 + lane (vmin, len; len 0 past the end). Writes the lines'
+// tiles at out0 + [0, total) and returns total; nothing at or past `end` (the Gaussian's range, which
+// the counts fix) is written. s_start, s_vmin: 64 ints each of this wave's LDS.
+template <class K>
+__device__ __forceinline__ int64_t wave_emit_lines(int u0, int vmin, int len, bool row_major, int tw, int g,
+                                                   int64_t out0, int64_t end, K* __restrict__ keys,
+                                                   int32_t* __restrict__ vals, int* s_start, int* s_vmin) {
+    const int lane = threadIdx.x & 63;
+    int incl = len;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
     }
+    const int total = __shfl(incl, 63, 64);
+    s_start[lane] = incl - len;
+    s_vmin[lane] = vmin;
+    __builtin_amdgcn_wave_barrier();
+    const int n = static_cast<int>(min<int64_t>(total, end - out0));
+    for (int e = lane; e < n; e += 64) {
+        int l = 0;  // the last line starting at or before e (lines of length 0 share the next start)
+#pragma unroll
+        for (int step = 32; step > 0; step >>= 1)
+            if (s_start[l + step] <= e) l += step;
+        const int u = u0 + l;
+        const int v = s_vmin[l] + (e - s_start[l]);
+        keys[out0 + e] = static_cast<K>(row_major ? u * tw + v : v * tw + u);
+        vals[out0 + e] = g;
+    }
+    __builtin_amdgcn_wave_barrier();  // every lane has read s_start before the next chunk writes it
+    return total;
+}
+
+template <class K>
+__global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float4* __restrict__ splats,
+                                                        const int32_t* __restrict__ radii,
+                                                        const int32_t* __restrict__ order,
+                                                        const int64_t* __restrict__ cum, K* __restrict__ keys,
+                                                        int32_t* __restrict__ vals) {
+    __shared__ int s_start[kBlock / 64][64];
+    __shared__ int s_vmin[kBlock / 64][64];
+    const int j = blockIdx.x * kBlock + threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tw = c.tile_width;
+    int64_t my0 = 0, cnt = 0;
+    int g = 0;
+    float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
+    int32_t rx = 0, ry = 0;
+    if (j < c.count) {
+        my0 = j == 0 ? 0 : cum[j - 1];
+        cnt = cum[j] - my0;
+        if (cnt > 0) {
+            g = order[j];
+            s0 = splats[3 * (size_t)g];
+            if (c.accutile) {
+                s1 = splats[3 * (size_t)g + 1];
+            } else {
+                rx = radii[2 * g];
+                ry = radii[2 * g + 1];
+            }
+        }
+    }
+    if (cnt > 0 && cnt <= kEmitLaneMax) {
+        int64_t cur = my0;
+        auto line = [&](int32_t u, int32_t vmin, int32_t vmax, bool row_major) {
+            for (int32_t v = vmin; v < vmax; ++v) {
+                keys[cur] = static_cast<K>(row_major ? u * tw + v : v * tw + u);
+                vals[cur] = g;
+                ++cur;
+            }
+            return true;
+        };
+        if (c.accutile) {
+            sxd::accutile_lines(s1.x, s1.y, s1.z, s0.z, s0.x, s0.y, 16.0f, tw, c.tile_height, line);
+        } else {
+            const sxd::TileRect r = sxd::aabb_rect(s0.x, s0.y, static_cast<float>(rx), static_cast<float>(ry), 16.0f,
+                                                   tw, c.tile_height);
+            for (int32_t y = r.min_y; y < r.max_y; y++) line(y, r.min_x, r.max_x, true);
+        }
+    }
+    uint64_t pending = __ballot(cnt > kEmitLaneMax);
+    while (pending) {
+        const int src = static_cast<int>(__builtin_ctzll(pending));
+        pending &= pending - 1;
+        const int gg = __shfl(g, src, 64);
+        int64_t out0 = static_cast<int64_t>(
+            (static_cast<uint64_t>(static_cast<uint32_t>(__shfl(static_cast<int>(my0 >> 32), src, 64))) << 32) |
+            static_cast<uint32_t>(__shfl(static_cast<int>(my0), src, 64)));
+        const int64_t end = out0 + static_cast<int64_t>(__shfl(static_cast<int>(cnt), src, 64));
+        // the Gaussian's projected values from the lane that loaded them
+        const float mx = __shfl(s0.x, src, 64), my = __shfl(s0.y, src, 64);
+        if (c.accutile) {
+            const float op = __shfl(s0.z, src, 64);
+            const float ca = __shfl(s1.x, src, 64), cb = __shfl(s1.y, src, 64), cc = __shfl(s1.z, src, 64);
+            sxd::AccuSweep sw;
+            if (!sxd::accutile_setup(ca, cb, cc, op, mx, my, 16.0f, tw, c.tile_height, sw)) continue;
+            const float ts = 16.0f;
+            const float first_edge = sw.rect_min_x * ts;
+            const sxd::F2 start = sxd::accutile_start(sw);
+            sxd::F2 carry = start;  // upper cut of the line before the chunk
+            for (int u0 = sw.rect_min_x; u0 < sw.rect_max_x; u0 += 64) {
+                const int u = u0 + lane;
+                const bool valid = u < sw.rect_max_x;
+                // line u spans [u ts, (u + 1) ts): the sweep's running sums of ts are exact integers
+                const float min_line = static_cast<float>(u) * ts;
+                const float max_line = min_line + ts;
+                const bool cut = valid && max_line <= sw.bbox_max.x;  // true on a prefix of the lanes
+                sxd::F2 own = {0.f, 0.f};
+                if (cut) own = sxd::accutile_cut(sw, max_line);
+                const int n_cut = __popcll(__ballot(cut));
+                sxd::F2 imax_line = carry;
+                if (n_cut > 0) {
+                    const float2 last = shfl_f2(own, n_cut - 1);
+                    imax_line = {last.x, last.y};
+                }
+                if (cut) imax_line = own;
+                const float2 up = make_float2(__shfl_up(imax_line.x, 1, 64), __shfl_up(imax_line.y, 1, 64));
+                sxd::F2 imin_line = {up.x, up.y};
+                if (lane == 0) {
+                    if (u0 == sw.rect_min_x)
+                        imin_line = sw.bbox_min.x <= first_edge ? sxd::accutile_cut(sw, first_edge) : start;
+                    else imin_line = carry;
+                }
+                int32_t vmin = 0, vmax = 0;
+                if (valid) sxd::accutile_span(sw, min_line, max_line, imin_line, imax_line, ts, vmin, vmax);
+                const float2 c63 = shfl_f2(imax_line, 63);
+                carry = {c63.x, c63.y};
+                const int len = vmax > vmin ? vmax - vmin : 0;
+                out0 += wave_emit_lines(u0, vmin, len, sw.isY, tw, gg, out0, end, keys, vals, s_start[wave], s_vmin[wave]);
+            }
+        } else {
+            const float frx = static_cast<float>(__shfl(rx, src, 64)), fry = static_cast<float>(__shfl(ry, src, 64));
+            const sxd::TileRect r = sxd::aabb_rect(mx, my, frx, fry, 16.0f, tw, c.tile_height);
+            for (int y0 = r.min_y; y0 < r.max_y; y0 += 64) {
+                const int len = y0 + lane < r.max_y ? r.max_x - r.min_x : 0;
+                out0 += wave_emit_lines(y0, r.min_x, len, true, tw, gg, out0, end, keys, vals, s_start[wave], s_vmin[wave]);
+            }
+        }
+    }
+}
+
+// offsets[t] = first position of tile t in the sorted tile ids (lower bound; n for trailing empty
+// tiles) — the isect_offset_encode contract for one image
+template <class K>
+__global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ keys, int64_t n, int n_tiles,
+                                                         int32_t* __restrict__ off) {
+    const int t = blockIdx.x * kBlock + threadIdx.x;
+    if (t >= n_tiles) return;
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = lo + ((hi - lo) >> 1);
+        if (static_cast<int>(keys[mid]) < t) lo = mid + 1;
+        else hi = mid;
+    }
+    off[t] = static_cast<int32_t>(lo);
 }
 
 // NC = the arena's SH coefficient count (1, 4, 9 or 16), a compile-time bound so that the SH basis and
@@ -447,10 +619,36 @@ void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t
 
 int step_preprocess_blocks(int64_t count) { return grid_for(count); }
 
-void step_emit(const StepConst& c, const float4* splats, const int32_t* radii, const int64_t* cum, uint64_t* keys,
-               int32_t* vals, hipStream_t s) {
+void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* tiles, uint32_t* keys, int32_t* vals,
+                     hipStream_t s) {
     if (c.count <= 0) return;
-    hipLaunchKernelGGL(k_emit, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, cum, keys, vals);
+    hipLaunchKernelGGL(k_depth_keys, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, tiles, keys, vals);
+}
+
+void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
+                      const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s) {
+    if (c.count <= 0) return;
+    hipLaunchKernelGGL(k_emit_sorted<uint16_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
+                       cum, keys, vals);
+}
+
+void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
+                      const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s) {
+    if (c.count <= 0) return;
+    hipLaunchKernelGGL(k_emit_sorted<uint32_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
+                       cum, keys, vals);
+}
+
+void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s) {
+    if (n_tiles <= 0) return;
+    hipLaunchKernelGGL(k_tile_offsets<uint16_t>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles,
+                       offsets);
+}
+
+void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s) {
+    if (n_tiles <= 0) return;
+    hipLaunchKernelGGL(k_tile_offsets<uint32_t>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles,
+                       offsets);
 }
 
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads, hipStream_t s) {

@@ -424,16 +424,26 @@ SX_DEV F2 ellipse_intersection(float A, float B, float C, float disc, float t, F
     return r;
 }
 
-// AccuTile for one Gaussian. Returns the tile count; calls emit(tile_id) in emit order when
-// EMIT is true.
-template <bool EMIT, class Emit>
-SX_DEV uint32_t accutile(float A, float B, float C, float opacity, float mean_x, float mean_y, float ts,
-                         int32_t tw, int32_t th, Emit emit) {
-    const float disc = B * B - A * C;
-    const float t = __builtin_fminf(sx::kGaussianExtend * sx::kGaussianExtend,
-                                    2.0f * sxm::logf_(opacity / sx::kAlphaThreshold));
-    if (t <= 0.f) return 0;
-    const float neg_t_over_disc = -t / disc;
+// AccuTile sweep state of one Gaussian after SNUGBOX and the line/column swap: lines u in
+// [rect_min_x, rect_max_x), each a run of tiles v in [vmin, vmax) of the other axis.
+struct AccuSweep {
+    float A, B, C, disc, t;
+    F2 p, bbox_min, bbox_max, bbox_argmin, bbox_argmax;
+    int32_t rect_min_x, rect_min_y, rect_max_x, rect_max_y;
+    bool isY;
+};
+
+// false when the Gaussian covers no tile
+SX_DEV bool accutile_setup(float A, float B, float C, float opacity, float mean_x, float mean_y, float ts,
+                           int32_t tw, int32_t th, AccuSweep& s) {
+    s.A = A;
+    s.B = B;
+    s.C = C;
+    s.disc = B * B - A * C;
+    s.t = __builtin_fminf(sx::kGaussianExtend * sx::kGaussianExtend,
+                          2.0f * sxm::logf_(opacity / sx::kAlphaThreshold));
+    if (s.t <= 0.f) return false;
+    const float neg_t_over_disc = -s.t / s.disc;
     const float x_extent = __builtin_sqrtf(neg_t_over_disc * C);
     const float y_extent = __builtin_sqrtf(neg_t_over_disc * A);
     F2 bbox_min = {mean_x - x_extent, mean_y - y_extent};
@@ -448,10 +458,10 @@ SX_DEV uint32_t accutile(float A, float B, float C, float opacity, float mean_x,
     int32_t rect_max_y = imax(0, imin(th, sxm::f2i_trunc(bbox_max.y / ts + 1.f)));
     const int32_t y_span = rect_max_y - rect_min_y;
     const int32_t x_span = rect_max_x - rect_min_x;
-    if (y_span * x_span == 0) return 0;
-    const bool isY = y_span < x_span;
-    const F2 p = {mean_x, mean_y};
-    if (isY) {
+    if (y_span * x_span == 0) return false;
+    s.isY = y_span < x_span;
+    s.p = {mean_x, mean_y};
+    if (s.isY) {
         int32_t tmp = rect_min_x; rect_min_x = rect_min_y; rect_min_y = tmp;
         tmp = rect_max_x; rect_max_x = rect_max_y; rect_max_y = tmp;
         bbox_min = {bbox_min.y, bbox_min.x};
@@ -459,30 +469,78 @@ SX_DEV uint32_t accutile(float A, float B, float C, float opacity, float mean_x,
         bbox_argmin = {bbox_argmin.y, bbox_argmin.x};
         bbox_argmax = {bbox_argmax.y, bbox_argmax.x};
     }
+    s.bbox_min = bbox_min;
+    s.bbox_max = bbox_max;
+    s.bbox_argmin = bbox_argmin;
+    s.bbox_argmax = bbox_argmax;
+    s.rect_min_x = rect_min_x;
+    s.rect_min_y = rect_min_y;
+    s.rect_max_x = rect_max_x;
+    s.rect_max_y = rect_max_y;
+    return true;
+}
+
+SX_DEV F2 accutile_cut(const AccuSweep& s, float coord) {
+    return ellipse_intersection(s.A, s.B, s.C, s.disc, s.t, s.p, s.isY, coord);
+}
+
+// The tile run of the line [min_line, max_line) given the ellipse cuts at its two edges.
+SX_DEV void accutile_span(const AccuSweep& s, float min_line, float max_line, F2 imin_line, F2 imax_line, float ts,
+                          int32_t& vmin, int32_t& vmax) {
+    float emin, emax;
+    if (min_line <= s.bbox_argmin.y && s.bbox_argmin.y < max_line) emin = s.bbox_min.y;
+    else emin = __builtin_fminf(imin_line.x, imax_line.x);
+    if (min_line <= s.bbox_argmax.y && s.bbox_argmax.y < max_line) emax = s.bbox_max.y;
+    else emax = __builtin_fmaxf(imin_line.y, imax_line.y);
+    vmin = imax(s.rect_min_y, imin(s.rect_max_y, sxm::f2i_trunc(emin / ts)));
+    vmax = imin(s.rect_max_y, imax(s.rect_min_y, sxm::f2i_trunc(emax / ts + 1.f)));
+}
+
+// The sweep's cut state, stated per line (lines can then be evaluated independently): line u spans
+// [u ts, (u + 1) ts) (exact in float), its upper cut is the ellipse cut at (u + 1) ts while that edge
+// is <= bbox_max.x and otherwise the last such cut (the start value {bbox_max.y, bbox_min.y} if there
+// was none), and its lower cut is the previous line's upper cut — for the first line the cut at its
+// own edge when bbox_min.x <= that edge, else the start value.
+SX_DEV F2 accutile_start(const AccuSweep& s) { return F2{s.bbox_max.y, s.bbox_min.y}; }
+
+// AccuTile for one Gaussian as a sweep over lines: calls line(u, vmin, vmax, isY) for every line u
+// of the sweep in order, the line's tiles being v in [vmin, vmax) with tile id u * tw + v when isY,
+// else v * tw + u (the reference's emit order). line returns false to end the sweep early.
+template <class Line>
+SX_DEV void accutile_lines(float A, float B, float C, float opacity, float mean_x, float mean_y, float ts,
+                           int32_t tw, int32_t th, Line line) {
+    AccuSweep s;
+    if (!accutile_setup(A, B, C, opacity, mean_x, mean_y, ts, tw, th, s)) return;
     const float BLOCK = ts;
-    uint32_t count = 0;
     F2 imin_line, imax_line;
-    imax_line = {bbox_max.y, bbox_min.y};
-    float min_line = rect_min_x * BLOCK;
-    if (bbox_min.x <= min_line) imin_line = ellipse_intersection(A, B, C, disc, t, p, isY, min_line);
+    imax_line = accutile_start(s);
+    float min_line = s.rect_min_x * BLOCK;
+    if (s.bbox_min.x <= min_line) imin_line = accutile_cut(s, min_line);
     else imin_line = imax_line;
-    for (int32_t u = rect_min_x; u < rect_max_x; ++u) {
+    for (int32_t u = s.rect_min_x; u < s.rect_max_x; ++u) {
         const float max_line = min_line + BLOCK;
-        if (max_line <= bbox_max.x) imax_line = ellipse_intersection(A, B, C, disc, t, p, isY, max_line);
-        float emin, emax;
-        if (min_line <= bbox_argmin.y && bbox_argmin.y < max_line) emin = bbox_min.y;
-        else emin = __builtin_fminf(imin_line.x, imax_line.x);
-        if (min_line <= bbox_argmax.y && bbox_argmax.y < max_line) emax = bbox_max.y;
-        else emax = __builtin_fmaxf(imin_line.y, imax_line.y);
-        const int32_t vmin = imax(rect_min_y, imin(rect_max_y, sxm::f2i_trunc(emin / BLOCK)));
-        const int32_t vmax = imin(rect_max_y, imax(rect_min_y, sxm::f2i_trunc(emax / BLOCK + 1.f)));
+        if (max_line <= s.bbox_max.x) imax_line = accutile_cut(s, max_line);
+        int32_t vmin, vmax;
+        accutile_span(s, min_line, max_line, imin_line, imax_line, BLOCK, vmin, vmax);
+        if (!line(u, vmin, vmax, s.isY)) return;
+        imin_line = imax_line;
+        min_line = max_line;
+    }
+}
+
+// AccuTile for one Gaussian. Returns the tile count; calls emit(tile_id) in emit order when
+// EMIT is true.
+template <bool EMIT, class Emit>
+SX_DEV uint32_t accutile(float A, float B, float C, float opacity, float mean_x, float mean_y, float ts,
+                         int32_t tw, int32_t th, Emit emit) {
+    uint32_t count = 0;
+    accutile_lines(A, B, C, opacity, mean_x, mean_y, ts, tw, th, [&](int32_t u, int32_t vmin, int32_t vmax, bool isY) {
         if (EMIT) {
             for (int32_t v = vmin; v < vmax; ++v) emit(isY ? u * tw + v : v * tw + u);
         }
         if (vmax > vmin) count += static_cast<uint32_t>(vmax - vmin);
-        imin_line = imax_line;
-        min_line = max_line;
-    }
+        return true;
+    });
     return count;
 }
 

@@ -41,6 +41,8 @@ struct sxh_executor {
     sxh::DevBuf<float4> splats, grads;
     sxh::DevBuf<int32_t> radii, tiles;
     sxh::DevBuf<int64_t> cum;
+    sxh::DevBuf<uint32_t> dkey_a, dkey_b;    // depth sort keys
+    sxh::DevBuf<int32_t> order_a, order_b;   // Gaussian indices in depth order
     sxh::DevBuf<uint8_t> scan_scratch;
     sxh::DevBuf<unsigned long long> n_vis;
     sxh::DevBuf<uint32_t> vis_part;
@@ -100,7 +102,8 @@ struct sxh_executor {
         keys_b.alloc(cap);
         vals_a.alloc(cap);
         vals_b.alloc(cap);
-        sort_scratch.alloc(sxk::sort_scratch_bytes(static_cast<int64_t>(cap)));
+        // shared by the depth sort (rows keys) and the tile sort (intersections)
+        sort_scratch.alloc(sxk::sort_scratch_bytes(static_cast<int64_t>(std::max<size_t>(cap, rows))));
         isect_cap = cap;
     }
 

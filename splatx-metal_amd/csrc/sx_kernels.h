@@ -61,18 +61,26 @@ struct IsectArgs {
 void isect_count(const IsectArgs& a, int32_t* tiles_per_gauss, hipStream_t s);
 void isect_emit(const IsectArgs& a, const int64_t* cum, uint64_t* keys, int32_t* vals, hipStream_t s);
 
-// inclusive int32 -> int64 scan; scratch needs scan_scratch_bytes(n) bytes.
+// inclusive int32 -> int64 scan; scratch needs scan_scratch_bytes(n) bytes. With `gather` the
+// scanned sequence is in[gather[0]], in[gather[1]], ...
 size_t scan_scratch_bytes(int64_t n);
-void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s);
+void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s,
+                  const int32_t* gather = nullptr);
 
-// Stable LSD radix sort of (u64 key, i32 value) on bits [0, key_bits). Result lands in
-// keys_a/vals_a when the pass count is even, else in keys_b/vals_b; returns 0 or 1 accordingly.
+// Stable LSD radix sort of (key, i32 value) on bits [0, key_bits), keys u64, u32 or u16. Result
+// lands in keys_a/vals_a when the pass count is even, else in keys_b/vals_b; returns 0 or 1
+// accordingly. The scratch needs sort_scratch_bytes(n) bytes for n keys.
 size_t sort_scratch_bytes(int64_t n);
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n,
-               uint32_t key_bits, void* scratch, hipStream_t s);
-// device word in the sort's scratch that a sort of n keys sets non-zero when a tile's look-back
-// gave up (a broken invariant, never expected); read it after the sort
-uint32_t* sort_error_flag(void* scratch, int64_t n);
+               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true);
+int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
+               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true);
+int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
+               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true);
+// device word in the sort's scratch that a sort sets non-zero when a tile's look-back gave up (a
+// broken invariant, never expected). A sort with clear_err zeroes it first; one without adds to
+// what the sorts before it left, so several sorts in a row can be checked with one read.
+uint32_t* sort_error_flag(void* scratch);
 
 // offsets[I*n_tiles] from sorted keys; n_isects > 0.
 // key_shift: position of the (image, tile) id in the key (32 for the isect_tiles encoding)
