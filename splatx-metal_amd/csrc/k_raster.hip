@@ -233,6 +233,10 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     __shared__ float4 s_rgb[kThreads];
     __shared__ int32_t s_id[kThreads];
     __shared__ float4 s_part4[NV * kThreads / 4];  // per-tile sums [k][t], the four waves add into it
+    __shared__ uint8_t s_list[4][kThreads];
+    __shared__ int s_wc[4][4];
+    __shared__ int s_len[4];
+    __shared__ int32_t s_wbf[4];  // each wave's last contributing intersection
     float* s_part = reinterpret_cast<float*>(s_part4);
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
@@ -240,7 +244,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     if (a.masks && a.masks[(size_t)img * n_tiles + tile] == 0) return;  // uniform
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
+    const int lane = tid & 63, wave = tid >> 6;
     const int px_i = tx * 16 + (tid & 15), py_i = ty * 16 + (tid >> 4);
     const bool inside = px_i < a.width && py_i < a.height;
     const size_t pix = inside ? (size_t)img * a.height * a.width + (size_t)py_i * a.width + px_i
@@ -259,126 +263,108 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     const float bg_dot = bg ? (bg[0] * vc0 + bg[1] * vc1 + bg[2] * vc2) : 0.f;
     const float tva = T_final * (va - bg_dot);  // the alpha and background terms of every v_alpha, over ra
     const int32_t wave_bin_final = sxd::wave_max_i(bin_final);
-    const int32_t num = range_end - range_start;
+    if (lane == 0) s_wbf[wave] = wave_bin_final;
+    __syncthreads();
+    // the walk starts at the tile's last contributing intersection: everything behind it (most of
+    // a dense tile's list, once its pixels saturate) has no pixel to contribute to
+    const int32_t tile_end = min(range_end, max(max(s_wbf[0], s_wbf[1]), max(s_wbf[2], s_wbf[3])) + 1);
+    const int32_t num = max(0, tile_end - range_start);
     const int num_batches = (num + kThreads - 1) / kThreads;
     // row r of a wave_sum4 result belongs to slot A=0, C=2, B=1, D=3 for r = 0..3
     const int row = lane >> 4;
     const int row_slot = row == 0 ? 0 : row == 1 ? 2 : row == 2 ? 1 : 3;
     for (int b = 0; b < num_batches; b++) {
         __syncthreads();
-        const int32_t batch_end = range_end - 1 - kThreads * b;
+        const int32_t batch_end = tile_end - 1 - kThreads * b;
         const int32_t batch_size = min(kThreads, batch_end + 1 - range_start);
         const int32_t idx = batch_end - tid;
+        uint32_t wm = 0u;
         if (idx >= range_start) {
             const int32_t gid = a.flatten_ids[idx];
             s_id[tid] = gid;
             float4 xyo = a.splats[(size_t)gid * 3];
             xyo.w = sigma_cutoff(xyo.z);
+            const float4 con = a.splats[(size_t)gid * 3 + 1];
             s_xyo[tid] = xyo;
-            s_con[tid] = a.splats[(size_t)gid * 3 + 1];
+            s_con[tid] = con;
             s_rgb[tid] = a.splats[(size_t)gid * 3 + 2];
+            // waves whose rows the cutoff set can reach, less those whose every pixel stopped before it
+            wm = wave_rows_mask(xyo, con, ty * 16);
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+                if (idx > s_wbf[w]) wm &= ~(1u << w);
         }
 #pragma unroll
         for (int j = tid; j < NV * kThreads / 4; j += kThreads) s_part4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        __syncthreads();
+        build_wave_lists(wm, s_list, s_wc, s_len);
 
-        // A candidate: the first batch-local Gaussian at or after t with a lane of this wave inside
-        // its sigma cutoff and before the lane's last contributor (t is wave-uniform), with this
-        // lane's offsets, sigma and the Gaussian's record kept for its gradient.
-        struct Cand {
-            int t;
-            bool valid;
-            float dx, dy, sigma;
-            float4 xyo, con;
-        };
-        auto next_active = [&](int t, Cand& q) {
-            for (; t < batch_size; t++) {
-                q.xyo = s_xyo[t];
-                q.con = s_con[t];
-                q.dx = q.xyo.x - px;
-                q.dy = q.xyo.y - py;
-                q.sigma = sigma_of(q.con.x, q.con.y, q.con.z, q.dx, q.dy);
-                q.valid = inside && (batch_end - t) <= bin_final && !(q.sigma > q.xyo.w);
-                if (__any(q.valid)) break;
+        // This wave's Gaussians back to front, four at a time: the four pairs' exponentials are
+        // independent, only T and the back-sum run through them in order. A pair that does not
+        // contribute (or a slot past the list) gets alpha = 0, so T (times 1/(1 - 0) = 1), the
+        // back-sum and every gradient term are left unchanged / zero.
+        const int len = s_len[wave];
+        const uint8_t* list = s_list[wave];
+        for (int j = 0; j < len; j += 4) {
+            int ts[4];
+            float gv[4][NV];
+            float alpha[4], vis[4], dxs[4], dys[4];
+            float4 con[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                ts[k] = j + k < len ? static_cast<int>(list[j + k]) : -1;
+                const int t = ts[k] < 0 ? 0 : ts[k];
+                const float4 xyo = s_xyo[t];
+                con[k] = s_con[t];
+                const float dx = xyo.x - px, dy = xyo.y - py;
+                const float sigma = sigma_of(con[k].x, con[k].y, con[k].z, dx, dy);
+                const bool valid = ts[k] >= 0 && inside && (batch_end - t) <= bin_final && !(sigma > xyo.w);
+                const float vis_raw = exp_neg(sigma, xyo.w);
+                const float oa = xyo.z * vis_raw;
+                const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
+                const bool ok = valid && !(sigma < 0.f || alpha_raw < sx::kAlphaThreshold);
+                alpha[k] = ok ? alpha_raw : 0.0f;
+                vis[k] = (ok && oa <= sx::kMaxAlpha) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
+                dxs[k] = dx;
+                dys[k] = dy;
+                gv[k][2] = xyo.z;  // opacity, replaced by its gradient below
             }
-            q.t = t;
-        };
-        // this lane's gradient terms for the candidate, without branches: a pair that does not
-        // contribute gets alpha = 0, so T (times 1/(1 - 0) = 1), the back-sums and every term are
-        // left unchanged / zero
-        auto grads_of = [&](const Cand& q, float* gv) {
-            const float opac = q.xyo.z;
-            const float vis_raw = exp_neg(q.sigma, q.xyo.w);
-            const float oa = opac * vis_raw;
-            const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
-            const bool ok = q.valid && !(q.sigma < 0.f || alpha_raw < sx::kAlphaThreshold);
-            const float alpha = ok ? alpha_raw : 0.0f;
-            // hardware reciprocal (1 ulp; exact for 1): the backward is compared at a relative
-            // tolerance, and an IEEE division costs ~10 instructions per pair
-            const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - alpha));
-            T *= ra;
-            const float fac = alpha * T;
-            const float4 c = s_rgb[q.t];
-            gv[6] = fac * vc0;
-            gv[7] = fac * vc1;
-            gv[8] = fac * vc2;
-            // v_alpha = sum_c (c_c T - b_c ra) vc_c + T_final ra (va - <bg, vc>), with the back-sum kept
-            // as its dot product with v_render
-            const float cvc = c.x * vc0 + c.y * vc1 + c.z * vc2;
-            const float v_alpha = T * cvc + ra * (tva - bdot);
-            const float vis = (ok && oa <= sx::kMaxAlpha) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
-            const float v_sigma = -opac * vis * v_alpha;
-            const float dx = q.dx, dy = q.dy;
-            gv[3] = 0.5f * v_sigma * dx * dx;
-            gv[4] = v_sigma * dx * dy;
-            gv[5] = 0.5f * v_sigma * dy * dy;
-            gv[0] = v_sigma * (q.con.x * dx + q.con.y * dy);
-            gv[1] = v_sigma * (q.con.y * dx + q.con.z * dy);
-            if (ABSGRAD) {
-                gv[9] = fabsf(gv[0]);
-                gv[10] = fabsf(gv[1]);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                // hardware reciprocal (1 ulp; exact for 1): the backward is compared at a relative
+                // tolerance, and an IEEE division costs ~10 instructions per pair
+                const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - alpha[k]));
+                T *= ra;
+                const float fac = alpha[k] * T;
+                const float4 c = s_rgb[ts[k] < 0 ? 0 : ts[k]];
+                gv[k][6] = fac * vc0;
+                gv[k][7] = fac * vc1;
+                gv[k][8] = fac * vc2;
+                // v_alpha = sum_c (c_c T - b_c ra) vc_c + T_final ra (va - <bg, vc>), with the back-sum
+                // kept as its dot product with v_render
+                const float cvc = c.x * vc0 + c.y * vc1 + c.z * vc2;
+                const float v_alpha = T * cvc + ra * (tva - bdot);
+                const float v_sigma = -gv[k][2] * vis[k] * v_alpha;
+                const float dx = dxs[k], dy = dys[k];
+                gv[k][3] = 0.5f * v_sigma * dx * dx;
+                gv[k][4] = v_sigma * dx * dy;
+                gv[k][5] = 0.5f * v_sigma * dy * dy;
+                gv[k][0] = v_sigma * (con[k].x * dx + con[k].y * dy);
+                gv[k][1] = v_sigma * (con[k].y * dx + con[k].z * dy);
+                if (ABSGRAD) {
+                    gv[k][9] = fabsf(gv[k][0]);
+                    gv[k][10] = fabsf(gv[k][1]);
+                }
+                gv[k][2] = vis[k] * v_alpha;
+                bdot += fac * cvc;
             }
-            gv[2] = vis * v_alpha;
-            bdot += fac * cvc;
-        };
-
-        int t = max(0, batch_end - wave_bin_final);
-        while (true) {
-            // up to four contributing Gaussians, in order, then one transposed reduction for all four
-            float gA[NV], gB[NV], gC[NV], gD[NV];
-            Cand q;
-            next_active(t, q);
-            const int tA = q.t;
-            if (tA >= batch_size) break;
-            grads_of(q, gA);
-            next_active(tA + 1, q);
-            const int tB = q.t;
-            if (tB < batch_size) grads_of(q, gB);
-            else
-#pragma unroll
-                for (int k = 0; k < NV; k++) gB[k] = 0.f;
-            if (tB < batch_size) next_active(tB + 1, q);
-            const int tC = tB < batch_size ? q.t : batch_size;
-            if (tC < batch_size) grads_of(q, gC);
-            else
-#pragma unroll
-                for (int k = 0; k < NV; k++) gC[k] = 0.f;
-            if (tC < batch_size) next_active(tC + 1, q);
-            const int tD = tC < batch_size ? q.t : batch_size;
-            if (tD < batch_size) grads_of(q, gD);
-            else
-#pragma unroll
-                for (int k = 0; k < NV; k++) gD[k] = 0.f;
-            const int t_row = row_slot == 0 ? tA : row_slot == 1 ? tB : row_slot == 2 ? tC : tD;
-            const bool writer = (lane & 15) == 0 && t_row < batch_size;
-            float* dst = s_part + t_row;
+            const int t_row = ts[row_slot];
+            const bool writer = (lane & 15) == 0 && t_row >= 0;
+            float* dst = s_part + (t_row < 0 ? 0 : t_row);
 #pragma unroll
             for (int k = 0; k < NV; k++) {
-                const float v = wave_sum4(gA[k], gB[k], gC[k], gD[k]);
+                const float v = wave_sum4(gv[0][k], gv[1][k], gv[2][k], gv[3][k]);
                 if (writer) atomicAdd(&dst[k * kThreads], v);  // LDS add: the four waves of the tile
             }
-            if (tD >= batch_size) break;
-            t = tD + 1;
         }
         __syncthreads();
         // one thread per Gaussian of the batch: one global atomic per gradient component
