@@ -23,11 +23,9 @@ namespace {
 constexpr int kThreads = 256;
 
 // sxm::expf_fast(-sigma) without its range branches: identical for sigma in [0, 86] (no overflow,
-// no subnormal scaling); `cut` is the Gaussian's sigma cutoff, wave-uniform, and only an opacity
-// above ~1e35 pushes it past that range, in which case the general function is used.
-__device__ __forceinline__ float exp_neg(float sigma, float cut) {
-    const float cut_u = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cut)));  // uniform branch
-    if (__builtin_expect(cut_u > 86.0f, 0)) return sxm::expf_fast(-sigma);
+// no subnormal scaling). exp_neg: `cut` is the Gaussian's sigma cutoff, wave-uniform, and only an
+// opacity above ~1e35 pushes it past that range, in which case the general function is used.
+__device__ __forceinline__ float exp_neg_poly(float sigma) {
     const float x = -sigma;
     const float kf = __builtin_rintf(x * 1.44269502f);
     float r = __builtin_fmaf(kf, -0.693145751953125f, x);
@@ -43,6 +41,12 @@ __device__ __forceinline__ float exp_neg(float sigma, float cut) {
     p = __builtin_fmaf(p, r, 1.0f);
     const int k = static_cast<int>(kf);
     return p * __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
+}
+
+__device__ __forceinline__ float exp_neg(float sigma, float cut) {
+    const float cut_u = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cut)));  // uniform branch
+    if (__builtin_expect(cut_u > 86.0f, 0)) return sxm::expf_fast(-sigma);
+    return exp_neg_poly(sigma);
 }
 
 __device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx, float dy) {
@@ -233,7 +237,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     __shared__ float4 s_rgb[kThreads];
     __shared__ int32_t s_id[kThreads];
     __shared__ float4 s_part4[NV * kThreads / 4];  // per-tile sums [k][t], the four waves add into it
-    __shared__ uint8_t s_list[4][kThreads];
+    __shared__ __align__(16) uint8_t s_list[4][kThreads];
     __shared__ int s_wc[4][4];
     __shared__ int s_len[4];
     __shared__ int32_t s_wbf[4];  // each wave's last contributing intersection
@@ -298,35 +302,78 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
         for (int j = tid; j < NV * kThreads / 4; j += kThreads) s_part4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         build_wave_lists(wm, s_list, s_wc, s_len);
 
-        // This wave's Gaussians back to front, four at a time: the four pairs' exponentials are
-        // independent, only T and the back-sum run through them in order. A pair that does not
-        // contribute (or a slot past the list) gets alpha = 0, so T (times 1/(1 - 0) = 1), the
-        // back-sum and every gradient term are left unchanged / zero.
+        // This wave's Gaussians back to front, four at a time: the four list entries come in one
+        // LDS read and their records in one burst, the four pairs' exponentials are independent,
+        // only T and the back-sum run through them in order. A pair that does not contribute (or a
+        // slot past the list) gets alpha = 0, so T (times 1/(1 - 0) = 1), the back-sum and every
+        // gradient term are left unchanged / zero.
         const int len = s_len[wave];
-        const uint8_t* list = s_list[wave];
+        const uint32_t* list4 = reinterpret_cast<const uint32_t*>(s_list[wave]);
         for (int j = 0; j < len; j += 4) {
-            int ts[4];
-            float gv[4][NV];
-            float alpha[4], vis[4], dxs[4], dys[4];
-            float4 con[4];
+            const uint32_t packed = list4[j >> 2];
+            int ts[4], tc[4];
+            float4 xyo[4], con[4], rgb[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                ts[k] = j + k < len ? static_cast<int>(list[j + k]) : -1;
-                const int t = ts[k] < 0 ? 0 : ts[k];
-                const float4 xyo = s_xyo[t];
-                con[k] = s_con[t];
-                const float dx = xyo.x - px, dy = xyo.y - py;
-                const float sigma = sigma_of(con[k].x, con[k].y, con[k].z, dx, dy);
-                const bool valid = ts[k] >= 0 && inside && (batch_end - t) <= bin_final && !(sigma > xyo.w);
-                const float vis_raw = exp_neg(sigma, xyo.w);
-                const float oa = xyo.z * vis_raw;
+                ts[k] = j + k < len ? static_cast<int>((packed >> (8 * k)) & 0xFFu) : -1;
+                tc[k] = ts[k] < 0 ? 0 : ts[k];
+                xyo[k] = s_xyo[tc[k]];
+                con[k] = s_con[tc[k]];
+                rgb[k] = s_rgb[tc[k]];
+            }
+            // one wave-uniform choice of exponential for the chunk: the branch-free polynomial unless
+            // some cutoff exceeds its range (opacity above ~1e35)
+            const float cmax = sxd::smax(sxd::smax(xyo[0].w, xyo[1].w), sxd::smax(xyo[2].w, xyo[3].w));
+            const bool general = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cmax))) > 86.0f;
+            float gv[4][NV];
+            float alpha[4], vis[4], dxs[4], dys[4], sig[4], e[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                dxs[k] = xyo[k].x - px;
+                dys[k] = xyo[k].y - py;
+                sig[k] = sigma_of(con[k].x, con[k].y, con[k].z, dxs[k], dys[k]);
+            }
+            bool valid[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                valid[k] = ts[k] >= 0 && inside && (batch_end - tc[k]) <= bin_final && !(sig[k] > xyo[k].w);
+            // The exponential's value only enters gradients (compared at a relative tolerance), so the
+            // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
+            // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at
+            // least 1/255, and opacity * exp at most the 0.99 clamp — must be the forward's. Where a lane
+            // lies within 2^-16 (1 + sigma) of either boundary (over 50 times that error), the chunk
+            // takes the forward's exponential instead.
+            bool exact = general;
+            if (!exact) {
+                bool near = false;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    e[k] = __builtin_amdgcn_exp2f(-sig[k] * 1.44269504f);
+                    const float oa = xyo[k].z * e[k];
+                    const float band = 0x1p-16f * (1.0f + sig[k]);
+                    near |= valid[k] && (__builtin_fabsf(oa * 255.0f - 1.0f) < band ||
+                                         __builtin_fabsf(oa - sx::kMaxAlpha) < band);
+                }
+                exact = __any(near);
+            }
+            if (__builtin_expect(exact, 0)) {
+                if (general) {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) e[k] = sxm::expf_fast(-sig[k]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) e[k] = exp_neg_poly(sig[k]);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float sigma = sig[k];
+                const float vis_raw = e[k];
+                const float oa = xyo[k].z * vis_raw;
                 const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
-                const bool ok = valid && !(sigma < 0.f || alpha_raw < sx::kAlphaThreshold);
+                const bool ok = valid[k] && !(sigma < 0.f || alpha_raw < sx::kAlphaThreshold);
                 alpha[k] = ok ? alpha_raw : 0.0f;
                 vis[k] = (ok && oa <= sx::kMaxAlpha) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
-                dxs[k] = dx;
-                dys[k] = dy;
-                gv[k][2] = xyo.z;  // opacity, replaced by its gradient below
             }
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -335,27 +382,27 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
                 const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - alpha[k]));
                 T *= ra;
                 const float fac = alpha[k] * T;
-                const float4 c = s_rgb[ts[k] < 0 ? 0 : ts[k]];
                 gv[k][6] = fac * vc0;
                 gv[k][7] = fac * vc1;
                 gv[k][8] = fac * vc2;
                 // v_alpha = sum_c (c_c T - b_c ra) vc_c + T_final ra (va - <bg, vc>), with the back-sum
-                // kept as its dot product with v_render
-                const float cvc = c.x * vc0 + c.y * vc1 + c.z * vc2;
-                const float v_alpha = T * cvc + ra * (tva - bdot);
-                const float v_sigma = -gv[k][2] * vis[k] * v_alpha;
+                // kept as its dot product with v_render (fused multiply-adds: gradient algebra only)
+                const float cvc = __builtin_fmaf(rgb[k].x, vc0, __builtin_fmaf(rgb[k].y, vc1, rgb[k].z * vc2));
+                const float v_alpha = __builtin_fmaf(T, cvc, ra * (tva - bdot));
+                const float v_sigma = -xyo[k].z * vis[k] * v_alpha;
                 const float dx = dxs[k], dy = dys[k];
-                gv[k][3] = 0.5f * v_sigma * dx * dx;
-                gv[k][4] = v_sigma * dx * dy;
-                gv[k][5] = 0.5f * v_sigma * dy * dy;
-                gv[k][0] = v_sigma * (con[k].x * dx + con[k].y * dy);
-                gv[k][1] = v_sigma * (con[k].y * dx + con[k].z * dy);
+                const float vdx = v_sigma * dx, vdy = v_sigma * dy;
+                gv[k][3] = 0.5f * vdx * dx;
+                gv[k][4] = vdx * dy;
+                gv[k][5] = 0.5f * vdy * dy;
+                gv[k][0] = __builtin_fmaf(con[k].x, vdx, con[k].y * vdy);
+                gv[k][1] = __builtin_fmaf(con[k].y, vdx, con[k].z * vdy);
                 if (ABSGRAD) {
                     gv[k][9] = fabsf(gv[k][0]);
                     gv[k][10] = fabsf(gv[k][1]);
                 }
                 gv[k][2] = vis[k] * v_alpha;
-                bdot += fac * cvc;
+                bdot = __builtin_fmaf(fac, cvc, bdot);
             }
             const int t_row = ts[row_slot];
             const bool writer = (lane & 15) == 0 && t_row >= 0;
