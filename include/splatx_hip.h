@@ -499,6 +499,133 @@ int32_t sxh_render_session_frame(sxh_render_session* s, const float* viewmat, fl
                                  int32_t width, int32_t height, uint8_t* out_rgba /* [height*width*4] */);
 void sxh_render_session_close(sxh_render_session* s);
 
+/* ------------------------------------------------------------------------------------------ */
+/* The caller loop: the training loop of sx_train_run_ex (TrainC.cpp:743-906) over           */
+/* Trainer::step_resident (Trainer.cpp:916-969), every GT image resident in the executor's   */
+/* GT cache. Per iteration it: uses camera it % n_cameras (TrainC.cpp:785); takes the         */
+/* schedules means_lr_at / sh_degree_at (Trainer.cpp:496-508) and the regularization weights */
+/* (:933-940); injects noise with Philox offset = it unless a refine is due (:942-950); runs */
+/* the MCMC refine when Trainer::mcmc_refine_due (:1261-1271) holds, on the device           */
+/* (sxh_exec_mcmc_refine, noise after it over the new count, :957-967); evaluates, saves a   */
+/* checkpoint, writes the live PLY and calls the snapshot and progress callbacks at the step */
+/* boundary in the reference's order (TrainC.cpp:820-905).                                    */
+/* ------------------------------------------------------------------------------------------ */
+
+/* TrainingCamera (Trainer.h) with its image's slot in the GT cache. */
+typedef struct {
+    float viewmat[16];       /* world->camera, row-major */
+    float K[9];
+    int32_t width, height;   /* must be the GT cache's image size */
+    int32_t gt_index;        /* its image in the GT cache (sxh_exec_set_gt_cache) */
+} sxh_train_camera;
+
+/* The TrainConfig (Trainer.h:206-243) and McmcOptions (Trainer.h:186-198) fields the loop reads;
+ * sxh_train_schedule_defaults fills the reference's defaults. */
+typedef struct {
+    int32_t total_iters;
+    float scene_scale;
+    float lr_means, lr_quats, lr_scales, lr_opacities, lr_sh0, lr_shN;
+    float sh_degree_interval_ratio;
+    float opacity_reg, scale_reg;
+    uint8_t mcmc_enabled;
+    int64_t cap_max;         /* <= arena_rows */
+    float min_opacity;
+    float refine_start_ratio, refine_stop_ratio, refine_every_ratio;
+    float noise_lr;
+    uint64_t mcmc_seed;      /* the Philox noise key (the generator state comes in `rng`) */
+} sxh_train_schedule;
+int32_t sxh_train_schedule_defaults(sxh_train_schedule* out);
+
+/* One iteration's step arguments under the schedule, as Trainer::step_resident forms them
+ * (Trainer.cpp:920-952): means_lr_at and sh_degree_at (:496-508), the regularization weights
+ * over the live count, Trainer::mcmc_refine_due (:1261-1271). Host only; the loop uses it. */
+typedef struct {
+    uint32_t degrees_to_use;
+    float lr[6];
+    float opacity_reg_w, scale_reg_w;
+    uint8_t refine_due;      /* the MCMC refine runs after this iteration's step */
+    uint8_t inject_noise;    /* MCMC on and no refine due: the step injects the noise */
+    float noise_scale;       /* means_lr_at(iter) * noise_lr (also the refine's noise) */
+} sxh_train_plan;
+int32_t sxh_train_plan_at(const sxh_train_schedule* s, int32_t iter, int32_t sh_degree, int64_t count,
+                          sxh_train_plan* out);
+
+/* SxTrainProgress (splatx_train_c.h:185-195), plus the tick's refine (TrainC.cpp:804-810). */
+typedef struct {
+    int32_t iter;            /* completed iterations, this step included */
+    int32_t run_until, total_iters;
+    float loss;
+    float psnr;              /* mean PSNR of the eval views if an eval ran on this tick, else NaN */
+    double step_ms;          /* the step, and the refine when one ran */
+    int64_t n_isects;
+    int64_t splat_count;     /* live rows after this tick */
+    int32_t thermal_state;   /* 0: no thermal governor here */
+    int32_t mcmc_refined;
+    int64_t n_relocated, n_added;
+} sxh_train_progress;
+typedef void (*sxh_train_progress_fn)(const sxh_train_progress* p, void* user);
+
+/* SxSplatSnapshot (splatx_train_c.h:236-246): the filtered rows (filter_cloud_for_export,
+ * min opacity 0.005) in the raw domain, valid only during the callback. */
+typedef struct {
+    int32_t iter, sh_degree;
+    int64_t count;
+    const float* means;      /* [count,3] */
+    const float* quats;      /* [count,4] */
+    const float* scales;     /* [count,3] log */
+    const float* opacities;  /* [count] logit */
+    const float* sh0;        /* [count,3] */
+    const float* shN;        /* [count,K,3]; NULL at degree 0 */
+} sxh_splat_snapshot;
+typedef void (*sxh_snapshot_fn)(const sxh_splat_snapshot* s, void* user);
+
+typedef struct {
+    const sxh_train_camera* cameras;  /* the train split in order */
+    int32_t n_cameras;
+    const sxh_train_camera* eval_cameras;  /* the test split (NULL when n_eval_cameras is 0) */
+    int32_t n_eval_cameras;
+    int32_t eval_every;      /* eval after iteration it when (it + 1) % eval_every == 0; 0: never */
+    int32_t start_iter, run_until;
+    int64_t count;           /* live rows at start_iter */
+    sxh_train_schedule sched;
+    const float* binoms;     /* MCMC: the relocation LUT [n_max * n_max] (sxh_make_binoms_lut) */
+    int32_t n_max;
+    sxh_mt64_state* rng;     /* MCMC: the multinomial generator, advanced in place */
+    /* seeded pose jitter (0: none): iteration it composes a rotation by at most jitter_max_deg
+     * about a random axis and a translation of length at most jitter_max_t, drawn from
+     * (jitter_seed, it), with the camera's view (the config-3 workload's per-step jitter) */
+    float jitter_max_deg, jitter_max_t;
+    uint64_t jitter_seed;
+    sxh_train_progress_fn progress;  /* may be NULL */
+    void* progress_user;
+    sxh_snapshot_fn snapshot;        /* with snapshot_every > 0 */
+    void* snapshot_user;
+    int32_t snapshot_every;
+    int32_t live_ply_every;          /* (it + 1) % every == 0: write live_ply_path via "<path>.tmp" */
+    const char* live_ply_path;
+    int32_t checkpoint_every;        /* (it + 1) % every == 0 and it + 1 < run_until */
+    const char* checkpoint_path;
+    const sxh_checkpoint_config* checkpoint_config;
+    uint8_t checkpoint_fp16;
+} sxh_train_loop_args;
+
+typedef struct {
+    int32_t completed_iters; /* the next iteration to run (SxTrainStats.completed_iters) */
+    int64_t count;           /* live rows at the end */
+    float first_loss, last_loss;
+    float last_eval_psnr;    /* NaN when no eval ran */
+    double train_seconds;
+    int32_t stopped;         /* 1 when sxh_exec_request_stop ended the loop early */
+} sxh_train_loop_result;
+
+/* Live PLY, snapshot and eval failures warn on stderr and training continues (TrainC.cpp:840-889);
+ * a step, refine or checkpoint failure ends the loop with its error (out->completed_iters says
+ * where). Callbacks run synchronously on the calling thread and must not re-enter the loop. */
+int32_t sxh_exec_train_loop(sxh_executor* e, const sxh_train_loop_args* a, sxh_train_loop_result* out);
+/* sx_train_request_stop: from any thread (a callback included); the loop ends at the next step
+ * boundary with stopped = 1. A new sxh_exec_train_loop call clears the request. */
+int32_t sxh_exec_request_stop(sxh_executor* e);
+
 /* Per-kernel timing of the last step (HIP events on the executor's stream), enabled by
  * sxh_exec_set_profiling(e, 1). Names are stable strings; times are milliseconds. */
 typedef struct {

@@ -60,7 +60,15 @@ class HipTrainCase(C.Structure):
                 ("resident", C.c_uint8), ("mcmc", C.c_uint8), ("cap_max", C.c_int64), ("seed", C.c_uint64),
                 ("refine_start_ratio", C.c_float), ("refine_stop_ratio", C.c_float),
                 ("refine_every_ratio", C.c_float), ("out_params", sh.fp * 6), ("losses", sh.fp),
-                ("n_isects", sh.i64p), ("render0", sh.fp), ("out_count", C.c_int64), ("n_refined", C.c_int32)]
+                ("n_isects", sh.i64p), ("render0", sh.fp), ("out_count", C.c_int64), ("n_refined", C.c_int32),
+                ("n_cams", C.c_int32), ("viewmats", sh.fp), ("Ks", sh.fp), ("gts", sh.fp), ("start_iter", C.c_int32),
+                ("scene_scale", C.c_float), ("sh_degree_interval_ratio", C.c_float)]
+
+
+class RefSchedule(C.Structure):
+    _fields_ = [("total_iters", C.c_int32), ("scene_scale", C.c_float), ("lr_means", C.c_float),
+                ("sh_degree_interval_ratio", C.c_float), ("mcmc_enabled", C.c_uint8), ("refine_start_ratio", C.c_float),
+                ("refine_stop_ratio", C.c_float), ("refine_every_ratio", C.c_float)]
 
 
 class RefCloudIn(C.Structure):
@@ -99,6 +107,29 @@ class Oracle(sh.Ops):
         out = np.zeros(n_max * n_max, np.float32)
         self._call("make_binoms_lut", n_max, sh.ptr(out))
         return out
+
+    TRAIN_DEFAULT_FIELDS = ("total_iters", "scene_scale", "lr_means", "lr_quats", "lr_scales", "lr_opacities", "lr_sh0",
+                            "lr_shN", "sh_degree_interval_ratio", "opacity_reg", "scale_reg", "cap_max",
+                            "min_opacity", "refine_start_ratio", "refine_stop_ratio", "refine_every_ratio",
+                            "noise_lr", "mcmc_seed")
+
+    def train_defaults(self) -> dict:
+        """TrainConfig / McmcOptions defaults of the reference's Trainer.h."""
+        out = np.zeros(18, np.float64)
+        self._call("train_defaults", out.ctypes.data_as(C.POINTER(C.c_double)))
+        return dict(zip(self.TRAIN_DEFAULT_FIELDS, out.tolist()))
+
+    def train_plans(self, total_iters, scene_scale, lr_means, sh_degree_interval_ratio, mcmc_enabled,
+                    refine_start_ratio, refine_stop_ratio, refine_every_ratio, sh_degree, iters):
+        """means_lr_at, sh_degree_at and Trainer::mcmc_refine_due of the reference for `iters`."""
+        s = RefSchedule(total_iters, scene_scale, lr_means, sh_degree_interval_ratio, int(bool(mcmc_enabled)),
+                        refine_start_ratio, refine_stop_ratio, refine_every_ratio)
+        it = np.ascontiguousarray(iters, np.int32)
+        lr0 = np.zeros(it.size, np.float32)
+        deg = np.zeros(it.size, np.uint32)
+        due = np.zeros(it.size, np.uint8)
+        self._call("train_plans", C.byref(s), sh_degree, it.size, sh.ptr(it), sh.ptr(lr0), sh.ptr(deg), sh.ptr(due))
+        return lr0, deg, due
 
     def quat_scale_to_covar(self, quats, scales):
         q, s = sh.f32(quats), sh.f32(scales)
@@ -221,6 +252,29 @@ class Reference(sh.Ops):
         out = np.zeros(n_max * n_max, np.float32)
         self._call("make_binoms_lut", n_max, sh.ptr(out))
         return out
+
+    TRAIN_DEFAULT_FIELDS = ("total_iters", "scene_scale", "lr_means", "lr_quats", "lr_scales", "lr_opacities", "lr_sh0",
+                            "lr_shN", "sh_degree_interval_ratio", "opacity_reg", "scale_reg", "cap_max",
+                            "min_opacity", "refine_start_ratio", "refine_stop_ratio", "refine_every_ratio",
+                            "noise_lr", "mcmc_seed")
+
+    def train_defaults(self) -> dict:
+        """TrainConfig / McmcOptions defaults of the reference's Trainer.h."""
+        out = np.zeros(18, np.float64)
+        self._call("train_defaults", out.ctypes.data_as(C.POINTER(C.c_double)))
+        return dict(zip(self.TRAIN_DEFAULT_FIELDS, out.tolist()))
+
+    def train_plans(self, total_iters, scene_scale, lr_means, sh_degree_interval_ratio, mcmc_enabled,
+                    refine_start_ratio, refine_stop_ratio, refine_every_ratio, sh_degree, iters):
+        """means_lr_at, sh_degree_at and Trainer::mcmc_refine_due of the reference for `iters`."""
+        s = RefSchedule(total_iters, scene_scale, lr_means, sh_degree_interval_ratio, int(bool(mcmc_enabled)),
+                        refine_start_ratio, refine_stop_ratio, refine_every_ratio)
+        it = np.ascontiguousarray(iters, np.int32)
+        lr0 = np.zeros(it.size, np.float32)
+        deg = np.zeros(it.size, np.uint32)
+        due = np.zeros(it.size, np.uint8)
+        self._call("train_plans", C.byref(s), sh_degree, it.size, sh.ptr(it), sh.ptr(lr0), sh.ptr(deg), sh.ptr(due))
+        return lr0, deg, due
 
     def trainer_mcmc_refine(self, params, exp_avg, exp_avg_sq, count, cap_max, sh_degree, seed, n_refine,
                             min_opacity=0.005):
@@ -362,8 +416,17 @@ class ReferenceTrainerOnHip:
 
     def run(self, params, count, sh_degree, viewmat, K, width, height, gt, steps, lr, total_iters=100,
             ssim_weight=0.2, opacity_reg=0.0, scale_reg=0.0, antialiased=False, resident=True, mcmc=False,
-            cap_max=0, seed=42, refine_start_ratio=0.0, refine_stop_ratio=1.0, refine_every_ratio=0.02):
+            cap_max=0, seed=42, refine_start_ratio=0.0, refine_stop_ratio=1.0, refine_every_ratio=0.02,
+            cameras=None, start_iter=0, scene_scale=0.0, sh_degree_interval_ratio=0.0):
+        """Steps start_iter .. start_iter + steps of Trainer::step; with cameras = (viewmats [n,16],
+        Ks [n,9], gts [n,H,W,3]) step it uses camera it % n (viewmat/K/gt are then ignored)."""
         c = HipTrainCase()
+        if cameras is not None:
+            cv, ck, cg = (sh.f32(x) for x in cameras)
+            self._cams = (cv, ck, cg)
+            c.n_cams, c.viewmats, c.Ks, c.gts = cv.shape[0], sh.ptr(cv), sh.ptr(ck), sh.ptr(cg)
+            viewmat, K, gt = cv[0], ck[0], cg[0]
+        c.start_iter, c.scene_scale, c.sh_degree_interval_ratio = start_iter, scene_scale, sh_degree_interval_ratio
         keep = [sh.f32(x).reshape(count, -1) for x in params]
         for g in range(6):
             c.params[g] = _ptr_or_null(keep[g])

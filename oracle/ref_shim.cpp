@@ -417,3 +417,63 @@ int32_t sxr_trainer_mcmc_refine(sxr_refine_case* c) {
 }
 
 } // extern "C"
+
+// ---- the caller loop's schedule: the reference's own functions ----------------------------------
+extern "C" {
+
+typedef struct {
+    int32_t total_iters;
+    float scene_scale, lr_means, sh_degree_interval_ratio;
+    uint8_t mcmc_enabled;
+    float refine_start_ratio, refine_stop_ratio, refine_every_ratio;
+} sxr_schedule;
+
+/* TrainConfig / McmcOptions defaults (Trainer.h), as floats in sxh_train_schedule's order:
+ * total_iters, scene_scale, lr_means, lr_quats, lr_scales, lr_opacities, lr_sh0, lr_shN,
+ * sh_degree_interval_ratio, opacity_reg, scale_reg, cap_max, min_opacity, refine_start_ratio,
+ * refine_stop_ratio, refine_every_ratio, noise_lr, seed (18 values) */
+int32_t sxr_train_defaults(double* out) {
+    const splatx::TrainConfig c;
+    const splatx::McmcOptions m;
+    const double v[18] = {static_cast<double>(c.total_iters), c.scene_scale, c.lr_means, c.lr_quats, c.lr_scales,
+                          c.lr_opacities, c.lr_sh0, c.lr_shN, c.sh_degree_interval_ratio, c.opacity_reg, c.scale_reg,
+                          static_cast<double>(m.cap_max), m.min_opacity, m.refine_start_ratio, m.refine_stop_ratio,
+                          m.refine_every_ratio, m.noise_lr, static_cast<double>(m.seed)};
+    std::memcpy(out, v, sizeof(v));
+    return SXH_OK;
+}
+
+/* means_lr_at, sh_degree_at and Trainer::mcmc_refine_due for iterations iters[0 .. n) */
+int32_t sxr_train_plans(const sxr_schedule* s, int32_t sh_degree, int32_t n, const int32_t* iters, float* lr0,
+                        uint32_t* degrees, uint8_t* due) {
+    return guarded([&] {
+        splatx::TrainConfig cfg;
+        cfg.total_iters = s->total_iters;
+        cfg.scene_scale = s->scene_scale;
+        cfg.lr_means = s->lr_means;
+        cfg.sh_degree_interval_ratio = s->sh_degree_interval_ratio;
+        cfg.mcmc.enabled = s->mcmc_enabled != 0;
+        cfg.mcmc.refine_start_ratio = s->refine_start_ratio;
+        cfg.mcmc.refine_stop_ratio = s->refine_stop_ratio;
+        cfg.mcmc.refine_every_ratio = s->refine_every_ratio;
+        cfg.mcmc.cap_max = 4;
+        auto cpu = splatx::make_cpu_backend();
+        splatx::SplatCloud cloud;  // one Gaussian: the Trainer only has to exist
+        cloud.count = 1;
+        cloud.sh_degree = sh_degree;
+        cloud.means = {0.f, 0.f, 3.f};
+        cloud.quats = {1.f, 0.f, 0.f, 0.f};
+        cloud.scales = {-3.f, -3.f, -3.f};
+        cloud.opacities = {0.f};
+        cloud.sh0 = {0.f, 0.f, 0.f};
+        cloud.shN.assign(static_cast<size_t>(cloud.sh_rest_coeffs()) * 3, 0.f);
+        splatx::Trainer tr(*cpu, std::move(cloud), cfg);
+        for (int32_t k = 0; k < n; k++) {
+            lr0[k] = splatx::means_lr_at(cfg, iters[k]);
+            degrees[k] = splatx::sh_degree_at(cfg, iters[k], sh_degree);
+            due[k] = tr.mcmc_refine_due(iters[k]) ? 1 : 0;
+        }
+    });
+}
+
+}  // extern "C"

@@ -49,6 +49,13 @@ typedef struct {
     float* render0;          /* [H,W,3]: the first step's render */
     int64_t out_count;
     int32_t n_refined;
+    /* optional: a camera list (step it uses camera it % n_cams and its own GT) and a first iteration */
+    int32_t n_cams;
+    const float* viewmats;   /* [n_cams,16] */
+    const float* Ks;         /* [n_cams,9] */
+    const float* gts;        /* [n_cams,H,W,3] */
+    int32_t start_iter;
+    float scene_scale, sh_degree_interval_ratio;
 } sxr_hip_train_case;
 
 const char* sxr_hip_last_error(void) { return g_err.c_str(); }
@@ -65,6 +72,8 @@ int32_t sxr_hip_trainer_run(sxr_hip_train_case* c) {
         for (int g = 0; g < 6; g++) vs[g]->assign(c->params[g], c->params[g] + c->count * dims[g]);
         splatx::TrainConfig cfg;
         cfg.total_iters = c->total_iters;
+        if (c->scene_scale > 0.0f) cfg.scene_scale = c->scene_scale;
+        if (c->sh_degree_interval_ratio > 0.0f) cfg.sh_degree_interval_ratio = c->sh_degree_interval_ratio;
         cfg.lr_means = c->lr[0];
         cfg.lr_quats = c->lr[1];
         cfg.lr_scales = c->lr[2];
@@ -85,18 +94,25 @@ int32_t sxr_hip_trainer_run(sxr_hip_train_case* c) {
             cfg.mcmc.refine_every_ratio = c->refine_every_ratio;
         }
         splatx::Trainer tr(*backend, std::move(cloud), cfg);
-        splatx::TrainingCamera cam;
-        std::memcpy(cam.viewmat, c->viewmat, sizeof(cam.viewmat));
-        std::memcpy(cam.K, c->K, sizeof(cam.K));
-        cam.width = c->width;
-        cam.height = c->height;
+        const int n_cams = c->n_cams > 0 ? c->n_cams : 1;
+        std::vector<splatx::TrainingCamera> cams(static_cast<size_t>(n_cams));
+        for (int k = 0; k < n_cams; k++) {
+            std::memcpy(cams[k].viewmat, c->n_cams > 0 ? c->viewmats + 16 * k : c->viewmat, sizeof(cams[k].viewmat));
+            std::memcpy(cams[k].K, c->n_cams > 0 ? c->Ks + 9 * k : c->K, sizeof(cams[k].K));
+            cams[k].width = c->width;
+            cams[k].height = c->height;
+        }
+        const size_t img = static_cast<size_t>(c->width) * c->height * 3;
         c->n_refined = 0;
-        for (int it = 0; it < c->steps; it++) {
-            const splatx::TrainStepResult r = tr.step(cam, c->gt_rgb, it);
-            c->losses[it] = r.loss;
-            c->n_isects[it] = r.n_isects;
+        for (int s = 0; s < c->steps; s++) {
+            const int it = c->start_iter + s;
+            const int k = it % n_cams;
+            const float* gt = c->n_cams > 0 ? c->gts + img * static_cast<size_t>(k) : c->gt_rgb;
+            const splatx::TrainStepResult r = tr.step(cams[static_cast<size_t>(k)], gt, it);
+            c->losses[s] = r.loss;
+            c->n_isects[s] = r.n_isects;
             if (r.mcmc_refined) c->n_refined++;
-            if (it == 0 && c->render0 && !r.render_colors.empty())
+            if (s == 0 && c->render0 && !r.render_colors.empty())
                 std::memcpy(c->render0, r.render_colors.data(), r.render_colors.size() * sizeof(float));
         }
         const splatx::SplatCloud& out = tr.cloud();

@@ -146,7 +146,53 @@ __global__ void __launch_bounds__(kBlock) k_rgba8(const float* __restrict__ rgb,
     out[p] = word;
 }
 
+// rows list[j], j in [0, n), of one SoA group -> row-major [n, dim] (raw values, the snapshot layout)
+__global__ void __launch_bounds__(kBlock) k_gather_rows(const float* __restrict__ soa, int R, int dim,
+                                                        const int32_t* __restrict__ list, int64_t n,
+                                                        float* __restrict__ out) {
+    const int64_t t = blockIdx.x * static_cast<int64_t>(kBlock) + threadIdx.x;
+    if (t >= n * dim) return;
+    const int64_t j = t / dim;
+    const int k = static_cast<int>(t - j * dim);
+    out[t] = soa[static_cast<size_t>(k) * R + static_cast<size_t>(list[j])];
+}
+
+// partials[b] = f64 sum over block b's grid-stride share of (clamp(a, 0, 1) - b)^2, clamp as
+// std::clamp (NaN passes through); a fixed grid, so the host sums the partials in a fixed order
+constexpr int kSqBlocks = 512;
+__global__ void __launch_bounds__(kBlock) k_sq_err(const float* __restrict__ a, const float* __restrict__ b,
+                                                   int64_t n, double* __restrict__ partials) {
+    __shared__ double s_red[kBlock];
+    double acc = 0.0;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(kBlock) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(kSqBlocks) * kBlock) {
+        float v = a[i];
+        v = v < 0.0f ? 0.0f : (1.0f < v ? 1.0f : v);
+        const double d = static_cast<double>(v) - static_cast<double>(b[i]);
+        acc += d * d;
+    }
+    s_red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = kBlock / 2; o > 0; o >>= 1) {
+        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partials[blockIdx.x] = s_red[0];
+}
+
 }  // namespace
+
+void gather_rows(const float* soa, int R, int dim, const int32_t* list, int64_t n, float* out, hipStream_t s) {
+    const int64_t total = n * dim;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(k_gather_rows, dim3(grid_for(total)), dim3(kBlock), 0, s, soa, R, dim, list, n, out);
+}
+
+int sq_err_blocks() { return kSqBlocks; }
+
+void sq_err(const float* a, const float* b, int64_t n, double* partials, hipStream_t s) {
+    hipLaunchKernelGGL(k_sq_err, dim3(kSqBlocks), dim3(kBlock), 0, s, a, b, n, partials);
+}
 
 void export_flags(const Arena& A, const Dims6& dims, int count, float min_opacity, int32_t* keep,
                   unsigned long long* removed, hipStream_t s) {

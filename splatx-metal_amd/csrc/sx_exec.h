@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 
 #include "splatx_hip.h"
@@ -37,6 +38,7 @@ struct sxh_executor {
     int n_coeffs = 1;
     int dims[6] = {3, 4, 3, 1, 3, 0};
     int rows = 0;
+    std::atomic<int> stop_requested{0};  // sxh_exec_request_stop -> the caller loop's next boundary
     sxh::DevBuf<float> p[6], m[6], v[6];
     sxh::DevBuf<float4> splats, grads;
     sxh::DevBuf<int32_t> radii, tiles;

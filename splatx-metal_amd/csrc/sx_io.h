@@ -23,6 +23,11 @@ void export_flags(const Arena& A, const Dims6& dims, int count, float min_opacit
                   unsigned long long* removed, hipStream_t s);
 // list[cum[i]-1] = i for kept rows (cum = inclusive int64 scan of keep)
 void export_list(const int32_t* keep, const int64_t* cum, int count, int32_t* list, hipStream_t s);
+// rows list[0 .. n) of one SoA group (R rows per column) -> row-major [n, dim]
+void gather_rows(const float* soa, int R, int dim, const int32_t* list, int64_t n, float* out, hipStream_t s);
+// sq_err_blocks() f64 partial sums of (clamp(a, 0, 1) - b)^2 over n floats
+int sq_err_blocks();
+void sq_err(const float* a, const float* b, int64_t n, double* partials, hipStream_t s);
 // floats per PLY row with Kw f_rest coefficients per channel
 int export_row_floats(int Kw);
 // PLY rows [row0, row0 + rows) of the kept list, row-major floats

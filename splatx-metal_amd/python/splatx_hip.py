@@ -250,6 +250,96 @@ class RenderSessionArgs(C.Structure):
     _fields_ = [("ply_path", C.c_char_p), ("antialiased", C.c_int32), ("sh_degree", C.c_int32)]
 
 
+class TrainCamera(C.Structure):
+    """TrainingCamera with its image's slot in the GT cache (sxh_train_camera)."""
+    _fields_ = [("viewmat", C.c_float * 16), ("K", C.c_float * 9), ("width", C.c_int32), ("height", C.c_int32),
+                ("gt_index", C.c_int32)]
+
+    @staticmethod
+    def make(viewmat, K, width, height, gt_index):
+        c = TrainCamera()
+        c.viewmat[:] = [float(x) for x in np.asarray(viewmat, np.float32).ravel()]
+        c.K[:] = [float(x) for x in np.asarray(K, np.float32).ravel()]
+        c.width, c.height, c.gt_index = width, height, gt_index
+        return c
+
+
+class TrainSchedule(C.Structure):
+    """TrainConfig / McmcOptions fields the caller loop reads (sxh_train_schedule)."""
+    _fields_ = [("total_iters", C.c_int32), ("scene_scale", C.c_float), ("lr_means", C.c_float),
+                ("lr_quats", C.c_float), ("lr_scales", C.c_float), ("lr_opacities", C.c_float), ("lr_sh0", C.c_float),
+                ("lr_shN", C.c_float), ("sh_degree_interval_ratio", C.c_float), ("opacity_reg", C.c_float),
+                ("scale_reg", C.c_float), ("mcmc_enabled", C.c_uint8), ("cap_max", C.c_int64),
+                ("min_opacity", C.c_float), ("refine_start_ratio", C.c_float), ("refine_stop_ratio", C.c_float),
+                ("refine_every_ratio", C.c_float), ("noise_lr", C.c_float), ("mcmc_seed", C.c_uint64)]
+
+
+class TrainProgress(C.Structure):
+    """SxTrainProgress (sxh_train_progress)."""
+    _fields_ = [("iter", C.c_int32), ("run_until", C.c_int32), ("total_iters", C.c_int32), ("loss", C.c_float),
+                ("psnr", C.c_float), ("step_ms", C.c_double), ("n_isects", C.c_int64), ("splat_count", C.c_int64),
+                ("thermal_state", C.c_int32), ("mcmc_refined", C.c_int32), ("n_relocated", C.c_int64),
+                ("n_added", C.c_int64)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class SplatSnapshot(C.Structure):
+    """SxSplatSnapshot (sxh_splat_snapshot)."""
+    _fields_ = [("iter", C.c_int32), ("sh_degree", C.c_int32), ("count", C.c_int64), ("means", fp), ("quats", fp),
+                ("scales", fp), ("opacities", fp), ("sh0", fp), ("shN", fp)]
+
+
+class TrainPlan(C.Structure):
+    """One iteration's step arguments under a schedule (sxh_train_plan)."""
+    _fields_ = [("degrees_to_use", C.c_uint32), ("lr", C.c_float * 6), ("opacity_reg_w", C.c_float),
+                ("scale_reg_w", C.c_float), ("refine_due", C.c_uint8), ("inject_noise", C.c_uint8),
+                ("noise_scale", C.c_float)]
+
+
+def train_schedule_defaults(lib=None) -> TrainSchedule:
+    lib = lib or load_library()
+    s = TrainSchedule()
+    lib.sxh_train_schedule_defaults.restype = C.c_int32
+    _raise(lib, lib.sxh_train_schedule_defaults(C.byref(s)))
+    return s
+
+
+def train_plan_at(schedule: TrainSchedule, iter: int, sh_degree: int, count: int, lib=None) -> TrainPlan:
+    """Trainer::step_resident's arguments for iteration `iter` (sxh_train_plan_at, host only)."""
+    lib = lib or load_library()
+    p = TrainPlan()
+    lib.sxh_train_plan_at.restype = C.c_int32
+    _raise(lib, lib.sxh_train_plan_at(C.byref(schedule), iter, sh_degree, C.c_int64(count), C.byref(p)))
+    return p
+
+
+PROGRESS_FN = C.CFUNCTYPE(None, C.POINTER(TrainProgress), C.c_void_p)
+SNAPSHOT_FN = C.CFUNCTYPE(None, C.POINTER(SplatSnapshot), C.c_void_p)
+
+
+class TrainLoopArgs(C.Structure):
+    _fields_ = [("cameras", C.POINTER(TrainCamera)), ("n_cameras", C.c_int32),
+                ("eval_cameras", C.POINTER(TrainCamera)), ("n_eval_cameras", C.c_int32), ("eval_every", C.c_int32),
+                ("start_iter", C.c_int32), ("run_until", C.c_int32), ("count", C.c_int64), ("sched", TrainSchedule),
+                ("binoms", fp), ("n_max", C.c_int32), ("rng", C.POINTER(MtState)), ("jitter_max_deg", C.c_float),
+                ("jitter_max_t", C.c_float), ("jitter_seed", C.c_uint64), ("progress", PROGRESS_FN),
+                ("progress_user", C.c_void_p), ("snapshot", SNAPSHOT_FN), ("snapshot_user", C.c_void_p),
+                ("snapshot_every", C.c_int32), ("live_ply_every", C.c_int32), ("live_ply_path", C.c_char_p),
+                ("checkpoint_every", C.c_int32), ("checkpoint_path", C.c_char_p),
+                ("checkpoint_config", C.POINTER(CkptConfig)), ("checkpoint_fp16", C.c_uint8)]
+
+
+class TrainLoopResult(C.Structure):
+    _fields_ = [("completed_iters", C.c_int32), ("count", C.c_int64), ("first_loss", C.c_float),
+                ("last_loss", C.c_float), ("last_eval_psnr", C.c_float), ("train_seconds", C.c_double),
+                ("stopped", C.c_int32)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
 def _raise(lib, rc):
     if rc != SXH_OK:
         msg = lib.sxh_last_error().decode(errors="replace")
@@ -580,7 +670,9 @@ class Ops:
 def load_library(path: str = LIB_PATH):
     if not os.path.exists(path):
         raise SxRuntimeError(f"splatx HIP library not built: {path} (run __graft_entry__.build())")
-    return C.CDLL(path)
+    lib = C.CDLL(path)
+    lib.sxh_last_error.restype = C.c_char_p
+    return lib
 
 
 class Backend(Ops):
@@ -774,6 +866,72 @@ class Executor:
         d = h.as_dict()
         d["rng_state"] = buf.value.decode()
         return d
+
+    def train_schedule_defaults(self) -> TrainSchedule:
+        s = TrainSchedule()
+        f = self.lib.sxh_train_schedule_defaults
+        f.restype = C.c_int32
+        self._check(f(C.byref(s)))
+        return s
+
+    def train_loop(self, cameras, start_iter, run_until, count, schedule: TrainSchedule, rng: MtState = None,
+                   binoms=None, n_max=51, eval_cameras=(), eval_every=0, jitter=None, progress=None,
+                   snapshot=None, snapshot_every=0, live_ply_every=0, live_ply_path=None, checkpoint_every=0,
+                   checkpoint_path=None, checkpoint_config: CkptConfig = None, checkpoint_fp16=False):
+        """The caller loop (sxh_exec_train_loop) over `cameras` (TrainCamera, GT in the cache).
+        progress(dict) is called at every step boundary; snapshot(dict of arrays) every
+        snapshot_every steps; jitter = (max_deg, max_t, seed) or None. `rng` is advanced in place."""
+        cams = (TrainCamera * len(cameras))(*cameras)
+        ecams = (TrainCamera * max(1, len(eval_cameras)))(*eval_cameras) if eval_cameras else None
+        a = TrainLoopArgs()
+        a.cameras, a.n_cameras = cams, len(cameras)
+        if ecams is not None:
+            a.eval_cameras, a.n_eval_cameras = ecams, len(eval_cameras)
+        a.eval_every = eval_every
+        a.start_iter, a.run_until, a.count, a.sched = start_iter, run_until, count, schedule
+        keep = []
+        if binoms is not None:
+            b = f32(binoms)
+            keep.append(b)
+            a.binoms, a.n_max = ptr(b), n_max
+        if rng is not None:
+            a.rng = C.pointer(rng)
+        if jitter is not None:
+            a.jitter_max_deg, a.jitter_max_t, a.jitter_seed = jitter
+        if progress is not None:
+            cb = PROGRESS_FN(lambda p, _u: progress(p.contents.as_dict()))
+            keep.append(cb)
+            a.progress = cb
+        if snapshot is not None:
+            def snap(sp, _u):
+                s = sp.contents
+                n = int(s.count)
+                k = (s.sh_degree + 1) ** 2 - 1
+                def arr(pp, dim):
+                    return np.ctypeslib.as_array(pp, shape=(n, dim)).copy() if n and pp else np.zeros((n, dim), np.float32)
+                snapshot(dict(iter=int(s.iter), sh_degree=int(s.sh_degree), count=n, means=arr(s.means, 3),
+                              quats=arr(s.quats, 4), scales=arr(s.scales, 3), opacities=arr(s.opacities, 1)[:, 0],
+                              sh0=arr(s.sh0, 3), shN=arr(s.shN, 3 * k) if k else None))
+            cb = SNAPSHOT_FN(snap)
+            keep.append(cb)
+            a.snapshot, a.snapshot_every = cb, snapshot_every
+        a.live_ply_every = live_ply_every
+        a.live_ply_path = live_ply_path.encode() if live_ply_path else None
+        a.checkpoint_every = checkpoint_every
+        a.checkpoint_path = checkpoint_path.encode() if checkpoint_path else None
+        if checkpoint_config is not None:
+            a.checkpoint_config = C.pointer(checkpoint_config)
+        a.checkpoint_fp16 = int(bool(checkpoint_fp16))
+        out = TrainLoopResult()
+        f = self.lib.sxh_exec_train_loop
+        f.restype = C.c_int32
+        self._check(f(self.h, C.byref(a), C.byref(out)))
+        return out.as_dict()
+
+    def request_stop(self):
+        f = self.lib.sxh_exec_request_stop
+        f.restype = C.c_int32
+        self._check(f(self.h))
 
     def set_profiling(self, enable: bool):
         self._check(self.lib.sxh_exec_set_profiling(self.h, int(bool(enable))))

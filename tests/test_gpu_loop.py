@@ -1,0 +1,231 @@
+"""The caller loop (sxh_exec_train_loop) on the device.
+
+- Against the reference's own Trainer (oracle/_ref/libsx_ref_hip.so: Trainer.cpp unchanged, on this
+  repository's backend; skipped where it was not built) over the same iterations: several cameras
+  (iteration it uses camera it % n), SH degrees stepping up, MCMC refines with growth and noise,
+  regularization. The loop's step is the same device step, so the losses and the final cloud agree
+  to the step's own tolerance (atomic accumulation order): the live count exactly, n_isects of the
+  first iteration exactly, losses within 1e-4 relative, parameters within 1e-3 relative L2.
+- The hooks at the step boundary: one progress tick per iteration with the refine iterations the
+  schedule names, the eval PSNR equal to one computed here from a render, the checkpoint, the live
+  PLY (byte-identical to an export of the final state), the snapshot (equal to the export filter's
+  rows), a stop requested from the progress callback.
+- Resuming (two calls, the generator carried) matches one call; invalid arguments are rejected
+  before anything runs.
+"""
+import numpy as np
+import pytest
+
+import oracle_py
+import scene
+import splatx_hip as sh
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+
+
+def rel_l2(a, e):
+    a = np.asarray(a, np.float64).ravel()
+    e = np.asarray(e, np.float64).ravel()
+    return float(np.sqrt(((a - e) ** 2).sum()) / max(np.sqrt((e * e).sum()), 1e-30))
+
+
+N, DEG, W, H, FX = 3000, 2, 128, 96, 110.0
+CAP = 4200
+
+
+def make_setup(gpu, n_cams=3, seed=5):
+    """A scene, n_cams jittered cameras and their GT images (a second scene rendered per view)."""
+    sc = scene.make_scene(n=N, sh_degree=DEG, width=W, height=H, fx=FX, seed=seed, logit_sd=3.0)
+    tgt = scene.make_scene(n=N, sh_degree=DEG, width=W, height=H, fx=FX, seed=seed + 100)
+    rng = np.random.Generator(np.random.PCG64(seed))
+    views = [scene.identity_view()] + [scene.jittered_view(rng, 8.0, 0.3) for _ in range(n_cams - 1)]
+    ex = gpu.make_train_step_executor(arena_rows=N, sh_degree=DEG, ssim_weight=0.2)
+    p, m, v = scene.copy_state(tgt)
+    ex.upload_params(p, m, v, N)
+    gts = np.stack([ex.step(want_render=True, forward_only=True, **dict(scene.step_kwargs(tgt), viewmat=vm))
+                    ["render_colors"] for vm in views])
+    ex.close()
+    return sc, views, gts
+
+
+def schedule(total_iters=40, mcmc=True):
+    s = sh.train_schedule_defaults()
+    s.total_iters = total_iters
+    s.lr_means, s.lr_quats, s.lr_scales, s.lr_opacities, s.lr_sh0, s.lr_shN = 1.6e-3, 1e-3, 5e-3, 5e-2, 2.5e-3, 1.25e-4
+    s.sh_degree_interval_ratio = 0.2  # degree +1 every 8 iterations
+    s.opacity_reg, s.scale_reg = 0.01, 0.01
+    s.mcmc_enabled = int(mcmc)
+    s.cap_max = CAP
+    s.refine_start_ratio, s.refine_stop_ratio, s.refine_every_ratio = 0.1, 0.9, 0.125  # refines at 5, 10, ... 35
+    s.mcmc_seed = 42
+    return s
+
+
+def arena(sc, rows):
+    p, m, v = scene.copy_state(sc)
+    pad = lambda a: np.concatenate([a.reshape(sc.n, -1), np.zeros((rows - sc.n, a.reshape(sc.n, -1).shape[1]), F)])
+    return [pad(x) for x in p], [pad(x) for x in m], [pad(x) for x in v]
+
+
+def loop_executor(gpu, sc, gts, rows=CAP):
+    ex = gpu.make_train_step_executor(arena_rows=rows, sh_degree=DEG, ssim_weight=0.2)
+    ex.set_gt_cache(gts)
+    ex.upload_params(*arena(sc, rows), rows)
+    return ex
+
+
+def cameras(sc, views):
+    return [sh.TrainCamera.make(vm, sc.K, W, H, k) for k, vm in enumerate(views)]
+
+
+def download(ex, rows):
+    out = [[np.zeros((rows, d), F) for d in scene.group_dims(DEG)] for _ in range(3)]
+    ex.download_params(*out, rows)
+    return out
+
+
+@pytest.mark.skipif(not oracle_py.ReferenceTrainerOnHip.available(), reason="oracle/_ref not built")
+def test_loop_matches_reference_trainer(gpu):
+    sc, views, gts = make_setup(gpu)
+    s = schedule()
+    steps = 40
+    ref = oracle_py.ReferenceTrainerOnHip().run(
+        sc.params, N, DEG, None, None, W, H, None, steps,
+        [s.lr_means, s.lr_quats, s.lr_scales, s.lr_opacities, s.lr_sh0, s.lr_shN], total_iters=s.total_iters,
+        ssim_weight=0.2, opacity_reg=0.01, scale_reg=0.01, resident=True, mcmc=True, cap_max=CAP, seed=42,
+        refine_start_ratio=s.refine_start_ratio, refine_stop_ratio=s.refine_stop_ratio,
+        refine_every_ratio=s.refine_every_ratio, cameras=(np.stack(views), np.stack([sc.K] * len(views)), gts),
+        sh_degree_interval_ratio=s.sh_degree_interval_ratio, scene_scale=1.0)
+    ex = loop_executor(gpu, sc, gts)
+    ticks = []
+    rng = gpu.mt64_seed(42)
+    res = ex.train_loop(cameras(sc, views), 0, steps, N, s, rng=rng, binoms=gpu.make_binoms_lut(), progress=ticks.append)
+    assert res["completed_iters"] == steps and res["stopped"] == 0
+    assert len(ticks) == steps and [t["iter"] for t in ticks] == list(range(1, steps + 1))
+    assert sum(t["mcmc_refined"] for t in ticks) == ref["n_refined"] == 7
+    assert res["count"] == ref["count"] > N
+    assert ticks[0]["n_isects"] == ref["n_isects"][0]
+    losses = np.array([t["loss"] for t in ticks])
+    assert np.all(np.abs(losses - ref["losses"]) <= 1e-4 * np.abs(ref["losses"]) + 1e-6), (losses, ref["losses"])
+    dp, _, _ = download(ex, CAP)
+    for g in range(6):
+        assert rel_l2(dp[g][:res["count"]], ref["params"][g][:res["count"]]) <= 1e-3, g
+    ex.close()
+
+
+def test_loop_hooks(gpu, tmp_path):
+    sc, views, gts = make_setup(gpu, n_cams=2, seed=9)
+    s = schedule(total_iters=24)
+    ex = loop_executor(gpu, sc, gts)
+    ticks, snaps = [], []
+    ck, live = str(tmp_path / "ck.sxck"), str(tmp_path / "live.ply")
+    cfg = sh.CkptConfig.make(sh_degree=DEG, total_iters=24, mcmc_enabled=1, cap_max=CAP, mcmc_seed=42)
+    rng = gpu.mt64_seed(42)
+    res = ex.train_loop(cameras(sc, views), 0, 24, N, s, rng=rng, binoms=gpu.make_binoms_lut(),
+                        eval_cameras=cameras(sc, views), eval_every=12, progress=ticks.append, snapshot=snaps.append,
+                        snapshot_every=8, live_ply_every=12, live_ply_path=live, checkpoint_every=10,
+                        checkpoint_path=ck, checkpoint_config=cfg)
+    count = res["count"]
+    assert [t["iter"] for t in ticks] == list(range(1, 25))
+    due = [sh.train_plan_at(s, it, DEG, N).refine_due for it in range(24)]
+    assert [t["mcmc_refined"] for t in ticks] == due and sum(due) == 7  # iterations 3, 6, ... 21
+    for t in ticks:
+        assert t["run_until"] == 24 and t["total_iters"] == 24 and t["thermal_state"] == 0 and t["step_ms"] > 0
+        assert (t["psnr"] == t["psnr"]) == (t["iter"] % 12 == 0)  # NaN except on eval ticks
+    assert ticks[-1]["splat_count"] == count
+    # eval: the mean over the eval views of 10 log10(1 / mse) of the clamped render
+    ps = []
+    for k, vm in enumerate(views):
+        r = ex.step(want_render=True, forward_only=True, viewmat=vm, K=sc.K, width=W, height=H, count=count,
+                    degrees_to_use=DEG, lr=[0.0] * 6)["render_colors"]
+        mse = float(((np.clip(r, 0, 1).astype(np.float64) - gts[k]) ** 2).mean())
+        ps.append(float(F(10.0 * np.log10(1.0 / mse))))
+    assert abs(ticks[-1]["psnr"] - np.mean(ps)) <= 1e-4 and abs(res["last_eval_psnr"] - np.mean(ps)) <= 1e-4
+    # checkpoint: saved after iteration 20 (iterations 10 and 20; 24 is the run's end)
+    h = sh.checkpoint_read_header(ck)
+    assert h["iter"] == 20 and h["alive_count"] == ticks[19]["splat_count"]
+    # live PLY of the final state == an export of it
+    mine = str(tmp_path / "final.ply")
+    ex.export_ply(count, mine)
+    assert open(live, "rb").read() == open(mine, "rb").read()
+    # snapshots at 8, 16, 24; the last one is the export filter's rows of the final state
+    assert [x["iter"] for x in snaps] == [8, 16, 24]
+    flat = str(tmp_path / "flat.ply")
+    ex.export_ply(count, flat, pad_sh_full=False)
+    cl = sh.ply_read(flat)
+    last = snaps[-1]
+    assert last["count"] == cl["count"]
+    for g, key in enumerate(("means", "quats", "scales", "opacities", "sh0", "shN")):
+        assert np.array_equal(np.asarray(last[key], F).reshape(cl["count"], -1),
+                              np.asarray(cl["params"][g], F).reshape(cl["count"], -1)), key
+    ex.close()
+
+
+def test_loop_stop_request_and_resume(gpu):
+    sc, views, gts = make_setup(gpu, n_cams=2, seed=13)
+    s = schedule(total_iters=30)
+    cams = cameras(sc, views)
+    binoms = gpu.make_binoms_lut()
+    # a stop requested from the progress callback ends the loop at the next boundary
+    ex = loop_executor(gpu, sc, gts)
+    seen = []
+
+    def stop_at_6(t):
+        seen.append(t["iter"])
+        if t["iter"] == 6:
+            ex.request_stop()
+
+    res = ex.train_loop(cams, 0, 30, N, s, rng=gpu.mt64_seed(42), binoms=binoms, progress=stop_at_6)
+    assert res["stopped"] == 1 and res["completed_iters"] == 6 and seen == list(range(1, 7))
+    ex.close()
+    # one call over [0, 30) against two calls over [0, 17) and [17, 30), the generator carried
+    ex1 = loop_executor(gpu, sc, gts)
+    r1 = ex1.train_loop(cams, 0, 30, N, s, rng=gpu.mt64_seed(42), binoms=binoms)
+    p1 = download(ex1, CAP)[0]
+    ex1.close()
+    ex2 = loop_executor(gpu, sc, gts)
+    rng = gpu.mt64_seed(42)
+    a = ex2.train_loop(cams, 0, 17, N, s, rng=rng, binoms=binoms)
+    b = ex2.train_loop(cams, 17, 30, a["count"], s, rng=rng, binoms=binoms)
+    p2 = download(ex2, CAP)[0]
+    ex2.close()
+    assert b["completed_iters"] == 30 and b["count"] == r1["count"]
+    for g in range(6):
+        assert rel_l2(p2[g][:r1["count"]], p1[g][:r1["count"]]) <= 1e-3, g
+
+
+def test_loop_jitter_is_seeded(gpu):
+    sc, views, gts = make_setup(gpu, n_cams=1, seed=17)
+    s = schedule(total_iters=10, mcmc=False)
+    first = {}
+    for key, seed in (("a", 7), ("b", 7), ("c", 8), ("none", None)):
+        ex = loop_executor(gpu, sc, gts, rows=N)
+        ticks = []
+        ex.train_loop(cameras(sc, views), 0, 1, N, s, progress=ticks.append,
+                      jitter=None if seed is None else (5.0, 0.2, seed))
+        first[key] = ticks[0]["n_isects"]
+        ex.close()
+    assert first["a"] == first["b"]
+    assert first["a"] != first["none"] and first["c"] != first["a"]
+
+
+def test_loop_rejects_invalid_arguments(gpu):
+    sc, views, gts = make_setup(gpu, n_cams=1, seed=21)
+    s = schedule(total_iters=10)
+    ex = loop_executor(gpu, sc, gts)
+    cam = cameras(sc, views)
+    bad_size = [sh.TrainCamera.make(views[0], sc.K, W + 1, H, 0)]
+    bad_index = [sh.TrainCamera.make(views[0], sc.K, W, H, 5)]
+    binoms = gpu.make_binoms_lut()
+    ticks = []
+    for kw in (dict(cameras=bad_size), dict(cameras=bad_index), dict(count=CAP + 1), dict(rng=None),
+               dict(run_until=-1), dict(checkpoint_every=5)):
+        args = dict(cameras=cam, start_iter=0, run_until=5, count=N, schedule=s, rng=gpu.mt64_seed(42),
+                    binoms=binoms, progress=ticks.append)
+        args.update(kw)
+        with pytest.raises(sh.SxInvalidArgument):
+            ex.train_loop(**args)
+    assert ticks == []
+    ex.close()
