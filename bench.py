@@ -175,6 +175,22 @@ def load_traffic(kernel: str, cfg: int):
     return k["hbm_bytes"]
 
 
+def load_valu(kernel: str, cfg: int):
+    """VALU issue bound of one launch of `kernel` from the counter run recorded in profiles/valu.json
+    (SQ_INSTS_VALU: wave-level VALU instructions; each occupies a 16-lane SIMD for 4 cycles); None if
+    not recorded."""
+    path = os.path.join(REPO, "profiles", "valu.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    k = rec.get("kernels", {}).get(kernel)
+    if k is None or rec.get("config") != cfg:
+        return None
+    return {"valu_insts": k["valu_insts"], "bound_ms": k["issue_bound_ms"], "simds": rec["simds"],
+            "clock_hz": rec["clock_hz"], "cycles_per_wave_instr": rec["cycles_per_wave_instr"]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -325,8 +341,14 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(dom, args.config), "alg_bytes": round(dom_bytes)},
         "kernels": per_kernel,
+        "valu_issue": None,
         "host_waits_ms": {k: round(avg[k], 4) for k in avg if k.startswith("host_")},
     }
+    vi = load_valu(dom, args.config)
+    if vi is not None:  # the dominant kernel's own bound when it is compute-, not memory-bound
+        vi["kernel"] = dom
+        vi["frac"] = round(vi["bound_ms"] / avg[dom], 4)
+        res["valu_issue"] = vi
     if mcmc:
         res["config"]["workload"] = (f"config 4: {sc.n} live of a {arena}-row arena, SH{sc.sh_degree}, "
                                      f"{sc.width}x{sc.height}, AccuTile, SSIM, opacity/scale reg 1e-2; every step "
