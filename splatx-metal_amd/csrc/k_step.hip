@@ -35,16 +35,18 @@ __device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + sx
 
 // Adam of one element whose parameter and moments were already loaded (CpuKernels.cpp:127-144 arithmetic);
 // returns the updated parameter
+// One Adam step of one element; a row that is not `live` (culled: the reference's valid mask skips
+// it) writes its values back unchanged, so that a wave stores whole lines of every column.
 __device__ __forceinline__ float adam_update(float* __restrict__ p, float* __restrict__ m, float* __restrict__ v,
                                              size_t idx, float p0, float mm, float vv, float g, float lr, float b1,
-                                             float b2, float eps) {
-    mm = b1 * mm + (1.0f - b1) * g;
-    vv = b2 * vv + (1.0f - b2) * g * g;
-    const float p1 = p0 + -lr * mm / (__builtin_sqrtf(vv) + eps);
-    p[idx] = p1;
-    m[idx] = mm;
-    v[idx] = vv;
-    return p1;
+                                             float b2, float eps, bool live) {
+    const float mn = b1 * mm + (1.0f - b1) * g;
+    const float vn = b2 * vv + (1.0f - b2) * g * g;
+    const float p1 = p0 + -lr * mn / (__builtin_sqrtf(vn) + eps);
+    p[idx] = live ? p1 : p0;
+    m[idx] = live ? mn : mm;
+    v[idx] = live ? vn : vv;
+    return live ? p1 : p0;
 }
 
 
@@ -384,12 +386,17 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
     if (i >= c.count) return;
     const size_t R = static_cast<size_t>(A.rows);
     const uint32_t meta = __float_as_uint(splats[3 * (size_t)i + 2].w);
-    if (!(meta & 1u) && !c.inject_noise) return;  // culled and no noise: nothing to read or write
+    const bool live = meta & 1u;
+    // A wave with a visible row takes its culled rows along (loaded and stored back unchanged): the
+    // columns are SoA, so skipping them would leave every line partially written (a read-modify-write
+    // in the memory system). A wave of culled rows with no noise has nothing to read or write.
+    const bool wave_live = __any(live);
+    if (!wave_live && !c.inject_noise) return;
     float mw[3] = {A.p[0][i], A.p[0][R + i], A.p[0][2 * R + i]};
     float q[4] = {A.p[1][i], A.p[1][R + i], A.p[1][2 * R + i], A.p[1][3 * R + i]};
     float sl[3] = {A.p[2][i], A.p[2][R + i], A.p[2][2 * R + i]};
     float logit = A.p[3][i];
-    if (meta & 1u) {
+    if (wave_live) {
         const float4 g0 = grads[3 * (size_t)i];
         const float4 g1 = grads[3 * (size_t)i + 1];
         const float4 g2 = grads[3 * (size_t)i + 2];
@@ -460,7 +467,7 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
                     const size_t idx = (k == 0 ? (size_t)ch : (size_t)((k - 1) * 3 + ch)) * R + i;
                     const float g = k < nb ? b.Y[k] * vrgb[ch] : 0.0f;
                     adam_update(A.p[grp], A.m[grp], A.v[grp], idx, co[k][ch], mm[dk][ch], vv[dk][ch], g, c.lr[grp],
-                                c.b1, c.b2, c.eps);
+                                c.b1, c.b2, c.eps, live);
                 }
         }
         float vdir[3] = {0.f, 0.f, 0.f};
@@ -499,15 +506,16 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         // (the updated values stay in registers for the noise step below)
         for (int k = 0; k < 3; k++)
             mw[k] = adam_update(A.p[0], A.m[0], A.v[0], k * R + i, mw[k], m0[k], v0[k], vm_[k], c.lr[0], c.b1, c.b2,
-                                c.eps);
+                                c.eps, live);
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            q[k] = adam_update(A.p[1], A.m[1], A.v[1], k * R + i, q[k], m1[k], v1[k], vq[k], c.lr[1], c.b1, c.b2, c.eps);
+            q[k] = adam_update(A.p[1], A.m[1], A.v[1], k * R + i, q[k], m1[k], v1[k], vq[k], c.lr[1], c.b1, c.b2, c.eps,
+                               live);
 #pragma unroll
         for (int k = 0; k < 3; k++)
             sl[k] = adam_update(A.p[2], A.m[2], A.v[2], k * R + i, sl[k], m2[k], v2[k], vsl[k], c.lr[2], c.b1, c.b2,
-                                c.eps);
-        logit = adam_update(A.p[3], A.m[3], A.v[3], i, logit, m3, v3, vlog, c.lr[3], c.b1, c.b2, c.eps);
+                                c.eps, live);
+        logit = adam_update(A.p[3], A.m[3], A.v[3], i, logit, m3, v3, vlog, c.lr[3], c.b1, c.b2, c.eps, live);
     }
     if (c.inject_noise) {
         // normals 3i..3i+2 of the Philox stream (seed, offset): blocks t = n / 4
