@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     const float T_final = 1.0f - ralpha[pix];
     float T = T_final;
     float bdot = 0.f;  // <accumulated back colour, v_render> (the back-sum dotted with v_render)
-    const int32_t bin_final = inside ? last_ids[pix] : -1;
+    const int32_t bin_final = inside ? last_ids[pix] : -1;  // -1: no pair of an outside pixel is valid
     const float vc0 = v_rc[pix * 3], vc1 = v_rc[pix * 3 + 1], vc2 = v_rc[pix * 3 + 2];
     const float va = v_ra[pix];
     const float bg_dot = bg ? (bg[0] * vc0 + bg[1] * vc1 + bg[2] * vc2) : 0.f;
@@ -288,10 +288,15 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
             s_id[tid] = gid;
             float4 xyo = a.splats[(size_t)gid * 3];
             xyo.w = sigma_cutoff(xyo.z);
-            const float4 con = a.splats[(size_t)gid * 3 + 1];
+            float4 con = a.splats[(size_t)gid * 3 + 1];
+            float4 rgb = a.splats[(size_t)gid * 3 + 2];
+            // the sigmas at which the two alpha decisions turn: opacity * e^-sigma = 1/255 and = 0.99
+            // (approximate; only used to find the pairs close to them)
+            con.w = __logf(xyo.z * (1.0f / sx::kMaxAlpha));
+            rgb.w = __logf(xyo.z * 255.0f);
             s_xyo[tid] = xyo;
             s_con[tid] = con;
-            s_rgb[tid] = a.splats[(size_t)gid * 3 + 2];
+            s_rgb[tid] = rgb;
             // waves whose rows the cutoff set can reach, less those whose every pixel stopped before it
             wm = wave_rows_mask(xyo, con, ty * 16);
 #pragma unroll
@@ -309,6 +314,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
         // gradient term are left unchanged / zero.
         const int len = s_len[wave];
         const uint32_t* list4 = reinterpret_cast<const uint32_t*>(s_list[wave]);
+        const int t_min = batch_end - bin_final;  // slots t >= t_min are at or before the lane's last contributor
         for (int j = 0; j < len; j += 4) {
             const uint32_t packed = list4[j >> 2];
             int ts[4], tc[4];
@@ -327,32 +333,29 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
             const bool general = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cmax))) > 86.0f;
             float gv[4][NV];
             float alpha[4], vis[4], dxs[4], dys[4], sig[4], e[4];
+            bool valid[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 dxs[k] = xyo[k].x - px;
                 dys[k] = xyo[k].y - py;
                 sig[k] = sigma_of(con[k].x, con[k].y, con[k].z, dxs[k], dys[k]);
+                valid[k] = (ts[k] >= 0) & (tc[k] >= t_min) & !(sig[k] > xyo[k].w);  // bitwise: no branches
             }
-            bool valid[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                valid[k] = ts[k] >= 0 && inside && (batch_end - tc[k]) <= bin_final && !(sig[k] > xyo[k].w);
             // The exponential's value only enters gradients (compared at a relative tolerance), so the
             // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
             // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at
             // least 1/255, and opacity * exp at most the 0.99 clamp — must be the forward's. Where a lane
-            // lies within 2^-16 (1 + sigma) of either boundary (over 50 times that error), the chunk
-            // takes the forward's exponential instead.
+            // lies within 2^-12 in sigma of either turning point, the chunk takes the forward's
+            // exponential instead (the points themselves are approximate to ~1e-6).
             bool exact = general;
             if (!exact) {
                 bool near = false;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     e[k] = __builtin_amdgcn_exp2f(-sig[k] * 1.44269504f);
-                    const float oa = xyo[k].z * e[k];
-                    const float band = 0x1p-16f * (1.0f + sig[k]);
-                    near |= valid[k] && (__builtin_fabsf(oa * 255.0f - 1.0f) < band ||
-                                         __builtin_fabsf(oa - sx::kMaxAlpha) < band);
+                    const bool n1 = __builtin_fabsf(sig[k] - rgb[k].w) < 0x1p-12f;
+                    const bool n2 = __builtin_fabsf(sig[k] - con[k].w) < 0x1p-12f;
+                    near = near | (valid[k] & (n1 | n2));
                 }
                 exact = __any(near);
             }
@@ -367,13 +370,12 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
             }
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const float sigma = sig[k];
                 const float vis_raw = e[k];
                 const float oa = xyo[k].z * vis_raw;
                 const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
-                const bool ok = valid[k] && !(sigma < 0.f || alpha_raw < sx::kAlphaThreshold);
+                const bool ok = valid[k] & !((sig[k] < 0.f) | (alpha_raw < sx::kAlphaThreshold));
                 alpha[k] = ok ? alpha_raw : 0.0f;
-                vis[k] = (ok && oa <= sx::kMaxAlpha) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
+                vis[k] = (ok & (oa <= sx::kMaxAlpha)) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
             }
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -392,15 +394,20 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
                 const float v_sigma = -xyo[k].z * vis[k] * v_alpha;
                 const float dx = dxs[k], dy = dys[k];
                 const float vdx = v_sigma * dx, vdy = v_sigma * dy;
-                gv[k][3] = 0.5f * vdx * dx;
-                gv[k][4] = vdx * dy;
-                gv[k][5] = 0.5f * vdy * dy;
-                gv[k][0] = __builtin_fmaf(con[k].x, vdx, con[k].y * vdy);
-                gv[k][1] = __builtin_fmaf(con[k].y, vdx, con[k].z * vdy);
-                if (ABSGRAD) {
+                if (ABSGRAD) {  // per-pixel 2D gradients are needed for their absolute values
+                    gv[k][0] = __builtin_fmaf(con[k].x, vdx, con[k].y * vdy);
+                    gv[k][1] = __builtin_fmaf(con[k].y, vdx, con[k].z * vdy);
+                    gv[k][3] = 0.5f * vdx * dx;
+                    gv[k][5] = 0.5f * vdy * dy;
                     gv[k][9] = fabsf(gv[k][0]);
                     gv[k][10] = fabsf(gv[k][1]);
+                } else {  // moments: the conic and the halves are applied once per splat at the flush
+                    gv[k][0] = vdx;
+                    gv[k][1] = vdy;
+                    gv[k][3] = vdx * dx;
+                    gv[k][5] = vdy * dy;
                 }
+                gv[k][4] = vdx * dy;
                 gv[k][2] = vis[k] * v_alpha;
                 bdot = __builtin_fmaf(fac, cvc, bdot);
             }
@@ -422,6 +429,14 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
             for (int k = 0; k < NV; k++) {
                 v[k] = s_part[k * kThreads + tid];
                 any |= v[k] != 0.f;
+            }
+            if (!ABSGRAD) {  // sum_p v_sigma (a dx + b dy, b dx + c dy) and the halves of dx^2, dy^2
+                const float4 cn = s_con[tid];
+                const float sdx = v[0], sdy = v[1];
+                v[0] = __builtin_fmaf(cn.x, sdx, cn.y * sdy);
+                v[1] = __builtin_fmaf(cn.y, sdx, cn.z * sdy);
+                v[3] *= 0.5f;
+                v[5] *= 0.5f;
             }
             if (any) {
                 const int32_t gid = s_id[tid];
