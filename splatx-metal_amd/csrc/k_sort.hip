@@ -299,6 +299,70 @@ __global__ void __launch_bounds__(kThreads) k_os_hist(const K* __restrict__ keys
     }
 }
 
+// The same digit totals for keys of at most kFullBits significant bits: one LDS counter per key
+// value (2^key_bits of them, dynamic LDS), one add per key, then each pass's digit totals are sums
+// of those counters. With few digit values (a 13-bit tile id sorts as 128 + 64 bins) a wave's 64
+// random keys would collide on the same digit counter and serialize; over 8192 key counters they
+// rarely do, and there is one add per key instead of one per pass.
+constexpr uint32_t kFullBits = 14;
+// blocks of the histogram kernels: each adds its digit counts to the same few totals, and adds to one
+// address serialize, so the grid is kept near the CU count (grid-stride over the chunks)
+constexpr int kHistBlocks = 512;
+template <class K>
+__global__ void __launch_bounds__(kThreads) k_os_hist_full(const K* __restrict__ keys, int64_t n, int passes, int dbits,
+                                                           uint32_t key_bits, uint32_t* __restrict__ totals,
+                                                           uint32_t* __restrict__ status0, int64_t status_words,
+                                                           uint32_t* __restrict__ counters) {
+    extern __shared__ uint32_t hf[];
+    __shared__ uint32_t s_dig[kBins];
+    const uint32_t nb = 1u << key_bits;
+    for (uint32_t i = threadIdx.x; i < nb; i += kThreads) hf[i] = 0;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < status_words; i += (int64_t)gridDim.x * kThreads)
+        status0[i] = 0u;
+    if (blockIdx.x == 0 && threadIdx.x < kMaxPassesOs) counters[threadIdx.x] = 0u;
+    __syncthreads();
+    const uint32_t kmask = nb - 1u;
+    const int64_t chunks = (n + kTile - 1) / kTile;
+    for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const int64_t base = c * kTile;
+        K key[kRounds];
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const int64_t idx = base + r * kThreads + threadIdx.x;
+            key[r] = idx < n ? keys[idx] : K(0);
+        }
+#pragma unroll
+        for (int r = 0; r < kRounds; r++)
+            if (base + r * kThreads + threadIdx.x < n) atomicAdd(&hf[static_cast<uint32_t>(key[r]) & kmask], 1u);
+    }
+    __syncthreads();
+    // pass p, digit d (width w at shift s) counts the key values (hi << (s + w)) | (d << s) | lo, i.e.
+    // the j-th of its 2^(key_bits - w) counters is j = hi 2^s + lo; the 256 threads split the digits'
+    // counters evenly and add their partial sums to the totals
+    for (int p = 0; p < passes; p++) {
+        const int s = dbits * p;
+        const uint32_t dm = digit_mask(p, dbits, key_bits);
+        const int w = __popc(dm);
+        const uint32_t per_digit = nb >> w;                        // counters per digit
+        const uint32_t tpd = kThreads >> w;                        // threads per digit (w <= 8)
+        const uint32_t d = threadIdx.x >> (8 - w);                 // this thread's digit
+        const uint32_t span = per_digit / tpd ? per_digit / tpd : 1u;
+        const uint32_t j0 = (threadIdx.x & (tpd - 1)) * span;
+        uint32_t acc = 0;
+        if (j0 < per_digit)
+            for (uint32_t j = j0; j < j0 + span && j < per_digit; j++)
+                acc += hf[((j >> s) << (s + w)) | (d << s) | (j & ((1u << s) - 1u))];
+        // one global add per digit and block: the totals are few addresses that every block adds to,
+        // and adds to one address serialize
+        s_dig[threadIdx.x] = 0;
+        __syncthreads();
+        if (acc) atomicAdd(&s_dig[d], acc);
+        __syncthreads();
+        if (threadIdx.x <= dm && s_dig[threadIdx.x]) atomicAdd(&totals[p * kBins + threadIdx.x], s_dig[threadIdx.x]);
+        __syncthreads();
+    }
+}
+
 // totals[p][d] -> base[p][d] = keys of digits < d (exclusive scan per pass); totals left as is
 __global__ void __launch_bounds__(kThreads) k_os_scan(const uint32_t* __restrict__ totals, int passes,
                                                       uint32_t* __restrict__ base) {
@@ -481,9 +545,13 @@ int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t
     hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins,
                        clear_err ? err : nullptr);
     if (n < (int64_t{1} << 30)) {  // onesweep: counts and prefixes fit the 30-bit status words
-        const int hist_blocks = std::min(tiles, 2048);
-        hipLaunchKernelGGL(k_os_hist<K>, dim3(hist_blocks), dim3(kThreads), 0, s, kin, n, passes, dbits, key_bits,
-                           totals, hist, hist_n, counters);
+        const int hist_blocks = std::min(tiles, kHistBlocks);
+        if (key_bits <= kFullBits)
+            hipLaunchKernelGGL(k_os_hist_full<K>, dim3(hist_blocks), dim3(kThreads), sizeof(uint32_t) << key_bits, s,
+                               kin, n, passes, dbits, key_bits, totals, hist, hist_n, counters);
+        else
+            hipLaunchKernelGGL(k_os_hist<K>, dim3(hist_blocks), dim3(kThreads), 0, s, kin, n, passes, dbits,
+                               key_bits, totals, hist, hist_n, counters);
         hipLaunchKernelGGL(k_os_scan, dim3(1), dim3(kThreads), 0, s, totals, passes, bases);
         uint32_t* st[2] = {hist, status_b};
         for (int p = 0; p < passes; p++) {
