@@ -245,7 +245,11 @@ constexpr uint32_t kFlagAgg = 1u << 30;
 constexpr uint32_t kFlagInc = 2u << 30;
 constexpr uint32_t kValMask = (1u << 30) - 1u;
 constexpr uint32_t kSpinLimit = 1u << 20;
-constexpr int kLook = 8;  // predecessor words per look-back round trip
+constexpr int kLook = 8;  // predecessor words per lane and look-back round trip
+// A pass with 2^w < 256 digit values gives each digit G = min(256 / 2^w, kLookLanes) adjacent lanes
+// for its look-back, so a round trip reads G * kLook predecessors: the chain of inclusive prefixes
+// then advances G times faster, which is what bounds a pass over many tiles.
+constexpr int kLookLanes = 16;
 
 __device__ __forceinline__ uint32_t ld_status(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -386,6 +390,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     __shared__ uint32_t s_lstart[kBins];
     __shared__ uint32_t s_woff[kWaves][kBins];
     __shared__ uint32_t s_wave[kWaves];
+    __shared__ uint32_t s_cnt[kBins];  // this tile's count of each digit
     __shared__ uint32_t s_tile;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -441,8 +446,8 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     }
     // publish this tile's digit counts now; the look-back for the prefixes of the tiles before it
     // waits until the tile has been reordered in LDS, which gives them time to finish theirs
-    uint32_t* my = status + (size_t)tile * kBins + tid;
-    st_status(my, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
+    st_status(status + (size_t)tile * kBins + tid, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
+    s_cnt[tid] = tile_count;
     __syncthreads();
     uint32_t* woff = s_woff[wave];
 #pragma unroll
@@ -460,31 +465,55 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    // look back (thread = digit): kLook predecessors' words per round trip, newest first, adding
-    // counts until an inclusive prefix; then publish this tile's inclusive prefix
-    uint32_t excl = 0;
-    if (tile > 0) {
+    // look back: the G lanes of digit d read kLook predecessors' words each per round trip, lane s
+    // the s-th run of kLook below j, newest first; the group adds counts up to the newest inclusive
+    // prefix among them, or up to the newest word not yet published and retries from there
+    const int bins = static_cast<int>(mask) + 1;
+    const int G = min(kThreads / bins, kLookLanes);  // a power of two dividing 64
+    if (tile == 0) {
+        s_gstart[tid] = digit_base[tid];
+    } else if (tid < bins * G) {
+        const int d = tid / G, sub = tid & (G - 1);
+        const int gbase = lane & ~(G - 1);
+        const uint64_t gmask = (G == 64 ? ~0ull : ((1ull << G) - 1ull)) << gbase;
+        uint32_t excl = 0;
         int64_t j = (int64_t)tile - 1;
         uint32_t spins = 0;
-        while (j >= 0) {
+        for (;;) {  // the group's lanes take every branch together
+            const int64_t top = j - (int64_t)sub * kLook;
             uint32_t w[kLook];
 #pragma unroll
-            for (int q = 0; q < kLook; q++) w[q] = j - q >= 0 ? ld_status(status + (size_t)(j - q) * kBins + tid) : kFlagInc;
-            int adv = kLook;  // predecessors consumed this round
-            bool done = false;
+            for (int q = 0; q < kLook; q++)
+                w[q] = top - q >= 0 ? ld_status(status + (size_t)(top - q) * kBins + d) : kFlagInc;
+            uint32_t part = 0;
+            int stop = 0, at = kLook;  // stop: 1 = met an inclusive prefix, 2 = met an unpublished word at q = at
 #pragma unroll
             for (int q = 0; q < kLook; q++) {
-                if (!done && adv == kLook) {
+                if (stop == 0) {
                     const uint32_t f = w[q] & ~kValMask;
                     if (f == 0u) {
-                        adv = q;  // not published yet: retry from this tile
+                        stop = 2;
+                        at = q;
                     } else {
-                        if (j - q >= 0) excl += w[q] & kValMask;
-                        if (f == kFlagInc) done = true;
+                        part += w[q] & kValMask;
+                        if (f == kFlagInc) stop = 1;
                     }
                 }
             }
-            if (done) break;
+            uint32_t scan = part;  // inclusive over the group's lanes
+            for (int o = 1; o < G; o <<= 1) {
+                const uint32_t y = __shfl_up(scan, o, 64);
+                if (sub >= o) scan += y;
+            }
+            const uint64_t stops = __ballot(stop != 0) & gmask;
+            const int first = stops ? static_cast<int>(__builtin_ctzll(stops)) - gbase : G - 1;
+            excl += __shfl(scan, gbase + first, 64);
+            if (!stops) {
+                j -= (int64_t)G * kLook;
+                continue;
+            }
+            if (__shfl(stop, gbase + first, 64) == 1) break;
+            const int64_t adv = (int64_t)first * kLook + __shfl(at, gbase + first, 64);
             j -= adv;
             if (adv == 0) {
                 if (++spins > kSpinLimit) {
@@ -494,9 +523,11 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
                 __builtin_amdgcn_s_sleep(1);
             }
         }
-        st_status(my, kFlagInc | (excl + tile_count));
+        if (sub == 0) {
+            st_status(status + (size_t)tile * kBins + d, kFlagInc | (excl + s_cnt[d]));
+            s_gstart[d] = digit_base[d] + excl;
+        }
     }
-    s_gstart[tid] = digit_base[tid] + excl;
     if (status_next) status_next[(size_t)tile * kBins + tid] = 0u;
     __syncthreads();
     for (int p = tid; p < tile_n; p += kThreads) {
