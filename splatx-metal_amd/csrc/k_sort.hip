@@ -377,7 +377,29 @@ __global__ void __launch_bounds__(kThreads) k_os_scan(const uint32_t* __restrict
     }
 }
 
-template <class K>
+// Lanes of the wave (among `valid_mask`) whose digit, the low NB bits of x, equals this lane's: one
+// ballot per bit, each lane collecting the lanes that differ from it in that bit.
+template <int NB>
+__device__ __forceinline__ uint64_t digit_match_bits(uint32_t x, uint64_t valid_mask) {
+    uint32_t mis_lo = 0u, mis_hi = 0u;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(x), b, 1));  // 0 or ~0
+        const uint64_t bal = __ballot(m != 0u);
+        mis_lo |= static_cast<uint32_t>(bal) ^ m;
+        mis_hi |= static_cast<uint32_t>(bal >> 32) ^ m;
+    }
+    return valid_mask & ~((static_cast<uint64_t>(mis_hi) << 32) | mis_lo);
+}
+
+// Set bits of `mask` in the lanes below this one.
+__device__ __forceinline__ uint32_t lanes_below_count(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// NB = the digit's width in bits (mask = 2^NB - 1).
+template <class K, int NB>
 __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin, const int32_t* __restrict__ vin,
                                                       K* __restrict__ kout, int32_t* __restrict__ vout,
                                                       int64_t n, int shift, uint32_t mask, const uint32_t* __restrict__ digit_base,
@@ -386,7 +408,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     constexpr int kPerWave = kTile / kWaves;  // 1024
     __shared__ K s_k[kTile];
     __shared__ int32_t s_v[kTile];
-    __shared__ uint32_t s_gstart[kBins];
+    __shared__ uint32_t s_gstart[kBins];  // global start of this tile's run of each digit, minus its local start
     __shared__ uint32_t s_lstart[kBins];
     __shared__ uint32_t s_woff[kWaves][kBins];
     __shared__ uint32_t s_wave[kWaves];
@@ -403,27 +425,38 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
     K key[kRounds];
     int32_t val[kRounds];
+    if (tile_n == kTile) {  // uniform
 #pragma unroll
-    for (int r = 0; r < kRounds; r++) {
-        const int i = wave * kPerWave + r * 64 + lane;
-        key[r] = i < tile_n ? kin[base + i] : K(0);
-        val[r] = i < tile_n ? vin[base + i] : 0;
+        for (int r = 0; r < kRounds; r++) {
+            const int i = wave * kPerWave + r * 64 + lane;
+            key[r] = kin[base + i];
+            val[r] = vin[base + i];
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const int i = wave * kPerWave + r * 64 + lane;
+            key[r] = i < tile_n ? kin[base + i] : K(0);
+            val[r] = i < tile_n ? vin[base + i] : 0;
+        }
     }
-    const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    uint8_t rank[kRounds];
-    uint8_t cnt[kRounds];
+    // per-wave digit counts, rounds in order; off[r] = the key's place among the wave's keys of its
+    // digit (keys of earlier rounds, then lanes below it with the same digit). All lanes read the
+    // digit's running count before one leader lane per digit group advances it.
+    uint32_t off[kRounds];
+    uint32_t* woff = s_woff[wave];
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
-        const uint32_t d = static_cast<uint32_t>(key[r] >> shift) & mask;
-        const uint64_t match = digit_match(d, valid);
-        rank[r] = static_cast<uint8_t>(__popcll(match & lanes_below));
-        cnt[r] = 0;
-        if (valid && rank[r] == 0) {
-            const uint32_t c = static_cast<uint32_t>(__popcll(match));
-            cnt[r] = static_cast<uint8_t>(c - 1);
-            s_woff[wave][d] += c;
-        }
+        const uint32_t x = static_cast<uint32_t>(key[r] >> shift);
+        const uint32_t d = x & mask;
+        const uint64_t match = digit_match_bits<NB>(x, __ballot(valid));
+        const uint32_t rank = lanes_below_count(match);
+        const uint32_t prior = valid ? woff[d] : 0u;
+        __builtin_amdgcn_wave_barrier();
+        if (valid && rank == 0u) woff[d] = prior + static_cast<uint32_t>(__popcll(match));
+        __builtin_amdgcn_wave_barrier();
+        off[r] = prior + rank;
     }
     __syncthreads();
     uint32_t tile_count;
@@ -449,20 +482,14 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     st_status(status + (size_t)tile * kBins + tid, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
     s_cnt[tid] = tile_count;
     __syncthreads();
-    uint32_t* woff = s_woff[wave];
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
         if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
-        const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
-        const uint32_t digit = static_cast<uint32_t>(key[r] >> shift) & mask;
-        if (valid) {
-            const uint32_t pos = woff[digit] + rank[r];
+        if (wave * kPerWave + r * 64 + lane < tile_n) {
+            const uint32_t pos = woff[static_cast<uint32_t>(key[r] >> shift) & mask] + off[r];
             s_k[pos] = key[r];
             s_v[pos] = val[r];
         }
-        __builtin_amdgcn_wave_barrier();
-        if (valid && rank[r] == 0) woff[digit] += static_cast<uint32_t>(cnt[r]) + 1u;
-        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
     // look back: the G lanes of digit d read kLook predecessors' words each per round trip, lane s
@@ -471,7 +498,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     const int bins = static_cast<int>(mask) + 1;
     const int G = min(kThreads / bins, kLookLanes);  // a power of two dividing 64
     if (tile == 0) {
-        s_gstart[tid] = digit_base[tid];
+        s_gstart[tid] = digit_base[tid] - s_lstart[tid];
     } else if (tid < bins * G) {
         const int d = tid / G, sub = tid & (G - 1);
         const int gbase = lane & ~(G - 1);
@@ -525,16 +552,16 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
         }
         if (sub == 0) {
             st_status(status + (size_t)tile * kBins + d, kFlagInc | (excl + s_cnt[d]));
-            s_gstart[d] = digit_base[d] + excl;
+            s_gstart[d] = digit_base[d] + excl - s_lstart[d];
         }
     }
     if (status_next) status_next[(size_t)tile * kBins + tid] = 0u;
     __syncthreads();
+    const uint32_t n32 = static_cast<uint32_t>(n);  // onesweep runs below 2^30 keys
     for (int p = tid; p < tile_n; p += kThreads) {
         const K k = s_k[p];
-        const uint32_t d = static_cast<uint32_t>(k >> shift) & mask;
-        const uint32_t g = s_gstart[d] + (static_cast<uint32_t>(p) - s_lstart[d]);
-        if (g < n) {  // always, unless the look-back gave up (err set): then no write lands out of range
+        const uint32_t g = s_gstart[static_cast<uint32_t>(k >> shift) & mask] + static_cast<uint32_t>(p);
+        if (g < n32) {  // always, unless the look-back gave up (err set): then no write lands out of range
             kout[g] = k;
             vout[g] = s_v[p];
         }
@@ -542,6 +569,27 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
 }
 
 int tiles_for(int64_t n) { return static_cast<int>((n + kTile - 1) / kTile); }
+
+// One onesweep pass over the digit of `mask`'s width at `shift`.
+template <class K>
+void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, K* kout, int32_t* vout, int64_t n,
+                    int shift, uint32_t mask, const uint32_t* digit_base, uint32_t* status, uint32_t* status_next,
+                    uint32_t* counter, uint32_t* err) {
+#define SX_OS_PASS(NB)                                                                                          \
+    hipLaunchKernelGGL((k_os_pass<K, NB>), dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, mask, \
+                       digit_base, status, status_next, counter, err)
+    switch (__builtin_popcount(mask)) {
+        case 1: SX_OS_PASS(1); break;
+        case 2: SX_OS_PASS(2); break;
+        case 3: SX_OS_PASS(3); break;
+        case 4: SX_OS_PASS(4); break;
+        case 5: SX_OS_PASS(5); break;
+        case 6: SX_OS_PASS(6); break;
+        case 7: SX_OS_PASS(7); break;
+        default: SX_OS_PASS(8); break;
+    }
+#undef SX_OS_PASS
+}
 
 constexpr int kMaxPasses = 8;
 // scratch layout: a fixed header (digit totals and bases of up to 8 passes, the per-pass tile
@@ -587,8 +635,8 @@ int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t
         uint32_t* st[2] = {hist, status_b};
         for (int p = 0; p < passes; p++) {
             uint32_t* next = p + 1 < passes ? st[(p + 1) & 1] : nullptr;
-            hipLaunchKernelGGL(k_os_pass<K>, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, dbits * p,
-                               digit_mask(p, dbits, key_bits), bases + p * kBins, st[p & 1], next, counters + p, err);
+            launch_os_pass<K>(tiles, s, kin, vin, kout, vout, n, dbits * p, digit_mask(p, dbits, key_bits),
+                              bases + p * kBins, st[p & 1], next, counters + p, err);
             std::swap(kin, kout);
             std::swap(vin, vout);
         }
