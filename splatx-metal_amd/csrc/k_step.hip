@@ -208,49 +208,58 @@ __global__ void __launch_bounds__(kBlock) k_depth_keys(StepConst c, const float4
 }
 
 // Thread per position j of the depth order: Gaussian g = order[j] owns the output range
-// [cum[j-1], cum[j]) and fills it with its tile ids in the reference's emit order, value g. Tile
-// counts are heavy-tailed, so a Gaussian with few tiles writes them from its own lane, and the
-// others are taken one at a time by the whole wave: lane l evaluates line u0 + l of the sweep (its
-// cuts are a function of the line alone; the sweep's carried state is rebuilt with shuffles), a
-// wave scan of the line lengths places the lines, and lane e then writes entry e — consecutive
-// lanes on consecutive addresses, with no lane waiting on the longest Gaussian of its wave.
-constexpr int kEmitLaneMax = 64;  // tiles a Gaussian may have to be emitted by its own lane
-
-__device__ __forceinline__ float2 shfl_f2(sxd::F2 v, int src) {
-    return make_float2(__shfl(v.x, src, 64), __shfl(v.y, src, 64));
-}
-
-// The lanes of the wave hold lines u0 + lane (vmin, len; len 0 past the end). Writes the lines'
-// tiles at out0 + [0, total) and returns total; nothing at or past `end` (the Gaussian's range, which
-// the counts fix) is written. s_start, s_vmin: 64 ints each of this wave's LDS.
-template <class K>
-__device__ __forceinline__ int64_t wave_emit_lines(int u0, int vmin, int len, bool row_major, int tw, int g,
-                                                   int64_t out0, int64_t end, K* __restrict__ keys,
-                                                   int32_t* __restrict__ vals, int* s_start, int* s_vmin) {
+// [cum[j-1], cum[j]) and fills it with its tile ids in the reference's emit order, value g. A wave
+// works as a queue over the lines of its 64 Gaussians: each lane sets up its own Gaussian's sweep
+// (kept in LDS) and counts its lines; the wave then takes the lines of all 64 Gaussians 64 at a
+// time, lane l evaluating one line (its cuts are a function of the line alone), and writes the
+// chunk's tiles with lane e on entry e — consecutive lanes on consecutive addresses. Tile counts are
+// heavy-tailed, and no lane waits on the largest Gaussian of its wave, nor idles through a Gaussian
+// of a few lines. A Gaussian of at most kEmitLaneMax tiles is written by its own lane instead (cheaper
+// than a queue round for a handful of tiles).
+constexpr int kEmitLaneMax = 16;
+__device__ __forceinline__ int wave_incl_scan(int v) {
     const int lane = threadIdx.x & 63;
-    int incl = len;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
+        const int y = __shfl_up(v, o, 64);
+        if (lane >= o) v += y;
     }
-    const int total = __shfl(incl, 63, 64);
-    s_start[lane] = incl - len;
-    s_vmin[lane] = vmin;
-    __builtin_amdgcn_wave_barrier();
-    const int n = static_cast<int>(min<int64_t>(total, end - out0));
-    for (int e = lane; e < n; e += 64) {
-        int l = 0;  // the last line starting at or before e (lines of length 0 share the next start)
+    return v;
+}
+
+// The last index l of a nondecreasing 64-entry array with a[l] <= x (a[0] <= x).
+__device__ __forceinline__ int last_le64(const int* a, int x) {
+    int l = 0;
 #pragma unroll
-        for (int step = 32; step > 0; step >>= 1)
-            if (s_start[l + step] <= e) l += step;
-        const int u = u0 + l;
-        const int v = s_vmin[l] + (e - s_start[l]);
-        keys[out0 + e] = static_cast<K>(row_major ? u * tw + v : v * tw + u);
-        vals[out0 + e] = g;
-    }
-    __builtin_amdgcn_wave_barrier();  // every lane has read s_start before the next chunk writes it
-    return total;
+    for (int step = 32; step > 0; step >>= 1)
+        if (a[l + step] <= x) l += step;
+    return l;
+}
+
+// Per wave: each Gaussian slot's sweep (the AccuSweep fields the cuts and spans read; with AABB
+// tiles, the row range and the column range) and its output range, then the current chunk's lines.
+struct EmitWave {
+    float4 geo0[64];  // A, B, C, disc
+    float4 geo1[64];  // t, p.x, p.y, bbox_max.x
+    float4 geo2[64];  // bbox_min.x, bbox_min.y, bbox_max.y, bbox_argmin.y
+    float4 geo3[64];  // bbox_argmax.y, rect_min_x (u of the first line), rect_min_y, rect_max_y (bits)
+    int is_y[64];
+    int line0[65];    // exclusive scan of the slots' line counts
+    int g[64];
+    long long out0[64], end[64], first[64];  // output range; wave entry index of the slot's first line
+    int estart[65];   // the chunk's lines: exclusive scan of their tile counts
+    int4 lin0[64];    // output position of the line's first tile (lo, hi), first tile id, id stride
+    int4 lin1[64];    // Gaussian, end of its output range (lo, hi)
+};
+
+// Upper cut of sweep line u: the cut at the line's far edge (u + 1) ts while that edge is <= bbox_max.x,
+// else the last such cut of the sweep, else the start value (the sweep's carried state, per line).
+__device__ __forceinline__ sxd::F2 line_upper_cut(const sxd::AccuSweep& sw, int u) {
+    const float e = static_cast<float>(u + 1) * 16.0f;
+    if (e <= sw.bbox_max.x) return sxd::accutile_cut(sw, e);
+    const float k = __builtin_floorf(sw.bbox_max.x * 0.0625f);  // the last edge index k with 16 k <= bbox_max.x
+    if (k >= static_cast<float>(sw.rect_min_x + 1)) return sxd::accutile_cut(sw, k * 16.0f);
+    return sxd::accutile_start(sw);
 }
 
 template <class K>
@@ -259,105 +268,136 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
                                                         const int32_t* __restrict__ order,
                                                         const int64_t* __restrict__ cum, K* __restrict__ keys,
                                                         int32_t* __restrict__ vals) {
-    __shared__ int s_start[kBlock / 64][64];
-    __shared__ int s_vmin[kBlock / 64][64];
+    __shared__ EmitWave s_w[kBlock / 64];
     const int j = blockIdx.x * kBlock + threadIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    EmitWave& W = s_w[threadIdx.x >> 6];
     const int tw = c.tile_width;
+    // this lane's Gaussian: its sweep and line count
     int64_t my0 = 0, cnt = 0;
-    int g = 0;
-    float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
-    int32_t rx = 0, ry = 0;
+    int g = 0, n_lines = 0;
+    sxd::AccuSweep sw = {};
     if (j < c.count) {
         my0 = j == 0 ? 0 : cum[j - 1];
         cnt = cum[j] - my0;
-        if (cnt > 0) {
+        if (cnt > 0 && cnt <= kEmitLaneMax) {
             g = order[j];
-            s0 = splats[3 * (size_t)g];
+            const float4 s0 = splats[3 * (size_t)g];
+            int64_t cur = my0;
+            const int64_t end = my0 + cnt;
+            auto line = [&](int32_t u, int32_t vmin, int32_t vmax, bool row_major) {
+                for (int32_t v = vmin; v < vmax && cur < end; ++v, ++cur) {
+                    keys[cur] = static_cast<K>(row_major ? u * tw + v : v * tw + u);
+                    vals[cur] = g;
+                }
+                return true;
+            };
             if (c.accutile) {
-                s1 = splats[3 * (size_t)g + 1];
+                const float4 s1 = splats[3 * (size_t)g + 1];
+                sxd::accutile_lines(s1.x, s1.y, s1.z, s0.z, s0.x, s0.y, 16.0f, tw, c.tile_height, line);
             } else {
-                rx = radii[2 * g];
-                ry = radii[2 * g + 1];
+                const sxd::TileRect r = sxd::aabb_rect(s0.x, s0.y, static_cast<float>(radii[2 * g]),
+                                                       static_cast<float>(radii[2 * g + 1]), 16.0f, tw, c.tile_height);
+                for (int32_t y = r.min_y; y < r.max_y; y++) line(y, r.min_x, r.max_x, true);
+            }
+        } else if (cnt > 0) {
+            g = order[j];
+            const float4 s0 = splats[3 * (size_t)g];
+            if (c.accutile) {
+                const float4 s1 = splats[3 * (size_t)g + 1];
+                if (sxd::accutile_setup(s1.x, s1.y, s1.z, s0.z, s0.x, s0.y, 16.0f, tw, c.tile_height, sw))
+                    n_lines = sw.rect_max_x - sw.rect_min_x;
+            } else {
+                const sxd::TileRect r = sxd::aabb_rect(s0.x, s0.y, static_cast<float>(radii[2 * g]),
+                                                       static_cast<float>(radii[2 * g + 1]), 16.0f, tw, c.tile_height);
+                sw.rect_min_x = r.min_y;  // lines are tile rows
+                sw.rect_min_y = r.min_x;
+                sw.rect_max_y = r.max_x;
+                sw.isY = true;
+                n_lines = r.max_x > r.min_x ? r.max_y - r.min_y : 0;
             }
         }
     }
-    if (cnt > 0 && cnt <= kEmitLaneMax) {
-        int64_t cur = my0;
-        auto line = [&](int32_t u, int32_t vmin, int32_t vmax, bool row_major) {
-            for (int32_t v = vmin; v < vmax; ++v) {
-                keys[cur] = static_cast<K>(row_major ? u * tw + v : v * tw + u);
-                vals[cur] = g;
-                ++cur;
+    W.geo0[lane] = make_float4(sw.A, sw.B, sw.C, sw.disc);
+    W.geo1[lane] = make_float4(sw.t, sw.p.x, sw.p.y, sw.bbox_max.x);
+    W.geo2[lane] = make_float4(sw.bbox_min.x, sw.bbox_min.y, sw.bbox_max.y, sw.bbox_argmin.y);
+    W.geo3[lane] = make_float4(sw.bbox_argmax.y, __int_as_float(sw.rect_min_x), __int_as_float(sw.rect_min_y),
+                               __int_as_float(sw.rect_max_y));
+    W.is_y[lane] = sw.isY ? 1 : 0;
+    W.g[lane] = g;
+    W.out0[lane] = my0;
+    W.end[lane] = my0 + cnt;
+    const int lincl = wave_incl_scan(n_lines);
+    W.line0[lane] = lincl - n_lines;
+    const int total_lines = __shfl(lincl, 63, 64);
+    if (lane == 63) W.line0[64] = total_lines;
+    __builtin_amdgcn_wave_barrier();
+    int64_t ebase = 0;  // wave entry index of the chunk's first tile
+    for (int q0 = 0; q0 < total_lines; q0 += 64) {  // uniform
+        const int q = q0 + lane;
+        const bool live = q < total_lines;
+        int k = 0, len = 0, key0 = 0, stride = 1;
+        if (live) {
+            k = last_le64(W.line0, q);
+            const float4 g3 = W.geo3[k];
+            const int u = __float_as_int(g3.y) + (q - W.line0[k]);
+            const int rmin_y = __float_as_int(g3.z), rmax_y = __float_as_int(g3.w);
+            int vmin = rmin_y, vmax = rmax_y;
+            const bool is_y = W.is_y[k] != 0;
+            if (c.accutile) {
+                const float4 g0 = W.geo0[k], g1 = W.geo1[k], g2 = W.geo2[k];
+                sxd::AccuSweep ls;
+                ls.A = g0.x; ls.B = g0.y; ls.C = g0.z; ls.disc = g0.w;
+                ls.t = g1.x; ls.p = {g1.y, g1.z};
+                ls.bbox_max = {g1.w, g2.z};
+                ls.bbox_min = {g2.x, g2.y};
+                ls.bbox_argmin = {0.f, g2.w};
+                ls.bbox_argmax = {0.f, g3.x};
+                ls.rect_min_x = __float_as_int(g3.y);
+                ls.rect_min_y = rmin_y;
+                ls.rect_max_y = rmax_y;
+                ls.rect_max_x = 0;  // not read by the cuts or spans
+                ls.isY = is_y;
+                const float min_line = static_cast<float>(u) * 16.0f;
+                const float max_line = min_line + 16.0f;
+                sxd::F2 lo;
+                if (u == ls.rect_min_x)
+                    lo = ls.bbox_min.x <= min_line ? sxd::accutile_cut(ls, min_line) : sxd::accutile_start(ls);
+                else
+                    lo = line_upper_cut(ls, u - 1);
+                const sxd::F2 hi = line_upper_cut(ls, u);
+                sxd::accutile_span(ls, min_line, max_line, lo, hi, 16.0f, vmin, vmax);
             }
-            return true;
-        };
-        if (c.accutile) {
-            sxd::accutile_lines(s1.x, s1.y, s1.z, s0.z, s0.x, s0.y, 16.0f, tw, c.tile_height, line);
-        } else {
-            const sxd::TileRect r = sxd::aabb_rect(s0.x, s0.y, static_cast<float>(rx), static_cast<float>(ry), 16.0f,
-                                                   tw, c.tile_height);
-            for (int32_t y = r.min_y; y < r.max_y; y++) line(y, r.min_x, r.max_x, true);
+            len = vmax > vmin ? vmax - vmin : 0;
+            key0 = is_y ? u * tw + vmin : vmin * tw + u;
+            stride = is_y ? 1 : tw;
         }
-    }
-    uint64_t pending = __ballot(cnt > kEmitLaneMax);
-    while (pending) {
-        const int src = static_cast<int>(__builtin_ctzll(pending));
-        pending &= pending - 1;
-        const int gg = __shfl(g, src, 64);
-        int64_t out0 = static_cast<int64_t>(
-            (static_cast<uint64_t>(static_cast<uint32_t>(__shfl(static_cast<int>(my0 >> 32), src, 64))) << 32) |
-            static_cast<uint32_t>(__shfl(static_cast<int>(my0), src, 64)));
-        const int64_t end = out0 + static_cast<int64_t>(__shfl(static_cast<int>(cnt), src, 64));
-        // the Gaussian's projected values from the lane that loaded them
-        const float mx = __shfl(s0.x, src, 64), my = __shfl(s0.y, src, 64);
-        if (c.accutile) {
-            const float op = __shfl(s0.z, src, 64);
-            const float ca = __shfl(s1.x, src, 64), cb = __shfl(s1.y, src, 64), cc = __shfl(s1.z, src, 64);
-            sxd::AccuSweep sw;
-            if (!sxd::accutile_setup(ca, cb, cc, op, mx, my, 16.0f, tw, c.tile_height, sw)) continue;
-            const float ts = 16.0f;
-            const float first_edge = sw.rect_min_x * ts;
-            const sxd::F2 start = sxd::accutile_start(sw);
-            sxd::F2 carry = start;  // upper cut of the line before the chunk
-            for (int u0 = sw.rect_min_x; u0 < sw.rect_max_x; u0 += 64) {
-                const int u = u0 + lane;
-                const bool valid = u < sw.rect_max_x;
-                // line u spans [u ts, (u + 1) ts): the sweep's running sums of ts are exact integers
-                const float min_line = static_cast<float>(u) * ts;
-                const float max_line = min_line + ts;
-                const bool cut = valid && max_line <= sw.bbox_max.x;  // true on a prefix of the lanes
-                sxd::F2 own = {0.f, 0.f};
-                if (cut) own = sxd::accutile_cut(sw, max_line);
-                const int n_cut = __popcll(__ballot(cut));
-                sxd::F2 imax_line = carry;
-                if (n_cut > 0) {
-                    const float2 last = shfl_f2(own, n_cut - 1);
-                    imax_line = {last.x, last.y};
-                }
-                if (cut) imax_line = own;
-                const float2 up = make_float2(__shfl_up(imax_line.x, 1, 64), __shfl_up(imax_line.y, 1, 64));
-                sxd::F2 imin_line = {up.x, up.y};
-                if (lane == 0) {
-                    if (u0 == sw.rect_min_x)
-                        imin_line = sw.bbox_min.x <= first_edge ? sxd::accutile_cut(sw, first_edge) : start;
-                    else imin_line = carry;
-                }
-                int32_t vmin = 0, vmax = 0;
-                if (valid) sxd::accutile_span(sw, min_line, max_line, imin_line, imax_line, ts, vmin, vmax);
-                const float2 c63 = shfl_f2(imax_line, 63);
-                carry = {c63.x, c63.y};
-                const int len = vmax > vmin ? vmax - vmin : 0;
-                out0 += wave_emit_lines(u0, vmin, len, sw.isY, tw, gg, out0, end, keys, vals, s_start[wave], s_vmin[wave]);
-            }
-        } else {
-            const float frx = static_cast<float>(__shfl(rx, src, 64)), fry = static_cast<float>(__shfl(ry, src, 64));
-            const sxd::TileRect r = sxd::aabb_rect(mx, my, frx, fry, 16.0f, tw, c.tile_height);
-            for (int y0 = r.min_y; y0 < r.max_y; y0 += 64) {
-                const int len = y0 + lane < r.max_y ? r.max_x - r.min_x : 0;
-                out0 += wave_emit_lines(y0, r.min_x, len, true, tw, gg, out0, end, keys, vals, s_start[wave], s_vmin[wave]);
+        const int eincl = wave_incl_scan(len);
+        const int estart = eincl - len;
+        const int chunk_total = __shfl(eincl, 63, 64);
+        if (live && q == W.line0[k]) W.first[k] = ebase + estart;
+        W.estart[lane] = live ? estart : chunk_total;
+        __builtin_amdgcn_wave_barrier();
+        if (live) {
+            const long long lbase = W.out0[k] + (ebase + estart - W.first[k]);
+            const long long lend = W.end[k];
+            W.lin0[lane] = make_int4(static_cast<int>(lbase), static_cast<int>(lbase >> 32), key0, stride);
+            W.lin1[lane] = make_int4(W.g[k], static_cast<int>(lend), static_cast<int>(lend >> 32), 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int e = lane; e < chunk_total; e += 64) {
+            const int l = last_le64(W.estart, e);
+            const int4 a = W.lin0[l], b = W.lin1[l];
+            const int i = e - W.estart[l];
+            const int64_t pos = ((static_cast<int64_t>(a.y) << 32) | static_cast<uint32_t>(a.x)) + i;
+            const int64_t end = (static_cast<int64_t>(b.z) << 32) | static_cast<uint32_t>(b.y);
+            if (pos < end) {
+                keys[pos] = static_cast<K>(a.z + i * a.w);
+                vals[pos] = b.x;
             }
         }
+        __builtin_amdgcn_wave_barrier();  // every lane is done with this chunk's lines
+        ebase += chunk_total;
     }
 }
 
