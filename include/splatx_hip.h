@@ -353,7 +353,7 @@ typedef struct {
     int64_t n_isects;        /* the sync-point readback */
     int64_t n_visible;       /* Gaussians with radii > 0 (device counter) */
     float* render_colors;    /* in: [H,W,3] host buffer to fill, or NULL for no readback */
-    uint32_t sort_key_bits;  /* out: significant bits of the step's sort keys (tile bits + compressed depth) */
+    uint32_t sort_key_bits;  /* out: significant bits of the step's sort keys (tile bits + 32 depth bits) */
 } sxh_step_outputs;
 
 int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor** out);
@@ -635,6 +635,10 @@ typedef struct {
 } sxh_exec_timing;
 int32_t sxh_exec_set_profiling(sxh_executor* e, int32_t enable);
 int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out);
+/* Whether the step's second segment (everything after the intersection-count readback) runs as a
+ * captured hipGraph (default 1) or as direct launches (0). Profiling always launches directly. No
+ * counterpart in the reference (its Metal command buffers are encoded per step). */
+int32_t sxh_exec_set_graph(sxh_executor* e, int32_t enable);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -66,8 +66,8 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->dkey_b.alloc(R);
             e->order_a.alloc(R);
             e->order_b.alloc(R);
-            e->n_vis.alloc(3);
-            e->vis_part.alloc(4 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
+            e->n_vis.alloc(2);
+            e->vis_part.alloc(2 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
             e->loss_dev.alloc(1);
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
@@ -86,6 +86,8 @@ void sxh_exec_destroy(sxh_executor* e) {
     (void)hipStreamSynchronize(e->b->stream);
     for (int k = 0; k < kMaxEvents; k++)
         if (e->ev[k]) (void)hipEventDestroy(e->ev[k]);
+    for (hipGraphExec_t x : e->graph_b)
+        if (x) (void)hipGraphExecDestroy(x);
     delete e;
 }
 
@@ -150,6 +152,13 @@ int32_t sxh_exec_set_profiling(sxh_executor* e, int32_t enable) {
     return guarded([&] {
         if (!e) invalid("TrainStepExecutor", "null executor");
         e->prof = enable != 0;
+    });
+}
+
+int32_t sxh_exec_set_graph(sxh_executor* e, int32_t enable) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor", "null executor");
+        e->use_graph = enable != 0;
     });
 }
 
@@ -221,106 +230,84 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     c.noise_scale = in->noise_scale;
     const sxk::Arena A = e->arena();
 
-    // ---- segment A: preprocess + scan ------------------------------------------------------------
+    // ---- segment A: preprocess + counts -----------------------------------------------------------
     e->mark("start");
     sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->grads.p, e->vis_part.p, e->n_vis.p, s);
     e->mark("preprocess");
     int64_t* hs = static_cast<int64_t*>(e->host_small.p);
-    // visible count, depth-bit range, intersection total
-    SXH_HIP(hipMemcpyAsync(&hs[0], e->n_vis.p, 24, hipMemcpyDeviceToHost, s));
-    SXH_HIP(hipGetLastError());
-    // ---- sync 1: n_isects (MetalBackend.cpp:1849-1858) --------------------------------------------
-    auto t0 = std::chrono::steady_clock::now();
-    SXH_HIP(hipStreamSynchronize(s));
-    e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    const int64_t n_isects = hs[2];
-    out->n_isects = n_isects;
-    out->sort_key_bits = 0;
-    out->n_visible = hs[0];
-    validate_n_isects_readback(n_isects, what);
-    e->ensure_isect(static_cast<size_t>(n_isects));
-    e->mark("sync1");
-    // depth keys: the depth bits of the visible Gaussians span [lo, hi]; storing depth - lo in just
-    // enough bits keeps the order and usually saves a radix pass
-    {
-        const uint64_t range = static_cast<uint64_t>(hs[1]);
-        const uint32_t lo = static_cast<uint32_t>(range), hi = static_cast<uint32_t>(range >> 32);
-        c.key_depth_bits = 32;
-        c.key_depth_base = 0;
-        if (out->n_visible > 0 && hi >= lo) {
-            const uint32_t span = hi - lo;
-            c.key_depth_bits = span ? 32u - static_cast<uint32_t>(__builtin_clz(span)) : 0u;
-            c.key_depth_base = lo;
+    // visible count, intersection total
+    SXH_HIP(hipMemcpyAsync(&hs[0], e->n_vis.p, 16, hipMemcpyDeviceToHost, s));
+    const float* gt = nullptr;
+    if (!fwd_only) {
+        if (use_gt_cache) {
+            gt = e->gt_cache.p + static_cast<size_t>(in->gt_index) * n_px;
+        } else {
+            SXH_HIP(hipMemcpyAsync(e->gt_stage.p, in->gt_rgb, n_px * 4, hipMemcpyHostToDevice, s));
+            gt = e->gt_stage.p;
         }
     }
-
-    // ---- segment B ---------------------------------------------------------------------------------
-    // intersections depth first (the Gaussians sorted by depth, tile ids emitted in that order, a
-    // stable sort on the tile bits): the order of the reference's (tile | depth) key sort
+    SXH_HIP(hipGetLastError());
+    const int64_t* n_isects_dev = reinterpret_cast<const int64_t*>(e->n_vis.p) + 1;
+    float* hloss = reinterpret_cast<float*>(&hs[3]);
+    *hloss = 0.0f;
+    int n_l1 = 0, n_ss = 0;
     int32_t* flat = e->vals_a.p;
-    if (n_isects > 0) {
-        out->sort_key_bits = c.key_depth_bits + c.tile_n_bits;
+
+    // ---- segment B: everything after the count. With n_dev the launches read the intersection count on
+    // the device (grids sized for the capacity), so they can be captured before the count is known.
+    auto launch_b = [&](int64_t n_host, const int64_t* n_dev) {
+        const int n_tiles = tw * th;
+        // intersections depth first (the Gaussians sorted by depth, tile ids emitted in that order, a
+        // stable sort on the tile bits): the order of the reference's (tile | depth) key sort
         sxk::step_depth_keys(c, e->splats.p, e->tiles.p, e->dkey_a.p, e->order_a.p, s);
-        const int wd = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, c.count,
-                                       c.key_depth_bits, e->sort_scratch.p, s, true);
+        const int wd = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, c.count, 32,
+                                       e->sort_scratch.p, s, true);
         const int32_t* order = wd ? e->order_b.p : e->order_a.p;
         e->mark("depth_sort");
         sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s, order);
         e->mark("scan");
-        const int n_tiles = tw * th;
+        int which = 0;
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
             uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
             sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->vals_a.p, s);
             e->mark("emit");
-            const int which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_isects, c.tile_n_bits,
-                                              e->sort_scratch.p, s, false);
+            which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits, e->sort_scratch.p, s,
+                                    false, n_dev);
             e->mark("sort");
-            flat = which ? e->vals_b.p : e->vals_a.p;
-            sxk::step_tile_offsets(which ? kb : ka, n_isects, n_tiles, e->offsets.p, s);
+            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         } else {
             uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
             uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
             sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->vals_a.p, s);
             e->mark("emit");
-            const int which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_isects, c.tile_n_bits,
-                                              e->sort_scratch.p, s, false);
+            which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits, e->sort_scratch.p, s,
+                                    false, n_dev);
             e->mark("sort");
-            flat = which ? e->vals_b.p : e->vals_a.p;
-            sxk::step_tile_offsets(which ? kb : ka, n_isects, n_tiles, e->offsets.p, s);
+            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         }
+        if (which < 0) throw std::runtime_error(std::string(what) + ": intersection capacity too large for a device count");
+        flat = which ? e->vals_b.p : e->vals_a.p;
         e->mark("offsets");
-    } else {
-        SXH_HIP(hipMemsetAsync(e->offsets.p, 0, static_cast<size_t>(tw) * th * 4, s));
-    }
-    sxk::RasterArgs ra{};
-    ra.splats = e->splats.p;
-    ra.offsets = e->offsets.p;
-    ra.flatten_ids = flat;
-    ra.I = 1;
-    ra.width = W;
-    ra.height = H;
-    ra.tile_width = tw;
-    ra.tile_height = th;
-    ra.n_isects = static_cast<int32_t>(n_isects);
-    sxk::raster_tile_order(e->offsets.p, tw * th, n_isects, e->tile_order.p, s);
-    ra.tile_order = e->tile_order.p;
-    sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
-    e->mark("raster_fwd");
-    float* hloss = reinterpret_cast<float*>(&hs[3]);
-    *hloss = 0.0f;
-    if (!fwd_only) {
-        const float* gt = nullptr;
-        if (use_gt_cache) gt = e->gt_cache.p + static_cast<size_t>(in->gt_index) * n_px;
-        else {
-            SXH_HIP(hipMemcpyAsync(e->gt_stage.p, in->gt_rgb, n_px * 4, hipMemcpyHostToDevice, s));
-            gt = e->gt_stage.p;
-        }
-        int n_l1 = 0, n_ss = 0;
+        sxk::RasterArgs ra{};
+        ra.splats = e->splats.p;
+        ra.offsets = e->offsets.p;
+        ra.flatten_ids = flat;
+        ra.I = 1;
+        ra.width = W;
+        ra.height = H;
+        ra.tile_width = tw;
+        ra.tile_height = th;
+        ra.n_isects = static_cast<int32_t>(n_host);
+        ra.n_isects_dev = n_dev;
+        sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev);
+        ra.tile_order = e->tile_order.p;
+        sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
+        e->mark("raster_fwd");
+        if (fwd_only) return;
         if (use_ssim) {
             n_ss = sxk::ssim_fwd_blocks(1, H, W, 3);
-            sxk::ssim_fwd(e->render.p, gt, 1, H, W, 3, 1, nullptr, e->cmu.p, e->csg.p, e->ccr.p,
-                          e->ssim_part.p, s);
+            sxk::ssim_fwd(e->render.p, gt, 1, H, W, 3, 1, nullptr, e->cmu.p, e->csg.p, e->ccr.p, e->ssim_part.p, s);
             e->mark("ssim_fwd");
             const float G = static_cast<float>(-static_cast<double>(e->d.ssim_weight) / static_cast<double>(map_n));
             n_l1 = sxk::step_ssim_bwd_blocks(H, W);
@@ -332,22 +319,72 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_l1_grad(e->render.p, gt, static_cast<int64_t>(n_px), e->v_render.p, e->l1_part.p, n_l1, s);
             e->mark("l1_grad");
         }
-        if (n_isects > 0) {
-            sxk::RasterBwdGrads gg{nullptr, nullptr, nullptr, nullptr, nullptr, e->grads.p};
-            sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
-            e->mark("raster_bwd");
-        }
+        sxk::RasterBwdGrads gg{nullptr, nullptr, nullptr, nullptr, nullptr, e->grads.p};
+        sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
+        e->mark("raster_bwd");
         sxk::step_postprocess(c, A, e->splats.p, e->grads.p, s);
         e->mark("postprocess");
         sxk::step_loss_final(e->l1_part.p, n_l1, e->ssim_part.p, n_ss, static_cast<double>(n_px),
                              static_cast<double>(map_n), e->d.ssim_weight, use_ssim ? 1 : 0, e->loss_dev.p, s);
         e->mark("loss");
-        SXH_HIP(hipMemcpyAsync(hloss, e->loss_dev.p, 4, hipMemcpyDeviceToHost, s));
+    };
+    // Segment B as a hipGraph (captured while the GPU runs segment A, replayed after the count; an
+    // executable graph per step kind is updated in place while the step's shape stays the same), unless
+    // per-kernel profiling is on or the capacity is past what the device-count sort handles.
+    const bool graph = e->use_graph && !e->prof && e->isect_cap < (size_t{1} << 30);
+    auto capture_b = [&]() {
+        hipGraph_t g = nullptr;
+        SXH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        try {
+            launch_b(static_cast<int64_t>(e->isect_cap), n_isects_dev);
+        } catch (...) {
+            (void)hipStreamEndCapture(s, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        SXH_HIP(hipStreamEndCapture(s, &g));
+        hipGraphExec_t& x = e->graph_b[fwd_only ? 1 : 0];
+        if (x) {
+            hipGraphNode_t err_node = nullptr;
+            hipGraphExecUpdateResult res{};
+            if (hipGraphExecUpdate(x, g, &err_node, &res) != hipSuccess || res != hipGraphExecUpdateSuccess) {
+                (void)hipGetLastError();
+                SXH_HIP(hipGraphExecDestroy(x));
+                x = nullptr;
+            }
+        }
+        if (!x) {
+            const hipError_t err = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            SXH_HIP(err);
+        } else {
+            SXH_HIP(hipGraphDestroy(g));
+        }
+    };
+    if (graph) capture_b();
+
+    // ---- sync 1: n_isects (MetalBackend.cpp:1849-1858) --------------------------------------------
+    auto t0 = std::chrono::steady_clock::now();
+    SXH_HIP(hipStreamSynchronize(s));
+    e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    const int64_t n_isects = hs[1];
+    out->n_isects = n_isects;
+    out->sort_key_bits = 32 + c.tile_n_bits;
+    out->n_visible = hs[0];
+    validate_n_isects_readback(n_isects, what);
+    e->mark("sync1");
+    const bool grown = static_cast<size_t>(n_isects) > e->isect_cap;
+    if (grown) e->ensure_isect(static_cast<size_t>(n_isects));
+    if (graph && e->isect_cap < (size_t{1} << 30)) {
+        if (grown) capture_b();  // new buffers: the captured graph is stale
+        SXH_HIP(hipGraphLaunch(e->graph_b[fwd_only ? 1 : 0], s));
+    } else {
+        launch_b(n_isects, nullptr);
     }
+    if (!fwd_only) SXH_HIP(hipMemcpyAsync(hloss, e->loss_dev.p, 4, hipMemcpyDeviceToHost, s));
     uint32_t* hsort = reinterpret_cast<uint32_t*>(&hs[4]);
     *hsort = 0;
-    if (n_isects > 0)
-        SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p), 4, hipMemcpyDeviceToHost, s));
+    SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p), 4, hipMemcpyDeviceToHost, s));
     if (render_to_dev)
         SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
     if (out->render_colors)

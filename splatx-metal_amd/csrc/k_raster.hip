@@ -137,7 +137,9 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     }
     const int32_t* offs = a.offsets + (size_t)img * n_tiles;
     const int32_t range_start = offs[tile];
-    const int32_t range_end = (img == a.I - 1 && tile == n_tiles - 1) ? a.n_isects : offs[tile + 1];
+    const int32_t range_end = (img == a.I - 1 && tile == n_tiles - 1)
+                                  ? (a.n_isects_dev ? static_cast<int32_t>(*a.n_isects_dev) : a.n_isects)
+                                  : offs[tile + 1];
     const float px = static_cast<float>(px_i) + 0.5f, py = static_cast<float>(py_i) + 0.5f;
     float T = 1.0f;
     int32_t cur = 0;
@@ -255,7 +257,9 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
                               : (size_t)img * a.height * a.width;
     const int32_t* offs = a.offsets + (size_t)img * n_tiles;
     const int32_t range_start = offs[tile];
-    const int32_t range_end = (img == a.I - 1 && tile == n_tiles - 1) ? a.n_isects : offs[tile + 1];
+    const int32_t range_end = (img == a.I - 1 && tile == n_tiles - 1)
+                                  ? (a.n_isects_dev ? static_cast<int32_t>(*a.n_isects_dev) : a.n_isects)
+                                  : offs[tile + 1];
     const float* bg = a.backgrounds ? a.backgrounds + img * 3 : nullptr;
     const float px = static_cast<float>(px_i) + 0.5f, py = static_cast<float>(py_i) + 0.5f;
     const float T_final = 1.0f - ralpha[pix];
@@ -477,8 +481,10 @@ namespace {
 // Counting sort of the tiles by descending intersection count (256 buckets of width w, w the
 // smallest power of two with max_count < 256 w), one workgroup.
 __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__ offsets, int n_tiles,
-                                                     int64_t n_isects, int32_t* __restrict__ order) {
+                                                     int64_t n_isects, int32_t* __restrict__ order,
+                                                     const int64_t* __restrict__ n_isects_dev) {
     __shared__ uint32_t s_hist[256];
+    if (n_isects_dev) n_isects = *n_isects_dev;
     __shared__ uint32_t s_max;
     const int t0 = threadIdx.x;
     if (t0 < 256) s_hist[t0] = 0;
@@ -510,9 +516,10 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
 }
 }  // namespace
 
-void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s) {
+void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s,
+                       const int64_t* n_isects_dev) {
     if (n_tiles <= 0) return;
-    hipLaunchKernelGGL(k_tile_order, dim3(1), dim3(1024), 0, s, offsets, n_tiles, n_isects, order);
+    hipLaunchKernelGGL(k_tile_order, dim3(1), dim3(1024), 0, s, offsets, n_tiles, n_isects, order, n_isects_dev);
 }
 
 void raster_fwd(const RasterArgs& a, float* rgb, float* alpha, int32_t* last, hipStream_t s) {
@@ -524,7 +531,7 @@ void raster_fwd(const RasterArgs& a, float* rgb, float* alpha, int32_t* last, hi
 void raster_bwd(const RasterArgs& a, const float* ralpha, const int32_t* last_ids, const float* v_rc,
                 const float* v_ra, const RasterBwdGrads& g, hipStream_t s) {
     const int blocks = a.I * a.tile_width * a.tile_height;
-    if (blocks <= 0 || a.n_isects <= 0) return;
+    if (blocks <= 0 || (!a.n_isects_dev && a.n_isects <= 0)) return;
     if (g.v_means2d_abs)
         hipLaunchKernelGGL(k_raster_bwd<true>, dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc, v_ra, g);
     else

@@ -265,8 +265,13 @@ __device__ __forceinline__ void st_status(uint32_t* p, uint32_t v) {
 template <class K>
 __global__ void __launch_bounds__(kThreads) k_os_hist(const K* __restrict__ keys, int64_t n, int passes, int dbits, uint32_t key_bits,
                                                       uint32_t* __restrict__ totals, uint32_t* __restrict__ status0,
-                                                      int64_t status_words, uint32_t* __restrict__ counters) {
+                                                      int64_t status_words, uint32_t* __restrict__ counters,
+                                                      const int64_t* __restrict__ n_dev) {
     __shared__ uint32_t h[kMaxPassesOs][kBins];
+    if (n_dev) {
+        n = *n_dev;
+        status_words = (n + kTile - 1) / kTile * kBins;
+    }
     for (int p = 0; p < kMaxPassesOs; p++) h[p][threadIdx.x] = 0;
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < status_words; i += (int64_t)gridDim.x * kThreads)
         status0[i] = 0u;
@@ -316,9 +321,13 @@ template <class K>
 __global__ void __launch_bounds__(kThreads) k_os_hist_full(const K* __restrict__ keys, int64_t n, int passes, int dbits,
                                                            uint32_t key_bits, uint32_t* __restrict__ totals,
                                                            uint32_t* __restrict__ status0, int64_t status_words,
-                                                           uint32_t* __restrict__ counters) {
+                                                           uint32_t* __restrict__ counters, const int64_t* __restrict__ n_dev) {
     extern __shared__ uint32_t hf[];
     __shared__ uint32_t s_dig[kBins];
+    if (n_dev) {
+        n = *n_dev;
+        status_words = (n + kTile - 1) / kTile * kBins;
+    }
     const uint32_t nb = 1u << key_bits;
     for (uint32_t i = threadIdx.x; i < nb; i += kThreads) hf[i] = 0;
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < status_words; i += (int64_t)gridDim.x * kThreads)
@@ -404,7 +413,8 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
                                                       K* __restrict__ kout, int32_t* __restrict__ vout,
                                                       int64_t n, int shift, uint32_t mask, const uint32_t* __restrict__ digit_base,
                                                       uint32_t* __restrict__ status, uint32_t* __restrict__ status_next,
-                                                      uint32_t* __restrict__ counter, uint32_t* __restrict__ err) {
+                                                      uint32_t* __restrict__ counter, uint32_t* __restrict__ err,
+                                                      const int64_t* __restrict__ n_dev) {
     constexpr int kPerWave = kTile / kWaves;  // 1024
     __shared__ K s_k[kTile];
     __shared__ int32_t s_v[kTile];
@@ -416,6 +426,10 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     __shared__ uint32_t s_tile;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
+    if (n_dev) {  // the grid is sized for a capacity: exactly one workgroup per tile of keys takes a tile
+        n = *n_dev;
+        if (static_cast<int64_t>(blockIdx.x) * kTile >= n) return;  // uniform
+    }
     if (tid == 0) s_tile = atomicAdd(counter, 1u);
 #pragma unroll
     for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
@@ -574,10 +588,10 @@ int tiles_for(int64_t n) { return static_cast<int>((n + kTile - 1) / kTile); }
 template <class K>
 void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, K* kout, int32_t* vout, int64_t n,
                     int shift, uint32_t mask, const uint32_t* digit_base, uint32_t* status, uint32_t* status_next,
-                    uint32_t* counter, uint32_t* err) {
+                    uint32_t* counter, uint32_t* err, const int64_t* n_dev) {
 #define SX_OS_PASS(NB)                                                                                          \
     hipLaunchKernelGGL((k_os_pass<K, NB>), dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, mask, \
-                       digit_base, status, status_next, counter, err)
+                       digit_base, status, status_next, counter, err, n_dev)
     switch (__builtin_popcount(mask)) {
         case 1: SX_OS_PASS(1); break;
         case 2: SX_OS_PASS(2); break;
@@ -597,9 +611,11 @@ constexpr int kMaxPasses = 8;
 // histogram, or the onesweep status words of alternate passes)
 constexpr int kHeaderWords = 2 * kMaxPasses * kBins + 64;
 
+// n_dev: when set, the key count is read on the device from *n_dev (at most n, the capacity the
+// grids are sized for), so the launches do not depend on it (a captured graph can replay them).
 template <class K>
 int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-                 void* scratch, bool clear_err, hipStream_t s) {
+                 void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev) {
     uint32_t* totals = static_cast<uint32_t*>(scratch);
     uint32_t* bases = totals + kMaxPasses * kBins;
     uint32_t* counters = bases + kMaxPasses * kBins;
@@ -613,6 +629,7 @@ int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t
         if (clear_err) hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, 0, err);
         return 0;
     }
+    if (n_dev && n >= (int64_t{1} << 30)) return -1;  // the three-launch path sizes its grids by the count
     const int tiles = std::max(1, tiles_for(n));
     const int64_t hist_n = (int64_t)tiles * kBins;
     uint32_t* hist = totals + kHeaderWords;
@@ -627,16 +644,16 @@ int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t
         const int hist_blocks = std::min(tiles, kHistBlocks);
         if (key_bits <= kFullBits)
             hipLaunchKernelGGL(k_os_hist_full<K>, dim3(hist_blocks), dim3(kThreads), sizeof(uint32_t) << key_bits, s,
-                               kin, n, passes, dbits, key_bits, totals, hist, hist_n, counters);
+                               kin, n, passes, dbits, key_bits, totals, hist, hist_n, counters, n_dev);
         else
             hipLaunchKernelGGL(k_os_hist<K>, dim3(hist_blocks), dim3(kThreads), 0, s, kin, n, passes, dbits,
-                               key_bits, totals, hist, hist_n, counters);
+                               key_bits, totals, hist, hist_n, counters, n_dev);
         hipLaunchKernelGGL(k_os_scan, dim3(1), dim3(kThreads), 0, s, totals, passes, bases);
         uint32_t* st[2] = {hist, status_b};
         for (int p = 0; p < passes; p++) {
             uint32_t* next = p + 1 < passes ? st[(p + 1) & 1] : nullptr;
             launch_os_pass<K>(tiles, s, kin, vin, kout, vout, n, dbits * p, digit_mask(p, dbits, key_bits),
-                              bases + p * kBins, st[p & 1], next, counters + p, err);
+                              bases + p * kBins, st[p & 1], next, counters + p, err, n_dev);
             std::swap(kin, kout);
             std::swap(vin, vout);
         }
@@ -668,18 +685,18 @@ uint32_t* sort_error_flag(void* scratch) {
 }
 
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-               void* scratch, hipStream_t s, bool clear_err) {
-    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s);
+               void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
+    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
 }
 
 int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-               void* scratch, hipStream_t s, bool clear_err) {
-    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s);
+               void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
+    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
 }
 
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-               void* scratch, hipStream_t s, bool clear_err) {
-    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s);
+               void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
+    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
 }
 
 } // namespace sxk

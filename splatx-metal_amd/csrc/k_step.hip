@@ -57,8 +57,7 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
                                                        float4* __restrict__ grads,
                                                        uint32_t* __restrict__ vis_part) {
-    __shared__ uint32_t s_vis[kBlock / 64], s_dmin[kBlock / 64], s_dmax[kBlock / 64], s_isect[kBlock / 64];
-    uint32_t dbits_min = 0xFFFFFFFFu, dbits_max = 0u;
+    __shared__ uint32_t s_vis[kBlock / 64], s_isect[kBlock / 64];
     uint32_t n_tiles_sum = 0;  // this lane's tile count; summed per block below
     const int i = blockIdx.x * kBlock + threadIdx.x;
     bool vis = false;
@@ -108,8 +107,6 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
                 cnt = (r.max_y - r.min_y) * (r.max_x - r.min_x);
             }
             splats[3 * (size_t)i] = make_float4(o.m2x, o.m2y, op_used, o.depth);
-            dbits_min = __float_as_uint(o.depth);
-            dbits_max = dbits_min;
             splats[3 * (size_t)i + 1] = make_float4(o.ca, o.cb, o.cc, o.comp);
             splats[3 * (size_t)i + 2] = make_float4(col[0], col[1], col[2], __uint_as_float(meta));
             const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -122,70 +119,51 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
         tiles[i] = cnt;
         n_tiles_sum = static_cast<uint32_t>(cnt);
     }
-    // visible count and depth-bit range per block (plain stores; a single global counter would
-    // serialize every wave)
+    // visible count and tile count per block (plain stores; a single global counter would serialize
+    // every wave)
     const unsigned long long bal = __ballot(vis);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        dbits_min = min(dbits_min, static_cast<uint32_t>(__shfl_xor(static_cast<int>(dbits_min), o, 64)));
-        dbits_max = max(dbits_max, static_cast<uint32_t>(__shfl_xor(static_cast<int>(dbits_max), o, 64)));
-        n_tiles_sum += static_cast<uint32_t>(__shfl_xor(static_cast<int>(n_tiles_sum), o, 64));
-    }
+    for (int o = 32; o > 0; o >>= 1) n_tiles_sum += static_cast<uint32_t>(__shfl_xor(static_cast<int>(n_tiles_sum), o, 64));
     if (sxd::lane_id() == 0) {
         s_vis[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal));
-        s_dmin[threadIdx.x >> 6] = dbits_min;
-        s_dmax[threadIdx.x >> 6] = dbits_max;
         s_isect[threadIdx.x >> 6] = n_tiles_sum;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t t = 0, lo = 0xFFFFFFFFu, hi = 0u, isect = 0u;
+        uint32_t t = 0, isect = 0u;
 #pragma unroll
         for (int w = 0; w < kBlock / 64; w++) {
             t += s_vis[w];
-            lo = min(lo, s_dmin[w]);
-            hi = max(hi, s_dmax[w]);
             isect += s_isect[w];
         }
-        vis_part[4 * blockIdx.x] = t;
-        vis_part[4 * blockIdx.x + 1] = lo;
-        vis_part[4 * blockIdx.x + 2] = hi;
-        vis_part[4 * blockIdx.x + 3] = isect;
+        vis_part[2 * blockIdx.x] = t;
+        vis_part[2 * blockIdx.x + 1] = isect;
     }
 }
 
-// sum of the per-block visible counts, the overall depth-bit range and the intersection total (one
-// block); out = {u64 visible count, u32 min | u32 max << 32, u64 intersections}
+// sum of the per-block visible counts and tile counts (one block); out = {u64 visible count, u64
+// intersections}
 __global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict__ part, int n,
                                                       unsigned long long* __restrict__ out) {
     __shared__ unsigned long long s_red[kBlock], s_isect[kBlock];
-    __shared__ uint32_t s_lo[kBlock], s_hi[kBlock];
     unsigned long long acc = 0, isect = 0;
-    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
     for (int k = threadIdx.x; k < n; k += kBlock) {
-        acc += part[4 * k];
-        lo = min(lo, part[4 * k + 1]);
-        hi = max(hi, part[4 * k + 2]);
-        isect += part[4 * k + 3];
+        acc += part[2 * k];
+        isect += part[2 * k + 1];
     }
     s_red[threadIdx.x] = acc;
     s_isect[threadIdx.x] = isect;
-    s_lo[threadIdx.x] = lo;
-    s_hi[threadIdx.x] = hi;
     __syncthreads();
     for (int o = kBlock / 2; o > 0; o >>= 1) {
         if (threadIdx.x < o) {
             s_red[threadIdx.x] += s_red[threadIdx.x + o];
             s_isect[threadIdx.x] += s_isect[threadIdx.x + o];
-            s_lo[threadIdx.x] = min(s_lo[threadIdx.x], s_lo[threadIdx.x + o]);
-            s_hi[threadIdx.x] = max(s_hi[threadIdx.x], s_hi[threadIdx.x + o]);
         }
         __syncthreads();
     }
     if (threadIdx.x == 0) {
         out[0] = s_red[0];
-        out[1] = (static_cast<unsigned long long>(s_hi[0]) << 32) | s_lo[0];
-        out[2] = s_isect[0];
+        out[1] = s_isect[0];
     }
 }
 
@@ -196,14 +174,15 @@ __global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict
 // alone finishes the job: within a tile the order is the depth order, ties by index — the same
 // permutation, for two radix passes over the intersections instead of five or six.
 
-// depth sort keys: depth bits - key_depth_base for Gaussians with tiles, 0 for the rest (which
-// emit nothing, so their place in the order does not matter); values = Gaussian index
+// depth sort keys: the depth's float bits for Gaussians with tiles (a visible depth is positive, so
+// its bits order as the depths do), 0 for the rest (which emit nothing, so their place in the order
+// does not matter); values = Gaussian index
 __global__ void __launch_bounds__(kBlock) k_depth_keys(StepConst c, const float4* __restrict__ splats,
                                                        const int32_t* __restrict__ tiles,
                                                        uint32_t* __restrict__ keys, int32_t* __restrict__ vals) {
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= c.count) return;
-    keys[i] = tiles[i] > 0 ? __float_as_uint(splats[3 * (size_t)i].w) - c.key_depth_base : 0u;
+    keys[i] = tiles[i] > 0 ? __float_as_uint(splats[3 * (size_t)i].w) : 0u;
     vals[i] = i;
 }
 
@@ -405,9 +384,10 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
 // tiles) — the isect_offset_encode contract for one image
 template <class K>
 __global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ keys, int64_t n, int n_tiles,
-                                                         int32_t* __restrict__ off) {
+                                                         int32_t* __restrict__ off, const int64_t* __restrict__ n_dev) {
     const int t = blockIdx.x * kBlock + threadIdx.x;
     if (t >= n_tiles) return;
+    if (n_dev) n = *n_dev;
     int64_t lo = 0, hi = n;
     while (lo < hi) {
         const int64_t mid = lo + ((hi - lo) >> 1);
@@ -687,16 +667,18 @@ void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* r
                        cum, keys, vals);
 }
 
-void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s) {
+void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
+                       const int64_t* n_dev) {
     if (n_tiles <= 0) return;
     hipLaunchKernelGGL(k_tile_offsets<uint16_t>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles,
-                       offsets);
+                       offsets, n_dev);
 }
 
-void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s) {
+void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
+                       const int64_t* n_dev) {
     if (n_tiles <= 0) return;
     hipLaunchKernelGGL(k_tile_offsets<uint32_t>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles,
-                       offsets);
+                       offsets, n_dev);
 }
 
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads, hipStream_t s) {

@@ -72,6 +72,9 @@ struct sxh_executor {
     sxh::DevBuf<double> mc_cdf, mc_total;
     sxh::DevBuf<uint64_t> mc_raw, mc_mt;
     sxh::DevBuf<uint8_t> mc_cdf_scratch;
+    // segment B of the step as executable graphs: [0] training step, [1] forward only
+    hipGraphExec_t graph_b[2] = {nullptr, nullptr};
+    bool use_graph = true;
     // profiling
     bool prof = false;
     hipEvent_t ev[kMaxEvents] = {};

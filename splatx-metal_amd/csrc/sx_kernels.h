@@ -69,14 +69,19 @@ void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hip
 
 // Stable LSD radix sort of (key, i32 value) on bits [0, key_bits), keys u64, u32 or u16. Result
 // lands in keys_a/vals_a when the pass count is even, else in keys_b/vals_b; returns 0 or 1
-// accordingly. The scratch needs sort_scratch_bytes(n) bytes for n keys.
+// accordingly. The scratch needs sort_scratch_bytes(n) bytes for n keys. With n_dev the key count is
+// read on the device from *n_dev (<= n, which then only sizes the grids; n < 2^30, else -1 is
+// returned and nothing is launched): the launches no longer depend on the count.
 size_t sort_scratch_bytes(int64_t n);
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n,
-               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true);
+               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
+               const int64_t* n_dev = nullptr);
 int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
-               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true);
+               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
+               const int64_t* n_dev = nullptr);
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
-               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true);
+               uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
+               const int64_t* n_dev = nullptr);
 // device word in the sort's scratch that a sort sets non-zero when a tile's look-back gave up (a
 // broken invariant, never expected). A sort with clear_err zeroes it first; one without adds to
 // what the sorts before it left, so several sorts in a row can be checked with one read.
@@ -103,10 +108,14 @@ struct RasterArgs {
     // optional (I == 1): workgroup b renders tile tile_order[b] — heaviest tiles first, so the
     // last workgroups to start are the short ones; null = tile b
     const int32_t* tile_order;
+    // optional: the intersection count on the device (read instead of n_isects), so that the
+    // launches do not depend on it
+    const int64_t* n_isects_dev;
 };
 // tile_order for raster_fwd/raster_bwd: the n_tiles tile ids by descending intersection count
 // (counting sort on 256 buckets of the count; order within a bucket unspecified)
-void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s);
+void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s,
+                       const int64_t* n_isects_dev = nullptr);
 void raster_fwd(const RasterArgs& a, float* render_colors, float* render_alphas, int32_t* last_ids,
                 hipStream_t s);
 // Gradient outputs zeroed by the caller; packed as 3 x float4 per Gaussian when `packed_grads`

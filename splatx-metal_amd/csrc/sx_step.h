@@ -36,9 +36,6 @@ struct StepConst {
     int accutile;
     int tile_width, tile_height;
     uint32_t tile_n_bits;
-    // executor depth sort keys: depth bits - key_depth_base in key_depth_bits bits, the depth range
-    // of the visible Gaussians (order-preserving for positive depths)
-    uint32_t key_depth_bits, key_depth_base;
     float lr[6];
     float b1, b2, eps;
     float opacity_reg_w, scale_reg_w;
@@ -47,14 +44,14 @@ struct StepConst {
     float noise_scale;
 };
 
-// vis_part: 4 u32 per block (visible count, min and max depth bits, tile count); out_vis: {u64
-// visible count, u32 min | u32 max << 32 depth bits of the visible Gaussians, u64 intersections}
+// vis_part: 2 u32 per block (visible count, tile count); out_vis: {u64 visible count, u64
+// intersections}
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      float4* grads, uint32_t* vis_part, unsigned long long* out_vis, hipStream_t s);
-// number of blocks of step_preprocess (vis_part holds 4 u32 per block)
+// number of blocks of step_preprocess (vis_part holds 2 u32 per block)
 int step_preprocess_blocks(int64_t count);
-// depth-first intersections: depth keys of the Gaussians that emit (values = index) for a stable sort
-// on key_depth_bits; then, over that order, each Gaussian's tile ids at [cum[j-1], cum[j]) (cum =
+// depth-first intersections: depth keys of the Gaussians that emit (values = index) for a stable
+// 32-bit sort; then, over that order, each Gaussian's tile ids at [cum[j-1], cum[j]) (cum =
 // inclusive scan of the tile counts gathered through the order); after a stable sort of the tile
 // ids, offsets[t] = lower bound of t
 void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* tiles, uint32_t* keys, int32_t* vals,
@@ -63,8 +60,11 @@ void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* r
                       const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s);
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
                       const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s);
-void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s);
-void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s);
+// n_dev: the key count on the device, read instead of n
+void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
+                       const int64_t* n_dev = nullptr);
+void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
+                       const int64_t* n_dev = nullptr);
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
                       hipStream_t s);
 // Noise only (the forward-only path never calls it; a training step fuses it into postprocess).

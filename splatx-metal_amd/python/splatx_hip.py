@@ -759,7 +759,7 @@ class Executor:
         self._check(self.lib.sxh_exec_create(backend.handle, C.byref(d), C.byref(h)))
         self.h = h
         for n in ("sxh_exec_upload", "sxh_exec_download", "sxh_exec_step", "sxh_exec_set_gt_cache",
-                  "sxh_exec_render_to_gt_cache", "sxh_exec_set_profiling", "sxh_exec_get_timing",
+                  "sxh_exec_render_to_gt_cache", "sxh_exec_set_profiling", "sxh_exec_get_timing", "sxh_exec_set_graph",
                   "sxh_exec_mcmc_refine"):
             getattr(self.lib, n).restype = C.c_int32
         self.lib.sxh_exec_destroy.argtypes = [C.c_void_p]
@@ -935,6 +935,10 @@ class Executor:
 
     def set_profiling(self, enable: bool):
         self._check(self.lib.sxh_exec_set_profiling(self.h, int(bool(enable))))
+
+    def set_graph(self, enable: bool):
+        """Run the step's second segment as a captured hipGraph (default) or as direct launches."""
+        self._check(self.lib.sxh_exec_set_graph(self.h, int(bool(enable))))
 
     def get_timing(self):
         t = ExecTiming()
