@@ -141,7 +141,8 @@ def test_full_size_forward_matches_oracle(gpu):
 @pytest.mark.parametrize("isect", [sh.SXH_ISECT_ACCUTILE, sh.SXH_ISECT_AABB])
 def test_large_splats_forward_matches_oracle(gpu, isect):
     """Splats covering up to thousands of tiles, both sweep orientations and more than 64 tile lines
-    (the wave-cooperative emit, chunked over lines): n_isects exact, the render bit-identical."""
+    (the emit's line queue, whose chunks of 64 lines then split one Gaussian's lines and mix
+    Gaussians): n_isects exact, the render bit-identical."""
     sc = scene.make_scene(n=400, sh_degree=1, width=1100, height=1060, fx=500.0, seed=11, xy=2.0, z=(2.0, 5.0),
                           log_scale_mu=np.log(0.4), log_scale_sd=0.8)
     ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=1, ssim_weight=0.0, isect_mode=isect)
