@@ -160,31 +160,32 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             wm = wave_rows_mask(xyo, con, ty * 16);
         }
         build_wave_lists(wm, s_list, s_wc, s_len);
-        if (!done) {
-            const int len = s_len[wave];
-            for (int j = 0; j < len; j++) {
-                const int t = s_list[wave][j];
-                const float4 xyo = s_xyo[t];
-                const float4 con = s_con[t];
-                const float dx = xyo.x - px, dy = xyo.y - py;
-                const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
-                if (sigma > xyo.w) continue;  // provably below the alpha threshold
-                const float vis = exp_neg(sigma, xyo.w);
-                const float alpha = sxd::smin(sx::kMaxAlpha, xyo.z * vis);
-                if (sigma < 0.f || alpha < sx::kAlphaThreshold) continue;
-                const float next_T = T * (1.0f - alpha);
-                if (next_T <= sx::kTransmittanceThreshold) {
-                    done = true;
-                    break;
-                }
-                const float w = alpha * T;
-                const float4 c = s_rgb[t];
-                r0 = __builtin_fmaf(c.x, w, r0);
-                r1 = __builtin_fmaf(c.y, w, r1);
-                r2 = __builtin_fmaf(c.z, w, r2);
-                cur = bstart + t;
-                T = next_T;
-            }
+        // the wave walks its list together (index and count are wave-uniform); a lane takes a pair
+        // through selects rather than branches, and stops taking pairs once its T is spent
+        const int len = __builtin_amdgcn_readfirstlane(s_len[wave]);
+        for (int j = 0; j < len; j++) {
+            if (__all(done)) break;  // uniform
+            const int t = __builtin_amdgcn_readfirstlane(s_list[wave][j]);
+            const float4 xyo = s_xyo[t];
+            const float4 con = s_con[t];
+            const float dx = xyo.x - px, dy = xyo.y - py;
+            const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
+            bool take = !done && !(sigma > xyo.w);  // past the cutoff: provably below the alpha threshold
+            if (!__any(take)) continue;             // uniform: no lane of the wave needs the exponential
+            const float vis = exp_neg(sigma, xyo.w);
+            const float alpha = sxd::smin(sx::kMaxAlpha, xyo.z * vis);
+            take = take && !(sigma < 0.f) && !(alpha < sx::kAlphaThreshold);
+            const float next_T = T * (1.0f - alpha);
+            const bool spent = take && next_T <= sx::kTransmittanceThreshold;
+            done = done || spent;
+            take = take && !spent;
+            const float w = alpha * T;
+            const float4 c = s_rgb[t];
+            r0 = take ? __builtin_fmaf(c.x, w, r0) : r0;
+            r1 = take ? __builtin_fmaf(c.y, w, r1) : r1;
+            r2 = take ? __builtin_fmaf(c.z, w, r2) : r2;
+            cur = take ? bstart + t : cur;
+            T = take ? next_T : T;
         }
     }
     if (!inside) return;
