@@ -480,14 +480,28 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
 
 namespace {
 // Counting sort of the tiles by descending intersection count (256 buckets of width w, w the
-// smallest power of two with max_count < 256 w), one workgroup.
+// smallest power of two with max_count < 256 w), one workgroup. Most tiles share a few buckets, so a
+// wave's lanes with the same bucket are grouped (one ballot per bucket bit) and one leader lane adds
+// the group's size: the LDS adds then never collide within a wave. The order within a bucket is
+// arbitrary (the order is only the rasterisers' schedule).
+__device__ __forceinline__ uint64_t same_byte_lanes(uint32_t b, bool valid) {
+    uint64_t match = __ballot(valid);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const bool bit = (b >> k) & 1u;
+        const uint64_t bal = __ballot(bit);
+        match &= bit ? bal : ~bal;
+    }
+    return match;
+}
+
 __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__ offsets, int n_tiles,
                                                      int64_t n_isects, int32_t* __restrict__ order,
                                                      const int64_t* __restrict__ n_isects_dev) {
     __shared__ uint32_t s_hist[256];
-    if (n_isects_dev) n_isects = *n_isects_dev;
     __shared__ uint32_t s_max;
-    const int t0 = threadIdx.x;
+    if (n_isects_dev) n_isects = *n_isects_dev;
+    const int t0 = threadIdx.x, lane = t0 & 63;
     if (t0 < 256) s_hist[t0] = 0;
     if (t0 == 0) s_max = 0;
     __syncthreads();
@@ -495,11 +509,23 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
         const int64_t e = t + 1 < n_tiles ? offsets[t + 1] : n_isects;
         return static_cast<uint32_t>(e - offsets[t]);
     };
-    for (int t = t0; t < n_tiles; t += 1024) atomicMax(&s_max, count_of(t));
+    uint32_t mx = 0;
+    for (int t = t0; t < n_tiles; t += 1024) mx = max(mx, count_of(t));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), o, 64)));
+    if (lane == 0) atomicMax(&s_max, mx);
     __syncthreads();
     int shift = 0;
     while ((s_max >> shift) >= 256u) shift++;
-    for (int t = t0; t < n_tiles; t += 1024) atomicAdd(&s_hist[255u - (count_of(t) >> shift)], 1u);
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    // rounds are uniform over the workgroup (every thread runs ceil(n_tiles / 1024) of them)
+    for (int t1 = 0; t1 < n_tiles; t1 += 1024) {
+        const int t = t1 + t0;
+        const bool valid = t < n_tiles;
+        const uint32_t b = valid ? 255u - (count_of(t) >> shift) : 0u;
+        const uint64_t m = same_byte_lanes(b, valid);
+        if (valid && (m & below) == 0) atomicAdd(&s_hist[b], static_cast<uint32_t>(__popcll(m)));
+    }
     __syncthreads();
     if (t0 == 0) {  // exclusive prefix over 256 buckets
         uint32_t run = 0;
@@ -510,9 +536,16 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
         }
     }
     __syncthreads();
-    for (int t = t0; t < n_tiles; t += 1024) {
-        const uint32_t pos = atomicAdd(&s_hist[255u - (count_of(t) >> shift)], 1u);
-        order[pos] = t;
+    for (int t1 = 0; t1 < n_tiles; t1 += 1024) {
+        const int t = t1 + t0;
+        const bool valid = t < n_tiles;
+        const uint32_t b = valid ? 255u - (count_of(t) >> shift) : 0u;
+        const uint64_t m = same_byte_lanes(b, valid);
+        const int leader = m ? static_cast<int>(__builtin_ctzll(m)) : 0;
+        uint32_t base = 0;
+        if (valid && lane == leader) base = atomicAdd(&s_hist[b], static_cast<uint32_t>(__popcll(m)));
+        base = static_cast<uint32_t>(__shfl(static_cast<int>(base), leader, 64));
+        if (valid) order[base + static_cast<uint32_t>(__popcll(m & below))] = t;
     }
 }
 }  // namespace
