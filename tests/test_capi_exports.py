@@ -36,3 +36,14 @@ def test_abi_version_without_gpu():
     lib = ctypes.CDLL(LIB)
     lib.sxh_abi_version.restype = ctypes.c_int32
     assert lib.sxh_abi_version() == 1
+
+
+def test_executor_switches_reject_a_null_executor_without_gpu():
+    lib = ctypes.CDLL(LIB)
+    lib.sxh_last_error.restype = ctypes.c_char_p
+    for name in ("sxh_exec_set_graph", "sxh_exec_set_profiling"):
+        f = getattr(lib, name)
+        f.restype = ctypes.c_int32
+        f.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+        assert f(None, 1) != 0, name
+        assert b"null executor" in lib.sxh_last_error(), name
