@@ -257,6 +257,7 @@ def main():
         return ex.make_step_inputs(**dict(base, viewmat=poses[k], **extra), gt_index=k)
 
     steps = [step_inputs(k, count) for k in range(n_poses)]
+    steps0 = list(steps)  # the timed region's inputs as first built (MCMC rebuilds them as the count grows)
     n_tiles = ((sc.width + 15) // 16) * ((sc.height + 15) // 16)
     tile_bits = int(n_tiles - 1).bit_length()  # the tile id's bits (bits_for_count)
     out = sh.StepOutputs()
@@ -293,11 +294,18 @@ def main():
             counts.append(count)
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
-    # per-kernel times: the same poses again with HIP events between the kernels (profiling launches
-    # the kernels directly; their durations are those of the graph replays, which rocprof confirms)
+    # per-kernel times: the timed region's work again — the same start state, warm-up and poses — with
+    # HIP events between the kernels (profiling launches the kernels directly; their durations are
+    # those of the graph replays, which rocprof confirms). With MCMC the steps follow the timed loop's
+    # final state instead (its refines are not replayed).
+    if not mcmc:
+        ex.upload_params(p, m, v, arena)
+        for k in range(args.warmup):
+            if ex.step_raw(steps0[k][0], out) != 0:
+                raise RuntimeError(b.lib.sxh_last_error())
     ex.set_profiling(True)
     for k in range(args.warmup, n_poses):
-        rc = ex.step_raw(steps[k][0], out)
+        rc = ex.step_raw((steps if mcmc else steps0)[k][0], out)
         if rc != 0:
             raise RuntimeError(b.lib.sxh_last_error())
         for name, ms in ex.get_timing().items():
