@@ -95,10 +95,10 @@ int32_t sxh_make_binoms_lut(int32_t n_max, float* out) {
 // ---- fused_adam --------------------------------------------------------------------------------
 int32_t sxh_fused_adam(sxh_backend* b, const sxh_adam_inputs* in) {
     return guarded([&] {
-        need(b, "fused_adam", "backend");
         need(in, "fused_adam", "inputs");
-        if (in->n_elems == 0) return;  // dispatch skip (D8-6)
-        validate_adam(*in, "fused_adam");
+        if (in->n_elems != 0) validate_adam(*in, "fused_adam");  // empty: dispatch skip before validation (D8-6)
+        need(b, "fused_adam", "backend");
+        if (in->n_elems == 0) return;
         SXH_HIP(hipSetDevice(b->device));
         const size_t n = static_cast<size_t>(in->n_elems);
         auto p = upload(in->param, n, b->stream);
@@ -120,7 +120,6 @@ int32_t sxh_fused_adam(sxh_backend* b, const sxh_adam_inputs* in) {
 // ---- projection ------------------------------------------------------------------------------
 int32_t sxh_projection_fused_fwd(sxh_backend* b, const sxh_projection_inputs* in, sxh_projection_outputs* out) {
     return guarded([&] {
-        need(b, "projection_fused_fwd", "backend");
         need(in, "projection_fused_fwd", "inputs");
         need(out, "projection_fused_fwd", "outputs");
         validate_projection(*in, "projection_fused_fwd");
@@ -128,6 +127,7 @@ int32_t sxh_projection_fused_fwd(sxh_backend* b, const sxh_projection_inputs* in
         if (!out->radii || !out->means2d || !out->depths || !out->conics ||
             (in->calc_compensations && !out->compensations))
             invalid("projection_fused_fwd", "null output buffer");
+        need(b, "projection_fused_fwd", "backend");
         if (CN == 0) return;
         SXH_HIP(hipSetDevice(b->device));
         hipStream_t s = b->stream;
@@ -161,7 +161,6 @@ int32_t sxh_projection_fused_fwd(sxh_backend* b, const sxh_projection_inputs* in
 int32_t sxh_projection_fused_bwd(sxh_backend* b, const sxh_projection_inputs* in, const sxh_projection_grads_in* g,
                                  sxh_projection_grads* out) {
     return guarded([&] {
-        need(b, "projection_fused_bwd", "backend");
         need(in, "projection_fused_bwd", "inputs");
         need(g, "projection_fused_bwd", "grads_in");
         need(out, "projection_fused_bwd", "outputs");
@@ -176,6 +175,7 @@ int32_t sxh_projection_fused_bwd(sxh_backend* b, const sxh_projection_inputs* in
             need(out->v_scales, "projection_fused_bwd", "v_scales");
         }
         if (g->viewmats_grad) need(out->v_viewmats, "projection_fused_bwd", "v_viewmats");
+        need(b, "projection_fused_bwd", "backend");
         SXH_HIP(hipSetDevice(b->device));
         hipStream_t s = b->stream;
         auto means = upload(in->means, N * 3, s);
@@ -219,10 +219,10 @@ int32_t sxh_projection_fused_bwd(sxh_backend* b, const sxh_projection_inputs* in
 // ---- SH --------------------------------------------------------------------------------------------
 int32_t sxh_sh_fwd(sxh_backend* b, const sxh_sh_inputs* in, float* colors) {
     return guarded([&] {
-        need(b, "sh_fwd", "backend");
         need(in, "sh_fwd", "inputs");
         validate_sh(*in, "sh_fwd");
         const size_t BN = static_cast<size_t>(in->B * in->N);
+        need(b, "sh_fwd", "backend");
         if (BN == 0) return;
         need(colors, "sh_fwd", "colors");
         SXH_HIP(hipSetDevice(b->device));
@@ -243,13 +243,13 @@ int32_t sxh_sh_fwd(sxh_backend* b, const sxh_sh_inputs* in, float* colors) {
 
 int32_t sxh_sh_bwd(sxh_backend* b, const sxh_sh_inputs* in, const float* v_colors, float* v_coeffs, float* v_dirs) {
     return guarded([&] {
-        need(b, "sh_bwd", "backend");
         need(in, "sh_bwd", "inputs");
         validate_sh(*in, "sh_bwd");
         const size_t BN = static_cast<size_t>(in->B * in->N);
         const size_t NKD = static_cast<size_t>(in->N * in->K) * in->D;
         need(v_coeffs, "sh_bwd", "v_coeffs");
         if (in->compute_v_dirs) need(v_dirs, "sh_bwd", "v_dirs");
+        need(b, "sh_bwd", "backend");
         if (BN == 0) {
             std::fill(v_coeffs, v_coeffs + NKD, 0.0f);
             return;
@@ -277,7 +277,6 @@ int32_t sxh_sh_bwd(sxh_backend* b, const sxh_sh_inputs* in, const float* v_color
 // ---- isect / scan / sort / offsets ---------------------------------------------------------------
 int32_t sxh_isect_tiles(sxh_backend* b, const sxh_isect_inputs* in, sxh_isect_outputs* out) {
     return guarded([&] {
-        need(b, "isect_tiles", "backend");
         need(in, "isect_tiles", "inputs");
         need(out, "isect_tiles", "outputs");
         validate_isect(*in, "isect_tiles");
@@ -285,6 +284,7 @@ int32_t sxh_isect_tiles(sxh_backend* b, const sxh_isect_inputs* in, sxh_isect_ou
         out->tile_n_bits = sx::bits_for_count(static_cast<int64_t>(in->tile_width) * in->tile_height);
         out->image_n_bits = sx::bits_for_count(in->I);
         out->n_isects = 0;
+        need(b, "isect_tiles", "backend");
         if (n_el == 0) return;
         need(out->tiles_per_gauss, "isect_tiles", "tiles_per_gauss");
         SXH_HIP(hipSetDevice(b->device));
@@ -334,8 +334,8 @@ int32_t sxh_isect_tiles(sxh_backend* b, const sxh_isect_inputs* in, sxh_isect_ou
 
 int32_t sxh_prefix_scan_i64(sxh_backend* b, const int32_t* in, int64_t n, int64_t* out) {
     return guarded([&] {
-        need(b, "prefix_scan_i64", "backend");
         if (n < 0) invalid("prefix_scan_i64", "negative n");
+        need(b, "prefix_scan_i64", "backend");
         if (n == 0) return;
         need(in, "prefix_scan_i64", "in");
         need(out, "prefix_scan_i64", "out");
@@ -353,10 +353,10 @@ int32_t sxh_prefix_scan_i64(sxh_backend* b, const int32_t* in, int64_t n, int64_
 
 int32_t sxh_sort_isect(sxh_backend* b, const sxh_sort_inputs* in, uint64_t* keys_sorted, int32_t* values_sorted) {
     return guarded([&] {
-        need(b, "sort_isect", "backend");
         need(in, "sort_isect", "inputs");
         validate_sort(*in, "sort_isect");
         const size_t n = static_cast<size_t>(in->n);
+        need(b, "sort_isect", "backend");
         if (n == 0) return;
         need(keys_sorted, "sort_isect", "keys_sorted");
         need(values_sorted, "sort_isect", "values_sorted");
@@ -381,11 +381,11 @@ int32_t sxh_sort_isect(sxh_backend* b, const sxh_sort_inputs* in, uint64_t* keys
 
 int32_t sxh_isect_offset_encode(sxh_backend* b, const sxh_offset_inputs* in, int32_t* offsets) {
     return guarded([&] {
-        need(b, "isect_offset_encode", "backend");
         need(in, "isect_offset_encode", "inputs");
         validate_offsets(*in, "isect_offset_encode");
         const int64_t n_tiles = static_cast<int64_t>(in->tile_width) * in->tile_height;
         const size_t total = static_cast<size_t>(in->I * n_tiles);
+        need(b, "isect_offset_encode", "backend");
         if (total == 0) return;
         need(offsets, "isect_offset_encode", "offsets");
         if (in->n_isects == 0) {  // offsets.fill_(0) (CpuKernels.cpp:713)
@@ -458,11 +458,11 @@ void stage_raster(const sxh_raster_inputs& in, hipStream_t s, RasterStage& st) {
 
 int32_t sxh_rasterize_fwd(sxh_backend* b, const sxh_raster_inputs* in, sxh_raster_outputs* out) {
     return guarded([&] {
-        need(b, "rasterize_fwd", "backend");
         need(in, "rasterize_fwd", "inputs");
         need(out, "rasterize_fwd", "outputs");
         validate_raster(*in, "rasterize_fwd");
         const size_t P = static_cast<size_t>(in->I) * in->image_width * in->image_height;
+        need(b, "rasterize_fwd", "backend");
         if (P == 0) return;
         if (!out->render_colors || !out->render_alphas || !out->last_ids) invalid("rasterize_fwd", "null output buffer");
         SXH_HIP(hipSetDevice(b->device));
@@ -483,7 +483,6 @@ int32_t sxh_rasterize_fwd(sxh_backend* b, const sxh_raster_inputs* in, sxh_raste
 int32_t sxh_rasterize_bwd(sxh_backend* b, const sxh_raster_inputs* in, const sxh_raster_grads_in* g,
                           sxh_raster_grads* out) {
     return guarded([&] {
-        need(b, "rasterize_bwd", "backend");
         need(in, "rasterize_bwd", "inputs");
         need(g, "rasterize_bwd", "grads_in");
         need(out, "rasterize_bwd", "outputs");
@@ -494,6 +493,7 @@ int32_t sxh_rasterize_bwd(sxh_backend* b, const sxh_raster_inputs* in, const sxh
         if (!out->v_means2d || !out->v_conics || !out->v_colors || !out->v_opacities ||
             (g->absgrad && !out->v_means2d_abs))
             invalid("rasterize_bwd", "null output buffer");
+        need(b, "rasterize_bwd", "backend");
         SXH_HIP(hipSetDevice(b->device));
         hipStream_t s = b->stream;
         auto vm2 = zeros<float>(n * 2, s);
@@ -525,9 +525,9 @@ int32_t sxh_rasterize_bwd(sxh_backend* b, const sxh_raster_inputs* in, const sxh
 // ---- RNG / MCMC ---------------------------------------------------------------------------------------
 int32_t sxh_rng_normal_f32(sxh_backend* b, const sxh_rng_inputs* in, float* out) {
     return guarded([&] {
-        need(b, "rng_normal_f32", "backend");
         need(in, "rng_normal_f32", "inputs");
         validate_rng(*in, "rng_normal_f32");
+        need(b, "rng_normal_f32", "backend");
         if (in->count == 0) return;
         need(out, "rng_normal_f32", "out");
         SXH_HIP(hipSetDevice(b->device));
@@ -541,9 +541,9 @@ int32_t sxh_rng_normal_f32(sxh_backend* b, const sxh_rng_inputs* in, float* out)
 
 int32_t sxh_rng_philox_u32(sxh_backend* b, const sxh_rng_inputs* in, uint32_t* out) {
     return guarded([&] {
-        need(b, "rng_philox_u32", "backend");
         need(in, "rng_philox_u32", "inputs");
         validate_rng(*in, "rng_philox_u32");
+        need(b, "rng_philox_u32", "backend");
         if (in->count == 0) return;
         need(out, "rng_philox_u32", "out");
         SXH_HIP(hipSetDevice(b->device));
@@ -557,10 +557,10 @@ int32_t sxh_rng_philox_u32(sxh_backend* b, const sxh_rng_inputs* in, uint32_t* o
 
 int32_t sxh_mcmc_relocation(sxh_backend* b, const sxh_relocation_inputs* in, float* new_op, float* new_sc) {
     return guarded([&] {
-        need(b, "mcmc_relocation", "backend");
         need(in, "mcmc_relocation", "inputs");
         validate_relocation(*in, "mcmc_relocation");
         const size_t N = static_cast<size_t>(in->N);
+        need(b, "mcmc_relocation", "backend");
         if (N == 0) return;
         need(new_op, "mcmc_relocation", "new_opacities");
         need(new_sc, "mcmc_relocation", "new_scales");
@@ -585,10 +585,10 @@ int32_t sxh_mcmc_relocation(sxh_backend* b, const sxh_relocation_inputs* in, flo
 
 int32_t sxh_mcmc_perturb_positions(sxh_backend* b, const sxh_perturb_inputs* in) {
     return guarded([&] {
-        need(b, "mcmc_perturb_positions", "backend");
         need(in, "mcmc_perturb_positions", "inputs");
+        if (in->N != 0) validate_perturb(*in, "mcmc_perturb_positions");  // empty: skip before validation
+        need(b, "mcmc_perturb_positions", "backend");
         if (in->N == 0) return;
-        validate_perturb(*in, "mcmc_perturb_positions");
         const size_t N = static_cast<size_t>(in->N);
         SXH_HIP(hipSetDevice(b->device));
         hipStream_t s = b->stream;
@@ -607,7 +607,6 @@ int32_t sxh_mcmc_perturb_positions(sxh_backend* b, const sxh_perturb_inputs* in)
 // ---- SSIM ---------------------------------------------------------------------------------------------
 int32_t sxh_ssim_fwd(sxh_backend* b, const sxh_ssim_inputs* in, sxh_ssim_outputs* out) {
     return guarded([&] {
-        need(b, "ssim_fwd", "backend");
         need(in, "ssim_fwd", "inputs");
         need(out, "ssim_fwd", "outputs");
         validate_ssim(*in, "ssim_fwd");
@@ -617,6 +616,7 @@ int32_t sxh_ssim_fwd(sxh_backend* b, const sxh_ssim_inputs* in, sxh_ssim_outputs
         const size_t M = static_cast<size_t>(I) * (H - 10) * (W - 10) * C;
         if (!out->ssim_map || (in->need_coeffs && (!out->coeff_mu || !out->coeff_sigma || !out->coeff_cross)))
             invalid("ssim_fwd", "null output buffer");
+        need(b, "ssim_fwd", "backend");
         SXH_HIP(hipSetDevice(b->device));
         hipStream_t s = b->stream;
         auto a = upload(in->img1, n, s);
@@ -639,7 +639,6 @@ int32_t sxh_ssim_fwd(sxh_backend* b, const sxh_ssim_inputs* in, sxh_ssim_outputs
 
 int32_t sxh_ssim_bwd(sxh_backend* b, const sxh_ssim_inputs* in, const sxh_ssim_grads_in* gin, float* v_img1) {
     return guarded([&] {
-        need(b, "ssim_bwd", "backend");
         need(in, "ssim_bwd", "inputs");
         need(gin, "ssim_bwd", "grads_in");
         validate_ssim(*in, "ssim_bwd");
@@ -649,6 +648,7 @@ int32_t sxh_ssim_bwd(sxh_backend* b, const sxh_ssim_inputs* in, const sxh_ssim_g
                   C = static_cast<int>(in->C);
         const size_t n = static_cast<size_t>(I) * H * W * C;
         const size_t M = static_cast<size_t>(I) * (H - 10) * (W - 10) * C;
+        need(b, "ssim_bwd", "backend");
         SXH_HIP(hipSetDevice(b->device));
         hipStream_t s = b->stream;
         auto a = upload(in->img1, n, s);

@@ -401,9 +401,10 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         t.n = 0;
         for (int k = 1; k < e->n_ev && t.n < 30; k++) {
             float ms = 0.f;
-            if (std::strcmp(e->ev_name[k], "sync1") == 0) continue;  // host wait, reported below
-            const int prev = (std::strcmp(e->ev_name[k - 1], "sync1") == 0 && k >= 2) ? k - 1 : k - 1;
-            SXH_HIP(hipEventElapsedTime(&ms, e->ev[prev], e->ev[k]));
+            // the interval ending at the sync1 mark is the host wait (reported below); segment B's first
+            // interval starts at the sync1 event, which the stream reaches once the host launches again
+            if (std::strcmp(e->ev_name[k], "sync1") == 0) continue;
+            SXH_HIP(hipEventElapsedTime(&ms, e->ev[k - 1], e->ev[k]));
             t.names[t.n] = e->ev_name[k];
             t.ms[t.n++] = ms;
         }

@@ -779,11 +779,20 @@ class Executor:
             self.h = None
 
     def _sync(self, params, exp_avg, exp_avg_sq, rows):
+        """ParamSync over the caller's arrays. The library copies rows * dim floats per group from or
+        into each array, so every array given must hold at least that many elements."""
         s = ParamSync()
+        dims = GROUP_DIMS(self.sh_degree)
         for g in range(6):
-            s.params[g] = ptr(params[g]) if params[g] is not None and params[g].size else None
-            s.exp_avg[g] = ptr(exp_avg[g]) if exp_avg[g] is not None and exp_avg[g].size else None
-            s.exp_avg_sq[g] = ptr(exp_avg_sq[g]) if exp_avg_sq[g] is not None and exp_avg_sq[g].size else None
+            for name, arrs, field in (("params", params, s.params), ("exp_avg", exp_avg, s.exp_avg),
+                                      ("exp_avg_sq", exp_avg_sq, s.exp_avg_sq)):
+                a = arrs[g]
+                if a is not None and a.size:
+                    if a.size < rows * dims[g]:
+                        raise ValueError(f"{name}[{g}] holds {a.size} floats; rows * dim = {rows * dims[g]}")
+                    field[g] = ptr(a)
+                else:
+                    field[g] = None
         s.rows = rows
         return s
 
@@ -799,6 +808,10 @@ class Executor:
                          gt_index=-1, opacity_reg_w=0.0, scale_reg_w=0.0, forward_only=False,
                          inject_noise=False, noise_seed=0, noise_offset=0, noise_scale=0.0):
         keep = [f32(viewmat), f32(K), f32(gt_rgb)]
+        if keep[0].size != 16 or keep[1].size != 9:
+            raise ValueError("viewmat must hold 16 floats and K 9")
+        if gt_rgb is not None and keep[2].size != width * height * 3:
+            raise ValueError(f"gt_rgb holds {keep[2].size} floats; width * height * 3 = {width * height * 3}")
         s = StepInputs(ptr(keep[0]), ptr(keep[1]), width, height, ptr(keep[2]), gt_index, count,
                        degrees_to_use, (C.c_float * 6)(*lr), opacity_reg_w, scale_reg_w,
                        int(bool(forward_only)), int(bool(inject_noise)), noise_seed, noise_offset,

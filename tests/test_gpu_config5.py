@@ -9,7 +9,9 @@ At full size the oracle is too slow, so the checks are size-independent:
 - the per-op sort output is ascending and stable (equal keys keep ascending Gaussian ids, which is
   the emit order);
 - on a handful of tiles (masks) the GPU rasterizer matches the CPU oracle bit for bit on the same
-  sorted lists;
+  sorted lists, and its backward (many 256-entry batches per tile, the walk from the tile's last
+  contributor, the hardware exponential with its exact fallback near the alpha decisions) matches the
+  oracle's backward within rel_l2 1e-4 (float atomics: order-dependent sums);
 - one full training step at this size stays finite.
 """
 import numpy as np
@@ -28,6 +30,23 @@ F = np.float32
 def cfg5():
     sc, cfg = scene.config_scene(5, seed=0)
     return sc, cfg
+
+
+# sampled tiles (tile row, tile column) as fractions of the tile grid: the dense centre, off-centre
+# tiles, the corners and the edges
+def sample_tiles(th, tw):
+    return [(th // 2, tw // 2), (th // 2, tw // 2 + 1), (th // 3, tw // 4), (2 * th // 3, 3 * tw // 4),
+            (0, 0), (th - 1, tw - 1), (th // 2, 0), (5, tw - 6)]
+
+
+@pytest.fixture(scope="module")
+def fwd5(gpu, cfg5):
+    """The per-op forward pipeline's raster inputs at config 5 and its sorted keys."""
+    sc, _ = cfg5
+    orc = oracle_py.Oracle(libm=False)
+    rk, ks = per_op_forward(gpu, orc, sc)
+    print(f"config 5: n_isects={rk['n_isects']}", flush=True)
+    return rk, ks
 
 
 def per_op_forward(gpu, orc, sc):
@@ -59,19 +78,18 @@ def per_op_forward(gpu, orc, sc):
     return rk, ks
 
 
-def test_config5_executor_matches_per_op_pipeline(gpu, cfg5):
+def test_config5_executor_matches_per_op_pipeline(gpu, cfg5, fwd5):
     sc, cfg = cfg5
     orc = oracle_py.Oracle(libm=False)
-    rk, ks = per_op_forward(gpu, orc, sc)
+    rk, ks = fwd5
     n_isects = rk["n_isects"]
-    print(f"config 5: n_isects={n_isects}", flush=True)
     assert 150_000_000 <= n_isects <= 250_000_000
     # ascending, and stable: equal keys keep ascending Gaussian ids (the emit order)
     same = ks[1:] == ks[:-1]
     assert np.all(ks[1:] >= ks[:-1])
     assert np.all(rk["flatten_ids"][1:][same] > rk["flatten_ids"][:-1][same])
     assert same.sum() > 1000  # ties exercised (the 10% shared depth)
-    del ks, same
+    del same
     ref = gpu.rasterize_fwd(**rk)
 
     ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
@@ -86,8 +104,7 @@ def test_config5_executor_matches_per_op_pipeline(gpu, cfg5):
     # a few tiles against the CPU oracle, on the same sorted lists
     tw, th = rk["tile_width"], rk["tile_height"]
     masks = np.zeros((1, th, tw), np.uint8)
-    sel = [(th // 2, tw // 2), (th // 2, tw // 2 + 1), (th // 3, tw // 4), (2 * th // 3, 3 * tw // 4),
-           (0, 0), (th - 1, tw - 1), (th // 2, 0), (5, tw - 6)]
+    sel = sample_tiles(th, tw)
     for y, x in sel:
         masks[0, y, x] = 1
     g_m = gpu.rasterize_fwd(masks=masks, **rk)
@@ -108,3 +125,48 @@ def test_config5_executor_matches_per_op_pipeline(gpu, cfg5):
     for g in range(6):
         assert np.all(np.isfinite(p[g])) and np.all(np.isfinite(v[g]))
     ex.close()
+
+
+def rel_l2(a, e):
+    a = np.asarray(a, np.float64).ravel()
+    e = np.asarray(e, np.float64).ravel()
+    den = np.sqrt((e * e).sum())
+    return float(np.sqrt(((a - e) ** 2).sum()) / max(den, 1e-30))
+
+
+def test_config5_sampled_tiles_backward_matches_oracle(gpu, fwd5):
+    """The raster backward on the sampled config-5 tiles (about 20k intersections each at the centre)
+    against the oracle's backward on the same sorted lists, forward outputs and seeded v_render."""
+    rk, _ = fwd5
+    orc = oracle_py.Oracle(libm=False)
+    tw, th = rk["tile_width"], rk["tile_height"]
+    masks = np.zeros((1, th, tw), np.uint8)
+    sel = sample_tiles(th, tw)
+    for y, x in sel:
+        masks[0, y, x] = 1
+    off = rk["isect_offsets"].ravel()
+    per_tile = [int((off[t + 1] if t + 1 < off.size else rk["n_isects"]) - off[t]) for t in (y * tw + x for y, x in sel)]
+    print(f"config 5 sampled tiles: intersections {per_tile}", flush=True)
+    assert max(per_tile) > 10 * 256  # many batches per tile
+    fw = gpu.rasterize_fwd(masks=masks, **rk)
+    rng = np.random.Generator(np.random.PCG64(55))
+    H, W = rk["height"], rk["width"]
+    v_rc = rng.normal(0.0, 1e-3, (1, H, W, 3)).astype(np.float32)
+    v_ra = rng.normal(0.0, 1e-4, (1, H, W, 1)).astype(np.float32)
+    bk = dict(render_alphas=fw["render_alphas"], last_ids=fw["last_ids"], v_render_colors=v_rc,
+              v_render_alphas=v_ra, masks=masks, **rk)
+    g = gpu.rasterize_bwd(**bk)
+    o = orc.rasterize_bwd(**bk)
+    # only the Gaussians of the sampled tiles get gradients
+    touched = np.zeros(rk["N"], bool)
+    for y, x in sel:
+        t = y * tw + x
+        e = off[t + 1] if t + 1 < off.size else rk["n_isects"]
+        touched[rk["flatten_ids"][off[t]:e]] = True
+    for key in ("v_means2d", "v_conics", "v_colors", "v_opacities"):
+        a, b = g[key], o[key]
+        assert np.count_nonzero(b) > 0, key
+        assert not np.any(a.reshape(rk["N"], -1)[~touched]), key
+        d = rel_l2(a, b)
+        print(f"  {key}: rel_l2 {d:.3e}", flush=True)
+        assert d <= 1e-4, (key, d)

@@ -1,0 +1,121 @@
+"""The resident training step at the workloads BASELINE.json states, against the CPU oracle's host-path
+step: configs 1 and 2 exactly as stated (one camera at the origin looking +z, AABB tiles; config 1 SH0 and
+L1 against a seeded U[0,1] target with lr 1e-3, config 2 SH3 with 0.8 L1 + 0.2 (1 - SSIM) against the
+render of a second seeded scene) and one full fwd+bwd+Adam step of the config-3 headline (N = 1M, SH3,
+1297x840, AccuTile, SSIM, a jittered pose).
+
+Gates are the reference's resident-vs-host contrast (TrainerTests.cpp:1720-1746): n_isects exact, the
+first render bit-exact (the forward is bit-identical), |dloss| <= 1e-6 + 1e-4 |loss|, parameters and both
+Adam moments after the steps within rel_l2 1e-4 (float atomics in the raster backward make the gradient
+sums order dependent)."""
+import numpy as np
+import pytest
+
+import oracle_py
+import scene
+import splatx_hip as sh
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, e):
+    a = np.asarray(a, np.float64).ravel()
+    e = np.asarray(e, np.float64).ravel()
+    den = np.sqrt((e * e).sum())
+    return float(np.sqrt(((a - e) ** 2).sum()) / max(den, 1e-30))
+
+
+def isect_mode(cfg):
+    return sh.SXH_ISECT_ACCUTILE if cfg["isect"] == "accutile" else sh.SXH_ISECT_AABB
+
+
+def scene_target(gpu, orc, cfg_id, viewmat):
+    """The config's target image: the second seeded scene (seed 1) rendered from `viewmat` on the GPU,
+    checked bit for bit against the oracle's render of the same scene."""
+    tgt, cfg = scene.config_scene(cfg_id, seed=1)
+    ex = gpu.make_train_step_executor(arena_rows=tgt.n, sh_degree=tgt.sh_degree, ssim_weight=cfg["ssim"],
+                                      isect_mode=isect_mode(cfg))
+    p, m, v = scene.copy_state(tgt)
+    ex.upload_params(p, m, v, tgt.n)
+    kw = dict(scene.step_kwargs(tgt), viewmat=viewmat)
+    img = ex.step(want_render=True, forward_only=True, **kw)["render_colors"]
+    ex.close()
+    ro = orc.train_step(p, m, v, tgt.n, tgt.sh_degree, viewmat, tgt.K, tgt.width, tgt.height, None,
+                        tgt.sh_degree, kw["lr"], forward_only=True, isect_mode=isect_mode(cfg))
+    assert np.array_equal(img.view(np.uint32), ro["render_colors"].view(np.uint32))
+    return img
+
+
+def run_config(gpu, cfg_id, steps, viewmat=None, lr=None):
+    sc, cfg = scene.config_scene(cfg_id, seed=0)
+    orc = oracle_py.Oracle(libm=False)
+    vm = sc.viewmat if viewmat is None else viewmat
+    if cfg["target"] == "uniform":  # a seeded U[0,1] target image
+        rng = np.random.Generator(np.random.PCG64(1000))
+        gt = rng.uniform(0.0, 1.0, (sc.height, sc.width, 3)).astype(np.float32)
+    else:
+        gt = scene_target(gpu, orc, cfg_id, vm)
+    lr = list(sc.lr) if lr is None else lr
+    ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
+                                      antialiased=bool(cfg.get("antialiased", False)), isect_mode=isect_mode(cfg))
+    gp, gm, gv = scene.copy_state(sc)
+    ex.upload_params(gp, gm, gv, sc.n)
+    op, om, ov = scene.copy_state(sc)
+    kw = dict(scene.step_kwargs(sc), viewmat=vm, lr=lr)
+    out = []
+    for it in range(steps):
+        rg = ex.step(want_render=True, gt_rgb=gt, **kw)
+        ro = orc.train_step(op, om, ov, sc.n, sc.sh_degree, vm, sc.K, sc.width, sc.height, gt, sc.sh_degree, lr,
+                            ssim_weight=cfg["ssim"], antialiased=bool(cfg.get("antialiased", False)),
+                            isect_mode=isect_mode(cfg))
+        print(f"config {cfg_id} step {it}: n_isects {rg['n_isects']} / {ro['n_isects']}, loss {rg['loss']:.7f} / "
+              f"{ro['loss']:.7f}", flush=True)
+        out.append((rg, ro))
+    ex.download_params(gp, gm, gv, sc.n)
+    ex.close()
+    return sc, out, (gp, gm, gv), (op, om, ov)
+
+
+def check_contrast(sc, out, g, o, expect_isects):
+    lo, hi = expect_isects
+    for it, (rg, ro) in enumerate(out):
+        assert rg["n_isects"] == ro["n_isects"], (it, rg["n_isects"], ro["n_isects"])
+        assert lo <= rg["n_isects"] <= hi, rg["n_isects"]
+        assert rg["n_visible"] == ro["n_visible"]
+        assert abs(rg["loss"] - ro["loss"]) <= 1e-6 + 1e-4 * abs(ro["loss"]), (it, rg["loss"], ro["loss"])
+        if it == 0:
+            assert np.array_equal(rg["render_colors"].view(np.uint32), ro["render_colors"].view(np.uint32))
+        else:
+            assert rel_l2(rg["render_colors"], ro["render_colors"]) <= 1e-5
+    names = ("means", "quats", "scales", "opacities", "sh0", "shN")
+    for grp in range(6):
+        for kind, a, b in zip(("param", "exp_avg", "exp_avg_sq"), (g[0][grp], g[1][grp], g[2][grp]),
+                              (o[0][grp], o[1][grp], o[2][grp])):
+            if b.size:
+                d = rel_l2(a, b)
+                assert d <= 1e-4, (names[grp], kind, d)
+        # the step moved the parameters (the comparison is not of two untouched copies)
+        if sc.params[grp].size:
+            assert not np.array_equal(g[0][grp], sc.params[grp]), names[grp]
+
+
+def test_config1_step_matches_oracle(gpu):
+    """Config 1: N = 10k, SH0, 256x256, fx = fy = 230, AABB, L1 against a seeded U[0,1] target, Adam lr 1e-3."""
+    sc, out, g, o = run_config(gpu, 1, steps=2, lr=[1e-3] * 6)
+    check_contrast(sc, out, g, o, (5_000, 200_000))
+
+
+def test_config2_step_matches_oracle(gpu):
+    """Config 2: N = 100k, SH3, 800x800, fx = fy = 720, AABB, 0.8 L1 + 0.2 (1 - SSIM) against the second
+    seeded scene's render."""
+    sc, out, g, o = run_config(gpu, 2, steps=2)
+    check_contrast(sc, out, g, o, (100_000, 5_000_000))
+
+
+def test_config3_full_step_matches_oracle(gpu):
+    """Config 3 (the headline): one full fwd + bwd + Adam step at N = 1M, SH3, 1297x840, AccuTile, SSIM,
+    from the first jittered pose of the benchmark's pose sequence, against the oracle's step."""
+    rng = np.random.Generator(np.random.PCG64(1234))
+    pose = scene.jittered_view(rng)
+    sc, out, g, o = run_config(gpu, 3, steps=1, viewmat=pose)
+    check_contrast(sc, out, g, o, (1_000_000, 4_000_000))

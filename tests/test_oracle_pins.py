@@ -259,3 +259,69 @@ def test_scan_sort_offsets_brute_force(oracle):
     off = oracle.isect_offset_encode(keys, I, tw, th)
     np.testing.assert_array_equal(off, np.searchsorted(tiles, np.arange(I * nt), side="left"))
     np.testing.assert_array_equal(oracle.isect_offset_encode(keys[:0], I, tw, th, n_isects=0), np.zeros(I * nt))
+
+
+# ---------------------------------------------------------------- projection bwd, covars path ----
+def covars_fd_case(oracle, aa):
+    """Projection backward on the covariance path (6-triu input), with the directional-free reference:
+    central differences of L = <v_conics, conics> (+ <v_comp, compensations> when antialiased) in each
+    triu entry, Richardson-extrapolated. An off-diagonal entry c_ij (i < j) sits at (i, j) and (j, i)
+    of the symmetric matrix, so dL/dc_ij is the sum of both positions' derivatives
+    (ProjectionEWA.metal:475-480)."""
+    kw = inputs.proj_kwargs(n=96, seed=91, covars=True, aa=aa, znear=1.5)
+    r = inputs.rng(92)
+    fwd = oracle.projection_fused_fwd(**kw)
+    n = kw["covars"].shape[0]
+    v_conics = r.standard_normal((1, n, 3)).astype(F)
+    v_comp = r.standard_normal((1, n)).astype(F) if aa else None
+    bwd = oracle.projection_fused_bwd(radii=fwd["radii"], conics=fwd["conics"], compensations=fwd["compensations"],
+                                      v_means2d=np.zeros((1, n, 2), F), v_depths=np.zeros((1, n), F),
+                                      v_conics=v_conics, v_compensations=v_comp, **kw)
+    cov0 = kw["covars"].astype(np.float64)
+    keep = (fwd["radii"][0] > 0).all(axis=1)
+
+    def loss(cov):
+        o = oracle.projection_fused_fwd(**dict(kw, covars=cov.astype(F)))
+        l = (o["conics"][0].astype(np.float64) * v_conics[0]).sum(1)
+        if aa:
+            l = l + o["compensations"][0].astype(np.float64) * v_comp[0]
+        return l, (o["radii"][0] > 0).all(axis=1)
+
+    def central(k, rel):
+        h = rel * np.abs(cov0[:, [0, 3, 5]]).max(axis=1)  # step relative to the covariance's scale
+        cp, cm = cov0.copy(), cov0.copy()
+        cp[:, k] += h
+        cm[:, k] -= h
+        lp, vp = loss(cp)
+        lm, vm_ = loss(cm)
+        steps = cp[:, k].astype(F).astype(np.float64) - cm[:, k].astype(F).astype(np.float64)
+        return (lp - lm) / steps, vp & vm_
+
+    fd = np.zeros((n, 6))
+    for k in range(6):
+        a, va = central(k, 2e-3)
+        b, vb = central(k, 4e-3)
+        fd[:, k] = (4 * a - b) / 3
+        keep &= va & vb
+    assert keep.sum() > 40
+    return bwd["v_covars"].astype(np.float64)[keep], fd[keep]
+
+
+@pytest.mark.parametrize("aa", [False, True])
+def test_projection_bwd_covars_central_differences(oracle, aa):
+    got, fd = covars_fd_case(oracle, aa)
+    err = np.linalg.norm(got - fd) / np.linalg.norm(fd)
+    assert err < 1e-3, err
+    # the off-diagonal entries carry a real share of the gradient (the check below is not vacuous)
+    assert np.linalg.norm(fd[:, [1, 2, 4]]) > 0.1 * np.linalg.norm(fd)
+
+
+def test_projection_bwd_covars_planted_error_is_caught(oracle):
+    """A plausible mistake, one of the symmetric off-diagonal contributions not summed (any one of the
+    c01, c02, c12 entries halved), fails the central-difference check above."""
+    got, fd = covars_fd_case(oracle, False)
+    for k in (1, 2, 4):
+        bad = got.copy()
+        bad[:, k] *= 0.5
+        err = np.linalg.norm(bad - fd) / np.linalg.norm(fd)
+        assert err > 1e-2, (k, err)

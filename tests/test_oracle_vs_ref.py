@@ -44,8 +44,9 @@ def test_projection_fwd(reference, oracle_libm, oracle, case):
         if r[k] is None:
             continue
         assert same_bits(o[k][valid], r[k][valid]), k
-    # deterministic transcendentals: radii may differ only where a radius sits on an integer edge
-    assert (s["radii"] != r["radii"]).any(axis=-1).mean() < 1e-3
+    # deterministic transcendentals: the integer radii are identical (on these seeded inputs no radius
+    # sits within an ulp of an integer edge, where the two exp/log layers could round apart)
+    assert same_bits(s["radii"], r["radii"])
     both = valid & (s["radii"][..., 0] > 0)
     for k in ("means2d", "depths", "conics", "compensations"):
         if r[k] is not None:
@@ -95,7 +96,9 @@ def test_isect_with_deterministic_exp_matches(reference, oracle):
     kw = inputs.isect_kwargs(oracle, n=3000, seed=41, accutile=True)
     r = reference.isect_tiles(**kw)
     s = oracle.isect_tiles(**kw)
-    assert np.mean(s["tiles_per_gauss"] != r["tiles_per_gauss"]) < 1e-3
+    assert r["n_isects"] > 1000
+    for k in ("tiles_per_gauss", "isect_ids", "flatten_ids"):
+        assert same_bits(s[k], r[k]), k
 
 
 @pytest.mark.parametrize("bg,masks", [(False, False), (True, False), (True, True)])
@@ -113,7 +116,7 @@ def test_rasterize_fwd_deterministic_exp_close(reference, oracle):
     r = reference.rasterize_fwd(**kw)
     s = oracle.rasterize_fwd(**kw)
     close(s["render_colors"], r["render_colors"], rtol=1e-5, atol=1e-6)
-    assert np.mean(s["last_ids"] != r["last_ids"]) < 1e-3
+    assert same_bits(s["last_ids"], r["last_ids"])
 
 
 def test_ssim_fwd(reference, oracle_libm):
