@@ -60,10 +60,13 @@ int32_t sxh_backend_create(int32_t device_ordinal, sxh_backend** out) {
         auto* b = new sxh_backend();
         b->device = device_ordinal;
         b->name = std::string("hip-gfx950:") + prop.gcnArchName;
-        hipError_t e = hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking);
-        if (e != hipSuccess) {
-            delete b;
-            hip_check(e, "hipStreamCreateWithFlags");
+        try {
+            SXH_HIP(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking));
+            SXH_HIP(hipHostMalloc(reinterpret_cast<void**>(&b->pinned_word), sizeof(uint32_t), hipHostMallocDefault));
+            noalloc_init(device_ordinal);  // the allocation-free entry points' scratch on this device
+        } catch (...) {
+            sxh_backend_destroy(b);
+            throw;
         }
         *out = b;
     });
@@ -72,6 +75,7 @@ int32_t sxh_backend_create(int32_t device_ordinal, sxh_backend** out) {
 void sxh_backend_destroy(sxh_backend* b) {
     if (!b) return;
     if (b->stream) (void)hipStreamDestroy(b->stream);
+    if (b->pinned_word) (void)hipHostFree(b->pinned_word);
     delete b;
 }
 

@@ -611,11 +611,15 @@ constexpr int kMaxPasses = 8;
 // histogram, or the onesweep status words of alternate passes)
 constexpr int kHeaderWords = 2 * kMaxPasses * kBins + 64;
 
-// n_dev: when set, the key count is read on the device from *n_dev (at most n, the capacity the
-// grids are sized for), so the launches do not depend on it (a captured graph can replay them).
+// The passes read `src` first and then alternate between the two sides: pass p writes side[p & 1],
+// pass p > 0 reads side[(p - 1) & 1]. src may be side[1] (the sort then works in place over two
+// buffers). n_dev: when set, the key count is read on the device from *n_dev (at most n, the capacity
+// the grids are sized for), so the launches do not depend on it (a captured graph can replay them).
+// Returns the number of passes, or -1 when nothing was launched because n_dev asks for the
+// three-launch path.
 template <class K>
-int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-                 void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev) {
+int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32_t* const side_v[2], int64_t n,
+                 uint32_t key_bits, void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev) {
     uint32_t* totals = static_cast<uint32_t*>(scratch);
     uint32_t* bases = totals + kMaxPasses * kBins;
     uint32_t* counters = bases + kMaxPasses * kBins;
@@ -634,12 +638,10 @@ int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t
     const int64_t hist_n = (int64_t)tiles * kBins;
     uint32_t* hist = totals + kHeaderWords;
     uint32_t* status_b = hist + hist_n;
-    K* kin = keys_a;
-    int32_t* vin = vals_a;
-    K* kout = keys_b;
-    int32_t* vout = vals_b;
     hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins,
                        clear_err ? err : nullptr);
+    const K* kin = src_k;
+    const int32_t* vin = src_v;
     if (n < (int64_t{1} << 30)) {  // onesweep: counts and prefixes fit the 30-bit status words
         const int hist_blocks = std::min(tiles, kHistBlocks);
         if (key_bits <= kFullBits)
@@ -652,12 +654,13 @@ int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t
         uint32_t* st[2] = {hist, status_b};
         for (int p = 0; p < passes; p++) {
             uint32_t* next = p + 1 < passes ? st[(p + 1) & 1] : nullptr;
-            launch_os_pass<K>(tiles, s, kin, vin, kout, vout, n, dbits * p, digit_mask(p, dbits, key_bits),
-                              bases + p * kBins, st[p & 1], next, counters + p, err, n_dev);
-            std::swap(kin, kout);
-            std::swap(vin, vout);
+            launch_os_pass<K>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p,
+                              digit_mask(p, dbits, key_bits), bases + p * kBins, st[p & 1], next, counters + p, err,
+                              n_dev);
+            kin = side_k[p & 1];
+            vin = side_v[p & 1];
         }
-        return (passes & 1) ? 1 : 0;
+        return passes;
     }
     for (int p = 0; p < passes; p++) {
         const int shift = dbits * p;
@@ -665,12 +668,22 @@ int radix_sort_t(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t
         hipLaunchKernelGGL(k_hist<K>, dim3(tiles), dim3(kThreads), 0, s, kin, n, shift, mask, hist, tiles,
                            totals + p * kBins);
         hipLaunchKernelGGL(k_scan_digit, dim3(kBins), dim3(kThreads), 0, s, hist, tiles, totals + p * kBins);
-        hipLaunchKernelGGL(k_scatter<K>, dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, mask,
-                           hist, tiles);
-        std::swap(kin, kout);
-        std::swap(vin, vout);
+        hipLaunchKernelGGL(k_scatter<K>, dim3(tiles), dim3(kThreads), 0, s, kin, vin, side_k[p & 1], side_v[p & 1],
+                           n, shift, mask, hist, tiles);
+        kin = side_k[p & 1];
+        vin = side_v[p & 1];
     }
-    return (passes & 1) ? 1 : 0;
+    return passes;
+}
+
+// In place over two buffers: a -> b -> a -> ...; the result is in a after an even pass count.
+template <class K>
+int radix_sort_ab(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
+                  void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev) {
+    K* const sk[2] = {keys_b, keys_a};
+    int32_t* const sv[2] = {vals_b, vals_a};
+    const int passes = radix_sort_t<K>(keys_a, vals_a, sk, sv, n, key_bits, scratch, clear_err, s, n_dev);
+    return passes < 0 ? -1 : (passes & 1);
 }
 
 } // namespace
@@ -686,17 +699,27 @@ uint32_t* sort_error_flag(void* scratch) {
 
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
                void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
-    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
 }
 
 int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
                void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
-    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
 }
 
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
                void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
-    return radix_sort_t(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
+}
+
+void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_out, int32_t* vals_out,
+                     uint64_t* keys_tmp, int32_t* vals_tmp, int64_t n, uint32_t key_bits, void* scratch,
+                     hipStream_t s) {
+    const int passes = static_cast<int>((std::min<uint32_t>(key_bits, 64) + 7) / 8);
+    // the last pass, passes - 1, writes side[(passes - 1) & 1]: make that side the output
+    uint64_t* const sk[2] = {(passes & 1) ? keys_out : keys_tmp, (passes & 1) ? keys_tmp : keys_out};
+    int32_t* const sv[2] = {(passes & 1) ? vals_out : vals_tmp, (passes & 1) ? vals_tmp : vals_out};
+    (void)radix_sort_t<uint64_t>(keys, vals, sk, sv, n, key_bits, scratch, true, s, nullptr);
 }
 
 } // namespace sxk

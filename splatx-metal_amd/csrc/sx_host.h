@@ -239,4 +239,10 @@ struct sxh_backend {
     int device = 0;
     hipStream_t stream = nullptr;
     std::string name;
+    uint32_t* pinned_word = nullptr;  // a pinned host word for status readbacks of the allocation-free calls
 };
+
+namespace sxh {
+// Resolves the allocation-free entry points' scratch array on `device` (the current device).
+void noalloc_init(int device);
+}  // namespace sxh

@@ -82,6 +82,12 @@ int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* val
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
                uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
                const int64_t* n_dev = nullptr);
+// The same sort of n u64 keys from read-only inputs into keys_out/vals_out, with keys_tmp/vals_tmp as
+// the second ping-pong side (n > 0, key_bits in 1..64, the onesweep range n < 2^30). No buffer may
+// alias another.
+void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_out, int32_t* vals_out,
+                     uint64_t* keys_tmp, int32_t* vals_tmp, int64_t n, uint32_t key_bits, void* scratch,
+                     hipStream_t s);
 // device word in the sort's scratch that a sort sets non-zero when a tile's look-back gave up (a
 // broken invariant, never expected). A sort with clear_err zeroes it first; one without adds to
 // what the sorts before it left, so several sorts in a row can be checked with one read.
