@@ -273,12 +273,14 @@ def main():
 
     # timed loop: the product path (segment B of each step replayed as a captured hipGraph)
     totals = {}
-    n_isects, n_vis, losses, passes = [], [], [], []
+    n_isects, n_vis, losses, passes, step_ms = [], [], [], [], []
     t0 = time.perf_counter()
     for k in range(args.warmup, n_poses):
         if mcmc and count != sc.n:
             steps[k] = step_inputs(k, count)
+        ts = time.perf_counter()
         rc = ex.step_raw(steps[k][0], out)
+        step_ms.append((time.perf_counter() - ts) * 1000.0)  # the step returns after its loss readback
         if rc != 0:
             raise RuntimeError(b.lib.sxh_last_error())
         n_isects.append(out.n_isects)
@@ -312,6 +314,20 @@ def main():
             totals[name] = totals.get(name, 0.0) + ms
     ex.set_profiling(False)
     avg = {k: x / args.steps for k, x in totals.items()}
+    # raster pair counts: the timed region's work once more with the counting raster kernels
+    pair_tot = {}
+    if not mcmc:
+        ex.upload_params(p, m, v, arena)
+        for k in range(args.warmup):
+            if ex.step_raw(steps0[k][0], out) != 0:
+                raise RuntimeError(b.lib.sxh_last_error())
+        ex.set_profiling(False, pair_stats=True)
+        for k in range(args.warmup, n_poses):
+            if ex.step_raw(steps0[k][0], out) != 0:
+                raise RuntimeError(b.lib.sxh_last_error())
+            for name, x in ex.get_raster_stats().items():
+                pair_tot[name] = pair_tot.get(name, 0) + x
+        ex.set_profiling(False)
 
     I, V = float(np.mean(n_isects)), float(np.mean(n_vis))
     px = sc.width * sc.height
@@ -346,6 +362,8 @@ def main():
                                f"fx=fy={cfg['fx']}, {cfg['isect']} isect, ssim_weight={cfg['ssim']}, "
                                f"pose jittered per step", "gaussians": sc.n, "width": sc.width,
                    "height": sc.height, "sh_degree": sc.sh_degree, "parallelism": "single GPU"},
+        "ms_p50": round(float(np.percentile(step_ms, 50)), 4),
+        "ms_p90": round(float(np.percentile(step_ms, 90)), 4),
         "gaussians_per_s": round(sc.n / (ms_per_step / 1e3), 1),
         "mean_n_isects": round(I, 1),
         "mean_visible": round(V, 1),
@@ -360,6 +378,16 @@ def main():
         "valu_issue": None,
         "host_waits_ms": {k: round(avg[k], 4) for k in avg if k.startswith("host_")},
     }
+    if pair_tot:  # per-step means; a list entry is one splat against the 64 pixels of a wave
+        pm = {k: x / args.steps for k, x in pair_tot.items()}
+        rp = {"fwd_lane_pairs": round(pm["fwd_entries"] * 64), "fwd_composited": round(pm["fwd_taken"]),
+              "bwd_lane_pairs": round(pm["bwd_entries"] * 64), "bwd_in_cutoff": round(pm["bwd_in_cutoff"]),
+              "bwd_contributing": round(pm["bwd_contrib"]), "bwd_chunks": round(pm["bwd_chunks"]),
+              "bwd_empty_chunks": round(pm["bwd_empty_chunks"]), "upper_bound_256I": round(256 * I)}
+        vb = load_valu("raster_bwd", args.config)
+        if vb is not None and pm["bwd_entries"] > 0:  # wave-level VALU instructions per list entry
+            rp["bwd_valu_per_entry"] = round(vb["valu_insts"] / pm["bwd_entries"], 1)
+        res["raster_pairs"] = rp
     vi = load_valu(dom, args.config)
     if vi is not None:  # the dominant kernel's own bound when it is compute-, not memory-bound
         vi["kernel"] = dom

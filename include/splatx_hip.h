@@ -637,14 +637,29 @@ int32_t sxh_exec_train_loop(sxh_executor* e, const sxh_train_loop_args* a, sxh_t
 int32_t sxh_exec_request_stop(sxh_executor* e);
 
 /* Per-kernel timing of the last step (HIP events on the executor's stream), enabled by
- * sxh_exec_set_profiling(e, 1). Names are stable strings; times are milliseconds. */
+ * sxh_exec_set_profiling(e, enable) with bit 0 of enable. Names are stable strings; times are
+ * milliseconds. Bit 1 of enable also counts the rasterisers' pair work of each step (counting
+ * instantiations of the raster kernels, slower than the production ones: use the counts, not the
+ * times, of such steps). No counterpart in the reference (its per-segment timing probe is
+ * MetalBackend.cpp:56-69). */
 typedef struct {
     int32_t n;
     const char* names[32];
     float ms[32];
 } sxh_exec_timing;
+typedef struct {
+    uint64_t fwd_entries;       /* list entries walked: one splat against the 64 pixels of a wave */
+    uint64_t fwd_taken;         /* pairs composited (alpha >= 1/255, T not yet spent) */
+    uint64_t bwd_chunks;        /* 4-entry chunks of the per-wave lists */
+    uint64_t bwd_entries;       /* list entries in those chunks (x 64 = lane pairs evaluated) */
+    uint64_t bwd_empty_chunks;  /* chunks in which no lane's pair is inside the cutoff (skipped) */
+    uint64_t bwd_in_cutoff;     /* lane pairs inside the cutoff and at or before the pixel's last contributor */
+    uint64_t bwd_contrib;       /* pairs that contribute a gradient (alpha >= 1/255) */
+} sxh_raster_stats;
 int32_t sxh_exec_set_profiling(sxh_executor* e, int32_t enable);
 int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out);
+/* The pair counts of the last step run with bit 1 of profiling set (zeros otherwise). */
+int32_t sxh_exec_get_raster_stats(sxh_executor* e, sxh_raster_stats* out);
 /* Whether the step's second segment (everything after the intersection-count readback) runs as a
  * captured hipGraph (default 1) or as direct launches (0). Profiling always launches directly. No
  * counterpart in the reference (its Metal command buffers are encoded per step). */

@@ -152,6 +152,15 @@ int32_t sxh_exec_set_profiling(sxh_executor* e, int32_t enable) {
     return guarded([&] {
         if (!e) invalid("TrainStepExecutor", "null executor");
         e->prof = enable != 0;
+        e->prof_stats = (enable & 2) != 0;
+        if (e->prof_stats && !e->rstats.p) e->rstats.alloc(sxk::kRasterStats);
+    });
+}
+
+int32_t sxh_exec_get_raster_stats(sxh_executor* e, sxh_raster_stats* out) {
+    return guarded([&] {
+        if (!e || !out) invalid("TrainStepExecutor", "null argument");
+        *out = e->rstats_host;
     });
 }
 
@@ -231,6 +240,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     const sxk::Arena A = e->arena();
 
     // ---- segment A: preprocess + counts -----------------------------------------------------------
+    if (e->prof_stats) SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
     e->mark("start");
     sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->grads.p, e->vis_part.p, e->n_vis.p, s);
     e->mark("preprocess");
@@ -300,6 +310,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         ra.tile_height = th;
         ra.n_isects = static_cast<int32_t>(n_host);
         ra.n_isects_dev = n_dev;
+        ra.stats = e->prof_stats ? e->rstats.p : nullptr;  // never in a captured graph (profiling launches directly)
         sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev);
         ra.tile_order = e->tile_order.p;
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
@@ -395,6 +406,13 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     SXH_HIP(hipStreamSynchronize(s));
     e->sync_ms[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     out->loss = fwd_only ? 0.0f : *hloss;
+    if (e->prof_stats) {
+        unsigned long long st[sxk::kRasterStats];
+        SXH_HIP(hipMemcpy(st, e->rstats.p, sizeof(st), hipMemcpyDeviceToHost));
+        e->rstats_host = sxh_raster_stats{st[sxk::kStatFwdEntries], st[sxk::kStatFwdTaken], st[sxk::kStatBwdChunks],
+                                          st[sxk::kStatBwdEntries], st[sxk::kStatBwdEmptyChunks],
+                                          st[sxk::kStatBwdInCutoff], st[sxk::kStatBwdContrib]};
+    }
     if (*hsort) throw std::runtime_error(std::string(what) + ": radix sort look-back did not complete");
     if (e->prof) {
         sxh_exec_timing& t = e->timing;

@@ -108,6 +108,7 @@ __device__ __forceinline__ void build_wave_lists(uint32_t m, uint8_t (*s_list)[k
     __syncthreads();
 }
 
+template <bool STATS>
 __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __restrict__ out_rgb,
                                                          float* __restrict__ out_alpha, int32_t* __restrict__ out_last) {
     __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
@@ -145,6 +146,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     int32_t cur = 0;
     float r0 = 0.f, r1 = 0.f, r2 = 0.f;
     bool done = !inside;
+    unsigned long long st_entries = 0, st_taken = 0;  // STATS only (wave-uniform)
     for (int32_t bstart = range_start; bstart < range_end; bstart += kThreads) {
         if (__syncthreads_count(done) == kThreads) break;  // also the barrier before LDS reuse
         const int32_t idx = bstart + tid;
@@ -165,6 +167,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
         const int len = __builtin_amdgcn_readfirstlane(s_len[wave]);
         for (int j = 0; j < len; j++) {
             if (__all(done)) break;  // uniform
+            if (STATS) st_entries++;
             const int t = __builtin_amdgcn_readfirstlane(s_list[wave][j]);
             const float4 xyo = s_xyo[t];
             const float4 con = s_con[t];
@@ -186,7 +189,12 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             r2 = take ? __builtin_fmaf(c.z, w, r2) : r2;
             cur = take ? bstart + t : cur;
             T = take ? next_T : T;
+            if (STATS) st_taken += __popcll(__ballot(take));
         }
+    }
+    if (STATS && (tid & 63) == 0) {
+        atomicAdd(&a.stats[kStatFwdEntries], st_entries);
+        atomicAdd(&a.stats[kStatFwdTaken], st_taken);
     }
     if (!inside) return;
     out_alpha[pix] = 1.0f - T;
@@ -229,7 +237,7 @@ __device__ __forceinline__ float wave_sum4(float a, float b, float c, float d) {
 
 constexpr int kGrads = 9;  // v_xy(2), v_opacity, v_conic(3), v_rgb(3)
 
-template <bool ABSGRAD>
+template <bool ABSGRAD, bool STATS>
 __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const float* __restrict__ ralpha,
                                                          const int32_t* __restrict__ last_ids,
                                                          const float* __restrict__ v_rc, const float* __restrict__ v_ra,
@@ -282,6 +290,8 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     // row r of a wave_sum4 result belongs to slot A=0, C=2, B=1, D=3 for r = 0..3
     const int row = lane >> 4;
     const int row_slot = row == 0 ? 0 : row == 1 ? 2 : row == 2 ? 1 : 3;
+    // STATS only (wave-uniform)
+    unsigned long long st_chunks = 0, st_entries = 0, st_empty = 0, st_cut = 0, st_contrib = 0;
     for (int b = 0; b < num_batches; b++) {
         __syncthreads();
         const int32_t batch_end = tile_end - 1 - kThreads * b;
@@ -346,6 +356,17 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
                 sig[k] = sigma_of(con[k].x, con[k].y, con[k].z, dxs[k], dys[k]);
                 valid[k] = (ts[k] >= 0) & (tc[k] >= t_min) & !(sig[k] > xyo[k].w);  // bitwise: no branches
             }
+            const bool any_valid = __any(valid[0] | valid[1] | valid[2] | valid[3]);
+            if (STATS) {
+                st_chunks++;
+                st_entries += min(4, len - j);
+                st_empty += any_valid ? 0 : 1;
+#pragma unroll
+                for (int k = 0; k < 4; k++) st_cut += __popcll(__ballot(valid[k]));
+            }
+            // no lane has a pair inside the cutoff: every alpha would be 0, leaving T, the back-sum and
+            // the gradients as they are
+            if (!any_valid) continue;  // uniform
             // The exponential's value only enters gradients (compared at a relative tolerance), so the
             // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
             // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at
@@ -381,6 +402,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
                 const bool ok = valid[k] & !((sig[k] < 0.f) | (alpha_raw < sx::kAlphaThreshold));
                 alpha[k] = ok ? alpha_raw : 0.0f;
                 vis[k] = (ok & (oa <= sx::kMaxAlpha)) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
+                if (STATS) st_contrib += __popcll(__ballot(ok));
             }
 #pragma unroll
             for (int k = 0; k < 4; k++) {
@@ -474,6 +496,13 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
             }
         }
     }
+    if (STATS && lane == 0) {
+        atomicAdd(&a.stats[kStatBwdChunks], st_chunks);
+        atomicAdd(&a.stats[kStatBwdEntries], st_entries);
+        atomicAdd(&a.stats[kStatBwdEmptyChunks], st_empty);
+        atomicAdd(&a.stats[kStatBwdInCutoff], st_cut);
+        atomicAdd(&a.stats[kStatBwdContrib], st_contrib);
+    }
 }
 
 } // namespace
@@ -559,17 +588,25 @@ void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, in
 void raster_fwd(const RasterArgs& a, float* rgb, float* alpha, int32_t* last, hipStream_t s) {
     const int blocks = a.I * a.tile_width * a.tile_height;
     if (blocks <= 0) return;
-    hipLaunchKernelGGL(k_raster_fwd, dim3(blocks), dim3(kThreads), 0, s, a, rgb, alpha, last);
+    if (a.stats)
+        hipLaunchKernelGGL(k_raster_fwd<true>, dim3(blocks), dim3(kThreads), 0, s, a, rgb, alpha, last);
+    else
+        hipLaunchKernelGGL(k_raster_fwd<false>, dim3(blocks), dim3(kThreads), 0, s, a, rgb, alpha, last);
 }
 
 void raster_bwd(const RasterArgs& a, const float* ralpha, const int32_t* last_ids, const float* v_rc,
                 const float* v_ra, const RasterBwdGrads& g, hipStream_t s) {
     const int blocks = a.I * a.tile_width * a.tile_height;
     if (blocks <= 0 || (!a.n_isects_dev && a.n_isects <= 0)) return;
-    if (g.v_means2d_abs)
-        hipLaunchKernelGGL(k_raster_bwd<true>, dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc, v_ra, g);
+    if (g.v_means2d_abs)  // the per-op entry's absgrad (never counted)
+        hipLaunchKernelGGL((k_raster_bwd<true, false>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc,
+                           v_ra, g);
+    else if (a.stats)
+        hipLaunchKernelGGL((k_raster_bwd<false, true>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc,
+                           v_ra, g);
     else
-        hipLaunchKernelGGL(k_raster_bwd<false>, dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc, v_ra, g);
+        hipLaunchKernelGGL((k_raster_bwd<false, false>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc,
+                           v_ra, g);
 }
 
 } // namespace sxk

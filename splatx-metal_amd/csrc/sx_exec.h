@@ -75,8 +75,11 @@ struct sxh_executor {
     // segment B of the step as executable graphs: [0] training step, [1] forward only
     hipGraphExec_t graph_b[2] = {nullptr, nullptr};
     bool use_graph = true;
-    // profiling
+    // profiling: per-kernel events (bit 0), raster pair counts (bit 1)
     bool prof = false;
+    bool prof_stats = false;
+    sxh::DevBuf<unsigned long long> rstats;
+    sxh_raster_stats rstats_host{};
     hipEvent_t ev[kMaxEvents] = {};
     const char* ev_name[kMaxEvents] = {};
     int n_ev = 0;

@@ -117,6 +117,23 @@ struct RasterArgs {
     // optional: the intersection count on the device (read instead of n_isects), so that the
     // launches do not depend on it
     const int64_t* n_isects_dev;
+    // optional (profiling): pair counters the rasterisers add into, kRasterStat* indices; null in
+    // production (the counting kernels are separate instantiations)
+    unsigned long long* stats;
+};
+// raster pair counters (RasterArgs::stats): list entries walked (one splat against the 64 pixels of
+// a wave), pairs composited (forward), 4-entry chunks, chunks in which no lane's pair is inside the
+// cutoff, lane pairs inside the cutoff and before the pixel's last contributor, pairs that
+// contribute (alpha >= 1/255) (backward)
+enum RasterStat : int {
+    kStatFwdEntries = 0,
+    kStatFwdTaken = 1,
+    kStatBwdChunks = 2,
+    kStatBwdEntries = 3,
+    kStatBwdEmptyChunks = 4,
+    kStatBwdInCutoff = 5,
+    kStatBwdContrib = 6,
+    kRasterStats = 8
 };
 // tile_order for raster_fwd/raster_bwd: the n_tiles tile ids by descending intersection count
 // (counting sort on 256 buckets of the count; order within a bucket unspecified)

@@ -407,6 +407,11 @@ class RenderSession:
         self.h = None
 
 
+class RasterStats(C.Structure):
+    _fields_ = [(k, C.c_uint64) for k in ("fwd_entries", "fwd_taken", "bwd_chunks", "bwd_entries", "bwd_empty_chunks",
+                                          "bwd_in_cutoff", "bwd_contrib")]
+
+
 class ExecTiming(C.Structure):
     _fields_ = [("n", C.c_int32), ("names", C.c_char_p * 32), ("ms", C.c_float * 32)]
 
@@ -946,8 +951,18 @@ class Executor:
         f.restype = C.c_int32
         self._check(f(self.h))
 
-    def set_profiling(self, enable: bool):
-        self._check(self.lib.sxh_exec_set_profiling(self.h, int(bool(enable))))
+    def set_profiling(self, enable: bool, pair_stats: bool = False):
+        """Per-kernel HIP-event times of each step (enable); with pair_stats also the rasterisers' pair
+        counts (counting kernels: use the counts, not the times, of such steps)."""
+        flags = (1 if enable else 0) | (2 if pair_stats else 0)
+        self._check(self.lib.sxh_exec_set_profiling(self.h, flags))
+
+    def get_raster_stats(self) -> dict:
+        st = RasterStats()
+        f = self.lib.sxh_exec_get_raster_stats
+        f.restype = C.c_int32
+        self._check(f(self.h, C.byref(st)))
+        return {k: int(getattr(st, k)) for k, _ in RasterStats._fields_}
 
     def set_graph(self, enable: bool):
         """Run the step's second segment as a captured hipGraph (default) or as direct launches."""
