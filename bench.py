@@ -38,15 +38,22 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
     kb = shape["key_b"]
     if name == "preprocess":
         # params of every Gaussian (44 B) + SH coefficients of visible ones; writes radii+count (12 B),
-        # and for visible ones the 48-B splat record and the zeroed 48-B gradient record
-        return 44.0 * n + 4.0 * 3 * sh_k * v + 12.0 * n + 96.0 * v
+        # and for visible ones the 48-B splat record
+        return 44.0 * n + 4.0 * 3 * sh_k * v + 12.0 * n + 48.0 * v
     if name == "postprocess":
-        # visible: read params, both moments, grads (36 B) and conic/comp/meta (20 B); write params+moments
-        return 4.0 * (n - v) + v * (4.0 * pd * 3 + 36 + 20 + 4.0 * pd * 3)
+        # every row's meta word and touched flag; visible: read params, both moments, grads (36 B) and
+        # conic/comp/meta (20 B); write params+moments
+        return 5.0 * n + v * (4.0 * pd * 3 + 36 + 20 + 4.0 * pd * 3)
     if name == "raster_fwd":
-        return i * (4 + 36) + px * 20.0
+        # per intersection: its emit position (4 B), the Gaussian of that position (4 B), the 36-B record
+        return i * (4 + 4 + 36) + px * 20.0
     if name == "raster_bwd":
-        return i * (4 + 36 + 36) + px * (4 + 4 + 12)
+        # as the forward, plus the 36-B sums stored per (tile, Gaussian) and its valid bit
+        return i * (4 + 4 + 36 + 36 + 1.0 / 8.0) + px * (4 + 4 + 12)
+    if name == "gather":
+        # depth order and the scan per Gaussian (12 B), the valid bits and 36-B sums of the entries, the
+        # 48-B gradient record of the visible Gaussians
+        return n * 12.0 + i * (36.0 + 1.0 / 8.0) + v * 48.0
     if name == "depth_sort":
         # keys: tile counts (4 B) and the depths of the visible (4 B) in, (key, index) out (8 B); then the
         # onesweep sort of n (u32, i32) pairs: one histogram read (4 B), per pass a read and a write (16 B)
@@ -59,8 +66,9 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
         # (tile id, index) entries out
         return n * 12.0 + v * 32.0 + i * (kb + 4.0)
     if name == "sort":
-        # tile sort: one histogram read of the ids, per pass a read and a write of (id, index)
-        return i * (kb + 2.0 * (kb + 4.0) * shape["tile_passes"])
+        # tile sort: one histogram read of the ids, per pass a read and a write of (id, emit position); the
+        # first pass takes the positions from the key index instead of reading them
+        return i * (kb + 2.0 * (kb + 4.0) * shape["tile_passes"] - 4.0)
     if name == "offsets":
         return 4.0 * (px / 256.0)
     if name == "ssim_fwd":
@@ -380,13 +388,14 @@ def main():
     }
     if pair_tot:  # per-step means; a list entry is one splat against the 64 pixels of a wave
         pm = {k: x / args.steps for k, x in pair_tot.items()}
-        rp = {"fwd_lane_pairs": round(pm["fwd_entries"] * 64), "fwd_composited": round(pm["fwd_taken"]),
-              "bwd_lane_pairs": round(pm["bwd_entries"] * 64), "bwd_in_cutoff": round(pm["bwd_in_cutoff"]),
+        rp = {"fwd_lane_pairs": round(pm["fwd_iters"] * 64), "fwd_block_entries": round(pm["fwd_entries"]),
+              "fwd_composited": round(pm["fwd_taken"]), "bwd_lane_pairs": round(pm["bwd_chunks"] * 256),
+              "bwd_block_entries": round(pm["bwd_entries"]), "bwd_in_cutoff": round(pm["bwd_in_cutoff"]),
               "bwd_contributing": round(pm["bwd_contrib"]), "bwd_chunks": round(pm["bwd_chunks"]),
               "bwd_empty_chunks": round(pm["bwd_empty_chunks"]), "upper_bound_256I": round(256 * I)}
         vb = load_valu("raster_bwd", args.config)
-        if vb is not None and pm["bwd_entries"] > 0:  # wave-level VALU instructions per list entry
-            rp["bwd_valu_per_entry"] = round(vb["valu_insts"] / pm["bwd_entries"], 1)
+        if vb is not None and pm["bwd_chunks"] > 0:  # wave-level VALU instructions per 4-iteration chunk
+            rp["bwd_valu_per_chunk"] = round(vb["valu_insts"] / pm["bwd_chunks"], 1)
         res["raster_pairs"] = rp
     vi = load_valu(dom, args.config)
     if vi is not None:  # the dominant kernel's own bound when it is compute-, not memory-bound

@@ -648,10 +648,11 @@ typedef struct {
     float ms[32];
 } sxh_exec_timing;
 typedef struct {
-    uint64_t fwd_entries;       /* list entries walked: one splat against the 64 pixels of a wave */
+    uint64_t fwd_iters;         /* forward wave iterations (x 64 = lane pairs evaluated) */
+    uint64_t fwd_entries;       /* block-list entries walked: one splat against a 4x4 pixel block */
     uint64_t fwd_taken;         /* pairs composited (alpha >= 1/255, T not yet spent) */
-    uint64_t bwd_chunks;        /* 4-entry chunks of the per-wave lists */
-    uint64_t bwd_entries;       /* list entries in those chunks (x 64 = lane pairs evaluated) */
+    uint64_t bwd_chunks;        /* backward 4-iteration chunks (x 256 = lane pairs evaluated) */
+    uint64_t bwd_entries;       /* block-list entries in those chunks */
     uint64_t bwd_empty_chunks;  /* chunks in which no lane's pair is inside the cutoff (skipped) */
     uint64_t bwd_in_cutoff;     /* lane pairs inside the cutoff and at or before the pixel's last contributor */
     uint64_t bwd_contrib;       /* pairs that contribute a gradient (alpha >= 1/255) */

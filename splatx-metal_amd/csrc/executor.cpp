@@ -61,6 +61,9 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->radii.alloc(R * 2);
             e->tiles.alloc(R);
             e->cum.alloc(R);
+            e->long_list.alloc(R);
+            e->long_count.alloc(1);
+            e->touched.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
             e->dkey_a.alloc(R);
             e->dkey_b.alloc(R);
@@ -242,7 +245,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     // ---- segment A: preprocess + counts -----------------------------------------------------------
     if (e->prof_stats) SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
     e->mark("start");
-    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->grads.p, e->vis_part.p, e->n_vis.p, s);
+    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, s);
     e->mark("preprocess");
     int64_t* hs = static_cast<int64_t*>(e->host_small.p);
     // visible count, intersection total
@@ -280,19 +283,19 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
             uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->vals_a.p, s);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s);
             e->mark("emit");
-            which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits, e->sort_scratch.p, s,
-                                    false, n_dev);
+            which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
+                                              e->sort_scratch.p, s, false, n_dev);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         } else {
             uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
             uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->vals_a.p, s);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s);
             e->mark("emit");
-            which = sxk::radix_sort(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits, e->sort_scratch.p, s,
-                                    false, n_dev);
+            which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
+                                              e->sort_scratch.p, s, false, n_dev);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         }
@@ -310,6 +313,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         ra.tile_height = th;
         ra.n_isects = static_cast<int32_t>(n_host);
         ra.n_isects_dev = n_dev;
+        ra.id_of = e->emit_gid.p;  // the sorted values are emit positions
         ra.stats = e->prof_stats ? e->rstats.p : nullptr;  // never in a captured graph (profiling launches directly)
         sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev);
         ra.tile_order = e->tile_order.p;
@@ -330,10 +334,18 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_l1_grad(e->render.p, gt, static_cast<int64_t>(n_px), e->v_render.p, e->l1_part.p, n_l1, s);
             e->mark("l1_grad");
         }
-        sxk::RasterBwdGrads gg{nullptr, nullptr, nullptr, nullptr, nullptr, e->grads.p};
+        // the backward stores per-(tile, Gaussian) sums; the gather adds them per Gaussian in emit order, so
+        // the gradients do not depend on the order in which tiles finish (no float atomics)
+        sxk::raster_clear_valid(e->valid.p, n_dev ? static_cast<int64_t>(e->isect_cap) : n_host, n_dev, e->touched.p,
+                                c.count, e->long_count.p, s);
+        sxk::RasterBwdGrads gg{nullptr, nullptr,   nullptr,    nullptr,    nullptr,
+                               e->grads.p, e->part.p, e->valid.p, e->touched.p};
         sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
         e->mark("raster_bwd");
-        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, s);
+        sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->valid.p, e->touched.p, e->grads.p,
+                                 e->long_list.p, e->long_count.p, s);
+        e->mark("gather");
+        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s);
         e->mark("postprocess");
         sxk::step_loss_final(e->l1_part.p, n_l1, e->ssim_part.p, n_ss, static_cast<double>(n_px),
                              static_cast<double>(map_n), e->d.ssim_weight, use_ssim ? 1 : 0, e->loss_dev.p, s);
@@ -409,9 +421,10 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     if (e->prof_stats) {
         unsigned long long st[sxk::kRasterStats];
         SXH_HIP(hipMemcpy(st, e->rstats.p, sizeof(st), hipMemcpyDeviceToHost));
-        e->rstats_host = sxh_raster_stats{st[sxk::kStatFwdEntries], st[sxk::kStatFwdTaken], st[sxk::kStatBwdChunks],
-                                          st[sxk::kStatBwdEntries], st[sxk::kStatBwdEmptyChunks],
-                                          st[sxk::kStatBwdInCutoff], st[sxk::kStatBwdContrib]};
+        e->rstats_host = sxh_raster_stats{st[sxk::kStatFwdIters],       st[sxk::kStatFwdEntries],
+                                          st[sxk::kStatFwdTaken],       st[sxk::kStatBwdChunks],
+                                          st[sxk::kStatBwdEntries],     st[sxk::kStatBwdEmptyChunks],
+                                          st[sxk::kStatBwdInCutoff],    st[sxk::kStatBwdContrib]};
     }
     if (*hsort) throw std::runtime_error(std::string(what) + ": radix sort look-back did not complete");
     if (e->prof) {

@@ -3,16 +3,25 @@
 // Contracts: rasterize_to_pixels_3dgs_fwd/bwd (Rasterize3DGSFwd.metal:57-204,
 // Rasterize3DGSBwd.metal:70-298). One 256-thread workgroup (4 waves of 64) per 16x16 tile, one
 // thread per pixel. Splat records (3 x float4) are staged through LDS in batches of 256.
+//
+// Block groups: the tile is sixteen 4x4 pixel blocks. Wave w covers the 8x8 quadrant
+// (w & 1, w >> 1); its lanes form four 16-lane groups, one block each (lane l: group l >> 4, pixel
+// l & 15 at (l & 3, (l >> 2) & 3) of the block). Per batch each block gets the list of the batch's
+// splats whose cutoff set can reach it, in depth order, and the four groups of a wave walk their own
+// lists in lockstep: a group reads its own splat from LDS, so a wave evaluates four splats against
+// the 16 pixels each can reach instead of one splat against a 64-pixel strip (the splats are small:
+// most of a strip's lanes would sit outside their cutoff).
 // Forward: front-to-back compositing with the exclusive T <= 1e-4 stop, per-pixel arithmetic in
 // the CPU reference's order (CpuKernels.cpp:821-849) and the deterministic exp of sx_fmath.h, so
 // colors/alphas/last_ids are bit-identical to the CPU oracle; the workgroup exits as soon as all
 // its pixels are done.
-// Backward: back-to-front walk recovering T by division. Contributing Gaussians are taken four at a
-// time; their nine gradient components are summed over the wave with one transposed reduction
-// (gfx950 v_permlane32_swap / v_permlane16_swap folds, then DPP within 16-lane rows), the four waves
-// of the tile add their sums into LDS, and one set of float atomics per (tile, Gaussian) is issued
-// after each batch.
+// Backward: back-to-front walk recovering T by division, four list entries per group at a time;
+// a group sums its four splats' nine gradient components over its 16 lanes with one transposed
+// reduction (11 DPP/select instructions per component), the groups add their sums into LDS, and one
+// set of float atomics per (tile, Gaussian) is issued after each batch.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "sx_dev.h"
 #include "sx_kernels.h"
@@ -21,10 +30,16 @@ namespace sxk {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kBlocks = 16;  // 4x4 pixel blocks of a tile
+#ifndef SX_BWD_SEG
+#define SX_BWD_SEG 32
+#endif
+// backward segment: batch slots whose sums are flushed together (32: 34 KB of LDS, 4 workgroups per CU)
+constexpr int kBwdSeg = SX_BWD_SEG;
 
 // sxm::expf_fast(-sigma) without its range branches: identical for sigma in [0, 86] (no overflow,
-// no subnormal scaling). exp_neg: `cut` is the Gaussian's sigma cutoff, wave-uniform, and only an
-// opacity above ~1e35 pushes it past that range, in which case the general function is used.
+// no subnormal scaling). Only an opacity above ~1e35 pushes a cutoff past that range; the callers
+// then take the general function for the whole wave.
 __device__ __forceinline__ float exp_neg_poly(float sigma) {
     const float x = -sigma;
     const float kf = __builtin_rintf(x * 1.44269502f);
@@ -43,12 +58,6 @@ __device__ __forceinline__ float exp_neg_poly(float sigma) {
     return p * __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
 }
 
-__device__ __forceinline__ float exp_neg(float sigma, float cut) {
-    const float cut_u = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cut)));  // uniform branch
-    if (__builtin_expect(cut_u > 86.0f, 0)) return sxm::expf_fast(-sigma);
-    return exp_neg_poly(sigma);
-}
-
 __device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx, float dy) {
     return 0.5f * (ca * dx * dx + cc * dy * dy) + cb * dx * dy;
 }
@@ -58,54 +67,70 @@ __device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx
 // most e^-0.01/255), so skipping its exp leaves every result bit-identical.
 __device__ __forceinline__ float sigma_cutoff(float opac) { return __logf(opac * 255.0f) + 0.01f; }
 
-// Which of the tile's four waves (pixel rows y0 + 4w .. y0 + 4w + 3) the Gaussian's cutoff set
-// {sigma <= cut} can reach: for a positive-definite conic the set's y half-extent is
-// sqrt(2 cut a / det). Conservative: the extent gets a relative and an absolute margin far above
-// float rounding of sigma, and every degenerate, nearly degenerate or non-finite case keeps all
-// four waves.
-__device__ __forceinline__ uint32_t wave_rows_mask(float4 xyo, float4 con, int y0) {
+// The block of lane `lane` in wave `wave` (bit index by * 4 + bx of a block mask).
+__device__ __forceinline__ int block_of(int wave, int lane) {
+    const int q = lane >> 4;
+    return (2 * (wave >> 1) + (q >> 1)) * 4 + 2 * (wave & 1) + (q & 1);
+}
+
+// Which of the tile's sixteen 4x4 blocks the Gaussian's cutoff set {sigma <= cut} can reach (bit
+// by * 4 + bx): the set's bounding box, half-extents sqrt(2 cut c / det) in x and sqrt(2 cut a / det)
+// in y for a positive-definite conic, against each block's rectangle of pixel centres. Conservative:
+// the extents get a relative and an absolute margin far above float rounding of sigma, and every
+// degenerate, nearly degenerate or non-finite case keeps all sixteen blocks.
+__device__ __forceinline__ uint32_t block_mask(float4 xyo, float4 con, float x0, float y0) {
     const float a = con.x, b = con.y, c = con.z, cut = xyo.w;
     if (cut == -__builtin_inff()) return 0u;  // opacity 0: no pixel passes
     const float det = a * c - b * b;
     const bool finite = __builtin_isfinite(a) && __builtin_isfinite(b) && __builtin_isfinite(c) &&
                         __builtin_isfinite(cut) && __builtin_fabsf(xyo.x) < 1e18f && __builtin_fabsf(xyo.y) < 1e18f;
-    if (!finite || !(a > 0.f) || !(det > 1e-4f * a * c)) return 0xFu;
+    if (!finite || !(a > 0.f) || !(det > 1e-4f * a * c)) return 0xFFFFu;
     if (cut < 0.f) return 0u;  // sigma >= 0 everywhere for a positive-definite conic
+    const float rx = __builtin_sqrtf(2.0f * cut * c / det) * 1.001f + 0.01f;
     const float ry = __builtin_sqrtf(2.0f * cut * a / det) * 1.001f + 0.01f;
-    const float lo = xyo.y - ry, hi = xyo.y + ry;
+    uint32_t cols = 0u, rows = 0u;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float bx0 = x0 + static_cast<float>(4 * k) + 0.5f, by0 = y0 + static_cast<float>(4 * k) + 0.5f;
+        if (xyo.x + rx >= bx0 && xyo.x - rx <= bx0 + 3.0f) cols |= 1u << k;
+        if (xyo.y + ry >= by0 && xyo.y - ry <= by0 + 3.0f) rows |= 1u << k;
+    }
     uint32_t m = 0u;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const float r0 = static_cast<float>(y0 + 4 * w) + 0.5f, r1 = r0 + 3.0f;
-        if (hi >= r0 && lo <= r1) m |= 1u << w;
-    }
+    for (int k = 0; k < 4; k++)
+        if ((rows >> k) & 1u) m |= cols << (4 * k);
     return m;
 }
 
-// Per-wave Gaussian lists of a batch: s_list[w][0 .. s_len[w]) = the batch-local indices t (in
-// increasing order) whose mask has bit w. All 256 threads call it; thread t passes Gaussian t's mask
+// Per-block Gaussian lists of a batch: s_list[bl][0 .. s_len[bl]) = the batch-local indices t (in
+// increasing order) whose mask has bit bl. All 256 threads call it; thread t passes Gaussian t's mask
 // (0 for slots past the batch). Ends with a barrier.
-__device__ __forceinline__ void build_wave_lists(uint32_t m, uint8_t (*s_list)[kThreads], int (*s_wc)[4],
-                                                 int* s_len) {
+__device__ __forceinline__ void build_block_lists(uint32_t m, uint8_t (*s_list)[kThreads], int (*s_bc)[4],
+                                                  int* s_len) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int pos[4];
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const unsigned long long bal = __ballot((m >> w) & 1u);
-        pos[w] = __popcll(bal & below);
-        if (lane == 0) s_wc[w][wave] = __popcll(bal);
+    for (int bl = 0; bl < kBlocks; bl++) {
+        const unsigned long long bal = __ballot((m >> bl) & 1u);
+        if (lane == 0) s_bc[bl][wave] = __popcll(bal);
     }
     __syncthreads();
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
+    for (int bl = 0; bl < kBlocks; bl++) {
+        const unsigned long long bal = __ballot((m >> bl) & 1u);
         int off = 0;
 #pragma unroll
-        for (int sw = 0; sw < 4; sw++) off += sw < wave ? s_wc[w][sw] : 0;
-        if ((m >> w) & 1u) s_list[w][off + pos[w]] = static_cast<uint8_t>(tid);
-        if (tid == 0) s_len[w] = s_wc[w][0] + s_wc[w][1] + s_wc[w][2] + s_wc[w][3];
+        for (int sw = 0; sw < 4; sw++) off += sw < wave ? s_bc[bl][sw] : 0;
+        if ((m >> bl) & 1u) s_list[bl][off + __popcll(bal & below)] = static_cast<uint8_t>(tid);
     }
+    if (tid < kBlocks) s_len[tid] = s_bc[tid][0] + s_bc[tid][1] + s_bc[tid][2] + s_bc[tid][3];
     __syncthreads();
+}
+
+// The longest of the four block lists of wave `wave` (wave-uniform).
+__device__ __forceinline__ int wave_list_max(const int* s_len, int wave) {
+    const int b0 = block_of(wave, 0), b1 = block_of(wave, 16), b2 = block_of(wave, 32), b3 = block_of(wave, 48);
+    return max(max(s_len[b0], s_len[b1]), max(s_len[b2], s_len[b3]));
 }
 
 template <bool STATS>
@@ -114,16 +139,17 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
     __shared__ float4 s_con[kThreads];
     __shared__ float4 s_rgb[kThreads];
-    __shared__ uint8_t s_list[4][kThreads];
-    __shared__ int s_wc[4][4];
-    __shared__ int s_len[4];
+    __shared__ __align__(16) uint8_t s_list[kBlocks][kThreads];
+    __shared__ int s_bc[kBlocks][4];
+    __shared__ int s_len[kBlocks];
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
     const int tile = a.tile_order ? a.tile_order[blockIdx.x % n_tiles] : static_cast<int>(blockIdx.x % n_tiles);
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int px_i = tx * 16 + (tid & 15), py_i = ty * 16 + (tid >> 4);
+    const int wave = tid >> 6, lane = tid & 63;
+    const int bl = block_of(wave, lane);
+    const int px_i = tx * 16 + 4 * (bl & 3) + (lane & 3), py_i = ty * 16 + 4 * (bl >> 2) + ((lane >> 2) & 3);
     const bool inside = px_i < a.width && py_i < a.height;
     const size_t pix = (size_t)img * a.height * a.width + (size_t)py_i * a.width + px_i;
     const float* bg = a.backgrounds ? a.backgrounds + img * 3 : nullptr;
@@ -146,36 +172,44 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     int32_t cur = 0;
     float r0 = 0.f, r1 = 0.f, r2 = 0.f;
     bool done = !inside;
-    unsigned long long st_entries = 0, st_taken = 0;  // STATS only (wave-uniform)
+    unsigned long long st_iters = 0, st_entries = 0, st_taken = 0;  // STATS only (wave-uniform)
     for (int32_t bstart = range_start; bstart < range_end; bstart += kThreads) {
         if (__syncthreads_count(done) == kThreads) break;  // also the barrier before LDS reuse
         const int32_t idx = bstart + tid;
-        uint32_t wm = 0u;
+        uint32_t bm = 0u;
         if (idx < range_end) {
-            const int32_t g = a.flatten_ids[idx];
+            const int32_t f = a.flatten_ids[idx];
+            const int32_t g = a.id_of ? a.id_of[f] : f;
             float4 xyo = a.splats[(size_t)g * 3];
             xyo.w = sigma_cutoff(xyo.z);
             const float4 con = a.splats[(size_t)g * 3 + 1];
             s_xyo[tid] = xyo;
             s_con[tid] = con;
             s_rgb[tid] = a.splats[(size_t)g * 3 + 2];
-            wm = wave_rows_mask(xyo, con, ty * 16);
+            bm = block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
         }
-        build_wave_lists(wm, s_list, s_wc, s_len);
-        // the wave walks its list together (index and count are wave-uniform); a lane takes a pair
-        // through selects rather than branches, and stops taking pairs once its T is spent
-        const int len = __builtin_amdgcn_readfirstlane(s_len[wave]);
-        for (int j = 0; j < len; j++) {
+        build_block_lists(bm, s_list, s_bc, s_len);
+        // the groups walk their lists together (the iteration count is the wave's longest list); a
+        // lane takes a pair through selects rather than branches, and stops once its T is spent
+        const int len = s_len[bl];
+        const int n_it = wave_list_max(s_len, wave);
+        for (int j = 0; j < n_it; j++) {
             if (__all(done)) break;  // uniform
-            if (STATS) st_entries++;
-            const int t = __builtin_amdgcn_readfirstlane(s_list[wave][j]);
-            const float4 xyo = s_xyo[t];
-            const float4 con = s_con[t];
+            const int t = j < len ? static_cast<int>(s_list[bl][j]) : -1;  // group-uniform
+            const int tc = t < 0 ? 0 : t;
+            const float4 xyo = s_xyo[tc];
+            const float4 con = s_con[tc];
             const float dx = xyo.x - px, dy = xyo.y - py;
             const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
-            bool take = !done && !(sigma > xyo.w);  // past the cutoff: provably below the alpha threshold
-            if (!__any(take)) continue;             // uniform: no lane of the wave needs the exponential
-            const float vis = exp_neg(sigma, xyo.w);
+            bool take = (t >= 0) & !done & !(sigma > xyo.w);  // past the cutoff: provably below the alpha threshold
+            if (STATS) {
+                st_iters++;
+                st_entries += __popcll(__ballot((lane & 15) == 0 && t >= 0));
+            }
+            if (!__any(take)) continue;  // uniform: no lane of the wave needs the exponential
+            // one wave-uniform choice of exponential: the branch-free polynomial unless a cutoff in use
+            // exceeds its range (opacity above ~1e35)
+            const float vis = __any(take & (xyo.w > 86.0f)) ? sxm::expf_fast(-sigma) : exp_neg_poly(sigma);
             const float alpha = sxd::smin(sx::kMaxAlpha, xyo.z * vis);
             take = take && !(sigma < 0.f) && !(alpha < sx::kAlphaThreshold);
             const float next_T = T * (1.0f - alpha);
@@ -183,7 +217,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             done = done || spent;
             take = take && !spent;
             const float w = alpha * T;
-            const float4 c = s_rgb[t];
+            const float4 c = s_rgb[tc];
             r0 = take ? __builtin_fmaf(c.x, w, r0) : r0;
             r1 = take ? __builtin_fmaf(c.y, w, r1) : r1;
             r2 = take ? __builtin_fmaf(c.z, w, r2) : r2;
@@ -192,7 +226,8 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             if (STATS) st_taken += __popcll(__ballot(take));
         }
     }
-    if (STATS && (tid & 63) == 0) {
+    if (STATS && lane == 0) {
+        atomicAdd(&a.stats[kStatFwdIters], st_iters);
         atomicAdd(&a.stats[kStatFwdEntries], st_entries);
         atomicAdd(&a.stats[kStatFwdTaken], st_taken);
     }
@@ -204,55 +239,111 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     out_last[pix] = cur;
 }
 
-// ---- wave reductions -----------------------------------------------------------------------------
+// ---- group reductions ------------------------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-// Sum over each 16-lane row; every lane of the row ends with the row total.
-__device__ __forceinline__ float row_sum16(float v) {
-    v += dpp_f<0xB1>(v);   // quad_perm(1,0,3,2): pairs
-    v += dpp_f<0x4E>(v);   // quad_perm(2,3,0,1): quads
-    v += dpp_f<0x141>(v);  // row_half_mirror: 8 lanes
-    v += dpp_f<0x140>(v);  // row_mirror: the 16-lane row
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+// Maximum over each 16-lane row (every lane of the row ends with it).
+__device__ __forceinline__ int row_max16(int v) {
+    v = max(v, dpp_i<0xB1>(v));   // quad_perm(1,0,3,2)
+    v = max(v, dpp_i<0x4E>(v));   // quad_perm(2,3,0,1)
+    v = max(v, dpp_i<0x141>(v));  // row_half_mirror
+    v = max(v, dpp_i<0x140>(v));  // row_mirror
     return v;
 }
-// v_permlane32_swap exchanges lanes 32-63 of `a` with lanes 0-31 of `b`; the sum of the two results
-// holds a's 32-lane half sums in lanes 0-31 and b's in lanes 32-63.
-__device__ __forceinline__ float fold32(float a, float b) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-// v_permlane16_swap exchanges the odd 16-lane rows of `a` with the even rows of `b`; after the sum,
-// row 0 holds a's row-0 + row-1 partials, row 1 b's, row 2 a's rows 2 + 3, row 3 b's.
-__device__ __forceinline__ float fold16(float a, float b) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-// Four per-lane values (one per Gaussian slot A..D) reduced over the 64 lanes in 10 instructions: the
-// result's row 0 holds the total of A, row 1 of C, row 2 of B, row 3 of D (every lane of the row).
-__device__ __forceinline__ float wave_sum4(float a, float b, float c, float d) {
-    return row_sum16(fold16(fold32(a, b), fold32(c, d)));
+// Four per-lane values (one per list slot A..D of the group) summed over each 16-lane group in 11
+// instructions. lo8: lane bit 3 clear; lo4: lane bit 2 clear. Stage 1 pairs lane r with r ^ 8
+// (row_ror:8) and keeps A in lanes 0-7, B in 8-15 (C and D likewise); stage 2 pairs r with its
+// mirror in the 8-lane half (row_half_mirror) and keeps A / B in quads 0 and 2, C / D in quads 1 and
+// 3; the quad sums finish it. The result: quad 0 holds the group total of A, quad 1 of C, quad 2 of
+// B, quad 3 of D (every lane of the quad).
+__device__ __forceinline__ float group_sum4(float a, float b, float c, float d, bool lo8, bool lo4) {
+    const float s1 = (lo8 ? a : b) + dpp_f<0x128>(lo8 ? b : a);
+    const float t1 = (lo8 ? c : d) + dpp_f<0x128>(lo8 ? d : c);
+    float v = (lo4 ? s1 : t1) + dpp_f<0x141>(lo4 ? t1 : s1);
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    return v;
 }
 
 constexpr int kGrads = 9;  // v_xy(2), v_opacity, v_conic(3), v_rgb(3)
+// log(255 * 0.99): from the sigma where alpha turns 1/255 to the sigma where it reaches the 0.99 clamp
+constexpr float kLogAlphaSpan = 5.53121185f;
 
-template <bool ABSGRAD, bool STATS>
-__global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const float* __restrict__ ralpha,
+// The gradient components that term group q of the flush adds (-1: none). Components 0 and 1 (the
+// position moments) stay in one group. With 4 groups: {0,1} {2,3,4} {5,6,(9)} {7,8,(10)}; with 8 or
+// more: {0,1} {2} ... {8} and the absolute moments (9), (10) in groups 4 and 5 (8 groups) or 8 and 9.
+template <int NV, int G>
+__device__ __forceinline__ void flush_terms(int q, int* ks) {
+    ks[0] = ks[1] = ks[2] = -1;
+    if (G == 4) {
+        if (q == 0) { ks[0] = 0; ks[1] = 1; }
+        if (q == 1) { ks[0] = 2; ks[1] = 3; ks[2] = 4; }
+        if (q == 2) { ks[0] = 5; ks[1] = 6; ks[2] = NV > 9 ? 9 : -1; }
+        if (q == 3) { ks[0] = 7; ks[1] = 8; ks[2] = NV > 9 ? 10 : -1; }
+    } else {
+        if (q == 0) { ks[0] = 0; ks[1] = 1; }
+        else if (q <= 7) ks[0] = q + 1;
+        if (NV > 9) {
+            if (G == 8 && q == 4) ks[1] = 9;
+            if (G == 8 && q == 5) ks[1] = 10;
+            if (G >= 16 && q == 8) ks[0] = 9;
+            if (G >= 16 && q == 9) ks[0] = 10;
+        }
+    }
+}
+
+// The address of gradient component k of Gaussian gid: the packed record (x, y, opacity, - | conic
+// a, b, c, - | r, g, b, -) or the per-op arrays.
+__device__ __forceinline__ float* grad_slot(const RasterBwdGrads& g, int32_t gid, int k) {
+    if (g.packed) {
+        static constexpr int kRec[9] = {0, 1, 2, 4, 5, 6, 8, 9, 10};
+        return reinterpret_cast<float*>(g.packed + (size_t)gid * 3) + kRec[k];
+    }
+    switch (k) {
+        case 0: return &g.v_means2d[(size_t)gid * 2];
+        case 1: return &g.v_means2d[(size_t)gid * 2 + 1];
+        case 2: return &g.v_opacities[gid];
+        case 3: return &g.v_conics[(size_t)gid * 3];
+        case 4: return &g.v_conics[(size_t)gid * 3 + 1];
+        case 5: return &g.v_conics[(size_t)gid * 3 + 2];
+        case 6: return &g.v_colors[(size_t)gid * 3];
+        case 7: return &g.v_colors[(size_t)gid * 3 + 1];
+        case 8: return &g.v_colors[(size_t)gid * 3 + 2];
+        case 9: return &g.v_means2d_abs[(size_t)gid * 2];
+        default: return &g.v_means2d_abs[(size_t)gid * 2 + 1];
+    }
+}
+
+// Position of entry e of block bl in its row of the backward's entry buffer: rotated by 4 for the
+// blocks of odd block rows, so that the 16 writers of a chunk (the 2x2 blocks of a wave, four consecutive
+// entries each; rows of kSeg words, a multiple of 32) use 16 different LDS banks.
+__device__ __forceinline__ int ent_rot(int e, int bl, int seg) { return (e + 4 * ((bl >> 2) & 1)) & (seg - 1); }
+
+template <bool ABSGRAD, bool STATS, int kSeg>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5, 8))) k_raster_bwd(RasterArgs a, const float* __restrict__ ralpha,
                                                          const int32_t* __restrict__ last_ids,
                                                          const float* __restrict__ v_rc, const float* __restrict__ v_ra,
                                                          RasterBwdGrads g) {
     constexpr int NV = ABSGRAD ? kGrads + 2 : kGrads;
+    // a segment: kSeg consecutive batch slots (32 or 64); its per-entry sums are flushed before the next
+    constexpr int kBitsPerLane = kSeg / 16;  // list building: lane r of a group places bits [r kBitsPerLane, ...)
+    constexpr int kTermGroups = kThreads / kSeg;  // flush: the threads of a segment's splat share its components
     __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
-    __shared__ float4 s_con[kThreads];
-    __shared__ float4 s_rgb[kThreads];
-    __shared__ int32_t s_id[kThreads];
-    __shared__ float4 s_part4[NV * kThreads / 4];  // per-tile sums [k][t], the four waves add into it
-    __shared__ __align__(16) uint8_t s_list[4][kThreads];
-    __shared__ int s_wc[4][4];
-    __shared__ int s_len[4];
-    __shared__ int32_t s_wbf[4];  // each wave's last contributing intersection
-    float* s_part = reinterpret_cast<float*>(s_part4);
+    __shared__ float4 s_con[kThreads];  // {a, b, c, Gaussian id (int bits)}
+    __shared__ float4 s_rgb[kThreads];  // {r, g, b, flatten_ids entry (int bits)}
+    // per-entry gradient sums of the current segment: [block][component][position in the block's list,
+    // rotated by ent_rot so that the 16 writers of a chunk land in 16 different banks]
+    __shared__ float s_ent[kBlocks][NV][kSeg];
+    __shared__ unsigned long long s_bits[kBlocks][4];  // [block][wave]: the wave's batch slots that reach the block
+    __shared__ uint8_t s_seg[kBlocks][kSeg];          // the block's list of the current segment (slots within it)
+    __shared__ uint16_t s_bm[kThreads];               // each batch slot's block mask
+    __shared__ int32_t s_bbf[kBlocks];                // each block's last contributing intersection
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
     const int tile = a.tile_order ? a.tile_order[blockIdx.x % n_tiles] : static_cast<int>(blockIdx.x % n_tiles);
@@ -260,7 +351,9 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     const int tx = tile % a.tile_width, ty = tile / a.tile_width;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int px_i = tx * 16 + (tid & 15), py_i = ty * 16 + (tid >> 4);
+    const int r = lane & 15;  // lane within its group
+    const int bl = block_of(wave, lane);
+    const int px_i = tx * 16 + 4 * (bl & 3) + (r & 3), py_i = ty * 16 + 4 * (bl >> 2) + (r >> 2);
     const bool inside = px_i < a.width && py_i < a.height;
     const size_t pix = inside ? (size_t)img * a.height * a.width + (size_t)py_i * a.width + px_i
                               : (size_t)img * a.height * a.width;
@@ -279,221 +372,266 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
     const float va = v_ra[pix];
     const float bg_dot = bg ? (bg[0] * vc0 + bg[1] * vc1 + bg[2] * vc2) : 0.f;
     const float tva = T_final * (va - bg_dot);  // the alpha and background terms of every v_alpha, over ra
-    const int32_t wave_bin_final = sxd::wave_max_i(bin_final);
-    if (lane == 0) s_wbf[wave] = wave_bin_final;
+    const int32_t block_bin_final = row_max16(bin_final);
+    if (r == 0) s_bbf[bl] = block_bin_final;
     __syncthreads();
     // the walk starts at the tile's last contributing intersection: everything behind it (most of
     // a dense tile's list, once its pixels saturate) has no pixel to contribute to
-    const int32_t tile_end = min(range_end, max(max(s_wbf[0], s_wbf[1]), max(s_wbf[2], s_wbf[3])) + 1);
+    int32_t tile_bf = s_bbf[0];
+#pragma unroll
+    for (int k = 1; k < kBlocks; k++) tile_bf = max(tile_bf, s_bbf[k]);
+    const int32_t tile_end = min(range_end, tile_bf + 1);
     const int32_t num = max(0, tile_end - range_start);
     const int num_batches = (num + kThreads - 1) / kThreads;
-    // row r of a wave_sum4 result belongs to slot A=0, C=2, B=1, D=3 for r = 0..3
-    const int row = lane >> 4;
-    const int row_slot = row == 0 ? 0 : row == 1 ? 2 : row == 2 ? 1 : 3;
+    // a group's reduction leaves slot A in lane 0, B in 8, C in 4, D in 12: those lanes store them
+    const bool lo8 = (r & 8) == 0, lo4 = (r & 4) == 0;
+    const int wslot = (r == 0) ? 0 : (r == 8) ? 1 : (r == 4) ? 2 : (r == 12) ? 3 : -1;
+    // blocks of this wave's four groups (for the lockstep chunk count)
+    const int wb0 = block_of(wave, 0), wb1 = block_of(wave, 16), wb2 = block_of(wave, 32), wb3 = block_of(wave, 48);
     // STATS only (wave-uniform)
     unsigned long long st_chunks = 0, st_entries = 0, st_empty = 0, st_cut = 0, st_contrib = 0;
     for (int b = 0; b < num_batches; b++) {
-        __syncthreads();
+        __syncthreads();  // the previous batch's flush has read the records
         const int32_t batch_end = tile_end - 1 - kThreads * b;
         const int32_t batch_size = min(kThreads, batch_end + 1 - range_start);
         const int32_t idx = batch_end - tid;
-        uint32_t wm = 0u;
+        uint32_t bm = 0u;
         if (idx >= range_start) {
-            const int32_t gid = a.flatten_ids[idx];
-            s_id[tid] = gid;
+            const int32_t f = a.flatten_ids[idx];  // the Gaussian, or its emit position (id_of)
+            const int32_t gid = a.id_of ? a.id_of[f] : f;
             float4 xyo = a.splats[(size_t)gid * 3];
             xyo.w = sigma_cutoff(xyo.z);
             float4 con = a.splats[(size_t)gid * 3 + 1];
             float4 rgb = a.splats[(size_t)gid * 3 + 2];
-            // the sigmas at which the two alpha decisions turn: opacity * e^-sigma = 1/255 and = 0.99
-            // (approximate; only used to find the pairs close to them)
-            con.w = __logf(xyo.z * (1.0f / sx::kMaxAlpha));
-            rgb.w = __logf(xyo.z * 255.0f);
+            con.w = __int_as_float(gid);
+            rgb.w = __int_as_float(f);
             s_xyo[tid] = xyo;
             s_con[tid] = con;
             s_rgb[tid] = rgb;
-            // waves whose rows the cutoff set can reach, less those whose every pixel stopped before it
-            wm = wave_rows_mask(xyo, con, ty * 16);
+            // blocks the cutoff set can reach, less those whose every pixel stopped before it
+            bm = block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
 #pragma unroll
-            for (int w = 0; w < 4; w++)
-                if (idx > s_wbf[w]) wm &= ~(1u << w);
+            for (int k = 0; k < kBlocks; k++)
+                if (idx > s_bbf[k]) bm &= ~(1u << k);
         }
+        s_bm[tid] = static_cast<uint16_t>(bm);
 #pragma unroll
-        for (int j = tid; j < NV * kThreads / 4; j += kThreads) s_part4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        build_wave_lists(wm, s_list, s_wc, s_len);
-
-        // This wave's Gaussians back to front, four at a time: the four list entries come in one
-        // LDS read and their records in one burst, the four pairs' exponentials are independent,
-        // only T and the back-sum run through them in order. A pair that does not contribute (or a
-        // slot past the list) gets alpha = 0, so T (times 1/(1 - 0) = 1), the back-sum and every
-        // gradient term are left unchanged / zero.
-        const int len = s_len[wave];
-        const uint32_t* list4 = reinterpret_cast<const uint32_t*>(s_list[wave]);
-        const int t_min = batch_end - bin_final;  // slots t >= t_min are at or before the lane's last contributor
-        for (int j = 0; j < len; j += 4) {
-            const uint32_t packed = list4[j >> 2];
-            int ts[4], tc[4];
-            float4 xyo[4], con[4], rgb[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                ts[k] = j + k < len ? static_cast<int>((packed >> (8 * k)) & 0xFFu) : -1;
-                tc[k] = ts[k] < 0 ? 0 : ts[k];
-                xyo[k] = s_xyo[tc[k]];
-                con[k] = s_con[tc[k]];
-                rgb[k] = s_rgb[tc[k]];
-            }
-            // one wave-uniform choice of exponential for the chunk: the branch-free polynomial unless
-            // some cutoff exceeds its range (opacity above ~1e35)
-            const float cmax = sxd::smax(sxd::smax(xyo[0].w, xyo[1].w), sxd::smax(xyo[2].w, xyo[3].w));
-            const bool general = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cmax))) > 86.0f;
-            float gv[4][NV];
-            float alpha[4], vis[4], dxs[4], dys[4], sig[4], e[4];
-            bool valid[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                dxs[k] = xyo[k].x - px;
-                dys[k] = xyo[k].y - py;
-                sig[k] = sigma_of(con[k].x, con[k].y, con[k].z, dxs[k], dys[k]);
-                valid[k] = (ts[k] >= 0) & (tc[k] >= t_min) & !(sig[k] > xyo[k].w);  // bitwise: no branches
-            }
-            const bool any_valid = __any(valid[0] | valid[1] | valid[2] | valid[3]);
-            if (STATS) {
-                st_chunks++;
-                st_entries += min(4, len - j);
-                st_empty += any_valid ? 0 : 1;
-#pragma unroll
-                for (int k = 0; k < 4; k++) st_cut += __popcll(__ballot(valid[k]));
-            }
-            // no lane has a pair inside the cutoff: every alpha would be 0, leaving T, the back-sum and
-            // the gradients as they are
-            if (!any_valid) continue;  // uniform
-            // The exponential's value only enters gradients (compared at a relative tolerance), so the
-            // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
-            // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at
-            // least 1/255, and opacity * exp at most the 0.99 clamp — must be the forward's. Where a lane
-            // lies within 2^-12 in sigma of either turning point, the chunk takes the forward's
-            // exponential instead (the points themselves are approximate to ~1e-6).
-            bool exact = general;
-            if (!exact) {
-                bool near = false;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    e[k] = __builtin_amdgcn_exp2f(-sig[k] * 1.44269504f);
-                    const bool n1 = __builtin_fabsf(sig[k] - rgb[k].w) < 0x1p-12f;
-                    const bool n2 = __builtin_fabsf(sig[k] - con[k].w) < 0x1p-12f;
-                    near = near | (valid[k] & (n1 | n2));
-                }
-                exact = __any(near);
-            }
-            if (__builtin_expect(exact, 0)) {
-                if (general) {
-#pragma unroll
-                    for (int k = 0; k < 4; k++) e[k] = sxm::expf_fast(-sig[k]);
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 4; k++) e[k] = exp_neg_poly(sig[k]);
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float vis_raw = e[k];
-                const float oa = xyo[k].z * vis_raw;
-                const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
-                const bool ok = valid[k] & !((sig[k] < 0.f) | (alpha_raw < sx::kAlphaThreshold));
-                alpha[k] = ok ? alpha_raw : 0.0f;
-                vis[k] = (ok & (oa <= sx::kMaxAlpha)) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
-                if (STATS) st_contrib += __popcll(__ballot(ok));
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                // hardware reciprocal (1 ulp; exact for 1): the backward is compared at a relative
-                // tolerance, and an IEEE division costs ~10 instructions per pair
-                const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - alpha[k]));
-                T *= ra;
-                const float fac = alpha[k] * T;
-                gv[k][6] = fac * vc0;
-                gv[k][7] = fac * vc1;
-                gv[k][8] = fac * vc2;
-                // v_alpha = sum_c (c_c T - b_c ra) vc_c + T_final ra (va - <bg, vc>), with the back-sum
-                // kept as its dot product with v_render (fused multiply-adds: gradient algebra only)
-                const float cvc = __builtin_fmaf(rgb[k].x, vc0, __builtin_fmaf(rgb[k].y, vc1, rgb[k].z * vc2));
-                const float v_alpha = __builtin_fmaf(T, cvc, ra * (tva - bdot));
-                const float v_sigma = -xyo[k].z * vis[k] * v_alpha;
-                const float dx = dxs[k], dy = dys[k];
-                const float vdx = v_sigma * dx, vdy = v_sigma * dy;
-                if (ABSGRAD) {  // per-pixel 2D gradients are needed for their absolute values
-                    gv[k][0] = __builtin_fmaf(con[k].x, vdx, con[k].y * vdy);
-                    gv[k][1] = __builtin_fmaf(con[k].y, vdx, con[k].z * vdy);
-                    gv[k][3] = 0.5f * vdx * dx;
-                    gv[k][5] = 0.5f * vdy * dy;
-                    gv[k][9] = fabsf(gv[k][0]);
-                    gv[k][10] = fabsf(gv[k][1]);
-                } else {  // moments: the conic and the halves are applied once per splat at the flush
-                    gv[k][0] = vdx;
-                    gv[k][1] = vdy;
-                    gv[k][3] = vdx * dx;
-                    gv[k][5] = vdy * dy;
-                }
-                gv[k][4] = vdx * dy;
-                gv[k][2] = vis[k] * v_alpha;
-                bdot = __builtin_fmaf(fac, cvc, bdot);
-            }
-            const int t_row = ts[row_slot];
-            const bool writer = (lane & 15) == 0 && t_row >= 0;
-            float* dst = s_part + (t_row < 0 ? 0 : t_row);
-#pragma unroll
-            for (int k = 0; k < NV; k++) {
-                const float v = wave_sum4(gv[0][k], gv[1][k], gv[2][k], gv[3][k]);
-                if (writer) atomicAdd(&dst[k * kThreads], v);  // LDS add: the four waves of the tile
-            }
+        for (int k = 0; k < kBlocks; k++) {
+            const unsigned long long bal = __ballot((bm >> k) & 1u);
+            if (lane == 0) s_bits[k][wave] = bal;
         }
         __syncthreads();
-        // one thread per Gaussian of the batch: one global atomic per gradient component
-        if (tid < batch_size) {
-            float v[NV];
-            bool any = false;
+
+        const int t_min = batch_end - bin_final;  // slots t >= t_min are at or before the lane's last contributor
+        const int n_seg = (batch_size + kSeg - 1) / kSeg;
+        for (int sg = 0; sg < n_seg; sg++) {
+            // the segment's slots that reach a block: bits of the owning wave's ballot
+            auto seg_bits = [&](int blk) -> unsigned long long {
+                const unsigned long long w = s_bits[blk][(kSeg * sg) >> 6];
+                if constexpr (kSeg == 64) return w;
+                else return (w >> ((kSeg * sg) & 63)) & ((1ull << kSeg) - 1ull);
+            };
+            // this group's list of the segment: lane r places the set slots among its kBitsPerLane bits
+            const unsigned long long bits = seg_bits(bl);
+            const int cnt = __popcll(bits);
+            {
+                const int b0 = kBitsPerLane * r;  // at most kSeg - kBitsPerLane: the shifts stay below 64
+                const uint32_t nib = static_cast<uint32_t>(bits >> b0) & ((1u << kBitsPerLane) - 1u);
+                int pos = __popcll(bits & ((1ull << b0) - 1ull));
 #pragma unroll
-            for (int k = 0; k < NV; k++) {
-                v[k] = s_part[k * kThreads + tid];
-                any |= v[k] != 0.f;
+                for (int i = 0; i < kBitsPerLane; i++)
+                    if ((nib >> i) & 1u) s_seg[bl][pos++] = static_cast<uint8_t>(b0 + i);
             }
-            if (!ABSGRAD) {  // sum_p v_sigma (a dx + b dy, b dx + c dy) and the halves of dx^2, dy^2
-                const float4 cn = s_con[tid];
-                const float sdx = v[0], sdy = v[1];
-                v[0] = __builtin_fmaf(cn.x, sdx, cn.y * sdy);
-                v[1] = __builtin_fmaf(cn.y, sdx, cn.z * sdy);
-                v[3] *= 0.5f;
-                v[5] *= 0.5f;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the group's lanes read what the others wrote
+            const int n4 = (max(max(__popcll(seg_bits(wb0)), __popcll(seg_bits(wb1))),
+                                max(__popcll(seg_bits(wb2)), __popcll(seg_bits(wb3)))) + 3) >> 2;
+            const uint32_t* seg4 = reinterpret_cast<const uint32_t*>(s_seg[bl]);
+            // The group's Gaussians back to front, four at a time: the four list entries come in one
+            // LDS read and their records in one burst, the four pairs' exponentials are independent,
+            // only T and the back-sum run through them in order. A pair that does not contribute (or a
+            // slot past the list) gets alpha = 0, so T (times 1/(1 - 0) = 1), the back-sum and every
+            // gradient term are left unchanged / zero.
+            for (int j4 = 0; j4 < n4; j4++) {
+                const int j = 4 * j4;
+                const uint32_t packed = seg4[j4];  // bytes past the list are masked below
+                int ts[4], tc[4];
+                float4 xyo[4], con[4], rgb[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    ts[k] = j + k < cnt ? kSeg * sg + static_cast<int>((packed >> (8 * k)) & 0xFFu) : -1;
+                    tc[k] = ts[k] < 0 ? 0 : ts[k];
+                    xyo[k] = s_xyo[tc[k]];
+                    con[k] = s_con[tc[k]];
+                    rgb[k] = s_rgb[tc[k]];
+                }
+                // the lane storing a slot's sums, and where: the slot's position in the block's list
+                const int e_w = wslot >= 0 && j + wslot < cnt ? j + wslot : -1;
+                float gv[4][NV];
+                float alpha[4], vis[4], dxs[4], dys[4], sig[4], e[4];
+                bool valid[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    dxs[k] = xyo[k].x - px;
+                    dys[k] = xyo[k].y - py;
+                    sig[k] = sigma_of(con[k].x, con[k].y, con[k].z, dxs[k], dys[k]);
+                    valid[k] = (ts[k] >= 0) & (tc[k] >= t_min) & !(sig[k] > xyo[k].w);  // bitwise: no branches
+                }
+                const bool any_valid = __any(valid[0] | valid[1] | valid[2] | valid[3]);
+                if (STATS) {
+                    st_chunks++;
+                    st_empty += any_valid ? 0 : 1;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        st_entries += __popcll(__ballot(r == 0 && ts[k] >= 0));
+                        st_cut += __popcll(__ballot(valid[k]));
+                    }
+                }
+                if (!any_valid) {  // uniform: every alpha 0, T, the back-sum and the gradients unchanged
+                    if (e_w >= 0) {
+#pragma unroll
+                        for (int k = 0; k < NV; k++) s_ent[bl][k][ent_rot(e_w, bl, kSeg)] = 0.f;
+                    }
+                    continue;
+                }
+                // one wave-uniform choice of exponential for the chunk: the branch-free polynomial unless
+                // some cutoff in use exceeds its range (opacity above ~1e35)
+                const float cmax = sxd::smax(sxd::smax(valid[0] ? xyo[0].w : 0.f, valid[1] ? xyo[1].w : 0.f),
+                                             sxd::smax(valid[2] ? xyo[2].w : 0.f, valid[3] ? xyo[3].w : 0.f));
+                const bool general = __any(cmax > 86.0f);
+                // The exponential's value only enters gradients (compared at a relative tolerance), so the
+                // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
+                // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at
+                // least 1/255, and opacity * exp at most the 0.99 clamp — must be the forward's. Where a
+                // lane lies within 2^-12 in sigma of either turning point, the chunk takes the forward's
+                // exponential instead (the points themselves are approximate to ~1e-6).
+                // (the turning points: opacity * e^-sigma = 1/255 at the cutoff less its 0.01 margin, and
+                // = 0.99 at log(255 * 0.99) below that; approximate, only used to find the pairs close to them)
+                bool exact = general;
+                if (!exact) {
+                    bool near = false;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        e[k] = __builtin_amdgcn_exp2f(-sig[k] * 1.44269504f);
+                        const float t1 = xyo[k].w - 0.01f;
+                        const bool n1 = __builtin_fabsf(sig[k] - t1) < 0x1p-12f;
+                        const bool n2 = __builtin_fabsf(sig[k] - (t1 - kLogAlphaSpan)) < 0x1p-12f;
+                        near = near | (valid[k] & (n1 | n2));
+                    }
+                    exact = __any(near);
+                }
+                if (__builtin_expect(exact, 0)) {
+                    if (general) {
+#pragma unroll
+                        for (int k = 0; k < 4; k++) e[k] = sxm::expf_fast(-sig[k]);
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 4; k++) e[k] = exp_neg_poly(sig[k]);
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float vis_raw = e[k];
+                    const float oa = xyo[k].z * vis_raw;
+                    const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
+                    const bool ok = valid[k] & !((sig[k] < 0.f) | (alpha_raw < sx::kAlphaThreshold));
+                    alpha[k] = ok ? alpha_raw : 0.0f;
+                    vis[k] = (ok & (oa <= sx::kMaxAlpha)) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
+                    if (STATS) st_contrib += __popcll(__ballot(ok));
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    // hardware reciprocal (1 ulp; exact for 1): the backward is compared at a relative
+                    // tolerance, and an IEEE division costs ~10 instructions per pair
+                    const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - alpha[k]));
+                    T *= ra;
+                    const float fac = alpha[k] * T;
+                    gv[k][6] = fac * vc0;
+                    gv[k][7] = fac * vc1;
+                    gv[k][8] = fac * vc2;
+                    // v_alpha = sum_c (c_c T - b_c ra) vc_c + T_final ra (va - <bg, vc>), with the back-sum
+                    // kept as its dot product with v_render (fused multiply-adds: gradient algebra only)
+                    const float cvc = __builtin_fmaf(rgb[k].x, vc0, __builtin_fmaf(rgb[k].y, vc1, rgb[k].z * vc2));
+                    const float v_alpha = __builtin_fmaf(T, cvc, ra * (tva - bdot));
+                    const float v_sigma = -xyo[k].z * vis[k] * v_alpha;
+                    const float dx = dxs[k], dy = dys[k];
+                    const float vdx = v_sigma * dx, vdy = v_sigma * dy;
+                    if (ABSGRAD) {  // per-pixel 2D gradients are needed for their absolute values
+                        gv[k][0] = __builtin_fmaf(con[k].x, vdx, con[k].y * vdy);
+                        gv[k][1] = __builtin_fmaf(con[k].y, vdx, con[k].z * vdy);
+                        gv[k][3] = 0.5f * vdx * dx;
+                        gv[k][5] = 0.5f * vdy * dy;
+                        gv[k][9] = fabsf(gv[k][0]);
+                        gv[k][10] = fabsf(gv[k][1]);
+                    } else {  // moments: the conic and the halves are applied once per splat at the flush
+                        gv[k][0] = vdx;
+                        gv[k][1] = vdy;
+                        gv[k][3] = vdx * dx;
+                        gv[k][5] = vdy * dy;
+                    }
+                    gv[k][4] = vdx * dy;
+                    gv[k][2] = vis[k] * v_alpha;
+                    bdot = __builtin_fmaf(fac, cvc, bdot);
+                }
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    const float v = group_sum4(gv[0][k], gv[1][k], gv[2][k], gv[3][k], lo8, lo4);
+                    if (e_w >= 0) s_ent[bl][k][ent_rot(e_w, bl, kSeg)] = v;  // plain store: one writer per (block, entry)
+                }
             }
-            if (any) {
-                const int32_t gid = s_id[tid];
-                if (g.packed) {
-                    float* rec = reinterpret_cast<float*>(g.packed + (size_t)gid * 3);
-                    atomicAdd(&rec[0], v[0]);
-                    atomicAdd(&rec[1], v[1]);
-                    atomicAdd(&rec[2], v[2]);
-                    atomicAdd(&rec[4], v[3]);
-                    atomicAdd(&rec[5], v[4]);
-                    atomicAdd(&rec[6], v[5]);
-                    atomicAdd(&rec[8], v[6]);
-                    atomicAdd(&rec[9], v[7]);
-                    atomicAdd(&rec[10], v[8]);
-                } else {
-                    atomicAdd(&g.v_means2d[(size_t)gid * 2], v[0]);
-                    atomicAdd(&g.v_means2d[(size_t)gid * 2 + 1], v[1]);
-                    atomicAdd(&g.v_opacities[gid], v[2]);
-                    atomicAdd(&g.v_conics[(size_t)gid * 3], v[3]);
-                    atomicAdd(&g.v_conics[(size_t)gid * 3 + 1], v[4]);
-                    atomicAdd(&g.v_conics[(size_t)gid * 3 + 2], v[5]);
-                    atomicAdd(&g.v_colors[(size_t)gid * 3], v[6]);
-                    atomicAdd(&g.v_colors[(size_t)gid * 3 + 1], v[7]);
-                    atomicAdd(&g.v_colors[(size_t)gid * 3 + 2], v[8]);
-                    if (ABSGRAD) {
-                        atomicAdd(&g.v_means2d_abs[(size_t)gid * 2], v[9]);
-                        atomicAdd(&g.v_means2d_abs[(size_t)gid * 2 + 1], v[10]);
+            __syncthreads();
+            // the segment's totals: the threads of slot j sum its entries over the blocks it reaches, each
+            // thread a few of the components, and add them with one float atomic per component
+            {
+                const int j = tid % kSeg, q = tid / kSeg;
+                const int slot = kSeg * sg + j;
+                const uint32_t m0 = slot < batch_size ? static_cast<uint32_t>(s_bm[slot]) : 0u;
+                if (m0) {
+                    // components of term group q: the two position moments stay together (the conic
+                    // applies to both at once)
+                    int ks[3];
+                    flush_terms<NV, kTermGroups>(q, ks);
+                    float v[3] = {0.f, 0.f, 0.f};
+                    const unsigned long long below_j = (1ull << j) - 1ull;  // j < 64
+                    uint32_t m = m0;
+                    while (m) {
+                        const int b2 = __builtin_ctz(m);
+                        m &= m - 1u;
+                        const int e2 = ent_rot(__popcll(seg_bits(b2) & below_j), b2, kSeg);  // the slot's entry
+#pragma unroll
+                        for (int i = 0; i < 3; i++)
+                            if (ks[i] >= 0) v[i] += s_ent[b2][ks[i]][e2];
+                    }
+                    if (!ABSGRAD && ks[0] == 0) {  // sum_p v_sigma (a dx + b dy, b dx + c dy)
+                        const float4 cn = s_con[slot];
+                        const float sdx = v[0], sdy = v[1];
+                        v[0] = __builtin_fmaf(cn.x, sdx, cn.y * sdy);
+                        v[1] = __builtin_fmaf(cn.y, sdx, cn.z * sdy);
+                    }
+                    const int32_t f = __float_as_int(s_rgb[slot].w);
+                    if (g.part) {  // plain stores at the emit position; the gather sums them in a fixed order
+                        float* dst = g.part + (size_t)f * kPartStride;
+#pragma unroll
+                        for (int i = 0; i < 3; i++) {
+                            const int k = ks[i];
+                            if (k < 0) continue;
+                            dst[k] = (!ABSGRAD && (k == 3 || k == 5)) ? 0.5f * v[i] : v[i];  // halves of dx^2, dy^2
+                        }
+                        if (q == 0) {
+                            atomicOr(&g.valid[f >> 5], 1u << (f & 31));  // integer: order-free
+                            g.touched[__float_as_int(s_con[slot].w)] = 1;  // the Gaussian has entries to gather
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 3; i++) {
+                            const int k = ks[i];
+                            if (k < 0 || v[i] == 0.f) continue;
+                            const float x = (!ABSGRAD && (k == 3 || k == 5)) ? 0.5f * v[i] : v[i];
+                            atomicAdd(grad_slot(g, f, k), x);
+                        }
                     }
                 }
             }
+            __syncthreads();  // the next segment overwrites the entries and the group lists
         }
     }
     if (STATS && lane == 0) {
@@ -506,6 +644,169 @@ __global__ void __launch_bounds__(kThreads) k_raster_bwd(RasterArgs a, const flo
 }
 
 } // namespace
+
+namespace {
+constexpr int kLongRange = 64;  // gather: longer entry ranges are reduced by a whole wave
+
+// bit words of the backward's valid bitmap, for the device intersection count (grid sized for the
+// capacity), the rows' touched flags, and the gather's long-range queue count
+__global__ void __launch_bounds__(kThreads) k_clear_valid(uint32_t* __restrict__ valid, int64_t n_words,
+                                                          const int64_t* __restrict__ n_isects_dev,
+                                                          uint8_t* __restrict__ touched, int rows,
+                                                          int32_t* __restrict__ long_count) {
+    if (n_isects_dev) n_words = (*n_isects_dev + 31) / 32;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *long_count = 0;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_words; i += (int64_t)gridDim.x * kThreads)
+        valid[i] = 0u;
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) touched[i] = 0;
+}
+
+// entry p of `part` as three aligned float4 loads (the 9 sums and 3 unused floats)
+__device__ __forceinline__ void load_entry(const float* __restrict__ part, int32_t p, float* e) {
+    const float4* a = reinterpret_cast<const float4*>(part + (size_t)p * kPartStride);
+    const float4 x = a[0], y = a[1], z = a[2];
+    e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w;
+    e[4] = y.x; e[5] = y.y; e[6] = y.z; e[7] = y.w;
+    e[8] = z.x;
+}
+
+__device__ __forceinline__ void add_entry(const float* __restrict__ part, int32_t p, float* v) {
+    float e[kPartFloats];
+    load_entry(part, p, e);
+#pragma unroll
+    for (int k = 0; k < kPartFloats; k++) v[k] += e[k];
+}
+
+__device__ __forceinline__ void store_grad_record(float4* grads, size_t g, const float* v) {
+    grads[3 * g] = make_float4(v[0], v[1], v[2], 0.f);
+    grads[3 * g + 1] = make_float4(v[3], v[4], v[5], 0.f);
+    grads[3 * g + 2] = make_float4(v[6], v[7], v[8], 0.f);
+}
+
+// One thread per position j of the depth order, for Gaussian order[j]: the sums of its (tile, Gaussian)
+// entries, which the emit placed at [cum[j-1], cum[j]), in emit order (its tiles in the order the
+// intersection emit visits them), into its gradient record {v_x, v_y, v_opacity, 0 | v_conic a, b, c,
+// 0 | v_r, v_g, v_b, 0}. Entries whose valid bit is clear (tiles that never reached the Gaussian) count
+// as zero; a Gaussian with none (exactly the untouched ones) gets no record: the postprocess reads zeros
+// for it. Ranges longer than kLongRange are queued for k_gather_long when touched (the queue's order does
+// not matter: each range is reduced on its own).
+__global__ void __launch_bounds__(kThreads) k_gather_grads(int count, const int32_t* __restrict__ order,
+                                                           const int64_t* __restrict__ cum,
+                                                           const float* __restrict__ part,
+                                                           const uint32_t* __restrict__ valid,
+                                                           const uint8_t* __restrict__ touched,
+                                                           float4* __restrict__ grads, int32_t* __restrict__ long_list,
+                                                           int32_t* __restrict__ long_count) {
+    const int j = blockIdx.x * kThreads + threadIdx.x;
+    if (j >= count) return;
+    const int32_t p1 = static_cast<int32_t>(cum[j]);
+    const int32_t p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
+    if (p1 == p0) return;
+    const int g = order[j];
+    if (p1 - p0 > kLongRange) {
+        if (touched[g]) long_list[atomicAdd(long_count, 1)] = j;  // an untouched range has no valid entry
+        return;
+    }
+    // a short range spans at most three bit words: all three loads first, then the set bits in order
+    const int32_t w0 = p0 >> 5, w_last = (p1 - 1) >> 5;
+    uint32_t wb[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        const int32_t w = w0 + k;
+        uint32_t m = 0u;
+        if (w <= w_last) {
+            const int lo = w == w0 ? (p0 & 31) : 0, hi = w == w_last ? ((p1 - 1) & 31) : 31;
+            m = (0xFFFFFFFFu << lo) & (0xFFFFFFFFu >> (31 - hi));
+        }
+        wb[k] = m ? valid[w] & m : 0u;
+    }
+    if ((wb[0] | wb[1] | wb[2]) == 0u) return;  // untouched: no record (the postprocess reads zeros)
+    float v[kPartFloats];
+#pragma unroll
+    for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+        uint32_t bits = wb[k];
+        while (bits) {  // two entries per round (independent loads)
+            const int b0 = __builtin_ctz(bits);
+            bits &= bits - 1u;
+            const int b1 = bits ? __builtin_ctz(bits) : -1;
+            if (bits) bits &= bits - 1u;
+            float e0[kPartFloats], e1[kPartFloats];
+            load_entry(part, ((w0 + k) << 5) + b0, e0);
+            load_entry(part, ((w0 + k) << 5) + (b1 < 0 ? b0 : b1), e1);
+#pragma unroll
+            for (int q = 0; q < kPartFloats; q++) {
+                v[q] += e0[q];
+                if (b1 >= 0) v[q] += e1[q];
+            }
+        }
+    }
+    store_grad_record(grads, static_cast<size_t>(g), v);
+}
+
+// The queued long ranges, one wave each, 64 entries per round (lane l takes entry base + l when its
+// valid bit is set); each round's 64 values are added in a fixed tree (DPP within rows, then across
+// rows) and the rounds in order.
+__global__ void __launch_bounds__(kThreads) k_gather_long(const int32_t* __restrict__ order,
+                                                          const int64_t* __restrict__ cum,
+                                                          const float* __restrict__ part,
+                                                          const uint32_t* __restrict__ valid,
+                                                          float4* __restrict__ grads,
+                                                          const int32_t* __restrict__ long_list,
+                                                          const int32_t* __restrict__ long_count) {
+    const int lane = threadIdx.x & 63;
+    const int n_long = *long_count;
+    const int n_waves = gridDim.x * (kThreads / 64);
+    for (int q = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); q < n_long; q += n_waves) {  // wave-uniform
+        const int j = long_list[q];
+        const int32_t p1 = static_cast<int32_t>(cum[j]);
+        const int32_t p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
+        float v[kPartFloats];
+#pragma unroll
+        for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
+        for (int32_t base = p0; base < p1; base += 64) {
+            const int32_t p = base + lane;
+            const bool on = p < p1 && ((valid[p >> 5] >> (p & 31)) & 1u);
+            float x[kPartFloats];
+#pragma unroll
+            for (int k = 0; k < kPartFloats; k++) x[k] = 0.f;
+            if (on) add_entry(part, p, x);
+#pragma unroll
+            for (int k = 0; k < kPartFloats; k++) {
+                float y = x[k];
+                y += dpp_f<0xB1>(y);   // quad_perm(1,0,3,2)
+                y += dpp_f<0x4E>(y);   // quad_perm(2,3,0,1)
+                y += dpp_f<0x141>(y);  // row_half_mirror
+                y += dpp_f<0x140>(y);  // row_mirror: the 16-lane row total
+                y += __shfl_xor(y, 16, 64);
+                y += __shfl_xor(y, 32, 64);
+                v[k] += y;
+            }
+        }
+        if (lane == 0) store_grad_record(grads, static_cast<size_t>(order[j]), v);
+    }
+}
+}  // namespace
+
+void raster_clear_valid(uint32_t* valid, int64_t cap, const int64_t* n_isects_dev, uint8_t* touched, int rows,
+                        int32_t* long_count, hipStream_t s) {
+    const int64_t words = (cap + 31) / 32;
+    const int64_t need = std::max<int64_t>(words, rows);
+    const int blocks = static_cast<int>(std::min<int64_t>(std::max<int64_t>((need + kThreads - 1) / kThreads, 1), 4096));
+    hipLaunchKernelGGL(k_clear_valid, dim3(blocks), dim3(kThreads), 0, s, valid, words, n_isects_dev, touched, rows,
+                       long_count);
+}
+
+void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part, const uint32_t* valid,
+                         const uint8_t* touched, float4* grads, int32_t* long_list, int32_t* long_count,
+                         hipStream_t s) {
+    if (count <= 0) return;
+    hipLaunchKernelGGL(k_gather_grads, dim3((count + kThreads - 1) / kThreads), dim3(kThreads), 0, s, count, order, cum,
+                       part, valid, touched, grads, long_list, long_count);
+    hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, valid, grads, long_list,
+                       long_count);
+}
 
 namespace {
 // Counting sort of the tiles by descending intersection count (256 buckets of width w, w the
@@ -599,14 +900,14 @@ void raster_bwd(const RasterArgs& a, const float* ralpha, const int32_t* last_id
     const int blocks = a.I * a.tile_width * a.tile_height;
     if (blocks <= 0 || (!a.n_isects_dev && a.n_isects <= 0)) return;
     if (g.v_means2d_abs)  // the per-op entry's absgrad (never counted)
-        hipLaunchKernelGGL((k_raster_bwd<true, false>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc,
-                           v_ra, g);
+        hipLaunchKernelGGL((k_raster_bwd<true, false, kBwdSeg>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids,
+                           v_rc, v_ra, g);
     else if (a.stats)
-        hipLaunchKernelGGL((k_raster_bwd<false, true>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc,
-                           v_ra, g);
+        hipLaunchKernelGGL((k_raster_bwd<false, true, kBwdSeg>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids,
+                           v_rc, v_ra, g);
     else
-        hipLaunchKernelGGL((k_raster_bwd<false, false>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids, v_rc,
-                           v_ra, g);
+        hipLaunchKernelGGL((k_raster_bwd<false, false, kBwdSeg>), dim3(blocks), dim3(kThreads), 0, s, a, ralpha, last_ids,
+                           v_rc, v_ra, g);
 }
 
 } // namespace sxk

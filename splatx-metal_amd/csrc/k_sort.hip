@@ -170,7 +170,7 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const K* __restrict__ kin,
     for (int r = 0; r < kRounds; r++) {
         const int i = wave * kPerWave + r * 64 + lane;
         key[r] = i < tile_n ? kin[base + i] : K(0);
-        val[r] = i < tile_n ? vin[base + i] : 0;
+        val[r] = i < tile_n ? (vin ? vin[base + i] : static_cast<int32_t>(base + i)) : 0;  // null: the index
     }
     // per-wave digit histograms: one leader lane per distinct digit of a round; the ranks among
     // equal digits (and the leaders' counts) are kept for the placement below
@@ -444,14 +444,14 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
         for (int r = 0; r < kRounds; r++) {
             const int i = wave * kPerWave + r * 64 + lane;
             key[r] = kin[base + i];
-            val[r] = vin[base + i];
+            val[r] = vin ? vin[base + i] : static_cast<int32_t>(base + i);  // null values: the input index
         }
     } else {
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
             const int i = wave * kPerWave + r * 64 + lane;
             key[r] = i < tile_n ? kin[base + i] : K(0);
-            val[r] = i < tile_n ? vin[base + i] : 0;
+            val[r] = i < tile_n ? (vin ? vin[base + i] : static_cast<int32_t>(base + i)) : 0;
         }
     }
     // per-wave digit counts, rounds in order; off[r] = the key's place among the wave's keys of its
@@ -676,13 +676,15 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
     return passes;
 }
 
-// In place over two buffers: a -> b -> a -> ...; the result is in a after an even pass count.
+// In place over two buffers: a -> b -> a -> ...; the result is in a after an even pass count. With
+// index_values the first pass takes each key's input position as its value (vals_a is not read).
 template <class K>
 int radix_sort_ab(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-                  void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev) {
+                  void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev, bool index_values = false) {
     K* const sk[2] = {keys_b, keys_a};
     int32_t* const sv[2] = {vals_b, vals_a};
-    const int passes = radix_sort_t<K>(keys_a, vals_a, sk, sv, n, key_bits, scratch, clear_err, s, n_dev);
+    const int passes = radix_sort_t<K>(keys_a, index_values ? nullptr : vals_a, sk, sv, n, key_bits, scratch,
+                                       clear_err, s, n_dev);
     return passes < 0 ? -1 : (passes & 1);
 }
 
@@ -710,6 +712,16 @@ int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* val
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
                void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
     return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
+}
+
+int radix_sort_positions(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
+                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true);
+}
+
+int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
+                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true);
 }
 
 void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_out, int32_t* vals_out,

@@ -62,7 +62,6 @@ __device__ __forceinline__ float adam_update(float* __restrict__ p, float* __res
 template <int NC>
 __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, float4* __restrict__ splats,
                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
-                                                       float4* __restrict__ grads,
                                                        uint32_t* __restrict__ vis_part) {
     __shared__ uint32_t s_vis[kBlock / 64], s_isect[kBlock / 64];
     uint32_t n_tiles_sum = 0;  // this lane's tile count; summed per block below
@@ -116,10 +115,6 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
             splats[3 * (size_t)i] = make_float4(o.m2x, o.m2y, op_used, o.depth);
             splats[3 * (size_t)i + 1] = make_float4(o.ca, o.cb, o.cc, o.comp);
             splats[3 * (size_t)i + 2] = make_float4(col[0], col[1], col[2], __uint_as_float(meta));
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            grads[3 * (size_t)i] = z;
-            grads[3 * (size_t)i + 1] = z;
-            grads[3 * (size_t)i + 2] = z;
         } else {
             splats[3 * (size_t)i + 2] = make_float4(0.f, 0.f, 0.f, __uint_as_float(0u));
         }
@@ -409,7 +404,8 @@ __global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ k
 // its partials stay in registers
 template <int NC>
 __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, const float4* __restrict__ splats,
-                                                        const float4* __restrict__ grads) {
+                                                        const float4* __restrict__ grads,
+                                                        const uint8_t* __restrict__ touched) {
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= c.count) return;
     const size_t R = static_cast<size_t>(A.rows);
@@ -426,9 +422,12 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
     float sl[3] = {ld_stream(&A.p[2][i]), ld_stream(&A.p[2][R + i]), ld_stream(&A.p[2][2 * R + i])};
     float logit = ld_stream(&A.p[3][i]);
     if (wave_live) {
-        const float4 g0 = grads[3 * (size_t)i];
-        const float4 g1 = grads[3 * (size_t)i + 1];
-        const float4 g2 = grads[3 * (size_t)i + 2];
+        // rows no tile reached have no gradient record this step: zeros
+        const bool has_g = live && touched[i];
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 g0 = has_g ? grads[3 * (size_t)i] : z4;
+        const float4 g1 = has_g ? grads[3 * (size_t)i + 1] : z4;
+        const float4 g2 = has_g ? grads[3 * (size_t)i + 2] : z4;
         const float4 s1 = splats[3 * (size_t)i + 1];
         // relu mask (train_relu_mask_apply)
         const float vrgb[3] = {(meta & 2u) ? g2.x : 0.0f, (meta & 4u) ? g2.y : 0.0f, (meta & 8u) ? g2.z : 0.0f};
@@ -641,15 +640,15 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 
 } // namespace
 
-void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles, float4* grads,
+void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* n_visible, hipStream_t s) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
-        case 1: hipLaunchKernelGGL(k_preprocess<1>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
-        case 4: hipLaunchKernelGGL(k_preprocess<4>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
-        case 9: hipLaunchKernelGGL(k_preprocess<9>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
-        case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, grads, vis_part); break;
+        case 1: hipLaunchKernelGGL(k_preprocess<1>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
+        case 4: hipLaunchKernelGGL(k_preprocess<4>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
+        case 9: hipLaunchKernelGGL(k_preprocess<9>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
+        case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
     hipLaunchKernelGGL(k_count_sum, dim3(1), dim3(kBlock), 0, s, vis_part, static_cast<int>(grid.x), n_visible);
@@ -691,14 +690,15 @@ void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* of
                        offsets, n_dev);
 }
 
-void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads, hipStream_t s) {
+void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
+                      const uint8_t* touched, hipStream_t s) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
-        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads); break;
-        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads); break;
-        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads); break;
-        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads); break;
+        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads, touched); break;
+        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads, touched); break;
+        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads, touched); break;
+        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads, touched); break;
         default: throw std::invalid_argument("postprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
 }

@@ -43,6 +43,9 @@ struct sxh_executor {
     sxh::DevBuf<float4> splats, grads;
     sxh::DevBuf<int32_t> radii, tiles;
     sxh::DevBuf<int64_t> cum;
+    sxh::DevBuf<int32_t> long_list;          // gradient gather: the depth positions of long entry ranges
+    sxh::DevBuf<int32_t> long_count;
+    sxh::DevBuf<uint8_t> touched;            // rows the raster backward reached this step
     sxh::DevBuf<uint32_t> dkey_a, dkey_b;    // depth sort keys
     sxh::DevBuf<int32_t> order_a, order_b;   // Gaussian indices in depth order
     sxh::DevBuf<uint8_t> scan_scratch;
@@ -51,7 +54,10 @@ struct sxh_executor {
     // intersections (grow 1.5x, reused)
     size_t isect_cap = 0;
     sxh::DevBuf<uint64_t> keys_a, keys_b;
-    sxh::DevBuf<int32_t> vals_a, vals_b;
+    sxh::DevBuf<int32_t> vals_a, vals_b;   // sorted: emit positions
+    sxh::DevBuf<int32_t> emit_gid;         // the Gaussian of each emit position
+    sxh::DevBuf<float> part;               // raster backward sums per emit position (kPartStride floats each)
+    sxh::DevBuf<uint32_t> valid;           // their valid bits
     sxh::DevBuf<uint8_t> sort_scratch;
     // image-sized buffers
     size_t img_px = 0, img_tiles = 0, img_map = 0;
@@ -110,6 +116,9 @@ struct sxh_executor {
         keys_b.alloc(cap);
         vals_a.alloc(cap);
         vals_b.alloc(cap);
+        emit_gid.alloc(cap);
+        part.alloc(cap * sxk::kPartStride);
+        valid.alloc((cap + 31) / 32);
         // shared by the depth sort (rows keys) and the tile sort (intersections)
         sort_scratch.alloc(sxk::sort_scratch_bytes(static_cast<int64_t>(std::max<size_t>(cap, rows))));
         isect_cap = cap;

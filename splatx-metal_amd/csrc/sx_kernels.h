@@ -82,6 +82,14 @@ int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* val
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
                uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
                const int64_t* n_dev = nullptr);
+// The same sort with each key's input position as its value (vals_a is not read; the sorted values
+// are the positions of the keys in the unsorted array).
+int radix_sort_positions(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
+                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
+                         const int64_t* n_dev = nullptr);
+int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
+                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
+                         const int64_t* n_dev = nullptr);
 // The same sort of n u64 keys from read-only inputs into keys_out/vals_out, with keys_tmp/vals_tmp as
 // the second ping-pong side (n > 0, key_bits in 1..64, the onesweep range n < 2^30). No buffer may
 // alias another.
@@ -117,22 +125,26 @@ struct RasterArgs {
     // optional: the intersection count on the device (read instead of n_isects), so that the
     // launches do not depend on it
     const int64_t* n_isects_dev;
+    // optional: flatten_ids hold emit positions p and the Gaussian of p is id_of[p] (the resident step)
+    const int32_t* id_of;
     // optional (profiling): pair counters the rasterisers add into, kRasterStat* indices; null in
     // production (the counting kernels are separate instantiations)
     unsigned long long* stats;
 };
-// raster pair counters (RasterArgs::stats): list entries walked (one splat against the 64 pixels of
-// a wave), pairs composited (forward), 4-entry chunks, chunks in which no lane's pair is inside the
-// cutoff, lane pairs inside the cutoff and before the pixel's last contributor, pairs that
-// contribute (alpha >= 1/255) (backward)
+// raster pair counters (RasterArgs::stats): forward wave iterations (x 64 lane pairs), block-list
+// entries walked (one splat against a 4x4 block) and pairs composited; backward 4-iteration chunks
+// (x 256 lane pairs), block-list entries in them, chunks in which no lane's pair is inside the cutoff,
+// lane pairs inside the cutoff and before the pixel's last contributor, pairs that contribute
+// (alpha >= 1/255)
 enum RasterStat : int {
-    kStatFwdEntries = 0,
-    kStatFwdTaken = 1,
-    kStatBwdChunks = 2,
-    kStatBwdEntries = 3,
-    kStatBwdEmptyChunks = 4,
-    kStatBwdInCutoff = 5,
-    kStatBwdContrib = 6,
+    kStatFwdIters = 0,
+    kStatFwdEntries = 1,
+    kStatFwdTaken = 2,
+    kStatBwdChunks = 3,
+    kStatBwdEntries = 4,
+    kStatBwdEmptyChunks = 5,
+    kStatBwdInCutoff = 6,
+    kStatBwdContrib = 7,
     kRasterStats = 8
 };
 // tile_order for raster_fwd/raster_bwd: the n_tiles tile ids by descending intersection count
@@ -150,7 +162,28 @@ struct RasterBwdGrads {
     float* v_opacities;
     float* v_means2d_abs;
     float4* packed;  // when set: the resident-step record layout (3 x float4 per Gaussian)
+    // when set (with RasterArgs::id_of): no atomics; the sums of each (tile, Gaussian) are stored at the
+    // intersection's emit position p (flatten_ids[idx]) as kPartFloats floats (stride kPartStride), bit p of `valid` and the
+    // Gaussian's `touched` flag are set (both cleared by the caller); raster_gather_grads then sums each
+    // Gaussian's entries in order
+    float* part;
+    uint32_t* valid;
+    uint8_t* touched;  // with part: set for every Gaussian that got an entry (cleared by the caller)
 };
+constexpr int kPartFloats = 9;  // v_xy (2), v_opacity, v_conic (3), v_rgb (3)
+constexpr int kPartStride = 12;  // floats per `part` entry: three aligned float4 (the last 3 floats unused)
+// clears the bitmap words of the first *n_isects_dev (or cap) intersections, touched[0, rows) and the
+// gather's queue count
+void raster_clear_valid(uint32_t* valid, int64_t cap, const int64_t* n_isects_dev, uint8_t* touched, int rows,
+                        int32_t* long_count, hipStream_t s);
+// For each Gaussian order[j] with touched set: grads[order[j]] (3 x float4 record) = the sum of the `part`
+// entries at [cum[j-1], cum[j]) whose valid bit is set (order and cum: the depth order and the inclusive
+// scan of its tile counts that placed the emit), in a fixed order per range: the deterministic end of
+// raster_bwd's `part` mode. Untouched Gaussians' records are not written. long_list holds `count` ints,
+// long_count one (reset by raster_clear_valid).
+void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part,
+                         const uint32_t* valid, const uint8_t* touched, float4* grads, int32_t* long_list,
+                         int32_t* long_count, hipStream_t s);
 void raster_bwd(const RasterArgs& a, const float* render_alphas, const int32_t* last_ids,
                 const float* v_render_colors, const float* v_render_alphas, const RasterBwdGrads& g,
                 hipStream_t s);

@@ -47,7 +47,7 @@ struct StepConst {
 // vis_part: 2 u32 per block (visible count, tile count); out_vis: {u64 visible count, u64
 // intersections}
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
-                     float4* grads, uint32_t* vis_part, unsigned long long* out_vis, hipStream_t s);
+                     uint32_t* vis_part, unsigned long long* out_vis, hipStream_t s);
 // number of blocks of step_preprocess (vis_part holds 2 u32 per block)
 int step_preprocess_blocks(int64_t count);
 // depth-first intersections: depth keys of the Gaussians that emit (values = index) for a stable
@@ -66,7 +66,7 @@ void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* of
 void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev = nullptr);
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
-                      hipStream_t s);
+                      const uint8_t* touched, hipStream_t s);
 // Noise only (the forward-only path never calls it; a training step fuses it into postprocess).
 // L1 gradient without SSIM: v_render = sign(render - gt) / n, per-block f64 sums of |render - gt|.
 void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_render, double* partials,

@@ -408,8 +408,8 @@ class RenderSession:
 
 
 class RasterStats(C.Structure):
-    _fields_ = [(k, C.c_uint64) for k in ("fwd_entries", "fwd_taken", "bwd_chunks", "bwd_entries", "bwd_empty_chunks",
-                                          "bwd_in_cutoff", "bwd_contrib")]
+    _fields_ = [(k, C.c_uint64) for k in ("fwd_iters", "fwd_entries", "fwd_taken", "bwd_chunks", "bwd_entries",
+                                          "bwd_empty_chunks", "bwd_in_cutoff", "bwd_contrib")]
 
 
 class ExecTiming(C.Structure):
