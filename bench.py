@@ -171,32 +171,67 @@ def bench_formats(cfg_id: int) -> None:
 
 def load_traffic(kernel: str, cfg: int):
     """HBM bytes per launch of `kernel`, as measured by the counter runs recorded in profiles/traffic.json
-    (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel yardstick); None if not recorded."""
+    (FETCH_SIZE and WRITE_SIZE per training step, each scaled by the copy-kernel yardstick, divided by the
+    kernel's dispatches per step); None if not recorded for this configuration."""
     path = os.path.join(REPO, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         rec = json.load(f)
-    k = rec.get("kernels", {}).get(kernel)
-    if k is None or rec.get("config") != cfg:
+    k = rec.get("configs", {}).get(str(cfg), {}).get("kernels", {}).get(kernel)
+    if k is None:
         return None
-    return k["hbm_bytes"]
+    return round(k["hbm_bytes"] / max(1, k["dispatches"]))
+
+
+# Cycles a SIMD spends per wave-level VALU instruction (measured by --calibrate-valu on MI355X): 4 for
+# f32 arithmetic, bitwise and DPP moves, 8 for transcendentals (v_exp_f32, v_rcp_f32, ...). v_add_u32
+# and plain v_mov_b32 issue at about twice the f32 rate, so the bound below is an upper estimate when
+# a kernel has many of them.
+VALU_CYCLES, TRANS_CYCLES, SIMDS, CLOCK_HZ = 4, 8, 1024, 2.4e9
 
 
 def load_valu(kernel: str, cfg: int):
-    """VALU issue bound of one launch of `kernel` from the counter run recorded in profiles/valu.json
-    (SQ_INSTS_VALU: wave-level VALU instructions; each occupies a 16-lane SIMD for 4 cycles); None if
-    not recorded."""
-    path = os.path.join(REPO, "profiles", "valu.json")
+    """VALU issue bound of one training step's launches of `kernel` from the counter runs recorded in
+    profiles/counters.json (SQ_INSTS_VALU and SQ_INSTS_VALU_TRANS_F32 over training-step dispatches);
+    None if not recorded for this configuration."""
+    path = os.path.join(REPO, "profiles", "counters.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         rec = json.load(f)
-    k = rec.get("kernels", {}).get(kernel)
-    if k is None or rec.get("config") != cfg:
+    k = rec.get("configs", {}).get(str(cfg), {}).get("kernels", {}).get(kernel)
+    if k is None or "SQ_INSTS_VALU" not in k:
         return None
-    return {"valu_insts": k["valu_insts"], "bound_ms": k["issue_bound_ms"], "simds": rec["simds"],
-            "clock_hz": rec["clock_hz"], "cycles_per_wave_instr": rec["cycles_per_wave_instr"]}
+    v, t = k["SQ_INSTS_VALU"], k.get("SQ_INSTS_VALU_TRANS_F32", 0)
+    cycles = VALU_CYCLES * (v - t) + TRANS_CYCLES * t
+    return {"valu_insts": v, "trans_insts": t, "bound_ms": round(cycles / (SIMDS * CLOCK_HZ) * 1e3, 4),
+            "simds": SIMDS, "clock_hz": CLOCK_HZ, "cycles_per_wave_instr": VALU_CYCLES,
+            "cycles_per_trans_instr": TRANS_CYCLES}
+
+
+def calibrate_valu(blocks: int = 8192, reps: int = 5) -> None:
+    """VALU issue rates per instruction class on device 0 (the yardstick kernels of k_yardstick.hip):
+    wave-level instructions per SIMD per 4 cycles at CLOCK_HZ, and the cycles per instruction."""
+    import ctypes
+    lib = sh.load_library()
+    lib.sxh_yardstick_valu_name.restype = ctypes.c_char_p
+    lib.sxh_yardstick_valu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_double)]
+    out = {"blocks": blocks, "waves": blocks * 4, "clock_hz": CLOCK_HZ, "simds": SIMDS, "ops": {}}
+    for op in range(lib.sxh_yardstick_valu_count()):
+        name = lib.sxh_yardstick_valu_name(op).decode()
+        slow = "exp" in name or "rcp" in name
+        iters = 1024 if slow else 4096
+        ms = ctypes.c_double()
+        if lib.sxh_yardstick_valu(0, op, blocks, iters, reps, ctypes.byref(ms)) != 0:
+            raise RuntimeError(f"yardstick {name} failed")
+        insts = blocks * 4 * iters * 8
+        rate = insts / SIMDS / (ms.value * 1e-3 * CLOCK_HZ / 4.0)
+        out["ops"][name] = {"iters": iters, "wave_instrs": insts, "ms": round(ms.value, 4),
+                            "per_simd_per_4_cycles": round(rate, 3), "cycles_per_instr": round(4.0 / rate, 2)}
+        print(f"{name:40s} {ms.value:8.4f} ms  {rate:6.3f} per SIMD per 4 cycles", file=sys.stderr, flush=True)
+    print(json.dumps(out), flush=True)
 
 
 def main():
@@ -209,6 +244,8 @@ def main():
     ap.add_argument("--formats", action="store_true",
                     help="time the formats either side of the step (PLY export, checkpoint save/load, render-session "
                          "frames) on the config's arena instead of the training step, and exit")
+    ap.add_argument("--calibrate-valu", action="store_true",
+                    help="only time the VALU yardstick kernels (issue rate per instruction class) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run device copies of MIB MiB (yardstick for the HBM byte counters) and exit")
     args = ap.parse_args()
@@ -218,6 +255,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy > 0:
         calibrate_copy(args.calibrate_copy)
+        return
+    if args.calibrate_valu:
+        calibrate_valu()
         return
 
     if args.formats:
