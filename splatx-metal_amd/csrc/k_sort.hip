@@ -166,11 +166,20 @@ __global__ void __launch_bounds__(kThreads) k_scatter(const K* __restrict__ kin,
     __syncthreads();
     K key[kRounds];
     int32_t val[kRounds];
+    if (vin) {  // uniform; null values: the input index
 #pragma unroll
-    for (int r = 0; r < kRounds; r++) {
-        const int i = wave * kPerWave + r * 64 + lane;
-        key[r] = i < tile_n ? kin[base + i] : K(0);
-        val[r] = i < tile_n ? (vin ? vin[base + i] : static_cast<int32_t>(base + i)) : 0;  // null: the index
+        for (int r = 0; r < kRounds; r++) {
+            const int i = wave * kPerWave + r * 64 + lane;
+            key[r] = i < tile_n ? kin[base + i] : K(0);
+            val[r] = i < tile_n ? vin[base + i] : 0;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const int i = wave * kPerWave + r * 64 + lane;
+            key[r] = i < tile_n ? kin[base + i] : K(0);
+            val[r] = i < tile_n ? static_cast<int32_t>(base + i) : 0;
+        }
     }
     // per-wave digit histograms: one leader lane per distinct digit of a round; the ranks among
     // equal digits (and the leaders' counts) are kept for the placement below
@@ -439,19 +448,37 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
     K key[kRounds];
     int32_t val[kRounds];
+    // null values: the input index. The (uniform) choice is taken once around straight-line loads: a
+    // choice per round compiles to a wait for every load before the next is issued.
     if (tile_n == kTile) {  // uniform
+        if (vin) {
+#pragma unroll
+            for (int r = 0; r < kRounds; r++) {
+                const int i = wave * kPerWave + r * 64 + lane;
+                key[r] = kin[base + i];
+                val[r] = vin[base + i];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < kRounds; r++) {
+                const int i = wave * kPerWave + r * 64 + lane;
+                key[r] = kin[base + i];
+                val[r] = static_cast<int32_t>(base + i);
+            }
+        }
+    } else if (vin) {
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
             const int i = wave * kPerWave + r * 64 + lane;
-            key[r] = kin[base + i];
-            val[r] = vin ? vin[base + i] : static_cast<int32_t>(base + i);  // null values: the input index
+            key[r] = i < tile_n ? kin[base + i] : K(0);
+            val[r] = i < tile_n ? vin[base + i] : 0;
         }
     } else {
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
             const int i = wave * kPerWave + r * 64 + lane;
             key[r] = i < tile_n ? kin[base + i] : K(0);
-            val[r] = i < tile_n ? (vin ? vin[base + i] : static_cast<int32_t>(base + i)) : 0;
+            val[r] = i < tile_n ? static_cast<int32_t>(base + i) : 0;
         }
     }
     // per-wave digit counts, rounds in order; off[r] = the key's place among the wave's keys of its
