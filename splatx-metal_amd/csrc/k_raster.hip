@@ -13,12 +13,14 @@
 // most of a strip's lanes would sit outside their cutoff).
 // Forward: front-to-back compositing with the exclusive T <= 1e-4 stop, per-pixel arithmetic in
 // the CPU reference's order (CpuKernels.cpp:821-849) and the deterministic exp of sx_fmath.h, so
-// colors/alphas/last_ids are bit-identical to the CPU oracle; the workgroup exits as soon as all
-// its pixels are done.
+// colors/alphas/last_ids are bit-identical to the CPU oracle; two list entries per iteration; the
+// workgroup exits as soon as all its pixels are done.
 // Backward: back-to-front walk recovering T by division, four list entries per group at a time;
 // a group sums its four splats' nine gradient components over its 16 lanes with one transposed
-// reduction (11 DPP/select instructions per component), the groups add their sums into LDS, and one
-// set of float atomics per (tile, Gaussian) is issued after each batch.
+// reduction (11 DPP/select instructions per component) and stores the sums in an LDS entry buffer;
+// per segment of 32 batch slots the threads of each slot add its entries over the blocks it reached
+// and store the (tile, Gaussian) totals at the slot's emit position (plain stores), which the gather
+// then adds per Gaussian in a fixed order. The per-op entry point adds them with float atomics.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -192,26 +194,12 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
         // the groups walk their lists together (the iteration count is the wave's longest list); a
         // lane takes a pair through selects rather than branches, and stops once its T is spent
         const int len = s_len[bl];
-        const int n_it = wave_list_max(s_len, wave);
-        for (int j = 0; j < n_it; j++) {
-            if (__all(done)) break;  // uniform
-            const int t = j < len ? static_cast<int>(s_list[bl][j]) : -1;  // group-uniform
-            const int tc = t < 0 ? 0 : t;
-            const float4 xyo = s_xyo[tc];
-            const float4 con = s_con[tc];
-            const float dx = xyo.x - px, dy = xyo.y - py;
-            const float sigma = sigma_of(con.x, con.y, con.z, dx, dy);
-            bool take = (t >= 0) & !done & !(sigma > xyo.w);  // past the cutoff: provably below the alpha threshold
-            if (STATS) {
-                st_iters++;
-                st_entries += __popcll(__ballot((lane & 15) == 0 && t >= 0));
-            }
-            if (!__any(take)) continue;  // uniform: no lane of the wave needs the exponential
-            // one wave-uniform choice of exponential: the branch-free polynomial unless a cutoff in use
-            // exceeds its range (opacity above ~1e35)
-            const float vis = __any(take & (xyo.w > 86.0f)) ? sxm::expf_fast(-sigma) : exp_neg_poly(sigma);
-            const float alpha = sxd::smin(sx::kMaxAlpha, xyo.z * vis);
-            take = take && !(sigma < 0.f) && !(alpha < sx::kAlphaThreshold);
+        const int n_it = __builtin_amdgcn_readfirstlane(wave_list_max(s_len, wave));
+        const uint8_t* my_list = s_list[bl];
+        // one list entry composited into the lane's pixel: opacity * exp(-sigma) = oe
+        auto composite = [&](bool in, float sg, float oe, int tc, int32_t id) {
+            const float alpha = sxd::smin(sx::kMaxAlpha, oe);
+            bool take = in && !done && !(sg < 0.f) && !(alpha < sx::kAlphaThreshold);
             const float next_T = T * (1.0f - alpha);
             const bool spent = take && next_T <= sx::kTransmittanceThreshold;
             done = done || spent;
@@ -221,9 +209,34 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             r0 = take ? __builtin_fmaf(c.x, w, r0) : r0;
             r1 = take ? __builtin_fmaf(c.y, w, r1) : r1;
             r2 = take ? __builtin_fmaf(c.z, w, r2) : r2;
-            cur = take ? bstart + t : cur;
+            cur = take ? id : cur;
             T = take ? next_T : T;
             if (STATS) st_taken += __popcll(__ballot(take));
+        };
+        // two list entries per iteration: their sigmas and exponentials are independent, only T and
+        // the colour sums run through them in order
+        for (int j = 0; j < n_it; j += 2) {
+            if (__all(done)) break;  // uniform
+            const int raw0 = my_list[j], raw1 = my_list[min(j + 1, kThreads - 1)];  // past the list: masked
+            const int t0 = j < len ? raw0 : -1, t1 = j + 1 < len ? raw1 : -1;  // group-uniform
+            const int tc0 = t0 < 0 ? 0 : t0, tc1 = t1 < 0 ? 0 : t1;
+            const float4 xyo0 = s_xyo[tc0], con0 = s_con[tc0];
+            const float4 xyo1 = s_xyo[tc1], con1 = s_con[tc1];
+            const float sg0 = sigma_of(con0.x, con0.y, con0.z, xyo0.x - px, xyo0.y - py);
+            const float sg1 = sigma_of(con1.x, con1.y, con1.z, xyo1.x - px, xyo1.y - py);
+            const bool in0 = (t0 >= 0) & !done & !(sg0 > xyo0.w);
+            const bool in1 = (t1 >= 0) & !done & !(sg1 > xyo1.w);
+            if (STATS) {
+                st_iters += 1 + (j + 1 < n_it ? 1 : 0);
+                st_entries += __popcll(__ballot((lane & 15) == 0 && t0 >= 0)) + __popcll(__ballot((lane & 15) == 0 && t1 >= 0));
+            }
+            if (!__any(in0 | in1)) continue;  // uniform
+            const bool general = __any((in0 & (xyo0.w > 86.0f)) | (in1 & (xyo1.w > 86.0f)));
+            const float vis0 = general ? sxm::expf_fast(-sg0) : exp_neg_poly(sg0);
+            const float vis1 = general ? sxm::expf_fast(-sg1) : exp_neg_poly(sg1);
+            // front to back: a lane that stopped at entry 0 takes nothing more
+            composite(in0, sg0, xyo0.z * vis0, tc0, bstart + t0);
+            composite(in1, sg1, xyo1.z * vis1, tc1, bstart + t1);
         }
     }
     if (STATS && lane == 0) {
