@@ -17,7 +17,7 @@
 // workgroup exits as soon as all its pixels are done.
 // Backward: back-to-front walk recovering T by division, four list entries per group at a time;
 // a group sums its four splats' nine gradient components over its 16 lanes with one transposed
-// reduction (11 DPP/select instructions per component) and stores the sums in an LDS entry buffer;
+// reduction (8 DPP instructions per component) and stores the sums in an LDS entry buffer;
 // per segment of 32 batch slots the threads of each slot add its entries over the blocks it reached
 // and store the (tile, Gaussian) totals at the slot's emit position (plain stores), which the gather
 // then adds per Gaussian in a fixed order. The per-op entry point adds them with float atomics.
@@ -269,16 +269,30 @@ __device__ __forceinline__ int row_max16(int v) {
     v = max(v, dpp_i<0x140>(v));  // row_mirror
     return v;
 }
-// Four per-lane values (one per list slot A..D of the group) summed over each 16-lane group in 11
-// instructions. lo8: lane bit 3 clear; lo4: lane bit 2 clear. Stage 1 pairs lane r with r ^ 8
-// (row_ror:8) and keeps A in lanes 0-7, B in 8-15 (C and D likewise); stage 2 pairs r with its
-// mirror in the 8-lane half (row_half_mirror) and keeps A / B in quads 0 and 2, C / D in quads 1 and
-// 3; the quad sums finish it. The result: quad 0 holds the group total of A, quad 1 of C, quad 2 of
-// B, quad 3 of D (every lane of the quad).
-__device__ __forceinline__ float group_sum4(float a, float b, float c, float d, bool lo8, bool lo4) {
-    const float s1 = (lo8 ? a : b) + dpp_f<0x128>(lo8 ? b : a);
-    const float t1 = (lo8 ? c : d) + dpp_f<0x128>(lo8 ? d : c);
-    float v = (lo4 ? s1 : t1) + dpp_f<0x141>(lo4 ? t1 : s1);
+// Four per-lane values (one per list slot A..D of the group) summed over each 16-lane group in 8
+// instructions. Stage 1 pairs lane r with r ^ 8 (row_ror:8): lanes 0-7 sum A, lanes 8-15 sum B (C
+// and D likewise); stage 2 pairs r with its mirror in the 8-lane half (row_half_mirror): quads 0 and
+// 2 sum the stage-1 A / B, quads 1 and 3 the C / D; the quad sums finish it. The result: quad 0 holds
+// the group total of A, quad 1 of C, quad 2 of B, quad 3 of D (every lane of the quad). Each stage
+// writes its two halves with two DPP adds whose bank masks (4-lane banks of the 16-lane row) select
+// the lanes, so no select instruction picks the operands. The outputs are early-clobber (the second
+// add of a pair still reads the inputs); the s_nop covers the DPP read of a just-written VGPR.
+__device__ __forceinline__ float group_sum4(float a, float b, float c, float d) {
+    float s1, t1, v;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %2, %2 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+        "v_add_f32_dpp %0, %3, %3 row_ror:8 row_mask:0xf bank_mask:0xc\n\t"
+        "v_add_f32_dpp %1, %4, %4 row_ror:8 row_mask:0xf bank_mask:0x3\n\t"
+        "v_add_f32_dpp %1, %5, %5 row_ror:8 row_mask:0xf bank_mask:0xc"
+        : "=&v"(s1), "=&v"(t1)
+        : "v"(a), "v"(b), "v"(c), "v"(d));
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+        "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa"
+        : "=&v"(v)
+        : "v"(s1), "v"(t1));
     v += dpp_f<0xB1>(v);
     v += dpp_f<0x4E>(v);
     return v;
@@ -397,7 +411,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     const int32_t num = max(0, tile_end - range_start);
     const int num_batches = (num + kThreads - 1) / kThreads;
     // a group's reduction leaves slot A in lane 0, B in 8, C in 4, D in 12: those lanes store them
-    const bool lo8 = (r & 8) == 0, lo4 = (r & 4) == 0;
     const int wslot = (r == 0) ? 0 : (r == 8) ? 1 : (r == 4) ? 2 : (r == 12) ? 3 : -1;
     // blocks of this wave's four groups (for the lockstep chunk count)
     const int wb0 = block_of(wave, 0), wb1 = block_of(wave, 16), wb2 = block_of(wave, 32), wb3 = block_of(wave, 48);
@@ -587,7 +600,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                 }
 #pragma unroll
                 for (int k = 0; k < NV; k++) {
-                    const float v = group_sum4(gv[0][k], gv[1][k], gv[2][k], gv[3][k], lo8, lo4);
+                    const float v = group_sum4(gv[0][k], gv[1][k], gv[2][k], gv[3][k]);
                     if (e_w >= 0) s_ent[bl][k][ent_rot(e_w, bl, kSeg)] = v;  // plain store: one writer per (block, entry)
                 }
             }
