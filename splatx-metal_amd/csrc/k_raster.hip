@@ -480,12 +480,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
             for (int j4 = 0; j4 < n4; j4++) {
                 const int j = 4 * j4;
                 const uint32_t packed = seg4[j4];  // bytes past the list are masked below
-                int ts[4], tc[4];
+                int tc[4];
+                bool inl[4];
                 float4 xyo[4], con[4], rgb[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    ts[k] = j + k < cnt ? kSeg * sg + static_cast<int>((packed >> (8 * k)) & 0xFFu) : -1;
-                    tc[k] = ts[k] < 0 ? 0 : ts[k];
+                    // past the list the byte is stale (or never written): masked into the segment's
+                    // slots for the read, and the entry is invalid
+                    inl[k] = j + k < cnt;
+                    tc[k] = kSeg * sg + static_cast<int>((packed >> (8 * k)) & static_cast<uint32_t>(kSeg - 1));
                     xyo[k] = s_xyo[tc[k]];
                     con[k] = s_con[tc[k]];
                     rgb[k] = s_rgb[tc[k]];
@@ -500,7 +503,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                     dxs[k] = xyo[k].x - px;
                     dys[k] = xyo[k].y - py;
                     sig[k] = sigma_of(con[k].x, con[k].y, con[k].z, dxs[k], dys[k]);
-                    valid[k] = (ts[k] >= 0) & (tc[k] >= t_min) & !(sig[k] > xyo[k].w);  // bitwise: no branches
+                    valid[k] = inl[k] & (tc[k] >= t_min) & !(sig[k] > xyo[k].w);  // bitwise: no branches
                 }
                 const bool any_valid = __any(valid[0] | valid[1] | valid[2] | valid[3]);
                 if (STATS) {
@@ -508,7 +511,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                     st_empty += any_valid ? 0 : 1;
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
-                        st_entries += __popcll(__ballot(r == 0 && ts[k] >= 0));
+                        st_entries += __popcll(__ballot(r == 0 && inl[k]));
                         st_cut += __popcll(__ballot(valid[k]));
                     }
                 }
@@ -521,9 +524,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                 }
                 // one wave-uniform choice of exponential for the chunk: the branch-free polynomial unless
                 // some cutoff in use exceeds its range (opacity above ~1e35)
-                const float cmax = sxd::smax(sxd::smax(valid[0] ? xyo[0].w : 0.f, valid[1] ? xyo[1].w : 0.f),
-                                             sxd::smax(valid[2] ? xyo[2].w : 0.f, valid[3] ? xyo[3].w : 0.f));
-                const bool general = __any(cmax > 86.0f);
+                const bool general = __any((valid[0] & (xyo[0].w > 86.0f)) | (valid[1] & (xyo[1].w > 86.0f)) |
+                                           (valid[2] & (xyo[2].w > 86.0f)) | (valid[3] & (xyo[3].w > 86.0f)));
                 // The exponential's value only enters gradients (compared at a relative tolerance), so the
                 // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
                 // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at
@@ -538,9 +540,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         e[k] = __builtin_amdgcn_exp2f(-sig[k] * 1.44269504f);
-                        const float t1 = xyo[k].w - 0.01f;
-                        const bool n1 = __builtin_fabsf(sig[k] - t1) < 0x1p-12f;
-                        const bool n2 = __builtin_fabsf(sig[k] - (t1 - kLogAlphaSpan)) < 0x1p-12f;
+                        // sigma less the cutoff: the turning points sit at -0.01 and -0.01 - kLogAlphaSpan
+                        const float d = sig[k] - xyo[k].w;
+                        const bool n1 = __builtin_fabsf(d + 0.01f) < 0x1p-12f;
+                        const bool n2 = __builtin_fabsf(d + (0.01f + kLogAlphaSpan)) < 0x1p-12f;
                         near = near | (valid[k] & (n1 | n2));
                     }
                     exact = __any(near);
