@@ -4,9 +4,11 @@
 // Contract: KernelBackend.h:130-148 / sort_isect (ascending unsigned key, stable, only bits
 // [0, key_bits) significant). Design: digits of at most 8 bits, the key bits spread evenly over the
 // fewest passes, so a 45-bit isect key needs 6 passes (the reference's 4-bit digits need 12) and a
-// 13-bit tile id two passes of 7 and 6 bits. Below 2^30 keys the passes run onesweep (see k_os_pass): the
-// digit histograms of all passes come from one read of the keys, and each pass is one launch
-// whose tiles chain their digit prefixes by look-back. The fallback is three launches per pass
+// 13-bit tile id two passes of 7 and 6 bits. Below 2^30 keys and 2048 tiles of 4096 keys the passes
+// run onesweep (see k_os_pass): the digit histograms of all passes come from one read of the keys,
+// and each pass is one launch whose tiles chain their digit prefixes by look-back. From 2048 tiles on
+// each pass counts its tiles' digits, scans the count matrix and scatters with the same pass kernel,
+// without the chain (see k_rs_count). The fallback at 2^30 keys and above is three launches per pass
 // with no inter-workgroup waiting:
 //   1. per-tile digit histogram (LDS counters)        -> hist[digit][tile], plus the digit totals
 //   2. one workgroup per digit scans its row of hist   -> global start of (digit, tile)
@@ -416,14 +418,157 @@ __device__ __forceinline__ uint32_t lanes_below_count(uint64_t mask) {
                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
 }
 
-// NB = the digit's width in bits (mask = 2^NB - 1).
-template <class K, int NB>
+// ---- reduce-then-scan: the pass's prefixes without a chain between tiles ------------------------
+// For sorts of many tiles the onesweep pass is bound by its look-back: a tile waits until its
+// predecessors' inclusive prefixes have been published, which advance at a fixed rate along the chain.
+// Instead each pass counts the digits of every tile (k_rs_count, digit-major: cnt[d][tile]), scans the
+// whole count matrix once (the exclusive prefix of entry (d, tile) is where the tile's run of digit d
+// starts in the output: all keys of smaller digits, then those of digit d in earlier tiles), and the
+// pass kernel places its keys with these starts. Counts fit u32: a pass sorts fewer than 2^30 keys.
+constexpr int kScanChunk = kThreads * 16;  // elements per workgroup of the count-matrix scan
+
+// Digit counts of tile blockIdx.x -> cnt[d * n_tiles + tile] for d <= mask. Every workgroup of the grid
+// writes its counts (zeros for a tile past the device count), so the scanned matrix is complete. A
+// thread takes 16 consecutive keys (16-B loads) and adds each run of equal digits once: neighbouring
+// keys often share the high digits (the tiles of one Gaussian along a row), and the lanes of a wave,
+// 16 keys apart, rarely hit the same counter at once.
+template <class K>
+__global__ void __launch_bounds__(kThreads) k_rs_count(const K* __restrict__ keys, int64_t n, int shift, uint32_t mask,
+                                                       uint32_t* __restrict__ cnt, int n_tiles,
+                                                       const int64_t* __restrict__ n_dev) {
+    static_assert(kRounds * sizeof(K) % 16 == 0, "a thread's keys are whole 16-B vectors");
+    __shared__ uint32_t h[kBins];
+    if (n_dev) n = *n_dev;
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t i0 = (int64_t)blockIdx.x * kTile + (int64_t)threadIdx.x * kRounds;
+    K key[kRounds];
+    if (i0 + kRounds <= n) {  // the tile is 16-B aligned (4096 keys), and so is each thread's part
+        constexpr int kVec = kRounds * sizeof(K) / 16;
+        uint4 w[kVec];
+#pragma unroll
+        for (int q = 0; q < kVec; q++) w[q] = reinterpret_cast<const uint4*>(keys + i0)[q];
+        __builtin_memcpy(key, w, sizeof(key));
+    } else {
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) key[r] = i0 + r < n ? keys[i0 + r] : K(0);
+    }
+    const int valid = static_cast<int>(min<int64_t>(kRounds, max<int64_t>(0, n - i0)));  // keys of the thread
+    uint32_t run_d = static_cast<uint32_t>(key[0] >> shift) & mask, run_n = 0;
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+        const uint32_t d = static_cast<uint32_t>(key[r] >> shift) & mask;
+        if (r < valid) {
+            if (d != run_d) {
+                if (run_n) atomicAdd(&h[run_d], run_n);
+                run_d = d;
+                run_n = 0;
+            }
+            run_n++;
+        }
+    }
+    if (run_n) atomicAdd(&h[run_d], run_n);
+    __syncthreads();
+    if (threadIdx.x <= mask) cnt[(size_t)threadIdx.x * n_tiles + blockIdx.x] = h[threadIdx.x];
+}
+
+// Exclusive scan of v[0, len) in place, in three launches: chunk sums, their exclusive scan (one
+// workgroup), and the scan of each chunk from its prefix. v starts 64-B aligned (16-B loads).
+__global__ void __launch_bounds__(kThreads) k_rs_reduce(const uint32_t* __restrict__ v, int64_t len,
+                                                        uint32_t* __restrict__ sums) {
+    __shared__ uint32_t s_wave[kWaves];
+    const int64_t base = (int64_t)blockIdx.x * kScanChunk;
+    uint32_t acc = 0;
+    if (base + kScanChunk <= len) {  // four coalesced 16-B loads per thread
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint4 w = reinterpret_cast<const uint4*>(v + base)[q * kThreads + threadIdx.x];
+            acc += w.x + w.y + w.z + w.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int64_t k = base + i * kThreads + threadIdx.x;
+            acc += k < len ? v[k] : 0u;
+        }
+    }
+    uint32_t all = 0;
+    block_excl_scan_u32(acc, s_wave, &all);
+    if (threadIdx.x == 0) sums[blockIdx.x] = all;
+}
+
+__global__ void __launch_bounds__(kThreads) k_rs_top(uint32_t* __restrict__ sums, int n) {
+    __shared__ uint32_t s_wave[kWaves];
+    uint32_t carry = 0;
+    for (int c0 = 0; c0 < n; c0 += kScanChunk) {  // uniform
+        const int i0 = c0 + threadIdx.x * 16;
+        uint32_t x[16], acc = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            x[i] = i0 + i < n ? sums[i0 + i] : 0u;
+            acc += x[i];
+        }
+        uint32_t all = 0;
+        uint32_t run = block_excl_scan_u32(acc, s_wave, &all) + carry;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            if (i0 + i < n) sums[i0 + i] = run;
+            run += x[i];
+        }
+        carry += all;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) k_rs_down(uint32_t* __restrict__ v, int64_t len,
+                                                      const uint32_t* __restrict__ sums) {
+    __shared__ uint32_t s_wave[kWaves];
+    const int64_t i0 = (int64_t)blockIdx.x * kScanChunk + threadIdx.x * 16;  // 16 consecutive per thread
+    uint32_t x[16], acc = 0;
+    if (i0 + 16 <= len) {  // four 16-B loads
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint4 w = reinterpret_cast<const uint4*>(v + i0)[q];
+            x[4 * q] = w.x;
+            x[4 * q + 1] = w.y;
+            x[4 * q + 2] = w.z;
+            x[4 * q + 3] = w.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) x[i] = i0 + i < len ? v[i0 + i] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc += x[i];
+    uint32_t all = 0;
+    uint32_t run = block_excl_scan_u32(acc, s_wave, &all) + sums[blockIdx.x];
+    uint32_t y[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        y[i] = run;
+        run += x[i];
+    }
+    if (i0 + 16 <= len) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            reinterpret_cast<uint4*>(v + i0)[q] = make_uint4(y[4 * q], y[4 * q + 1], y[4 * q + 2], y[4 * q + 3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (i0 + i < len) v[i0 + i] = y[i];
+    }
+}
+
+// NB = the digit's width in bits (mask = 2^NB - 1). CHAIN: the onesweep pass (tile index from the
+// counter, prefixes by look-back); otherwise tile = blockIdx.x and the tile's run of digit d starts at
+// starts[d * n_tiles + tile] (the scanned count matrix of the reduce-then-scan path).
+template <class K, int NB, bool CHAIN>
 __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin, const int32_t* __restrict__ vin,
                                                       K* __restrict__ kout, int32_t* __restrict__ vout,
                                                       int64_t n, int shift, uint32_t mask, const uint32_t* __restrict__ digit_base,
                                                       uint32_t* __restrict__ status, uint32_t* __restrict__ status_next,
                                                       uint32_t* __restrict__ counter, uint32_t* __restrict__ err,
-                                                      const int64_t* __restrict__ n_dev) {
+                                                      const int64_t* __restrict__ n_dev,
+                                                      const uint32_t* __restrict__ starts, int n_tiles) {
     constexpr int kPerWave = kTile / kWaves;  // 1024
     __shared__ K s_k[kTile];
     __shared__ int32_t s_v[kTile];
@@ -439,11 +584,11 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
         n = *n_dev;
         if (static_cast<int64_t>(blockIdx.x) * kTile >= n) return;  // uniform
     }
-    if (tid == 0) s_tile = atomicAdd(counter, 1u);
+    if (CHAIN && tid == 0) s_tile = atomicAdd(counter, 1u);
 #pragma unroll
     for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
     __syncthreads();
-    const uint32_t tile = s_tile;
+    const uint32_t tile = CHAIN ? s_tile : blockIdx.x;
     const int64_t base = (int64_t)tile * kTile;
     const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
     K key[kRounds];
@@ -520,7 +665,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     }
     // publish this tile's digit counts now; the look-back for the prefixes of the tiles before it
     // waits until the tile has been reordered in LDS, which gives them time to finish theirs
-    st_status(status + (size_t)tile * kBins + tid, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
+    if (CHAIN) st_status(status + (size_t)tile * kBins + tid, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
     s_cnt[tid] = tile_count;
     __syncthreads();
 #pragma unroll
@@ -538,7 +683,9 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     // prefix among them, or up to the newest word not yet published and retries from there
     const int bins = static_cast<int>(mask) + 1;
     const int G = min(kThreads / bins, kLookLanes);  // a power of two dividing 64
-    if (tile == 0) {
+    if (!CHAIN) {
+        if (tid < bins) s_gstart[tid] = starts[(size_t)tid * n_tiles + tile] - s_lstart[tid];
+    } else if (tile == 0) {
         s_gstart[tid] = digit_base[tid] - s_lstart[tid];
     } else if (tid < bins * G) {
         const int d = tid / G, sub = tid & (G - 1);
@@ -596,7 +743,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
             s_gstart[d] = digit_base[d] + excl - s_lstart[d];
         }
     }
-    if (status_next) status_next[(size_t)tile * kBins + tid] = 0u;
+    if (CHAIN && status_next) status_next[(size_t)tile * kBins + tid] = 0u;
     __syncthreads();
     const uint32_t n32 = static_cast<uint32_t>(n);  // onesweep runs below 2^30 keys
     for (int p = tid; p < tile_n; p += kThreads) {
@@ -612,13 +759,13 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
 int tiles_for(int64_t n) { return static_cast<int>((n + kTile - 1) / kTile); }
 
 // One onesweep pass over the digit of `mask`'s width at `shift`.
-template <class K>
+template <class K, bool CHAIN>
 void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, K* kout, int32_t* vout, int64_t n,
                     int shift, uint32_t mask, const uint32_t* digit_base, uint32_t* status, uint32_t* status_next,
-                    uint32_t* counter, uint32_t* err, const int64_t* n_dev) {
+                    uint32_t* counter, uint32_t* err, const int64_t* n_dev, const uint32_t* starts = nullptr) {
 #define SX_OS_PASS(NB)                                                                                          \
-    hipLaunchKernelGGL((k_os_pass<K, NB>), dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, mask, \
-                       digit_base, status, status_next, counter, err, n_dev)
+    hipLaunchKernelGGL((k_os_pass<K, NB, CHAIN>), dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, \
+                       mask, digit_base, status, status_next, counter, err, n_dev, starts, tiles)
     switch (__builtin_popcount(mask)) {
         case 1: SX_OS_PASS(1); break;
         case 2: SX_OS_PASS(2); break;
@@ -633,10 +780,14 @@ void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, 
 }
 
 constexpr int kMaxPasses = 8;
+// From this many 4096-key tiles on (8.4 M keys) a pass takes its prefixes from a scan of the tiles'
+// digit counts instead of the look-back chain: the counting read costs less than the chain's waits.
+constexpr int kRtsMinTiles = 2048;
 // scratch layout: a fixed header (digit totals and bases of up to 8 passes, the per-pass tile
 // counters, the error word) and then two tiles x 256 word buffers (the three-launch path's
 // histogram, or the onesweep status words of alternate passes)
 constexpr int kHeaderWords = 2 * kMaxPasses * kBins + 64;
+static_assert(kHeaderWords * sizeof(uint32_t) % 64 == 0, "the count matrix after the header is 64-B aligned");
 
 // The passes read `src` first and then alternate between the two sides: pass p writes side[p & 1],
 // pass p > 0 reads side[(p - 1) & 1]. src may be side[1] (the sort then works in place over two
@@ -669,6 +820,25 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
                        clear_err ? err : nullptr);
     const K* kin = src_k;
     const int32_t* vin = src_v;
+    if (n < (int64_t{1} << 30) && tiles >= kRtsMinTiles) {  // reduce-then-scan (see k_rs_count); no histogram kernel
+        uint32_t* cnt = hist;       // (mask + 1) x tiles counts, then their starts
+        uint32_t* sums = status_b;  // the scan's chunk sums
+        for (int p = 0; p < passes; p++) {
+            const uint32_t mask = digit_mask(p, dbits, key_bits);
+            const int64_t len = static_cast<int64_t>(mask + 1) * tiles;
+            const int chunks = static_cast<int>((len + kScanChunk - 1) / kScanChunk);
+            hipLaunchKernelGGL(k_rs_count<K>, dim3(tiles), dim3(kThreads), 0, s, kin, n, dbits * p, mask, cnt, tiles,
+                               n_dev);
+            hipLaunchKernelGGL(k_rs_reduce, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
+            hipLaunchKernelGGL(k_rs_top, dim3(1), dim3(kThreads), 0, s, sums, chunks);
+            hipLaunchKernelGGL(k_rs_down, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
+            launch_os_pass<K, false>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p, mask, nullptr,
+                                     nullptr, nullptr, nullptr, err, n_dev, cnt);
+            kin = side_k[p & 1];
+            vin = side_v[p & 1];
+        }
+        return passes;
+    }
     if (n < (int64_t{1} << 30)) {  // onesweep: counts and prefixes fit the 30-bit status words
         const int hist_blocks = std::min(tiles, kHistBlocks);
         if (key_bits <= kFullBits)
@@ -681,7 +851,7 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
         uint32_t* st[2] = {hist, status_b};
         for (int p = 0; p < passes; p++) {
             uint32_t* next = p + 1 < passes ? st[(p + 1) & 1] : nullptr;
-            launch_os_pass<K>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p,
+            launch_os_pass<K, true>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p,
                               digit_mask(p, dbits, key_bits), bases + p * kBins, st[p & 1], next, counters + p, err,
                               n_dev);
             kin = side_k[p & 1];

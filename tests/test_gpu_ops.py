@@ -142,6 +142,25 @@ def test_sort_3m_with_ties_and_determinism(gpu):
     assert len(digests) == 1
 
 
+# From 2048 tiles of 4096 keys on (8.4 M keys) every pass takes its prefixes from a scan of the tiles'
+# digit counts instead of the look-back chain: the same stable order, checked at the threshold, with a
+# ragged last tile, and for 2, 6 and 8 passes; and all keys equal (every tile's run of one digit).
+@pytest.mark.parametrize("n,bits", [(8_388_608, 13), (9_000_001, 45), (9_000_001, 64)])
+def test_sort_reduce_then_scan_matches_stable_sort(gpu, n, bits):
+    keys, vals = inputs.sort_inputs(n, bits, seed=n + bits)
+    ks, vs = gpu.sort_isect(keys, vals, bits)
+    rk, rv = inputs.stable_sort_ref(keys, vals)
+    assert np.array_equal(ks, rk) and np.array_equal(vs, rv)
+
+
+def test_sort_reduce_then_scan_equal_keys(gpu):
+    n = 8_500_000
+    keys = np.full(n, (np.uint64(5) << np.uint64(32)) | np.uint64(77), np.uint64)
+    vals = np.arange(n, dtype=np.int32)[::-1].copy()
+    ks, vs = gpu.sort_isect(keys, vals, 45)
+    assert np.array_equal(ks, keys) and np.array_equal(vs, vals)
+
+
 def test_offsets_doc_example_and_edges(gpu, oracle):
     # IsectTests/ScanTests doc example: tile ids [1,1,1,3,3] over 6 tiles -> [0,0,3,3,5,5]
     ids = (np.array([1, 1, 1, 3, 3], np.uint64) << np.uint64(32))
