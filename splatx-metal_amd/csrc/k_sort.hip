@@ -582,177 +582,186 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
     const int lane = tid & 63, wave = tid >> 6;
     if (n_dev) {  // the grid is sized for a capacity: exactly one workgroup per tile of keys takes a tile
         n = *n_dev;
-        if (static_cast<int64_t>(blockIdx.x) * kTile >= n) return;  // uniform
+        if (CHAIN && static_cast<int64_t>(blockIdx.x) * kTile >= n) return;  // uniform
     }
-    if (CHAIN && tid == 0) s_tile = atomicAdd(counter, 1u);
+    // CHAIN: one tile, from the counter. Otherwise tiles blockIdx.x, + gridDim.x, ... below the (device)
+    // key count (the launch gives one workgroup per tile; the loop form measured faster at config 5).
+    const int64_t n_work = (n + kTile - 1) / kTile;
+    for (int64_t t = blockIdx.x; CHAIN || t < n_work; t += gridDim.x) {  // uniform
+        if (CHAIN && tid == 0) s_tile = atomicAdd(counter, 1u);
 #pragma unroll
-    for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
-    __syncthreads();
-    const uint32_t tile = CHAIN ? s_tile : blockIdx.x;
-    const int64_t base = (int64_t)tile * kTile;
-    const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
-    K key[kRounds];
-    int32_t val[kRounds];
-    // null values: the input index. The (uniform) choice is taken once around straight-line loads: a
-    // choice per round compiles to a wait for every load before the next is issued.
-    if (tile_n == kTile) {  // uniform
-        if (vin) {
+        for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
+        __syncthreads();
+        const uint32_t tile = CHAIN ? s_tile : static_cast<uint32_t>(t);
+        // the tile's digit starts are requested now, so their latency overlaps the loads and the ranking
+        const uint32_t my_start = (!CHAIN && tid <= mask) ? starts[(size_t)tid * n_tiles + tile] : 0u;
+        const int64_t base = (int64_t)tile * kTile;
+        const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
+        K key[kRounds];
+        int32_t val[kRounds];
+        // null values: the input index. The (uniform) choice is taken once around straight-line loads: a
+        // choice per round compiles to a wait for every load before the next is issued.
+        if (tile_n == kTile) {  // uniform
+            if (vin) {
+#pragma unroll
+                for (int r = 0; r < kRounds; r++) {
+                    const int i = wave * kPerWave + r * 64 + lane;
+                    key[r] = kin[base + i];
+                    val[r] = vin[base + i];
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < kRounds; r++) {
+                    const int i = wave * kPerWave + r * 64 + lane;
+                    key[r] = kin[base + i];
+                    val[r] = static_cast<int32_t>(base + i);
+                }
+            }
+        } else if (vin) {
 #pragma unroll
             for (int r = 0; r < kRounds; r++) {
                 const int i = wave * kPerWave + r * 64 + lane;
-                key[r] = kin[base + i];
-                val[r] = vin[base + i];
+                key[r] = i < tile_n ? kin[base + i] : K(0);
+                val[r] = i < tile_n ? vin[base + i] : 0;
             }
         } else {
 #pragma unroll
             for (int r = 0; r < kRounds; r++) {
                 const int i = wave * kPerWave + r * 64 + lane;
-                key[r] = kin[base + i];
-                val[r] = static_cast<int32_t>(base + i);
+                key[r] = i < tile_n ? kin[base + i] : K(0);
+                val[r] = i < tile_n ? static_cast<int32_t>(base + i) : 0;
             }
         }
-    } else if (vin) {
+        // per-wave digit counts, rounds in order; off[r] = the key's place among the wave's keys of its
+        // digit (keys of earlier rounds, then lanes below it with the same digit). All lanes read the
+        // digit's running count before one leader lane per digit group advances it.
+        uint32_t off[kRounds];
+        uint32_t* woff = s_woff[wave];
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
-            const int i = wave * kPerWave + r * 64 + lane;
-            key[r] = i < tile_n ? kin[base + i] : K(0);
-            val[r] = i < tile_n ? vin[base + i] : 0;
+            const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
+            const uint32_t x = static_cast<uint32_t>(key[r] >> shift);
+            const uint32_t d = x & mask;
+            const uint64_t match = digit_match_bits<NB>(x, __ballot(valid));
+            const uint32_t rank = lanes_below_count(match);
+            const uint32_t prior = valid ? woff[d] : 0u;
+            __builtin_amdgcn_wave_barrier();
+            if (valid && rank == 0u) woff[d] = prior + static_cast<uint32_t>(__popcll(match));
+            __builtin_amdgcn_wave_barrier();
+            off[r] = prior + rank;
         }
-    } else {
+        __syncthreads();
+        uint32_t tile_count;
+        {
+            uint32_t c[kWaves], tot = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) {
+                c[w] = s_woff[w][tid];
+                tot += c[w];
+            }
+            tile_count = tot;
+            uint32_t all = 0;
+            uint32_t run = block_excl_scan_u32(tot, s_wave, &all);
+            s_lstart[tid] = run;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) {
+                s_woff[w][tid] = run;
+                run += c[w];
+            }
+        }
+        // publish this tile's digit counts now; the look-back for the prefixes of the tiles before it
+        // waits until the tile has been reordered in LDS, which gives them time to finish theirs
+        if (CHAIN) st_status(status + (size_t)tile * kBins + tid, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
+        s_cnt[tid] = tile_count;
+        __syncthreads();
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
-            const int i = wave * kPerWave + r * 64 + lane;
-            key[r] = i < tile_n ? kin[base + i] : K(0);
-            val[r] = i < tile_n ? static_cast<int32_t>(base + i) : 0;
+            if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
+            if (wave * kPerWave + r * 64 + lane < tile_n) {
+                const uint32_t pos = woff[static_cast<uint32_t>(key[r] >> shift) & mask] + off[r];
+                s_k[pos] = key[r];
+                s_v[pos] = val[r];
+            }
         }
-    }
-    // per-wave digit counts, rounds in order; off[r] = the key's place among the wave's keys of its
-    // digit (keys of earlier rounds, then lanes below it with the same digit). All lanes read the
-    // digit's running count before one leader lane per digit group advances it.
-    uint32_t off[kRounds];
-    uint32_t* woff = s_woff[wave];
+        __syncthreads();
+        // look back: the G lanes of digit d read kLook predecessors' words each per round trip, lane s
+        // the s-th run of kLook below j, newest first; the group adds counts up to the newest inclusive
+        // prefix among them, or up to the newest word not yet published and retries from there
+        const int bins = static_cast<int>(mask) + 1;
+        const int G = min(kThreads / bins, kLookLanes);  // a power of two dividing 64
+        if (!CHAIN) {
+            if (tid < bins) s_gstart[tid] = my_start - s_lstart[tid];
+        } else if (tile == 0) {
+            s_gstart[tid] = digit_base[tid] - s_lstart[tid];
+        } else if (tid < bins * G) {
+            const int d = tid / G, sub = tid & (G - 1);
+            const int gbase = lane & ~(G - 1);
+            const uint64_t gmask = (G == 64 ? ~0ull : ((1ull << G) - 1ull)) << gbase;
+            uint32_t excl = 0;
+            int64_t j = (int64_t)tile - 1;
+            uint32_t spins = 0;
+            for (;;) {  // the group's lanes take every branch together
+                const int64_t top = j - (int64_t)sub * kLook;
+                uint32_t w[kLook];
 #pragma unroll
-    for (int r = 0; r < kRounds; r++) {
-        const bool valid = wave * kPerWave + r * 64 + lane < tile_n;
-        const uint32_t x = static_cast<uint32_t>(key[r] >> shift);
-        const uint32_t d = x & mask;
-        const uint64_t match = digit_match_bits<NB>(x, __ballot(valid));
-        const uint32_t rank = lanes_below_count(match);
-        const uint32_t prior = valid ? woff[d] : 0u;
-        __builtin_amdgcn_wave_barrier();
-        if (valid && rank == 0u) woff[d] = prior + static_cast<uint32_t>(__popcll(match));
-        __builtin_amdgcn_wave_barrier();
-        off[r] = prior + rank;
-    }
-    __syncthreads();
-    uint32_t tile_count;
-    {
-        uint32_t c[kWaves], tot = 0;
+                for (int q = 0; q < kLook; q++)
+                    w[q] = top - q >= 0 ? ld_status(status + (size_t)(top - q) * kBins + d) : kFlagInc;
+                uint32_t part = 0;
+                int stop = 0, at = kLook;  // stop: 1 = met an inclusive prefix, 2 = met an unpublished word at q = at
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) {
-            c[w] = s_woff[w][tid];
-            tot += c[w];
-        }
-        tile_count = tot;
-        uint32_t all = 0;
-        uint32_t run = block_excl_scan_u32(tot, s_wave, &all);
-        s_lstart[tid] = run;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) {
-            s_woff[w][tid] = run;
-            run += c[w];
-        }
-    }
-    // publish this tile's digit counts now; the look-back for the prefixes of the tiles before it
-    // waits until the tile has been reordered in LDS, which gives them time to finish theirs
-    if (CHAIN) st_status(status + (size_t)tile * kBins + tid, (tile == 0 ? kFlagInc : kFlagAgg) | tile_count);
-    s_cnt[tid] = tile_count;
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kRounds; r++) {
-        if (wave * kPerWave + r * 64 >= tile_n) break;  // uniform within the wave
-        if (wave * kPerWave + r * 64 + lane < tile_n) {
-            const uint32_t pos = woff[static_cast<uint32_t>(key[r] >> shift) & mask] + off[r];
-            s_k[pos] = key[r];
-            s_v[pos] = val[r];
-        }
-    }
-    __syncthreads();
-    // look back: the G lanes of digit d read kLook predecessors' words each per round trip, lane s
-    // the s-th run of kLook below j, newest first; the group adds counts up to the newest inclusive
-    // prefix among them, or up to the newest word not yet published and retries from there
-    const int bins = static_cast<int>(mask) + 1;
-    const int G = min(kThreads / bins, kLookLanes);  // a power of two dividing 64
-    if (!CHAIN) {
-        if (tid < bins) s_gstart[tid] = starts[(size_t)tid * n_tiles + tile] - s_lstart[tid];
-    } else if (tile == 0) {
-        s_gstart[tid] = digit_base[tid] - s_lstart[tid];
-    } else if (tid < bins * G) {
-        const int d = tid / G, sub = tid & (G - 1);
-        const int gbase = lane & ~(G - 1);
-        const uint64_t gmask = (G == 64 ? ~0ull : ((1ull << G) - 1ull)) << gbase;
-        uint32_t excl = 0;
-        int64_t j = (int64_t)tile - 1;
-        uint32_t spins = 0;
-        for (;;) {  // the group's lanes take every branch together
-            const int64_t top = j - (int64_t)sub * kLook;
-            uint32_t w[kLook];
-#pragma unroll
-            for (int q = 0; q < kLook; q++)
-                w[q] = top - q >= 0 ? ld_status(status + (size_t)(top - q) * kBins + d) : kFlagInc;
-            uint32_t part = 0;
-            int stop = 0, at = kLook;  // stop: 1 = met an inclusive prefix, 2 = met an unpublished word at q = at
-#pragma unroll
-            for (int q = 0; q < kLook; q++) {
-                if (stop == 0) {
-                    const uint32_t f = w[q] & ~kValMask;
-                    if (f == 0u) {
-                        stop = 2;
-                        at = q;
-                    } else {
-                        part += w[q] & kValMask;
-                        if (f == kFlagInc) stop = 1;
+                for (int q = 0; q < kLook; q++) {
+                    if (stop == 0) {
+                        const uint32_t f = w[q] & ~kValMask;
+                        if (f == 0u) {
+                            stop = 2;
+                            at = q;
+                        } else {
+                            part += w[q] & kValMask;
+                            if (f == kFlagInc) stop = 1;
+                        }
                     }
                 }
-            }
-            uint32_t scan = part;  // inclusive over the group's lanes
-            for (int o = 1; o < G; o <<= 1) {
-                const uint32_t y = __shfl_up(scan, o, 64);
-                if (sub >= o) scan += y;
-            }
-            const uint64_t stops = __ballot(stop != 0) & gmask;
-            const int first = stops ? static_cast<int>(__builtin_ctzll(stops)) - gbase : G - 1;
-            excl += __shfl(scan, gbase + first, 64);
-            if (!stops) {
-                j -= (int64_t)G * kLook;
-                continue;
-            }
-            if (__shfl(stop, gbase + first, 64) == 1) break;
-            const int64_t adv = (int64_t)first * kLook + __shfl(at, gbase + first, 64);
-            j -= adv;
-            if (adv == 0) {
-                if (++spins > kSpinLimit) {
-                    atomicOr(err, 1u);
-                    break;
+                uint32_t scan = part;  // inclusive over the group's lanes
+                for (int o = 1; o < G; o <<= 1) {
+                    const uint32_t y = __shfl_up(scan, o, 64);
+                    if (sub >= o) scan += y;
                 }
-                __builtin_amdgcn_s_sleep(1);
+                const uint64_t stops = __ballot(stop != 0) & gmask;
+                const int first = stops ? static_cast<int>(__builtin_ctzll(stops)) - gbase : G - 1;
+                excl += __shfl(scan, gbase + first, 64);
+                if (!stops) {
+                    j -= (int64_t)G * kLook;
+                    continue;
+                }
+                if (__shfl(stop, gbase + first, 64) == 1) break;
+                const int64_t adv = (int64_t)first * kLook + __shfl(at, gbase + first, 64);
+                j -= adv;
+                if (adv == 0) {
+                    if (++spins > kSpinLimit) {
+                        atomicOr(err, 1u);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            if (sub == 0) {
+                st_status(status + (size_t)tile * kBins + d, kFlagInc | (excl + s_cnt[d]));
+                s_gstart[d] = digit_base[d] + excl - s_lstart[d];
             }
         }
-        if (sub == 0) {
-            st_status(status + (size_t)tile * kBins + d, kFlagInc | (excl + s_cnt[d]));
-            s_gstart[d] = digit_base[d] + excl - s_lstart[d];
+        if (CHAIN && status_next) status_next[(size_t)tile * kBins + tid] = 0u;
+        __syncthreads();
+        const uint32_t n32 = static_cast<uint32_t>(n);  // onesweep runs below 2^30 keys
+        for (int p = tid; p < tile_n; p += kThreads) {
+            const K k = s_k[p];
+            const uint32_t g = s_gstart[static_cast<uint32_t>(k >> shift) & mask] + static_cast<uint32_t>(p);
+            if (g < n32) {  // always, unless the look-back gave up (err set): then no write lands out of range
+                kout[g] = k;
+                vout[g] = s_v[p];
+            }
         }
-    }
-    if (CHAIN && status_next) status_next[(size_t)tile * kBins + tid] = 0u;
-    __syncthreads();
-    const uint32_t n32 = static_cast<uint32_t>(n);  // onesweep runs below 2^30 keys
-    for (int p = tid; p < tile_n; p += kThreads) {
-        const K k = s_k[p];
-        const uint32_t g = s_gstart[static_cast<uint32_t>(k >> shift) & mask] + static_cast<uint32_t>(p);
-        if (g < n32) {  // always, unless the look-back gave up (err set): then no write lands out of range
-            kout[g] = k;
-            vout[g] = s_v[p];
-        }
+        if (CHAIN) break;
+        __syncthreads();  // the next tile reuses the LDS
     }
 }
 
