@@ -142,10 +142,11 @@ def test_sort_3m_with_ties_and_determinism(gpu):
     assert len(digests) == 1
 
 
-# From 2048 tiles of 4096 keys on (8.4 M keys) every pass takes its prefixes from a scan of the tiles'
-# digit counts instead of the look-back chain: the same stable order, checked at the threshold, with a
-# ragged last tile, and for 2, 6 and 8 passes; and all keys equal (every tile's run of one digit).
-@pytest.mark.parametrize("n,bits", [(8_388_608, 13), (9_000_001, 45), (9_000_001, 64)])
+# From 256 tiles of 4096 keys on (1 M keys) every pass takes its prefixes from a scan of the tiles'
+# digit counts instead of the look-back chain (below, the 300,001-key cases above take the chain): the
+# same stable order, checked at the threshold, with a ragged last tile, at config-5 scale in tiles,
+# and for 2, 6 and 8 passes; and all keys equal (every tile's run of one digit).
+@pytest.mark.parametrize("n,bits", [(1_048_576, 13), (1_048_577, 45), (9_000_001, 45), (9_000_001, 64)])
 def test_sort_reduce_then_scan_matches_stable_sort(gpu, n, bits):
     keys, vals = inputs.sort_inputs(n, bits, seed=n + bits)
     ks, vs = gpu.sort_isect(keys, vals, bits)
