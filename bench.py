@@ -48,12 +48,12 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
         # per intersection: its emit position (4 B), the Gaussian of that position (4 B), the 36-B record
         return i * (4 + 4 + 36) + px * 20.0
     if name == "raster_bwd":
-        # as the forward, plus the 36-B sums stored per (tile, Gaussian) and its valid bit
-        return i * (4 + 4 + 36 + 36 + 1.0 / 8.0) + px * (4 + 4 + 12)
+        # as the forward, plus the 36-B sums and the 4-B step stamp stored per (tile, Gaussian)
+        return i * (4 + 4 + 36 + 36 + 4) + px * (4 + 4 + 12)
     if name == "gather":
-        # depth order and the scan per Gaussian (12 B), the valid bits and 36-B sums of the entries, the
-        # 48-B gradient record of the visible Gaussians
-        return n * 12.0 + i * (36.0 + 1.0 / 8.0) + v * 48.0
+        # depth order, the scan and the touched flag per Gaussian (13 B), the 36-B sums and stamp of the
+        # entries, the 48-B gradient record of the visible Gaussians
+        return n * 13.0 + i * 40.0 + v * 48.0
     if name == "depth_sort":
         # keys: tile counts (4 B) and the depths of the visible (4 B) in, (key, index) out (8 B); then the
         # onesweep sort of n (u32, i32) pairs: one histogram read (4 B), per pass a read and a write (16 B)

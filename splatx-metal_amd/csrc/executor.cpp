@@ -63,6 +63,8 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->cum.alloc(R);
             e->long_list.alloc(R);
             e->long_count.alloc(1);
+            e->stamp.alloc(1);
+            SXH_HIP(hipMemsetAsync(e->stamp.p, 0, sizeof(uint32_t), b->stream));
             e->touched.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
             e->dkey_a.alloc(R);
@@ -336,13 +338,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         }
         // the backward stores per-(tile, Gaussian) sums; the gather adds them per Gaussian in emit order, so
         // the gradients do not depend on the order in which tiles finish (no float atomics)
-        sxk::raster_clear_valid(e->valid.p, n_dev ? static_cast<int64_t>(e->isect_cap) : n_host, n_dev, e->touched.p,
-                                c.count, e->long_count.p, s);
+        sxk::raster_bwd_begin(e->stamp.p, e->touched.p, c.count, e->long_count.p, s);
         sxk::RasterBwdGrads gg{nullptr, nullptr,   nullptr,    nullptr,    nullptr,
-                               e->grads.p, e->part.p, e->valid.p, e->touched.p};
+                               e->grads.p, e->part.p, e->stamp.p, e->touched.p};
         sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
         e->mark("raster_bwd");
-        sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->valid.p, e->touched.p, e->grads.p,
+        sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
                                  e->long_list.p, e->long_count.p, s);
         e->mark("gather");
         sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s);

@@ -400,6 +400,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     const float bg_dot = bg ? (bg[0] * vc0 + bg[1] * vc1 + bg[2] * vc2) : 0.f;
     const float tva = T_final * (va - bg_dot);  // the alpha and background terms of every v_alpha, over ra
     const int32_t block_bin_final = row_max16(bin_final);
+    const uint32_t stamp = g.part ? *g.stamp : 0u;  // the step's stamp for `part` entries
     if (r == 0) s_bbf[bl] = block_bin_final;
     __syncthreads();
     // the walk starts at the tile's last contributing intersection: everything behind it (most of
@@ -646,7 +647,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                             dst[k] = (!ABSGRAD && (k == 3 || k == 5)) ? 0.5f * v[i] : v[i];  // halves of dx^2, dy^2
                         }
                         if (q == 0) {
-                            atomicOr(&g.valid[f >> 5], 1u << (f & 31));  // integer: order-free
+                            dst[kPartFloats] = __uint_as_float(stamp);  // the entry is this step's
                             g.touched[__float_as_int(s_con[slot].w)] = 1;  // the Gaussian has entries to gather
                         }
                     } else {
@@ -677,33 +678,26 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
 namespace {
 constexpr int kLongRange = 64;  // gather: longer entry ranges are reduced by a whole wave
 
-// bit words of the backward's valid bitmap, for the device intersection count (grid sized for the
-// capacity), the rows' touched flags, and the gather's long-range queue count
-__global__ void __launch_bounds__(kThreads) k_clear_valid(uint32_t* __restrict__ valid, int64_t n_words,
-                                                          const int64_t* __restrict__ n_isects_dev,
-                                                          uint8_t* __restrict__ touched, int rows,
-                                                          int32_t* __restrict__ long_count) {
-    if (n_isects_dev) n_words = (*n_isects_dev + 31) / 32;
-    if (blockIdx.x == 0 && threadIdx.x == 0) *long_count = 0;
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n_words; i += (int64_t)gridDim.x * kThreads)
-        valid[i] = 0u;
+// the backward's new stamp (never 0: zeroed entries hold 0), the rows' touched flags and the gather's
+// long-range queue count
+__global__ void __launch_bounds__(kThreads) k_bwd_begin(uint32_t* __restrict__ stamp, uint8_t* __restrict__ touched,
+                                                        int rows, int32_t* __restrict__ long_count) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *long_count = 0;
+        const uint32_t next = *stamp + 1u;
+        *stamp = next ? next : 1u;
+    }
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < rows; i += gridDim.x * kThreads) touched[i] = 0;
 }
 
-// entry p of `part` as three aligned float4 loads (the 9 sums and 3 unused floats)
-__device__ __forceinline__ void load_entry(const float* __restrict__ part, int32_t p, float* e) {
+// entry p of `part` as three aligned float4 loads: the 9 sums, and whether its stamp is `stamp`
+__device__ __forceinline__ bool load_entry(const float* __restrict__ part, int32_t p, uint32_t stamp, float* e) {
     const float4* a = reinterpret_cast<const float4*>(part + (size_t)p * kPartStride);
     const float4 x = a[0], y = a[1], z = a[2];
     e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w;
     e[4] = y.x; e[5] = y.y; e[6] = y.z; e[7] = y.w;
     e[8] = z.x;
-}
-
-__device__ __forceinline__ void add_entry(const float* __restrict__ part, int32_t p, float* v) {
-    float e[kPartFloats];
-    load_entry(part, p, e);
-#pragma unroll
-    for (int k = 0; k < kPartFloats; k++) v[k] += e[k];
+    return __float_as_uint(z.y) == stamp;
 }
 
 __device__ __forceinline__ void store_grad_record(float4* grads, size_t g, const float* v) {
@@ -712,80 +706,67 @@ __device__ __forceinline__ void store_grad_record(float4* grads, size_t g, const
     grads[3 * g + 2] = make_float4(v[6], v[7], v[8], 0.f);
 }
 
+constexpr int kGatherRound = 8;  // short ranges: entries loaded per round (independent loads)
+
 // One thread per position j of the depth order, for Gaussian order[j]: the sums of its (tile, Gaussian)
 // entries, which the emit placed at [cum[j-1], cum[j]), in emit order (its tiles in the order the
 // intersection emit visits them), into its gradient record {v_x, v_y, v_opacity, 0 | v_conic a, b, c,
-// 0 | v_r, v_g, v_b, 0}. Entries whose valid bit is clear (tiles that never reached the Gaussian) count
-// as zero; a Gaussian with none (exactly the untouched ones) gets no record: the postprocess reads zeros
-// for it. Ranges longer than kLongRange are queued for k_gather_long when touched (the queue's order does
-// not matter: each range is reduced on its own).
+// 0 | v_r, v_g, v_b, 0}. Entries without this step's stamp (tiles that never reached the Gaussian) count
+// as zero: an added +0 leaves every partial sum as it was (a sum that starts at +0 never becomes -0).
+// A Gaussian with no stamped entry (exactly the untouched ones) gets no record: the postprocess reads
+// zeros for it. (Loading a range's entries before its touched flag has arrived costs more than the wait:
+// at dense settings most short ranges belong to Gaussians no tile reached.) Ranges longer than
+// kLongRange are queued for k_gather_long when touched (the queue's order does not matter: each range is
+// reduced on its own).
 __global__ void __launch_bounds__(kThreads) k_gather_grads(int count, const int32_t* __restrict__ order,
                                                            const int64_t* __restrict__ cum,
                                                            const float* __restrict__ part,
-                                                           const uint32_t* __restrict__ valid,
+                                                           const uint32_t* __restrict__ stamp_p,
                                                            const uint8_t* __restrict__ touched,
                                                            float4* __restrict__ grads, int32_t* __restrict__ long_list,
                                                            int32_t* __restrict__ long_count) {
     const int j = blockIdx.x * kThreads + threadIdx.x;
     if (j >= count) return;
+    const uint32_t stamp = *stamp_p;
     const int32_t p1 = static_cast<int32_t>(cum[j]);
     const int32_t p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
-    if (p1 == p0) return;
     const int g = order[j];
+    if (p1 == p0) return;
+    const bool hit = touched[g] != 0;
     if (p1 - p0 > kLongRange) {
-        if (touched[g]) long_list[atomicAdd(long_count, 1)] = j;  // an untouched range has no valid entry
+        if (hit) long_list[atomicAdd(long_count, 1)] = j;  // an untouched range has no stamped entry
         return;
     }
-    // a short range spans at most three bit words: all three loads first, then the set bits in order
-    const int32_t w0 = p0 >> 5, w_last = (p1 - 1) >> 5;
-    uint32_t wb[3];
-#pragma unroll
-    for (int k = 0; k < 3; k++) {
-        const int32_t w = w0 + k;
-        uint32_t m = 0u;
-        if (w <= w_last) {
-            const int lo = w == w0 ? (p0 & 31) : 0, hi = w == w_last ? ((p1 - 1) & 31) : 31;
-            m = (0xFFFFFFFFu << lo) & (0xFFFFFFFFu >> (31 - hi));
-        }
-        wb[k] = m ? valid[w] & m : 0u;
-    }
-    if ((wb[0] | wb[1] | wb[2]) == 0u) return;  // untouched: no record (the postprocess reads zeros)
+    if (!hit) return;  // no stamped entry: no record
     float v[kPartFloats];
 #pragma unroll
     for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
+    for (int32_t p = p0; p < p1; p += kGatherRound) {
+        float e[kGatherRound][kPartFloats];
+        bool on[kGatherRound];
 #pragma unroll
-    for (int k = 0; k < 3; k++) {
-        uint32_t bits = wb[k];
-        while (bits) {  // two entries per round (independent loads)
-            const int b0 = __builtin_ctz(bits);
-            bits &= bits - 1u;
-            const int b1 = bits ? __builtin_ctz(bits) : -1;
-            if (bits) bits &= bits - 1u;
-            float e0[kPartFloats], e1[kPartFloats];
-            load_entry(part, ((w0 + k) << 5) + b0, e0);
-            load_entry(part, ((w0 + k) << 5) + (b1 < 0 ? b0 : b1), e1);
+        for (int i = 0; i < kGatherRound; i++) on[i] = load_entry(part, min(p + i, p1 - 1), stamp, e[i]) & (p + i < p1);
 #pragma unroll
-            for (int q = 0; q < kPartFloats; q++) {
-                v[q] += e0[q];
-                if (b1 >= 0) v[q] += e1[q];
-            }
-        }
+        for (int i = 0; i < kGatherRound; i++)
+#pragma unroll
+            for (int k = 0; k < kPartFloats; k++) v[k] += on[i] ? e[i][k] : 0.f;
     }
     store_grad_record(grads, static_cast<size_t>(g), v);
 }
 
-// The queued long ranges, one wave each, 64 entries per round (lane l takes entry base + l when its
-// valid bit is set); each round's 64 values are added in a fixed tree (DPP within rows, then across
+// The queued long ranges, one wave each, 64 entries per round (lane l takes entry base + l when it
+// carries the stamp); each round's 64 values are added in a fixed tree (DPP within rows, then across
 // rows) and the rounds in order.
 __global__ void __launch_bounds__(kThreads) k_gather_long(const int32_t* __restrict__ order,
                                                           const int64_t* __restrict__ cum,
                                                           const float* __restrict__ part,
-                                                          const uint32_t* __restrict__ valid,
+                                                          const uint32_t* __restrict__ stamp_p,
                                                           float4* __restrict__ grads,
                                                           const int32_t* __restrict__ long_list,
                                                           const int32_t* __restrict__ long_count) {
     const int lane = threadIdx.x & 63;
     const int n_long = *long_count;
+    const uint32_t stamp = *stamp_p;
     const int n_waves = gridDim.x * (kThreads / 64);
     for (int q = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); q < n_long; q += n_waves) {  // wave-uniform
         const int j = long_list[q];
@@ -796,14 +777,11 @@ __global__ void __launch_bounds__(kThreads) k_gather_long(const int32_t* __restr
         for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
         for (int32_t base = p0; base < p1; base += 64) {
             const int32_t p = base + lane;
-            const bool on = p < p1 && ((valid[p >> 5] >> (p & 31)) & 1u);
             float x[kPartFloats];
-#pragma unroll
-            for (int k = 0; k < kPartFloats; k++) x[k] = 0.f;
-            if (on) add_entry(part, p, x);
+            const bool on = load_entry(part, min(p, p1 - 1), stamp, x) & (p < p1);
 #pragma unroll
             for (int k = 0; k < kPartFloats; k++) {
-                float y = x[k];
+                float y = on ? x[k] : 0.f;
                 y += dpp_f<0xB1>(y);   // quad_perm(1,0,3,2)
                 y += dpp_f<0x4E>(y);   // quad_perm(2,3,0,1)
                 y += dpp_f<0x141>(y);  // row_half_mirror
@@ -818,22 +796,18 @@ __global__ void __launch_bounds__(kThreads) k_gather_long(const int32_t* __restr
 }
 }  // namespace
 
-void raster_clear_valid(uint32_t* valid, int64_t cap, const int64_t* n_isects_dev, uint8_t* touched, int rows,
-                        int32_t* long_count, hipStream_t s) {
-    const int64_t words = (cap + 31) / 32;
-    const int64_t need = std::max<int64_t>(words, rows);
-    const int blocks = static_cast<int>(std::min<int64_t>(std::max<int64_t>((need + kThreads - 1) / kThreads, 1), 4096));
-    hipLaunchKernelGGL(k_clear_valid, dim3(blocks), dim3(kThreads), 0, s, valid, words, n_isects_dev, touched, rows,
-                       long_count);
+void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long_count, hipStream_t s) {
+    const int blocks = std::min(std::max((rows + kThreads - 1) / kThreads, 1), 4096);
+    hipLaunchKernelGGL(k_bwd_begin, dim3(blocks), dim3(kThreads), 0, s, stamp, touched, rows, long_count);
 }
 
-void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part, const uint32_t* valid,
+void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part, const uint32_t* stamp,
                          const uint8_t* touched, float4* grads, int32_t* long_list, int32_t* long_count,
                          hipStream_t s) {
     if (count <= 0) return;
     hipLaunchKernelGGL(k_gather_grads, dim3((count + kThreads - 1) / kThreads), dim3(kThreads), 0, s, count, order, cum,
-                       part, valid, touched, grads, long_list, long_count);
-    hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, valid, grads, long_list,
+                       part, stamp, touched, grads, long_list, long_count);
+    hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, stamp, grads, long_list,
                        long_count);
 }
 

@@ -57,7 +57,7 @@ struct sxh_executor {
     sxh::DevBuf<int32_t> vals_a, vals_b;   // sorted: emit positions
     sxh::DevBuf<int32_t> emit_gid;         // the Gaussian of each emit position
     sxh::DevBuf<float> part;               // raster backward sums per emit position (kPartStride floats each)
-    sxh::DevBuf<uint32_t> valid;           // their valid bits
+    sxh::DevBuf<uint32_t> stamp;           // the current backward's stamp (one word; entries carry it)
     sxh::DevBuf<uint8_t> sort_scratch;
     // image-sized buffers
     size_t img_px = 0, img_tiles = 0, img_map = 0;
@@ -118,7 +118,8 @@ struct sxh_executor {
         vals_b.alloc(cap);
         emit_gid.alloc(cap);
         part.alloc(cap * sxk::kPartStride);
-        valid.alloc((cap + 31) / 32);
+        // zero stamps: no entry of the new buffer passes for one written this step (stamps are never 0)
+        SXH_HIP(hipMemsetAsync(part.p, 0, cap * sxk::kPartStride * sizeof(float), b->stream));
         // shared by the depth sort (rows keys) and the tile sort (intersections)
         sort_scratch.alloc(sxk::sort_scratch_bytes(static_cast<int64_t>(std::max<size_t>(cap, rows))));
         isect_cap = cap;

@@ -163,26 +163,25 @@ struct RasterBwdGrads {
     float* v_means2d_abs;
     float4* packed;  // when set: the resident-step record layout (3 x float4 per Gaussian)
     // when set (with RasterArgs::id_of): no atomics; the sums of each (tile, Gaussian) are stored at the
-    // intersection's emit position p (flatten_ids[idx]) as kPartFloats floats (stride kPartStride), bit p of `valid` and the
-    // Gaussian's `touched` flag are set (both cleared by the caller); raster_gather_grads then sums each
-    // Gaussian's entries in order
+    // intersection's emit position p (flatten_ids[idx]) as kPartFloats floats (stride kPartStride), with the
+    // step's stamp (*stamp) in float kPartFloats, and the Gaussian's `touched` flag is set (cleared by
+    // the caller); raster_gather_grads then sums each Gaussian's entries that carry the stamp, in order
     float* part;
-    uint32_t* valid;
+    const uint32_t* stamp;
     uint8_t* touched;  // with part: set for every Gaussian that got an entry (cleared by the caller)
 };
 constexpr int kPartFloats = 9;  // v_xy (2), v_opacity, v_conic (3), v_rgb (3)
-constexpr int kPartStride = 12;  // floats per `part` entry: three aligned float4 (the last 3 floats unused)
-// clears the bitmap words of the first *n_isects_dev (or cap) intersections, touched[0, rows) and the
-// gather's queue count
-void raster_clear_valid(uint32_t* valid, int64_t cap, const int64_t* n_isects_dev, uint8_t* touched, int rows,
-                        int32_t* long_count, hipStream_t s);
+constexpr int kPartStride = 12;  // floats per `part` entry: three aligned float4 (the stamp, 2 unused)
+// Before each backward in `part` mode: advances the stamp (never 0, the value of zeroed entries), clears
+// touched[0, rows) and the gather's queue count
+void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long_count, hipStream_t s);
 // For each Gaussian order[j] with touched set: grads[order[j]] (3 x float4 record) = the sum of the `part`
-// entries at [cum[j-1], cum[j]) whose valid bit is set (order and cum: the depth order and the inclusive
-// scan of its tile counts that placed the emit), in a fixed order per range: the deterministic end of
-// raster_bwd's `part` mode. Untouched Gaussians' records are not written. long_list holds `count` ints,
-// long_count one (reset by raster_clear_valid).
+// entries at [cum[j-1], cum[j]) that carry the current stamp (order and cum: the depth order and the
+// inclusive scan of its tile counts that placed the emit), in a fixed order per range: the
+// deterministic end of raster_bwd's `part` mode. Untouched Gaussians' records are not written. long_list
+// holds `count` ints, long_count one (reset by raster_bwd_begin).
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part,
-                         const uint32_t* valid, const uint8_t* touched, float4* grads, int32_t* long_list,
+                         const uint32_t* stamp, const uint8_t* touched, float4* grads, int32_t* long_list,
                          int32_t* long_count, hipStream_t s);
 void raster_bwd(const RasterArgs& a, const float* render_alphas, const int32_t* last_ids,
                 const float* v_render_colors, const float* v_render_alphas, const RasterBwdGrads& g,
