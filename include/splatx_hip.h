@@ -665,6 +665,16 @@ int32_t sxh_exec_get_raster_stats(sxh_executor* e, sxh_raster_stats* out);
  * captured hipGraph (default 1) or as direct launches (0). Profiling always launches directly. No
  * counterpart in the reference (its Metal command buffers are encoded per step). */
 int32_t sxh_exec_set_graph(sxh_executor* e, int32_t enable);
+/* How the step orders its intersections (both give the reference's per-tile (depth, index) order,
+ * bit for bit): SXH_ISECT_ORDER_DEPTH_FIRST sorts the Gaussians by depth, emits in that order and
+ * sorts the tile ids; SXH_ISECT_ORDER_INDEX_FIRST emits in index order, sorts the tile ids and then
+ * each tile's list by depth in LDS (cheaper while tiles hold at most a few thousand entries);
+ * SXH_ISECT_ORDER_AUTO (default) takes index-first once the previous step's largest tile held at
+ * most 4096 entries. No counterpart in the reference (a tuning choice of this backend). */
+#define SXH_ISECT_ORDER_AUTO 0
+#define SXH_ISECT_ORDER_DEPTH_FIRST 1
+#define SXH_ISECT_ORDER_INDEX_FIRST 2
+int32_t sxh_exec_set_isect_order(sxh_executor* e, int32_t mode);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -64,6 +64,7 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->long_list.alloc(R);
             e->long_count.alloc(1);
             e->stamp.alloc(1);
+            e->max_tile.alloc(1);
             SXH_HIP(hipMemsetAsync(e->stamp.p, 0, sizeof(uint32_t), b->stream));
             e->touched.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
@@ -91,8 +92,9 @@ void sxh_exec_destroy(sxh_executor* e) {
     (void)hipStreamSynchronize(e->b->stream);
     for (int k = 0; k < kMaxEvents; k++)
         if (e->ev[k]) (void)hipEventDestroy(e->ev[k]);
-    for (hipGraphExec_t x : e->graph_b)
-        if (x) (void)hipGraphExecDestroy(x);
+    for (auto& row : e->graph_b)
+        for (hipGraphExec_t x : row)
+            if (x) (void)hipGraphExecDestroy(x);
     delete e;
 }
 
@@ -173,6 +175,15 @@ int32_t sxh_exec_set_graph(sxh_executor* e, int32_t enable) {
     return guarded([&] {
         if (!e) invalid("TrainStepExecutor", "null executor");
         e->use_graph = enable != 0;
+    });
+}
+
+int32_t sxh_exec_set_isect_order(sxh_executor* e, int32_t mode) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor", "null executor");
+        if (mode < SXH_ISECT_ORDER_AUTO || mode > SXH_ISECT_ORDER_INDEX_FIRST)
+            invalid("TrainStepExecutor", "unknown intersection order");
+        e->isect_order = mode;
     });
 }
 
@@ -267,43 +278,67 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     *hloss = 0.0f;
     int n_l1 = 0, n_ss = 0;
     int32_t* flat = e->vals_a.p;
+    // index-first needs every tile's list in LDS (4096 entries) to be fast; larger tiles still sort
+    // correctly through global scratch
+    constexpr int64_t kIndexFirstMaxTile = 4096;
+    const bool index_first = e->isect_order == SXH_ISECT_ORDER_INDEX_FIRST ||
+                             (e->isect_order == SXH_ISECT_ORDER_AUTO && e->last_max_tile >= 0 &&
+                              e->last_max_tile <= kIndexFirstMaxTile);
 
     // ---- segment B: everything after the count. With n_dev the launches read the intersection count on
     // the device (grids sized for the capacity), so they can be captured before the count is known.
     auto launch_b = [&](int64_t n_host, const int64_t* n_dev) {
         const int n_tiles = tw * th;
-        // intersections depth first (the Gaussians sorted by depth, tile ids emitted in that order, a
-        // stable sort on the tile bits): the order of the reference's (tile | depth) key sort
-        sxk::step_depth_keys(c, e->splats.p, e->tiles.p, e->dkey_a.p, e->order_a.p, s);
-        const int wd = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, c.count, 32,
-                                       e->sort_scratch.p, s, true);
-        const int32_t* order = wd ? e->order_b.p : e->order_a.p;
-        e->mark("depth_sort");
+        // the order of the reference's (tile | depth) key sort, two ways. Depth first: the Gaussians
+        // sorted by depth, their tile ids emitted in that order, a stable sort on the tile bits. Index
+        // first: the tile ids emitted in index order, a stable sort on the tile bits, then each tile's
+        // list sorted by depth (order null: position j of the emit is Gaussian j).
+        const int32_t* order = nullptr;
+        if (!index_first) {
+            sxk::step_depth_keys(c, e->splats.p, e->tiles.p, e->dkey_a.p, e->order_a.p, s);
+            const int wd = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, c.count, 32,
+                                           e->sort_scratch.p, s, true);
+            order = wd ? e->order_b.p : e->order_a.p;
+            e->mark("depth_sort");
+        }
         sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s, order);
         e->mark("scan");
+        // index first: the emit also writes each entry's depth bits, into the upper half of keys_b (u64
+        // words; the tile sort's keys and the large tiles' scratch use the lower half of each key buffer)
+        uint32_t* const edepth =
+            index_first ? reinterpret_cast<uint32_t*>(e->keys_b.p) + e->isect_cap : nullptr;
         int which = 0;
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
             uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
-                                              e->sort_scratch.p, s, false, n_dev);
+                                              e->sort_scratch.p, s, index_first, n_dev);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         } else {
             uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
             uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
-                                              e->sort_scratch.p, s, false, n_dev);
+                                              e->sort_scratch.p, s, index_first, n_dev);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         }
         if (which < 0) throw std::runtime_error(std::string(what) + ": intersection capacity too large for a device count");
         flat = which ? e->vals_b.p : e->vals_a.p;
         e->mark("offsets");
+        sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev, e->max_tile.p);
+        if (index_first) {
+            // the sorted tile keys are spent (the offsets are built): both key buffers and the other
+            // value buffer are the scratch of tiles too large for LDS
+            sxk::tile_depth_sort(e->offsets.p, n_tiles, n_host, n_dev, e->tile_order.p, flat, edepth,
+                                 reinterpret_cast<uint32_t*>(e->keys_a.p), reinterpret_cast<uint32_t*>(e->keys_b.p),
+                                 which ? e->vals_a.p : e->vals_b.p, s);
+            e->mark("tile_depth_sort");
+        }
         sxk::RasterArgs ra{};
         ra.splats = e->splats.p;
         ra.offsets = e->offsets.p;
@@ -317,7 +352,6 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         ra.n_isects_dev = n_dev;
         ra.id_of = e->emit_gid.p;  // the sorted values are emit positions
         ra.stats = e->prof_stats ? e->rstats.p : nullptr;  // never in a captured graph (profiling launches directly)
-        sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev);
         ra.tile_order = e->tile_order.p;
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
         e->mark("raster_fwd");
@@ -367,7 +401,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             throw;
         }
         SXH_HIP(hipStreamEndCapture(s, &g));
-        hipGraphExec_t& x = e->graph_b[fwd_only ? 1 : 0];
+        hipGraphExec_t& x = e->graph_b[index_first ? 1 : 0][fwd_only ? 1 : 0];
         if (x) {
             hipGraphNode_t err_node = nullptr;
             hipGraphExecUpdateResult res{};
@@ -401,7 +435,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     if (grown) e->ensure_isect(static_cast<size_t>(n_isects));
     if (graph && e->isect_cap < (size_t{1} << 30)) {
         if (grown) capture_b();  // new buffers: the captured graph is stale
-        SXH_HIP(hipGraphLaunch(e->graph_b[fwd_only ? 1 : 0], s));
+        SXH_HIP(hipGraphLaunch(e->graph_b[index_first ? 1 : 0][fwd_only ? 1 : 0], s));
     } else {
         launch_b(n_isects, nullptr);
     }
@@ -409,6 +443,9 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     uint32_t* hsort = reinterpret_cast<uint32_t*>(&hs[4]);
     *hsort = 0;
     SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p), 4, hipMemcpyDeviceToHost, s));
+    uint32_t* hmax = reinterpret_cast<uint32_t*>(&hs[5]);
+    *hmax = 0;
+    SXH_HIP(hipMemcpyAsync(hmax, e->max_tile.p, 4, hipMemcpyDeviceToHost, s));
     if (render_to_dev)
         SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
     if (out->render_colors)
@@ -419,6 +456,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     SXH_HIP(hipStreamSynchronize(s));
     e->sync_ms[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     out->loss = fwd_only ? 0.0f : *hloss;
+    e->last_max_tile = n_isects > 0 ? static_cast<int64_t>(*hmax) : 0;
     if (e->prof_stats) {
         unsigned long long st[sxk::kRasterStats];
         SXH_HIP(hipMemcpy(st, e->rstats.p, sizeof(st), hipMemcpyDeviceToHost));

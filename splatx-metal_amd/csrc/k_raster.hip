@@ -730,7 +730,7 @@ __global__ void __launch_bounds__(kThreads) k_gather_grads(int count, const int3
     const uint32_t stamp = *stamp_p;
     const int32_t p1 = static_cast<int32_t>(cum[j]);
     const int32_t p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
-    const int g = order[j];
+    const int g = order ? order[j] : j;
     if (p1 == p0) return;
     const bool hit = touched[g] != 0;
     if (p1 - p0 > kLongRange) {
@@ -791,7 +791,7 @@ __global__ void __launch_bounds__(kThreads) k_gather_long(const int32_t* __restr
                 v[k] += y;
             }
         }
-        if (lane == 0) store_grad_record(grads, static_cast<size_t>(order[j]), v);
+        if (lane == 0) store_grad_record(grads, static_cast<size_t>(order ? order[j] : j), v);
     }
 }
 }  // namespace
@@ -830,7 +830,8 @@ __device__ __forceinline__ uint64_t same_byte_lanes(uint32_t b, bool valid) {
 
 __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__ offsets, int n_tiles,
                                                      int64_t n_isects, int32_t* __restrict__ order,
-                                                     const int64_t* __restrict__ n_isects_dev) {
+                                                     const int64_t* __restrict__ n_isects_dev,
+                                                     uint32_t* __restrict__ max_count) {
     __shared__ uint32_t s_hist[256];
     __shared__ uint32_t s_max;
     if (n_isects_dev) n_isects = *n_isects_dev;
@@ -850,6 +851,7 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
     __syncthreads();
     int shift = 0;
     while ((s_max >> shift) >= 256u) shift++;
+    if (max_count && t0 == 0) *max_count = s_max;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     // rounds are uniform over the workgroup (every thread runs ceil(n_tiles / 1024) of them)
     for (int t1 = 0; t1 < n_tiles; t1 += 1024) {
@@ -884,9 +886,10 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
 }  // namespace
 
 void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s,
-                       const int64_t* n_isects_dev) {
+                       const int64_t* n_isects_dev, uint32_t* max_count) {
     if (n_tiles <= 0) return;
-    hipLaunchKernelGGL(k_tile_order, dim3(1), dim3(1024), 0, s, offsets, n_tiles, n_isects, order, n_isects_dev);
+    hipLaunchKernelGGL(k_tile_order, dim3(1), dim3(1024), 0, s, offsets, n_tiles, n_isects, order, n_isects_dev,
+                       max_count);
 }
 
 void raster_fwd(const RasterArgs& a, float* rgb, float* alpha, int32_t* last, hipStream_t s) {

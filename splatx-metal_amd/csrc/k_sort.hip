@@ -895,6 +895,242 @@ int radix_sort_ab(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_
     return passes < 0 ? -1 : (passes & 1);
 }
 
+// ---- the depth order within each tile (index-first intersections) --------------------------------
+// When the Gaussians emit in index order, a stable sort on the tile ids leaves each tile's entries in
+// index order; sorting them stably by the depth bits of their Gaussians (which the emit stored per
+// entry) then gives the order of the reference's (tile | depth) keys: depth, ties by index. One
+// workgroup per tile. A tile of at most kTile entries is sorted in LDS by 8-bit LSD passes, wave w
+// holding the w-th quarter of the list (in whole 64-key rounds) in registers and ranking with match
+// masks as the onesweep pass does; bytes on which every key of the tile agrees are skipped. A larger
+// tile runs the same passes through global scratch, a chunk of kTile keys at a time in list order.
+__device__ __forceinline__ uint32_t wave_and_u32(uint32_t x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x &= static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), o, 64));
+    return x;
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), o, 64));
+    return x;
+}
+
+// The bits in which the keys of the workgroup differ (AND and OR of each thread's `a` / `o`).
+__device__ __forceinline__ uint32_t block_key_diff(uint32_t a, uint32_t o, uint32_t* s_and, uint32_t* s_or) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    a = wave_and_u32(a);
+    o = wave_or_u32(o);
+    if (lane == 0) {
+        s_and[wave] = a;
+        s_or[wave] = o;
+    }
+    __syncthreads();
+    uint32_t A = ~0u, O = 0u;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+        A &= s_and[w];
+        O |= s_or[w];
+    }
+    return A ^ O;
+}
+
+// Ranks the wave's keys (rounds r < R, key index wave_base + 64 r + lane below `count`) by the byte at
+// `shift`: off[r] = the key's place among the wave's keys of that digit (earlier rounds, then lower
+// lanes); woff receives the wave's digit counts (zeroed by the caller).
+template <int RMAX>
+__device__ __forceinline__ void wave_rank_byte(const uint32_t* key, int R, int wave_base, int count, int shift,
+                                               uint32_t* woff, uint32_t* off) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int r = 0; r < RMAX; r++) {
+        if (r >= R) break;  // uniform
+        const bool valid = wave_base + r * 64 + lane < count;
+        const uint32_t x = key[r] >> shift;
+        const uint32_t d = x & 255u;
+        const uint64_t match = digit_match_bits<8>(x, __ballot(valid));
+        const uint32_t rank = lanes_below_count(match);
+        const uint32_t prior = valid ? woff[d] : 0u;
+        __builtin_amdgcn_wave_barrier();
+        if (valid && rank == 0u) woff[d] = prior + static_cast<uint32_t>(__popcll(match));
+        __builtin_amdgcn_wave_barrier();
+        off[r] = prior + rank;
+    }
+}
+
+// thread = digit: the waves' counts of digit tid become their first output places, from `base` on;
+// returns base + the digit's count
+__device__ __forceinline__ uint32_t wave_starts(uint32_t (*s_woff)[kBins], uint32_t base) {
+    const int tid = threadIdx.x;
+    uint32_t run = base;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+        const uint32_t c = s_woff[w][tid];
+        s_woff[w][tid] = run;
+        run += c;
+    }
+    return run;
+}
+
+// RMAX: rounds of 64 keys per wave that the kernel holds in registers; the small instance (RMAX 4)
+// takes the tiles of 2 to 1024 entries at twice the occupancy, the full one (RMAX = kRounds) the
+// larger ones. Every instance is launched over all tiles and leaves the others alone.
+template <int RMAX>
+__global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles,
+                                                              int32_t n_isects, const int64_t* __restrict__ n_dev,
+                                                              const int32_t* __restrict__ tile_order,
+                                                              int32_t* __restrict__ vals,
+                                                              const uint32_t* __restrict__ edepth,
+                                                              uint32_t* __restrict__ sk0, uint32_t* __restrict__ sk1,
+                                                              int32_t* __restrict__ sv) {
+    constexpr int kCap = kWaves * 64 * RMAX;
+    constexpr bool kFull = RMAX == kRounds;
+    constexpr int kSmallCap = kWaves * 64 * 4;
+    __shared__ uint32_t s_key[kCap];
+    __shared__ int32_t s_val[kCap];
+    __shared__ uint32_t s_woff[kWaves][kBins];
+    __shared__ uint32_t s_base[kFull ? kBins : 1];
+    __shared__ uint32_t s_wave[kWaves];
+    __shared__ uint32_t s_and[kWaves], s_or[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = tile_order ? tile_order[blockIdx.x] : static_cast<int>(blockIdx.x);
+    const int32_t n_all = n_dev ? static_cast<int32_t>(*n_dev) : n_isects;
+    const int32_t start = offsets[t];
+    const int32_t nt = (t + 1 < n_tiles ? offsets[t + 1] : n_all) - start;
+    if (nt <= 1 || (kFull ? nt <= kSmallCap : nt > kCap)) return;  // uniform: another instance's tile
+    int32_t* const seg = vals + start;
+    uint32_t key[RMAX];
+    int32_t val[RMAX];
+    uint32_t off[RMAX];
+    if (nt <= kCap) {
+        // wave w holds list entries [w Q, w Q + Q), Q a whole number of 64-entry rounds
+        const int Q = ((nt + kWaves - 1) / kWaves + 63) & ~63;
+        const int R = Q >> 6;
+        const int wb = wave * Q;
+#pragma unroll
+        for (int r = 0; r < RMAX; r++) {
+            const int i = wb + r * 64 + lane;
+            val[r] = (r < R && i < nt) ? seg[i] : 0;
+        }
+        uint32_t a = ~0u, o = 0u;
+#pragma unroll
+        for (int r = 0; r < RMAX; r++) {
+            const bool valid = r < R && wb + r * 64 + lane < nt;
+            key[r] = valid ? edepth[val[r]] : 0u;
+            if (valid) {
+                a &= key[r];
+                o |= key[r];
+            }
+        }
+        const uint32_t diff = block_key_diff(a, o, s_and, s_or);
+        if (diff == 0u) return;  // one depth: the index order stands
+        for (int p = 0; p < 4; p++) {
+            const int shift = 8 * p;
+            if (((diff >> shift) & 255u) == 0u) continue;  // uniform: every key has this byte
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
+            __syncthreads();
+            wave_rank_byte<RMAX>(key, R, wb, nt, shift, s_woff[wave], off);
+            __syncthreads();
+            {
+                uint32_t tot = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) tot += s_woff[w][tid];
+                uint32_t all = 0;
+                (void)wave_starts(s_woff, block_excl_scan_u32(tot, s_wave, &all));
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < RMAX; r++) {
+                if (r < R && wb + r * 64 + lane < nt) {
+                    const uint32_t pos = s_woff[wave][(key[r] >> shift) & 255u] + off[r];
+                    s_key[pos] = key[r];
+                    s_val[pos] = val[r];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < RMAX; r++) {
+                const int i = wb + r * 64 + lane;
+                if (r < R && i < nt) {
+                    key[r] = s_key[i];
+                    val[r] = s_val[i];
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int r = 0; r < RMAX; r++) {
+            const int i = wb + r * 64 + lane;
+            if (r < R && i < nt) seg[i] = val[r];
+        }
+        return;
+    }
+    if constexpr (kFull) {
+        // a tile of more than kTile entries: the keys go to sk0, then each pass moves (key, value) between
+        // (sk0, vals) and (sk1, sv) over the tile's range, chunk by chunk in list order
+        uint32_t a = ~0u, o = 0u;
+        for (int32_t i = tid; i < nt; i += kThreads) {
+            const uint32_t k = edepth[seg[i]];
+            sk0[start + i] = k;
+            a &= k;
+            o |= k;
+        }
+        const uint32_t diff = block_key_diff(a, o, s_and, s_or);  // (its barrier also orders the sk0 stores)
+        const uint32_t* src_k = sk0 + start;
+        const int32_t* src_v = seg;
+        uint32_t* dst_k = sk1 + start;
+        int32_t* dst_v = sv + start;
+        constexpr int kPerWave = kTile / kWaves;
+        for (int p = 0; p < 4; p++) {
+            const int shift = 8 * p;
+            if (((diff >> shift) & 255u) == 0u) continue;  // uniform
+            s_base[tid] = 0;
+            __syncthreads();
+            for (int32_t i = tid; i < nt; i += kThreads) atomicAdd(&s_base[(src_k[i] >> shift) & 255u], 1u);
+            __syncthreads();
+            {
+                uint32_t all = 0;
+                const uint32_t b = block_excl_scan_u32(s_base[tid], s_wave, &all);
+                s_base[tid] = b;  // every thread has read its own digit's count above
+            }
+            __syncthreads();
+            for (int32_t c0 = 0; c0 < nt; c0 += kTile) {  // uniform
+                const int cn = static_cast<int>(min<int32_t>(kTile, nt - c0));
+                const int wb = wave * kPerWave;
+#pragma unroll
+                for (int r = 0; r < kRounds; r++) {
+                    const int i = wb + r * 64 + lane;
+                    key[r] = i < cn ? src_k[c0 + i] : 0u;
+                    val[r] = i < cn ? src_v[c0 + i] : 0;
+                }
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
+                __syncthreads();
+                wave_rank_byte<kRounds>(key, kRounds, wb, cn, shift, s_woff[wave], off);
+                __syncthreads();
+                s_base[tid] = wave_starts(s_woff, s_base[tid]);
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < kRounds; r++) {
+                    if (wb + r * 64 + lane < cn) {
+                        const uint32_t pos = s_woff[wave][(key[r] >> shift) & 255u] + off[r];
+                        dst_k[pos] = key[r];
+                        dst_v[pos] = val[r];
+                    }
+                }
+                __syncthreads();  // s_woff is cleared for the next chunk; the next pass reads these stores
+            }
+            const uint32_t* tk = src_k;
+            src_k = dst_k;
+            dst_k = const_cast<uint32_t*>(tk);
+            const int32_t* tv = src_v;
+            src_v = dst_v;
+            dst_v = const_cast<int32_t*>(tv);
+        }
+        if (src_v != seg)
+            for (int32_t i = tid; i < nt; i += kThreads) seg[i] = src_v[i];
+    }
+}
+
 } // namespace
 
 size_t sort_scratch_bytes(int64_t n) {
@@ -929,6 +1165,18 @@ int radix_sort_positions(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, in
 int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
                          uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
     return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true);
+}
+
+void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
+                     const int32_t* tile_order, int32_t* vals, const uint32_t* edepth, uint32_t* scratch_k0,
+                     uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s) {
+    if (n_tiles <= 0 || (!n_dev && n_isects <= 1)) return;
+    hipLaunchKernelGGL(k_tile_depth_sort<kRounds>, dim3(n_tiles), dim3(kThreads), 0, s, offsets, n_tiles,
+                       static_cast<int32_t>(n_isects), n_dev, tile_order, vals, edepth, scratch_k0, scratch_k1,
+                       scratch_v);
+    hipLaunchKernelGGL(k_tile_depth_sort<4>, dim3(n_tiles), dim3(kThreads), 0, s, offsets, n_tiles,
+                       static_cast<int32_t>(n_isects), n_dev, tile_order, vals, edepth, scratch_k0, scratch_k1,
+                       scratch_v);
 }
 
 void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_out, int32_t* vals_out,

@@ -189,8 +189,9 @@ __global__ void __launch_bounds__(kBlock) k_depth_keys(StepConst c, const float4
     vals[i] = i;
 }
 
-// Thread per position j of the depth order: Gaussian g = order[j] owns the output range
-// [cum[j-1], cum[j]) and fills it with its tile ids in the reference's emit order, value g. A wave
+// Thread per position j of the depth order (of the index order when order is null): Gaussian g =
+// order[j] owns the output range [cum[j-1], cum[j]) and fills it with its tile ids in the
+// reference's emit order, value g. A wave
 // works as a queue over the lines of its 64 Gaussians: each lane sets up its own Gaussian's sweep
 // (kept in LDS) and counts its lines; the wave then takes the lines of all 64 Gaussians 64 at a
 // time, lane l evaluating one line (its cuts are a function of the line alone), and writes the
@@ -228,10 +229,11 @@ struct EmitWave {
     int is_y[64];
     int line0[65];    // exclusive scan of the slots' line counts
     int g[64];
+    uint32_t dbits[64];  // the Gaussian's depth bits (for the per-entry depths of index-first emits)
     long long out0[64], end[64], first[64];  // output range; wave entry index of the slot's first line
     int estart[65];   // the chunk's lines: exclusive scan of their tile counts
     int4 lin0[64];    // output position of the line's first tile (lo, hi), first tile id, id stride
-    int4 lin1[64];    // Gaussian, end of its output range (lo, hi)
+    int4 lin1[64];    // Gaussian, end of its output range (lo, hi), depth bits
 };
 
 // Upper cut of sweep line u: the cut at the line's far edge (u + 1) ts while that edge is <= bbox_max.x,
@@ -249,7 +251,7 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
                                                         const int32_t* __restrict__ radii,
                                                         const int32_t* __restrict__ order,
                                                         const int64_t* __restrict__ cum, K* __restrict__ keys,
-                                                        int32_t* __restrict__ vals) {
+                                                        int32_t* __restrict__ vals, uint32_t* __restrict__ edepth) {
     __shared__ EmitWave s_w[kBlock / 64];
     const int j = blockIdx.x * kBlock + threadIdx.x;
     const int lane = threadIdx.x & 63;
@@ -258,19 +260,22 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
     // this lane's Gaussian: its sweep and line count
     int64_t my0 = 0, cnt = 0;
     int g = 0, n_lines = 0;
+    uint32_t dbits = 0;
     sxd::AccuSweep sw = {};
     if (j < c.count) {
         my0 = j == 0 ? 0 : cum[j - 1];
         cnt = cum[j] - my0;
         if (cnt > 0 && cnt <= kEmitLaneMax) {
-            g = order[j];
+            g = order ? order[j] : j;
             const float4 s0 = splats[3 * (size_t)g];
+            dbits = __float_as_uint(s0.w);
             int64_t cur = my0;
             const int64_t end = my0 + cnt;
             auto line = [&](int32_t u, int32_t vmin, int32_t vmax, bool row_major) {
                 for (int32_t v = vmin; v < vmax && cur < end; ++v, ++cur) {
                     keys[cur] = static_cast<K>(row_major ? u * tw + v : v * tw + u);
                     vals[cur] = g;
+                    if (edepth) edepth[cur] = dbits;
                 }
                 return true;
             };
@@ -283,8 +288,9 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
                 for (int32_t y = r.min_y; y < r.max_y; y++) line(y, r.min_x, r.max_x, true);
             }
         } else if (cnt > 0) {
-            g = order[j];
+            g = order ? order[j] : j;
             const float4 s0 = splats[3 * (size_t)g];
+            dbits = __float_as_uint(s0.w);
             if (c.accutile) {
                 const float4 s1 = splats[3 * (size_t)g + 1];
                 if (sxd::accutile_setup(s1.x, s1.y, s1.z, s0.z, s0.x, s0.y, 16.0f, tw, c.tile_height, sw))
@@ -307,6 +313,7 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
                                __int_as_float(sw.rect_max_y));
     W.is_y[lane] = sw.isY ? 1 : 0;
     W.g[lane] = g;
+    W.dbits[lane] = dbits;
     W.out0[lane] = my0;
     W.end[lane] = my0 + cnt;
     const int lincl = wave_incl_scan(n_lines);
@@ -364,7 +371,8 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
             const long long lbase = W.out0[k] + (ebase + estart - W.first[k]);
             const long long lend = W.end[k];
             W.lin0[lane] = make_int4(static_cast<int>(lbase), static_cast<int>(lbase >> 32), key0, stride);
-            W.lin1[lane] = make_int4(W.g[k], static_cast<int>(lend), static_cast<int>(lend >> 32), 0);
+            W.lin1[lane] = make_int4(W.g[k], static_cast<int>(lend), static_cast<int>(lend >> 32),
+                                     static_cast<int>(W.dbits[k]));
         }
         __builtin_amdgcn_wave_barrier();
         for (int e = lane; e < chunk_total; e += 64) {
@@ -376,6 +384,7 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
             if (pos < end) {
                 keys[pos] = static_cast<K>(a.z + i * a.w);
                 vals[pos] = b.x;
+                if (edepth) edepth[pos] = static_cast<uint32_t>(b.w);
             }
         }
         __builtin_amdgcn_wave_barrier();  // every lane is done with this chunk's lines
@@ -663,17 +672,17 @@ void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* ti
 }
 
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s) {
+                      const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth) {
     if (c.count <= 0) return;
     hipLaunchKernelGGL(k_emit_sorted<uint16_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
-                       cum, keys, vals);
+                       cum, keys, vals, edepth);
 }
 
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s) {
+                      const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth) {
     if (c.count <= 0) return;
     hipLaunchKernelGGL(k_emit_sorted<uint32_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
-                       cum, keys, vals);
+                       cum, keys, vals, edepth);
 }
 
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,

@@ -78,9 +78,12 @@ struct sxh_executor {
     sxh::DevBuf<double> mc_cdf, mc_total;
     sxh::DevBuf<uint64_t> mc_raw, mc_mt;
     sxh::DevBuf<uint8_t> mc_cdf_scratch;
-    // segment B of the step as executable graphs: [0] training step, [1] forward only
-    hipGraphExec_t graph_b[2] = {nullptr, nullptr};
+    // segment B of the step as executable graphs: [index-first][0 training step, 1 forward only]
+    hipGraphExec_t graph_b[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
     bool use_graph = true;
+    int isect_order = SXH_ISECT_ORDER_AUTO;
+    int64_t last_max_tile = -1;      // the largest tile's entry count in the previous step (-1: none yet)
+    sxh::DevBuf<uint32_t> max_tile;  // written by the step's tile order
     // profiling: per-kernel events (bit 0), raster pair counts (bit 1)
     bool prof = false;
     bool prof_stats = false;

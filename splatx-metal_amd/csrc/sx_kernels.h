@@ -100,6 +100,15 @@ void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_o
 // broken invariant, never expected). A sort with clear_err zeroes it first; one without adds to
 // what the sorts before it left, so several sorts in a row can be checked with one read.
 uint32_t* sort_error_flag(void* scratch);
+// Index-first intersections: each tile's range [offsets[t], offsets[t+1]) of `vals` (emit positions,
+// in Gaussian index order after a stable tile sort) is sorted stably by edepth[p] (the depth bits of
+// the entry's Gaussian), in place: the (depth, index) order within each tile. The count is *n_dev
+// when set, else n_isects; tile_order (optional) is the order the workgroups take the tiles in.
+// Tiles of more than 4096 entries pass through scratch_k0 / scratch_k1 / scratch_v (each indexed like
+// vals, at least the count long).
+void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
+                     const int32_t* tile_order, int32_t* vals, const uint32_t* edepth, uint32_t* scratch_k0,
+                     uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s);
 
 // offsets[I*n_tiles] from sorted keys; n_isects > 0.
 // key_shift: position of the (image, tile) id in the key (32 for the isect_tiles encoding)
@@ -148,9 +157,10 @@ enum RasterStat : int {
     kRasterStats = 8
 };
 // tile_order for raster_fwd/raster_bwd: the n_tiles tile ids by descending intersection count
-// (counting sort on 256 buckets of the count; order within a bucket unspecified)
+// (counting sort on 256 buckets of the count; order within a bucket unspecified); max_count
+// (optional) receives the largest count
 void raster_tile_order(const int32_t* offsets, int n_tiles, int64_t n_isects, int32_t* order, hipStream_t s,
-                       const int64_t* n_isects_dev = nullptr);
+                       const int64_t* n_isects_dev = nullptr, uint32_t* max_count = nullptr);
 void raster_fwd(const RasterArgs& a, float* render_colors, float* render_alphas, int32_t* last_ids,
                 hipStream_t s);
 // Gradient outputs zeroed by the caller; packed as 3 x float4 per Gaussian when `packed_grads`
@@ -175,7 +185,7 @@ constexpr int kPartStride = 12;  // floats per `part` entry: three aligned float
 // Before each backward in `part` mode: advances the stamp (never 0, the value of zeroed entries), clears
 // touched[0, rows) and the gather's queue count
 void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long_count, hipStream_t s);
-// For each Gaussian order[j] with touched set: grads[order[j]] (3 x float4 record) = the sum of the `part`
+// For each Gaussian order[j] (j itself when order is null) with touched set: grads[order[j]] (3 x float4 record) = the sum of the `part`
 // entries at [cum[j-1], cum[j]) that carry the current stamp (order and cum: the depth order and the
 // inclusive scan of its tile counts that placed the emit), in a fixed order per range: the
 // deterministic end of raster_bwd's `part` mode. Untouched Gaussians' records are not written. long_list

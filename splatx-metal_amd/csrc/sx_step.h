@@ -53,13 +53,15 @@ int step_preprocess_blocks(int64_t count);
 // depth-first intersections: depth keys of the Gaussians that emit (values = index) for a stable
 // 32-bit sort; then, over that order, each Gaussian's tile ids at [cum[j-1], cum[j]) (cum =
 // inclusive scan of the tile counts gathered through the order); after a stable sort of the tile
-// ids, offsets[t] = lower bound of t
+// ids, offsets[t] = lower bound of t. Index-first: order null (position j is Gaussian j), cum the
+// plain scan of the tile counts, and the depth order within each tile comes after the tile sort
+// (tile_depth_sort), which reads each entry's depth bits from edepth (written by the emit when set)
 void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* tiles, uint32_t* keys, int32_t* vals,
                      hipStream_t s);
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s);
+                      const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth = nullptr);
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s);
+                      const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth = nullptr);
 // n_dev: the key count on the device, read instead of n
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev = nullptr);

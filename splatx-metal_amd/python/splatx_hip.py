@@ -28,6 +28,9 @@ SXH_ERR_RUNTIME = 2
 SXH_ERR_CAPACITY = 3
 SXH_ISECT_ACCUTILE = 0
 SXH_ISECT_AABB = 1
+SXH_ISECT_ORDER_AUTO = 0
+SXH_ISECT_ORDER_DEPTH_FIRST = 1
+SXH_ISECT_ORDER_INDEX_FIRST = 2
 
 
 class SxInvalidArgument(ValueError):
@@ -765,7 +768,7 @@ class Executor:
         self.h = h
         for n in ("sxh_exec_upload", "sxh_exec_download", "sxh_exec_step", "sxh_exec_set_gt_cache",
                   "sxh_exec_render_to_gt_cache", "sxh_exec_set_profiling", "sxh_exec_get_timing", "sxh_exec_set_graph",
-                  "sxh_exec_mcmc_refine"):
+                  "sxh_exec_set_isect_order", "sxh_exec_mcmc_refine"):
             getattr(self.lib, n).restype = C.c_int32
         self.lib.sxh_exec_destroy.argtypes = [C.c_void_p]
 
@@ -967,6 +970,11 @@ class Executor:
     def set_graph(self, enable: bool):
         """Run the step's second segment as a captured hipGraph (default) or as direct launches."""
         self._check(self.lib.sxh_exec_set_graph(self.h, int(bool(enable))))
+
+    def set_isect_order(self, mode: int):
+        """SXH_ISECT_ORDER_AUTO (default), _DEPTH_FIRST or _INDEX_FIRST: how the step
+        builds each tile's (depth, index)-ordered intersection list (the same lists either way)."""
+        self._check(self.lib.sxh_exec_set_isect_order(self.h, int(mode)))
 
     def get_timing(self):
         t = ExecTiming()

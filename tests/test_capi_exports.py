@@ -41,7 +41,7 @@ def test_abi_version_without_gpu():
 def test_executor_switches_reject_a_null_executor_without_gpu():
     lib = ctypes.CDLL(LIB)
     lib.sxh_last_error.restype = ctypes.c_char_p
-    for name in ("sxh_exec_set_graph", "sxh_exec_set_profiling"):
+    for name in ("sxh_exec_set_graph", "sxh_exec_set_profiling", "sxh_exec_set_isect_order"):
         f = getattr(lib, name)
         f.restype = ctypes.c_int32
         f.argtypes = [ctypes.c_void_p, ctypes.c_int32]
