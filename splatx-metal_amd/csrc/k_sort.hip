@@ -971,8 +971,10 @@ __device__ __forceinline__ uint32_t wave_starts(uint32_t (*s_woff)[kBins], uint3
 }
 
 // RMAX: rounds of 64 keys per wave that the kernel holds in registers; the small instance (RMAX 4)
-// takes the tiles of 2 to 1024 entries at twice the occupancy, the full one (RMAX = kRounds) the
-// larger ones. Every instance is launched over all tiles and leaves the others alone.
+// takes the tiles of 2 to 1024 entries at twice the occupancy, in tile order (one load less before
+// its list), the full one (RMAX = kRounds) the larger ones, heaviest first. Every instance is
+// launched over all tiles and leaves the others alone. (One wave per small tile, with no workgroup
+// barriers, measured slower: its ranking rounds wait on LDS one after another.)
 template <int RMAX>
 __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles,
                                                               int32_t n_isects, const int64_t* __restrict__ n_dev,
@@ -991,7 +993,7 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
     __shared__ uint32_t s_wave[kWaves];
     __shared__ uint32_t s_and[kWaves], s_or[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = tile_order ? tile_order[blockIdx.x] : static_cast<int>(blockIdx.x);
+    const int t = (tile_order && kFull) ? tile_order[blockIdx.x] : static_cast<int>(blockIdx.x);
     const int32_t n_all = n_dev ? static_cast<int32_t>(*n_dev) : n_isects;
     const int32_t start = offsets[t];
     const int32_t nt = (t + 1 < n_tiles ? offsets[t + 1] : n_all) - start;
