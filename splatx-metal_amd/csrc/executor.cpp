@@ -72,8 +72,10 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->dkey_b.alloc(R);
             e->order_a.alloc(R);
             e->order_b.alloc(R);
-            e->n_vis.alloc(2);
-            e->vis_part.alloc(2 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
+            e->n_vis.alloc(4);
+            e->vis_part.alloc(4 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
+            e->blk_base.alloc(2 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
+            e->emit_list.alloc(R);
             e->loss_dev.alloc(1);
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
@@ -258,7 +260,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     // ---- segment A: preprocess + counts -----------------------------------------------------------
     if (e->prof_stats) SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
     e->mark("start");
-    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, s);
+    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p, s);
     e->mark("preprocess");
     int64_t* hs = static_cast<int64_t*>(e->host_small.p);
     // visible count, intersection total
@@ -293,15 +295,20 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         // sorted by depth, their tile ids emitted in that order, a stable sort on the tile bits. Index
         // first: the tile ids emitted in index order, a stable sort on the tile bits, then each tile's
         // list sorted by depth (order null: position j of the emit is Gaussian j).
-        const int32_t* order = nullptr;
+        // positions of the emit: the Gaussians with tiles (*n_emit of them), compacted in index order
+        const unsigned long long* n_emit = e->n_vis.p + 2;
+        const int64_t* n_emit_i = reinterpret_cast<const int64_t*>(n_emit);
+        sxk::step_emit_compact(c, e->tiles.p, e->blk_base.p, e->emit_list.p, index_first ? e->cum.p : nullptr, s);
+        const int32_t* order = e->emit_list.p;
         if (!index_first) {
-            sxk::step_depth_keys(c, e->splats.p, e->tiles.p, e->dkey_a.p, e->order_a.p, s);
+            sxk::step_depth_keys(c, e->splats.p, e->emit_list.p, n_emit, e->dkey_a.p, e->order_a.p, s);
             const int wd = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, c.count, 32,
-                                           e->sort_scratch.p, s, true);
+                                           e->sort_scratch.p, s, true, n_emit_i);
+            if (wd < 0) throw std::runtime_error(std::string(what) + ": arena too large for a device-count depth sort");
             order = wd ? e->order_b.p : e->order_a.p;
             e->mark("depth_sort");
+            sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s, order, n_emit_i);
         }
-        sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s, order);
         e->mark("scan");
         // index first: the emit also writes each entry's depth bits, into the upper half of keys_b (u64
         // words; the tile sort's keys and the large tiles' scratch use the lower half of each key buffer)
@@ -311,7 +318,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
             uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s, edepth);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev);
@@ -320,7 +327,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         } else {
             uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
             uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, ka, e->emit_gid.p, s, edepth);
+            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev);
@@ -378,7 +385,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
         e->mark("raster_bwd");
         sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
-                                 e->long_list.p, e->long_count.p, s);
+                                 e->long_list.p, e->long_count.p, s, n_emit_i);
         e->mark("gather");
         sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s);
         e->mark("postprocess");

@@ -312,8 +312,9 @@ __device__ inline int64_t block_exclusive_scan_i64(int64_t v, int64_t* s_wave, i
 
 __global__ void __launch_bounds__(kBlock) k_scan_sums(const int32_t* __restrict__ in,
                                                       const int32_t* __restrict__ gather, int64_t n,
-                                                      int64_t* __restrict__ sums) {
+                                                      int64_t* __restrict__ sums, const int64_t* __restrict__ n_dev) {
     __shared__ int64_t s_wave[kBlock / 64];
+    if (n_dev) n = *n_dev;
     const int64_t base = blockIdx.x * (int64_t)kScanTile;
     int64_t acc = 0;
 #pragma unroll
@@ -328,9 +329,11 @@ __global__ void __launch_bounds__(kBlock) k_scan_sums(const int32_t* __restrict_
 
 __global__ void __launch_bounds__(kBlock) k_scan_tiles(const int32_t* __restrict__ in,
                                                        const int32_t* __restrict__ gather, int64_t n,
-                                                       const int64_t* __restrict__ sums, int64_t* __restrict__ out) {
+                                                       const int64_t* __restrict__ sums, int64_t* __restrict__ out,
+                                                       const int64_t* __restrict__ n_dev) {
     __shared__ int64_t s_wave[kBlock / 64];
     __shared__ int64_t s_prefix;
+    if (n_dev) n = *n_dev;
     // prefix of the preceding blocks
     int64_t p = 0;
     for (int b = threadIdx.x; b < static_cast<int>(blockIdx.x); b += kBlock) p += sums[b];
@@ -498,12 +501,13 @@ void isect_emit(const IsectArgs& a, const int64_t* cum, uint64_t* keys, int32_t*
 
 size_t scan_scratch_bytes(int64_t n) { return sizeof(int64_t) * (size_t)std::max<int64_t>(1, grid_for(n, kScanTile)); }
 
-void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s, const int32_t* gather) {
+void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s, const int32_t* gather,
+                  const int64_t* n_dev) {
     if (n <= 0) return;
     const int nb = grid_for(n, kScanTile);
     int64_t* sums = static_cast<int64_t*>(scratch);
-    hipLaunchKernelGGL(k_scan_sums, dim3(nb), dim3(kBlock), 0, s, in, gather, n, sums);
-    hipLaunchKernelGGL(k_scan_tiles, dim3(nb), dim3(kBlock), 0, s, in, gather, n, sums, out);
+    hipLaunchKernelGGL(k_scan_sums, dim3(nb), dim3(kBlock), 0, s, in, gather, n, sums, n_dev);
+    hipLaunchKernelGGL(k_scan_tiles, dim3(nb), dim3(kBlock), 0, s, in, gather, n, sums, out, n_dev);
 }
 
 void offset_encode(const uint64_t* keys, int64_t n, int I, int n_tiles, uint32_t tile_n_bits, int32_t* off,

@@ -724,9 +724,10 @@ __global__ void __launch_bounds__(kThreads) k_gather_grads(int count, const int3
                                                            const uint32_t* __restrict__ stamp_p,
                                                            const uint8_t* __restrict__ touched,
                                                            float4* __restrict__ grads, int32_t* __restrict__ long_list,
-                                                           int32_t* __restrict__ long_count) {
+                                                           int32_t* __restrict__ long_count,
+                                                           const int64_t* __restrict__ count_dev) {
     const int j = blockIdx.x * kThreads + threadIdx.x;
-    if (j >= count) return;
+    if (j >= (count_dev ? static_cast<int>(*count_dev) : count)) return;
     const uint32_t stamp = *stamp_p;
     const int32_t p1 = static_cast<int32_t>(cum[j]);
     const int32_t p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
@@ -803,10 +804,10 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part, const uint32_t* stamp,
                          const uint8_t* touched, float4* grads, int32_t* long_list, int32_t* long_count,
-                         hipStream_t s) {
+                         hipStream_t s, const int64_t* count_dev) {
     if (count <= 0) return;
     hipLaunchKernelGGL(k_gather_grads, dim3((count + kThreads - 1) / kThreads), dim3(kThreads), 0, s, count, order, cum,
-                       part, stamp, touched, grads, long_list, long_count);
+                       part, stamp, touched, grads, long_list, long_count, count_dev);
     hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, stamp, grads, long_list,
                        long_count);
 }

@@ -63,7 +63,7 @@ template <int NC>
 __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, float4* __restrict__ splats,
                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
                                                        uint32_t* __restrict__ vis_part) {
-    __shared__ uint32_t s_vis[kBlock / 64], s_isect[kBlock / 64];
+    __shared__ uint32_t s_vis[kBlock / 64], s_isect[kBlock / 64], s_emit[kBlock / 64];
     uint32_t n_tiles_sum = 0;  // this lane's tile count; summed per block below
     const int i = blockIdx.x * kBlock + threadIdx.x;
     bool vis = false;
@@ -121,52 +121,139 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
         tiles[i] = cnt;
         n_tiles_sum = static_cast<uint32_t>(cnt);
     }
-    // visible count and tile count per block (plain stores; a single global counter would serialize
-    // every wave)
+    // visible count, tile count and count of Gaussians with tiles per block (plain stores; a single
+    // global counter would serialize every wave)
     const unsigned long long bal = __ballot(vis);
+    const unsigned long long bal_emit = __ballot(n_tiles_sum > 0u);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1)
         n_tiles_sum += static_cast<uint32_t>(__shfl_xor(static_cast<int>(n_tiles_sum), o, 64));
     if (sxd::lane_id() == 0) {
         s_vis[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal));
         s_isect[threadIdx.x >> 6] = n_tiles_sum;
+        s_emit[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal_emit));
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t t = 0, isect = 0u;
+        uint32_t t = 0, isect = 0u, emit = 0u;
 #pragma unroll
         for (int w = 0; w < kBlock / 64; w++) {
             t += s_vis[w];
             isect += s_isect[w];
+            emit += s_emit[w];
         }
-        vis_part[2 * blockIdx.x] = t;
-        vis_part[2 * blockIdx.x + 1] = isect;
+        reinterpret_cast<uint4*>(vis_part)[blockIdx.x] = make_uint4(t, isect, emit, 0u);
     }
 }
 
-// sum of the per-block visible counts and tile counts (one block); out = {u64 visible count, u64
-// intersections}
-__global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict__ part, int n,
-                                                      unsigned long long* __restrict__ out) {
-    __shared__ unsigned long long s_red[kBlock], s_isect[kBlock];
-    unsigned long long acc = 0, isect = 0;
-    for (int k = threadIdx.x; k < n; k += kBlock) {
-        acc += part[2 * k];
-        isect += part[2 * k + 1];
-    }
-    s_red[threadIdx.x] = acc;
-    s_isect[threadIdx.x] = isect;
-    __syncthreads();
-    for (int o = kBlock / 2; o > 0; o >>= 1) {
-        if (threadIdx.x < o) {
-            s_red[threadIdx.x] += s_red[threadIdx.x + o];
-            s_isect[threadIdx.x] += s_isect[threadIdx.x + o];
+// One workgroup over the preprocess blocks' {visible, tiles, Gaussians with tiles} counts: the totals
+// (out = {u64 visible, u64 intersections, u64 Gaussians with tiles}) and, per block b, the
+// intersections and the Gaussians with tiles of the blocks before it (base[2 b], base[2 b + 1]).
+constexpr int kScanBlock = 1024;
+constexpr int kScanPer = 8;  // consecutive blocks per thread and chunk
+__global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restrict__ part, int n,
+                                                           unsigned long long* __restrict__ out,
+                                                           unsigned long long* __restrict__ base) {
+    __shared__ unsigned long long s_i[kScanBlock / 64], s_e[kScanBlock / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    unsigned long long vis = 0, carry_i = 0, carry_e = 0;
+    for (int b0 = 0; b0 < n; b0 += kScanBlock * kScanPer) {  // uniform
+        const int bt = b0 + tid * kScanPer;
+        uint4 v[kScanPer];
+        unsigned long long si = 0, se = 0;  // the thread's sums
+#pragma unroll
+        for (int k = 0; k < kScanPer; k++) {
+            v[k] = bt + k < n ? part[bt + k] : make_uint4(0u, 0u, 0u, 0u);
+            vis += v[k].x;
+            si += v[k].y;
+            se += v[k].z;
+        }
+        unsigned long long xi = si, xe = se;  // inclusive scans over the wave
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const unsigned long long yi = __shfl_up(xi, o, 64), ye = __shfl_up(xe, o, 64);
+            if (lane >= o) {
+                xi += yi;
+                xe += ye;
+            }
+        }
+        if (lane == 63) {
+            s_i[wave] = xi;
+            s_e[wave] = xe;
         }
         __syncthreads();
+        unsigned long long pi = carry_i + xi - si, pe = carry_e + xe - se, ti = 0, te = 0;
+#pragma unroll
+        for (int w = 0; w < kScanBlock / 64; w++) {
+            if (w < wave) {
+                pi += s_i[w];
+                pe += s_e[w];
+            }
+            ti += s_i[w];
+            te += s_e[w];
+        }
+#pragma unroll
+        for (int k = 0; k < kScanPer; k++) {
+            if (bt + k < n) {
+                base[2 * (size_t)(bt + k)] = pi;
+                base[2 * (size_t)(bt + k) + 1] = pe;
+            }
+            pi += v[k].y;
+            pe += v[k].z;
+        }
+        carry_i += ti;
+        carry_e += te;
+        __syncthreads();  // s_i / s_e are rewritten by the next chunk
     }
-    if (threadIdx.x == 0) {
-        out[0] = s_red[0];
-        out[1] = s_isect[0];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vis += __shfl_xor(vis, o, 64);
+    if (lane == 0) s_i[wave] = vis;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long v = 0;
+        for (int w = 0; w < kScanBlock / 64; w++) v += s_i[w];
+        out[0] = v;
+        out[1] = carry_i;
+        out[2] = carry_e;
+    }
+}
+
+// The Gaussians with tiles, in index order, compacted: position j = base[2 b + 1] + (its rank among
+// block b's) gets list[j] = the Gaussian and (cum set) cum[j] = the inclusive sum of the tile counts
+// up to it (base[2 b] + the block's running sum): the emit ranges of the index-first order, and the
+// list the depth-first order sorts.
+__global__ void __launch_bounds__(kBlock) k_emit_compact(const int32_t* __restrict__ tiles, int count,
+                                                         const unsigned long long* __restrict__ base,
+                                                         int32_t* __restrict__ list, int64_t* __restrict__ cum) {
+    __shared__ uint32_t s_n[kBlock / 64], s_t[kBlock / 64];
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t = i < count ? static_cast<uint32_t>(tiles[i]) : 0u;
+    const unsigned long long bal = __ballot(t > 0u);
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
+    uint32_t incl = t;  // the block's tile counts are 32-bit (256 Gaussians x at most 2^23 tiles)
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), o, 64));
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) {
+        s_n[wave] = static_cast<uint32_t>(__popcll(bal));
+        s_t[wave] = incl;
+    }
+    __syncthreads();
+    uint32_t pn = 0, pt = 0;
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; w++)
+        if (w < wave) {
+            pn += s_n[w];
+            pt += s_t[w];
+        }
+    if (t > 0u) {
+        const unsigned long long j = base[2 * (size_t)blockIdx.x + 1] + pn + rank;
+        list[j] = i;
+        if (cum) cum[j] = static_cast<int64_t>(base[2 * (size_t)blockIdx.x] + pt + incl);
     }
 }
 
@@ -177,16 +264,17 @@ __global__ void __launch_bounds__(kBlock) k_count_sum(const uint32_t* __restrict
 // alone finishes the job: within a tile the order is the depth order, ties by index — the same
 // permutation, for two radix passes over the intersections instead of five or six.
 
-// depth sort keys: the depth's float bits for Gaussians with tiles (a visible depth is positive, so
-// its bits order as the depths do), 0 for the rest (which emit nothing, so their place in the order
-// does not matter); values = Gaussian index
+// depth sort keys of the Gaussians with tiles (list[j], j below *n_list): the depth's float bits (a
+// visible depth is positive, so its bits order as the depths do); values = Gaussian index
 __global__ void __launch_bounds__(kBlock) k_depth_keys(StepConst c, const float4* __restrict__ splats,
-                                                       const int32_t* __restrict__ tiles,
+                                                       const int32_t* __restrict__ list,
+                                                       const unsigned long long* __restrict__ n_list,
                                                        uint32_t* __restrict__ keys, int32_t* __restrict__ vals) {
-    const int i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= c.count) return;
-    keys[i] = tiles[i] > 0 ? __float_as_uint(splats[3 * (size_t)i].w) : 0u;
-    vals[i] = i;
+    const int j = blockIdx.x * kBlock + threadIdx.x;
+    if (j >= c.count || static_cast<unsigned long long>(j) >= *n_list) return;
+    const int g = list[j];
+    keys[j] = __float_as_uint(splats[3 * (size_t)g].w);
+    vals[j] = g;
 }
 
 // Thread per position j of the depth order (of the index order when order is null): Gaussian g =
@@ -251,7 +339,8 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
                                                         const int32_t* __restrict__ radii,
                                                         const int32_t* __restrict__ order,
                                                         const int64_t* __restrict__ cum, K* __restrict__ keys,
-                                                        int32_t* __restrict__ vals, uint32_t* __restrict__ edepth) {
+                                                        int32_t* __restrict__ vals, uint32_t* __restrict__ edepth,
+                                                        const unsigned long long* __restrict__ n_pos) {
     __shared__ EmitWave s_w[kBlock / 64];
     const int j = blockIdx.x * kBlock + threadIdx.x;
     const int lane = threadIdx.x & 63;
@@ -262,7 +351,7 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
     int g = 0, n_lines = 0;
     uint32_t dbits = 0;
     sxd::AccuSweep sw = {};
-    if (j < c.count) {
+    if (j < c.count && static_cast<unsigned long long>(j) < *n_pos) {
         my0 = j == 0 ? 0 : cum[j - 1];
         cnt = cum[j] - my0;
         if (cnt > 0 && cnt <= kEmitLaneMax) {
@@ -650,7 +739,8 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 } // namespace
 
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
-                     uint32_t* vis_part, unsigned long long* n_visible, hipStream_t s) {
+                     uint32_t* vis_part, unsigned long long* n_visible, unsigned long long* block_base,
+                     hipStream_t s) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
@@ -660,29 +750,40 @@ void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t
         case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
-    hipLaunchKernelGGL(k_count_sum, dim3(1), dim3(kBlock), 0, s, vis_part, static_cast<int>(grid.x), n_visible);
+    hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
+                       static_cast<int>(grid.x), n_visible, block_base);
+}
+
+void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
+                       int64_t* cum, hipStream_t s) {
+    if (c.count <= 0) return;
+    hipLaunchKernelGGL(k_emit_compact, dim3(grid_for(c.count)), dim3(kBlock), 0, s, tiles, c.count, block_base, list,
+                       cum);
 }
 
 int step_preprocess_blocks(int64_t count) { return grid_for(count); }
 
-void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* tiles, uint32_t* keys, int32_t* vals,
-                     hipStream_t s) {
+void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* list, const unsigned long long* n_list,
+                     uint32_t* keys, int32_t* vals, hipStream_t s) {
     if (c.count <= 0) return;
-    hipLaunchKernelGGL(k_depth_keys, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, tiles, keys, vals);
+    hipLaunchKernelGGL(k_depth_keys, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, list, n_list, keys,
+                       vals);
 }
 
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth) {
+                      const int64_t* cum, const unsigned long long* n_pos, uint16_t* keys, int32_t* vals,
+                      hipStream_t s, uint32_t* edepth) {
     if (c.count <= 0) return;
     hipLaunchKernelGGL(k_emit_sorted<uint16_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
-                       cum, keys, vals, edepth);
+                       cum, keys, vals, edepth, n_pos);
 }
 
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth) {
+                      const int64_t* cum, const unsigned long long* n_pos, uint32_t* keys, int32_t* vals,
+                      hipStream_t s, uint32_t* edepth) {
     if (c.count <= 0) return;
     hipLaunchKernelGGL(k_emit_sorted<uint32_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
-                       cum, keys, vals, edepth);
+                       cum, keys, vals, edepth, n_pos);
 }
 
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,

@@ -49,8 +49,10 @@ struct sxh_executor {
     sxh::DevBuf<uint32_t> dkey_a, dkey_b;    // depth sort keys
     sxh::DevBuf<int32_t> order_a, order_b;   // Gaussian indices in depth order
     sxh::DevBuf<uint8_t> scan_scratch;
-    sxh::DevBuf<unsigned long long> n_vis;
-    sxh::DevBuf<uint32_t> vis_part;
+    sxh::DevBuf<unsigned long long> n_vis;     // visible count, intersections, Gaussians with tiles
+    sxh::DevBuf<uint32_t> vis_part;            // preprocess per-block counts
+    sxh::DevBuf<unsigned long long> blk_base;  // their prefixes (intersections, Gaussians with tiles)
+    sxh::DevBuf<int32_t> emit_list;            // the Gaussians with tiles, in index order
     // intersections (grow 1.5x, reused)
     size_t isect_cap = 0;
     sxh::DevBuf<uint64_t> keys_a, keys_b;

@@ -62,10 +62,11 @@ void isect_count(const IsectArgs& a, int32_t* tiles_per_gauss, hipStream_t s);
 void isect_emit(const IsectArgs& a, const int64_t* cum, uint64_t* keys, int32_t* vals, hipStream_t s);
 
 // inclusive int32 -> int64 scan; scratch needs scan_scratch_bytes(n) bytes. With `gather` the
-// scanned sequence is in[gather[0]], in[gather[1]], ...
+// scanned sequence is in[gather[0]], in[gather[1]], ...; with n_dev only the first *n_dev (<= n)
+// elements are scanned (n sizes the grids)
 size_t scan_scratch_bytes(int64_t n);
 void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hipStream_t s,
-                  const int32_t* gather = nullptr);
+                  const int32_t* gather = nullptr, const int64_t* n_dev = nullptr);
 
 // Stable LSD radix sort of (key, i32 value) on bits [0, key_bits), keys u64, u32 or u16. Result
 // lands in keys_a/vals_a when the pass count is even, else in keys_b/vals_b; returns 0 or 1
@@ -189,10 +190,11 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 // entries at [cum[j-1], cum[j]) that carry the current stamp (order and cum: the depth order and the
 // inclusive scan of its tile counts that placed the emit), in a fixed order per range: the
 // deterministic end of raster_bwd's `part` mode. Untouched Gaussians' records are not written. long_list
-// holds `count` ints, long_count one (reset by raster_bwd_begin).
+// holds `count` ints, long_count one (reset by raster_bwd_begin). With count_dev the positions are the
+// first *count_dev (<= count, which sizes the grid).
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part,
                          const uint32_t* stamp, const uint8_t* touched, float4* grads, int32_t* long_list,
-                         int32_t* long_count, hipStream_t s);
+                         int32_t* long_count, hipStream_t s, const int64_t* count_dev = nullptr);
 void raster_bwd(const RasterArgs& a, const float* render_alphas, const int32_t* last_ids,
                 const float* v_render_colors, const float* v_render_alphas, const RasterBwdGrads& g,
                 hipStream_t s);

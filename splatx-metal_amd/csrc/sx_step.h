@@ -44,24 +44,33 @@ struct StepConst {
     float noise_scale;
 };
 
-// vis_part: 2 u32 per block (visible count, tile count); out_vis: {u64 visible count, u64
-// intersections}
+// vis_part: 4 u32 per block (visible count, tile count, count of Gaussians with tiles, 0); out_vis:
+// {u64 visible count, u64 intersections, u64 Gaussians with tiles}; block_base: per block, the
+// intersections and the Gaussians with tiles of the blocks before it (2 u64)
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
-                     uint32_t* vis_part, unsigned long long* out_vis, hipStream_t s);
-// number of blocks of step_preprocess (vis_part holds 2 u32 per block)
-int step_preprocess_blocks(int64_t count);
-// depth-first intersections: depth keys of the Gaussians that emit (values = index) for a stable
-// 32-bit sort; then, over that order, each Gaussian's tile ids at [cum[j-1], cum[j]) (cum =
-// inclusive scan of the tile counts gathered through the order); after a stable sort of the tile
-// ids, offsets[t] = lower bound of t. Index-first: order null (position j is Gaussian j), cum the
-// plain scan of the tile counts, and the depth order within each tile comes after the tile sort
-// (tile_depth_sort), which reads each entry's depth bits from edepth (written by the emit when set)
-void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* tiles, uint32_t* keys, int32_t* vals,
+                     uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
                      hipStream_t s);
+// number of blocks of step_preprocess
+int step_preprocess_blocks(int64_t count);
+// The Gaussians with tiles in index order (list[j], j below out_vis[2]) and (cum set) cum[j], the
+// inclusive sum of their tile counts: the positions of the index-first emit.
+void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
+                       int64_t* cum, hipStream_t s);
+// depth-first intersections: depth keys of the listed Gaussians (values = index) for a stable 32-bit
+// sort of *n_list keys; then, over that order, each Gaussian's tile ids at [cum[j-1], cum[j]) (cum =
+// inclusive scan of the tile counts gathered through the order); after a stable sort of the tile ids,
+// offsets[t] = lower bound of t. Index-first: order = the list itself, cum from step_emit_compact,
+// and the depth order within each tile comes after the tile sort (tile_depth_sort), which reads each
+// entry's depth bits from edepth (written by the emit when set). The emit covers positions j below
+// *n_pos.
+void step_depth_keys(const StepConst& c, const float4* splats, const int32_t* list, const unsigned long long* n_list,
+                     uint32_t* keys, int32_t* vals, hipStream_t s);
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint16_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth = nullptr);
+                      const int64_t* cum, const unsigned long long* n_pos, uint16_t* keys, int32_t* vals,
+                      hipStream_t s, uint32_t* edepth = nullptr);
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
-                      const int64_t* cum, uint32_t* keys, int32_t* vals, hipStream_t s, uint32_t* edepth = nullptr);
+                      const int64_t* cum, const unsigned long long* n_pos, uint32_t* keys, int32_t* vals,
+                      hipStream_t s, uint32_t* edepth = nullptr);
 // n_dev: the key count on the device, read instead of n
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev = nullptr);
