@@ -32,10 +32,25 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 
 def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, shape: dict) -> float:
     """Minimum HBM bytes one launch of `name` must move (per-unit figures stated in DESIGN.md). shape:
-    depth_passes / tile_passes (radix passes of the depth sort over n keys and of the tile sort over the
-    i intersections) and key_b (bytes of a tile id: 2 up to 2^16 tiles, else 4)."""
+    index_first (the step's intersection order: emit in index order, then per-tile depth sorts; else
+    depth first), depth_passes / tile_passes (radix passes of the depth sort over the Gaussians with tiles
+    and of the tile sort over the i intersections) and key_b (bytes of a tile id: 2 up to 2^16 tiles,
+    else 4). The Gaussians with tiles, which the emit steps run over, are counted as the v visible ones
+    (a visible Gaussian without a tile is rare)."""
     pd = 3 + 4 + 3 + 1 + 3 + (sh_k - 1) * 3  # parameter floats per Gaussian (59 at SH3)
     kb = shape["key_b"]
+    if shape.get("index_first"):
+        if name == "scan":
+            # the compaction: every Gaussian's tile count (4 B) in, the list of those with tiles (4 B) and
+            # their inclusive offsets (8 B) out
+            return 4.0 * n + 12.0 * v
+        if name == "emit":
+            # list (4 B) and offset (8 B) per Gaussian, its 32-B conic/mean record; per entry the tile id,
+            # the Gaussian (4 B) and its depth bits (4 B) out
+            return v * (12.0 + 32.0) + i * (kb + 8.0)
+        if name == "tile_depth_sort":
+            # per entry: the emit position in and out (8 B), its depth bits gathered through it (4 B)
+            return 12.0 * i
     if name == "preprocess":
         # params of every Gaussian (44 B) + SH coefficients of visible ones; writes radii+count (12 B),
         # and for visible ones the 48-B splat record
@@ -51,20 +66,21 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
         # as the forward, plus the 36-B sums and the 4-B step stamp stored per (tile, Gaussian)
         return i * (4 + 4 + 36 + 36 + 4) + px * (4 + 4 + 12)
     if name == "gather":
-        # depth order, the scan and the touched flag per Gaussian (13 B), the 36-B sums and stamp of the
+        # order, offset and touched flag per Gaussian with tiles (13 B), the 36-B sums and stamp of the
         # entries, the 48-B gradient record of the visible Gaussians
-        return n * 13.0 + i * 40.0 + v * 48.0
+        return v * 13.0 + i * 40.0 + v * 48.0
     if name == "depth_sort":
-        # keys: tile counts (4 B) and the depths of the visible (4 B) in, (key, index) out (8 B); then the
-        # onesweep sort of n (u32, i32) pairs: one histogram read (4 B), per pass a read and a write (16 B)
-        return n * (4.0 + 8.0) + 4.0 * v + n * (4.0 + 16.0 * shape["depth_passes"])
+        # compaction: every tile count (4 B) in, the list of Gaussians with tiles (4 B) out; keys: their
+        # depths (4 B) in, (key, index) out (8 B); the onesweep sort of those (u32, i32) pairs: one histogram
+        # read (4 B), per pass a read and a write (16 B)
+        return 4.0 * n + v * (4.0 + 4.0 + 8.0) + v * (4.0 + 16.0 * shape["depth_passes"])
     if name == "scan":
         # tile counts gathered through the depth order: order (4 B) + count (4 B) in, offset (8 B) out
-        return n * 16.0
+        return v * 16.0
     if name == "emit":
-        # order (4 B) and offset (8 B) per position, the 32-B conic/mean record of the visible, and the
-        # (tile id, index) entries out
-        return n * 12.0 + v * 32.0 + i * (kb + 4.0)
+        # order (4 B) and offset (8 B) per position, the 32-B conic/mean record, and the (tile id, emit
+        # position's Gaussian) entries out
+        return v * (12.0 + 32.0) + i * (kb + 4.0)
     if name == "sort":
         # tile sort: one histogram read of the ids, per pass a read and a write of (id, emit position); the
         # first pass takes the positions from the key index instead of reading them
@@ -380,8 +396,11 @@ def main():
     I, V = float(np.mean(n_isects)), float(np.mean(n_vis))
     px = sc.width * sc.height
     sh_k = (sc.sh_degree + 1) ** 2
-    shape = {"depth_passes": float(np.mean(passes)), "tile_passes": (tile_bits + 7) // 8,
-             "key_b": 2 if tile_bits <= 16 else 4}
+    # the step's intersection order, as the profiled steps ran it (index first: a per-tile depth sort, no
+    # depth sort of the Gaussians)
+    index_first = "tile_depth_sort" in avg
+    shape = {"index_first": index_first, "depth_passes": 0.0 if index_first else float(np.mean(passes)),
+             "tile_passes": (tile_bits + 7) // 8, "key_b": 2 if tile_bits <= 16 else 4}
     kernel_names = [k for k in avg if not k.startswith("host_")]
     per_kernel = {}
     for k in kernel_names:
@@ -415,6 +434,7 @@ def main():
         "gaussians_per_s": round(sc.n / (ms_per_step / 1e3), 1),
         "mean_n_isects": round(I, 1),
         "mean_visible": round(V, 1),
+        "isect_order": "index_first" if index_first else "depth_first",
         "sort_passes": {"depth": round(shape["depth_passes"], 2), "tile": shape["tile_passes"]},
         "final_loss": round(float(losses[-1]), 6),
         "step_alg_GB": round(step_bytes / 1e9, 4),
