@@ -29,6 +29,7 @@ constexpr int kRounds = 16;
 constexpr int kTile = kThreads * kRounds;  // 4096 keys per workgroup
 constexpr int kBins = 256;
 constexpr int kMaxPassesOs = 8;
+constexpr int kXcds = 8;  // XCDs of an MI355X (workgroups are dealt to them round-robin)
 
 // Pass p of a sort on bits [0, key_bits) with digits of `dbits` bits covers bits [p dbits, p dbits +
 // width), the last pass only what is left of key_bits (bits above key_bits never count).
@@ -584,10 +585,20 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
         n = *n_dev;
         if (CHAIN && static_cast<int64_t>(blockIdx.x) * kTile >= n) return;  // uniform
     }
-    // CHAIN: one tile, from the counter. Otherwise tiles blockIdx.x, + gridDim.x, ... below the (device)
-    // key count (the launch gives one workgroup per tile; the loop form measured faster at config 5).
+    // CHAIN: one tile, from the counter. Otherwise one tile below the (device) key count, by the
+    // workgroup's index.
     const int64_t n_work = (n + kTile - 1) / kTile;
-    for (int64_t t = blockIdx.x; CHAIN || t < n_work; t += gridDim.x) {  // uniform
+    // XCD-aware tile order: the GPU deals workgroups to its kXcds XCDs round-robin (workgroup b to XCD
+    // b % kXcds, each XCD taking its share in order), so tile (b % kXcds) * per + b / kXcds gives every XCD
+    // a contiguous range of tiles. The runs of one digit that consecutive tiles write sit next to each
+    // other in the output: written from the same L2, their partial lines merge before they leave it. The
+    // grid has kXcds * ceil(tiles / kXcds) workgroups; the ones past the device count leave.
+    // (Fewer workgroups per CU, or each looping over several tiles, measured slower.)
+    const int64_t per = (n_work + kXcds - 1) / kXcds;
+    {
+        const int64_t k = blockIdx.x;
+        const int64_t t = CHAIN ? 0 : (k % kXcds) * per + k / kXcds;
+        if (!CHAIN && (k >= per * kXcds || t >= n_work)) return;  // uniform
         if (CHAIN && tid == 0) s_tile = atomicAdd(counter, 1u);
 #pragma unroll
         for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
@@ -760,8 +771,6 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
                 vout[g] = s_v[p];
             }
         }
-        if (CHAIN) break;
-        __syncthreads();  // the next tile reuses the LDS
     }
 }
 
@@ -773,8 +782,9 @@ void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, 
                     int shift, uint32_t mask, const uint32_t* digit_base, uint32_t* status, uint32_t* status_next,
                     uint32_t* counter, uint32_t* err, const int64_t* n_dev, const uint32_t* starts = nullptr) {
 #define SX_OS_PASS(NB)                                                                                          \
-    hipLaunchKernelGGL((k_os_pass<K, NB, CHAIN>), dim3(tiles), dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, \
-                       mask, digit_base, status, status_next, counter, err, n_dev, starts, tiles)
+    hipLaunchKernelGGL((k_os_pass<K, NB, CHAIN>), dim3(CHAIN ? tiles : (tiles + kXcds - 1) / kXcds * kXcds), \
+                       dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, mask, digit_base, status, status_next,  \
+                       counter, err, n_dev, starts, tiles)
     switch (__builtin_popcount(mask)) {
         case 1: SX_OS_PASS(1); break;
         case 2: SX_OS_PASS(2); break;
