@@ -433,12 +433,14 @@ constexpr int kScanChunk = kThreads * 16;  // elements per workgroup of the coun
 // thread takes 16 consecutive keys (16-B loads) and adds each run of equal digits once: neighbouring
 // keys often share the high digits (the tiles of one Gaussian along a row), and the lanes of a wave,
 // 16 keys apart, rarely hit the same counter at once.
+// err (optional): the sort's error word, zeroed by workgroup 0 (a sort that starts with this pass).
 template <class K>
 __global__ void __launch_bounds__(kThreads) k_rs_count(const K* __restrict__ keys, int64_t n, int shift, uint32_t mask,
                                                        uint32_t* __restrict__ cnt, int n_tiles,
-                                                       const int64_t* __restrict__ n_dev) {
+                                                       const int64_t* __restrict__ n_dev, uint32_t* __restrict__ err) {
     static_assert(kRounds * sizeof(K) % 16 == 0, "a thread's keys are whole 16-B vectors");
     __shared__ uint32_t h[kBins];
+    if (err && blockIdx.x == 0 && threadIdx.x == 0) *err = 0u;
     if (n_dev) n = *n_dev;
     h[threadIdx.x] = 0;
     __syncthreads();
@@ -836,11 +838,10 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
     const int64_t hist_n = (int64_t)tiles * kBins;
     uint32_t* hist = totals + kHeaderWords;
     uint32_t* status_b = hist + hist_n;
-    hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins,
-                       clear_err ? err : nullptr);
     const K* kin = src_k;
     const int32_t* vin = src_v;
     if (n < (int64_t{1} << 30) && tiles >= kRtsMinTiles) {  // reduce-then-scan (see k_rs_count); no histogram kernel
+        // (the digit totals are not used here; the first count kernel clears the error word)
         uint32_t* cnt = hist;       // (mask + 1) x tiles counts, then their starts
         uint32_t* sums = status_b;  // the scan's chunk sums
         for (int p = 0; p < passes; p++) {
@@ -848,7 +849,8 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
             const int64_t len = static_cast<int64_t>(mask + 1) * tiles;
             const int chunks = static_cast<int>((len + kScanChunk - 1) / kScanChunk);
             hipLaunchKernelGGL(k_rs_count<K>, dim3(tiles), dim3(kThreads), 0, s, kin, n, dbits * p, mask, cnt, tiles,
-                               n_dev);
+                               n_dev, (p == 0 && clear_err) ? err : nullptr);
+            // (one workgroup scanning a small matrix in one launch measured slower than these three)
             hipLaunchKernelGGL(k_rs_reduce, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
             hipLaunchKernelGGL(k_rs_top, dim3(1), dim3(kThreads), 0, s, sums, chunks);
             hipLaunchKernelGGL(k_rs_down, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
@@ -859,6 +861,8 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
         }
         return passes;
     }
+    hipLaunchKernelGGL(k_zero_totals, dim3(1), dim3(kThreads), 0, s, totals, passes * kBins,
+                       clear_err ? err : nullptr);
     if (n < (int64_t{1} << 30)) {  // onesweep: counts and prefixes fit the 30-bit status words
         const int hist_blocks = std::min(tiles, kHistBlocks);
         if (key_bits <= kFullBits)
