@@ -441,10 +441,16 @@ __global__ void __launch_bounds__(kThreads) k_rs_count(const K* __restrict__ key
     static_assert(kRounds * sizeof(K) % 16 == 0, "a thread's keys are whole 16-B vectors");
     __shared__ uint32_t h[kBins];
     if (err && blockIdx.x == 0 && threadIdx.x == 0) *err = 0u;
+    // tiles dealt XCD by XCD, as in k_os_pass (a grid of kXcds * ceil(n_tiles / kXcds)): a digit's counts
+    // of consecutive tiles are neighbouring words of the matrix, and their partial lines then merge in
+    // one L2
+    const int per = (n_tiles + kXcds - 1) / kXcds;
+    const int tile = static_cast<int>(blockIdx.x % kXcds) * per + static_cast<int>(blockIdx.x / kXcds);
+    if (tile >= n_tiles) return;  // uniform
     if (n_dev) n = *n_dev;
     h[threadIdx.x] = 0;
     __syncthreads();
-    const int64_t i0 = (int64_t)blockIdx.x * kTile + (int64_t)threadIdx.x * kRounds;
+    const int64_t i0 = (int64_t)tile * kTile + (int64_t)threadIdx.x * kRounds;
     K key[kRounds];
     if (i0 + kRounds <= n) {  // the tile is 16-B aligned (4096 keys), and so is each thread's part
         constexpr int kVec = kRounds * sizeof(K) / 16;
@@ -472,7 +478,7 @@ __global__ void __launch_bounds__(kThreads) k_rs_count(const K* __restrict__ key
     }
     if (run_n) atomicAdd(&h[run_d], run_n);
     __syncthreads();
-    if (threadIdx.x <= mask) cnt[(size_t)threadIdx.x * n_tiles + blockIdx.x] = h[threadIdx.x];
+    if (threadIdx.x <= mask) cnt[(size_t)threadIdx.x * n_tiles + tile] = h[threadIdx.x];
 }
 
 // Exclusive scan of v[0, len) in place, in three launches: chunk sums, their exclusive scan (one
@@ -848,8 +854,8 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
             const uint32_t mask = digit_mask(p, dbits, key_bits);
             const int64_t len = static_cast<int64_t>(mask + 1) * tiles;
             const int chunks = static_cast<int>((len + kScanChunk - 1) / kScanChunk);
-            hipLaunchKernelGGL(k_rs_count<K>, dim3(tiles), dim3(kThreads), 0, s, kin, n, dbits * p, mask, cnt, tiles,
-                               n_dev, (p == 0 && clear_err) ? err : nullptr);
+            hipLaunchKernelGGL(k_rs_count<K>, dim3((tiles + kXcds - 1) / kXcds * kXcds), dim3(kThreads), 0, s, kin, n,
+                               dbits * p, mask, cnt, tiles, n_dev, (p == 0 && clear_err) ? err : nullptr);
             // (one workgroup scanning a small matrix in one launch measured slower than these three)
             hipLaunchKernelGGL(k_rs_reduce, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
             hipLaunchKernelGGL(k_rs_top, dim3(1), dim3(kThreads), 0, s, sums, chunks);
