@@ -76,10 +76,17 @@ __device__ __forceinline__ int block_of(int wave, int lane) {
 }
 
 // Which of the tile's sixteen 4x4 blocks the Gaussian's cutoff set {sigma <= cut} can reach (bit
-// by * 4 + bx): the set's bounding box, half-extents sqrt(2 cut c / det) in x and sqrt(2 cut a / det)
-// in y for a positive-definite conic, against each block's rectangle of pixel centres. Conservative:
-// the extents get a relative and an absolute margin far above float rounding of sigma, and every
-// degenerate, nearly degenerate or non-finite case keeps all sixteen blocks.
+// by * 4 + bx). First the set's bounding box (half-extents rx = sqrt(2 cut c / det) in x and
+// ry = sqrt(2 cut a / det) in y for a positive-definite conic) against each block's rectangle of pixel
+// centres; then, per block row, the set's exact x-range within the row's band of pixel-centre rows:
+// for an offset v = y - my the set spans dx in [-(b/a) v -+ sqrt(2 cut a - det v^2) / a]; over the band
+// [v0, v1] the right end is largest at the set's rightmost point (v = -(b/c) rx, where it is rx) when
+// that lies in the band, else at an end of the band (it is concave in v), and the left end mirrors it.
+// A block is kept when both tests reach it: a splat's bounding box holds ~20 % more blocks than the
+// set itself reaches at the benchmark scenes, whose list entries and lane pairs this saves. Conservative:
+// the extents get a relative and an absolute margin far above the rounding of these float expressions
+// and of the rasterisers' sigma, and every degenerate, nearly degenerate or non-finite case keeps all
+// sixteen blocks.
 __device__ __forceinline__ uint32_t block_mask(float4 xyo, float4 con, float x0, float y0) {
     const float a = con.x, b = con.y, c = con.z, cut = xyo.w;
     if (cut == -__builtin_inff()) return 0u;  // opacity 0: no pixel passes
@@ -88,19 +95,36 @@ __device__ __forceinline__ uint32_t block_mask(float4 xyo, float4 con, float x0,
                         __builtin_isfinite(cut) && __builtin_fabsf(xyo.x) < 1e18f && __builtin_fabsf(xyo.y) < 1e18f;
     if (!finite || !(a > 0.f) || !(det > 1e-4f * a * c)) return 0xFFFFu;
     if (cut < 0.f) return 0u;  // sigma >= 0 everywhere for a positive-definite conic
-    const float rx = __builtin_sqrtf(2.0f * cut * c / det) * 1.001f + 0.01f;
-    const float ry = __builtin_sqrtf(2.0f * cut * a / det) * 1.001f + 0.01f;
-    uint32_t cols = 0u, rows = 0u;
+    const float k2 = 2.0f * cut;
+    const float idet = __builtin_amdgcn_rcpf(det);
+    const float rx0 = __builtin_amdgcn_sqrtf(k2 * c * idet), ry0 = __builtin_amdgcn_sqrtf(k2 * a * idet);
+    const float rx = rx0 * 1.001f + 0.01f, ry = ry0 * 1.001f + 0.01f;
+    const float mg = rx0 * 0.001f + 0.01f;  // margin of the per-row x-ranges
+    const float inva = __builtin_amdgcn_rcpf(a), ba = b * inva, ak2 = a * k2;
+    const float dyr = -(b * __builtin_amdgcn_rcpf(c)) * rx0;  // the rightmost point's offset; the leftmost: -dyr
+    uint32_t cols = 0u, m = 0u;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const float bx0 = x0 + static_cast<float>(4 * k) + 0.5f, by0 = y0 + static_cast<float>(4 * k) + 0.5f;
+        const float bx0 = x0 + static_cast<float>(4 * k) + 0.5f;
         if (xyo.x + rx >= bx0 && xyo.x - rx <= bx0 + 3.0f) cols |= 1u << k;
-        if (xyo.y + ry >= by0 && xyo.y - ry <= by0 + 3.0f) rows |= 1u << k;
     }
-    uint32_t m = 0u;
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-        if ((rows >> k) & 1u) m |= cols << (4 * k);
+    for (int k = 0; k < 4; k++) {  // block row k
+        const float u0 = y0 + static_cast<float>(4 * k) + 0.5f - xyo.y;
+        const float v0 = __builtin_fmaxf(u0, -ry), v1 = __builtin_fminf(u0 + 3.0f, ry);
+        const float s0 = __builtin_amdgcn_sqrtf(__builtin_fmaxf(0.f, ak2 - det * v0 * v0)) * inva;
+        const float s1 = __builtin_amdgcn_sqrtf(__builtin_fmaxf(0.f, ak2 - det * v1 * v1)) * inva;
+        const float c0 = -ba * v0, c1 = -ba * v1;
+        const float xmax = xyo.x + ((v0 <= dyr && dyr <= v1) ? rx0 : __builtin_fmaxf(c0 + s0, c1 + s1)) + mg;
+        const float xmin = xyo.x + ((v0 <= -dyr && -dyr <= v1) ? -rx0 : __builtin_fminf(c0 - s0, c1 - s1)) - mg;
+        uint32_t rc = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float bx0 = x0 + static_cast<float>(4 * j) + 0.5f;
+            if (xmax >= bx0 && xmin <= bx0 + 3.0f) rc |= 1u << j;
+        }
+        if (v0 <= v1) m |= (rc & cols) << (4 * k);  // an empty band: no block of this row
+    }
     return m;
 }
 
