@@ -858,6 +858,7 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
                                                      const int64_t* __restrict__ n_isects_dev,
                                                      uint32_t* __restrict__ max_count) {
     __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_wtot[4];
     __shared__ uint32_t s_max;
     if (n_isects_dev) n_isects = *n_isects_dev;
     const int t0 = threadIdx.x, lane = t0 & 63;
@@ -887,13 +888,24 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
         if (valid && (m & below) == 0) atomicAdd(&s_hist[b], static_cast<uint32_t>(__popcll(m)));
     }
     __syncthreads();
-    if (t0 == 0) {  // exclusive prefix over 256 buckets
-        uint32_t run = 0;
-        for (int b = 0; b < 256; b++) {
-            const uint32_t c = s_hist[b];
-            s_hist[b] = run;
-            run += c;
+    // exclusive prefix over the 256 buckets: waves 0-3 scan them, then add the lower waves' totals
+    uint32_t hc = 0, hx = 0;
+    if (t0 < 256) {  // whole waves
+        hc = s_hist[t0];
+        hx = hc;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = static_cast<uint32_t>(__shfl_up(static_cast<int>(hx), o, 64));
+            if (lane >= o) hx += y;
         }
+        if (lane == 63) s_wtot[t0 >> 6] = hx;
+    }
+    __syncthreads();
+    if (t0 < 256) {
+        uint32_t pre = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) pre += w < (t0 >> 6) ? s_wtot[w] : 0u;
+        s_hist[t0] = pre + hx - hc;
     }
     __syncthreads();
     for (int t1 = 0; t1 < n_tiles; t1 += 1024) {
