@@ -17,10 +17,11 @@
 // workgroup exits as soon as all its pixels are done.
 // Backward: back-to-front walk recovering T by division, four list entries per group at a time;
 // a group sums its four splats' nine gradient components over its 16 lanes with one transposed
-// reduction (8 DPP instructions per component) and stores the sums in an LDS entry buffer;
-// per segment of 32 batch slots the threads of each slot add its entries over the blocks it reached
-// and store the (tile, Gaussian) totals at the slot's emit position (plain stores), which the gather
-// then adds per Gaussian in a fixed order. The per-op entry point adds them with float atomics.
+// reduction (8 DPP instructions per component) and stores the sums in an LDS entry buffer; per
+// segment (a run of batch slots in which no block's list passes the buffer's 32 entries) the threads of
+// each slot add its entries over the blocks it reached and store the (tile, Gaussian) totals at the
+// slot's emit position (plain stores), which the gather then adds per Gaussian in a fixed order. The
+// per-op entry point adds them with float atomics.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -36,7 +37,8 @@ constexpr int kBlocks = 16;  // 4x4 pixel blocks of a tile
 #ifndef SX_BWD_SEG
 #define SX_BWD_SEG 32
 #endif
-// backward segment: batch slots whose sums are flushed together (32: 34 KB of LDS, 4 workgroups per CU)
+// backward segment: at most this many entries per block list between flushes (the entry buffer's row:
+// 32 gives 36 KB of LDS, 4 workgroups per CU)
 constexpr int kBwdSeg = SX_BWD_SEG;
 
 // sxm::expf_fast(-sigma) without its range branches: identical for sigma in [0, 86] (no overflow,
@@ -371,6 +373,24 @@ __device__ __forceinline__ float* grad_slot(const RasterBwdGrads& g, int32_t gid
     }
 }
 
+// The position of the n-th (1-based) set bit of w, for 1 <= n <= popcount(w): a binary descent over
+// the halves, quarters, ... of the word (uniform work, no loop over the bits).
+__device__ __forceinline__ int nth_set_bit(unsigned long long w, int n) {
+    int pos = 0;
+    uint32_t x = static_cast<uint32_t>(w);
+    int c = __popc(x);
+    if (n > c) { n -= c; x = static_cast<uint32_t>(w >> 32); pos = 32; }
+    c = __popc(x & 0xFFFFu);
+    if (n > c) { n -= c; x >>= 16; pos += 16; }
+    c = __popc(x & 0xFFu);
+    if (n > c) { n -= c; x >>= 8; pos += 8; }
+    c = __popc(x & 0xFu);
+    if (n > c) { n -= c; x >>= 4; pos += 4; }
+    c = __popc(x & 0x3u);
+    if (n > c) { n -= c; x >>= 2; pos += 2; }
+    return pos + (n > static_cast<int>(x & 1u) ? 1 : 0);
+}
+
 // Position of entry e of block bl in its row of the backward's entry buffer: rotated by 4 for the
 // blocks of odd block rows, so that the 16 writers of a chunk (the 2x2 blocks of a wave, four consecutive
 // entries each; rows of kSeg words, a multiple of 32) use 16 different LDS banks.
@@ -382,9 +402,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                                                          const float* __restrict__ v_rc, const float* __restrict__ v_ra,
                                                          RasterBwdGrads g) {
     constexpr int NV = ABSGRAD ? kGrads + 2 : kGrads;
-    // a segment: kSeg consecutive batch slots (32 or 64); its per-entry sums are flushed before the next
-    constexpr int kBitsPerLane = kSeg / 16;  // list building: lane r of a group places bits [r kBitsPerLane, ...)
-    constexpr int kTermGroups = kThreads / kSeg;  // flush: the threads of a segment's splat share its components
+    // A segment: a run of batch slots in which no block's list holds more than kSeg entries (the
+    // capacity of its entry buffer); its per-entry sums are flushed before the next.
+    static_assert(kSeg == 32 || kSeg == 64, "entry buffer rows of 32 or 64 words");
+    constexpr int kTermGroups = 8;  // flush: the threads of a slot share its components
     __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
     __shared__ float4 s_con[kThreads];  // {a, b, c, Gaussian id (int bits)}
     __shared__ float4 s_rgb[kThreads];  // {r, g, b, flatten_ids entry (int bits)}
@@ -392,7 +413,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     // rotated by ent_rot so that the 16 writers of a chunk land in 16 different banks]
     __shared__ float s_ent[kBlocks][NV][kSeg];
     __shared__ unsigned long long s_bits[kBlocks][4];  // [block][wave]: the wave's batch slots that reach the block
-    __shared__ uint8_t s_seg[kBlocks][kSeg];          // the block's list of the current segment (slots within it)
+    __shared__ uint8_t s_seg[kBlocks][kSeg];          // the block's list of the current segment (batch slots)
+    __shared__ uint8_t s_epos[kThreads][kBlocks];     // [slot][block]: the slot's position in the block's list
     __shared__ uint16_t s_bm[kThreads];               // each batch slot's block mask
     __shared__ int32_t s_bbf[kBlocks];                // each block's last contributing intersection
     const int n_tiles = a.tile_width * a.tile_height;
@@ -474,28 +496,82 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
         __syncthreads();
 
         const int t_min = batch_end - bin_final;  // slots t >= t_min are at or before the lane's last contributor
-        const int n_seg = (batch_size + kSeg - 1) / kSeg;
-        for (int sg = 0; sg < n_seg; sg++) {
-            // the segment's slots that reach a block: bits of the owning wave's ballot
-            auto seg_bits = [&](int blk) -> unsigned long long {
-                const unsigned long long w = s_bits[blk][(kSeg * sg) >> 6];
-                if constexpr (kSeg == 64) return w;
-                else return (w >> ((kSeg * sg) & 63)) & ((1ull << kSeg) - 1ull);
-            };
-            // this group's list of the segment: lane r places the set slots among its kBitsPerLane bits
-            const unsigned long long bits = seg_bits(bl);
-            const int cnt = __popcll(bits);
+        // The batch's slots are walked in segments [s0, s1), each ending before the slot of the entry
+        // with which some block's list would pass kSeg entries; so the lists are as long as the entry
+        // buffer allows whatever the slots' density (fixed 32-slot segments left ~6 entries per list,
+        // and half of the four groups' lockstep chunks past their lists). Every wave derives the same
+        // bounds from the block masks.
+        const unsigned long long w_bl[4] = {s_bits[bl][0], s_bits[bl][1], s_bits[bl][2], s_bits[bl][3]};
+        for (int s0 = 0; s0 < batch_size;) {  // uniform
+            // lane k < 16: the slot of block k's (kSeg + 1)-th entry from s0 (none: kThreads); s1 = the least
+            int lim = kThreads;
             {
-                const int b0 = kBitsPerLane * r;  // at most kSeg - kBitsPerLane: the shifts stay below 64
-                const uint32_t nib = static_cast<uint32_t>(bits >> b0) & ((1u << kBitsPerLane) - 1u);
-                int pos = __popcll(bits & ((1ull << b0) - 1ull));
+                const int k = lane & (kBlocks - 1);  // lanes 16-63 repeat lanes 0-15
+                int need = kSeg + 1;
+                bool found = false;
 #pragma unroll
-                for (int i = 0; i < kBitsPerLane; i++)
-                    if ((nib >> i) & 1u) s_seg[bl][pos++] = static_cast<uint8_t>(b0 + i);
+                for (int i = 0; i < 4; i++) {
+                    unsigned long long w = s_bits[k][i];
+                    w &= (64 * i + 63 < s0) ? 0ull : (64 * i >= s0 ? ~0ull : (~0ull << (s0 & 63)));
+                    const int c = __popcll(w);
+                    if (!found && c >= need) {
+                        lim = 64 * i + nth_set_bit(w, need);
+                        found = true;
+                    }
+                    if (!found) need -= c;
+                }
+            }
+            lim = min(lim, __shfl_xor(lim, 8, 64));
+            lim = min(lim, __shfl_xor(lim, 4, 64));
+            lim = min(lim, __shfl_xor(lim, 2, 64));
+            lim = min(lim, __shfl_xor(lim, 1, 64));
+            // (lim >= s0 + kSeg for every block, so s1 > s0; the max only makes progress explicit)
+            const int s1 = max(s0 + 1, min(static_cast<int>(batch_size), __builtin_amdgcn_readfirstlane(lim)));
+            // this group's list of the segment: lane r places the set slots among slots [16 r, 16 r + 16)
+            unsigned long long wr[4];
+            int cnt = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int lo = min(max(s0 - 64 * i, 0), 64), hi = min(max(s1 - 64 * i, 0), 64);
+                const unsigned long long mhi = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+                const unsigned long long mlo = lo >= 64 ? ~0ull : ((1ull << lo) - 1ull);
+                wr[i] = w_bl[i] & mhi & ~mlo;
+                cnt += __popcll(wr[i]);
+            }
+            {
+                // lane r takes the segment's slots [a, a + span): the span is at most 16, so its bits lie in
+                // one or two words
+                const int span = (s1 - s0 + 15) >> 4;
+                const int a0 = s0 + r * span;
+                const int a = min(a0, s1), e = min(a0 + span, s1);
+                const int ia = a >> 6, ib = (e - 1) >> 6;
+                const unsigned long long wa = ia == 0 ? wr[0] : ia == 1 ? wr[1] : ia == 2 ? wr[2] : wr[3];
+                const unsigned long long wb = ib == 0 ? wr[0] : ib == 1 ? wr[1] : ib == 2 ? wr[2] : wr[3];
+                int pos = __popcll(wa & ((1ull << (a & 63)) - 1ull));
+#pragma unroll
+                for (int k = 0; k < 3; k++) pos += k < ia ? __popcll(wr[k]) : 0;
+                // the span's bits, from slot a on: the rest of word ia, then the start of word ib
+                uint32_t bits = 0u;
+                if (e > a) {
+                    const unsigned long long lo = wa >> (a & 63);
+                    const unsigned long long hi = (ib != ia) ? (wb << (64 - (a & 63))) : 0ull;
+                    bits = static_cast<uint32_t>(lo | hi) & ((1u << (e - a)) - 1u);
+                }
+                while (bits) {  // at most kSeg entries over the group (the segment's bound)
+                    const int slot = a + __builtin_ctz(bits);
+                    bits &= bits - 1u;
+                    if (pos < kSeg) {  // always (the bound); kept so that no write can leave the row
+                        s_seg[bl][pos] = static_cast<uint8_t>(slot);
+                        s_epos[slot][bl] = static_cast<uint8_t>(pos);
+                    }
+                    pos++;
+                }
             }
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the group's lanes read what the others wrote
-            const int n4 = (max(max(__popcll(seg_bits(wb0)), __popcll(seg_bits(wb1))),
-                                max(__popcll(seg_bits(wb2)), __popcll(seg_bits(wb3)))) + 3) >> 2;
+            int lmax = cnt;  // the longest of the wave's four lists (cnt is uniform within a group)
+            lmax = max(lmax, __shfl_xor(lmax, 16, 64));
+            lmax = max(lmax, __shfl_xor(lmax, 32, 64));
+            const int n4 = (__builtin_amdgcn_readfirstlane(lmax) + 3) >> 2;
             const uint32_t* seg4 = reinterpret_cast<const uint32_t*>(s_seg[bl]);
             // The group's Gaussians back to front, four at a time: the four list entries come in one
             // LDS read and their records in one burst, the four pairs' exponentials are independent,
@@ -510,10 +586,12 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                 float4 xyo[4], con[4], rgb[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    // past the list the byte is stale (or never written): masked into the segment's
-                    // slots for the read, and the entry is invalid
+                    // past the list the byte is stale (or never written) and the entry invalid; it reads the
+                    // segment's first slot, a record loaded in this batch: a slot this workgroup never loaded
+                    // holds whatever an earlier kernel left in the LDS, and an infinite value there would
+                    // turn the back-sum's 0 * value into a NaN
                     inl[k] = j + k < cnt;
-                    tc[k] = kSeg * sg + static_cast<int>((packed >> (8 * k)) & static_cast<uint32_t>(kSeg - 1));
+                    tc[k] = inl[k] ? static_cast<int>((packed >> (8 * k)) & 0xFFu) : s0;
                     xyo[k] = s_xyo[tc[k]];
                     con[k] = s_con[tc[k]];
                     rgb[k] = s_rgb[tc[k]];
@@ -633,24 +711,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                 }
             }
             __syncthreads();
-            // the segment's totals: the threads of slot j sum its entries over the blocks it reaches, each
-            // thread a few of the components, and add them with one float atomic per component
-            {
-                const int j = tid % kSeg, q = tid / kSeg;
-                const int slot = kSeg * sg + j;
-                const uint32_t m0 = slot < batch_size ? static_cast<uint32_t>(s_bm[slot]) : 0u;
+            // the segment's totals: the threads of a slot sum its entries over the blocks it reaches, each
+            // thread a few of the components (eight term groups per slot). (Consecutive slots per lane and
+            // a term group per 2^k lanes, which keeps the buffer reads in different banks, measured slower:
+            // the segment's length then fills the passes only partly.)
+            for (int w = tid; w < (s1 - s0) * kTermGroups; w += kThreads) {
+                const int q = w & (kTermGroups - 1);
+                const int slot = s0 + (w >> 3);
+                const uint32_t m0 = static_cast<uint32_t>(s_bm[slot]);
                 if (m0) {
                     // components of term group q: the two position moments stay together (the conic
                     // applies to both at once)
                     int ks[3];
                     flush_terms<NV, kTermGroups>(q, ks);
                     float v[3] = {0.f, 0.f, 0.f};
-                    const unsigned long long below_j = (1ull << j) - 1ull;  // j < 64
                     uint32_t m = m0;
                     while (m) {
                         const int b2 = __builtin_ctz(m);
                         m &= m - 1u;
-                        const int e2 = ent_rot(__popcll(seg_bits(b2) & below_j), b2, kSeg);  // the slot's entry
+                        const int e2 = ent_rot(static_cast<int>(s_epos[slot][b2]), b2, kSeg);  // the slot's entry
 #pragma unroll
                         for (int i = 0; i < 3; i++)
                             if (ks[i] >= 0) v[i] += s_ent[b2][ks[i]][e2];
@@ -686,6 +765,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                 }
             }
             __syncthreads();  // the next segment overwrites the entries and the group lists
+            s0 = s1;
         }
     }
     if (STATS && lane == 0) {
