@@ -202,6 +202,56 @@ def test_raster_fwd_bitexact_bwd_close(gpu, oracle, case):
         assert rel_l2(gc2[k], ga[k]) <= 1e-5
 
 
+def extreme_splats(seed, n=400, width=80, height=56):
+    """Splats of every shape the rasterisers' block lists must keep or drop correctly: needle-thin ellipses
+    (aspect up to 1000:1) at every angle, sub-pixel and image-sized footprints, opacities from just above
+    1/255 (tiny cutoffs) to 0.99, centres inside, on tile and block edges and outside the image. Every
+    tile's list holds every splat (index order), so the lists, not the intersection test, decide which
+    pairs are evaluated."""
+    r = inputs.rng(seed)
+    s1 = np.exp(r.uniform(np.log(0.15), np.log(60.0), n))
+    s2 = s1 * np.exp(r.uniform(np.log(1e-3), 0.0, n))
+    th = r.uniform(0.0, np.pi, n)
+    c, s = np.cos(th), np.sin(th)
+    cxx = c * c * s1 ** 2 + s * s * s2 ** 2
+    cyy = s * s * s1 ** 2 + c * c * s2 ** 2
+    cxy = c * s * (s1 ** 2 - s2 ** 2)
+    det = cxx * cyy - cxy ** 2
+    conics = np.stack([cyy / det, -cxy / det, cxx / det], 1).astype(np.float32)[None]
+    means = np.stack([r.uniform(-10, width + 10, n), r.uniform(-10, height + 10, n)], 1)
+    snap = r.uniform(size=n) < 0.3  # a share of centres exactly on a 4-pixel block or tile boundary
+    means[snap] = np.round(means[snap] / 4.0) * 4.0
+    opac = np.exp(r.uniform(np.log(1.05 / 255.0), np.log(0.99), n)).astype(np.float32)[None]
+    tw, th_ = (width + 15) // 16, (height + 15) // 16
+    n_tiles = tw * th_
+    flat = np.tile(np.arange(n, dtype=np.int32), n_tiles)
+    off = (np.arange(n_tiles, dtype=np.int32) * n).reshape(1, th_, tw)
+    colors = r.uniform(0.0, 1.0, (1, n, 3)).astype(np.float32)
+    return dict(means2d=means.astype(np.float32)[None], conics=conics, colors=colors, opacities=opac,
+                isect_offsets=off, flatten_ids=flat, I=1, N=n, n_isects=int(flat.size), width=width, height=height,
+                tile_width=tw, tile_height=th_)
+
+
+@pytest.mark.parametrize("seed", [3, 4, 5])
+def test_raster_extreme_shapes(gpu, oracle, seed):
+    """The block lists (bounding box and exact per-row ellipse ranges) must keep every block a splat's
+    cutoff set reaches: any block dropped wrongly changes a pixel of the bit-exact forward."""
+    kw = extreme_splats(seed)
+    a = gpu.rasterize_fwd(**kw)
+    b = oracle.rasterize_fwd(**kw)
+    assert b["render_alphas"].max() > 0.5
+    for k in ("render_colors", "render_alphas", "last_ids"):
+        assert same_bits(a[k], b[k]), k
+    r = inputs.rng(seed + 100)
+    gin = dict(render_alphas=b["render_alphas"], last_ids=b["last_ids"],
+               v_render_colors=r.standard_normal(b["render_colors"].shape).astype(np.float32),
+               v_render_alphas=r.standard_normal(b["render_alphas"].shape).astype(np.float32))
+    ga = gpu.rasterize_bwd(absgrad=False, **gin, **kw)
+    gb = oracle.rasterize_bwd(absgrad=False, **gin, **kw)
+    for k in ("v_means2d", "v_conics", "v_colors", "v_opacities"):
+        assert rel_l2(ga[k], gb[k]) <= 1e-4, (k, rel_l2(ga[k], gb[k]))
+
+
 def test_raster_empty_and_background(gpu, oracle):
     kw = inputs.raster_kwargs(oracle, seed=43, backgrounds=True)
     kw["n_isects"] = 0
