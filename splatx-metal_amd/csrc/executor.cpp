@@ -72,7 +72,7 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->dkey_b.alloc(R);
             e->order_a.alloc(R);
             e->order_b.alloc(R);
-            e->n_vis.alloc(4);
+            e->n_vis.alloc(5);
             e->vis_part.alloc(4 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
             e->blk_base.alloc(2 * static_cast<size_t>(sxk::step_preprocess_blocks(desc->arena_rows)));
             e->emit_list.alloc(R);
@@ -80,6 +80,7 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
             for (int k = 0; k < kMaxEvents; k++) SXH_HIP(hipEventCreate(&e->ev[k]));
+            SXH_HIP(hipEventCreateWithFlags(&e->count_ev, hipEventDisableTiming));
             SXH_HIP(hipStreamSynchronize(b->stream));
         } catch (...) {
             delete e;
@@ -94,6 +95,7 @@ void sxh_exec_destroy(sxh_executor* e) {
     (void)hipStreamSynchronize(e->b->stream);
     for (int k = 0; k < kMaxEvents; k++)
         if (e->ev[k]) (void)hipEventDestroy(e->ev[k]);
+    if (e->count_ev) (void)hipEventDestroy(e->count_ev);
     for (auto& row : e->graph_b)
         for (hipGraphExec_t x : row)
             if (x) (void)hipGraphExecDestroy(x);
@@ -258,24 +260,33 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     const sxk::Arena A = e->arena();
 
     // ---- segment A: preprocess + counts -----------------------------------------------------------
-    if (e->prof_stats) SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
-    e->mark("start");
-    sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p, s);
-    e->mark("preprocess");
+    // `cap`: the intersection capacity segment B may assume; past it, segment B's counts read 0 and the
+    // arena update is skipped (n_vis words 3 and 4), so a segment B launched before the count is known
+    // leaves everything as it was and the step runs again on grown buffers
     int64_t* hs = static_cast<int64_t*>(e->host_small.p);
-    // visible count, intersection total
-    SXH_HIP(hipMemcpyAsync(&hs[0], e->n_vis.p, 16, hipMemcpyDeviceToHost, s));
+    auto launch_a = [&](unsigned long long cap) {
+        if (e->prof_stats)
+            SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
+        e->mark("start");
+        sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
+                             cap, s);
+        e->mark("preprocess");
+        // visible count, intersection total
+        SXH_HIP(hipMemcpyAsync(&hs[0], e->n_vis.p, 16, hipMemcpyDeviceToHost, s));
+    };
     const float* gt = nullptr;
-    if (!fwd_only) {
+    auto upload_gt = [&]() {
+        if (fwd_only) return;
         if (use_gt_cache) {
             gt = e->gt_cache.p + static_cast<size_t>(in->gt_index) * n_px;
         } else {
             SXH_HIP(hipMemcpyAsync(e->gt_stage.p, in->gt_rgb, n_px * 4, hipMemcpyHostToDevice, s));
             gt = e->gt_stage.p;
         }
-    }
-    SXH_HIP(hipGetLastError());
-    const int64_t* n_isects_dev = reinterpret_cast<const int64_t*>(e->n_vis.p) + 1;
+    };
+    // the intersection count segment B reads (0 after an overflow), and the overflow word
+    const int64_t* n_isects_dev = reinterpret_cast<const int64_t*>(e->n_vis.p) + 3;
+    const unsigned long long* overflow_dev = e->n_vis.p + 4;
     float* hloss = reinterpret_cast<float*>(&hs[3]);
     *hloss = 0.0f;
     int n_l1 = 0, n_ss = 0;
@@ -387,16 +398,16 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
                                  e->long_list.p, e->long_count.p, s, n_emit_i);
         e->mark("gather");
-        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s);
+        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s, overflow_dev);
         e->mark("postprocess");
         sxk::step_loss_final(e->l1_part.p, n_l1, e->ssim_part.p, n_ss, static_cast<double>(n_px),
                              static_cast<double>(map_n), e->d.ssim_weight, use_ssim ? 1 : 0, e->loss_dev.p, s);
         e->mark("loss");
     };
-    // Segment B as a hipGraph (captured while the GPU runs segment A, replayed after the count; an
-    // executable graph per step kind is updated in place while the step's shape stays the same), unless
-    // per-kernel profiling is on or the capacity is past what the device-count sort handles.
-    const bool graph = e->use_graph && !e->prof && e->isect_cap < (size_t{1} << 30);
+    // Segment B as a hipGraph (captured while the GPU runs segment A; an executable graph per step kind
+    // is updated in place while the step's shape stays the same), unless per-kernel profiling is on or
+    // the capacity is past what the device-count sort handles.
+    auto graph_ok = [&]() { return e->use_graph && !e->prof && e->isect_cap < (size_t{1} << 30); };
     auto capture_b = [&]() {
         hipGraph_t g = nullptr;
         SXH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -426,40 +437,70 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             SXH_HIP(hipGraphDestroy(g));
         }
     };
-    if (graph) capture_b();
+    uint32_t* hsort = reinterpret_cast<uint32_t*>(&hs[4]);
+    uint32_t* hmax = reinterpret_cast<uint32_t*>(&hs[5]);
+    // the step's read-backs, after segment B
+    auto launch_tail = [&]() {
+        if (!fwd_only) SXH_HIP(hipMemcpyAsync(hloss, e->loss_dev.p, 4, hipMemcpyDeviceToHost, s));
+        *hsort = 0;
+        SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p), 4, hipMemcpyDeviceToHost, s));
+        *hmax = 0;
+        SXH_HIP(hipMemcpyAsync(hmax, e->max_tile.p, 4, hipMemcpyDeviceToHost, s));
+        if (render_to_dev)
+            SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
+        if (out->render_colors)
+            SXH_HIP(hipMemcpyAsync(out->render_colors, e->render.p, n_px * 4, hipMemcpyDeviceToHost, s));
+        SXH_HIP(hipGetLastError());
+    };
 
     // ---- sync 1: n_isects (MetalBackend.cpp:1849-1858) --------------------------------------------
-    auto t0 = std::chrono::steady_clock::now();
-    SXH_HIP(hipStreamSynchronize(s));
-    e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    const int64_t n_isects = hs[1];
+    // With a graph, segment B is queued behind segment A before the host waits for the count (an event
+    // after the count's copy), so the GPU does not idle through the host's wake-up. If the count
+    // exceeds the capacity that segment B ran with (nothing done, arena untouched), the step runs again
+    // the plain way: sync on the count, grow, capture, launch.
+    int64_t n_isects = 0;
+    bool done = false;
+    e->sync_ms[0] = 0.0;
+    if (graph_ok()) {
+        const unsigned long long cap = e->isect_cap;
+        launch_a(cap);
+        upload_gt();
+        SXH_HIP(hipEventRecord(e->count_ev, s));
+        capture_b();
+        SXH_HIP(hipGraphLaunch(e->graph_b[index_first ? 1 : 0][fwd_only ? 1 : 0], s));
+        launch_tail();
+        const auto t0 = std::chrono::steady_clock::now();
+        SXH_HIP(hipEventSynchronize(e->count_ev));
+        e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        n_isects = hs[1];
+        validate_n_isects_readback(n_isects, what);
+        done = static_cast<unsigned long long>(n_isects) <= cap;
+        if (!done) SXH_HIP(hipStreamSynchronize(s));  // the overflowed pass ends before the buffers move
+    } else {
+        upload_gt();
+    }
+    if (!done) {
+        launch_a(~0ull);
+        const auto t0 = std::chrono::steady_clock::now();
+        SXH_HIP(hipStreamSynchronize(s));
+        e->sync_ms[0] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        n_isects = hs[1];
+        validate_n_isects_readback(n_isects, what);
+        e->mark("sync1");
+        e->ensure_isect(static_cast<size_t>(n_isects));
+        if (graph_ok()) {
+            capture_b();
+            SXH_HIP(hipGraphLaunch(e->graph_b[index_first ? 1 : 0][fwd_only ? 1 : 0], s));
+        } else {
+            launch_b(n_isects, nullptr);
+        }
+        launch_tail();
+    }
     out->n_isects = n_isects;
     out->sort_key_bits = 32 + c.tile_n_bits;
     out->n_visible = hs[0];
-    validate_n_isects_readback(n_isects, what);
-    e->mark("sync1");
-    const bool grown = static_cast<size_t>(n_isects) > e->isect_cap;
-    if (grown) e->ensure_isect(static_cast<size_t>(n_isects));
-    if (graph && e->isect_cap < (size_t{1} << 30)) {
-        if (grown) capture_b();  // new buffers: the captured graph is stale
-        SXH_HIP(hipGraphLaunch(e->graph_b[index_first ? 1 : 0][fwd_only ? 1 : 0], s));
-    } else {
-        launch_b(n_isects, nullptr);
-    }
-    if (!fwd_only) SXH_HIP(hipMemcpyAsync(hloss, e->loss_dev.p, 4, hipMemcpyDeviceToHost, s));
-    uint32_t* hsort = reinterpret_cast<uint32_t*>(&hs[4]);
-    *hsort = 0;
-    SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p), 4, hipMemcpyDeviceToHost, s));
-    uint32_t* hmax = reinterpret_cast<uint32_t*>(&hs[5]);
-    *hmax = 0;
-    SXH_HIP(hipMemcpyAsync(hmax, e->max_tile.p, 4, hipMemcpyDeviceToHost, s));
-    if (render_to_dev)
-        SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
-    if (out->render_colors)
-        SXH_HIP(hipMemcpyAsync(out->render_colors, e->render.p, n_px * 4, hipMemcpyDeviceToHost, s));
-    SXH_HIP(hipGetLastError());
     // ---- sync 2: loss (MetalBackend.cpp:2241-2261) ----------------------------------------------------
-    t0 = std::chrono::steady_clock::now();
+    const auto t0 = std::chrono::steady_clock::now();
     SXH_HIP(hipStreamSynchronize(s));
     e->sync_ms[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     out->loss = fwd_only ? 0.0f : *hloss;

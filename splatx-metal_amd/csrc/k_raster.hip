@@ -459,8 +459,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     const int num_batches = (num + kThreads - 1) / kThreads;
     // a group's reduction leaves slot A in lane 0, B in 8, C in 4, D in 12: those lanes store them
     const int wslot = (r == 0) ? 0 : (r == 8) ? 1 : (r == 4) ? 2 : (r == 12) ? 3 : -1;
-    // blocks of this wave's four groups (for the lockstep chunk count)
-    const int wb0 = block_of(wave, 0), wb1 = block_of(wave, 16), wb2 = block_of(wave, 32), wb3 = block_of(wave, 48);
     // STATS only (wave-uniform)
     unsigned long long st_chunks = 0, st_entries = 0, st_empty = 0, st_cut = 0, st_contrib = 0;
     for (int b = 0; b < num_batches; b++) {

@@ -147,13 +147,17 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
 }
 
 // One workgroup over the preprocess blocks' {visible, tiles, Gaussians with tiles} counts: the totals
-// (out = {u64 visible, u64 intersections, u64 Gaussians with tiles}) and, per block b, the
-// intersections and the Gaussians with tiles of the blocks before it (base[2 b], base[2 b + 1]).
+// (out = {u64 visible, u64 intersections, u64 Gaussians with tiles, u64 intersections, u64 overflow})
+// and, per block b, the intersections and the Gaussians with tiles of the blocks before it (base[2 b],
+// base[2 b + 1]). When the intersections exceed `cap` (the buffers' capacity) the step's later kernels
+// must not run: overflow = 1 and out[2] = out[3] = 0, the counts they read, so that every one of them
+// finds nothing to do (out[1] keeps the true total for the host).
 constexpr int kScanBlock = 1024;
 constexpr int kScanPer = 8;  // consecutive blocks per thread and chunk
 __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restrict__ part, int n,
                                                            unsigned long long* __restrict__ out,
-                                                           unsigned long long* __restrict__ base) {
+                                                           unsigned long long* __restrict__ base,
+                                                           unsigned long long cap) {
     __shared__ unsigned long long s_i[kScanBlock / 64], s_e[kScanBlock / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     unsigned long long vis = 0, carry_i = 0, carry_e = 0;
@@ -212,9 +216,12 @@ __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restri
     if (tid == 0) {
         unsigned long long v = 0;
         for (int w = 0; w < kScanBlock / 64; w++) v += s_i[w];
+        const bool ovf = carry_i > cap;
         out[0] = v;
         out[1] = carry_i;
-        out[2] = carry_e;
+        out[2] = ovf ? 0ull : carry_e;
+        out[3] = ovf ? 0ull : carry_i;
+        out[4] = ovf ? 1ull : 0ull;
     }
 }
 
@@ -503,7 +510,9 @@ __global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ k
 template <int NC>
 __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, const float4* __restrict__ splats,
                                                         const float4* __restrict__ grads,
-                                                        const uint8_t* __restrict__ touched) {
+                                                        const uint8_t* __restrict__ touched,
+                                                        const unsigned long long* __restrict__ skip) {
+    if (skip && *skip) return;  // the step overflowed its buffers and runs again: leave the arena as it was
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= c.count) return;
     const size_t R = static_cast<size_t>(A.rows);
@@ -740,7 +749,7 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* n_visible, unsigned long long* block_base,
-                     hipStream_t s) {
+                     unsigned long long isect_cap, hipStream_t s) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
@@ -751,7 +760,7 @@ void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
-                       static_cast<int>(grid.x), n_visible, block_base);
+                       static_cast<int>(grid.x), n_visible, block_base, isect_cap);
 }
 
 void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
@@ -801,14 +810,14 @@ void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* of
 }
 
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
-                      const uint8_t* touched, hipStream_t s) {
+                      const uint8_t* touched, hipStream_t s, const unsigned long long* skip) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
-        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads, touched); break;
-        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads, touched); break;
-        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads, touched); break;
-        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads, touched); break;
+        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
+        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
+        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
+        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
         default: throw std::invalid_argument("postprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
 }

@@ -92,6 +92,7 @@ struct sxh_executor {
     sxh::DevBuf<unsigned long long> rstats;
     sxh_raster_stats rstats_host{};
     hipEvent_t ev[kMaxEvents] = {};
+    hipEvent_t count_ev = nullptr;  // recorded after the step's count read-back
     const char* ev_name[kMaxEvents] = {};
     int n_ev = 0;
     sxh_exec_timing timing{};

@@ -44,12 +44,14 @@ struct StepConst {
     float noise_scale;
 };
 
-// vis_part: 4 u32 per block (visible count, tile count, count of Gaussians with tiles, 0); out_vis:
-// {u64 visible count, u64 intersections, u64 Gaussians with tiles}; block_base: per block, the
-// intersections and the Gaussians with tiles of the blocks before it (2 u64)
+// vis_part: 4 u32 per block (visible count, tile count, count of Gaussians with tiles, 0); out_vis (5
+// u64): {visible count, intersections, Gaussians with tiles, intersections, overflow}, where overflow =
+// intersections > isect_cap and then words 2 and 3 read 0 (the counts the rest of the step reads, so
+// that it does nothing); block_base: per block, the intersections and the Gaussians with tiles of the
+// blocks before it (2 u64)
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
-                     hipStream_t s);
+                     unsigned long long isect_cap, hipStream_t s);
 // number of blocks of step_preprocess
 int step_preprocess_blocks(int64_t count);
 // The Gaussians with tiles in index order (list[j], j below out_vis[2]) and (cum set) cum[j], the
@@ -76,8 +78,9 @@ void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* of
                        const int64_t* n_dev = nullptr);
 void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev = nullptr);
+// skip (when set): a device word; nonzero leaves the arena untouched (the overflow word of out_vis)
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
-                      const uint8_t* touched, hipStream_t s);
+                      const uint8_t* touched, hipStream_t s, const unsigned long long* skip = nullptr);
 // Noise only (the forward-only path never calls it; a training step fuses it into postprocess).
 // L1 gradient without SSIM: v_render = sign(render - gt) / n, per-block f64 sums of |render - gt|.
 void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_render, double* partials,
