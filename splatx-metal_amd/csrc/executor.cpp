@@ -263,16 +263,17 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     // `cap`: the intersection capacity segment B may assume; past it, segment B's counts read 0 and the
     // arena update is skipped (n_vis words 3 and 4), so a segment B launched before the count is known
     // leaves everything as it was and the step runs again on grown buffers
-    int64_t* hs = static_cast<int64_t*>(e->host_small.p);
+    // the step's read-back block: u64 visible, u64 intersections (stored by segment A's last kernel), u32
+    // loss bits, sort error flag, largest tile (stored by segment B's last kernel)
+    volatile unsigned long long* const hc = static_cast<volatile unsigned long long*>(e->step_rb.p);
+    volatile uint32_t* const hw = reinterpret_cast<volatile uint32_t*>(hc + 2);
     auto launch_a = [&](unsigned long long cap) {
         if (e->prof_stats)
             SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
         e->mark("start");
         sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
-                             cap, s);
+                             cap, static_cast<unsigned long long*>(e->step_rb.dev), s);
         e->mark("preprocess");
-        // visible count, intersection total
-        SXH_HIP(hipMemcpyAsync(&hs[0], e->n_vis.p, 16, hipMemcpyDeviceToHost, s));
     };
     const float* gt = nullptr;
     auto upload_gt = [&]() {
@@ -287,8 +288,6 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     // the intersection count segment B reads (0 after an overflow), and the overflow word
     const int64_t* n_isects_dev = reinterpret_cast<const int64_t*>(e->n_vis.p) + 3;
     const unsigned long long* overflow_dev = e->n_vis.p + 4;
-    float* hloss = reinterpret_cast<float*>(&hs[3]);
-    *hloss = 0.0f;
     int n_l1 = 0, n_ss = 0;
     int32_t* flat = e->vals_a.p;
     // index-first needs every tile's list in LDS (4096 entries) to be fast; larger tiles still sort
@@ -373,7 +372,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         ra.tile_order = e->tile_order.p;
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
         e->mark("raster_fwd");
-        if (fwd_only) return;
+        const sxk::StepReadback rb{sxk::sort_error_flag(e->sort_scratch.p), e->max_tile.p,
+                                   reinterpret_cast<uint32_t*>(static_cast<unsigned long long*>(e->step_rb.dev) + 2)};
+        if (fwd_only) {
+            sxk::step_readback(rb, s);
+            return;
+        }
         if (use_ssim) {
             n_ss = sxk::ssim_fwd_blocks(1, H, W, 3);
             sxk::ssim_fwd(e->render.p, gt, 1, H, W, 3, 1, nullptr, e->cmu.p, e->csg.p, e->ccr.p, e->ssim_part.p, s);
@@ -401,7 +405,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s, overflow_dev);
         e->mark("postprocess");
         sxk::step_loss_final(e->l1_part.p, n_l1, e->ssim_part.p, n_ss, static_cast<double>(n_px),
-                             static_cast<double>(map_n), e->d.ssim_weight, use_ssim ? 1 : 0, e->loss_dev.p, s);
+                             static_cast<double>(map_n), e->d.ssim_weight, use_ssim ? 1 : 0, e->loss_dev.p, s, rb);
         e->mark("loss");
     };
     // Segment B as a hipGraph (captured while the GPU runs segment A; an executable graph per step kind
@@ -437,15 +441,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             SXH_HIP(hipGraphDestroy(g));
         }
     };
-    uint32_t* hsort = reinterpret_cast<uint32_t*>(&hs[4]);
-    uint32_t* hmax = reinterpret_cast<uint32_t*>(&hs[5]);
-    // the step's read-backs, after segment B
+    // the render's copies, after segment B
     auto launch_tail = [&]() {
-        if (!fwd_only) SXH_HIP(hipMemcpyAsync(hloss, e->loss_dev.p, 4, hipMemcpyDeviceToHost, s));
-        *hsort = 0;
-        SXH_HIP(hipMemcpyAsync(hsort, sxk::sort_error_flag(e->sort_scratch.p), 4, hipMemcpyDeviceToHost, s));
-        *hmax = 0;
-        SXH_HIP(hipMemcpyAsync(hmax, e->max_tile.p, 4, hipMemcpyDeviceToHost, s));
         if (render_to_dev)
             SXH_HIP(hipMemcpyAsync(render_to_dev, e->render.p, n_px * 4, hipMemcpyDeviceToDevice, s));
         if (out->render_colors)
@@ -472,7 +469,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         const auto t0 = std::chrono::steady_clock::now();
         SXH_HIP(hipEventSynchronize(e->count_ev));
         e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        n_isects = hs[1];
+        n_isects = static_cast<int64_t>(hc[1]);
         validate_n_isects_readback(n_isects, what);
         done = static_cast<unsigned long long>(n_isects) <= cap;
         if (!done) SXH_HIP(hipStreamSynchronize(s));  // the overflowed pass ends before the buffers move
@@ -484,7 +481,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         const auto t0 = std::chrono::steady_clock::now();
         SXH_HIP(hipStreamSynchronize(s));
         e->sync_ms[0] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-        n_isects = hs[1];
+        n_isects = static_cast<int64_t>(hc[1]);
         validate_n_isects_readback(n_isects, what);
         e->mark("sync1");
         e->ensure_isect(static_cast<size_t>(n_isects));
@@ -498,13 +495,16 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     }
     out->n_isects = n_isects;
     out->sort_key_bits = 32 + c.tile_n_bits;
-    out->n_visible = hs[0];
+    out->n_visible = static_cast<int64_t>(hc[0]);
     // ---- sync 2: loss (MetalBackend.cpp:2241-2261) ----------------------------------------------------
     const auto t0 = std::chrono::steady_clock::now();
     SXH_HIP(hipStreamSynchronize(s));
     e->sync_ms[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
-    out->loss = fwd_only ? 0.0f : *hloss;
-    e->last_max_tile = n_isects > 0 ? static_cast<int64_t>(*hmax) : 0;
+    const uint32_t loss_bits = hw[0], sort_err = hw[1], max_tile = hw[2];
+    float loss = 0.0f;
+    std::memcpy(&loss, &loss_bits, 4);
+    out->loss = fwd_only ? 0.0f : loss;
+    e->last_max_tile = n_isects > 0 ? static_cast<int64_t>(max_tile) : 0;
     if (e->prof_stats) {
         unsigned long long st[sxk::kRasterStats];
         SXH_HIP(hipMemcpy(st, e->rstats.p, sizeof(st), hipMemcpyDeviceToHost));
@@ -513,7 +513,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
                                           st[sxk::kStatBwdEntries],     st[sxk::kStatBwdEmptyChunks],
                                           st[sxk::kStatBwdInCutoff],    st[sxk::kStatBwdContrib]};
     }
-    if (*hsort) throw std::runtime_error(std::string(what) + ": radix sort look-back did not complete");
+    if (sort_err) throw std::runtime_error(std::string(what) + ": radix sort look-back did not complete");
     if (e->prof) {
         sxh_exec_timing& t = e->timing;
         t.n = 0;

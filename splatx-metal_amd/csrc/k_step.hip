@@ -152,12 +152,18 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
 // base[2 b + 1]). When the intersections exceed `cap` (the buffers' capacity) the step's later kernels
 // must not run: overflow = 1 and out[2] = out[3] = 0, the counts they read, so that every one of them
 // finds nothing to do (out[1] keeps the true total for the host).
+// a store into mapped host memory, at system scope (no GPU cache keeps it from the host)
+template <class T>
+__device__ __forceinline__ void store_host(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 constexpr int kScanBlock = 1024;
 constexpr int kScanPer = 8;  // consecutive blocks per thread and chunk
 __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restrict__ part, int n,
                                                            unsigned long long* __restrict__ out,
                                                            unsigned long long* __restrict__ base,
-                                                           unsigned long long cap) {
+                                                           unsigned long long cap,
+                                                           unsigned long long* __restrict__ host) {
     __shared__ unsigned long long s_i[kScanBlock / 64], s_e[kScanBlock / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     unsigned long long vis = 0, carry_i = 0, carry_e = 0;
@@ -222,6 +228,10 @@ __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restri
         out[2] = ovf ? 0ull : carry_e;
         out[3] = ovf ? 0ull : carry_i;
         out[4] = ovf ? 1ull : 0ull;
+        if (host) {
+            store_host(&host[0], v);
+            store_host(&host[1], carry_i);
+        }
     }
 }
 
@@ -719,14 +729,27 @@ __device__ double block_sum_fixed(const double* __restrict__ p, int n, double* s
 
 __global__ void __launch_bounds__(kBlock) k_loss_final(const double* __restrict__ l1p, int n_l1,
                                                        const double* __restrict__ ssp, int n_ss, double n_px, double M,
-                                                       float lam, int use_ssim, float* __restrict__ out) {
+                                                       float lam, int use_ssim, float* __restrict__ out,
+                                                       StepReadback rb) {
     __shared__ double s_red[kBlock];
     const double l1s = block_sum_fixed(l1p, n_l1, s_red);
     const double sss = use_ssim ? block_sum_fixed(ssp, n_ss, s_red) : 0.0;
     if (threadIdx.x == 0) {
         const float l1 = static_cast<float>(l1s / n_px);
-        out[0] = use_ssim ? (1.0f - lam) * l1 + lam * (1.0f - static_cast<float>(sss / M)) : l1;
+        const float loss = use_ssim ? (1.0f - lam) * l1 + lam * (1.0f - static_cast<float>(sss / M)) : l1;
+        out[0] = loss;
+        if (rb.host) {
+            store_host(&rb.host[0], __float_as_uint(loss));
+            store_host(&rb.host[1], *rb.sort_err);
+            store_host(&rb.host[2], *rb.max_tile);
+        }
     }
+}
+
+__global__ void k_step_readback(StepReadback rb) {
+    store_host(&rb.host[0], 0u);
+    store_host(&rb.host[1], *rb.sort_err);
+    store_host(&rb.host[2], *rb.max_tile);
 }
 
 __global__ void __launch_bounds__(kBlock) k_aos_to_soa(const float* __restrict__ aos, float* __restrict__ soa, int rows,
@@ -749,7 +772,7 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* n_visible, unsigned long long* block_base,
-                     unsigned long long isect_cap, hipStream_t s) {
+                     unsigned long long isect_cap, unsigned long long* host_counts, hipStream_t s) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
@@ -760,7 +783,7 @@ void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
-                       static_cast<int>(grid.x), n_visible, block_base, isect_cap);
+                       static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts);
 }
 
 void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
@@ -831,8 +854,14 @@ void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_rend
 }
 
 void step_loss_final(const double* l1p, int n_l1, const double* ssp, int n_ss, double n_px, double M, float lam,
-                     int use_ssim, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(kBlock), 0, s, l1p, n_l1, ssp, n_ss, n_px, M, lam, use_ssim, out);
+                     int use_ssim, float* out, hipStream_t s, const StepReadback& rb) {
+    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(kBlock), 0, s, l1p, n_l1, ssp, n_ss, n_px, M, lam, use_ssim, out,
+                       rb);
+}
+
+void step_readback(const StepReadback& rb, hipStream_t s) {
+    if (!rb.host) return;
+    hipLaunchKernelGGL(k_step_readback, dim3(1), dim3(1), 0, s, rb);
 }
 
 void aos_to_soa(const float* aos, float* soa, int rows, int dim, int stride, hipStream_t s) {

@@ -17,7 +17,11 @@ namespace sxh_detail {
 
 struct PinnedHost {
     void* p = nullptr;
-    explicit PinnedHost(size_t bytes) { SXH_HIP(hipHostMalloc(&p, bytes, hipHostMallocDefault)); }
+    void* dev = nullptr;  // the device's address of the block (mapped memory)
+    explicit PinnedHost(size_t bytes, unsigned flags = hipHostMallocDefault) {
+        SXH_HIP(hipHostMalloc(&p, bytes, flags));
+        if (flags & hipHostMallocMapped) SXH_HIP(hipHostGetDevicePointer(&dev, p, 0));
+    }
     ~PinnedHost() {
         if (p) (void)hipHostFree(p);
     }
@@ -73,6 +77,9 @@ struct sxh_executor {
     int gt_n = 0, gt_w = 0, gt_h = 0;
     sxh::DevBuf<float> staging;
     PinnedHost host_small{64};
+    // the step's counts and read-back words, stored by its kernels (coherent, mapped): u64 visible, u64
+    // intersections, then u32 loss bits, sort error flag, largest tile's entry count
+    PinnedHost step_rb{64, hipHostMallocMapped | hipHostMallocCoherent};
     // device MCMC refine (allocated on the first refine, arena-sized)
     sxh::DevBuf<float> mc_op_act, mc_new_logit, mc_new_log_scale, mc_binoms;
     sxh::DevBuf<int32_t> mc_dead, mc_alive, mc_sampled;

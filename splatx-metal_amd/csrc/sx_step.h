@@ -49,9 +49,10 @@ struct StepConst {
 // intersections > isect_cap and then words 2 and 3 read 0 (the counts the rest of the step reads, so
 // that it does nothing); block_base: per block, the intersections and the Gaussians with tiles of the
 // blocks before it (2 u64)
+// host_counts (mapped host memory, may be null) receives words 0 and 1 of out_vis.
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
-                     unsigned long long isect_cap, hipStream_t s);
+                     unsigned long long isect_cap, unsigned long long* host_counts, hipStream_t s);
 // number of blocks of step_preprocess
 int step_preprocess_blocks(int64_t count);
 // The Gaussians with tiles in index order (list[j], j below out_vis[2]) and (cum set) cum[j], the
@@ -91,9 +92,21 @@ void step_ssim_bwd_l1(const float* render, const float* gt, const float* cmu, co
                       const float* ccr, int H, int W, float G, float w_l1, float g_l1, float* v_render,
                       double* l1_partials, hipStream_t s);
 int step_ssim_bwd_blocks(int H, int W);
-// loss = (1-lam) * float(l1_sum / n_px) + lam * (1 - float(ssim_sum / M)) (or the L1 alone)
+// The words a step reports to the host, stored by its last kernel straight into mapped host memory
+// (host: 3 u32, the loss bits, the sort's error flag, the largest tile's entry count) instead of one
+// copy each. Null host: nothing is stored.
+struct StepReadback {
+    const uint32_t* sort_err = nullptr;
+    const uint32_t* max_tile = nullptr;
+    uint32_t* host = nullptr;
+};
+// loss = (1-lam) * float(l1_sum / n_px) + lam * (1 - float(ssim_sum / M)) (or the L1 alone); with
+// rb.host set, the loss and rb's words also go to the host
 void step_loss_final(const double* l1_partials, int n_l1, const double* ssim_partials, int n_ssim,
-                     double n_px, double M, float lam, int use_ssim, float* loss_out, hipStream_t s);
+                     double n_px, double M, float lam, int use_ssim, float* loss_out, hipStream_t s,
+                     const StepReadback& rb = {});
+// rb's words to the host without a loss (the loss word is 0): the forward-only step
+void step_readback(const StepReadback& rb, hipStream_t s);
 void aos_to_soa(const float* aos, float* soa, int rows, int dim, int stride, hipStream_t s);
 void soa_to_aos(const float* soa, float* aos, int rows, int dim, int stride, hipStream_t s);
 
