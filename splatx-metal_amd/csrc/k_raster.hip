@@ -43,7 +43,7 @@ constexpr int kBwdSeg = SX_BWD_SEG;
 
 // sxm::expf_fast(-sigma) without its range branches: identical for sigma in [0, 86] (no overflow,
 // no subnormal scaling). Only an opacity above ~1e35 pushes a cutoff past that range; the callers
-// then take the general function for the whole wave.
+// then take the general function for the whole batch of splats.
 __device__ __forceinline__ float exp_neg_poly(float sigma) {
     const float x = -sigma;
     const float kf = __builtin_rintf(x * 1.44269502f);
@@ -170,6 +170,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     __shared__ __align__(16) uint8_t s_list[kBlocks][kThreads];
     __shared__ int s_bc[kBlocks][4];
     __shared__ int s_len[kBlocks];
+    __shared__ unsigned long long s_gen[kThreads / 64];  // per wave: the batch's splats past the polynomial's range
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
     const int tile = a.tile_order ? a.tile_order[blockIdx.x % n_tiles] : static_cast<int>(blockIdx.x % n_tiles);
@@ -205,6 +206,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
         if (__syncthreads_count(done) == kThreads) break;  // also the barrier before LDS reuse
         const int32_t idx = bstart + tid;
         uint32_t bm = 0u;
+        bool big = false;
         if (idx < range_end) {
             const int32_t f = a.flatten_ids[idx];
             const int32_t g = a.id_of ? a.id_of[f] : f;
@@ -215,8 +217,16 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             s_con[tid] = con;
             s_rgb[tid] = a.splats[(size_t)g * 3 + 2];
             bm = block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
+            big = bm != 0u && xyo.w > 86.0f;
         }
-        build_block_lists(bm, s_list, s_bc, s_len);
+        {
+            const unsigned long long gb = __ballot(big);
+            if (lane == 0) s_gen[wave] = gb;
+        }
+        build_block_lists(bm, s_list, s_bc, s_len);  // (its barriers publish s_gen too)
+        // one choice of exponential for the batch: the branch-free polynomial unless some splat's cutoff
+        // exceeds its range (opacity above ~1e35)
+        const bool general = (s_gen[0] | s_gen[1] | s_gen[2] | s_gen[3]) != 0ull;
         // the groups walk their lists together (the iteration count is the wave's longest list); a
         // lane takes a pair through selects rather than branches, and stops once its T is spent
         const int len = s_len[bl];
@@ -257,7 +267,6 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
                 st_entries += __popcll(__ballot((lane & 15) == 0 && t0 >= 0)) + __popcll(__ballot((lane & 15) == 0 && t1 >= 0));
             }
             if (!__any(in0 | in1)) continue;  // uniform
-            const bool general = __any((in0 & (xyo0.w > 86.0f)) | (in1 & (xyo1.w > 86.0f)));
             const float vis0 = general ? sxm::expf_fast(-sg0) : exp_neg_poly(sg0);
             const float vis1 = general ? sxm::expf_fast(-sg1) : exp_neg_poly(sg1);
             // front to back: a lane that stopped at entry 0 takes nothing more
@@ -417,6 +426,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     __shared__ uint8_t s_epos[kThreads][kBlocks];     // [slot][block]: the slot's position in the block's list
     __shared__ uint16_t s_bm[kThreads];               // each batch slot's block mask
     __shared__ int32_t s_bbf[kBlocks];                // each block's last contributing intersection
+    __shared__ unsigned long long s_gen[4];           // per wave: the batch's splats past the polynomial's range
     const int n_tiles = a.tile_width * a.tile_height;
     const int img = blockIdx.x / n_tiles;
     const int tile = a.tile_order ? a.tile_order[blockIdx.x % n_tiles] : static_cast<int>(blockIdx.x % n_tiles);
@@ -467,6 +477,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
         const int32_t batch_size = min(kThreads, batch_end + 1 - range_start);
         const int32_t idx = batch_end - tid;
         uint32_t bm = 0u;
+        bool big = false;
         if (idx >= range_start) {
             const int32_t f = a.flatten_ids[idx];  // the Gaussian, or its emit position (id_of)
             const int32_t gid = a.id_of ? a.id_of[f] : f;
@@ -484,6 +495,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
 #pragma unroll
             for (int k = 0; k < kBlocks; k++)
                 if (idx > s_bbf[k]) bm &= ~(1u << k);
+            big = bm != 0u && xyo.w > 86.0f;
         }
         s_bm[tid] = static_cast<uint16_t>(bm);
 #pragma unroll
@@ -491,7 +503,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
             const unsigned long long bal = __ballot((bm >> k) & 1u);
             if (lane == 0) s_bits[k][wave] = bal;
         }
+        {
+            const unsigned long long gb = __ballot(big);
+            if (lane == 0) s_gen[wave] = gb;
+        }
         __syncthreads();
+        // one choice of exponential for the batch: the branch-free polynomial (or the hardware exp2 with
+        // the checks below) unless some splat's cutoff exceeds its range (opacity above ~1e35)
+        const bool general = (s_gen[0] | s_gen[1] | s_gen[2] | s_gen[3]) != 0ull;
 
         const int t_min = batch_end - bin_final;  // slots t >= t_min are at or before the lane's last contributor
         // The batch's slots are walked in segments [s0, s1), each ending before the slot of the entry
@@ -623,10 +642,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                     }
                     continue;
                 }
-                // one wave-uniform choice of exponential for the chunk: the branch-free polynomial unless
-                // some cutoff in use exceeds its range (opacity above ~1e35)
-                const bool general = __any((valid[0] & (xyo[0].w > 86.0f)) | (valid[1] & (xyo[1].w > 86.0f)) |
-                                           (valid[2] & (xyo[2].w > 86.0f)) | (valid[3] & (xyo[3].w > 86.0f)));
                 // The exponential's value only enters gradients (compared at a relative tolerance), so the
                 // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
                 // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at

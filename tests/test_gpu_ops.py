@@ -252,6 +252,34 @@ def test_raster_extreme_shapes(gpu, oracle, seed):
         assert rel_l2(ga[k], gb[k]) <= 1e-4, (k, rel_l2(ga[k], gb[k]))
 
 
+def test_raster_general_exponential(gpu, oracle):
+    """Opacities above ~1e35 put a splat's cutoff past the range of the rasterisers' branch-free
+    exponential (and at 5e37 make it infinite): the batches holding one take the general exponential,
+    so the forward stays bit-exact and the backward within tolerance."""
+    kw = extreme_splats(6)
+    r = inputs.rng(106)
+    # small footprints late in the order (their cutoff radius is ~13 standard deviations), so that most
+    # pixels still composite the other splats first
+    con = kw["conics"][0]
+    small = np.flatnonzero((np.minimum(con[:, 0], con[:, 2]) > 4.0) & (np.arange(kw["N"]) > kw["N"] // 3))
+    huge = r.choice(small, 8, replace=False)
+    op = kw["opacities"].copy()
+    op[0, huge[:6]] = np.exp(r.uniform(np.log(1e35), np.log(1e36), 6)).astype(np.float32)
+    op[0, huge[6:]] = 5e37
+    kw["opacities"] = op
+    a = gpu.rasterize_fwd(**kw)
+    b = oracle.rasterize_fwd(**kw)
+    for k in ("render_colors", "render_alphas", "last_ids"):
+        assert same_bits(a[k], b[k]), k
+    gin = dict(render_alphas=b["render_alphas"], last_ids=b["last_ids"],
+               v_render_colors=r.standard_normal(b["render_colors"].shape).astype(np.float32),
+               v_render_alphas=r.standard_normal(b["render_alphas"].shape).astype(np.float32))
+    ga = gpu.rasterize_bwd(absgrad=False, **gin, **kw)
+    gb = oracle.rasterize_bwd(absgrad=False, **gin, **kw)
+    for k in ("v_means2d", "v_conics", "v_colors", "v_opacities"):
+        assert rel_l2(ga[k], gb[k]) <= 1e-4, (k, rel_l2(ga[k], gb[k]))
+
+
 def test_raster_empty_and_background(gpu, oracle):
     kw = inputs.raster_kwargs(oracle, seed=43, backgrounds=True)
     kw["n_isects"] = 0
