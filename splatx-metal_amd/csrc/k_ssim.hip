@@ -174,10 +174,27 @@ __global__ void __launch_bounds__(256) k_ssim_bwd(const float* __restrict__ img1
     }
 }
 
-// Three-channel variants (the training images): one workgroup per 16x16 tile covers all three
-// channels, so every global load and store touches whole interleaved pixels (coalesced), and each
-// channel's passes run exactly as above (same tap order, same results).
+// Three-channel variants (the training images). The forward: one workgroup per 16x16 tile covers all
+// three channels, so every global load and store touches whole interleaved pixels, and each channel's
+// passes run exactly as above (same tap order, same results). The backward: one workgroup per 16 x 32
+// tile, the apron of all three channels staged at once (whole pixels again) and the passes run one
+// channel after another. The taller tile cuts the horizontal pass's apron rows (42 per 32 outputs
+// instead of 26 per 16), and both passes are register-blocked: a horizontal task reads the 14 inputs
+// of 4 consecutive columns once, a vertical thread the 12 rows of 2 consecutive outputs. The LDS
+// strides keep both passes free of bank conflicts: a horizontal wave takes one column group over 42
+// rows (odd row strides 27 and 17), and a half-wave of the vertical pass two row pairs 16 rows apart.
+// (The same tiling measured slower for the forward: its 5 sums per tap need 43 KB of LDS per
+// workgroup, which leaves 3 workgroups per CU.)
 constexpr int C3 = 3;
+constexpr int TW3 = 16, TH3 = 32;              // output tile
+constexpr int AW3 = TW3 + 10, AH3 = TH3 + 10;  // its apron: 26 x 42
+constexpr int SX3 = AW3 + 1;                   // row stride of the staged inputs (odd)
+constexpr int SH3 = TW3 + 1;                   // row stride of the horizontal sums (odd)
+constexpr int CG3 = 4;                         // columns per horizontal task (wave w: columns 4w..4w+3)
+static_assert(TW3 == CG3 * 4 && AH3 <= 64 && TH3 == 32, "one wave per column group, 16 row pairs");
+
+// the vertical pass's thread: column tx, rows 2 rg and 2 rg + 1
+__device__ __forceinline__ int vert_rg(int tid) { return (tid >> 5) + 8 * ((tid >> 4) & 1); }
 
 __global__ void __launch_bounds__(256) k_ssim_fwd3(const float* __restrict__ img1, const float* __restrict__ img2,
                                                    int H, int W, int need_coeffs, float* __restrict__ map,
@@ -295,15 +312,17 @@ __global__ void __launch_bounds__(256) k_ssim_bwd3(const float* __restrict__ img
                                                    float* __restrict__ v_img1, float w_l1, float g_l1,
                                                    double* __restrict__ l1_partials) {
     __shared__ double s_red[256];
-    __shared__ float d[3][C3][A][A + 1];
-    __shared__ float h[3][A][T + 1];
+    __shared__ float d[3][C3][AH3][SX3];
+    __shared__ float h[3][AH3][SH3];
     const int mh = H - 10, mw = W - 10;
     const int img = blockIdx.z;
-    const int oy = blockIdx.y * T, ox = blockIdx.x * T;
-    const int tid = threadIdx.y * T + threadIdx.x;
-    for (int k = tid; k < A * A * C3; k += 256) {
-        const int ay = k / (A * C3), rem = k % (A * C3);
-        const int ax = rem / C3, c = rem % C3;
+    const int oy = blockIdx.y * TH3, ox = blockIdx.x * TW3;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tx = tid & 15, rg = vert_rg(tid);
+    const int qx = ox + tx;
+    for (int k = tid; k < AH3 * AW3 * C3; k += 256) {
+        const int ay = k / (AW3 * C3), rem = k - ay * (AW3 * C3);
+        const int ax = rem / C3, c = rem - ax * C3;
         const int y = oy + ay - 10, x = ox + ax - 10;
         float a = 0.f, b = 0.f, e = 0.f;
         if (y >= 0 && y < mh && x >= 0 && x < mw) {
@@ -316,58 +335,77 @@ __global__ void __launch_bounds__(256) k_ssim_bwd3(const float* __restrict__ img
         d[1][c][ay][ax] = b;
         d[2][c][ay][ax] = e;
     }
-    const int qy = oy + threadIdx.y, qx = ox + threadIdx.x;
-    const bool in = qy < H && qx < W;
-    const size_t q0 = ihwc(img, in ? qy : 0, in ? qx : 0, 0, H, W, C3);
-    float xs[C3], ys[C3];
+    // the two output pixels' inputs, all three channels (whole interleaved pixels)
+    float xs[2][C3], ys[2][C3], vout[2][C3];
 #pragma unroll
-    for (int c = 0; c < C3; c++) {
-        xs[c] = in ? img1[q0 + c] : 0.f;
-        ys[c] = in ? img2[q0 + c] : 0.f;
+    for (int i = 0; i < 2; i++) {
+        const int qy = oy + 2 * rg + i;
+        const bool in = qy < H && qx < W;
+        const size_t q0 = ihwc(img, in ? qy : 0, in ? qx : 0, 0, H, W, C3);
+#pragma unroll
+        for (int c = 0; c < C3; c++) {
+            xs[i][c] = in ? img1[q0 + c] : 0.f;
+            ys[i][c] = in ? img2[q0 + c] : 0.f;
+        }
     }
-    float vout[C3];
     double l1 = 0.0;
 #pragma unroll
     for (int c = 0; c < C3; c++) {
-        __syncthreads();
-        for (int k = tid; k < A * T; k += 256) {
-            const int r = k / T, cx = k % T;
-            float s1 = 0.f, s2 = 0.f, s3 = 0.f;
+        __syncthreads();  // the staged maps are in; the previous channel's vertical pass is done with h
+        if (lane < AH3) {  // horizontal: row `lane`, columns CG3 * wave + j
+            const int r = lane, c0 = CG3 * wave;
 #pragma unroll
-            for (int u = 0; u < 11; u++) {
-                const float w = c_taps[u];
-                s1 = __builtin_fmaf(w, d[0][c][r][cx + u], s1);
-                s2 = __builtin_fmaf(w, d[1][c][r][cx + u], s2);
-                s3 = __builtin_fmaf(w, d[2][c][r][cx + u], s3);
+            for (int q = 0; q < 3; q++) {
+                float dv[CG3 + 10];
+#pragma unroll
+                for (int i = 0; i < CG3 + 10; i++) dv[i] = d[q][c][r][c0 + i];
+#pragma unroll
+                for (int j = 0; j < CG3; j++) {
+                    float t = 0.f;
+#pragma unroll
+                    for (int u = 0; u < 11; u++) t = __builtin_fmaf(c_taps[u], dv[j + u], t);
+                    h[q][r][c0 + j] = t;
+                }
             }
-            h[0][r][cx] = s1;
-            h[1][r][cx] = s2;
-            h[2][r][cx] = s3;
         }
         __syncthreads();
-        float c1 = 0.f, c2 = 0.f, c3 = 0.f;
+        float acc[3][2];
 #pragma unroll
-        for (int v = 0; v < 11; v++) {
-            const float w = c_taps[v];
-            const int r = threadIdx.y + v;
-            c1 = __builtin_fmaf(w, h[0][r][threadIdx.x], c1);
-            c2 = __builtin_fmaf(w, h[1][r][threadIdx.x], c2);
-            c3 = __builtin_fmaf(w, h[2][r][threadIdx.x], c3);
+        for (int q = 0; q < 3; q++) {
+            float hv[12];
+#pragma unroll
+            for (int v = 0; v < 12; v++) hv[v] = h[q][2 * rg + v][tx];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                float t = 0.f;
+#pragma unroll
+                for (int v = 0; v < 11; v++) t = __builtin_fmaf(c_taps[v], hv[i + v], t);
+                acc[q][i] = t;
+            }
         }
-        const float x = xs[c], y = ys[c];
-        const float vd = G * (c1 + 2.f * x * c2 + y * c3);
-        if (FUSE_L1) {
-            const float dd = x - y;
-            const float base = dd > 0.0f ? g_l1 : (dd < 0.0f ? -g_l1 : 0.0f);
-            vout[c] = w_l1 * base + vd;
-            if (in) l1 += fabs(static_cast<double>(dd));
-        } else {
-            vout[c] = vd;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int qy = oy + 2 * rg + i;
+            const float x = xs[i][c], y = ys[i][c];
+            const float c1 = acc[0][i], c2 = acc[1][i], c3 = acc[2][i];
+            const float vd = G * (c1 + 2.f * x * c2 + y * c3);
+            if (FUSE_L1) {
+                const float dd = x - y;
+                const float base = dd > 0.0f ? g_l1 : (dd < 0.0f ? -g_l1 : 0.0f);
+                vout[i][c] = w_l1 * base + vd;
+                if (qy < H && qx < W) l1 += fabs(static_cast<double>(dd));
+            } else {
+                vout[i][c] = vd;
+            }
         }
     }
-    if (in) {
 #pragma unroll
-        for (int c = 0; c < C3; c++) v_img1[q0 + c] = vout[c];
+    for (int i = 0; i < 2; i++) {
+        const int qy = oy + 2 * rg + i;
+        if (qy >= H || qx >= W) continue;
+        const size_t q0 = ihwc(img, qy, qx, 0, H, W, C3);
+#pragma unroll
+        for (int c = 0; c < C3; c++) v_img1[q0 + c] = vout[i][c];
     }
     if (FUSE_L1) {
         s_red[tid] = l1;
@@ -405,8 +443,8 @@ void ssim_fwd(const float* img1, const float* img2, int I, int H, int W, int C, 
 void ssim_bwd(const float* img1, const float* img2, const float* cmu, const float* csg, const float* ccr, int I,
               int H, int W, int C, float G, float* v_img1, hipStream_t s) {
     if (C == C3) {
-        dim3 grid((W + T - 1) / T, (H + T - 1) / T, I);
-        hipLaunchKernelGGL(k_ssim_bwd3<false>, grid, dim3(T, T), 0, s, img1, img2, cmu, csg, ccr, H, W, G, v_img1,
+        dim3 grid((W + TW3 - 1) / TW3, (H + TH3 - 1) / TH3, I);
+        hipLaunchKernelGGL(k_ssim_bwd3<false>, grid, dim3(256), 0, s, img1, img2, cmu, csg, ccr, H, W, G, v_img1,
                            0.f, 0.f, nullptr);
         return;
     }
@@ -414,13 +452,13 @@ void ssim_bwd(const float* img1, const float* img2, const float* cmu, const floa
     hipLaunchKernelGGL(k_ssim_bwd, grid, dim3(T, T), 0, s, img1, img2, cmu, csg, ccr, H, W, C, G, v_img1);
 }
 
-int step_ssim_bwd_blocks(int H, int W) { return ((W + T - 1) / T) * ((H + T - 1) / T); }
+int step_ssim_bwd_blocks(int H, int W) { return ((W + TW3 - 1) / TW3) * ((H + TH3 - 1) / TH3); }
 
 void step_ssim_bwd_l1(const float* render, const float* gt, const float* cmu, const float* csg, const float* ccr,
                       int H, int W, float G, float w_l1, float g_l1, float* v_render, double* l1_partials,
                       hipStream_t s) {
-    dim3 grid((W + T - 1) / T, (H + T - 1) / T, 1);
-    hipLaunchKernelGGL(k_ssim_bwd3<true>, grid, dim3(T, T), 0, s, render, gt, cmu, csg, ccr, H, W, G, v_render,
+    dim3 grid((W + TW3 - 1) / TW3, (H + TH3 - 1) / TH3, 1);
+    hipLaunchKernelGGL(k_ssim_bwd3<true>, grid, dim3(256), 0, s, render, gt, cmu, csg, ccr, H, W, G, v_render,
                        w_l1, g_l1, l1_partials);
 }
 
