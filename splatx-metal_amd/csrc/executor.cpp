@@ -80,7 +80,6 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
             for (int k = 0; k < kMaxEvents; k++) SXH_HIP(hipEventCreate(&e->ev[k]));
-            SXH_HIP(hipEventCreateWithFlags(&e->count_ev, hipEventDisableTiming));
             SXH_HIP(hipStreamSynchronize(b->stream));
         } catch (...) {
             delete e;
@@ -95,7 +94,6 @@ void sxh_exec_destroy(sxh_executor* e) {
     (void)hipStreamSynchronize(e->b->stream);
     for (int k = 0; k < kMaxEvents; k++)
         if (e->ev[k]) (void)hipEventDestroy(e->ev[k]);
-    if (e->count_ev) (void)hipEventDestroy(e->count_ev);
     for (auto& row : e->graph_b)
         for (hipGraphExec_t x : row)
             if (x) (void)hipGraphExecDestroy(x);
@@ -200,6 +198,25 @@ int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out) {
 
 } // extern "C"
 
+// Sync 1 of a step whose segment B is already queued: wait until the block scan has stored `seq` into
+// the mapped word (its counts are then in place). The stream is polled now and then, so that an error
+// or a stream that finished without the store ends the wait instead of spinning forever.
+static void wait_count_word(volatile unsigned long long* word, unsigned long long seq, hipStream_t s,
+                            const char* what) {
+    for (uint32_t spins = 1;; spins++) {
+        if (*word == seq) return;
+        if ((spins & 1023u) == 0u) {
+            const hipError_t q = hipStreamQuery(s);
+            if (q == hipSuccess) {
+                if (*word == seq) return;
+                throw std::runtime_error(std::string(what) + ": the step's count word was not written");
+            }
+            if (q != hipErrorNotReady) SXH_HIP(q);
+        }
+        __builtin_ia32_pause();
+    }
+}
+
 // The step proper. `render_to_dev` (device), when not null, receives a copy of the render.
 void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out, float* render_to_dev) {
     const char* what = "TrainStepExecutor::step";
@@ -267,12 +284,14 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     // loss bits, sort error flag, largest tile (stored by segment B's last kernel)
     volatile unsigned long long* const hc = static_cast<volatile unsigned long long*>(e->step_rb.p);
     volatile uint32_t* const hw = reinterpret_cast<volatile uint32_t*>(hc + 2);
+    unsigned long long seq = 0;  // the last segment A's sequence number (its count word's tag)
     auto launch_a = [&](unsigned long long cap) {
+        seq = ++e->step_seq;
         if (e->prof_stats)
             SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
         e->mark("start");
         sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
-                             cap, static_cast<unsigned long long*>(e->step_rb.dev), s);
+                             cap, static_cast<unsigned long long*>(e->step_rb.dev), seq, s);
         e->mark("preprocess");
     };
     const float* gt = nullptr;
@@ -451,8 +470,9 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     };
 
     // ---- sync 1: n_isects (MetalBackend.cpp:1849-1858) --------------------------------------------
-    // With a graph, segment B is queued behind segment A before the host waits for the count (an event
-    // after the count's copy), so the GPU does not idle through the host's wake-up. If the count
+    // With a graph, segment B is queued behind segment A before the host waits for the count (a word
+    // the block scan stores into mapped host memory), so the GPU does not idle through the host's
+    // wake-up. If the count
     // exceeds the capacity that segment B ran with (nothing done, arena untouched), the step runs again
     // the plain way: sync on the count, grow, capture, launch.
     int64_t n_isects = 0;
@@ -462,12 +482,11 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         const unsigned long long cap = e->isect_cap;
         launch_a(cap);
         upload_gt();
-        SXH_HIP(hipEventRecord(e->count_ev, s));
         capture_b();
         SXH_HIP(hipGraphLaunch(e->graph_b[index_first ? 1 : 0][fwd_only ? 1 : 0], s));
         launch_tail();
         const auto t0 = std::chrono::steady_clock::now();
-        SXH_HIP(hipEventSynchronize(e->count_ev));
+        wait_count_word(hc + 4, seq, s, what);
         e->sync_ms[0] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         n_isects = static_cast<int64_t>(hc[1]);
         validate_n_isects_readback(n_isects, what);

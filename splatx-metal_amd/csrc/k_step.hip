@@ -146,24 +146,26 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
     }
 }
 
+// a store into mapped host memory, at system scope (no GPU cache keeps it from the host)
+template <class T>
+__device__ __forceinline__ void store_host(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // One workgroup over the preprocess blocks' {visible, tiles, Gaussians with tiles} counts: the totals
 // (out = {u64 visible, u64 intersections, u64 Gaussians with tiles, u64 intersections, u64 overflow})
 // and, per block b, the intersections and the Gaussians with tiles of the blocks before it (base[2 b],
 // base[2 b + 1]). When the intersections exceed `cap` (the buffers' capacity) the step's later kernels
 // must not run: overflow = 1 and out[2] = out[3] = 0, the counts they read, so that every one of them
 // finds nothing to do (out[1] keeps the true total for the host).
-// a store into mapped host memory, at system scope (no GPU cache keeps it from the host)
-template <class T>
-__device__ __forceinline__ void store_host(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
 constexpr int kScanBlock = 1024;
 constexpr int kScanPer = 8;  // consecutive blocks per thread and chunk
 __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restrict__ part, int n,
                                                            unsigned long long* __restrict__ out,
                                                            unsigned long long* __restrict__ base,
                                                            unsigned long long cap,
-                                                           unsigned long long* __restrict__ host) {
+                                                           unsigned long long* __restrict__ host,
+                                                           unsigned long long seq) {
     __shared__ unsigned long long s_i[kScanBlock / 64], s_e[kScanBlock / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     unsigned long long vis = 0, carry_i = 0, carry_e = 0;
@@ -231,6 +233,8 @@ __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restri
         if (host) {
             store_host(&host[0], v);
             store_host(&host[1], carry_i);
+            // the launch's sequence number last: a host that sees it sees the counts
+            __hip_atomic_store(&host[4], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }
@@ -772,7 +776,8 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* n_visible, unsigned long long* block_base,
-                     unsigned long long isect_cap, unsigned long long* host_counts, hipStream_t s) {
+                     unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
+                     hipStream_t s) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
@@ -783,7 +788,7 @@ void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
-                       static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts);
+                       static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts, seq);
 }
 
 void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,

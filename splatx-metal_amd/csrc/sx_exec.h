@@ -99,7 +99,7 @@ struct sxh_executor {
     sxh::DevBuf<unsigned long long> rstats;
     sxh_raster_stats rstats_host{};
     hipEvent_t ev[kMaxEvents] = {};
-    hipEvent_t count_ev = nullptr;  // recorded after the step's count read-back
+    unsigned long long step_seq = 0;  // segment A launches so far (the tag of the step's count word)
     const char* ev_name[kMaxEvents] = {};
     int n_ev = 0;
     sxh_exec_timing timing{};

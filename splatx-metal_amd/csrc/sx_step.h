@@ -49,10 +49,12 @@ struct StepConst {
 // intersections > isect_cap and then words 2 and 3 read 0 (the counts the rest of the step reads, so
 // that it does nothing); block_base: per block, the intersections and the Gaussians with tiles of the
 // blocks before it (2 u64)
-// host_counts (mapped host memory, may be null) receives words 0 and 1 of out_vis.
+// host_counts (mapped host memory, may be null) receives words 0 and 1 of out_vis, then `seq` in its
+// word 4 (release order: a host that reads seq there reads the counts).
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
-                     unsigned long long isect_cap, unsigned long long* host_counts, hipStream_t s);
+                     unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
+                     hipStream_t s);
 // number of blocks of step_preprocess
 int step_preprocess_blocks(int64_t count);
 // The Gaussians with tiles in index order (list[j], j below out_vis[2]) and (cum set) cum[j], the
