@@ -823,53 +823,87 @@ __device__ __forceinline__ void store_grad_record(float4* grads, size_t g, const
     grads[3 * g + 2] = make_float4(v[6], v[7], v[8], 0.f);
 }
 
-constexpr int kGatherRound = 8;  // short ranges: entries loaded per round (independent loads)
+constexpr int kGatherWave = 64;    // emit positions per gather workgroup (one wave)
+constexpr int kGatherStage = 256;  // entries staged in LDS per round
 
-// One thread per position j of the depth order, for Gaussian order[j]: the sums of its (tile, Gaussian)
-// entries, which the emit placed at [cum[j-1], cum[j]), in emit order (its tiles in the order the
-// intersection emit visits them), into its gradient record {v_x, v_y, v_opacity, 0 | v_conic a, b, c,
-// 0 | v_r, v_g, v_b, 0}. Entries without this step's stamp (tiles that never reached the Gaussian) count
-// as zero: an added +0 leaves every partial sum as it was (a sum that starts at +0 never becomes -0).
-// A Gaussian with no stamped entry (exactly the untouched ones) gets no record: the postprocess reads
-// zeros for it. (Loading a range's entries before its touched flag has arrived costs more than the wait:
-// at dense settings most short ranges belong to Gaussians no tile reached.) Ranges longer than
-// kLongRange are queued for k_gather_long when touched (the queue's order does not matter: each range is
-// reduced on its own).
-__global__ void __launch_bounds__(kThreads) k_gather_grads(int count, const int32_t* __restrict__ order,
-                                                           const int64_t* __restrict__ cum,
-                                                           const float* __restrict__ part,
-                                                           const uint32_t* __restrict__ stamp_p,
-                                                           const uint8_t* __restrict__ touched,
-                                                           float4* __restrict__ grads, int32_t* __restrict__ long_list,
-                                                           int32_t* __restrict__ long_count,
-                                                           const int64_t* __restrict__ count_dev) {
-    const int j = blockIdx.x * kThreads + threadIdx.x;
-    if (j >= (count_dev ? static_cast<int>(*count_dev) : count)) return;
+// One wave per 64 consecutive positions j of the emit order, for Gaussian order[j]: the sums of its
+// (tile, Gaussian) entries, which the emit placed at [cum[j-1], cum[j]), in emit order (its tiles in
+// the order the intersection emit visits them), into its gradient record {v_x, v_y, v_opacity, 0 |
+// v_conic a, b, c, 0 | v_r, v_g, v_b, 0}. The wave's ranges lie back to back in `part`, so the wave
+// stages them in LDS with loads of consecutive entries (a lane per entry) and each lane then adds its
+// own range from there, in order. Entries without this step's stamp (tiles that never reached the
+// Gaussian) are staged as zeros: an added +0 leaves every partial sum as it was (a sum that starts at
+// +0 never becomes -0). A Gaussian with no stamped entry (exactly the untouched ones) stages nothing
+// and gets no record: the postprocess reads zeros for it. Ranges longer than kLongRange are queued for
+// k_gather_long when touched (the queue's order does not matter: each range is reduced on its own).
+__global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const int32_t* __restrict__ order,
+                                                              const int64_t* __restrict__ cum,
+                                                              const float* __restrict__ part,
+                                                              const uint32_t* __restrict__ stamp_p,
+                                                              const uint8_t* __restrict__ touched,
+                                                              float4* __restrict__ grads,
+                                                              int32_t* __restrict__ long_list,
+                                                              int32_t* __restrict__ long_count,
+                                                              const int64_t* __restrict__ count_dev) {
+    __shared__ float s_rec[kGatherStage][kPartFloats];  // odd row stride: lanes on different rows, different banks
+    __shared__ int32_t s_off[kGatherWave];              // each lane's first staged entry
+    __shared__ int32_t s_src[kGatherWave];              // each lane's first entry in `part`
+    const int lane = threadIdx.x;
+    const int j = blockIdx.x * kGatherWave + lane;
+    const int n_pos = count_dev ? static_cast<int>(*count_dev) : count;
     const uint32_t stamp = *stamp_p;
-    const int32_t p1 = static_cast<int32_t>(cum[j]);
-    const int32_t p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
-    const int g = order ? order[j] : j;
-    if (p1 == p0) return;
-    const bool hit = touched[g] != 0;
-    if (p1 - p0 > kLongRange) {
-        if (hit) long_list[atomicAdd(long_count, 1)] = j;  // an untouched range has no stamped entry
-        return;
+    int32_t p0 = 0, n = 0;
+    int g = 0;
+    if (j < n_pos) {
+        const int32_t p1 = static_cast<int32_t>(cum[j]);
+        p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
+        g = order ? order[j] : j;
+        if (p1 > p0 && touched[g] != 0) {  // an untouched range has no stamped entry
+            if (p1 - p0 > kLongRange)
+                long_list[atomicAdd(long_count, 1)] = j;
+            else
+                n = p1 - p0;
+        }
     }
-    if (!hit) return;  // no stamped entry: no record
+    // exclusive scan of the staged lengths over the wave
+    int incl = n;
+#pragma unroll
+    for (int o = 1; o < kGatherWave; o <<= 1) {
+        const int y = __shfl_up(incl, o, kGatherWave);
+        if (lane >= o) incl += y;
+    }
+    const int off = incl - n;
+    const int total = __shfl(incl, kGatherWave - 1, kGatherWave);
+    if (total == 0) return;  // uniform
+    s_off[lane] = off;
+    s_src[lane] = p0;
+    __syncthreads();
     float v[kPartFloats];
 #pragma unroll
     for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
-    for (int32_t p = p0; p < p1; p += kGatherRound) {
-        float e[kGatherRound][kPartFloats];
-        bool on[kGatherRound];
+    for (int base = 0; base < total; base += kGatherStage) {  // uniform
+        const int cnt = min(kGatherStage, total - base);
+        for (int i = lane; i < cnt; i += kGatherWave) {
+            // the staged entry's owner: the last lane whose first staged entry is at or before it (lanes
+            // that stage nothing share the next lane's offset, and the search passes over them)
+            const int k = base + i;
+            int lo = 0;
 #pragma unroll
-        for (int i = 0; i < kGatherRound; i++) on[i] = load_entry(part, min(p + i, p1 - 1), stamp, e[i]) & (p + i < p1);
+            for (int step = kGatherWave / 2; step > 0; step >>= 1)
+                if (s_off[lo + step] <= k) lo += step;
+            float e[kPartFloats];
+            const bool on = load_entry(part, s_src[lo] + (k - s_off[lo]), stamp, e);
 #pragma unroll
-        for (int i = 0; i < kGatherRound; i++)
+            for (int c = 0; c < kPartFloats; c++) s_rec[i][c] = on ? e[c] : 0.f;
+        }
+        __syncthreads();
+        const int a = max(off, base), b = min(off + n, base + cnt);
+        for (int k = a; k < b; k++)
 #pragma unroll
-            for (int k = 0; k < kPartFloats; k++) v[k] += on[i] ? e[i][k] : 0.f;
+            for (int c = 0; c < kPartFloats; c++) v[c] += s_rec[k - base][c];
+        __syncthreads();  // the next round restages
     }
-    store_grad_record(grads, static_cast<size_t>(g), v);
+    if (n > 0) store_grad_record(grads, static_cast<size_t>(g), v);
 }
 
 // The queued long ranges, one wave each, 64 entries per round (lane l takes entry base + l when it
@@ -923,8 +957,8 @@ void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, co
                          const uint8_t* touched, float4* grads, int32_t* long_list, int32_t* long_count,
                          hipStream_t s, const int64_t* count_dev) {
     if (count <= 0) return;
-    hipLaunchKernelGGL(k_gather_grads, dim3((count + kThreads - 1) / kThreads), dim3(kThreads), 0, s, count, order, cum,
-                       part, stamp, touched, grads, long_list, long_count, count_dev);
+    hipLaunchKernelGGL(k_gather_grads, dim3((count + kGatherWave - 1) / kGatherWave), dim3(kGatherWave), 0, s, count,
+                       order, cum, part, stamp, touched, grads, long_list, long_count, count_dev);
     hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, stamp, grads, long_list,
                        long_count);
 }
