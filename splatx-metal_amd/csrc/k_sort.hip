@@ -481,8 +481,10 @@ __global__ void __launch_bounds__(kThreads) k_rs_count(const K* __restrict__ key
     if (threadIdx.x <= mask) cnt[(size_t)threadIdx.x * n_tiles + tile] = h[threadIdx.x];
 }
 
-// Exclusive scan of v[0, len) in place, in three launches: chunk sums, their exclusive scan (one
-// workgroup), and the scan of each chunk from its prefix. v starts 64-B aligned (16-B loads).
+// Exclusive scan of v[0, len) in place, in two launches: chunk sums, then the scan of each chunk
+// from its prefix, which each workgroup of the second adds up from the chunk sums before it (a few
+// thousand words at most: cheaper than a launch that scans them first). v starts 64-B aligned (16-B
+// loads).
 __global__ void __launch_bounds__(kThreads) k_rs_reduce(const uint32_t* __restrict__ v, int64_t len,
                                                         uint32_t* __restrict__ sums) {
     __shared__ uint32_t s_wave[kWaves];
@@ -506,28 +508,6 @@ __global__ void __launch_bounds__(kThreads) k_rs_reduce(const uint32_t* __restri
     if (threadIdx.x == 0) sums[blockIdx.x] = all;
 }
 
-__global__ void __launch_bounds__(kThreads) k_rs_top(uint32_t* __restrict__ sums, int n) {
-    __shared__ uint32_t s_wave[kWaves];
-    uint32_t carry = 0;
-    for (int c0 = 0; c0 < n; c0 += kScanChunk) {  // uniform
-        const int i0 = c0 + threadIdx.x * 16;
-        uint32_t x[16], acc = 0;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            x[i] = i0 + i < n ? sums[i0 + i] : 0u;
-            acc += x[i];
-        }
-        uint32_t all = 0;
-        uint32_t run = block_excl_scan_u32(acc, s_wave, &all) + carry;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            if (i0 + i < n) sums[i0 + i] = run;
-            run += x[i];
-        }
-        carry += all;
-    }
-}
-
 __global__ void __launch_bounds__(kThreads) k_rs_down(uint32_t* __restrict__ v, int64_t len,
                                                       const uint32_t* __restrict__ sums) {
     __shared__ uint32_t s_wave[kWaves];
@@ -548,8 +528,12 @@ __global__ void __launch_bounds__(kThreads) k_rs_down(uint32_t* __restrict__ v, 
     }
 #pragma unroll
     for (int i = 0; i < 16; i++) acc += x[i];
+    uint32_t pre = 0;  // the chunks before this one
+    for (int c = threadIdx.x; c < static_cast<int>(blockIdx.x); c += kThreads) pre += sums[c];
     uint32_t all = 0;
-    uint32_t run = block_excl_scan_u32(acc, s_wave, &all) + sums[blockIdx.x];
+    (void)block_excl_scan_u32(pre, s_wave, &all);  // (its closing barrier frees s_wave)
+    const uint32_t chunk_base = all;
+    uint32_t run = block_excl_scan_u32(acc, s_wave, &all) + chunk_base;
     uint32_t y[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -856,9 +840,8 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
             const int chunks = static_cast<int>((len + kScanChunk - 1) / kScanChunk);
             hipLaunchKernelGGL(k_rs_count<K>, dim3((tiles + kXcds - 1) / kXcds * kXcds), dim3(kThreads), 0, s, kin, n,
                                dbits * p, mask, cnt, tiles, n_dev, (p == 0 && clear_err) ? err : nullptr);
-            // (one workgroup scanning a small matrix in one launch measured slower than these three)
+            // (one workgroup scanning a small matrix in one launch measured slower than these)
             hipLaunchKernelGGL(k_rs_reduce, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
-            hipLaunchKernelGGL(k_rs_top, dim3(1), dim3(kThreads), 0, s, sums, chunks);
             hipLaunchKernelGGL(k_rs_down, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
             launch_os_pass<K, false>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p, mask, nullptr,
                                      nullptr, nullptr, nullptr, err, n_dev, cnt);
