@@ -309,8 +309,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     const unsigned long long* overflow_dev = e->n_vis.p + 4;
     int n_l1 = 0, n_ss = 0;
     int32_t* flat = e->vals_a.p;
-    // index-first needs every tile's list in LDS (4096 entries) to be fast; larger tiles still sort
-    // correctly through global scratch
+    // index-first sorts each tile's list by depth in one workgroup: fast while the tiles stay small
+    // (up to 2048 entries in LDS, larger ones through global scratch, correct at any size)
     constexpr int64_t kIndexFirstMaxTile = 4096;
     const bool index_first = e->isect_order == SXH_ISECT_ORDER_INDEX_FIRST ||
                              (e->isect_order == SXH_ISECT_ORDER_AUTO && e->last_max_tile >= 0 &&

@@ -902,10 +902,10 @@ int radix_sort_ab(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_
 // When the Gaussians emit in index order, a stable sort on the tile ids leaves each tile's entries in
 // index order; sorting them stably by the depth bits of their Gaussians (which the emit stored per
 // entry) then gives the order of the reference's (tile | depth) keys: depth, ties by index. One
-// workgroup per tile. A tile of at most kTile entries is sorted in LDS by 8-bit LSD passes, wave w
+// workgroup per tile. A tile of at most 2048 entries is sorted in LDS by 8-bit LSD passes, wave w
 // holding the w-th quarter of the list (in whole 64-key rounds) in registers and ranking with match
 // masks as the onesweep pass does; bytes on which every key of the tile agrees are skipped. A larger
-// tile runs the same passes through global scratch, a chunk of kTile keys at a time in list order.
+// tile runs the same passes through global scratch, 2048 keys at a time in list order.
 __device__ __forceinline__ uint32_t wave_and_u32(uint32_t x) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) x &= static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), o, 64));
@@ -973,11 +973,12 @@ __device__ __forceinline__ uint32_t wave_starts(uint32_t (*s_woff)[kBins], uint3
     return run;
 }
 
-// RMAX: rounds of 64 keys per wave that the kernel holds in registers; the small instance (RMAX 4)
-// takes the tiles of 2 to 1024 entries at twice the occupancy, in tile order (one load less before
-// its list), the full one (RMAX = kRounds) the larger ones, heaviest first. Every instance is
-// launched over all tiles and leaves the others alone. (One wave per small tile, with no workgroup
-// barriers, measured slower: its ranking rounds wait on LDS one after another.)
+// RMAX: rounds of 64 keys per wave that the kernel holds in registers. One launch takes every tile,
+// heaviest first (tile_order): up to kCap = 256 RMAX entries in LDS, larger ones through global
+// scratch. RMAX 8 (2048 entries, 12 KB of LDS) measured fastest: a separate launch for the tiles
+// past 1024 entries with 16 rounds (twice the LDS) left its few long tiles running alone after
+// the small ones, and 4 rounds send more tiles through global scratch. (One wave per small tile, with
+// no workgroup barriers, measured slower: its ranking rounds wait on LDS one after another.)
 template <int RMAX>
 __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles,
                                                               int32_t n_isects, const int64_t* __restrict__ n_dev,
@@ -987,20 +988,18 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
                                                               uint32_t* __restrict__ sk0, uint32_t* __restrict__ sk1,
                                                               int32_t* __restrict__ sv) {
     constexpr int kCap = kWaves * 64 * RMAX;
-    constexpr bool kFull = RMAX == kRounds;
-    constexpr int kSmallCap = kWaves * 64 * 4;
     __shared__ uint32_t s_key[kCap];
     __shared__ int32_t s_val[kCap];
     __shared__ uint32_t s_woff[kWaves][kBins];
-    __shared__ uint32_t s_base[kFull ? kBins : 1];
+    __shared__ uint32_t s_base[kBins];
     __shared__ uint32_t s_wave[kWaves];
     __shared__ uint32_t s_and[kWaves], s_or[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = (tile_order && kFull) ? tile_order[blockIdx.x] : static_cast<int>(blockIdx.x);
+    const int t = tile_order ? tile_order[blockIdx.x] : static_cast<int>(blockIdx.x);
     const int32_t n_all = n_dev ? static_cast<int32_t>(*n_dev) : n_isects;
     const int32_t start = offsets[t];
     const int32_t nt = (t + 1 < n_tiles ? offsets[t + 1] : n_all) - start;
-    if (nt <= 1 || (kFull ? nt <= kSmallCap : nt > kCap)) return;  // uniform: another instance's tile
+    if (nt <= 1) return;  // uniform
     int32_t* const seg = vals + start;
     uint32_t key[RMAX];
     int32_t val[RMAX];
@@ -1069,8 +1068,8 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
         }
         return;
     }
-    if constexpr (kFull) {
-        // a tile of more than kTile entries: the keys go to sk0, then each pass moves (key, value) between
+    {
+        // a tile of more than kCap entries: the keys go to sk0, then each pass moves (key, value) between
         // (sk0, vals) and (sk1, sv) over the tile's range, chunk by chunk in list order
         uint32_t a = ~0u, o = 0u;
         for (int32_t i = tid; i < nt; i += kThreads) {
@@ -1084,7 +1083,7 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
         const int32_t* src_v = seg;
         uint32_t* dst_k = sk1 + start;
         int32_t* dst_v = sv + start;
-        constexpr int kPerWave = kTile / kWaves;
+        constexpr int kPerWave = kCap / kWaves;
         for (int p = 0; p < 4; p++) {
             const int shift = 8 * p;
             if (((diff >> shift) & 255u) == 0u) continue;  // uniform
@@ -1098,11 +1097,11 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
                 s_base[tid] = b;  // every thread has read its own digit's count above
             }
             __syncthreads();
-            for (int32_t c0 = 0; c0 < nt; c0 += kTile) {  // uniform
-                const int cn = static_cast<int>(min<int32_t>(kTile, nt - c0));
+            for (int32_t c0 = 0; c0 < nt; c0 += kCap) {  // uniform
+                const int cn = static_cast<int>(min<int32_t>(kCap, nt - c0));
                 const int wb = wave * kPerWave;
 #pragma unroll
-                for (int r = 0; r < kRounds; r++) {
+                for (int r = 0; r < RMAX; r++) {
                     const int i = wb + r * 64 + lane;
                     key[r] = i < cn ? src_k[c0 + i] : 0u;
                     val[r] = i < cn ? src_v[c0 + i] : 0;
@@ -1110,12 +1109,12 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
 #pragma unroll
                 for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
                 __syncthreads();
-                wave_rank_byte<kRounds>(key, kRounds, wb, cn, shift, s_woff[wave], off);
+                wave_rank_byte<RMAX>(key, RMAX, wb, cn, shift, s_woff[wave], off);
                 __syncthreads();
                 s_base[tid] = wave_starts(s_woff, s_base[tid]);
                 __syncthreads();
 #pragma unroll
-                for (int r = 0; r < kRounds; r++) {
+                for (int r = 0; r < RMAX; r++) {
                     if (wb + r * 64 + lane < cn) {
                         const uint32_t pos = s_woff[wave][(key[r] >> shift) & 255u] + off[r];
                         dst_k[pos] = key[r];
@@ -1172,14 +1171,13 @@ int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, in
     return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true);
 }
 
+constexpr int kDepthSortRounds = 8;
+
 void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
                      const int32_t* tile_order, int32_t* vals, const uint32_t* edepth, uint32_t* scratch_k0,
                      uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s) {
     if (n_tiles <= 0 || (!n_dev && n_isects <= 1)) return;
-    hipLaunchKernelGGL(k_tile_depth_sort<kRounds>, dim3(n_tiles), dim3(kThreads), 0, s, offsets, n_tiles,
-                       static_cast<int32_t>(n_isects), n_dev, tile_order, vals, edepth, scratch_k0, scratch_k1,
-                       scratch_v);
-    hipLaunchKernelGGL(k_tile_depth_sort<4>, dim3(n_tiles), dim3(kThreads), 0, s, offsets, n_tiles,
+    hipLaunchKernelGGL(k_tile_depth_sort<kDepthSortRounds>, dim3(n_tiles), dim3(kThreads), 0, s, offsets, n_tiles,
                        static_cast<int32_t>(n_isects), n_dev, tile_order, vals, edepth, scratch_k0, scratch_k1,
                        scratch_v);
 }

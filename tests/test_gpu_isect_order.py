@@ -1,12 +1,12 @@
 """The step's two intersection orders (sxh_exec_set_isect_order): depth first (Gaussians sorted by
 depth, tile ids emitted in that order, a stable tile sort) and index first (tile ids emitted in index
 order, a stable tile sort, then each tile's list sorted by depth in LDS, or through global scratch
-for tiles of more than 4096 entries) must give the same per-tile (depth, index) lists, hence
+for tiles of more than 2048 entries) must give the same per-tile (depth, index) lists, hence
 bit-identical renders, losses and parameters over several training steps. The depth-first path is
 held to the CPU oracle in test_gpu_step.py; the first index-first step is checked against it here
 too. Cases cover both intersection modes, antialiasing, tied depths (the stable tie order), a
-single shared depth (the sort's all-equal exit) and tiles of up to ~4x4096 entries (the scratch
-path, several chunks)."""
+single shared depth (the sort's all-equal exit) and tiles of up to ~16 k entries (the scratch
+path, several chunks of 2048)."""
 import numpy as np
 import pytest
 
@@ -23,10 +23,10 @@ CASES = {
     "antialiased_ties": (dict(n=6000, sh_degree=1, tie_frac=0.3), (128, 96, 110.0),
                          dict(isect_mode=sh.SXH_ISECT_ACCUTILE, antialiased=True)),
     "one_depth": (dict(n=3000, sh_degree=0, tie_frac=1.0), (96, 64, 90.0), dict(isect_mode=sh.SXH_ISECT_AABB)),
-    # 16 tiles: the 4 central ones hold ~16 k entries each (the scratch path, 5 chunks), the rest ~1 k
+    # 16 tiles: the 4 central ones hold ~16 k entries each (the scratch path, 8 chunks), the rest ~1 k
     "big_tiles_ties": (dict(n=20000, sh_degree=0, tie_frac=0.2, xy=0.6, log_scale_mu=np.log(0.1)), (64, 64, 60.0),
                        dict(isect_mode=sh.SXH_ISECT_AABB)),
-    # 24 tiles: 4 of ~7 k entries (2 chunks), the rest under 4096 (LDS)
+    # 24 tiles: 4 of ~7 k entries (4 chunks), the rest under 4096 (LDS or 2 chunks)
     "mixed_tiles": (dict(n=12000, sh_degree=0, xy=1.0, log_scale_mu=np.log(0.1)), (96, 64, 80.0),
                     dict(isect_mode=sh.SXH_ISECT_AABB)),
 }
