@@ -176,7 +176,8 @@ __global__ void __launch_bounds__(256) k_ssim_bwd(const float* __restrict__ img1
 
 // Three-channel variants (the training images). The forward: one workgroup per 16x16 tile covers all
 // three channels, so every global load and store touches whole interleaved pixels, and each channel's
-// passes run exactly as above (same tap order, same results). The backward: one workgroup per 16 x 32
+// passes keep the tap order above (same results), register-blocked by two columns (horizontal) and two
+// rows (vertical) with conflict-free LDS strides. The backward: one workgroup per 16 x 32
 // tile, the apron of all three channels staged at once (whole pixels again) and the passes run one
 // channel after another. The taller tile cuts the horizontal pass's apron rows (42 per 32 outputs
 // instead of 26 per 16), and both passes are register-blocked: a horizontal task reads the 14 inputs
@@ -196,18 +197,21 @@ static_assert(TW3 == CG3 * 4 && AH3 <= 64 && TH3 == 32, "one wave per column gro
 // the vertical pass's thread: column tx, rows 2 rg and 2 rg + 1
 __device__ __forceinline__ int vert_rg(int tid) { return (tid >> 5) + 8 * ((tid >> 4) & 1); }
 
+constexpr int SHF = T + 2;  // the forward's row stride of the horizontal sums: 18 (see below)
+
 __global__ void __launch_bounds__(256) k_ssim_fwd3(const float* __restrict__ img1, const float* __restrict__ img2,
                                                    int H, int W, int need_coeffs, float* __restrict__ map,
                                                    float* __restrict__ cmu, float* __restrict__ csg,
                                                    float* __restrict__ ccr, double* __restrict__ block_sums) {
     __shared__ float sx[C3][A][A + 1];
     __shared__ float sy[C3][A][A + 1];
-    __shared__ float h[5][A][T + 1];
+    __shared__ float h[5][A][SHF];
     __shared__ double s_red[256];
     const int mh = H - 10, mw = W - 10;
     const int img = blockIdx.z;
     const int oy = blockIdx.y * T, ox = blockIdx.x * T;
     const int tid = threadIdx.y * T + threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
     for (int k = tid; k < A * A * C3; k += 256) {
         const int ay = k / (A * C3), rem = k % (A * C3);
         const int ax = rem / C3, c = rem % C3;
@@ -221,74 +225,104 @@ __global__ void __launch_bounds__(256) k_ssim_fwd3(const float* __restrict__ img
         sx[c][ay][ax] = a;
         sy[c][ay][ax] = b;
     }
-    const int my = oy + threadIdx.y, mx = ox + threadIdx.x;
-    const bool out = my < mh && mx < mw;
-    float S_[C3], cm_[C3], cs_[C3], cc_[C3];
+    // Register-blocked passes. Horizontal: a task is one row and two adjacent columns (12 inputs read
+    // once); half-wave h of wave w takes column pair 2w + h over the 26 rows (odd input row stride 27:
+    // no bank conflicts). Vertical: threads 0..127, column vtx, rows 2 rg and 2 rg + 1 (12 sums read
+    // once per quantity); the two 16-lane groups of a half-wave take row pairs 8 rows apart, which the
+    // sums' row stride 18 puts 16 banks apart.
+    const int hr = lane & 31, hc0 = 4 * wave + 2 * (lane >> 5);
+    const bool hor = hr < A;
+    const bool vert = tid < 128;
+    const int vtx = tid & 15, vrg = ((tid >> 5) & 3) + 4 * ((tid >> 4) & 1);
+    const int vmx = ox + vtx;
+    float res[2][C3][4];
     double contrib = 0.0;
 #pragma unroll
     for (int c = 0; c < C3; c++) {
         __syncthreads();  // loads done / previous channel's vertical pass done with h
-        for (int k = tid; k < A * T; k += 256) {
-            const int r = k / T, cx = k % T;
-            float m1 = 0.f, m2 = 0.f, e11 = 0.f, e22 = 0.f, e12 = 0.f;
+        if (hor) {
+            float xv[12], gv[12];
 #pragma unroll
-            for (int u = 0; u < 11; u++) {
-                const float w = c_taps[u];
-                const float x = sx[c][r][cx + u], g = sy[c][r][cx + u];
-                m1 = __builtin_fmaf(w, x, m1);
-                m2 = __builtin_fmaf(w, g, m2);
-                e11 = __builtin_fmaf(w * x, x, e11);
-                e22 = __builtin_fmaf(w * g, g, e22);
-                e12 = __builtin_fmaf(w * x, g, e12);
+            for (int i = 0; i < 12; i++) {
+                xv[i] = sx[c][hr][hc0 + i];
+                gv[i] = sy[c][hr][hc0 + i];
             }
-            h[0][r][cx] = m1;
-            h[1][r][cx] = m2;
-            h[2][r][cx] = e11;
-            h[3][r][cx] = e22;
-            h[4][r][cx] = e12;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                float m1 = 0.f, m2 = 0.f, e11 = 0.f, e22 = 0.f, e12 = 0.f;
+#pragma unroll
+                for (int u = 0; u < 11; u++) {
+                    const float w = c_taps[u];
+                    const float x = xv[j + u], g = gv[j + u];
+                    m1 = __builtin_fmaf(w, x, m1);
+                    m2 = __builtin_fmaf(w, g, m2);
+                    e11 = __builtin_fmaf(w * x, x, e11);
+                    e22 = __builtin_fmaf(w * g, g, e22);
+                    e12 = __builtin_fmaf(w * x, g, e12);
+                }
+                h[0][hr][hc0 + j] = m1;
+                h[1][hr][hc0 + j] = m2;
+                h[2][hr][hc0 + j] = e11;
+                h[3][hr][hc0 + j] = e22;
+                h[4][hr][hc0 + j] = e12;
+            }
         }
         __syncthreads();
-        S_[c] = cm_[c] = cs_[c] = cc_[c] = 0.f;
-        if (out) {
-            float mu1 = 0.f, mu2 = 0.f, e11 = 0.f, e22 = 0.f, e12 = 0.f;
+        if (vert) {
+            float acc[5][2];
 #pragma unroll
-            for (int v = 0; v < 11; v++) {
-                const float w = c_taps[v];
-                const int r = threadIdx.y + v;
-                mu1 = __builtin_fmaf(w, h[0][r][threadIdx.x], mu1);
-                mu2 = __builtin_fmaf(w, h[1][r][threadIdx.x], mu2);
-                e11 = __builtin_fmaf(w, h[2][r][threadIdx.x], e11);
-                e22 = __builtin_fmaf(w, h[3][r][threadIdx.x], e22);
-                e12 = __builtin_fmaf(w, h[4][r][threadIdx.x], e12);
+            for (int q = 0; q < 5; q++) {
+                float hv[12];
+#pragma unroll
+                for (int v = 0; v < 12; v++) hv[v] = h[q][2 * vrg + v][vtx];
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    float t = 0.f;
+#pragma unroll
+                    for (int v = 0; v < 11; v++) t = __builtin_fmaf(c_taps[v], hv[i + v], t);
+                    acc[q][i] = t;
+                }
             }
-            const float sigma1 = __builtin_fmaf(-mu1, mu1, e11);
-            const float sigma2 = __builtin_fmaf(-mu2, mu2, e22);
-            const float sigma12 = __builtin_fmaf(-mu1, mu2, e12);
-            const float A1 = 2.f * mu1 * mu2 + sx::kSsimC1;
-            const float B1 = mu1 * mu1 + mu2 * mu2 + sx::kSsimC1;
-            const float A2 = 2.f * sigma12 + sx::kSsimC2;
-            const float B2 = sigma1 + sigma2 + sx::kSsimC2;
-            const float denom = B1 * B2;
-            const float S = (A1 * A2) / denom;
-            S_[c] = S;
-            contrib += static_cast<double>(S);
-            const float dS_dmu1 = 2.f * (mu2 * A2 / denom - mu1 * S / B1);
-            const float dS_dsigma1 = -S / B2;
-            const float dS_dsigma12 = 2.f * A1 / denom;
-            cm_[c] = dS_dmu1 - 2.f * mu1 * dS_dsigma1 - mu2 * dS_dsigma12;
-            cs_[c] = dS_dsigma1;
-            cc_[c] = dS_dsigma12;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                res[i][c][0] = res[i][c][1] = res[i][c][2] = res[i][c][3] = 0.f;
+                const int my = oy + 2 * vrg + i;
+                if (my >= mh || vmx >= mw) continue;
+                const float mu1 = acc[0][i], mu2 = acc[1][i], e11 = acc[2][i], e22 = acc[3][i], e12 = acc[4][i];
+                const float sigma1 = __builtin_fmaf(-mu1, mu1, e11);
+                const float sigma2 = __builtin_fmaf(-mu2, mu2, e22);
+                const float sigma12 = __builtin_fmaf(-mu1, mu2, e12);
+                const float A1 = 2.f * mu1 * mu2 + sx::kSsimC1;
+                const float B1 = mu1 * mu1 + mu2 * mu2 + sx::kSsimC1;
+                const float A2 = 2.f * sigma12 + sx::kSsimC2;
+                const float B2 = sigma1 + sigma2 + sx::kSsimC2;
+                const float denom = B1 * B2;
+                const float S = (A1 * A2) / denom;
+                contrib += static_cast<double>(S);
+                const float dS_dmu1 = 2.f * (mu2 * A2 / denom - mu1 * S / B1);
+                const float dS_dsigma1 = -S / B2;
+                const float dS_dsigma12 = 2.f * A1 / denom;
+                res[i][c][0] = S;
+                res[i][c][1] = dS_dmu1 - 2.f * mu1 * dS_dsigma1 - mu2 * dS_dsigma12;
+                res[i][c][2] = dS_dsigma1;
+                res[i][c][3] = dS_dsigma12;
+            }
         }
     }
-    if (out) {
-        const size_t mo = ihwc(img, my, mx, 0, mh, mw, C3);
+    if (vert) {
 #pragma unroll
-        for (int c = 0; c < C3; c++) {
-            if (map) map[mo + c] = S_[c];
-            if (need_coeffs) {
-                cmu[mo + c] = cm_[c];
-                csg[mo + c] = cs_[c];
-                ccr[mo + c] = cc_[c];
+        for (int i = 0; i < 2; i++) {
+            const int my = oy + 2 * vrg + i;
+            if (my >= mh || vmx >= mw) continue;
+            const size_t mo = ihwc(img, my, vmx, 0, mh, mw, C3);
+#pragma unroll
+            for (int c = 0; c < C3; c++) {
+                if (map) map[mo + c] = res[i][c][0];
+                if (need_coeffs) {
+                    cmu[mo + c] = res[i][c][1];
+                    csg[mo + c] = res[i][c][2];
+                    ccr[mo + c] = res[i][c][3];
+                }
             }
         }
     }
