@@ -291,7 +291,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
         e->mark("start");
         sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
-                             cap, static_cast<unsigned long long*>(e->step_rb.dev), seq, s);
+                             cap, static_cast<unsigned long long*>(e->step_rb.dev), seq,
+                             fwd_only ? sxk::StepClear{} : sxk::StepClear{e->touched.p, e->stamp.p, e->long_count.p}, s);
         e->mark("preprocess");
     };
     const float* gt = nullptr;
@@ -412,8 +413,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             e->mark("l1_grad");
         }
         // the backward stores per-(tile, Gaussian) sums; the gather adds them per Gaussian in emit order, so
-        // the gradients do not depend on the order in which tiles finish (no float atomics)
-        sxk::raster_bwd_begin(e->stamp.p, e->touched.p, c.count, e->long_count.p, s);
+        // the gradients do not depend on the order in which tiles finish (no float atomics). Its stamp, the
+        // touched flags and the long-range queue were set up by the preprocess.
         sxk::RasterBwdGrads gg{nullptr, nullptr,   nullptr,    nullptr,    nullptr,
                                e->grads.p, e->part.p, e->stamp.p, e->touched.p};
         sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);

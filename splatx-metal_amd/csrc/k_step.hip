@@ -62,7 +62,7 @@ __device__ __forceinline__ float adam_update(float* __restrict__ p, float* __res
 template <int NC>
 __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, float4* __restrict__ splats,
                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
-                                                       uint32_t* __restrict__ vis_part) {
+                                                       uint32_t* __restrict__ vis_part, StepClear clr) {
     __shared__ uint32_t s_vis[kBlock / 64], s_isect[kBlock / 64], s_emit[kBlock / 64];
     uint32_t n_tiles_sum = 0;  // this lane's tile count; summed per block below
     const int i = blockIdx.x * kBlock + threadIdx.x;
@@ -120,6 +120,12 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
         }
         tiles[i] = cnt;
         n_tiles_sum = static_cast<uint32_t>(cnt);
+        if (clr.touched) clr.touched[i] = 0;
+    }
+    if (clr.stamp && blockIdx.x == 0 && threadIdx.x == 0) {
+        *clr.long_count = 0;
+        const uint32_t next = *clr.stamp + 1u;
+        *clr.stamp = next ? next : 1u;  // never 0: zeroed entries hold 0
     }
     // visible count, tile count and count of Gaussians with tiles per block (plain stores; a single
     // global counter would serialize every wave)
@@ -777,14 +783,14 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* n_visible, unsigned long long* block_base,
                      unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
-                     hipStream_t s) {
+                     const StepClear& clr, hipStream_t s) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
-        case 1: hipLaunchKernelGGL(k_preprocess<1>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
-        case 4: hipLaunchKernelGGL(k_preprocess<4>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
-        case 9: hipLaunchKernelGGL(k_preprocess<9>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
-        case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part); break;
+        case 1: hipLaunchKernelGGL(k_preprocess<1>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part, clr); break;
+        case 4: hipLaunchKernelGGL(k_preprocess<4>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part, clr); break;
+        case 9: hipLaunchKernelGGL(k_preprocess<9>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part, clr); break;
+        case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part, clr); break;
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),

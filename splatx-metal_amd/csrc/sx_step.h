@@ -51,10 +51,18 @@ struct StepConst {
 // blocks before it (2 u64)
 // host_counts (mapped host memory, may be null) receives words 0 and 1 of out_vis, then `seq` in its
 // word 4 (release order: a host that reads seq there reads the counts).
+// What a training step's backward starts from, set by its preprocess (null touched: nothing): the
+// rows' touched flags cleared, the gather's long-range queue emptied and the backward's stamp advanced
+// (never to 0: zeroed entries hold 0).
+struct StepClear {
+    uint8_t* touched = nullptr;
+    uint32_t* stamp = nullptr;
+    int32_t* long_count = nullptr;
+};
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
                      unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
-                     hipStream_t s);
+                     const StepClear& clr, hipStream_t s);
 // number of blocks of step_preprocess
 int step_preprocess_blocks(int64_t count);
 // The Gaussians with tiles in index order (list[j], j below out_vis[2]) and (cum set) cum[j], the
