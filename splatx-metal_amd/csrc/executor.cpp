@@ -422,11 +422,19 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
                                  e->long_list.p, e->long_count.p, s, n_emit_i);
         e->mark("gather");
-        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s, overflow_dev);
+        sxk::StepLoss loss{};
+        loss.l1p = e->l1_part.p;
+        loss.n_l1 = n_l1;
+        loss.ssp = e->ssim_part.p;
+        loss.n_ss = n_ss;
+        loss.n_px = static_cast<double>(n_px);
+        loss.M = static_cast<double>(map_n);
+        loss.lam = e->d.ssim_weight;
+        loss.use_ssim = use_ssim ? 1 : 0;
+        loss.out = e->loss_dev.p;
+        loss.rb = rb;
+        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s, overflow_dev, loss);
         e->mark("postprocess");
-        sxk::step_loss_final(e->l1_part.p, n_l1, e->ssim_part.p, n_ss, static_cast<double>(n_px),
-                             static_cast<double>(map_n), e->d.ssim_weight, use_ssim ? 1 : 0, e->loss_dev.p, s, rb);
-        e->mark("loss");
     };
     // Segment B as a hipGraph (captured while the GPU runs segment A; an executable graph per step kind
     // is updated in place while the step's shape stays the same), unless per-kernel profiling is on or

@@ -525,13 +525,58 @@ __global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ k
     off[t] = static_cast<int32_t>(lo);
 }
 
+__device__ double block_sum_fixed(const double* __restrict__ p, int n, double* s_red) {
+    double acc = 0.0;
+    int k = threadIdx.x;
+    // eight independent loads in flight, summed in the same (ascending) order as the plain loop
+    for (; k + 7 * kBlock < n; k += 8 * kBlock) {
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = p[k + j * kBlock];
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc += v[j];
+    }
+    for (; k < n; k += kBlock) acc += p[k];
+    s_red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = kBlock / 2; o > 0; o >>= 1) {
+        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
+        __syncthreads();
+    }
+    const double r = s_red[0];
+    __syncthreads();
+    return r;
+}
+
+// The step's loss from the per-block partial sums, by a whole workgroup: loss = (1-lam) * float(l1_sum /
+// n_px) + lam * (1 - float(ssim_sum / M)) (or the L1 alone); thread 0 stores it and, with rb.host set,
+// the loss and rb's words into mapped host memory.
+__device__ void loss_final(const StepLoss& L, double* s_red) {
+    const double l1s = block_sum_fixed(L.l1p, L.n_l1, s_red);
+    const double sss = L.use_ssim ? block_sum_fixed(L.ssp, L.n_ss, s_red) : 0.0;
+    if (threadIdx.x == 0) {
+        const float l1 = static_cast<float>(l1s / L.n_px);
+        const float loss =
+            L.use_ssim ? (1.0f - L.lam) * l1 + L.lam * (1.0f - static_cast<float>(sss / L.M)) : l1;
+        L.out[0] = loss;
+        if (L.rb.host) {
+            store_host(&L.rb.host[0], __float_as_uint(loss));
+            store_host(&L.rb.host[1], *L.rb.sort_err);
+            store_host(&L.rb.host[2], *L.rb.max_tile);
+        }
+    }
+}
+
 // NC = the arena's SH coefficient count (1, 4, 9 or 16), a compile-time bound so that the SH basis and
 // its partials stay in registers
 template <int NC>
 __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, const float4* __restrict__ splats,
                                                         const float4* __restrict__ grads,
                                                         const uint8_t* __restrict__ touched,
-                                                        const unsigned long long* __restrict__ skip) {
+                                                        const unsigned long long* __restrict__ skip, StepLoss L) {
+    __shared__ double s_red[kBlock];
+    // the first workgroup also reduces the loss (every thread of it, before any leaves)
+    if (L.out && blockIdx.x == 0) loss_final(L, s_red);
     if (skip && *skip) return;  // the step overflowed its buffers and runs again: leave the arena as it was
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= c.count) return;
@@ -714,47 +759,6 @@ __global__ void __launch_bounds__(kBlock) k_l1(const float* __restrict__ render,
     if (threadIdx.x == 0) partials[blockIdx.x] = s_red[0];
 }
 
-__device__ double block_sum_fixed(const double* __restrict__ p, int n, double* s_red) {
-    double acc = 0.0;
-    int k = threadIdx.x;
-    // eight independent loads in flight, summed in the same (ascending) order as the plain loop
-    for (; k + 7 * kBlock < n; k += 8 * kBlock) {
-        double v[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = p[k + j * kBlock];
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc += v[j];
-    }
-    for (; k < n; k += kBlock) acc += p[k];
-    s_red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int o = kBlock / 2; o > 0; o >>= 1) {
-        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
-        __syncthreads();
-    }
-    const double r = s_red[0];
-    __syncthreads();
-    return r;
-}
-
-__global__ void __launch_bounds__(kBlock) k_loss_final(const double* __restrict__ l1p, int n_l1,
-                                                       const double* __restrict__ ssp, int n_ss, double n_px, double M,
-                                                       float lam, int use_ssim, float* __restrict__ out,
-                                                       StepReadback rb) {
-    __shared__ double s_red[kBlock];
-    const double l1s = block_sum_fixed(l1p, n_l1, s_red);
-    const double sss = use_ssim ? block_sum_fixed(ssp, n_ss, s_red) : 0.0;
-    if (threadIdx.x == 0) {
-        const float l1 = static_cast<float>(l1s / n_px);
-        const float loss = use_ssim ? (1.0f - lam) * l1 + lam * (1.0f - static_cast<float>(sss / M)) : l1;
-        out[0] = loss;
-        if (rb.host) {
-            store_host(&rb.host[0], __float_as_uint(loss));
-            store_host(&rb.host[1], *rb.sort_err);
-            store_host(&rb.host[2], *rb.max_tile);
-        }
-    }
-}
 
 __global__ void k_step_readback(StepReadback rb) {
     store_host(&rb.host[0], 0u);
@@ -844,14 +848,15 @@ void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* of
 }
 
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
-                      const uint8_t* touched, hipStream_t s, const unsigned long long* skip) {
+                      const uint8_t* touched, hipStream_t s, const unsigned long long* skip,
+                      const StepLoss& loss) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
-        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
-        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
-        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
-        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads, touched, skip); break;
+        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
+        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
+        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
+        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
         default: throw std::invalid_argument("postprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
 }
@@ -862,12 +867,6 @@ void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_rend
                   hipStream_t s) {
     const float g = 1.0f / static_cast<float>(n);
     hipLaunchKernelGGL(k_l1, dim3(n_blocks), dim3(kBlock), 0, s, render, gt, n, g, v_render, partials);
-}
-
-void step_loss_final(const double* l1p, int n_l1, const double* ssp, int n_ss, double n_px, double M, float lam,
-                     int use_ssim, float* out, hipStream_t s, const StepReadback& rb) {
-    hipLaunchKernelGGL(k_loss_final, dim3(1), dim3(kBlock), 0, s, l1p, n_l1, ssp, n_ss, n_px, M, lam, use_ssim, out,
-                       rb);
 }
 
 void step_readback(const StepReadback& rb, hipStream_t s) {

@@ -89,9 +89,33 @@ void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* of
                        const int64_t* n_dev = nullptr);
 void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev = nullptr);
-// skip (when set): a device word; nonzero leaves the arena untouched (the overflow word of out_vis)
+// The words a step reports to the host, stored by its last kernel straight into mapped host memory
+// (host: 3 u32, the loss bits, the sort's error flag, the largest tile's entry count) instead of one
+// copy each. Null host: nothing is stored.
+struct StepReadback {
+    const uint32_t* sort_err = nullptr;
+    const uint32_t* max_tile = nullptr;
+    uint32_t* host = nullptr;
+};
+// A training step's loss, reduced by the postprocess's first workgroup from the per-block partial sums
+// (fixed order): loss = (1-lam) * float(l1_sum / n_px) + lam * (1 - float(ssim_sum / M)) (or the L1
+// alone) into out[0]; with rb.host set, the loss and rb's words also go to the host. Null out: none.
+struct StepLoss {
+    const double* l1p = nullptr;
+    int n_l1 = 0;
+    const double* ssp = nullptr;
+    int n_ss = 0;
+    double n_px = 1.0, M = 1.0;
+    float lam = 0.0f;
+    int use_ssim = 0;
+    float* out = nullptr;
+    StepReadback rb{};
+};
+// skip (when set): a device word; nonzero leaves the arena untouched (the overflow word of out_vis);
+// loss: the step's loss (computed whatever skip holds)
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
-                      const uint8_t* touched, hipStream_t s, const unsigned long long* skip = nullptr);
+                      const uint8_t* touched, hipStream_t s, const unsigned long long* skip = nullptr,
+                      const StepLoss& loss = {});
 // Noise only (the forward-only path never calls it; a training step fuses it into postprocess).
 // L1 gradient without SSIM: v_render = sign(render - gt) / n, per-block f64 sums of |render - gt|.
 void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_render, double* partials,
@@ -102,19 +126,6 @@ void step_ssim_bwd_l1(const float* render, const float* gt, const float* cmu, co
                       const float* ccr, int H, int W, float G, float w_l1, float g_l1, float* v_render,
                       double* l1_partials, hipStream_t s);
 int step_ssim_bwd_blocks(int H, int W);
-// The words a step reports to the host, stored by its last kernel straight into mapped host memory
-// (host: 3 u32, the loss bits, the sort's error flag, the largest tile's entry count) instead of one
-// copy each. Null host: nothing is stored.
-struct StepReadback {
-    const uint32_t* sort_err = nullptr;
-    const uint32_t* max_tile = nullptr;
-    uint32_t* host = nullptr;
-};
-// loss = (1-lam) * float(l1_sum / n_px) + lam * (1 - float(ssim_sum / M)) (or the L1 alone); with
-// rb.host set, the loss and rb's words also go to the host
-void step_loss_final(const double* l1_partials, int n_l1, const double* ssim_partials, int n_ssim,
-                     double n_px, double M, float lam, int use_ssim, float* loss_out, hipStream_t s,
-                     const StepReadback& rb = {});
 // rb's words to the host without a loss (the loss word is 0): the forward-only step
 void step_readback(const StepReadback& rb, hipStream_t s);
 void aos_to_soa(const float* aos, float* soa, int rows, int dim, int stride, hipStream_t s);
