@@ -338,6 +338,7 @@ def main():
     # timed loop: the product path (segment B of each step replayed as a captured hipGraph)
     totals = {}
     n_isects, n_vis, losses, passes, step_ms = [], [], [], [], []
+    ex.sync()  # the warm-up's last parameter update is done before the clock starts
     t0 = time.perf_counter()
     for k in range(args.warmup, n_poses):
         if mcmc and count != sc.n:
@@ -358,6 +359,7 @@ def main():
             refine_ms.append((time.perf_counter() - tr) * 1000.0)
             count = r["count"]
             counts.append(count)
+    ex.sync()  # a step returns at its loss: the last parameter update is inside the timed region
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1000.0 / args.steps
     # per-kernel times: the timed region's work again — the same start state, warm-up and poses — with

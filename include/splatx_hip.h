@@ -371,8 +371,13 @@ void sxh_exec_destroy(sxh_executor* e);
 /* TrainStepExecutor::upload_params / download_params. */
 int32_t sxh_exec_upload(sxh_executor* e, const sxh_param_sync* s);
 int32_t sxh_exec_download(sxh_executor* e, const sxh_param_sync* s);
-/* TrainStepExecutor::step: two host sync points (n_isects, loss). */
+/* TrainStepExecutor::step: two host sync points (n_isects, loss). It returns once the loss is read
+ * back; without a render read-back the device may still be finishing the step's parameter update,
+ * which every later call on the executor (the next step, a download, a refine) is ordered after. */
 int32_t sxh_exec_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out);
+/* Waits until the executor's device work has finished (for a caller that times steps). No
+ * counterpart in the reference (its step returns after its command buffers complete). */
+int32_t sxh_exec_sync(sxh_executor* e);
 /* Device-resident GT cache: n_images images of [height,width,3] floats, uploaded once. */
 int32_t sxh_exec_set_gt_cache(sxh_executor* e, const float* images, int32_t n_images,
                               int32_t width, int32_t height);

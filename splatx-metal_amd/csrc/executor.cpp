@@ -173,6 +173,13 @@ int32_t sxh_exec_get_raster_stats(sxh_executor* e, sxh_raster_stats* out) {
     });
 }
 
+int32_t sxh_exec_sync(sxh_executor* e) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor", "null executor");
+        SXH_HIP(hipStreamSynchronize(e->b->stream));
+    });
+}
+
 int32_t sxh_exec_set_graph(sxh_executor* e, int32_t enable) {
     return guarded([&] {
         if (!e) invalid("TrainStepExecutor", "null executor");
@@ -198,9 +205,10 @@ int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out) {
 
 } // extern "C"
 
-// Sync 1 of a step whose segment B is already queued: wait until the block scan has stored `seq` into
-// the mapped word (its counts are then in place). The stream is polled now and then, so that an error
-// or a stream that finished without the store ends the wait instead of spinning forever.
+// A sync point of the step: wait until a kernel has stored `seq` into the mapped word (sync 1: the
+// block scan, its counts then in place; sync 2: the postprocess's first workgroup, the loss). The
+// stream is polled now and then, so that an error or a stream that finished without the store ends
+// the wait instead of spinning forever.
 static void wait_count_word(volatile unsigned long long* word, unsigned long long seq, hipStream_t s,
                             const char* what) {
     for (uint32_t spins = 1;; spins++) {
@@ -209,7 +217,7 @@ static void wait_count_word(volatile unsigned long long* word, unsigned long lon
             const hipError_t q = hipStreamQuery(s);
             if (q == hipSuccess) {
                 if (*word == seq) return;
-                throw std::runtime_error(std::string(what) + ": the step's count word was not written");
+                throw std::runtime_error(std::string(what) + ": the step's read-back word was not written");
             }
             if (q != hipErrorNotReady) SXH_HIP(q);
         }
@@ -392,8 +400,10 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         ra.tile_order = e->tile_order.p;
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
         e->mark("raster_fwd");
+        // the loss words, then the launch's sequence number (word 5 of the block)
         const sxk::StepReadback rb{sxk::sort_error_flag(e->sort_scratch.p), e->max_tile.p,
-                                   reinterpret_cast<uint32_t*>(static_cast<unsigned long long*>(e->step_rb.dev) + 2)};
+                                   reinterpret_cast<uint32_t*>(static_cast<unsigned long long*>(e->step_rb.dev) + 2),
+                                   static_cast<unsigned long long*>(e->step_rb.dev) + 5, seq};
         if (fwd_only) {
             sxk::step_readback(rb, s);
             return;
@@ -525,8 +535,15 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     out->sort_key_bits = 32 + c.tile_n_bits;
     out->n_visible = static_cast<int64_t>(hc[0]);
     // ---- sync 2: loss (MetalBackend.cpp:2241-2261) ----------------------------------------------------
+    // The loss, the sort's error word and the largest tile's count are stored by the postprocess's first
+    // workgroup, with the step's sequence number after them: the host returns once it sees that number,
+    // while the postprocess may still run; everything later on the stream (the next step, a download, a
+    // refine) is ordered after it. A render read-back or profiling waits for the whole stream.
     const auto t0 = std::chrono::steady_clock::now();
-    SXH_HIP(hipStreamSynchronize(s));
+    if (!e->prof && !e->prof_stats && !render_to_dev && !out->render_colors)
+        wait_count_word(hc + 5, seq, s, what);
+    else
+        SXH_HIP(hipStreamSynchronize(s));
     e->sync_ms[1] = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     const uint32_t loss_bits = hw[0], sort_err = hw[1], max_tile = hw[2];
     float loss = 0.0f;

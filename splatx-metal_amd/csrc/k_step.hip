@@ -563,6 +563,7 @@ __device__ void loss_final(const StepLoss& L, double* s_red) {
             store_host(&L.rb.host[0], __float_as_uint(loss));
             store_host(&L.rb.host[1], *L.rb.sort_err);
             store_host(&L.rb.host[2], *L.rb.max_tile);
+            __hip_atomic_store(L.rb.seq_host, L.rb.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }
@@ -764,6 +765,7 @@ __global__ void k_step_readback(StepReadback rb) {
     store_host(&rb.host[0], 0u);
     store_host(&rb.host[1], *rb.sort_err);
     store_host(&rb.host[2], *rb.max_tile);
+    __hip_atomic_store(rb.seq_host, rb.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __global__ void __launch_bounds__(kBlock) k_aos_to_soa(const float* __restrict__ aos, float* __restrict__ soa, int rows,

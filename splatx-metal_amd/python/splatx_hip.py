@@ -768,7 +768,7 @@ class Executor:
         self.h = h
         for n in ("sxh_exec_upload", "sxh_exec_download", "sxh_exec_step", "sxh_exec_set_gt_cache",
                   "sxh_exec_render_to_gt_cache", "sxh_exec_set_profiling", "sxh_exec_get_timing", "sxh_exec_set_graph",
-                  "sxh_exec_set_isect_order", "sxh_exec_mcmc_refine"):
+                  "sxh_exec_set_isect_order", "sxh_exec_mcmc_refine", "sxh_exec_sync"):
             getattr(self.lib, n).restype = C.c_int32
         self.lib.sxh_exec_destroy.argtypes = [C.c_void_p]
 
@@ -966,6 +966,11 @@ class Executor:
         f.restype = C.c_int32
         self._check(f(self.h, C.byref(st)))
         return {k: int(getattr(st, k)) for k, _ in RasterStats._fields_}
+
+    def sync(self):
+        """Wait until the executor's device work has finished (a step returns once its loss is read
+        back, possibly before its parameter update completes on the device)."""
+        self._check(self.lib.sxh_exec_sync(self.h))
 
     def set_graph(self, enable: bool):
         """Run the step's second segment as a captured hipGraph (default) or as direct launches."""
