@@ -249,29 +249,38 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             T = take ? next_T : T;
             if (STATS) st_taken += __popcll(__ballot(take));
         };
-        // two list entries per iteration: their sigmas and exponentials are independent, only T and
-        // the colour sums run through them in order
-        for (int j = 0; j < n_it; j += 2) {
+        // four list entries per iteration (their indices in one LDS read): their sigmas and exponentials
+        // are independent, only T and the colour sums run through them in order
+        for (int j = 0; j < n_it; j += 4) {
             if (__all(done)) break;  // uniform
-            const int raw0 = my_list[j], raw1 = my_list[min(j + 1, kThreads - 1)];  // past the list: masked
-            const int t0 = j < len ? raw0 : -1, t1 = j + 1 < len ? raw1 : -1;  // group-uniform
-            const int tc0 = t0 < 0 ? 0 : t0, tc1 = t1 < 0 ? 0 : t1;
-            const float4 xyo0 = s_xyo[tc0], con0 = s_con[tc0];
-            const float4 xyo1 = s_xyo[tc1], con1 = s_con[tc1];
-            const float sg0 = sigma_of(con0.x, con0.y, con0.z, xyo0.x - px, xyo0.y - py);
-            const float sg1 = sigma_of(con1.x, con1.y, con1.z, xyo1.x - px, xyo1.y - py);
-            const bool in0 = (t0 >= 0) & !done & !(sg0 > xyo0.w);
-            const bool in1 = (t1 >= 0) & !done & !(sg1 > xyo1.w);
-            if (STATS) {
-                st_iters += 1 + (j + 1 < n_it ? 1 : 0);
-                st_entries += __popcll(__ballot((lane & 15) == 0 && t0 >= 0)) + __popcll(__ballot((lane & 15) == 0 && t1 >= 0));
+            // bytes past the list are masked (stale or never written); the row is 16-B aligned, j a
+            // multiple of 4 and at most 252
+            const uint32_t packed = *reinterpret_cast<const uint32_t*>(my_list + j);
+            int t[4], tc[4];
+            float4 xyo[4], con[4];
+            float sg[4];
+            bool in[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                t[k] = j + k < len ? static_cast<int>((packed >> (8 * k)) & 0xFFu) : -1;  // group-uniform
+                tc[k] = t[k] < 0 ? 0 : t[k];  // slot 0 holds a record of this batch
+                xyo[k] = s_xyo[tc[k]];
+                con[k] = s_con[tc[k]];
+                sg[k] = sigma_of(con[k].x, con[k].y, con[k].z, xyo[k].x - px, xyo[k].y - py);
+                in[k] = (t[k] >= 0) & !done & !(sg[k] > xyo[k].w);
             }
-            if (!__any(in0 | in1)) continue;  // uniform
-            const float vis0 = general ? sxm::expf_fast(-sg0) : exp_neg_poly(sg0);
-            const float vis1 = general ? sxm::expf_fast(-sg1) : exp_neg_poly(sg1);
-            // front to back: a lane that stopped at entry 0 takes nothing more
-            composite(in0, sg0, xyo0.z * vis0, tc0, bstart + t0);
-            composite(in1, sg1, xyo1.z * vis1, tc1, bstart + t1);
+            if (STATS) {
+                st_iters += min(4, n_it - j);
+#pragma unroll
+                for (int k = 0; k < 4; k++) st_entries += __popcll(__ballot((lane & 15) == 0 && t[k] >= 0));
+            }
+            if (!__any(in[0] | in[1] | in[2] | in[3])) continue;  // uniform
+            float vis[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) vis[k] = general ? sxm::expf_fast(-sg[k]) : exp_neg_poly(sg[k]);
+            // front to back: a lane that stopped at an entry takes nothing more
+#pragma unroll
+            for (int k = 0; k < 4; k++) composite(in[k], sg[k], xyo[k].z * vis[k], tc[k], bstart + t[k]);
         }
     }
     if (STATS && lane == 0) {
