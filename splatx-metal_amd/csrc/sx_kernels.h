@@ -190,7 +190,7 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 // entries at [cum[j-1], cum[j]) that carry the current stamp (order and cum: the depth order and the
 // inclusive scan of its tile counts that placed the emit), in a fixed order per range: the
 // deterministic end of raster_bwd's `part` mode. Untouched Gaussians' records are not written. long_list
-// holds `count` ints, long_count one (reset by raster_bwd_begin). With count_dev the positions are the
+// holds `count` ints, long_count one (reset by raster_bwd_begin or the step's preprocess). With count_dev the positions are the
 // first *count_dev (<= count, which sizes the grid).
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part,
                          const uint32_t* stamp, const uint8_t* touched, float4* grads, int32_t* long_list,
