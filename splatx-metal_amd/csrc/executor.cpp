@@ -398,6 +398,9 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         ra.id_of = e->emit_gid.p;  // the sorted values are emit positions
         ra.stats = e->prof_stats ? e->rstats.p : nullptr;  // never in a captured graph (profiling launches directly)
         ra.tile_order = e->tile_order.p;
+        // the block masks go where the tile ids were: both key buffers are free once the offsets (and,
+        // index first, the per-tile depth sort) are done
+        ra.block_masks = fwd_only ? nullptr : reinterpret_cast<uint16_t*>(e->keys_a.p);
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
         e->mark("raster_fwd");
         // the loss words, then the launch's sequence number (word 5 of the block)

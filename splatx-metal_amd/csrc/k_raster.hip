@@ -217,6 +217,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             s_con[tid] = con;
             s_rgb[tid] = a.splats[(size_t)g * 3 + 2];
             bm = block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
+            if (a.block_masks) a.block_masks[idx] = static_cast<uint16_t>(bm);
             big = bm != 0u && xyo.w > 86.0f;
         }
         {
@@ -499,8 +500,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
             s_xyo[tid] = xyo;
             s_con[tid] = con;
             s_rgb[tid] = rgb;
-            // blocks the cutoff set can reach, less those whose every pixel stopped before it
-            bm = block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
+            // blocks the cutoff set can reach (the forward's, when it kept them), less those whose every
+            // pixel stopped before it
+            bm = a.block_masks ? static_cast<uint32_t>(a.block_masks[idx])
+                               : block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
 #pragma unroll
             for (int k = 0; k < kBlocks; k++)
                 if (idx > s_bbf[k]) bm &= ~(1u << k);

@@ -140,6 +140,11 @@ struct RasterArgs {
     // optional (profiling): pair counters the rasterisers add into, kRasterStat* indices; null in
     // production (the counting kernels are separate instantiations)
     unsigned long long* stats;
+    // optional: one u16 per intersection, the 4x4 blocks its splat's cutoff set reaches in its tile;
+    // the forward stores the mask of every entry it loads, the backward reads it instead of working it
+    // out again (the forward loads every entry up to each tile's last contributor, which is as far as
+    // the backward goes). Null: both compute it.
+    uint16_t* block_masks;
 };
 // raster pair counters (RasterArgs::stats): forward wave iterations (x 64 lane pairs), block-list
 // entries walked (one splat against a 4x4 block) and pairs composited; backward 4-iteration chunks
