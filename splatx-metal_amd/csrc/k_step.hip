@@ -509,7 +509,29 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
 }
 
 // offsets[t] = first position of tile t in the sorted tile ids (lower bound; n for trailing empty
-// tiles) — the isect_offset_encode contract for one image
+// tiles) — the isect_offset_encode contract for one image. Two ways: a binary search per tile (cost
+// independent of n), or a pass over the ids in which position i writes the tiles t with
+// ids[i-1] < t <= ids[i] (ids[-1] = -1, ids[n] = n_tiles), every offset once (a few MB read, no
+// dependent loads: faster up to some tens of millions of ids).
+constexpr int kOffPer = 8;  // positions per thread of the pass
+template <class K>
+__global__ void __launch_bounds__(kBlock) k_tile_offsets_pass(const K* __restrict__ keys, int64_t n, int n_tiles,
+                                                              int32_t* __restrict__ off,
+                                                              const int64_t* __restrict__ n_dev) {
+    if (n_dev) n = *n_dev;
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * kOffPer;
+    if (i0 > n) return;
+    int prev = i0 == 0 ? -1 : static_cast<int>(keys[i0 - 1]);
+#pragma unroll
+    for (int k = 0; k < kOffPer; k++) {
+        const int64_t i = i0 + k;
+        if (i > n) break;
+        const int cur = i == n ? n_tiles : static_cast<int>(keys[i]);
+        for (int t = prev + 1; t <= cur && t < n_tiles; t++) off[t] = static_cast<int32_t>(i);
+        prev = cur;
+    }
+}
+
 template <class K>
 __global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ keys, int64_t n, int n_tiles,
                                                          int32_t* __restrict__ off, const int64_t* __restrict__ n_dev) {
@@ -835,18 +857,30 @@ void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* r
                        cum, keys, vals, edepth, n_pos);
 }
 
+// n (the count, or with n_dev its upper bound) picks the way: the pass up to 2^25 ids
+constexpr int64_t kOffPassMax = int64_t{1} << 25;
+template <class K>
+static void launch_tile_offsets(const K* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
+                                const int64_t* n_dev) {
+    if (n_tiles <= 0) return;
+    if (n <= kOffPassMax) {
+        const int64_t threads = n / kOffPer + 1;  // positions 0..n
+        hipLaunchKernelGGL(k_tile_offsets_pass<K>, dim3(grid_for(threads)), dim3(kBlock), 0, s, keys, n, n_tiles,
+                           offsets, n_dev);
+    } else {
+        hipLaunchKernelGGL(k_tile_offsets<K>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles, offsets,
+                           n_dev);
+    }
+}
+
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev) {
-    if (n_tiles <= 0) return;
-    hipLaunchKernelGGL(k_tile_offsets<uint16_t>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles,
-                       offsets, n_dev);
+    launch_tile_offsets(keys, n, n_tiles, offsets, s, n_dev);
 }
 
 void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev) {
-    if (n_tiles <= 0) return;
-    hipLaunchKernelGGL(k_tile_offsets<uint32_t>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles,
-                       offsets, n_dev);
+    launch_tile_offsets(keys, n, n_tiles, offsets, s, n_dev);
 }
 
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
