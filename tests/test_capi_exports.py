@@ -47,3 +47,12 @@ def test_executor_switches_reject_a_null_executor_without_gpu():
         f.argtypes = [ctypes.c_void_p, ctypes.c_int32]
         assert f(None, 1) != 0, name
         assert b"null executor" in lib.sxh_last_error(), name
+
+
+def test_executor_sync_rejects_a_null_executor_without_gpu():
+    lib = ctypes.CDLL(LIB)
+    lib.sxh_last_error.restype = ctypes.c_char_p
+    lib.sxh_exec_sync.restype = ctypes.c_int32
+    lib.sxh_exec_sync.argtypes = [ctypes.c_void_p]
+    assert lib.sxh_exec_sync(None) != 0
+    assert b"null executor" in lib.sxh_last_error()

@@ -105,3 +105,39 @@ def test_graph_training_steps_match_direct_launches(gpu):
                 assert rel_l2(x, y) <= 1e-4, (grp, rel_l2(x, y))
     eg.close()
     ed.close()
+
+
+def test_steps_returning_at_the_loss_match_fully_synced_steps(gpu):
+    """A step without a render read-back returns once its loss is read back, while its parameter update
+    may still run; the next step's preprocess is ordered after it on the executor's stream. Five such
+    steps back to back must leave exactly the parameters, losses and counts of five steps that each
+    wait for the whole stream (a render read-back forces that)."""
+    sc = scene.make_scene(n=8000, sh_degree=3, width=160, height=128, fx=140.0, seed=13)
+    execs = []
+    for _ in range(2):
+        ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=0.2,
+                                          isect_mode=sh.SXH_ISECT_ACCUTILE)
+        ex.upload_params(*scene.copy_state(sc), sc.n)
+        execs.append(ex)
+    early, synced = execs
+    rng = np.random.Generator(np.random.PCG64(5))
+    views = [scene.jittered_view(rng) for _ in range(5)]
+    out_e, out_s = [], []
+    for it, vm in enumerate(views):
+        kw = dict(scene.step_kwargs(sc), viewmat=vm, inject_noise=True, noise_seed=3, noise_offset=it,
+                  noise_scale=0.1)
+        print(f"early-return step {it}", flush=True)
+        out_e.append(early.step(gt_rgb=sc.gt, **kw))
+        out_s.append(synced.step(want_render=True, gt_rgb=sc.gt, **kw))
+    early.sync()
+    for it, (a, b) in enumerate(zip(out_e, out_s)):
+        assert a["n_isects"] == b["n_isects"], it
+        assert np.float32(a["loss"]).view(np.uint32) == np.float32(b["loss"]).view(np.uint32), (it, a, b)
+    pa, pb = scene.copy_state(sc), scene.copy_state(sc)
+    early.download_params(*pa, sc.n)
+    synced.download_params(*pb, sc.n)
+    for grp in range(3):
+        for x, y in zip(pa[grp], pb[grp]):
+            assert np.array_equal(np.asarray(x).view(np.uint32), np.asarray(y).view(np.uint32)), grp
+    early.close()
+    synced.close()
