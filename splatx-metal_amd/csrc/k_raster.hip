@@ -992,6 +992,7 @@ __device__ __forceinline__ uint64_t same_byte_lanes(uint32_t b, bool valid) {
     return match;
 }
 
+constexpr int kOrderKeep = 8;  // tile counts a thread of k_tile_order keeps (8192 tiles: 1920x1080)
 __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__ offsets, int n_tiles,
                                                      int64_t n_isects, int32_t* __restrict__ order,
                                                      const int64_t* __restrict__ n_isects_dev,
@@ -1008,8 +1009,18 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
         const int64_t e = t + 1 < n_tiles ? offsets[t + 1] : n_isects;
         return static_cast<uint32_t>(e - offsets[t]);
     };
+    // the counts of the thread's first kOrderKeep tiles stay in registers for the two later passes
+    // (one round of loads instead of three); tiles past 1024 kOrderKeep are loaded again
+    uint32_t kept[kOrderKeep];
     uint32_t mx = 0;
-    for (int t = t0; t < n_tiles; t += 1024) mx = max(mx, count_of(t));
+#pragma unroll
+    for (int r = 0; r < kOrderKeep; r++) {
+        const int t = t0 + 1024 * r;
+        kept[r] = t < n_tiles ? count_of(t) : 0u;
+        mx = max(mx, kept[r]);
+    }
+    for (int t = t0 + 1024 * kOrderKeep; t < n_tiles; t += 1024) mx = max(mx, count_of(t));
+    auto count_at = [&](int r, int t) -> uint32_t { return r < kOrderKeep ? kept[r] : count_of(t); };
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), o, 64)));
     if (lane == 0) atomicMax(&s_max, mx);
@@ -1019,10 +1030,10 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
     if (max_count && t0 == 0) *max_count = s_max;
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     // rounds are uniform over the workgroup (every thread runs ceil(n_tiles / 1024) of them)
-    for (int t1 = 0; t1 < n_tiles; t1 += 1024) {
+    for (int t1 = 0, r = 0; t1 < n_tiles; t1 += 1024, r++) {
         const int t = t1 + t0;
         const bool valid = t < n_tiles;
-        const uint32_t b = valid ? 255u - (count_of(t) >> shift) : 0u;
+        const uint32_t b = valid ? 255u - (count_at(r, t) >> shift) : 0u;
         const uint64_t m = same_byte_lanes(b, valid);
         if (valid && (m & below) == 0) atomicAdd(&s_hist[b], static_cast<uint32_t>(__popcll(m)));
     }
@@ -1047,10 +1058,10 @@ __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__
         s_hist[t0] = pre + hx - hc;
     }
     __syncthreads();
-    for (int t1 = 0; t1 < n_tiles; t1 += 1024) {
+    for (int t1 = 0, r = 0; t1 < n_tiles; t1 += 1024, r++) {
         const int t = t1 + t0;
         const bool valid = t < n_tiles;
-        const uint32_t b = valid ? 255u - (count_of(t) >> shift) : 0u;
+        const uint32_t b = valid ? 255u - (count_at(r, t) >> shift) : 0u;
         const uint64_t m = same_byte_lanes(b, valid);
         const int leader = m ? static_cast<int>(__builtin_ctzll(m)) : 0;
         uint32_t base = 0;
