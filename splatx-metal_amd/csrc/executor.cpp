@@ -1,11 +1,12 @@
 // executor.cpp — the device-resident train-step executor (TrainStepExecutor, KernelBackend.h:386-392;
 // the reference's MetalTrainStepExecutor, MetalBackend.cpp:1628-2460).
 //
-// One HIP stream. A step is: preprocess -> int64 scan -> [sync 1: n_isects readback, isect buffers
-// grow 1.5x when needed] -> emit -> radix sort -> offsets -> raster fwd -> SSIM fwd -> SSIM bwd
-// fused with the L1 gradient -> raster bwd -> postprocess (bwd chain + Adam + noise) -> device loss
-// reduction -> [sync 2: loss readback]. Parameters, moments and the GT cache stay in HBM; the
-// arena is sized once for arena_rows and never reallocated.
+// One HIP stream. A step is: preprocess -> block scan [sync 1: n_isects, stored into mapped host
+// memory; isect buffers grow 1.5x when needed] -> compaction -> emit -> radix sort -> offsets -> raster
+// fwd -> SSIM fwd -> SSIM bwd fused with the L1 gradient -> raster bwd -> gather -> postprocess (loss
+// reduction, then bwd chain + Adam + noise) [sync 2: the loss, stored the same way]. Everything after
+// sync 1 is a captured graph, queued before the host waits. Parameters, moments and the GT cache stay
+// in HBM; the arena is sized once for arena_rows and never reallocated.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -288,8 +289,9 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     // `cap`: the intersection capacity segment B may assume; past it, segment B's counts read 0 and the
     // arena update is skipped (n_vis words 3 and 4), so a segment B launched before the count is known
     // leaves everything as it was and the step runs again on grown buffers
-    // the step's read-back block: u64 visible, u64 intersections (stored by segment A's last kernel), u32
-    // loss bits, sort error flag, largest tile (stored by segment B's last kernel)
+    // the step's read-back block: u64 visible, u64 intersections (stored by segment A's block scan), u32
+    // loss bits, sort error flag, largest tile (stored by the postprocess's first workgroup), u64 segment
+    // A's sequence number (word 4, after the counts), u64 the loss's (word 5)
     volatile unsigned long long* const hc = static_cast<volatile unsigned long long*>(e->step_rb.p);
     volatile uint32_t* const hw = reinterpret_cast<volatile uint32_t*>(hc + 2);
     unsigned long long seq = 0;  // the last segment A's sequence number (its count word's tag)
