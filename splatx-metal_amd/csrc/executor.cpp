@@ -406,7 +406,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
         e->mark("raster_fwd");
         // the loss words, then the launch's sequence number (word 5 of the block)
-        const sxk::StepReadback rb{sxk::sort_error_flag(e->sort_scratch.p), e->max_tile.p,
+        const sxk::StepReadback rb{sxk::sort_error_flag(e->sort_scratch.p), e->max_tile.p, e->long_count.p,
                                    reinterpret_cast<uint32_t*>(static_cast<unsigned long long*>(e->step_rb.dev) + 2),
                                    static_cast<unsigned long long*>(e->step_rb.dev) + 5, seq};
         if (fwd_only) {
@@ -434,8 +434,13 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
                                e->grads.p, e->part.p, e->stamp.p, e->touched.p};
         sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
         e->mark("raster_bwd");
+        // long ranges reduced by the gather's own waves while the previous step had few (no second
+        // launch), queued for a wave each otherwise (measured: inline 41 -> 35 us at config 3, queued
+        // 94 us against 329 inline at config 5); either way the same sums
+        constexpr int64_t kInlineLongMax = 1024;
+        const bool inline_long = e->last_long >= 0 && e->last_long <= kInlineLongMax;
         sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
-                                 e->long_list.p, e->long_count.p, s, n_emit_i);
+                                 e->long_list.p, e->long_count.p, s, n_emit_i, inline_long);
         e->mark("gather");
         sxk::StepLoss loss{};
         loss.l1p = e->l1_part.p;
@@ -555,6 +560,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     std::memcpy(&loss, &loss_bits, 4);
     out->loss = fwd_only ? 0.0f : loss;
     e->last_max_tile = n_isects > 0 ? static_cast<int64_t>(max_tile) : 0;
+    if (!fwd_only) e->last_long = static_cast<int64_t>(hw[3]);
     if (e->prof_stats) {
         unsigned long long st[sxk::kRasterStats];
         SXH_HIP(hipMemcpy(st, e->rstats.p, sizeof(st), hipMemcpyDeviceToHost));

@@ -835,6 +835,32 @@ __device__ __forceinline__ void store_grad_record(float4* grads, size_t g, const
     grads[3 * g + 2] = make_float4(v[6], v[7], v[8], 0.f);
 }
 
+// One range [p0, p1) of `part` reduced by a whole wave: 64 entries per round (lane l takes entry
+// base + l when it carries the stamp), each round's values added in a fixed tree (DPP within rows, then
+// across rows) and the rounds in order; every lane ends with the sums.
+__device__ __forceinline__ void reduce_long_range(const float* __restrict__ part, int32_t p0, int32_t p1,
+                                                  uint32_t stamp, float* v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
+    for (int32_t base = p0; base < p1; base += 64) {
+        const int32_t p = base + lane;
+        float x[kPartFloats];
+        const bool on = load_entry(part, min(p, p1 - 1), stamp, x) & (p < p1);
+#pragma unroll
+        for (int k = 0; k < kPartFloats; k++) {
+            float y = on ? x[k] : 0.f;
+            y += dpp_f<0xB1>(y);   // quad_perm(1,0,3,2)
+            y += dpp_f<0x4E>(y);   // quad_perm(2,3,0,1)
+            y += dpp_f<0x141>(y);  // row_half_mirror
+            y += dpp_f<0x140>(y);  // row_mirror: the 16-lane row total
+            y += __shfl_xor(y, 16, 64);
+            y += __shfl_xor(y, 32, 64);
+            v[k] += y;
+        }
+    }
+}
+
 constexpr int kGatherWave = 64;    // emit positions per gather workgroup (one wave)
 constexpr int kGatherStage = 256;  // entries staged in LDS per round
 
@@ -846,8 +872,12 @@ constexpr int kGatherStage = 256;  // entries staged in LDS per round
 // own range from there, in order. Entries without this step's stamp (tiles that never reached the
 // Gaussian) are staged as zeros: an added +0 leaves every partial sum as it was (a sum that starts at
 // +0 never becomes -0). A Gaussian with no stamped entry (exactly the untouched ones) stages nothing
-// and gets no record: the postprocess reads zeros for it. Ranges longer than kLongRange are queued for
-// k_gather_long when touched (the queue's order does not matter: each range is reduced on its own).
+// and gets no record: the postprocess reads zeros for it. Touched ranges longer than kLongRange are
+// either queued for k_gather_long (the queue's order does not matter: each range is reduced on its
+// own) or, with inline_long, reduced by the wave itself after its short ranges, one after another,
+// and only counted in *long_count; both reduce a range the same way (the same sums, bit for bit).
+// Inline suits steps with few long ranges (it saves the second launch); many of them, one after
+// another per wave, are far slower than the queue's wave per range.
 __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const int32_t* __restrict__ order,
                                                               const int64_t* __restrict__ cum,
                                                               const float* __restrict__ part,
@@ -856,7 +886,8 @@ __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const i
                                                               float4* __restrict__ grads,
                                                               int32_t* __restrict__ long_list,
                                                               int32_t* __restrict__ long_count,
-                                                              const int64_t* __restrict__ count_dev) {
+                                                              const int64_t* __restrict__ count_dev,
+                                                              int inline_long) {
     __shared__ float s_rec[kGatherStage][kPartFloats];  // odd row stride: lanes on different rows, different banks
     __shared__ int32_t s_off[kGatherWave];              // each lane's first staged entry
     __shared__ int32_t s_src[kGatherWave];              // each lane's first entry in `part`
@@ -864,17 +895,23 @@ __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const i
     const int j = blockIdx.x * kGatherWave + lane;
     const int n_pos = count_dev ? static_cast<int>(*count_dev) : count;
     const uint32_t stamp = *stamp_p;
-    int32_t p0 = 0, n = 0;
+    int32_t p0 = 0, p1 = 0, n = 0;
     int g = 0;
+    bool is_long = false;
     if (j < n_pos) {
-        const int32_t p1 = static_cast<int32_t>(cum[j]);
+        p1 = static_cast<int32_t>(cum[j]);
         p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
         g = order ? order[j] : j;
         if (p1 > p0 && touched[g] != 0) {  // an untouched range has no stamped entry
-            if (p1 - p0 > kLongRange)
-                long_list[atomicAdd(long_count, 1)] = j;
-            else
+            if (p1 - p0 > kLongRange) {
+                const int32_t q = atomicAdd(long_count, 1);
+                if (inline_long)
+                    is_long = true;
+                else
+                    long_list[q] = j;
+            } else {
                 n = p1 - p0;
+            }
         }
     }
     // exclusive scan of the staged lengths over the wave
@@ -886,7 +923,7 @@ __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const i
     }
     const int off = incl - n;
     const int total = __shfl(incl, kGatherWave - 1, kGatherWave);
-    if (total == 0) return;  // uniform
+    if (total > 0) {  // uniform
     s_off[lane] = off;
     s_src[lane] = p0;
     __syncthreads();
@@ -916,6 +953,16 @@ __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const i
         __syncthreads();  // the next round restages
     }
     if (n > 0) store_grad_record(grads, static_cast<size_t>(g), v);
+    }
+    // inline: the wave's long ranges, as k_gather_long reduces them
+    for (unsigned long long lm = __ballot(is_long); lm; lm &= lm - 1) {  // uniform
+        const int L = static_cast<int>(__builtin_ctzll(lm));
+        const int32_t q0 = __shfl(p0, L, kGatherWave), q1 = __shfl(p1, L, kGatherWave);
+        const int gl = __shfl(g, L, kGatherWave);  // (every lane takes part in the shuffles)
+        float acc[kPartFloats];
+        reduce_long_range(part, q0, q1, stamp, acc);
+        if (lane == 0) store_grad_record(grads, static_cast<size_t>(gl), acc);
+    }
 }
 
 // The queued long ranges, one wave each, 64 entries per round (lane l takes entry base + l when it
@@ -937,24 +984,7 @@ __global__ void __launch_bounds__(kThreads) k_gather_long(const int32_t* __restr
         const int32_t p1 = static_cast<int32_t>(cum[j]);
         const int32_t p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
         float v[kPartFloats];
-#pragma unroll
-        for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
-        for (int32_t base = p0; base < p1; base += 64) {
-            const int32_t p = base + lane;
-            float x[kPartFloats];
-            const bool on = load_entry(part, min(p, p1 - 1), stamp, x) & (p < p1);
-#pragma unroll
-            for (int k = 0; k < kPartFloats; k++) {
-                float y = on ? x[k] : 0.f;
-                y += dpp_f<0xB1>(y);   // quad_perm(1,0,3,2)
-                y += dpp_f<0x4E>(y);   // quad_perm(2,3,0,1)
-                y += dpp_f<0x141>(y);  // row_half_mirror
-                y += dpp_f<0x140>(y);  // row_mirror: the 16-lane row total
-                y += __shfl_xor(y, 16, 64);
-                y += __shfl_xor(y, 32, 64);
-                v[k] += y;
-            }
-        }
+        reduce_long_range(part, p0, p1, stamp, v);
         if (lane == 0) store_grad_record(grads, static_cast<size_t>(order ? order[j] : j), v);
     }
 }
@@ -967,12 +997,14 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part, const uint32_t* stamp,
                          const uint8_t* touched, float4* grads, int32_t* long_list, int32_t* long_count,
-                         hipStream_t s, const int64_t* count_dev) {
+                         hipStream_t s, const int64_t* count_dev, bool inline_long) {
     if (count <= 0) return;
     hipLaunchKernelGGL(k_gather_grads, dim3((count + kGatherWave - 1) / kGatherWave), dim3(kGatherWave), 0, s, count,
-                       order, cum, part, stamp, touched, grads, long_list, long_count, count_dev);
-    hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, stamp, grads, long_list,
-                       long_count);
+                       order, cum, part, stamp, touched, grads, long_list, long_count, count_dev,
+                       inline_long ? 1 : 0);
+    if (!inline_long)
+        hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, stamp, grads,
+                           long_list, long_count);
 }
 
 namespace {

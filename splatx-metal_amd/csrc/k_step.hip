@@ -585,6 +585,7 @@ __device__ void loss_final(const StepLoss& L, double* s_red) {
             store_host(&L.rb.host[0], __float_as_uint(loss));
             store_host(&L.rb.host[1], *L.rb.sort_err);
             store_host(&L.rb.host[2], *L.rb.max_tile);
+            store_host(&L.rb.host[3], L.rb.long_count ? static_cast<uint32_t>(*L.rb.long_count) : 0u);
             __hip_atomic_store(L.rb.seq_host, L.rb.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
@@ -787,6 +788,7 @@ __global__ void k_step_readback(StepReadback rb) {
     store_host(&rb.host[0], 0u);
     store_host(&rb.host[1], *rb.sort_err);
     store_host(&rb.host[2], *rb.max_tile);
+    store_host(&rb.host[3], 0u);
     __hip_atomic_store(rb.seq_host, rb.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 

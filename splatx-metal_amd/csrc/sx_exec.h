@@ -92,6 +92,7 @@ struct sxh_executor {
     bool use_graph = true;
     int isect_order = SXH_ISECT_ORDER_AUTO;
     int64_t last_max_tile = -1;      // the largest tile's entry count in the previous step (-1: none yet)
+    int64_t last_long = -1;          // the previous training step's gather ranges past kLongRange (-1: none yet)
     sxh::DevBuf<uint32_t> max_tile;  // written by the step's tile order
     // profiling: per-kernel events (bit 0), raster pair counts (bit 1)
     bool prof = false;

@@ -195,11 +195,14 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 // entries at [cum[j-1], cum[j]) that carry the current stamp (order and cum: the depth order and the
 // inclusive scan of its tile counts that placed the emit), in a fixed order per range: the
 // deterministic end of raster_bwd's `part` mode. Untouched Gaussians' records are not written. long_list
-// holds `count` ints, long_count one (reset by raster_bwd_begin or the step's preprocess). With count_dev the positions are the
-// first *count_dev (<= count, which sizes the grid).
+// holds `count` ints, long_count one (reset by raster_bwd_begin or the step's preprocess; it ends as the
+// number of ranges longer than kLongRange). With count_dev the positions are the first *count_dev (<=
+// count, which sizes the grid). inline_long: the gather's waves reduce their long ranges themselves
+// instead of queueing them for a second launch (same sums; fast while they are few).
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part,
                          const uint32_t* stamp, const uint8_t* touched, float4* grads, int32_t* long_list,
-                         int32_t* long_count, hipStream_t s, const int64_t* count_dev = nullptr);
+                         int32_t* long_count, hipStream_t s, const int64_t* count_dev = nullptr,
+                         bool inline_long = false);
 void raster_bwd(const RasterArgs& a, const float* render_alphas, const int32_t* last_ids,
                 const float* v_render_colors, const float* v_render_alphas, const RasterBwdGrads& g,
                 hipStream_t s);

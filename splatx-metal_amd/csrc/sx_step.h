@@ -89,13 +89,14 @@ void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* of
                        const int64_t* n_dev = nullptr);
 void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev = nullptr);
-// The words a step reports to the host, stored straight into mapped host memory (host: 3 u32, the loss
-// bits, the sort's error flag, the largest tile's entry count) instead of one copy each, then `seq`
-// into *seq_host (release order: a host that reads seq there reads the words). Null host: nothing is
-// stored.
+// The words a step reports to the host, stored straight into mapped host memory (host: 4 u32, the loss
+// bits, the sort's error flag, the largest tile's entry count, the gather's long-range count (0 when
+// long_count is null)) instead of one copy each, then `seq` into *seq_host (release order: a host that
+// reads seq there reads the words). Null host: nothing is stored.
 struct StepReadback {
     const uint32_t* sort_err = nullptr;
     const uint32_t* max_tile = nullptr;
+    const int32_t* long_count = nullptr;
     uint32_t* host = nullptr;
     unsigned long long* seq_host = nullptr;
     unsigned long long seq = 0;

@@ -141,3 +141,41 @@ def test_steps_returning_at_the_loss_match_fully_synced_steps(gpu):
             assert np.array_equal(np.asarray(x).view(np.uint32), np.asarray(y).view(np.uint32)), grp
     early.close()
     synced.close()
+
+
+def test_gather_long_ranges_inline_match_queued(gpu, oracle):
+    """The gather reduces a Gaussian's entries past 64 tiles either queued (a wave each, in a second
+    launch) or inline (the gather's own waves, after its short ranges), chosen from the previous
+    step's count of such ranges: the first step of an executor queues them, the next one (with few)
+    reduces them inline. Both must give the same sums: with b1 = 0 the first moment after a step is
+    exactly its gradient, and with frozen parameters (learning rates 0) and the same pose the two
+    steps' gradients must agree bit for bit. Large splats in a 512x384 image give ranges past 64."""
+    sc = scene.make_scene(n=3000, sh_degree=1, width=512, height=384, fx=400.0, seed=21,
+                          log_scale_mu=math.log(0.12))
+    p = sc.params
+    proj = oracle.projection_fused_fwd(
+        means=p[0].reshape(-1, 3), quats=p[1].reshape(-1, 4), scales=np.exp(p[2].reshape(-1, 3)),
+        opacities=(1.0 / (1.0 + np.exp(-p[3].reshape(-1)))).astype(np.float32),
+        viewmats=sc.viewmat[None].astype(np.float32), Ks=sc.K[None].astype(np.float32), width=sc.width,
+        height=sc.height)
+    it = oracle.isect_tiles(means2d=proj["means2d"], radii=proj["radii"], depths=proj["depths"], I=1, N=sc.n,
+                            tile_width=(sc.width + 15) // 16, tile_height=(sc.height + 15) // 16)
+    n_long = int((np.asarray(it["tiles_per_gauss"]) > 64).sum())
+    assert 0 < n_long <= 1024, n_long  # some long ranges, few enough for the inline path
+    ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=0.2, b1=0.0,
+                                      isect_mode=sh.SXH_ISECT_AABB)
+    ex.upload_params(*scene.copy_state(sc), sc.n)
+    kw = dict(scene.step_kwargs(sc), lr=[0.0] * 6)
+    grads = []
+    for k in range(2):
+        print(f"long-range gather step {k}", flush=True)
+        ex.step(gt_rgb=sc.gt, **kw)
+        pp, mm, vv = scene.copy_state(sc)
+        ex.download_params(pp, mm, vv, sc.n)
+        grads.append([np.asarray(x).copy() for x in mm])
+        assert all(np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+                   for a, b in zip(pp, sc.params))  # frozen
+    for a, b in zip(*grads):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert any(np.abs(a).max() > 0 for a in grads[0])
+    ex.close()
