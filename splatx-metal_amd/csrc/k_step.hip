@@ -165,7 +165,7 @@ __device__ __forceinline__ void store_host(T* p, T v) {
 // must not run: overflow = 1 and out[2] = out[3] = 0, the counts they read, so that every one of them
 // finds nothing to do (out[1] keeps the true total for the host).
 constexpr int kScanBlock = 1024;
-constexpr int kScanPer = 8;  // consecutive blocks per thread and chunk
+constexpr int kScanPer = 4;  // consecutive blocks per thread and chunk
 __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restrict__ part, int n,
                                                            unsigned long long* __restrict__ out,
                                                            unsigned long long* __restrict__ base,
