@@ -4,9 +4,9 @@
 // Contract: KernelBackend.h:130-148 / sort_isect (ascending unsigned key, stable, only bits
 // [0, key_bits) significant). Design: digits of at most 8 bits, the key bits spread evenly over the
 // fewest passes, so a 45-bit isect key needs 6 passes (the reference's 4-bit digits need 12) and a
-// 13-bit tile id two passes of 7 and 6 bits. Below 2^30 keys and 256 tiles of 4096 keys the passes
-// run onesweep (see k_os_pass): the digit histograms of all passes come from one read of the keys,
-// and each pass is one launch whose tiles chain their digit prefixes by look-back. From 256 tiles on
+// 13-bit tile id two passes of 7 and 6 bits. Below 16 tiles of 4096 keys the passes run onesweep (see
+// k_os_pass): the digit histograms of all passes come from one read of the keys, and each pass is one
+// launch whose tiles chain their digit prefixes by look-back. From 16 tiles (and below 2^30 keys) on
 // each pass counts its tiles' digits, scans the count matrix and scatters with the same pass kernel,
 // without the chain (see k_rs_count). The fallback at 2^30 keys and above is three launches per pass
 // with no inter-workgroup waiting:
@@ -791,10 +791,11 @@ void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, 
 }
 
 constexpr int kMaxPasses = 8;
-// From this many 4096-key tiles on (1 M keys) a pass takes its prefixes from a scan of the tiles'
+// From this many 4096-key tiles on (64 Ki keys) a pass takes its prefixes from a scan of the tiles'
 // digit counts instead of the look-back chain: the counting read costs less than the chain's waits
-// (measured at 489 to 40,557 tiles; equal at 245).
-constexpr int kRtsMinTiles = 256;
+// (measured at 143 to 40,557 tiles: config 2's 0.58 M-key tile sort 44.7 -> 39.4 us; the two-launch
+// count scan made the difference at the small sizes).
+constexpr int kRtsMinTiles = 16;
 // scratch layout: a fixed header (digit totals and bases of up to 8 passes, the per-pass tile
 // counters, the error word) and then two tiles x 256 word buffers (the three-launch path's
 // histogram, or the onesweep status words of alternate passes)
