@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -80,6 +81,8 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->loss_dev.alloc(1);
             e->staging.alloc(R * 45);
             e->ensure_isect(1 << 16);
+            const char* dbg = std::getenv("SXH_DEBUG_FORCE_SORT_ERROR");
+            e->debug_sort_error = dbg && dbg[0] == '1';
             for (int k = 0; k < kMaxEvents; k++) SXH_HIP(hipEventCreate(&e->ev[k]));
             SXH_HIP(hipStreamSynchronize(b->stream));
         } catch (...) {
@@ -375,6 +378,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         }
         if (which < 0) throw std::runtime_error(std::string(what) + ": intersection capacity too large for a device count");
+        if (e->debug_sort_error) sxk::step_set_word(sxk::sort_error_flag(e->sort_scratch.p), 1u, s);
         flat = which ? e->vals_b.p : e->vals_a.p;
         e->mark("offsets");
         sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev, e->max_tile.p);
@@ -403,6 +407,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         // the block masks go where the tile ids were: both key buffers are free once the offsets (and,
         // index first, the per-tile depth sort) are done
         ra.block_masks = fwd_only ? nullptr : reinterpret_cast<uint16_t*>(e->keys_a.p);
+        ra.mask_end = e->mask_end.p;
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
         e->mark("raster_fwd");
         // the loss words, then the launch's sequence number (word 5 of the block)

@@ -202,8 +202,12 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     float r0 = 0.f, r1 = 0.f, r2 = 0.f;
     bool done = !inside;
     unsigned long long st_iters = 0, st_entries = 0, st_taken = 0;  // STATS only (wave-uniform)
+    int32_t loaded_end = range_end;  // the end of the entries loaded (and their block masks stored)
     for (int32_t bstart = range_start; bstart < range_end; bstart += kThreads) {
-        if (__syncthreads_count(done) == kThreads) break;  // also the barrier before LDS reuse
+        if (__syncthreads_count(done) == kThreads) {  // also the barrier before LDS reuse
+            loaded_end = bstart;
+            break;
+        }
         const int32_t idx = bstart + tid;
         uint32_t bm = 0u;
         bool big = false;
@@ -284,6 +288,9 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             for (int k = 0; k < 4; k++) composite(in[k], sg[k], xyo[k].z * vis[k], tc[k], bstart + t[k]);
         }
     }
+    // every pixel's last contributor lies in a loaded batch, before loaded_end: the backward's walk
+    // stays inside the stored masks
+    if (a.block_masks && tid == 0) a.mask_end[(size_t)img * n_tiles + tile] = loaded_end;
     if (STATS && lane == 0) {
         atomicAdd(&a.stats[kStatFwdIters], st_iters);
         atomicAdd(&a.stats[kStatFwdEntries], st_entries);
@@ -476,6 +483,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     for (int k = 1; k < kBlocks; k++) tile_bf = max(tile_bf, s_bbf[k]);
     const int32_t tile_end = min(range_end, tile_bf + 1);
     const int32_t num = max(0, tile_end - range_start);
+    // the forward stored the masks of [range_start, mask_end), which holds [range_start, tile_end): the
+    // forward loads whole batches until every pixel is done, and tile_end - 1 is some pixel's last
+    // contributor. An entry past mask_end would take the computed mask.
+    const int32_t mask_end = a.block_masks ? a.mask_end[(size_t)img * n_tiles + tile] : range_start;
     const int num_batches = (num + kThreads - 1) / kThreads;
     // a group's reduction leaves slot A in lane 0, B in 8, C in 4, D in 12: those lanes store them
     const int wslot = (r == 0) ? 0 : (r == 8) ? 1 : (r == 4) ? 2 : (r == 12) ? 3 : -1;
@@ -502,8 +513,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
             s_rgb[tid] = rgb;
             // blocks the cutoff set can reach (the forward's, when it kept them), less those whose every
             // pixel stopped before it
-            bm = a.block_masks ? static_cast<uint32_t>(a.block_masks[idx])
-                               : block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
+            bm = idx < mask_end ? static_cast<uint32_t>(a.block_masks[idx])
+                                : block_mask(xyo, con, static_cast<float>(tx * 16), static_cast<float>(ty * 16));
 #pragma unroll
             for (int k = 0; k < kBlocks; k++)
                 if (idx > s_bbf[k]) bm &= ~(1u << k);

@@ -601,7 +601,10 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
     __shared__ double s_red[kBlock];
     // the first workgroup also reduces the loss (every thread of it, before any leaves)
     if (L.out && blockIdx.x == 0) loss_final(L, s_red);
-    if (skip && *skip) return;  // the step overflowed its buffers and runs again: leave the arena as it was
+    // the step overflowed its buffers and runs again, or the tile sort gave up (its lists, and every
+    // gradient rasterised from them, are wrong; the host reports the error): leave the arena as it was
+    if (skip && *skip) return;
+    if (L.rb.sort_err && *L.rb.sort_err) return;
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= c.count) return;
     const size_t R = static_cast<size_t>(A.rows);
@@ -784,6 +787,8 @@ __global__ void __launch_bounds__(kBlock) k_l1(const float* __restrict__ render,
 }
 
 
+__global__ void k_set_word(uint32_t* word, uint32_t value) { *word = value; }
+
 __global__ void k_step_readback(StepReadback rb) {
     store_host(&rb.host[0], 0u);
     store_host(&rb.host[1], *rb.sort_err);
@@ -905,6 +910,10 @@ void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_rend
                   hipStream_t s) {
     const float g = 1.0f / static_cast<float>(n);
     hipLaunchKernelGGL(k_l1, dim3(n_blocks), dim3(kBlock), 0, s, render, gt, n, g, v_render, partials);
+}
+
+void step_set_word(uint32_t* word, uint32_t value, hipStream_t s) {
+    hipLaunchKernelGGL(k_set_word, dim3(1), dim3(1), 0, s, word, value);
 }
 
 void step_readback(const StepReadback& rb, hipStream_t s) {

@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstddef>
+#include <cstring>
 
 #include "splatx_hip.h"
 #include "sx_host.h"
@@ -15,11 +16,15 @@
 
 namespace sxh_detail {
 
+// Pinned host memory, zeroed at allocation: the runtime may hand back a block a destroyed executor
+// used, and the step's read-back words are tagged with sequence numbers that every executor starts
+// from 1 again, so a stale tag would end a wait before the new step stored its words.
 struct PinnedHost {
     void* p = nullptr;
     void* dev = nullptr;  // the device's address of the block (mapped memory)
     explicit PinnedHost(size_t bytes, unsigned flags = hipHostMallocDefault) {
         SXH_HIP(hipHostMalloc(&p, bytes, flags));
+        std::memset(p, 0, bytes);
         if (flags & hipHostMallocMapped) SXH_HIP(hipHostGetDevicePointer(&dev, p, 0));
     }
     ~PinnedHost() {
@@ -67,7 +72,7 @@ struct sxh_executor {
     sxh::DevBuf<uint8_t> sort_scratch;
     // image-sized buffers
     size_t img_px = 0, img_tiles = 0, img_map = 0;
-    sxh::DevBuf<int32_t> offsets, last_ids, tile_order;
+    sxh::DevBuf<int32_t> offsets, last_ids, tile_order, mask_end;
     sxh::DevBuf<float> render, alpha, v_render, v_alpha_zero, gt_stage;
     sxh::DevBuf<float> cmu, csg, ccr;  // SSIM coefficient maps (the map itself is only summed)
     sxh::DevBuf<double> ssim_part, l1_part;
@@ -90,6 +95,9 @@ struct sxh_executor {
     // segment B of the step as executable graphs: [index-first][0 training step, 1 forward only]
     hipGraphExec_t graph_b[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
     bool use_graph = true;
+    // test switch (environment SXH_DEBUG_FORCE_SORT_ERROR=1 at creation): after the tile sort, a kernel
+    // sets the sort's error word, as a sort that gave up would; every kernel still runs to its end
+    bool debug_sort_error = false;
     int isect_order = SXH_ISECT_ORDER_AUTO;
     int64_t last_max_tile = -1;      // the largest tile's entry count in the previous step (-1: none yet)
     int64_t last_long = -1;          // the previous training step's gather ranges past kLongRange (-1: none yet)
@@ -160,6 +168,7 @@ struct sxh_executor {
         if (tiles_n > img_tiles) {
             offsets.alloc(tiles_n);
             tile_order.alloc(tiles_n);
+            mask_end.alloc(tiles_n);
             img_tiles = tiles_n;
         }
         if (use_ssim) {

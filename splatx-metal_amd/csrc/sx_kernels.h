@@ -142,9 +142,13 @@ struct RasterArgs {
     unsigned long long* stats;
     // optional: one u16 per intersection, the 4x4 blocks its splat's cutoff set reaches in its tile;
     // the forward stores the mask of every entry it loads, the backward reads it instead of working it
-    // out again (the forward loads every entry up to each tile's last contributor, which is as far as
-    // the backward goes). Null: both compute it.
+    // out again. Null: both compute it. With block_masks, mask_end (one i32 per tile, required) gets
+    // the end of the entries whose masks the forward stored: it stops loading at a batch boundary once
+    // every pixel of the tile is done, so it stores masks for [range_start, mask_end). The backward
+    // walks from the tile's last contributor down, which lies before mask_end, so it always finds a
+    // stored mask; it works out the mask itself for any entry at or past mask_end all the same.
     uint16_t* block_masks;
+    int32_t* mask_end;
 };
 // raster pair counters (RasterArgs::stats): forward wave iterations (x 64 lane pairs), block-list
 // entries walked (one splat against a 4x4 block) and pairs composited; backward 4-iteration chunks

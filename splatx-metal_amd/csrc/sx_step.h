@@ -130,6 +130,8 @@ void step_ssim_bwd_l1(const float* render, const float* gt, const float* cmu, co
                       const float* ccr, int H, int W, float G, float w_l1, float g_l1, float* v_render,
                       double* l1_partials, hipStream_t s);
 int step_ssim_bwd_blocks(int H, int W);
+// *word = value, by a one-thread kernel (a graph-capturable store; no memset node)
+void step_set_word(uint32_t* word, uint32_t value, hipStream_t s);
 // rb's words to the host without a loss (the loss word is 0): the forward-only step
 void step_readback(const StepReadback& rb, hipStream_t s);
 void aos_to_soa(const float* aos, float* soa, int rows, int dim, int stride, hipStream_t s);
