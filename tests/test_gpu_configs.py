@@ -8,10 +8,16 @@ Every step starts the GPU and the oracle from the same state (the GPU's paramete
 the previous step), and the reference's resident-vs-host gates (TrainerTests.cpp:1720-1746) apply to
 each step: n_isects exact, the render bit-exact (the forward is bit-identical; the reference asks
 rel_l2 <= 1e-5 of the first one), |dloss| <= 1e-6 + 1e-4 |loss|, and parameters and both Adam moments
-after the step within rel_l2 1e-4 (float atomics in the raster backward make the gradient sums order
-dependent). Chaining independent runs instead would compare the amplification of that order: Adam's
-first update is +-lr for any nonzero gradient, so a near-zero gradient whose sign the summation order
-decides moves its parameter by 2 lr, and the next step's gradients follow the moved parameters."""
+after the step within rel_l2 1e-4 (the backward sums each gradient in another order than the oracle,
+whose accumulators are f64, and uses the hardware exponential where it cannot change a decision).
+Chaining independent runs instead would compare the amplification of that difference: Adam's first
+update is +-lr for any nonzero gradient, so a near-zero gradient whose sign the summation order decides
+moves its parameter by 2 lr, and the next step's gradients follow the moved parameters.
+
+The headline config runs under both intersection orders (the executor's automatic choice takes depth
+first on its first step and index first from the second on at this size, so each is pinned
+explicitly), and once more without a render read-back: that step returns at the loss word while the
+parameter update still runs, and its downloaded state must equal the fully synced step's bit for bit."""
 import numpy as np
 import pytest
 
@@ -50,7 +56,7 @@ def scene_target(gpu, orc, cfg_id, viewmat):
     return img
 
 
-def run_config(gpu, cfg_id, steps, viewmat=None, lr=None):
+def run_config(gpu, cfg_id, steps, viewmat=None, lr=None, order=sh.SXH_ISECT_ORDER_AUTO):
     sc, cfg = scene.config_scene(cfg_id, seed=0)
     orc = oracle_py.Oracle(libm=False)
     vm = sc.viewmat if viewmat is None else viewmat
@@ -62,6 +68,7 @@ def run_config(gpu, cfg_id, steps, viewmat=None, lr=None):
     lr = list(sc.lr) if lr is None else lr
     ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
                                       antialiased=bool(cfg.get("antialiased", False)), isect_mode=isect_mode(cfg))
+    ex.set_isect_order(order)
     state = scene.copy_state(sc)
     ex.upload_params(*state, sc.n)
     kw = dict(scene.step_kwargs(sc), viewmat=vm, lr=lr)
@@ -79,7 +86,7 @@ def run_config(gpu, cfg_id, steps, viewmat=None, lr=None):
         out.append((rg, ro, state, (gp, gm, gv), (op, om, ov)))
         state = (gp, gm, gv)
     ex.close()
-    return sc, out
+    return sc, out, gt
 
 
 def check_contrast(sc, out, expect_isects):
@@ -105,21 +112,40 @@ def check_contrast(sc, out, expect_isects):
 
 def test_config1_step_matches_oracle(gpu):
     """Config 1: N = 10k, SH0, 256x256, fx = fy = 230, AABB, L1 against a seeded U[0,1] target, Adam lr 1e-3."""
-    sc, out = run_config(gpu, 1, steps=2, lr=[1e-3] * 6)
+    sc, out, _ = run_config(gpu, 1, steps=2, lr=[1e-3] * 6)
     check_contrast(sc, out, (5_000, 200_000))
 
 
 def test_config2_step_matches_oracle(gpu):
     """Config 2: N = 100k, SH3, 800x800, fx = fy = 720, AABB, 0.8 L1 + 0.2 (1 - SSIM) against the second
     seeded scene's render."""
-    sc, out = run_config(gpu, 2, steps=2)
+    sc, out, _ = run_config(gpu, 2, steps=2)
     check_contrast(sc, out, (100_000, 5_000_000))
 
 
-def test_config3_full_step_matches_oracle(gpu):
+@pytest.mark.parametrize("order", [sh.SXH_ISECT_ORDER_DEPTH_FIRST, sh.SXH_ISECT_ORDER_INDEX_FIRST],
+                         ids=["depth_first", "index_first"])
+def test_config3_full_step_matches_oracle(gpu, order):
     """Config 3 (the headline): one full fwd + bwd + Adam step at N = 1M, SH3, 1297x840, AccuTile, SSIM,
-    from the first jittered pose of the benchmark's pose sequence, against the oracle's step."""
+    from the first jittered pose of the benchmark's pose sequence, against the oracle's step; then the
+    same step from the same state without a render read-back (the step returns at its loss word) gives
+    the same parameters and moments bit for bit."""
     rng = np.random.Generator(np.random.PCG64(1234))
     pose = scene.jittered_view(rng)
-    sc, out = run_config(gpu, 3, steps=1, viewmat=pose)
+    sc, out, gt = run_config(gpu, 3, steps=1, viewmat=pose, order=order)
     check_contrast(sc, out, (1_000_000, 4_000_000))
+    rg, _, start, synced, _ = out[0]
+    _, cfg = scene.config_scene(3, seed=0)
+    ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
+                                      isect_mode=isect_mode(cfg))
+    ex.set_isect_order(order)
+    ex.upload_params(*start, sc.n)
+    r = ex.step(want_render=False, gt_rgb=gt, **dict(scene.step_kwargs(sc), viewmat=pose))
+    assert r["n_isects"] == rg["n_isects"]
+    assert np.float32(r["loss"]).view(np.uint32) == np.float32(rg["loss"]).view(np.uint32)
+    gp, gm, gv = ([np.zeros_like(x) for x in grp] for grp in start)
+    ex.download_params(gp, gm, gv, sc.n)
+    ex.close()
+    for grp in range(6):
+        for a, b in ((gp[grp], synced[0][grp]), (gm[grp], synced[1][grp]), (gv[grp], synced[2][grp])):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), grp

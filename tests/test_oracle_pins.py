@@ -261,6 +261,32 @@ def test_scan_sort_offsets_brute_force(oracle):
     np.testing.assert_array_equal(oracle.isect_offset_encode(keys[:0], I, tw, th, n_isects=0), np.zeros(I * nt))
 
 
+def test_sort_counting_passes_brute_force(oracle):
+    """The oracle's sort (LSD counting passes over the significant bits) against numpy's stable argsort
+    where the passes matter most: few key bits with heavy ties, keys whose low or middle bytes are all
+    equal (passes skipped), a key width that is not a multiple of 8, one key, and keys in descending
+    order. A pass that dropped stability, used the wrong digit or skipped a needed byte would reorder
+    equal keys or leave keys unsorted."""
+    r = inputs.rng(21)
+    cases = {
+        "13 bits, heavy ties": r.integers(0, 1 << 13, 40_000).astype(np.uint64),
+        "1 bit": r.integers(0, 2, 5_000).astype(np.uint64),
+        "45 bits, low 32 bits equal": (r.integers(0, 1 << 13, 30_000).astype(np.uint64) << np.uint64(32)) | np.uint64(7),
+        "40 bits, middle bytes equal": (r.integers(0, 256, 20_000).astype(np.uint64) << np.uint64(32))
+        | np.uint64(0x00ABCD00) | r.integers(0, 256, 20_000).astype(np.uint64),
+        "one key": np.array([5], np.uint64),
+        "descending 17 bits": np.arange(70_000, 0, -1).astype(np.uint64),
+    }
+    widths = {"13 bits, heavy ties": 13, "1 bit": 1, "45 bits, low 32 bits equal": 45,
+              "40 bits, middle bytes equal": 40, "one key": 3, "descending 17 bits": 17}
+    for name, keys in cases.items():
+        vals = r.integers(-2**31, 2**31 - 1, keys.size).astype(np.int32)
+        ks, vs = oracle.sort_isect(keys, vals, widths[name])
+        ek, ev = inputs.stable_sort_ref(keys, vals)
+        np.testing.assert_array_equal(ks, ek, err_msg=name)
+        np.testing.assert_array_equal(vs, ev, err_msg=name)
+
+
 # ---------------------------------------------------------------- projection bwd, covars path ----
 def covars_fd_case(oracle, aa):
     """Projection backward on the covariance path (6-triu input), with the directional-free reference:
