@@ -94,6 +94,24 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
     return 0.0
 
 
+# The oracle's backward stages are this build's own code: the reference's CPU path has no backward
+# (its raster, SH, projection and SSIM VJPs exist only as GPU kernels), so these are reported apart from
+# the stages the reference's CPU kernels also run.
+OWN_BACKWARD_STAGES = ("raster_bwd", "sh_bwd", "projection_bwd", "ssim_bwd")
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (first `model name` of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(sc, pose, gt, lr) -> dict:
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle_py
@@ -112,7 +130,10 @@ def cpu_baseline(sc, pose, gt, lr) -> dict:
     return {"value": round(dt, 1), "unit": "ms/iter", "cores": 1, "kind": "port",
             "sample": f"{n_steps} consecutive full fwd+bwd+Adam steps of the same config-3 workload (N=1M, SH3, "
                       "1297x840, AccuTile, SSIM; first timed pose and its target) by the single-threaded CPU oracle",
-            "n_isects": r["n_isects"], "stages_ms": {k: round(x, 1) for k, x in stages.items() if x > 0}}
+            "n_isects": r["n_isects"], "cpu_model": cpu_model(),
+            "stages_ms": {k: round(x, 1) for k, x in stages.items() if x > 0 and k not in OWN_BACKWARD_STAGES},
+            "own_backward_stages_ms": {k: round(stages[k], 1) for k in OWN_BACKWARD_STAGES if stages.get(k, 0) > 0},
+            "own_backward_note": "the reference has no CPU backward; these stages are this build's own CPU code"}
 
 
 def calibrate_copy(mib: int, reps: int = 4) -> None:
@@ -227,20 +248,24 @@ def load_valu(kernel: str, cfg: int):
 
 
 def calibrate_valu(blocks: int = 8192, reps: int = 5) -> None:
-    """VALU issue rates per instruction class on device 0 (the yardstick kernels of k_yardstick.hip):
-    wave-level instructions per SIMD per 4 cycles at CLOCK_HZ, and the cycles per instruction."""
+    """VALU issue rates per instruction class on device 0 (the yardstick kernels of
+    splatx-metal_amd/yardstick/k_yardstick.hip, a library of their own): wave-level instructions per SIMD
+    per 4 cycles at CLOCK_HZ, and the cycles per instruction."""
     import ctypes
-    lib = sh.load_library()
-    lib.sxh_yardstick_valu_name.restype = ctypes.c_char_p
-    lib.sxh_yardstick_valu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                       ctypes.POINTER(ctypes.c_double)]
+    path = os.path.join(REPO, "splatx-metal_amd", "build", "libsplatx_yardstick.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"yardstick library not built: {path} (run __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    lib.sxy_valu_name.restype = ctypes.c_char_p
+    lib.sxy_valu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                             ctypes.POINTER(ctypes.c_double)]
     out = {"blocks": blocks, "waves": blocks * 4, "clock_hz": CLOCK_HZ, "simds": SIMDS, "ops": {}}
-    for op in range(lib.sxh_yardstick_valu_count()):
-        name = lib.sxh_yardstick_valu_name(op).decode()
+    for op in range(lib.sxy_valu_count()):
+        name = lib.sxy_valu_name(op).decode()
         slow = "exp" in name or "rcp" in name
         iters = 1024 if slow else 4096
         ms = ctypes.c_double()
-        if lib.sxh_yardstick_valu(0, op, blocks, iters, reps, ctypes.byref(ms)) != 0:
+        if lib.sxy_valu(0, op, blocks, iters, reps, ctypes.byref(ms)) != 0:
             raise RuntimeError(f"yardstick {name} failed")
         insts = blocks * 4 * iters * 8
         rate = insts / SIMDS / (ms.value * 1e-3 * CLOCK_HZ / 4.0)

@@ -1,13 +1,12 @@
 // k_yardstick.hip — VALU issue-rate yardstick: kernels of one instruction class each, with a known
 // number of wave-level instructions, timed with HIP events. It calibrates the cycles-per-instruction
 // model that turns the SQ_INSTS_VALU counters of the step's kernels into a VALU issue bound (how
-// long the SIMDs need for a kernel's instructions when they issue nothing else). Not part of the
-// step: only bench.py's --calibrate-valu mode calls it.
+// long the SIMDs need for a kernel's instructions when they issue nothing else). Built into its own
+// library (build/libsplatx_yardstick.so), not into the product library: only bench.py's
+// --calibrate-valu mode loads it.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
-
-#include "sx_host.h"
 
 namespace {
 
@@ -68,21 +67,21 @@ const char* const kYardName[kYardOps] = {"v_fma_f32", "v_mul_f32", "v_add_f32", 
 extern "C" {
 
 // Number of yardstick kernels and the name of kernel `op` (null when out of range).
-int sxh_yardstick_valu_count(void) { return kYardOps; }
-const char* sxh_yardstick_valu_name(int op) { return op >= 0 && op < kYardOps ? kYardName[op] : nullptr; }
+int sxy_valu_count(void) { return kYardOps; }
+const char* sxy_valu_name(int op) { return op >= 0 && op < kYardOps ? kYardName[op] : nullptr; }
 
 // Runs yardstick kernel `op` on device `device` over `blocks` workgroups of 4 waves, `iters` loop trips
 // of 8 instructions of the class per wave (the loop adds 3 scalar instructions per trip): one
 // untimed launch, then `reps` timed ones; *best_ms receives the fastest. Returns 0, or -1 on a bad
 // argument or HIP error (message on stderr).
-int sxh_yardstick_valu(int device, int op, int blocks, int iters, int reps, double* best_ms) {
+int sxy_valu(int device, int op, int blocks, int iters, int reps, double* best_ms) {
     if (op < 0 || op >= kYardOps || blocks <= 0 || iters <= 0 || reps <= 0 || !best_ms) return -1;
     float* out = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     int rc = -1;
     float best = 1e30f;
     auto ok = [](hipError_t e) {
-        if (e != hipSuccess) std::fprintf(stderr, "sxh_yardstick_valu: %s\n", hipGetErrorString(e));
+        if (e != hipSuccess) std::fprintf(stderr, "sxy_valu: %s\n", hipGetErrorString(e));
         return e == hipSuccess;
     };
     if (!ok(hipSetDevice(device)) || !ok(hipMalloc(&out, sizeof(float) * 256 * static_cast<size_t>(blocks))))

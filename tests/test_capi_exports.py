@@ -2,6 +2,8 @@
 import ctypes
 import os
 import re
+import shutil
+import subprocess
 
 import pytest
 
@@ -30,6 +32,17 @@ def test_library_exports_every_declared_symbol():
     assert len(names) >= 30
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
+
+
+def test_library_exports_nothing_else():
+    """The dynamic symbol table holds the header's entry points and nothing more: no C++ internals and no
+    undeclared extern "C" function (the library is linked with a version script)."""
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", LIB], check=True, capture_output=True, text=True).stdout
+    exported = sorted({ln.split()[-1] for ln in out.splitlines() if ln.strip()})
+    assert exported == declared(), (sorted(set(exported) - set(declared())), sorted(set(declared()) - set(exported)))
 
 
 def test_abi_version_without_gpu():
