@@ -184,8 +184,10 @@ int32_t sxh_sort_isect(sxh_backend* b, const sxh_sort_inputs* in, uint64_t* keys
  * DEVICE buffers of the backend's device (keys, values in; keys_sorted, values_sorted out; no
  * aliasing), that allocates nothing. Its working memory is a fixed per-device array of the
  * library (26 MiB, held until the process ends), so n is limited to 2,097,152 keys (larger n:
- * SXH_ERR_INVALID_ARGUMENT). It runs on the backend's stream and returns when the sort is done.
- * Calls that overlap on one device share that array and race. */
+ * SXH_ERR_INVALID_ARGUMENT; so are buffers whose allocation holds fewer than n elements and outputs
+ * that overlap an input or each other). It runs on the backend's stream and returns when the sort
+ * is done. Calls on one device share that array; a per-device lock inside the call serialises calls
+ * from several host threads. */
 int32_t sxh_sort_isect_noalloc(sxh_backend* b, const uint64_t* keys, const int32_t* values, int64_t n,
                                uint32_t key_n_bits, uint64_t* keys_sorted, int32_t* values_sorted);
 

@@ -6,10 +6,12 @@
 // file-scope `scratch` array below, sized for at most kNoAllocMaxKeys keys. Each device the library
 // runs on holds its own copy of the array until the process ends. The sort itself is the onesweep
 // radix sort of sort_isect (k_sort.hip); it clears the words that must start at zero at the start of
-// every call, so the array's left-over contents never matter. Calls that overlap on one device share
-// the array and race: the entry point is for one caller at a time per device.
+// every call, so the array's left-over contents never matter. Calls on one device share the array, so
+// a per-device mutex is held across each call: calls from several host threads are serialised, not
+// raced (work the caller queued on other streams that reads the outputs must wait for the return).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -30,6 +32,7 @@ __device__ __align__(256) unsigned char scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};  // the device address of `scratch`, per device
+std::mutex g_call_mu[kMaxDevices];  // held across a call: one call at a time uses a device's array
 
 }  // namespace
 
@@ -59,13 +62,30 @@ void* scratch_of(int device) {
     return (device >= 0 && device < kMaxDevices) ? g_ptr[device] : nullptr;
 }
 
-// Device memory of `device` (not host, not another device's): the kernels dereference it.
-void need_device(const void* p, int device, const char* name) {
+// Device memory of `device` (not host, not another device's) whose allocation holds `bytes` from p on:
+// the kernels read or write all of them.
+void need_device(const void* p, size_t bytes, int device, const char* name) {
     hipPointerAttribute_t attr{};
     const hipError_t e = hipPointerGetAttributes(&attr, p);
     (void)hipGetLastError();  // an unknown host pointer leaves an error behind; it is reported below
     if (e != hipSuccess || attr.type != hipMemoryTypeDevice || attr.device != device)
         sxh::invalid("sort_isect_noalloc", std::string(name) + " is not device memory of the backend's device");
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) != hipSuccess || !base) {
+        (void)hipGetLastError();
+        sxh::invalid("sort_isect_noalloc", std::string(name) + ": the allocation holding it is unknown");
+    }
+    const size_t off = static_cast<size_t>(static_cast<const char*>(p) - static_cast<const char*>(base));
+    if (off > size || size - off < bytes)
+        sxh::invalid("sort_isect_noalloc", std::string(name) + " holds fewer than n elements (" +
+                                               std::to_string(size - std::min(off, size)) + " bytes from it, " +
+                                               std::to_string(bytes) + " needed)");
+}
+
+bool overlap(const void* a, size_t na, const void* b, size_t nb) {
+    const auto x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + nb && y < x + na;
 }
 
 }  // namespace
@@ -84,13 +104,19 @@ extern "C" int32_t sxh_sort_isect_noalloc(sxh_backend* b, const uint64_t* keys, 
         if (!b) invalid(what, "null backend");
         if (n == 0) return;
         if (!keys_sorted || !values_sorted) invalid(what, "null keys_sorted/values_sorted");
-        if (static_cast<const void*>(keys_sorted) == keys || static_cast<const void*>(values_sorted) == values)
+        const size_t nk = sizeof(uint64_t) * static_cast<size_t>(n), nv = sizeof(int32_t) * static_cast<size_t>(n);
+        // the outputs are written while the inputs are read: no byte of an output may lie in another buffer
+        if (overlap(keys_sorted, nk, keys, nk) || overlap(keys_sorted, nk, values, nv) ||
+            overlap(values_sorted, nv, keys, nk) || overlap(values_sorted, nv, values, nv))
             invalid(what, "outputs must not alias the inputs");
+        if (overlap(keys_sorted, nk, values_sorted, nv)) invalid(what, "keys_sorted and values_sorted overlap");
         SXH_HIP(hipSetDevice(b->device));
-        need_device(keys, b->device, "keys");
-        need_device(values, b->device, "values");
-        need_device(keys_sorted, b->device, "keys_sorted");
-        need_device(values_sorted, b->device, "values_sorted");
+        need_device(keys, nk, b->device, "keys");
+        need_device(values, nv, b->device, "values");
+        need_device(keys_sorted, nk, b->device, "keys_sorted");
+        need_device(values_sorted, nv, b->device, "values_sorted");
+        if (b->device < 0 || b->device >= kMaxDevices) invalid(what, "device ordinal out of range");
+        std::lock_guard<std::mutex> call_lock(g_call_mu[b->device]);
         unsigned char* base = static_cast<unsigned char*>(scratch_of(b->device));
         if (!base) throw std::runtime_error("sort_isect_noalloc: scratch not initialised on this device");
         auto* keys_tmp = reinterpret_cast<uint64_t*>(base + kSortRegion);

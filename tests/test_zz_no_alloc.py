@@ -4,7 +4,8 @@ Two calls in a row on the same device share the library's scratch array: the fir
 capacity (2^21 keys, 45-bit keys: 6 passes, the result's last pass lands in the output after an even
 count), the second smaller (36-bit keys: 5 passes, odd), over what the first left in the array. Each
 result is compared bit for bit with the staged entry point's, whose sort is the same. Then the
-rejections: one key over the capacity, a host pointer, an output aliasing its input.
+rejections: one key over the capacity, a host pointer, an output aliasing its input (the same address
+or one element past it), outputs overlapping each other, buffers shorter than n elements.
 """
 import ctypes as C
 
@@ -23,13 +24,19 @@ class Hip:
 
     def __init__(self):
         self.lib = C.CDLL("libamdhip64.so.7")
-        for f in ("hipMalloc", "hipFree", "hipMemcpy", "hipDeviceSynchronize"):
+        for f in ("hipMalloc", "hipFree", "hipMemcpy", "hipDeviceSynchronize", "hipMemGetAddressRange"):
             getattr(self.lib, f).restype = C.c_int
 
     def alloc(self, nbytes):
         p = C.c_void_p()
         assert self.lib.hipMalloc(C.byref(p), C.c_size_t(max(nbytes, 16))) == 0
         return p
+
+    def size_from(self, p):
+        """Bytes of p's allocation from p on, as the runtime reports them."""
+        base, size = C.c_void_p(), C.c_size_t()
+        assert self.lib.hipMemGetAddressRange(C.byref(base), C.byref(size), p) == 0
+        return size.value - (p.value - base.value)
 
     def free(self, p):
         assert self.lib.hipFree(p) == 0
@@ -105,6 +112,22 @@ def test_noalloc_sort_rejections(gpu):
         assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"keys is not device memory" in gpu.lib.sxh_last_error()
         rc = f(gpu.handle, kd, vd, 64, 45, kd, vo)
         assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"must not alias" in gpu.lib.sxh_last_error()
+        # an output one element past its input (partly overlapping), and one over the other input
+        rc = f(gpu.handle, kd, vd, 32, 45, C.c_void_p(kd.value + 8), vo)
+        assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"must not alias" in gpu.lib.sxh_last_error()
+        rc = f(gpu.handle, kd, vd, 16, 45, ko, C.c_void_p(kd.value + 8))
+        assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"must not alias" in gpu.lib.sxh_last_error()
+        rc = f(gpu.handle, kd, vd, 16, 45, ko, C.c_void_p(ko.value + 64))
+        assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"overlap" in gpu.lib.sxh_last_error()
+        # one element more than the keys' allocation holds (as the runtime reports its size), and an
+        # output that starts 8 elements before the end of its allocation
+        n_over = hip.size_from(kd) // 8 + 1
+        assert n_over <= MAX_KEYS
+        rc = f(gpu.handle, kd, vd, n_over, 45, ko, vo)
+        assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"fewer than n elements" in gpu.lib.sxh_last_error()
+        tail = C.c_void_p(ko.value + hip.size_from(ko) - 64)
+        rc = f(gpu.handle, kd, vd, 16, 45, tail, vo)
+        assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"keys_sorted holds fewer than n" in gpu.lib.sxh_last_error()
         rc = f(gpu.handle, kd, vd, 64, 0, ko, vo)
         assert rc == sh.SXH_ERR_INVALID_ARGUMENT and b"key_n_bits must be 1..64" in gpu.lib.sxh_last_error()
         assert f(gpu.handle, kd, vd, 0, 45, ko, vo) == sh.SXH_OK  # empty: nothing to do
