@@ -69,7 +69,8 @@ __device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx
 // Largest sigma for which opacity * exp(-sigma) can still reach the 1/255 alpha threshold, plus a
 // 0.01 margin: any pair with sigma above it is invalid in the exact evaluation too (its alpha is at
 // most e^-0.01/255), so skipping its exp leaves every result bit-identical.
-__device__ __forceinline__ float sigma_cutoff(float opac) { return __logf(opac * 255.0f) + 0.01f; }
+constexpr float kCutoffMargin = 0.01f;
+__device__ __forceinline__ float sigma_cutoff(float opac) { return __logf(opac * 255.0f) + kCutoffMargin; }
 
 // The block of lane `lane` in wave `wave` (bit index by * 4 + bx of a block mask).
 __device__ __forceinline__ int block_of(int wave, int lane) {
@@ -345,8 +346,14 @@ __device__ __forceinline__ float group_sum4(float a, float b, float c, float d) 
         "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa"
         : "=&v"(v)
         : "v"(s1), "v"(t1));
-    v += dpp_f<0xB1>(v);
-    v += dpp_f<0x4E>(v);
+    // the quad sums, in place (a DPP source reads the VGPR before the add writes it); each reads the
+    // value the previous instruction wrote, hence the s_nop
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
+        : "+v"(v));
     return v;
 }
 
@@ -423,7 +430,7 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long w, int n) {
 __device__ __forceinline__ int ent_rot(int e, int bl, int seg) { return (e + 4 * ((bl >> 2) & 1)) & (seg - 1); }
 
 template <bool ABSGRAD, bool STATS, int kSeg>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5, 8))) k_raster_bwd(RasterArgs a, const float* __restrict__ ralpha,
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) k_raster_bwd(RasterArgs a, const float* __restrict__ ralpha,
                                                          const int32_t* __restrict__ last_ids,
                                                          const float* __restrict__ v_rc, const float* __restrict__ v_ra,
                                                          RasterBwdGrads g) {
@@ -432,14 +439,18 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     // capacity of its entry buffer); its per-entry sums are flushed before the next.
     static_assert(kSeg == 32 || kSeg == 64, "entry buffer rows of 32 or 64 words");
     constexpr int kTermGroups = 8;  // flush: the threads of a slot share its components
-    __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
-    __shared__ float4 s_con[kThreads];  // {a, b, c, Gaussian id (int bits)}
-    __shared__ float4 s_rgb[kThreads];  // {r, g, b, flatten_ids entry (int bits)}
+    // the batch's records, and after them one record that no pixel reaches (slot kThreads: turning
+    // point -inf, so its sigma fails the cutoff), which pads the block lists to whole chunks
+    __shared__ float4 s_xyo[kThreads + 1];  // {x, y, opacity, sigma where alpha turns 1/255}
+    __shared__ float4 s_con[kThreads + 1];  // {a, b, c, Gaussian id (int bits)}
+    __shared__ float4 s_rgb[kThreads + 1];  // {r, g, b, flatten_ids entry (int bits)}
     // per-entry gradient sums of the current segment: [block][component][position in the block's list,
     // rotated by ent_rot so that the 16 writers of a chunk land in 16 different banks]
     __shared__ float s_ent[kBlocks][NV][kSeg];
     __shared__ unsigned long long s_bits[kBlocks][4];  // [block][wave]: the wave's batch slots that reach the block
-    __shared__ uint8_t s_seg[kBlocks][kSeg];          // the block's list of the current segment (batch slots)
+    // the block's list of the current segment as byte offsets of the slots' records (slot * 16), padded to
+    // kSeg entries with the record no pixel reaches
+    __shared__ __align__(8) uint16_t s_seg[kBlocks][kSeg];
     __shared__ uint8_t s_epos[kThreads][kBlocks];     // [slot][block]: the slot's position in the block's list
     __shared__ uint16_t s_bm[kThreads];               // each batch slot's block mask
     __shared__ int32_t s_bbf[kBlocks];                // each block's last contributing intersection
@@ -475,6 +486,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     const int32_t block_bin_final = row_max16(bin_final);
     const uint32_t stamp = g.part ? *g.stamp : 0u;  // the step's stamp for `part` entries
     if (r == 0) s_bbf[bl] = block_bin_final;
+    if (tid == 0) {
+        s_xyo[kThreads] = make_float4(0.f, 0.f, 0.f, -__builtin_inff());
+        s_con[kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+        s_rgb[kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     __syncthreads();
     // the walk starts at the tile's last contributing intersection: everything behind it (most of
     // a dense tile's list, once its pixels saturate) has no pixel to contribute to
@@ -506,11 +522,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
             xyo.w = sigma_cutoff(xyo.z);
             float4 con = a.splats[(size_t)gid * 3 + 1];
             float4 rgb = a.splats[(size_t)gid * 3 + 2];
-            con.w = __int_as_float(gid);
-            rgb.w = __int_as_float(f);
-            s_xyo[tid] = xyo;
-            s_con[tid] = con;
-            s_rgb[tid] = rgb;
             // blocks the cutoff set can reach (the forward's, when it kept them), less those whose every
             // pixel stopped before it
             bm = idx < mask_end ? static_cast<uint32_t>(a.block_masks[idx])
@@ -519,6 +530,12 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
             for (int k = 0; k < kBlocks; k++)
                 if (idx > s_bbf[k]) bm &= ~(1u << k);
             big = bm != 0u && xyo.w > 86.0f;
+            xyo.w -= kCutoffMargin;  // the walk keeps the turning point: sigma - it decides cutoff and nearness
+            con.w = __int_as_float(gid);
+            rgb.w = __int_as_float(f);
+            s_xyo[tid] = xyo;
+            s_con[tid] = con;
+            s_rgb[tid] = rgb;
         }
         s_bm[tid] = static_cast<uint16_t>(bm);
 #pragma unroll
@@ -536,6 +553,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
         const bool general = (s_gen[0] | s_gen[1] | s_gen[2] | s_gen[3]) != 0ull;
 
         const int t_min = batch_end - bin_final;  // slots t >= t_min are at or before the lane's last contributor
+        // the same bound on the list's record offsets (slot * 16; the padding record at kThreads * 16 passes
+        // it whenever any slot does, and fails the cutoff)
+        const int tmin16 = t_min * static_cast<int>(sizeof(float4));
         // The batch's slots are walked in segments [s0, s1), each ending before the slot of the entry
         // with which some block's list would pass kSeg entries; so the lists are as long as the entry
         // buffer allows whatever the slots' density (fixed 32-slot segments left ~6 entries per list,
@@ -601,52 +621,59 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                     const int slot = a + __builtin_ctz(bits);
                     bits &= bits - 1u;
                     if (pos < kSeg) {  // always (the bound); kept so that no write can leave the row
-                        s_seg[bl][pos] = static_cast<uint8_t>(slot);
+                        s_seg[bl][pos] = static_cast<uint16_t>(slot * sizeof(float4));
                         s_epos[slot][bl] = static_cast<uint8_t>(pos);
                     }
                     pos++;
                 }
+                // the rest of the row: the record no pixel reaches (positions past the list, disjoint from
+                // the ones written above)
+                static_assert(kSeg == 32 || kSeg == 64, "two or four pad positions per lane");
+#pragma unroll
+                for (int q = r; q < kSeg; q += 16)
+                    if (q >= cnt) s_seg[bl][q] = static_cast<uint16_t>(kThreads * sizeof(float4));
             }
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the group's lanes read what the others wrote
             int lmax = cnt;  // the longest of the wave's four lists (cnt is uniform within a group)
             lmax = max(lmax, __shfl_xor(lmax, 16, 64));
             lmax = max(lmax, __shfl_xor(lmax, 32, 64));
             const int n4 = (__builtin_amdgcn_readfirstlane(lmax) + 3) >> 2;
-            const uint32_t* seg4 = reinterpret_cast<const uint32_t*>(s_seg[bl]);
-            // The group's Gaussians back to front, four at a time: the four list entries come in one
-            // LDS read and their records in one burst, the four pairs' exponentials are independent,
-            // only T and the back-sum run through them in order. A pair that does not contribute (or a
-            // slot past the list) gets alpha = 0, so T (times 1/(1 - 0) = 1), the back-sum and every
-            // gradient term are left unchanged / zero.
+            const uint2* seg8 = reinterpret_cast<const uint2*>(s_seg[bl]);
+            const char* const lds_xyo = reinterpret_cast<const char*>(s_xyo);
+            const char* const lds_con = reinterpret_cast<const char*>(s_con);
+            const char* const lds_rgb = reinterpret_cast<const char*>(s_rgb);
+            // The group's Gaussians back to front, four at a time: the four list entries (record offsets)
+            // come in one LDS read and their records in one burst, the four pairs' exponentials are
+            // independent, only T and the back-sum run through them in order. A pair that does not
+            // contribute (or a position past the list, which holds the record no pixel reaches) gets
+            // alpha = 0, so T (times 1/(1 - 0) = 1), the back-sum and every gradient term are left
+            // unchanged / zero.
             for (int j4 = 0; j4 < n4; j4++) {
                 const int j = 4 * j4;
-                const uint32_t packed = seg4[j4];  // bytes past the list are masked below
-                int tc[4];
-                bool inl[4];
+                const uint2 pk = seg8[j4];
+                const int off[4] = {static_cast<int>(pk.x & 0xFFFFu), static_cast<int>(pk.x >> 16),
+                                    static_cast<int>(pk.y & 0xFFFFu), static_cast<int>(pk.y >> 16)};
                 float4 xyo[4], con[4], rgb[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    // past the list the byte is stale (or never written) and the entry invalid; it reads the
-                    // segment's first slot, a record loaded in this batch: a slot this workgroup never loaded
-                    // holds whatever an earlier kernel left in the LDS, and an infinite value there would
-                    // turn the back-sum's 0 * value into a NaN
-                    inl[k] = j + k < cnt;
-                    tc[k] = inl[k] ? static_cast<int>((packed >> (8 * k)) & 0xFFu) : s0;
-                    xyo[k] = s_xyo[tc[k]];
-                    con[k] = s_con[tc[k]];
-                    rgb[k] = s_rgb[tc[k]];
+                    xyo[k] = *reinterpret_cast<const float4*>(lds_xyo + off[k]);
+                    con[k] = *reinterpret_cast<const float4*>(lds_con + off[k]);
+                    rgb[k] = *reinterpret_cast<const float4*>(lds_rgb + off[k]);
                 }
                 // the lane storing a slot's sums, and where: the slot's position in the block's list
                 const int e_w = wslot >= 0 && j + wslot < cnt ? j + wslot : -1;
                 float gv[4][NV];
-                float alpha[4], vis[4], dxs[4], dys[4], sig[4], e[4];
+                float alpha[4], vis[4], dxs[4], dys[4], sig[4], d1[4], e[4];
                 bool valid[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     dxs[k] = xyo[k].x - px;
                     dys[k] = xyo[k].y - py;
+                    // the forward's sigma expression, bit for bit: the decisions below must be the forward's
                     sig[k] = sigma_of(con[k].x, con[k].y, con[k].z, dxs[k], dys[k]);
-                    valid[k] = inl[k] & (tc[k] >= t_min) & !(sig[k] > xyo[k].w);  // bitwise: no branches
+                    d1[k] = sig[k] - xyo[k].w;  // sigma less the turning point (alpha = 1/255 there)
+                    // at or before the lane's last contributor (slot >= t_min), and inside the cutoff
+                    valid[k] = (off[k] >= tmin16) & !(d1[k] > kCutoffMargin);  // bitwise: no branches
                 }
                 const bool any_valid = __any(valid[0] | valid[1] | valid[2] | valid[3]);
                 if (STATS) {
@@ -654,7 +681,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                     st_empty += any_valid ? 0 : 1;
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
-                        st_entries += __popcll(__ballot(r == 0 && inl[k]));
+                        st_entries += __popcll(__ballot(r == 0 && j + k < cnt));
                         st_cut += __popcll(__ballot(valid[k]));
                     }
                 }
@@ -667,33 +694,29 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                 }
                 // The exponential's value only enters gradients (compared at a relative tolerance), so the
                 // hardware exp2 serves (relative error below 1.2e-7 (1 + 1.5 sigma): the rounded argument,
-                // log2(e) in float, one ulp of v_exp_f32), but the two decisions taken on it — alpha at
-                // least 1/255, and opacity * exp at most the 0.99 clamp — must be the forward's. Where a
-                // lane lies within 2^-12 in sigma of either turning point, the chunk takes the forward's
-                // exponential instead (the points themselves are approximate to ~1e-6).
-                // (the turning points: opacity * e^-sigma = 1/255 at the cutoff less its 0.01 margin, and
-                // = 0.99 at log(255 * 0.99) below that; approximate, only used to find the pairs close to them)
+                // log2(e) in float, one ulp of v_exp_f32), but the decisions taken on it — alpha at least
+                // 1/255, opacity * exp at most the 0.99 clamp, and sigma not negative — must be the
+                // forward's. Where a valid lane lies within 2^-12 in sigma of either turning point (alpha =
+                // 1/255 at d1 = 0, alpha = 0.99 at d1 = -log(255 * 0.99); both approximate to ~1e-6 and
+                // only used to find the pairs close to them) or has sigma below 2^-12, the chunk takes the
+                // forward's exponential and sign test instead.
                 bool exact = general;
                 if (!exact) {
                     bool near = false;
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         e[k] = __builtin_amdgcn_exp2f(-sig[k] * 1.44269504f);
-                        // sigma less the cutoff: the turning points sit at -0.01 and -0.01 - kLogAlphaSpan
-                        const float d = sig[k] - xyo[k].w;
-                        const bool n1 = __builtin_fabsf(d + 0.01f) < 0x1p-12f;
-                        const bool n2 = __builtin_fabsf(d + (0.01f + kLogAlphaSpan)) < 0x1p-12f;
-                        near = near | (valid[k] & (n1 | n2));
+                        const float m = __builtin_fminf(
+                            __builtin_fminf(__builtin_fabsf(d1[k]), __builtin_fabsf(d1[k] + kLogAlphaSpan)), sig[k]);
+                        near = near | (valid[k] & (m < 0x1p-12f));
                     }
                     exact = __any(near);
                 }
                 if (__builtin_expect(exact, 0)) {
-                    if (general) {
 #pragma unroll
-                        for (int k = 0; k < 4; k++) e[k] = sxm::expf_fast(-sig[k]);
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < 4; k++) e[k] = exp_neg_poly(sig[k]);
+                    for (int k = 0; k < 4; k++) {
+                        e[k] = general ? sxm::expf_fast(-sig[k]) : exp_neg_poly(sig[k]);
+                        valid[k] = valid[k] & !(sig[k] < 0.f);  // (the fast path has no valid lane below 2^-12)
                     }
                 }
 #pragma unroll
@@ -701,7 +724,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
                     const float vis_raw = e[k];
                     const float oa = xyo[k].z * vis_raw;
                     const float alpha_raw = sxd::smin(sx::kMaxAlpha, oa);
-                    const bool ok = valid[k] & !((sig[k] < 0.f) | (alpha_raw < sx::kAlphaThreshold));
+                    const bool ok = valid[k] & !(alpha_raw < sx::kAlphaThreshold);
                     alpha[k] = ok ? alpha_raw : 0.0f;
                     vis[k] = (ok & (oa <= sx::kMaxAlpha)) ? vis_raw : 0.0f;  // clamped alpha: no sigma/opacity terms
                     if (STATS) st_contrib += __popcll(__ballot(ok));
@@ -709,8 +732,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     // hardware reciprocal (1 ulp; exact for 1): the backward is compared at a relative
-                    // tolerance, and an IEEE division costs ~10 instructions per pair
-                    const float ra = __builtin_amdgcn_rcpf(sxd::smax(sx::kMinOneMinusAlpha, 1.0f - alpha[k]));
+                    // tolerance, and an IEEE division costs ~10 instructions per pair. alpha is 0 or in
+                    // [1/255, 0.99], so 1 - alpha >= 0.01 needs no floor.
+                    const float ra = __builtin_amdgcn_rcpf(1.0f - alpha[k]);
                     T *= ra;
                     const float fac = alpha[k] * T;
                     gv[k][6] = fac * vc0;
