@@ -354,9 +354,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         }
         e->mark("scan");
         // index first: the emit also writes each entry's depth bits, into the upper half of keys_b (u64
-        // words; the tile sort's keys and the large tiles' scratch use the lower half of each key buffer)
+        // words; the tile sort's keys and the large tiles' scratch use the lower half of each key buffer);
+        // the tile sort carries them with the keys, between there and the upper half of keys_a
         uint32_t* const edepth =
             index_first ? reinterpret_cast<uint32_t*>(e->keys_b.p) + e->isect_cap : nullptr;
+        uint32_t* const edepth_b =
+            index_first ? reinterpret_cast<uint32_t*>(e->keys_a.p) + e->isect_cap : nullptr;
         int which = 0;
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
@@ -364,7 +367,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
-                                              e->sort_scratch.p, s, index_first, n_dev);
+                                              e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         } else {
@@ -373,7 +376,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
-                                              e->sort_scratch.p, s, index_first, n_dev);
+                                              e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         }
@@ -385,7 +388,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         if (index_first) {
             // the sorted tile keys are spent (the offsets are built): both key buffers and the other
             // value buffer are the scratch of tiles too large for LDS
-            sxk::tile_depth_sort(e->offsets.p, n_tiles, n_host, n_dev, e->tile_order.p, flat, edepth,
+            sxk::tile_depth_sort(e->offsets.p, n_tiles, n_host, n_dev, e->tile_order.p, flat, which ? edepth_b : edepth,
                                  reinterpret_cast<uint32_t*>(e->keys_a.p), reinterpret_cast<uint32_t*>(e->keys_b.p),
                                  which ? e->vals_a.p : e->vals_b.p, s);
             e->mark("tile_depth_sort");

@@ -554,17 +554,21 @@ __global__ void __launch_bounds__(kThreads) k_rs_down(uint32_t* __restrict__ v, 
 // NB = the digit's width in bits (mask = 2^NB - 1). CHAIN: the onesweep pass (tile index from the
 // counter, prefixes by look-back); otherwise tile = blockIdx.x and the tile's run of digit d starts at
 // starts[d * n_tiles + tile] (the scanned count matrix of the reduce-then-scan path).
-template <class K, int NB, bool CHAIN>
+// X: each key also carries a u32 second value, read from xin at the key's input position and written to
+// xout at its output position (null pointers when X is false).
+template <class K, int NB, bool CHAIN, bool X>
 __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin, const int32_t* __restrict__ vin,
                                                       K* __restrict__ kout, int32_t* __restrict__ vout,
                                                       int64_t n, int shift, uint32_t mask, const uint32_t* __restrict__ digit_base,
                                                       uint32_t* __restrict__ status, uint32_t* __restrict__ status_next,
                                                       uint32_t* __restrict__ counter, uint32_t* __restrict__ err,
                                                       const int64_t* __restrict__ n_dev,
-                                                      const uint32_t* __restrict__ starts, int n_tiles) {
+                                                      const uint32_t* __restrict__ starts, int n_tiles,
+                                                      const uint32_t* __restrict__ xin, uint32_t* __restrict__ xout) {
     constexpr int kPerWave = kTile / kWaves;  // 1024
     __shared__ K s_k[kTile];
     __shared__ int32_t s_v[kTile];
+    __shared__ uint32_t s_x[X ? kTile : 1];
     __shared__ uint32_t s_gstart[kBins];  // global start of this tile's run of each digit, minus its local start
     __shared__ uint32_t s_lstart[kBins];
     __shared__ uint32_t s_woff[kWaves][kBins];
@@ -602,6 +606,14 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
         const int tile_n = static_cast<int>(min<int64_t>(kTile, n - base));
         K key[kRounds];
         int32_t val[kRounds];
+        uint32_t xv[X ? kRounds : 1];
+        if (X) {
+#pragma unroll
+            for (int r = 0; r < kRounds; r++) {
+                const int i = wave * kPerWave + r * 64 + lane;
+                xv[r] = i < tile_n ? xin[base + i] : 0u;
+            }
+        }
         // null values: the input index. The (uniform) choice is taken once around straight-line loads: a
         // choice per round compiles to a wait for every load before the next is issued.
         if (tile_n == kTile) {  // uniform
@@ -684,6 +696,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
                 const uint32_t pos = woff[static_cast<uint32_t>(key[r] >> shift) & mask] + off[r];
                 s_k[pos] = key[r];
                 s_v[pos] = val[r];
+                if (X) s_x[pos] = xv[r];
             }
         }
         __syncthreads();
@@ -761,6 +774,7 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
             if (g < n32) {  // always, unless the look-back gave up (err set): then no write lands out of range
                 kout[g] = k;
                 vout[g] = s_v[p];
+                if (X) xout[g] = s_x[p];
             }
         }
     }
@@ -769,14 +783,15 @@ __global__ void __launch_bounds__(kThreads) k_os_pass(const K* __restrict__ kin,
 int tiles_for(int64_t n) { return static_cast<int>((n + kTile - 1) / kTile); }
 
 // One onesweep pass over the digit of `mask`'s width at `shift`.
-template <class K, bool CHAIN>
+template <class K, bool CHAIN, bool X = false>
 void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, K* kout, int32_t* vout, int64_t n,
                     int shift, uint32_t mask, const uint32_t* digit_base, uint32_t* status, uint32_t* status_next,
-                    uint32_t* counter, uint32_t* err, const int64_t* n_dev, const uint32_t* starts = nullptr) {
+                    uint32_t* counter, uint32_t* err, const int64_t* n_dev, const uint32_t* starts = nullptr,
+                    const uint32_t* xin = nullptr, uint32_t* xout = nullptr) {
 #define SX_OS_PASS(NB)                                                                                          \
-    hipLaunchKernelGGL((k_os_pass<K, NB, CHAIN>), dim3(CHAIN ? tiles : (tiles + kXcds - 1) / kXcds * kXcds), \
+    hipLaunchKernelGGL((k_os_pass<K, NB, CHAIN, X>), dim3(CHAIN ? tiles : (tiles + kXcds - 1) / kXcds * kXcds), \
                        dim3(kThreads), 0, s, kin, vin, kout, vout, n, shift, mask, digit_base, status, status_next,  \
-                       counter, err, n_dev, starts, tiles)
+                       counter, err, n_dev, starts, tiles, xin, xout)
     switch (__builtin_popcount(mask)) {
         case 1: SX_OS_PASS(1); break;
         case 2: SX_OS_PASS(2); break;
@@ -788,6 +803,18 @@ void launch_os_pass(int tiles, hipStream_t s, const K* kin, const int32_t* vin, 
         default: SX_OS_PASS(8); break;
     }
 #undef SX_OS_PASS
+}
+
+// x_dst[i] = x_src[pos[i]] (grid-stride)
+__global__ void __launch_bounds__(kThreads) k_gather_x(const int32_t* __restrict__ pos, const uint32_t* __restrict__ x_src,
+                                                       uint32_t* __restrict__ x_dst, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+        x_dst[i] = x_src[pos[i]];
+}
+__global__ void __launch_bounds__(kThreads) k_copy_u32(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                                       int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+        dst[i] = src[i];
 }
 
 constexpr int kMaxPasses = 8;
@@ -807,10 +834,14 @@ static_assert(kHeaderWords * sizeof(uint32_t) % 64 == 0, "the count matrix after
 // buffers). n_dev: when set, the key count is read on the device from *n_dev (at most n, the capacity
 // the grids are sized for), so the launches do not depend on it (a captured graph can replay them).
 // Returns the number of passes, or -1 when nothing was launched because n_dev asks for the
-// three-launch path.
+// three-launch path. src_x (optional; then side_x too): a u32 second value per key that travels with it
+// through the passes like the values (pass p writes side_x[p & 1]); the three-launch path, whose
+// scatter does not carry it, gathers it once after the sort through the values, which must then be
+// the input positions (src_v null).
 template <class K>
 int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32_t* const side_v[2], int64_t n,
-                 uint32_t key_bits, void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev) {
+                 uint32_t key_bits, void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev,
+                 const uint32_t* src_x = nullptr, uint32_t* const* side_x = nullptr) {
     uint32_t* totals = static_cast<uint32_t*>(scratch);
     uint32_t* bases = totals + kMaxPasses * kBins;
     uint32_t* counters = bases + kMaxPasses * kBins;
@@ -844,8 +875,13 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
             // (one workgroup scanning a small matrix in one launch measured slower than these)
             hipLaunchKernelGGL(k_rs_reduce, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
             hipLaunchKernelGGL(k_rs_down, dim3(chunks), dim3(kThreads), 0, s, cnt, len, sums);
-            launch_os_pass<K, false>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p, mask, nullptr,
-                                     nullptr, nullptr, nullptr, err, n_dev, cnt);
+            if (src_x)
+                launch_os_pass<K, false, true>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p, mask,
+                                               nullptr, nullptr, nullptr, nullptr, err, n_dev, cnt,
+                                               p == 0 ? src_x : side_x[(p - 1) & 1], side_x[p & 1]);
+            else
+                launch_os_pass<K, false>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p, mask, nullptr,
+                                         nullptr, nullptr, nullptr, err, n_dev, cnt);
             kin = side_k[p & 1];
             vin = side_v[p & 1];
         }
@@ -865,9 +901,15 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
         uint32_t* st[2] = {hist, status_b};
         for (int p = 0; p < passes; p++) {
             uint32_t* next = p + 1 < passes ? st[(p + 1) & 1] : nullptr;
-            launch_os_pass<K, true>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p,
-                              digit_mask(p, dbits, key_bits), bases + p * kBins, st[p & 1], next, counters + p, err,
-                              n_dev);
+            if (src_x)
+                launch_os_pass<K, true, true>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p,
+                                              digit_mask(p, dbits, key_bits), bases + p * kBins, st[p & 1], next,
+                                              counters + p, err, n_dev, nullptr,
+                                              p == 0 ? src_x : side_x[(p - 1) & 1], side_x[p & 1]);
+            else
+                launch_os_pass<K, true>(tiles, s, kin, vin, side_k[p & 1], side_v[p & 1], n, dbits * p,
+                                        digit_mask(p, dbits, key_bits), bases + p * kBins, st[p & 1], next,
+                                        counters + p, err, n_dev);
             kin = side_k[p & 1];
             vin = side_v[p & 1];
         }
@@ -884,6 +926,18 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
         kin = side_k[p & 1];
         vin = side_v[p & 1];
     }
+    if (src_x) {
+        // the sorted values are the input positions: the second values follow them by a gather, into the
+        // side the passes would have left them in (through side[0] when that is the input itself)
+        const int blocks = static_cast<int>(std::min<int64_t>((n + kThreads - 1) / kThreads, int64_t{1} << 20));
+        uint32_t* const dst = side_x[(passes - 1) & 1];
+        if (dst != src_x) {
+            hipLaunchKernelGGL(k_gather_x, dim3(blocks), dim3(kThreads), 0, s, vin, src_x, dst, n);
+        } else {
+            hipLaunchKernelGGL(k_gather_x, dim3(blocks), dim3(kThreads), 0, s, vin, src_x, side_x[0], n);
+            hipLaunchKernelGGL(k_copy_u32, dim3(blocks), dim3(kThreads), 0, s, side_x[0], dst, n);
+        }
+    }
     return passes;
 }
 
@@ -891,11 +945,13 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
 // index_values the first pass takes each key's input position as its value (vals_a is not read).
 template <class K>
 int radix_sort_ab(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-                  void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev, bool index_values = false) {
+                  void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev, bool index_values = false,
+                  uint32_t* x_a = nullptr, uint32_t* x_b = nullptr) {
     K* const sk[2] = {keys_b, keys_a};
     int32_t* const sv[2] = {vals_b, vals_a};
+    uint32_t* const sx[2] = {x_b, x_a};
     const int passes = radix_sort_t<K>(keys_a, index_values ? nullptr : vals_a, sk, sv, n, key_bits, scratch,
-                                       clear_err, s, n_dev);
+                                       clear_err, s, n_dev, x_a, x_a ? sx : nullptr);
     return passes < 0 ? -1 : (passes & 1);
 }
 
@@ -985,7 +1041,7 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
                                                               int32_t n_isects, const int64_t* __restrict__ n_dev,
                                                               const int32_t* __restrict__ tile_order,
                                                               int32_t* __restrict__ vals,
-                                                              const uint32_t* __restrict__ edepth,
+                                                              const uint32_t* __restrict__ sdepth,
                                                               uint32_t* __restrict__ sk0, uint32_t* __restrict__ sk1,
                                                               int32_t* __restrict__ sv) {
     constexpr int kCap = kWaves * 64 * RMAX;
@@ -1015,11 +1071,12 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
             const int i = wb + r * 64 + lane;
             val[r] = (r < R && i < nt) ? seg[i] : 0;
         }
+        const uint32_t* const dk = sdepth + start;
         uint32_t a = ~0u, o = 0u;
 #pragma unroll
         for (int r = 0; r < RMAX; r++) {
             const bool valid = r < R && wb + r * 64 + lane < nt;
-            key[r] = valid ? edepth[val[r]] : 0u;
+            key[r] = valid ? dk[wb + r * 64 + lane] : 0u;
             if (valid) {
                 a &= key[r];
                 o |= key[r];
@@ -1074,7 +1131,7 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
         // (sk0, vals) and (sk1, sv) over the tile's range, chunk by chunk in list order
         uint32_t a = ~0u, o = 0u;
         for (int32_t i = tid; i < nt; i += kThreads) {
-            const uint32_t k = edepth[seg[i]];
+            const uint32_t k = sdepth[start + i];
             sk0[start + i] = k;
             a &= k;
             o |= k;
@@ -1163,23 +1220,25 @@ int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* val
 }
 
 int radix_sort_positions(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
-                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
-    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true);
+                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev,
+                         uint32_t* x_a, uint32_t* x_b) {
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true, x_a, x_b);
 }
 
 int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
-                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
-    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true);
+                         uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev,
+                         uint32_t* x_a, uint32_t* x_b) {
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true, x_a, x_b);
 }
 
 constexpr int kDepthSortRounds = 8;
 
 void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
-                     const int32_t* tile_order, int32_t* vals, const uint32_t* edepth, uint32_t* scratch_k0,
+                     const int32_t* tile_order, int32_t* vals, const uint32_t* sdepth, uint32_t* scratch_k0,
                      uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s) {
     if (n_tiles <= 0 || (!n_dev && n_isects <= 1)) return;
     hipLaunchKernelGGL(k_tile_depth_sort<kDepthSortRounds>, dim3(n_tiles), dim3(kThreads), 0, s, offsets, n_tiles,
-                       static_cast<int32_t>(n_isects), n_dev, tile_order, vals, edepth, scratch_k0, scratch_k1,
+                       static_cast<int32_t>(n_isects), n_dev, tile_order, vals, sdepth, scratch_k0, scratch_k1,
                        scratch_v);
 }
 

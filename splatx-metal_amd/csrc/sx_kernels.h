@@ -84,13 +84,15 @@ int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* val
                uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
                const int64_t* n_dev = nullptr);
 // The same sort with each key's input position as its value (vals_a is not read; the sorted values
-// are the positions of the keys in the unsorted array).
+// are the positions of the keys in the unsorted array). x_a (optional, then x_b too): a u32 per key
+// that moves with it, sorted into x_a or x_b like the keys (x_a is the input and, after an even pass
+// count, the output).
 int radix_sort_positions(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
                          uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
-                         const int64_t* n_dev = nullptr);
+                         const int64_t* n_dev = nullptr, uint32_t* x_a = nullptr, uint32_t* x_b = nullptr);
 int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
                          uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
-                         const int64_t* n_dev = nullptr);
+                         const int64_t* n_dev = nullptr, uint32_t* x_a = nullptr, uint32_t* x_b = nullptr);
 // The same sort of n u64 keys from read-only inputs into keys_out/vals_out, with keys_tmp/vals_tmp as
 // the second ping-pong side (n > 0, key_bits in 1..64, the onesweep range n < 2^30). No buffer may
 // alias another.
@@ -102,13 +104,14 @@ void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_o
 // what the sorts before it left, so several sorts in a row can be checked with one read.
 uint32_t* sort_error_flag(void* scratch);
 // Index-first intersections: each tile's range [offsets[t], offsets[t+1]) of `vals` (emit positions,
-// in Gaussian index order after a stable tile sort) is sorted stably by edepth[p] (the depth bits of
-// the entry's Gaussian), in place: the (depth, index) order within each tile. The count is *n_dev
-// when set, else n_isects; tile_order (optional) is the order the workgroups take the tiles in.
-// Tiles of more than 4096 entries pass through scratch_k0 / scratch_k1 / scratch_v (each indexed like
-// vals, at least the count long).
+// in Gaussian index order after a stable tile sort) is sorted stably by its entries' depth bits, in
+// place: the (depth, index) order within each tile. sdepth[i] is the depth of entry vals[i] (the
+// tile sort carried them along, so a tile reads its keys in sequence). The count is *n_dev when set,
+// else n_isects; tile_order (optional) is the order the workgroups take the tiles in. Tiles of more
+// than 2048 entries pass through scratch_k0 / scratch_k1 / scratch_v (each indexed like vals, at least
+// the count long; none of them may overlap sdepth).
 void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
-                     const int32_t* tile_order, int32_t* vals, const uint32_t* edepth, uint32_t* scratch_k0,
+                     const int32_t* tile_order, int32_t* vals, const uint32_t* sdepth, uint32_t* scratch_k0,
                      uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s);
 
 // offsets[I*n_tiles] from sorted keys; n_isects > 0.
