@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "sx_dev.h"
 #include "sx_kernels.h"
@@ -131,10 +132,16 @@ __device__ __forceinline__ uint32_t block_mask(float4 xyo, float4 con, float x0,
     return m;
 }
 
-// Per-block Gaussian lists of a batch: s_list[bl][0 .. s_len[bl]) = the batch-local indices t (in
-// increasing order) whose mask has bit bl. All 256 threads call it; thread t passes Gaussian t's mask
-// (0 for slots past the batch). Ends with a barrier.
-__device__ __forceinline__ void build_block_lists(uint32_t m, uint8_t (*s_list)[kThreads], int (*s_bc)[4],
+// Rows of the forward's block lists: a batch's slots plus the padding to a whole chunk of four.
+constexpr int kListRow = kThreads + 4;
+// LDS byte offset of the record that no pixel reaches (slot kThreads of the record arrays).
+constexpr uint32_t kPadRecord = kThreads * sizeof(float4);
+
+// Per-block Gaussian lists of a batch: s_list[bl][0 .. s_len[bl]) = the LDS byte offsets (slot * 16) of
+// the batch-local slots t (in increasing order) whose mask has bit bl, padded to a multiple of four
+// entries with kPadRecord. All 256 threads call it; thread t passes Gaussian t's mask (0 for slots past
+// the batch). Ends with a barrier.
+__device__ __forceinline__ void build_block_lists(uint32_t m, uint16_t (*s_list)[kListRow], int (*s_bc)[4],
                                                   int* s_len) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -150,9 +157,13 @@ __device__ __forceinline__ void build_block_lists(uint32_t m, uint8_t (*s_list)[
         int off = 0;
 #pragma unroll
         for (int sw = 0; sw < 4; sw++) off += sw < wave ? s_bc[bl][sw] : 0;
-        if ((m >> bl) & 1u) s_list[bl][off + __popcll(bal & below)] = static_cast<uint8_t>(tid);
+        if ((m >> bl) & 1u) s_list[bl][off + __popcll(bal & below)] = static_cast<uint16_t>(tid * sizeof(float4));
     }
-    if (tid < kBlocks) s_len[tid] = s_bc[tid][0] + s_bc[tid][1] + s_bc[tid][2] + s_bc[tid][3];
+    if (tid < kBlocks) {
+        const int len = s_bc[tid][0] + s_bc[tid][1] + s_bc[tid][2] + s_bc[tid][3];
+        s_len[tid] = len;
+        for (int q = len; q < ((len + 3) & ~3); q++) s_list[tid][q] = static_cast<uint16_t>(kPadRecord);
+    }
     __syncthreads();
 }
 
@@ -165,10 +176,11 @@ __device__ __forceinline__ int wave_list_max(const int* s_len, int wave) {
 template <bool STATS>
 __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __restrict__ out_rgb,
                                                          float* __restrict__ out_alpha, int32_t* __restrict__ out_last) {
-    __shared__ float4 s_xyo[kThreads];  // {x, y, opacity, sigma cutoff}
-    __shared__ float4 s_con[kThreads];
-    __shared__ float4 s_rgb[kThreads];
-    __shared__ __align__(16) uint8_t s_list[kBlocks][kThreads];
+    // the batch's records, then (slot kThreads) one that no pixel reaches: cutoff -inf, the lists' padding
+    __shared__ float4 s_xyo[kThreads + 1];  // {x, y, opacity, sigma cutoff}
+    __shared__ float4 s_con[kThreads + 1];
+    __shared__ float4 s_rgb[kThreads + 1];
+    __shared__ __align__(16) uint16_t s_list[kBlocks][kListRow];
     __shared__ int s_bc[kBlocks][4];
     __shared__ int s_len[kBlocks];
     __shared__ unsigned long long s_gen[kThreads / 64];  // per wave: the batch's splats past the polynomial's range
@@ -204,6 +216,11 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     bool done = !inside;
     unsigned long long st_iters = 0, st_entries = 0, st_taken = 0;  // STATS only (wave-uniform)
     int32_t loaded_end = range_end;  // the end of the entries loaded (and their block masks stored)
+    if (tid == 0) {  // (published by the first batch's barriers)
+        s_xyo[kThreads] = make_float4(0.f, 0.f, 0.f, -__builtin_inff());
+        s_con[kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+        s_rgb[kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     for (int32_t bstart = range_start; bstart < range_end; bstart += kThreads) {
         if (__syncthreads_count(done) == kThreads) {  // also the barrier before LDS reuse
             loaded_end = bstart;
@@ -237,9 +254,12 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
         // lane takes a pair through selects rather than branches, and stops once its T is spent
         const int len = s_len[bl];
         const int n_it = __builtin_amdgcn_readfirstlane(wave_list_max(s_len, wave));
-        const uint8_t* my_list = s_list[bl];
+        const uint2* const list4 = reinterpret_cast<const uint2*>(s_list[bl]);
+        const char* const lds_xyo = reinterpret_cast<const char*>(s_xyo);
+        const char* const lds_con = reinterpret_cast<const char*>(s_con);
+        const char* const lds_rgb = reinterpret_cast<const char*>(s_rgb);
         // one list entry composited into the lane's pixel: opacity * exp(-sigma) = oe
-        auto composite = [&](bool in, float sg, float oe, int tc, int32_t id) {
+        auto composite = [&](bool in, float sg, float oe, int off, int32_t id) {
             const float alpha = sxd::smin(sx::kMaxAlpha, oe);
             bool take = in && !done && !(sg < 0.f) && !(alpha < sx::kAlphaThreshold);
             const float next_T = T * (1.0f - alpha);
@@ -247,7 +267,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             done = done || spent;
             take = take && !spent;
             const float w = alpha * T;
-            const float4 c = s_rgb[tc];
+            const float4 c = *reinterpret_cast<const float4*>(lds_rgb + off);
             r0 = take ? __builtin_fmaf(c.x, w, r0) : r0;
             r1 = take ? __builtin_fmaf(c.y, w, r1) : r1;
             r2 = take ? __builtin_fmaf(c.z, w, r2) : r2;
@@ -255,39 +275,49 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
             T = take ? next_T : T;
             if (STATS) st_taken += __popcll(__ballot(take));
         };
-        // four list entries per iteration (their indices in one LDS read): their sigmas and exponentials
-        // are independent, only T and the colour sums run through them in order
-        for (int j = 0; j < n_it; j += 4) {
-            if (__all(done)) break;  // uniform
-            // bytes past the list are masked (stale or never written); the row is 16-B aligned, j a
-            // multiple of 4 and at most 252
-            const uint32_t packed = *reinterpret_cast<const uint32_t*>(my_list + j);
-            int t[4], tc[4];
-            float4 xyo[4], con[4];
-            float sg[4];
-            bool in[4];
+        // four list entries per iteration (their record offsets in one LDS read): their sigmas and
+        // exponentials are independent, only T and the colour sums run through them in order. The
+        // iteration loop is compiled once per exponential (the choice is the batch's), so no entry tests it.
+        auto walk = [&](auto general_exp) {
+            for (int j = 0; j < n_it; j += 4) {
+                if (__all(done)) break;  // uniform
+                // a chunk past the group's list (the list is padded to whole chunks) reads the padding record
+                const uint2 pk4 = list4[j >> 2];
+                const uint2 pk = j < len ? pk4 : make_uint2(kPadRecord * 0x10001u, kPadRecord * 0x10001u);
+                const int off[4] = {static_cast<int>(pk.x & 0xFFFFu), static_cast<int>(pk.x >> 16),
+                                    static_cast<int>(pk.y & 0xFFFFu), static_cast<int>(pk.y >> 16)};
+                float4 xyo[4];
+                float sg[4];
+                bool in[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                t[k] = j + k < len ? static_cast<int>((packed >> (8 * k)) & 0xFFu) : -1;  // group-uniform
-                tc[k] = t[k] < 0 ? 0 : t[k];  // slot 0 holds a record of this batch
-                xyo[k] = s_xyo[tc[k]];
-                con[k] = s_con[tc[k]];
-                sg[k] = sigma_of(con[k].x, con[k].y, con[k].z, xyo[k].x - px, xyo[k].y - py);
-                in[k] = (t[k] >= 0) & !done & !(sg[k] > xyo[k].w);
+                for (int k = 0; k < 4; k++) {
+                    xyo[k] = *reinterpret_cast<const float4*>(lds_xyo + off[k]);
+                    const float4 con = *reinterpret_cast<const float4*>(lds_con + off[k]);
+                    sg[k] = sigma_of(con.x, con.y, con.z, xyo[k].x - px, xyo[k].y - py);
+                    in[k] = !done & !(sg[k] > xyo[k].w);  // (the padding record's cutoff is -inf)
+                }
+                if (STATS) {
+                    st_iters += min(4, n_it - j);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) st_entries += __popcll(__ballot((lane & 15) == 0 && j + k < len));
+                }
+                if (!__any(in[0] | in[1] | in[2] | in[3])) continue;  // uniform
+                float vis[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if constexpr (decltype(general_exp)::value) vis[k] = sxm::expf_fast(-sg[k]);
+                    else vis[k] = exp_neg_poly(sg[k]);
+                }
+                // front to back: a lane that stopped at an entry takes nothing more
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    composite(in[k], sg[k], xyo[k].z * vis[k], off[k], bstart + (off[k] >> 4));
             }
-            if (STATS) {
-                st_iters += min(4, n_it - j);
-#pragma unroll
-                for (int k = 0; k < 4; k++) st_entries += __popcll(__ballot((lane & 15) == 0 && t[k] >= 0));
-            }
-            if (!__any(in[0] | in[1] | in[2] | in[3])) continue;  // uniform
-            float vis[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) vis[k] = general ? sxm::expf_fast(-sg[k]) : exp_neg_poly(sg[k]);
-            // front to back: a lane that stopped at an entry takes nothing more
-#pragma unroll
-            for (int k = 0; k < 4; k++) composite(in[k], sg[k], xyo[k].z * vis[k], tc[k], bstart + t[k]);
-        }
+        };
+        if (general)
+            walk(std::true_type{});
+        else
+            walk(std::false_type{});
     }
     // every pixel's last contributor lies in a loaded batch, before loaded_end: the backward's walk
     // stays inside the stored masks
