@@ -49,8 +49,11 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
             # the Gaussian (4 B) and its depth bits (4 B) out
             return v * (12.0 + 32.0) + i * (kb + 8.0)
         if name == "tile_depth_sort":
-            # per entry: the emit position in and out (8 B), its depth bits gathered through it (4 B)
+            # per entry: the emit position in and out (8 B), its depth bits (4 B, carried by the tile sort)
             return 12.0 * i
+        if name == "sort":
+            # as below, plus each entry's depth bits (4 B) read and written with it by every pass
+            return i * (kb + 2.0 * (kb + 4.0 + 4.0) * shape["tile_passes"] - 4.0)
     if name == "preprocess":
         # params of every Gaussian (44 B) + SH coefficients of visible ones; writes radii+count (12 B),
         # and for visible ones the 48-B splat record
@@ -60,11 +63,13 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
         # conic/comp/meta (20 B); write params+moments
         return 5.0 * n + v * (4.0 * pd * 3 + 36 + 20 + 4.0 * pd * 3)
     if name == "raster_fwd":
-        # per intersection: its emit position (4 B), the Gaussian of that position (4 B), the 36-B record
-        return i * (4 + 4 + 36) + px * 20.0
+        # the survey's per-unit figures: 40 B read per intersection (its sorted id and the splat's record),
+        # 20 B written per pixel (colour, alpha, last id)
+        return i * 40.0 + px * 20.0
     if name == "raster_bwd":
-        # as the forward, plus the 36-B sums and the 4-B step stamp stored per (tile, Gaussian)
-        return i * (4 + 4 + 36 + 36 + 4) + px * (4 + 4 + 12)
+        # the survey's per-unit figures: 40 B read and 36 B of gradient sums scattered per intersection,
+        # 20 B read per pixel (alpha, last id, v_render)
+        return i * (40.0 + 36.0) + px * 20.0
     if name == "gather":
         # order, offset and touched flag per Gaussian with tiles (13 B), the 36-B sums and stamp of the
         # entries, the 48-B gradient record of the visible Gaussians
@@ -438,6 +443,7 @@ def main():
     dom_bytes = algorithmic_bytes(dom, sc.n, V, I, px, sh_k, shape)
     achieved = dom_bytes / 1e9 / (avg[dom] / 1e3)
     step_bytes = sum(algorithmic_bytes(k, sc.n, V, I, px, sh_k, shape) for k in kernel_names)
+    ref_step_bytes = 84.0 * sc.n + 1708.0 * V + 288.0 * I + 160.0 * px
 
     res = {
         "metric": "train-step ms/iter (fwd+bwd+Adam) at N=1M, 1297x840; % HBM roofline",
@@ -466,6 +472,11 @@ def main():
         "final_loss": round(float(losses[-1]), 6),
         "step_alg_GB": round(step_bytes / 1e9, 4),
         "step_hbm_roofline_frac": round(step_bytes / 1e9 / (ms_per_step / 1e3) / HBM_PEAK_GBS, 5),
+        # the reference design's step bytes, 84 N + 1708 V + 288 I + 160 P (an unfused 8-bit sort over 45-bit
+        # keys, a perturb pass), over the measured step time
+        "step_alg_GB_reference_design": round(ref_step_bytes / 1e9, 4),
+        "step_hbm_roofline_frac_reference_design": round(ref_step_bytes / 1e9 / (ms_per_step / 1e3)
+                                                         / HBM_PEAK_GBS, 5),
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(dom, args.config), "alg_bytes": round(dom_bytes)},
