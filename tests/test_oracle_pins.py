@@ -262,11 +262,12 @@ def test_scan_sort_offsets_brute_force(oracle):
 
 
 def test_sort_counting_passes_brute_force(oracle):
-    """The oracle's sort (LSD counting passes over the significant bits) against numpy's stable argsort
-    where the passes matter most: few key bits with heavy ties, keys whose low or middle bytes are all
-    equal (passes skipped), a key width that is not a multiple of 8, one key, and keys in descending
-    order. A pass that dropped stability, used the wrong digit or skipped a needed byte would reorder
-    equal keys or leave keys unsorted."""
+    """The oracle's sort (a counting pass on the top 16 significant bits, then 8-bit LSD counting passes
+    inside each run of equal top bits) against numpy's stable argsort where the passes matter most: few
+    key bits with heavy ties, keys whose low or middle bytes are all equal (passes skipped), long runs of
+    equal top bits whose low bits need two passes, a key width that is not a multiple of 8, one key, and
+    keys in descending order. A pass that dropped stability, used the wrong digit, split the bits at the
+    wrong place or skipped a needed byte would reorder equal keys or leave keys unsorted."""
     r = inputs.rng(21)
     cases = {
         "13 bits, heavy ties": r.integers(0, 1 << 13, 40_000).astype(np.uint64),
@@ -274,11 +275,13 @@ def test_sort_counting_passes_brute_force(oracle):
         "45 bits, low 32 bits equal": (r.integers(0, 1 << 13, 30_000).astype(np.uint64) << np.uint64(32)) | np.uint64(7),
         "40 bits, middle bytes equal": (r.integers(0, 256, 20_000).astype(np.uint64) << np.uint64(32))
         | np.uint64(0x00ABCD00) | r.integers(0, 256, 20_000).astype(np.uint64),
+        "30 bits, 4 runs of top bits": (r.integers(0, 4, 30_000).astype(np.uint64) << np.uint64(14))
+        | r.integers(0, 1 << 14, 30_000).astype(np.uint64),
         "one key": np.array([5], np.uint64),
         "descending 17 bits": np.arange(70_000, 0, -1).astype(np.uint64),
     }
     widths = {"13 bits, heavy ties": 13, "1 bit": 1, "45 bits, low 32 bits equal": 45,
-              "40 bits, middle bytes equal": 40, "one key": 3, "descending 17 bits": 17}
+              "40 bits, middle bytes equal": 40, "30 bits, 4 runs of top bits": 30, "one key": 3, "descending 17 bits": 17}
     for name, keys in cases.items():
         vals = r.integers(-2**31, 2**31 - 1, keys.size).astype(np.int32)
         ks, vs = oracle.sort_isect(keys, vals, widths[name])
