@@ -352,6 +352,14 @@ __device__ __forceinline__ int row_max16(int v) {
     v = max(v, dpp_i<0x140>(v));  // row_mirror
     return v;
 }
+// Minimum over each 16-lane row (every lane of the row ends with it).
+__device__ __forceinline__ int row_min16(int v) {
+    v = min(v, dpp_i<0xB1>(v));
+    v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0x141>(v));
+    v = min(v, dpp_i<0x140>(v));
+    return v;
+}
 // Four per-lane values (one per list slot A..D of the group) summed over each 16-lane group in 8
 // instructions. Stage 1 pairs lane r with r ^ 8 (row_ror:8): lanes 0-7 sum A, lanes 8-15 sum B (C
 // and D likewise); stage 2 pairs r with its mirror in the 8-lane half (row_half_mirror): quads 0 and
@@ -390,29 +398,6 @@ __device__ __forceinline__ float group_sum4(float a, float b, float c, float d) 
 constexpr int kGrads = 9;  // v_xy(2), v_opacity, v_conic(3), v_rgb(3)
 // log(255 * 0.99): from the sigma where alpha turns 1/255 to the sigma where it reaches the 0.99 clamp
 constexpr float kLogAlphaSpan = 5.53121185f;
-
-// The gradient components that term group q of the flush adds (-1: none). Components 0 and 1 (the
-// position moments) stay in one group. With 4 groups: {0,1} {2,3,4} {5,6,(9)} {7,8,(10)}; with 8 or
-// more: {0,1} {2} ... {8} and the absolute moments (9), (10) in groups 4 and 5 (8 groups) or 8 and 9.
-template <int NV, int G>
-__device__ __forceinline__ void flush_terms(int q, int* ks) {
-    ks[0] = ks[1] = ks[2] = -1;
-    if (G == 4) {
-        if (q == 0) { ks[0] = 0; ks[1] = 1; }
-        if (q == 1) { ks[0] = 2; ks[1] = 3; ks[2] = 4; }
-        if (q == 2) { ks[0] = 5; ks[1] = 6; ks[2] = NV > 9 ? 9 : -1; }
-        if (q == 3) { ks[0] = 7; ks[1] = 8; ks[2] = NV > 9 ? 10 : -1; }
-    } else {
-        if (q == 0) { ks[0] = 0; ks[1] = 1; }
-        else if (q <= 7) ks[0] = q + 1;
-        if (NV > 9) {
-            if (G == 8 && q == 4) ks[1] = 9;
-            if (G == 8 && q == 5) ks[1] = 10;
-            if (G >= 16 && q == 8) ks[0] = 9;
-            if (G >= 16 && q == 9) ks[0] = 10;
-        }
-    }
-}
 
 // The address of gradient component k of Gaussian gid: the packed record (x, y, opacity, - | conic
 // a, b, c, - | r, g, b, -) or the per-op arrays.
@@ -454,6 +439,22 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long w, int n) {
     return pos + (n > static_cast<int>(x & 1u) ? 1 : 0);
 }
 
+// The slot of the (seg + 1)-th set bit at or after slot s0 (uniform) of a 256-bit slot mask, kThreads if
+// there is none: where a block's list from s0 on would pass seg entries. It is the (r + seg + 1)-th set
+// bit of the whole mask, r the set bits before s0, so one descent over the word that holds it finds it.
+__device__ __forceinline__ int seg_limit(const unsigned long long* w4, int s0, int seg) {
+    const unsigned long long w0 = w4[0], w1 = w4[1], w2 = w4[2], w3 = w4[3];
+    const int p1 = __popcll(w0), p2 = p1 + __popcll(w1), p3 = p2 + __popcll(w2), p4 = p3 + __popcll(w3);
+    const int i0 = s0 >> 6;
+    const unsigned long long ws = i0 == 0 ? w0 : i0 == 1 ? w1 : i0 == 2 ? w2 : w3;
+    const int before = (i0 == 0 ? 0 : i0 == 1 ? p1 : i0 == 2 ? p2 : p3) + __popcll(ws & ((1ull << (s0 & 63)) - 1ull));
+    const int need = before + seg + 1;
+    if (need > p4) return kThreads;
+    const int i = need <= p1 ? 0 : need <= p2 ? 1 : need <= p3 ? 2 : 3;
+    const unsigned long long w = i == 0 ? w0 : i == 1 ? w1 : i == 2 ? w2 : w3;
+    return 64 * i + nth_set_bit(w, need - (i == 0 ? 0 : i == 1 ? p1 : i == 2 ? p2 : p3));
+}
+
 // Position of entry e of block bl in its row of the backward's entry buffer: rotated by 4 for the
 // blocks of odd block rows, so that the 16 writers of a chunk (the 2x2 blocks of a wave, four consecutive
 // entries each; rows of kSeg words, a multiple of 32) use 16 different LDS banks.
@@ -468,7 +469,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     // A segment: a run of batch slots in which no block's list holds more than kSeg entries (the
     // capacity of its entry buffer); its per-entry sums are flushed before the next.
     static_assert(kSeg == 32 || kSeg == 64, "entry buffer rows of 32 or 64 words");
-    constexpr int kTermGroups = 8;  // flush: the threads of a slot share its components
     // the batch's records, and after them one record that no pixel reaches (slot kThreads: turning
     // point -inf, so its sigma fails the cutoff), which pads the block lists to whole chunks
     __shared__ float4 s_xyo[kThreads + 1];  // {x, y, opacity, sigma where alpha turns 1/255}
@@ -481,7 +481,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     // the block's list of the current segment as byte offsets of the slots' records (slot * 16), padded to
     // kSeg entries with the record no pixel reaches
     __shared__ __align__(8) uint16_t s_seg[kBlocks][kSeg];
-    __shared__ uint8_t s_epos[kThreads][kBlocks];     // [slot][block]: the slot's position in the block's list
+    __shared__ uint8_t s_epos[kThreads][kBlocks];     // [slot][block]: the slot's entry in the block's row (ent_rot)
     __shared__ uint16_t s_bm[kThreads];               // each batch slot's block mask
     __shared__ int32_t s_bbf[kBlocks];                // each block's last contributing intersection
     __shared__ unsigned long long s_gen[4];           // per wave: the batch's splats past the polynomial's range
@@ -593,28 +593,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
         // bounds from the block masks.
         const unsigned long long w_bl[4] = {s_bits[bl][0], s_bits[bl][1], s_bits[bl][2], s_bits[bl][3]};
         for (int s0 = 0; s0 < batch_size;) {  // uniform
-            // lane k < 16: the slot of block k's (kSeg + 1)-th entry from s0 (none: kThreads); s1 = the least
-            int lim = kThreads;
-            {
-                const int k = lane & (kBlocks - 1);  // lanes 16-63 repeat lanes 0-15
-                int need = kSeg + 1;
-                bool found = false;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    unsigned long long w = s_bits[k][i];
-                    w &= (64 * i + 63 < s0) ? 0ull : (64 * i >= s0 ? ~0ull : (~0ull << (s0 & 63)));
-                    const int c = __popcll(w);
-                    if (!found && c >= need) {
-                        lim = 64 * i + nth_set_bit(w, need);
-                        found = true;
-                    }
-                    if (!found) need -= c;
-                }
-            }
-            lim = min(lim, __shfl_xor(lim, 8, 64));
-            lim = min(lim, __shfl_xor(lim, 4, 64));
-            lim = min(lim, __shfl_xor(lim, 2, 64));
-            lim = min(lim, __shfl_xor(lim, 1, 64));
+            // lane k < 16 (lanes 16-63 repeat them): the slot of block k's (kSeg + 1)-th entry from s0 (none:
+            // kThreads); s1 = the least
+            const int lim = row_min16(seg_limit(s_bits[lane & (kBlocks - 1)], s0, kSeg));
             // (lim >= s0 + kSeg for every block, so s1 > s0; the max only makes progress explicit)
             const int s1 = max(s0 + 1, min(static_cast<int>(batch_size), __builtin_amdgcn_readfirstlane(lim)));
             // this group's list of the segment: lane r places the set slots among slots [16 r, 16 r + 16)
@@ -652,7 +633,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     bits &= bits - 1u;
                     if (pos < kSeg) {  // always (the bound); kept so that no write can leave the row
                         s_seg[bl][pos] = static_cast<uint16_t>(slot * sizeof(float4));
-                        s_epos[slot][bl] = static_cast<uint8_t>(pos);
+                        s_epos[slot][bl] = static_cast<uint8_t>(ent_rot(pos, bl, kSeg));
                     }
                     pos++;
                 }
@@ -774,24 +755,27 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     // kept as its dot product with v_render (fused multiply-adds: gradient algebra only)
                     const float cvc = __builtin_fmaf(rgb[k].x, vc0, __builtin_fmaf(rgb[k].y, vc1, rgb[k].z * vc2));
                     const float v_alpha = __builtin_fmaf(T, cvc, ra * (tva - bdot));
-                    const float v_sigma = -xyo[k].z * vis[k] * v_alpha;
                     const float dx = dxs[k], dy = dys[k];
-                    const float vdx = v_sigma * dx, vdy = v_sigma * dy;
+                    const float gw = vis[k] * v_alpha;  // v_opacity's term; v_sigma = -opacity * gw
+                    gv[k][2] = gw;
                     if (ABSGRAD) {  // per-pixel 2D gradients are needed for their absolute values
+                        const float v_sigma = -xyo[k].z * vis[k] * v_alpha;
+                        const float vdx = v_sigma * dx, vdy = v_sigma * dy;
                         gv[k][0] = __builtin_fmaf(con[k].x, vdx, con[k].y * vdy);
                         gv[k][1] = __builtin_fmaf(con[k].y, vdx, con[k].z * vdy);
                         gv[k][3] = 0.5f * vdx * dx;
+                        gv[k][4] = vdx * dy;
                         gv[k][5] = 0.5f * vdy * dy;
                         gv[k][9] = fabsf(gv[k][0]);
                         gv[k][10] = fabsf(gv[k][1]);
-                    } else {  // moments: the conic and the halves are applied once per splat at the flush
-                        gv[k][0] = vdx;
-                        gv[k][1] = vdy;
-                        gv[k][3] = vdx * dx;
-                        gv[k][5] = vdy * dy;
+                    } else {  // moments of gw: the conic, -opacity and the halves are applied once per splat
+                        const float wdx = gw * dx, wdy = gw * dy;  // at the flush
+                        gv[k][0] = wdx;
+                        gv[k][1] = wdy;
+                        gv[k][3] = wdx * dx;
+                        gv[k][4] = wdx * dy;
+                        gv[k][5] = wdy * dy;
                     }
-                    gv[k][4] = vdx * dy;
-                    gv[k][2] = vis[k] * v_alpha;
                     bdot = __builtin_fmaf(fac, cvc, bdot);
                 }
 #pragma unroll
@@ -801,56 +785,46 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 }
             }
             __syncthreads();
-            // the segment's totals: the threads of a slot sum its entries over the blocks it reaches, each
-            // thread a few of the components (eight term groups per slot). (Consecutive slots per lane and
-            // a term group per 2^k lanes, which keeps the buffer reads in different banks, measured slower:
-            // the segment's length then fills the passes only partly.)
-            for (int w = tid; w < (s1 - s0) * kTermGroups; w += kThreads) {
-                const int q = w & (kTermGroups - 1);
-                const int slot = s0 + (w >> 3);
-                const uint32_t m0 = static_cast<uint32_t>(s_bm[slot]);
-                if (m0) {
-                    // components of term group q: the two position moments stay together (the conic
-                    // applies to both at once)
-                    int ks[3];
-                    flush_terms<NV, kTermGroups>(q, ks);
-                    float v[3] = {0.f, 0.f, 0.f};
-                    uint32_t m = m0;
+            // the segment's totals: thread t sums slot s0 + t's entries over the blocks it reaches, all
+            // components at once (s1 - s0 <= kThreads). (Components shared out over 2, 3, 4 or 8 threads
+            // per slot measured slower: each thread walks the slot's blocks again.)
+            if (tid < s1 - s0) {
+                const int slot = s0 + tid;
+                uint32_t m = static_cast<uint32_t>(s_bm[slot]);
+                if (m) {
+                    float v[NV];
+#pragma unroll
+                    for (int k = 0; k < NV; k++) v[k] = 0.f;
                     while (m) {
                         const int b2 = __builtin_ctz(m);
                         m &= m - 1u;
-                        const int e2 = ent_rot(static_cast<int>(s_epos[slot][b2]), b2, kSeg);  // the slot's entry
+                        const int e2 = s_epos[slot][b2];  // the slot's entry in the block's row
 #pragma unroll
-                        for (int i = 0; i < 3; i++)
-                            if (ks[i] >= 0) v[i] += s_ent[b2][ks[i]][e2];
+                        for (int k = 0; k < NV; k++) v[k] += s_ent[b2][k][e2];
                     }
-                    if (!ABSGRAD && ks[0] == 0) {  // sum_p v_sigma (a dx + b dy, b dx + c dy)
+                    if (!ABSGRAD) {
+                        // sum_p gw (a dx + b dy, b dx + c dy); the moments of gw times -opacity are those of
+                        // v_sigma, and dx^2, dy^2 take a half
                         const float4 cn = s_con[slot];
                         const float sdx = v[0], sdy = v[1];
-                        v[0] = __builtin_fmaf(cn.x, sdx, cn.y * sdy);
-                        v[1] = __builtin_fmaf(cn.y, sdx, cn.z * sdy);
+                        const float nop = -s_xyo[slot].z;
+                        v[0] = __builtin_fmaf(cn.x, sdx, cn.y * sdy) * nop;
+                        v[1] = __builtin_fmaf(cn.y, sdx, cn.z * sdy) * nop;
+                        v[3] *= 0.5f * nop;
+                        v[4] *= nop;
+                        v[5] *= 0.5f * nop;
                     }
                     const int32_t f = __float_as_int(s_rgb[slot].w);
                     if (g.part) {  // plain stores at the emit position; the gather sums them in a fixed order
-                        float* dst = g.part + (size_t)f * kPartStride;
-#pragma unroll
-                        for (int i = 0; i < 3; i++) {
-                            const int k = ks[i];
-                            if (k < 0) continue;
-                            dst[k] = (!ABSGRAD && (k == 3 || k == 5)) ? 0.5f * v[i] : v[i];  // halves of dx^2, dy^2
-                        }
-                        if (q == 0) {
-                            dst[kPartFloats] = __uint_as_float(stamp);  // the entry is this step's
-                            g.touched[__float_as_int(s_con[slot].w)] = 1;  // the Gaussian has entries to gather
-                        }
+                        float4* dst = reinterpret_cast<float4*>(g.part + (size_t)f * kPartStride);
+                        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+                        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+                        dst[2] = make_float4(v[8], __uint_as_float(stamp), 0.f, 0.f);  // the entry is this step's
+                        g.touched[__float_as_int(s_con[slot].w)] = 1;  // the Gaussian has entries to gather
                     } else {
 #pragma unroll
-                        for (int i = 0; i < 3; i++) {
-                            const int k = ks[i];
-                            if (k < 0 || v[i] == 0.f) continue;
-                            const float x = (!ABSGRAD && (k == 3 || k == 5)) ? 0.5f * v[i] : v[i];
-                            atomicAdd(grad_slot(g, f, k), x);
-                        }
+                        for (int k = 0; k < NV; k++)
+                            if (v[k] != 0.f) atomicAdd(grad_slot(g, f, k), v[k]);
                     }
                 }
             }
