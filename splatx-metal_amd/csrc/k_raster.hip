@@ -455,10 +455,13 @@ __device__ __forceinline__ int seg_limit(const unsigned long long* w4, int s0, i
     return 64 * i + nth_set_bit(w, need - (i == 0 ? 0 : i == 1 ? p1 : i == 2 ? p2 : p3));
 }
 
-// Position of entry e of block bl in its row of the backward's entry buffer: rotated by 4 for the
-// blocks of odd block rows, so that the 16 writers of a chunk (the 2x2 blocks of a wave, four consecutive
-// entries each; rows of kSeg words, a multiple of 32) use 16 different LDS banks.
-__device__ __forceinline__ int ent_rot(int e, int bl, int seg) { return (e + 4 * ((bl >> 2) & 1)) & (seg - 1); }
+// Position of entry e of block bl in its row of the backward's entry buffer: rotated by 0, 4, 8 or 12
+// by the block's place in its 2x2 quadrant, so that the 16 writers of a chunk (the four blocks of a wave,
+// four consecutive entries each; entries of 10 or 12 words, written as pairs of words) use different
+// LDS banks.
+__device__ __forceinline__ int ent_rot(int e, int bl, int seg) {
+    return (e + 4 * ((bl & 1) + 2 * ((bl >> 2) & 1))) & (seg - 1);
+}
 
 template <bool ABSGRAD, bool STATS, int kSeg>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 8))) k_raster_bwd(RasterArgs a, const float* __restrict__ ralpha,
@@ -474,14 +477,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
     __shared__ float4 s_xyo[kThreads + 1];  // {x, y, opacity, sigma where alpha turns 1/255}
     __shared__ float4 s_con[kThreads + 1];  // {a, b, c, Gaussian id (int bits)}
     __shared__ float4 s_rgb[kThreads + 1];  // {r, g, b, flatten_ids entry (int bits)}
-    // per-entry gradient sums of the current segment: [block][component][position in the block's list,
-    // rotated by ent_rot so that the 16 writers of a chunk land in 16 different banks]
-    __shared__ float s_ent[kBlocks][NV][kSeg];
+    // per-entry gradient sums of the current segment: [block][position in the block's list, rotated by
+    // ent_rot][component], an entry's components contiguous (written and read as pairs of words)
+    constexpr int kEntWords = (NV + 2) & ~1;
+    __shared__ __align__(16) float s_ent[kBlocks][kSeg][kEntWords];
     __shared__ unsigned long long s_bits[kBlocks][4];  // [block][wave]: the wave's batch slots that reach the block
     // the block's list of the current segment as byte offsets of the slots' records (slot * 16), padded to
     // kSeg entries with the record no pixel reaches
     __shared__ __align__(8) uint16_t s_seg[kBlocks][kSeg];
-    __shared__ uint8_t s_epos[kThreads][kBlocks];     // [slot][block]: the slot's entry in the block's row (ent_rot)
+    __shared__ uint8_t s_epos[kThreads][kBlocks];     // [slot][block]: the slot's entry in the block's row
     __shared__ uint16_t s_bm[kThreads];               // each batch slot's block mask
     __shared__ int32_t s_bbf[kBlocks];                // each block's last contributing intersection
     __shared__ unsigned long long s_gen[4];           // per wave: the batch's splats past the polynomial's range
@@ -698,8 +702,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                 }
                 if (!any_valid) {  // uniform: every alpha 0, T, the back-sum and the gradients unchanged
                     if (e_w >= 0) {
+                        float* ent = s_ent[bl][ent_rot(e_w, bl, kSeg)];
 #pragma unroll
-                        for (int k = 0; k < NV; k++) s_ent[bl][k][ent_rot(e_w, bl, kSeg)] = 0.f;
+                        for (int k = 0; k < NV; k += 2) {
+                            if (k + 1 < NV)
+                                *reinterpret_cast<float2*>(ent + k) = make_float2(0.f, 0.f);
+                            else
+                                ent[k] = 0.f;
+                        }
                     }
                     continue;
                 }
@@ -778,16 +788,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     }
                     bdot = __builtin_fmaf(fac, cvc, bdot);
                 }
+                float sv[NV];
 #pragma unroll
-                for (int k = 0; k < NV; k++) {
-                    const float v = group_sum4(gv[0][k], gv[1][k], gv[2][k], gv[3][k]);
-                    if (e_w >= 0) s_ent[bl][k][ent_rot(e_w, bl, kSeg)] = v;  // plain store: one writer per (block, entry)
+                for (int k = 0; k < NV; k++) sv[k] = group_sum4(gv[0][k], gv[1][k], gv[2][k], gv[3][k]);
+                if (e_w >= 0) {  // plain stores: one writer per (block, entry)
+                    float* ent = s_ent[bl][ent_rot(e_w, bl, kSeg)];
+#pragma unroll
+                    for (int k = 0; k < NV; k += 2) {
+                        if (k + 1 < NV)
+                            *reinterpret_cast<float2*>(ent + k) = make_float2(sv[k], sv[k + 1]);
+                        else
+                            ent[k] = sv[k];
+                    }
                 }
             }
             __syncthreads();
             // the segment's totals: thread t sums slot s0 + t's entries over the blocks it reaches, all
             // components at once (s1 - s0 <= kThreads). (Components shared out over 2, 3, 4 or 8 threads
-            // per slot measured slower: each thread walks the slot's blocks again.)
+            // per slot measured slower: each thread walks the slot's blocks again; so did slots dealt to
+            // the four waves in turn, which spreads the same issue over four waves instead of one or two.)
             if (tid < s1 - s0) {
                 const int slot = s0 + tid;
                 uint32_t m = static_cast<uint32_t>(s_bm[slot]);
@@ -798,9 +817,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4
                     while (m) {
                         const int b2 = __builtin_ctz(m);
                         m &= m - 1u;
-                        const int e2 = s_epos[slot][b2];  // the slot's entry in the block's row
+                        const float* ent = s_ent[b2][s_epos[slot][b2]];  // the slot's entry in the block's row
 #pragma unroll
-                        for (int k = 0; k < NV; k++) v[k] += s_ent[b2][k][e2];
+                        for (int k = 0; k < NV; k += 2) {
+                            if (k + 1 < NV) {
+                                const float2 x = *reinterpret_cast<const float2*>(ent + k);
+                                v[k] += x.x;
+                                v[k + 1] += x.y;
+                            } else {
+                                v[k] += ent[k];
+                            }
+                        }
                     }
                     if (!ABSGRAD) {
                         // sum_p gw (a dx + b dy, b dx + c dy); the moments of gw times -opacity are those of
