@@ -140,29 +140,37 @@ constexpr uint32_t kPadRecord = kThreads * sizeof(float4);
 // Per-block Gaussian lists of a batch: s_list[bl][0 .. s_len[bl]) = the LDS byte offsets (slot * 16) of
 // the batch-local slots t (in increasing order) whose mask has bit bl, padded to a multiple of four
 // entries with kPadRecord. All 256 threads call it; thread t passes Gaussian t's mask (0 for slots past
-// the batch). Ends with a barrier.
+// the batch). Ends with a barrier. Each block's ballot is taken once; lane bl < 16 then holds the
+// block's offset for the wave (the counts of the waves before it), and a lane's place among the wave's
+// lanes with the bit is its count of them below it (mbcnt).
 __device__ __forceinline__ void build_block_lists(uint32_t m, uint16_t (*s_list)[kListRow], int (*s_bc)[4],
                                                   int* s_len) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    unsigned long long bal[kBlocks];
+    int cnt = 0;  // lane bl < 16: the wave's count for block bl
 #pragma unroll
     for (int bl = 0; bl < kBlocks; bl++) {
-        const unsigned long long bal = __ballot((m >> bl) & 1u);
-        if (lane == 0) s_bc[bl][wave] = __popcll(bal);
+        bal[bl] = __ballot((m >> bl) & 1u);
+        cnt = lane == bl ? __popcll(bal[bl]) : cnt;
     }
+    if (lane < kBlocks) s_bc[lane][wave] = cnt;
     __syncthreads();
+    int off = 0;  // lane bl < 16: where the wave's entries of block bl start
+    if (lane < kBlocks) {
+        const int4 c = *reinterpret_cast<const int4*>(s_bc[lane]);
+        off = (wave > 0 ? c.x : 0) + (wave > 1 ? c.y : 0) + (wave > 2 ? c.z : 0);
+        if (wave == 0) {  // the list's length and padding
+            const int len = c.x + c.y + c.z + c.w;
+            s_len[lane] = len;
+            for (int q = len; q < ((len + 3) & ~3); q++) s_list[lane][q] = static_cast<uint16_t>(kPadRecord);
+        }
+    }
 #pragma unroll
     for (int bl = 0; bl < kBlocks; bl++) {
-        const unsigned long long bal = __ballot((m >> bl) & 1u);
-        int off = 0;
-#pragma unroll
-        for (int sw = 0; sw < 4; sw++) off += sw < wave ? s_bc[bl][sw] : 0;
-        if ((m >> bl) & 1u) s_list[bl][off + __popcll(bal & below)] = static_cast<uint16_t>(tid * sizeof(float4));
-    }
-    if (tid < kBlocks) {
-        const int len = s_bc[tid][0] + s_bc[tid][1] + s_bc[tid][2] + s_bc[tid][3];
-        s_len[tid] = len;
-        for (int q = len; q < ((len + 3) & ~3); q++) s_list[tid][q] = static_cast<uint16_t>(kPadRecord);
+        const int base = __builtin_amdgcn_readlane(off, bl);
+        const int rank = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[bl] >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[bl]), 0u)));
+        if ((m >> bl) & 1u) s_list[bl][base + rank] = static_cast<uint16_t>(tid * sizeof(float4));
     }
     __syncthreads();
 }
@@ -181,7 +189,7 @@ __global__ void __launch_bounds__(kThreads) k_raster_fwd(RasterArgs a, float* __
     __shared__ float4 s_con[kThreads + 1];
     __shared__ float4 s_rgb[kThreads + 1];
     __shared__ __align__(16) uint16_t s_list[kBlocks][kListRow];
-    __shared__ int s_bc[kBlocks][4];
+    __shared__ __align__(16) int s_bc[kBlocks][4];
     __shared__ int s_len[kBlocks];
     __shared__ unsigned long long s_gen[kThreads / 64];  // per wave: the batch's splats past the polynomial's range
     const int n_tiles = a.tile_width * a.tile_height;
