@@ -212,18 +212,34 @@ __global__ void __launch_bounds__(256) k_ssim_fwd3(const float* __restrict__ img
     const int oy = blockIdx.y * T, ox = blockIdx.x * T;
     const int tid = threadIdx.y * T + threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    for (int k = tid; k < A * A * C3; k += 256) {
-        const int ay = k / (A * C3), rem = k % (A * C3);
-        const int ax = rem / C3, c = rem % C3;
-        const int y = oy + ay, x = ox + ax;
-        float a = 0.f, b = 0.f;
-        if (y < H && x < W) {
-            const size_t off = ihwc(img, y, x, c, H, W, C3);
-            a = img1[off];
-            b = img2[off];
+    {
+        // every load of the apron issued before the first LDS store: one wait for all of them
+        constexpr int kN = A * A * C3, kIt = (kN + 255) / 256;
+        float va[kIt], vb[kIt];
+#pragma unroll
+        for (int it = 0; it < kIt; it++) {
+            const int k = tid + 256 * it;
+            const int ay = k / (A * C3), rem = k % (A * C3);
+            const int ax = rem / C3, c = rem % C3;
+            const int y = oy + ay, x = ox + ax;
+            va[it] = 0.f;
+            vb[it] = 0.f;
+            if (k < kN && y < H && x < W) {
+                const size_t off = ihwc(img, y, x, c, H, W, C3);
+                va[it] = img1[off];
+                vb[it] = img2[off];
+            }
         }
-        sx[c][ay][ax] = a;
-        sy[c][ay][ax] = b;
+#pragma unroll
+        for (int it = 0; it < kIt; it++) {
+            const int k = tid + 256 * it;
+            if (k < kN) {
+                const int ay = k / (A * C3), rem = k % (A * C3);
+                const int ax = rem / C3, c = rem % C3;
+                sx[c][ay][ax] = va[it];
+                sy[c][ay][ax] = vb[it];
+            }
+        }
     }
     // Register-blocked passes. Horizontal: a task is one row and two adjacent columns (12 inputs read
     // once); half-wave h of wave w takes column pair 2w + h over the 26 rows (odd input row stride 27:
@@ -354,20 +370,37 @@ __global__ void __launch_bounds__(256) k_ssim_bwd3(const float* __restrict__ img
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tx = tid & 15, rg = vert_rg(tid);
     const int qx = ox + tx;
-    for (int k = tid; k < AH3 * AW3 * C3; k += 256) {
-        const int ay = k / (AW3 * C3), rem = k - ay * (AW3 * C3);
-        const int ax = rem / C3, c = rem - ax * C3;
-        const int y = oy + ay - 10, x = ox + ax - 10;
-        float a = 0.f, b = 0.f, e = 0.f;
-        if (y >= 0 && y < mh && x >= 0 && x < mw) {
-            const size_t off = ihwc(img, y, x, c, mh, mw, C3);
-            a = cmu[off];
-            b = csg[off];
-            e = ccr[off];
+    {
+        // every load of the apron issued before the first LDS store: one wait for all of them
+        constexpr int kN = AH3 * AW3 * C3, kIt = (kN + 255) / 256;
+        float va[kIt], vb[kIt], ve[kIt];
+#pragma unroll
+        for (int it = 0; it < kIt; it++) {
+            const int k = tid + 256 * it;
+            const int ay = k / (AW3 * C3), rem = k - ay * (AW3 * C3);
+            const int ax = rem / C3, c = rem - ax * C3;
+            const int y = oy + ay - 10, x = ox + ax - 10;
+            va[it] = 0.f;
+            vb[it] = 0.f;
+            ve[it] = 0.f;
+            if (k < kN && y >= 0 && y < mh && x >= 0 && x < mw) {
+                const size_t off = ihwc(img, y, x, c, mh, mw, C3);
+                va[it] = cmu[off];
+                vb[it] = csg[off];
+                ve[it] = ccr[off];
+            }
         }
-        d[0][c][ay][ax] = a;
-        d[1][c][ay][ax] = b;
-        d[2][c][ay][ax] = e;
+#pragma unroll
+        for (int it = 0; it < kIt; it++) {
+            const int k = tid + 256 * it;
+            if (k < kN) {
+                const int ay = k / (AW3 * C3), rem = k - ay * (AW3 * C3);
+                const int ax = rem / C3, c = rem - ax * C3;
+                d[0][c][ay][ax] = va[it];
+                d[1][c][ay][ax] = vb[it];
+                d[2][c][ay][ax] = ve[it];
+            }
+        }
     }
     // the two output pixels' inputs, all three channels (whole interleaved pixels)
     float xs[2][C3], ys[2][C3], vout[2][C3];
