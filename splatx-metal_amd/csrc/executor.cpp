@@ -345,8 +345,9 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         const int32_t* order = e->emit_list.p;
         if (!index_first) {
             sxk::step_depth_keys(c, e->splats.p, e->emit_list.p, n_emit, e->dkey_a.p, e->order_a.p, s);
+            // (the step's sorts never wait on another workgroup: they cannot give up halfway through a step)
             const int wd = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, c.count, 32,
-                                           e->sort_scratch.p, s, true, n_emit_i);
+                                           e->sort_scratch.p, s, true, n_emit_i, true);
             if (wd < 0) throw std::runtime_error(std::string(what) + ": arena too large for a device-count depth sort");
             order = wd ? e->order_b.p : e->order_a.p;
             e->mark("depth_sort");
@@ -367,7 +368,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
-                                              e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b);
+                                              e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         } else {
@@ -376,7 +377,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
-                                              e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b);
+                                              e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);
             e->mark("sort");
             sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         }

@@ -838,10 +838,13 @@ static_assert(kHeaderWords * sizeof(uint32_t) % 64 == 0, "the count matrix after
 // through the passes like the values (pass p writes side_x[p & 1]); the three-launch path, whose
 // scatter does not carry it, gathers it once after the sort through the values, which must then be
 // the input positions (src_v null).
+// no_wait: reduce-then-scan at every size below 2^30 keys (no workgroup ever waits on another, so the
+// sort cannot give up; the onesweep passes below 16 tiles wait on their predecessors with a bounded
+// spin and set the error word if it runs out).
 template <class K>
 int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32_t* const side_v[2], int64_t n,
                  uint32_t key_bits, void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev,
-                 const uint32_t* src_x = nullptr, uint32_t* const* side_x = nullptr) {
+                 const uint32_t* src_x = nullptr, uint32_t* const* side_x = nullptr, bool no_wait = false) {
     uint32_t* totals = static_cast<uint32_t*>(scratch);
     uint32_t* bases = totals + kMaxPasses * kBins;
     uint32_t* counters = bases + kMaxPasses * kBins;
@@ -862,7 +865,7 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
     uint32_t* status_b = hist + hist_n;
     const K* kin = src_k;
     const int32_t* vin = src_v;
-    if (n < (int64_t{1} << 30) && tiles >= kRtsMinTiles) {  // reduce-then-scan (see k_rs_count); no histogram kernel
+    if (n < (int64_t{1} << 30) && (tiles >= kRtsMinTiles || no_wait)) {  // reduce-then-scan (see k_rs_count)
         // (the digit totals are not used here; the first count kernel clears the error word)
         uint32_t* cnt = hist;       // (mask + 1) x tiles counts, then their starts
         uint32_t* sums = status_b;  // the scan's chunk sums
@@ -946,12 +949,12 @@ int radix_sort_t(const K* src_k, const int32_t* src_v, K* const side_k[2], int32
 template <class K>
 int radix_sort_ab(K* keys_a, int32_t* vals_a, K* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
                   void* scratch, bool clear_err, hipStream_t s, const int64_t* n_dev, bool index_values = false,
-                  uint32_t* x_a = nullptr, uint32_t* x_b = nullptr) {
+                  uint32_t* x_a = nullptr, uint32_t* x_b = nullptr, bool no_wait = false) {
     K* const sk[2] = {keys_b, keys_a};
     int32_t* const sv[2] = {vals_b, vals_a};
     uint32_t* const sx[2] = {x_b, x_a};
     const int passes = radix_sort_t<K>(keys_a, index_values ? nullptr : vals_a, sk, sv, n, key_bits, scratch,
-                                       clear_err, s, n_dev, x_a, x_a ? sx : nullptr);
+                                       clear_err, s, n_dev, x_a, x_a ? sx : nullptr, no_wait);
     return passes < 0 ? -1 : (passes & 1);
 }
 
@@ -1210,8 +1213,9 @@ int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* val
 }
 
 int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
-               void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev) {
-    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev);
+               void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev, bool no_wait) {
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, false, nullptr,
+                         nullptr, no_wait);
 }
 
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n, uint32_t key_bits,
@@ -1221,14 +1225,16 @@ int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* val
 
 int radix_sort_positions(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
                          uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev,
-                         uint32_t* x_a, uint32_t* x_b) {
-    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true, x_a, x_b);
+                         uint32_t* x_a, uint32_t* x_b, bool no_wait) {
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true, x_a, x_b,
+                         no_wait);
 }
 
 int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
                          uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err, const int64_t* n_dev,
-                         uint32_t* x_a, uint32_t* x_b) {
-    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true, x_a, x_b);
+                         uint32_t* x_a, uint32_t* x_b, bool no_wait) {
+    return radix_sort_ab(keys_a, vals_a, keys_b, vals_b, n, key_bits, scratch, clear_err, s, n_dev, true, x_a, x_b,
+                         no_wait);
 }
 
 constexpr int kDepthSortRounds = 8;

@@ -72,14 +72,17 @@ void scan_i32_i64(const int32_t* in, int64_t* out, int64_t n, void* scratch, hip
 // lands in keys_a/vals_a when the pass count is even, else in keys_b/vals_b; returns 0 or 1
 // accordingly. The scratch needs sort_scratch_bytes(n) bytes for n keys. With n_dev the key count is
 // read on the device from *n_dev (<= n, which then only sizes the grids; n < 2^30, else -1 is
-// returned and nothing is launched): the launches no longer depend on the count.
+// returned and nothing is launched): the launches no longer depend on the count. no_wait (u32 keys and
+// the position sorts): every pass counts its tiles' digits and scans the counts (reduce-then-scan) at
+// any size, so no workgroup waits on another and the sort cannot give up (below 16 tiles of 4096 keys
+// the default onesweep passes wait on their predecessors with a bounded spin).
 size_t sort_scratch_bytes(int64_t n);
 int radix_sort(uint64_t* keys_a, int32_t* vals_a, uint64_t* keys_b, int32_t* vals_b, int64_t n,
                uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
                const int64_t* n_dev = nullptr);
 int radix_sort(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
                uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
-               const int64_t* n_dev = nullptr);
+               const int64_t* n_dev = nullptr, bool no_wait = false);
 int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
                uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
                const int64_t* n_dev = nullptr);
@@ -89,10 +92,12 @@ int radix_sort(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* val
 // count, the output).
 int radix_sort_positions(uint16_t* keys_a, int32_t* vals_a, uint16_t* keys_b, int32_t* vals_b, int64_t n,
                          uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
-                         const int64_t* n_dev = nullptr, uint32_t* x_a = nullptr, uint32_t* x_b = nullptr);
+                         const int64_t* n_dev = nullptr, uint32_t* x_a = nullptr, uint32_t* x_b = nullptr,
+                         bool no_wait = false);
 int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, int32_t* vals_b, int64_t n,
                          uint32_t key_bits, void* scratch, hipStream_t s, bool clear_err = true,
-                         const int64_t* n_dev = nullptr, uint32_t* x_a = nullptr, uint32_t* x_b = nullptr);
+                         const int64_t* n_dev = nullptr, uint32_t* x_a = nullptr, uint32_t* x_b = nullptr,
+                         bool no_wait = false);
 // The same sort of n u64 keys from read-only inputs into keys_out/vals_out, with keys_tmp/vals_tmp as
 // the second ping-pong side (n > 0, key_bits in 1..64, the onesweep range n < 2^30). No buffer may
 // alias another.
