@@ -59,8 +59,9 @@ __device__ __forceinline__ float exp_neg_poly(float sigma) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    const int k = static_cast<int>(kf);
-    return p * __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
+    // p * 2^k with k in [-125, 0]: the product is a normal float, so scaling the exponent (v_ldexp_f32)
+    // gives the same bits as multiplying by 2^k, in one instruction instead of three
+    return __builtin_amdgcn_ldexpf(p, static_cast<int>(kf));
 }
 
 __device__ __forceinline__ float sigma_of(float ca, float cb, float cc, float dx, float dy) {
