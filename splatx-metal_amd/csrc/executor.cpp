@@ -385,14 +385,16 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         if (e->debug_sort_error) sxk::step_set_word(sxk::sort_error_flag(e->sort_scratch.p), 1u, s);
         flat = which ? e->vals_b.p : e->vals_a.p;
         e->mark("offsets");
-        sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev, e->max_tile.p);
         if (index_first) {
             // the sorted tile keys are spent (the offsets are built): both key buffers and the other
-            // value buffer are the scratch of tiles too large for LDS
-            sxk::tile_depth_sort(e->offsets.p, n_tiles, n_host, n_dev, e->tile_order.p, flat, which ? edepth_b : edepth,
+            // value buffer are the scratch of tiles too large for LDS. The rasterisers' tile order comes
+            // from one more workgroup of the same launch.
+            sxk::tile_depth_sort(e->offsets.p, n_tiles, n_host, n_dev, nullptr, flat, which ? edepth_b : edepth,
                                  reinterpret_cast<uint32_t*>(e->keys_a.p), reinterpret_cast<uint32_t*>(e->keys_b.p),
-                                 which ? e->vals_a.p : e->vals_b.p, s);
+                                 which ? e->vals_a.p : e->vals_b.p, s, e->tile_order.p, e->max_tile.p);
             e->mark("tile_depth_sort");
+        } else {
+            sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev, e->max_tile.p);
         }
         sxk::RasterArgs ra{};
         ra.splats = e->splats.p;

@@ -29,6 +29,7 @@
 
 #include "sx_dev.h"
 #include "sx_kernels.h"
+#include "sx_order.h"
 
 namespace sxk {
 namespace {
@@ -1088,94 +1089,14 @@ namespace {
 // wave's lanes with the same bucket are grouped (one ballot per bucket bit) and one leader lane adds
 // the group's size: the LDS adds then never collide within a wave. The order within a bucket is
 // arbitrary (the order is only the rasterisers' schedule).
-__device__ __forceinline__ uint64_t same_byte_lanes(uint32_t b, bool valid) {
-    uint64_t match = __ballot(valid);
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const bool bit = (b >> k) & 1u;
-        const uint64_t bal = __ballot(bit);
-        match &= bit ? bal : ~bal;
-    }
-    return match;
-}
-
-constexpr int kOrderKeep = 8;  // tile counts a thread of k_tile_order keeps (8192 tiles: 1920x1080)
+// One workgroup of 1024 threads: the order, and the largest count into *max_count when given.
 __global__ void __launch_bounds__(1024) k_tile_order(const int32_t* __restrict__ offsets, int n_tiles,
                                                      int64_t n_isects, int32_t* __restrict__ order,
                                                      const int64_t* __restrict__ n_isects_dev,
                                                      uint32_t* __restrict__ max_count) {
-    __shared__ uint32_t s_hist[256];
-    __shared__ uint32_t s_wtot[4];
-    __shared__ uint32_t s_max;
+    __shared__ OrderScratch sc;
     if (n_isects_dev) n_isects = *n_isects_dev;
-    const int t0 = threadIdx.x, lane = t0 & 63;
-    if (t0 < 256) s_hist[t0] = 0;
-    if (t0 == 0) s_max = 0;
-    __syncthreads();
-    auto count_of = [&](int t) -> uint32_t {
-        const int64_t e = t + 1 < n_tiles ? offsets[t + 1] : n_isects;
-        return static_cast<uint32_t>(e - offsets[t]);
-    };
-    // the counts of the thread's first kOrderKeep tiles stay in registers for the two later passes
-    // (one round of loads instead of three); tiles past 1024 kOrderKeep are loaded again
-    uint32_t kept[kOrderKeep];
-    uint32_t mx = 0;
-#pragma unroll
-    for (int r = 0; r < kOrderKeep; r++) {
-        const int t = t0 + 1024 * r;
-        kept[r] = t < n_tiles ? count_of(t) : 0u;
-        mx = max(mx, kept[r]);
-    }
-    for (int t = t0 + 1024 * kOrderKeep; t < n_tiles; t += 1024) mx = max(mx, count_of(t));
-    auto count_at = [&](int r, int t) -> uint32_t { return r < kOrderKeep ? kept[r] : count_of(t); };
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), o, 64)));
-    if (lane == 0) atomicMax(&s_max, mx);
-    __syncthreads();
-    int shift = 0;
-    while ((s_max >> shift) >= 256u) shift++;
-    if (max_count && t0 == 0) *max_count = s_max;
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    // rounds are uniform over the workgroup (every thread runs ceil(n_tiles / 1024) of them)
-    for (int t1 = 0, r = 0; t1 < n_tiles; t1 += 1024, r++) {
-        const int t = t1 + t0;
-        const bool valid = t < n_tiles;
-        const uint32_t b = valid ? 255u - (count_at(r, t) >> shift) : 0u;
-        const uint64_t m = same_byte_lanes(b, valid);
-        if (valid && (m & below) == 0) atomicAdd(&s_hist[b], static_cast<uint32_t>(__popcll(m)));
-    }
-    __syncthreads();
-    // exclusive prefix over the 256 buckets: waves 0-3 scan them, then add the lower waves' totals
-    uint32_t hc = 0, hx = 0;
-    if (t0 < 256) {  // whole waves
-        hc = s_hist[t0];
-        hx = hc;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t y = static_cast<uint32_t>(__shfl_up(static_cast<int>(hx), o, 64));
-            if (lane >= o) hx += y;
-        }
-        if (lane == 63) s_wtot[t0 >> 6] = hx;
-    }
-    __syncthreads();
-    if (t0 < 256) {
-        uint32_t pre = 0;
-#pragma unroll
-        for (int w = 0; w < 4; w++) pre += w < (t0 >> 6) ? s_wtot[w] : 0u;
-        s_hist[t0] = pre + hx - hc;
-    }
-    __syncthreads();
-    for (int t1 = 0, r = 0; t1 < n_tiles; t1 += 1024, r++) {
-        const int t = t1 + t0;
-        const bool valid = t < n_tiles;
-        const uint32_t b = valid ? 255u - (count_at(r, t) >> shift) : 0u;
-        const uint64_t m = same_byte_lanes(b, valid);
-        const int leader = m ? static_cast<int>(__builtin_ctzll(m)) : 0;
-        uint32_t base = 0;
-        if (valid && lane == leader) base = atomicAdd(&s_hist[b], static_cast<uint32_t>(__popcll(m)));
-        base = static_cast<uint32_t>(__shfl(static_cast<int>(base), leader, 64));
-        if (valid) order[base + static_cast<uint32_t>(__popcll(m & below))] = t;
-    }
+    tile_order_block<1024, 8>(offsets, n_tiles, n_isects, order, max_count, &sc);  // 8192 tiles from registers
 }
 }  // namespace
 

@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include "sx_kernels.h"
+#include "sx_order.h"
 
 namespace sxk {
 namespace {
@@ -1039,6 +1040,9 @@ __device__ __forceinline__ uint32_t wave_starts(uint32_t (*s_woff)[kBins], uint3
 // past 1024 entries with 16 rounds (twice the LDS) left its few long tiles running alone after
 // the small ones, and 4 rounds send more tiles through global scratch. (One wave per small tile, with
 // no workgroup barriers, measured slower: its ranking rounds wait on LDS one after another.)
+// order_out (optional): workgroup 0 writes the rasterisers' tile order there instead (and the largest
+// tile's count into *max_count), beside the sorting workgroups, which then take tile blockIdx.x - 1: the
+// per-tile sorts gain nothing from running heaviest first, and the order costs no launch of its own.
 template <int RMAX>
 __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles,
                                                               int32_t n_isects, const int64_t* __restrict__ n_dev,
@@ -1046,7 +1050,8 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
                                                               int32_t* __restrict__ vals,
                                                               const uint32_t* __restrict__ sdepth,
                                                               uint32_t* __restrict__ sk0, uint32_t* __restrict__ sk1,
-                                                              int32_t* __restrict__ sv) {
+                                                              int32_t* __restrict__ sv, int32_t* __restrict__ order_out,
+                                                              uint32_t* __restrict__ max_count) {
     constexpr int kCap = kWaves * 64 * RMAX;
     __shared__ uint32_t s_key[kCap];
     __shared__ int32_t s_val[kCap];
@@ -1055,8 +1060,15 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
     __shared__ uint32_t s_wave[kWaves];
     __shared__ uint32_t s_and[kWaves], s_or[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = tile_order ? tile_order[blockIdx.x] : static_cast<int>(blockIdx.x);
     const int32_t n_all = n_dev ? static_cast<int32_t>(*n_dev) : n_isects;
+    if (order_out && blockIdx.x == 0) {  // uniform
+        static_assert(sizeof(OrderScratch) <= sizeof(s_woff), "the order's scratch fits in s_woff");
+        tile_order_block<kThreads, 8>(offsets, n_tiles, n_all, order_out, max_count,
+                                      reinterpret_cast<OrderScratch*>(&s_woff[0][0]));
+        return;
+    }
+    const int bx = order_out ? static_cast<int>(blockIdx.x) - 1 : static_cast<int>(blockIdx.x);
+    const int t = tile_order ? tile_order[bx] : bx;
     const int32_t start = offsets[t];
     const int32_t nt = (t + 1 < n_tiles ? offsets[t + 1] : n_all) - start;
     if (nt <= 1) return;  // uniform
@@ -1241,11 +1253,12 @@ constexpr int kDepthSortRounds = 8;
 
 void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
                      const int32_t* tile_order, int32_t* vals, const uint32_t* sdepth, uint32_t* scratch_k0,
-                     uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s) {
-    if (n_tiles <= 0 || (!n_dev && n_isects <= 1)) return;
-    hipLaunchKernelGGL(k_tile_depth_sort<kDepthSortRounds>, dim3(n_tiles), dim3(kThreads), 0, s, offsets, n_tiles,
-                       static_cast<int32_t>(n_isects), n_dev, tile_order, vals, sdepth, scratch_k0, scratch_k1,
-                       scratch_v);
+                     uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s, int32_t* order_out,
+                     uint32_t* max_count) {
+    if (n_tiles <= 0 || (!order_out && !n_dev && n_isects <= 1)) return;
+    hipLaunchKernelGGL(k_tile_depth_sort<kDepthSortRounds>, dim3(n_tiles + (order_out ? 1 : 0)), dim3(kThreads), 0,
+                       s, offsets, n_tiles, static_cast<int32_t>(n_isects), n_dev, tile_order, vals, sdepth,
+                       scratch_k0, scratch_k1, scratch_v, order_out, max_count);
 }
 
 void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_out, int32_t* vals_out,

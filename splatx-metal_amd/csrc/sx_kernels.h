@@ -114,10 +114,13 @@ uint32_t* sort_error_flag(void* scratch);
 // tile sort carried them along, so a tile reads its keys in sequence). The count is *n_dev when set,
 // else n_isects; tile_order (optional) is the order the workgroups take the tiles in. Tiles of more
 // than 2048 entries pass through scratch_k0 / scratch_k1 / scratch_v (each indexed like vals, at least
-// the count long; none of them may overlap sdepth).
+// the count long; none of them may overlap sdepth). order_out (optional): the launch also writes the
+// rasterisers' tile order (raster_tile_order's, from the same offsets) there and the largest tile's
+// count into *max_count, from one extra workgroup; the tiles are then sorted in index order.
 void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
                      const int32_t* tile_order, int32_t* vals, const uint32_t* sdepth, uint32_t* scratch_k0,
-                     uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s);
+                     uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s, int32_t* order_out = nullptr,
+                     uint32_t* max_count = nullptr);
 
 // offsets[I*n_tiles] from sorted keys; n_isects > 0.
 // key_shift: position of the (image, tile) id in the key (32 for the isect_tiles encoding)
