@@ -400,17 +400,24 @@ __global__ void __launch_bounds__(kThreads) k_os_scan(const uint32_t* __restrict
 }
 
 // Lanes of the wave (among `valid_mask`) whose digit, the low NB bits of x, equals this lane's: one
-// ballot per bit, each lane collecting the lanes that differ from it in that bit.
+// ballot per bit, each lane collecting the lanes that differ from it in that bit. Per bit: v_bfe_i32
+// (the bit as 0 or ~0; written as asm, as the compiler otherwise makes a shift pair of it), the ballot's
+// compare, and mis |= ballot ^ bit as one v_bitop3 per half (truth table 0xF6: src0 | (src1 ^ src2)).
+template <int B, int NB>
+__device__ __forceinline__ void digit_mismatch(uint32_t x, uint32_t& mis_lo, uint32_t& mis_hi) {
+    if constexpr (B < NB) {
+        uint32_t m;
+        asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(m) : "v"(x), "n"(B));
+        const uint64_t bal = __ballot(m != 0u);
+        mis_lo = __builtin_amdgcn_bitop3_b32(mis_lo, static_cast<uint32_t>(bal), m, 0xf6);
+        mis_hi = __builtin_amdgcn_bitop3_b32(mis_hi, static_cast<uint32_t>(bal >> 32), m, 0xf6);
+        digit_mismatch<B + 1, NB>(x, mis_lo, mis_hi);
+    }
+}
 template <int NB>
 __device__ __forceinline__ uint64_t digit_match_bits(uint32_t x, uint64_t valid_mask) {
     uint32_t mis_lo = 0u, mis_hi = 0u;
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        const uint32_t m = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(x), b, 1));  // 0 or ~0
-        const uint64_t bal = __ballot(m != 0u);
-        mis_lo |= static_cast<uint32_t>(bal) ^ m;
-        mis_hi |= static_cast<uint32_t>(bal >> 32) ^ m;
-    }
+    digit_mismatch<0, NB>(x, mis_lo, mis_hi);
     return valid_mask & ~((static_cast<uint64_t>(mis_hi) << 32) | mis_lo);
 }
 
