@@ -154,6 +154,36 @@ def test_sort_reduce_then_scan_matches_stable_sort(gpu, n, bits):
     assert np.array_equal(ks, rk) and np.array_equal(vs, rv)
 
 
+def _run_keys(n, key_bits, seed):
+    """Keys in runs, the way an emit lays out tile ids: runs of 1-40 keys that repeat a key or step by
+    2^s (s at a digit boundary or not), so some pass sees runs of equal digits and runs of consecutive
+    digits that wrap past the last digit into the next one."""
+    r = inputs.rng(seed)
+    top = np.uint64(2**min(key_bits, 63) - 1) if key_bits < 64 else np.uint64(2**64 - 1)
+    keys = np.empty(n, np.uint64)
+    i = 0
+    while i < n:
+        length = int(r.integers(1, 41))
+        start = np.uint64(r.integers(0, 2**min(key_bits, 62)))
+        s = int(r.choice([0, 0, 1, 5, 6, 7, 8, 13, 16, 24, 32, 40])) % max(1, key_bits)
+        step = np.uint64(0) if r.random() < 0.3 else np.uint64(1) << np.uint64(s)
+        k = min(length, n - i)
+        keys[i:i + k] = (start + step * np.arange(k, dtype=np.uint64)) & top
+        i += k
+    return keys, np.arange(n, dtype=np.int32)
+
+
+# Keys laid out in runs (an emit's tile ids along a row, repeated keys): the digit counts add a thread's
+# runs of equal digits at once, and the passes see runs of consecutive digits wrapping past the last
+# digit, for digit ranges from 16 (the last pass of 36 bits) to 256.
+@pytest.mark.parametrize("n,bits", [(1_048_577, 13), (1_048_576, 36), (2_000_003, 45), (1_100_000, 64)])
+def test_sort_reduce_then_scan_runs(gpu, n, bits):
+    keys, vals = _run_keys(n, bits, seed=n + bits)
+    ks, vs = gpu.sort_isect(keys, vals, bits)
+    rk, rv = inputs.stable_sort_ref(keys, vals)
+    assert np.array_equal(ks, rk) and np.array_equal(vs, rv)
+
+
 def test_sort_reduce_then_scan_equal_keys(gpu):
     n = 8_500_000
     keys = np.full(n, (np.uint64(5) << np.uint64(32)) | np.uint64(77), np.uint64)
