@@ -62,6 +62,11 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
         # every row's meta word and touched flag; visible: read params, both moments, grads (36 B) and
         # conic/comp/meta (20 B); write params+moments
         return 5.0 * n + v * (4.0 * pd * 3 + 36 + 20 + 4.0 * pd * 3)
+    if name == "update_preprocess":
+        # the previous step's postprocess and this step's preprocess in one pass: the postprocess's bytes
+        # and the preprocess's writes (radii + count 12 B per row, the 48-B record per visible one); the
+        # preprocess reads nothing again
+        return algorithmic_bytes("postprocess", n, v, i, px, sh_k, shape) + 12.0 * n + 48.0 * v
     if name == "raster_fwd":
         # the survey's per-unit figures: 40 B read per intersection (its sorted id and the splat's record),
         # 20 B written per pixel (colour, alpha, last id)

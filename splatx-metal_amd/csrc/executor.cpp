@@ -1,11 +1,13 @@
 // executor.cpp — the device-resident train-step executor (TrainStepExecutor, KernelBackend.h:386-392;
 // the reference's MetalTrainStepExecutor, MetalBackend.cpp:1628-2460).
 //
-// One HIP stream. A step is: preprocess -> block scan [sync 1: n_isects, stored into mapped host
-// memory; isect buffers grow 1.5x when needed] -> compaction -> emit -> radix sort -> offsets -> raster
-// fwd -> SSIM fwd -> SSIM bwd fused with the L1 gradient -> raster bwd -> gather -> postprocess (loss
-// reduction, then bwd chain + Adam + noise) [sync 2: the loss, stored the same way]. Everything after
-// sync 1 is a captured graph, queued before the host waits. Parameters, moments and the GT cache stay
+// One HIP stream. A step is: preprocess (with the previous step's parameter update: bwd chain + Adam +
+// noise, fused row by row) -> block scan [sync 1: n_isects, stored into mapped host memory; isect
+// buffers grow 1.5x when needed] -> compaction -> emit -> radix sort -> offsets -> raster fwd -> SSIM fwd
+// -> SSIM bwd fused with the L1 gradient -> raster bwd -> gather (its first workgroup reduces the loss)
+// [sync 2: the loss, stored the same way]. The step's own update waits for the next step's preprocess, or for anything
+// else that reads or writes the arena (flush_update). Everything after sync 1 is a captured graph,
+// queued before the host waits. Parameters, moments and the GT cache stay
 // in HBM; the arena is sized once for arena_rows and never reallocated.
 #include <hip/hip_runtime.h>
 
@@ -64,7 +66,8 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->tiles.alloc(R);
             e->cum.alloc(R);
             e->long_list.alloc(R);
-            e->long_count.alloc(1);
+            e->long_count.alloc(2);  // this step's long-range count, the previous step's
+            SXH_HIP(hipMemsetAsync(e->long_count.p, 0, 2 * sizeof(int32_t), e->b->stream));
             e->stamp.alloc(1);
             e->max_tile.alloc(1);
             SXH_HIP(hipMemsetAsync(e->stamp.p, 0, sizeof(uint32_t), b->stream));
@@ -108,6 +111,7 @@ static void sync_params(sxh_executor* e, const sxh_param_sync* s, bool up) {
     if (!s) invalid("TrainStepExecutor", "null sync");
     if (s->rows < 0 || s->rows > e->rows) invalid("TrainStepExecutor", "sync rows out of [0, arena_rows]");
     const int rows = static_cast<int>(s->rows);
+    sxh_detail::flush_update(e);  // (an upload overwrites rows the pending update would write later)
     if (rows == 0) return;
     hipStream_t st = e->b->stream;
     for (int g = 0; g < 6; g++) {
@@ -180,6 +184,8 @@ int32_t sxh_exec_get_raster_stats(sxh_executor* e, sxh_raster_stats* out) {
 int32_t sxh_exec_sync(sxh_executor* e) {
     return guarded([&] {
         if (!e) invalid("TrainStepExecutor", "null executor");
+        SXH_HIP(hipSetDevice(e->b->device));
+        sxh_detail::flush_update(e);  // the last step's parameter update is part of its work
         SXH_HIP(hipStreamSynchronize(e->b->stream));
     });
 }
@@ -210,7 +216,7 @@ int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out) {
 } // extern "C"
 
 // A sync point of the step: wait until a kernel has stored `seq` into the mapped word (sync 1: the
-// block scan, its counts then in place; sync 2: the postprocess's first workgroup, the loss). The
+// block scan, its counts then in place; sync 2: the gather's first workgroup, the loss). The
 // stream is polled now and then, so that an error or a stream that finished without the store ends
 // the wait instead of spinning forever.
 static void wait_count_word(volatile unsigned long long* word, unsigned long long seq, hipStream_t s,
@@ -227,6 +233,15 @@ static void wait_count_word(volatile unsigned long long* word, unsigned long lon
         }
         __builtin_ia32_pause();
     }
+}
+
+void sxh_detail::flush_update(sxh_executor* e) {
+    if (!e->update_pending) return;
+    e->update_pending = false;
+    // gated like the fused launch: the pending step's overflow word (n_vis word 4) and sort error word
+    sxk::step_postprocess(e->pending_c, e->arena(), e->splats.p, e->grads.p, e->touched.p, e->b->stream, e->n_vis.p + 4,
+                          e->sort_scratch.p ? sxk::sort_error_flag(e->sort_scratch.p) : nullptr);
+    SXH_HIP(hipGetLastError());
 }
 
 // The step proper. `render_to_dev` (device), when not null, receives a copy of the render.
@@ -287,13 +302,17 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     c.noise_offset = in->noise_offset;
     c.noise_scale = in->noise_scale;
     const sxk::Arena A = e->arena();
+    // the last training step's deferred update rides on this step's preprocess when both cover the same
+    // rows; a forward-only step (or another row count) applies it first
+    if (e->update_pending && (fwd_only || e->pending_c.count != c.count)) sxh_detail::flush_update(e);
 
     // ---- segment A: preprocess + counts -----------------------------------------------------------
     // `cap`: the intersection capacity segment B may assume; past it, segment B's counts read 0 and the
     // arena update is skipped (n_vis words 3 and 4), so a segment B launched before the count is known
     // leaves everything as it was and the step runs again on grown buffers
     // the step's read-back block: u64 visible, u64 intersections (stored by segment A's block scan), u32
-    // loss bits, sort error flag, largest tile (stored by the postprocess's first workgroup), u64 segment
+    // loss bits, sort error flag, largest tile, the previous step's long-range count (stored by the
+    // gather's first workgroup), u64 segment
     // A's sequence number (word 4, after the counts), u64 the loss's (word 5)
     volatile unsigned long long* const hc = static_cast<volatile unsigned long long*>(e->step_rb.p);
     volatile uint32_t* const hw = reinterpret_cast<volatile uint32_t*>(hc + 2);
@@ -303,10 +322,21 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         if (e->prof_stats)
             SXH_HIP(hipMemsetAsync(e->rstats.p, 0, sxk::kRasterStats * sizeof(unsigned long long), s));
         e->mark("start");
-        sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
-                             cap, static_cast<unsigned long long*>(e->step_rb.dev), seq,
-                             fwd_only ? sxk::StepClear{} : sxk::StepClear{e->touched.p, e->stamp.p, e->long_count.p}, s);
-        e->mark("preprocess");
+        const sxk::StepClear clr =
+            fwd_only ? sxk::StepClear{} : sxk::StepClear{e->touched.p, e->stamp.p, e->long_count.p, e->long_count.p + 1};
+        if (e->update_pending) {
+            // (taken once: an overflowed step that runs segment A again finds the update applied)
+            e->update_pending = false;
+            sxk::step_update_preprocess(e->pending_c, c, A, e->splats.p, e->grads.p, e->touched.p, e->n_vis.p + 4,
+                                        sxk::sort_error_flag(e->sort_scratch.p), e->radii.p, e->tiles.p,
+                                        e->vis_part.p, e->n_vis.p, e->blk_base.p, cap,
+                                        static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s);
+            e->mark("update_preprocess");
+        } else {
+            sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
+                                 cap, static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s);
+            e->mark("preprocess");
+        }
     };
     const float* gt = nullptr;
     auto upload_gt = [&]() {
@@ -318,9 +348,9 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             gt = e->gt_stage.p;
         }
     };
-    // the intersection count segment B reads (0 after an overflow), and the overflow word
+    // the intersection count segment B reads (0 after an overflow; the overflow word, n_vis word 4, gates
+    // the step's parameter update)
     const int64_t* n_isects_dev = reinterpret_cast<const int64_t*>(e->n_vis.p) + 3;
-    const unsigned long long* overflow_dev = e->n_vis.p + 4;
     int n_l1 = 0, n_ss = 0;
     int32_t* flat = e->vals_a.p;
     // index-first sorts each tile's list by depth in one workgroup: fast while the tiles stay small
@@ -417,7 +447,9 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         sxk::raster_fwd(ra, e->render.p, e->alpha.p, e->last_ids.p, s);
         e->mark("raster_fwd");
         // the loss words, then the launch's sequence number (word 5 of the block)
-        const sxk::StepReadback rb{sxk::sort_error_flag(e->sort_scratch.p), e->max_tile.p, e->long_count.p,
+        // (the long-range count reported is the previous training step's: this step's gather reports the
+        // words while its own ranges are still being counted)
+        const sxk::StepReadback rb{sxk::sort_error_flag(e->sort_scratch.p), e->max_tile.p, e->long_count.p + 1,
                                    reinterpret_cast<uint32_t*>(static_cast<unsigned long long*>(e->step_rb.dev) + 2),
                                    static_cast<unsigned long long*>(e->step_rb.dev) + 5, seq};
         if (fwd_only) {
@@ -445,14 +477,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
                                e->grads.p, e->part.p, e->stamp.p, e->touched.p};
         sxk::raster_bwd(ra, e->alpha.p, e->last_ids.p, e->v_render.p, e->v_alpha_zero.p, gg, s);
         e->mark("raster_bwd");
-        // long ranges reduced by the gather's own waves while the previous step had few (no second
-        // launch), queued for a wave each otherwise (measured: inline 41 -> 35 us at config 3, queued
-        // 94 us against 329 inline at config 5); either way the same sums
-        constexpr int64_t kInlineLongMax = 1024;
-        const bool inline_long = e->last_long >= 0 && e->last_long <= kInlineLongMax;
-        sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
-                                 e->long_list.p, e->long_count.p, s, n_emit_i, inline_long);
-        e->mark("gather");
+        // the step's loss and host words, reduced by the gather's first workgroup before its own ranges
         sxk::StepLoss loss{};
         loss.l1p = e->l1_part.p;
         loss.n_l1 = n_l1;
@@ -464,8 +489,16 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         loss.use_ssim = use_ssim ? 1 : 0;
         loss.out = e->loss_dev.p;
         loss.rb = rb;
-        sxk::step_postprocess(c, A, e->splats.p, e->grads.p, e->touched.p, s, overflow_dev, loss);
-        e->mark("postprocess");
+        // long ranges reduced by the gather's own waves while a recent step had few (no second launch;
+        // the count known when this step is queued is the one two steps back), queued for a wave each
+        // otherwise (measured: inline 41 -> 35 us at config 3, queued 94 us against 329 inline at
+        // config 5); either way the same sums
+        constexpr int64_t kInlineLongMax = 1024;
+        const bool inline_long = e->last_long >= 0 && e->last_long <= kInlineLongMax;
+        sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
+                                 e->long_list.p, e->long_count.p, s, n_emit_i, inline_long, &loss);
+        e->mark("gather");
+        // (the step's parameter update waits for the next step's preprocess, or a flush)
     };
     // Segment B as a hipGraph (captured while the GPU runs segment A; an executable graph per step kind
     // is updated in place while the step's shape stays the same), unless per-kernel profiling is on or
@@ -552,14 +585,19 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         }
         launch_tail();
     }
+    if (!fwd_only) {  // segment B is queued: its update is this step's pending one
+        e->update_pending = true;
+        e->pending_c = c;
+    }
     out->n_isects = n_isects;
     out->sort_key_bits = 32 + c.tile_n_bits;
     out->n_visible = static_cast<int64_t>(hc[0]);
     // ---- sync 2: loss (MetalBackend.cpp:2241-2261) ----------------------------------------------------
-    // The loss, the sort's error word and the largest tile's count are stored by the postprocess's first
-    // workgroup, with the step's sequence number after them: the host returns once it sees that number,
-    // while the postprocess may still run; everything later on the stream (the next step, a download, a
-    // refine) is ordered after it. A render read-back or profiling waits for the whole stream.
+    // The loss, the sort's error word and the largest tile's count are stored by the gather's first
+    // workgroup, with the step's sequence number after them: the host returns once it sees that
+    // number, while the gather may still run. The step's parameter update is applied by the next step's preprocess or by a flush before
+    // anything else reads or writes the arena (a download, a refine, a checkpoint, a sync). A render
+    // read-back or profiling waits for the whole stream.
     const auto t0 = std::chrono::steady_clock::now();
     if (!e->prof && !e->prof_stats && !render_to_dev && !out->render_colors)
         wait_count_word(hc + 5, seq, s, what);
@@ -571,7 +609,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     std::memcpy(&loss, &loss_bits, 4);
     out->loss = fwd_only ? 0.0f : loss;
     e->last_max_tile = n_isects > 0 ? static_cast<int64_t>(max_tile) : 0;
-    if (!fwd_only) e->last_long = static_cast<int64_t>(hw[3]);
+    if (!fwd_only) e->last_long = static_cast<int64_t>(hw[3]);  // the previous training step's count
     if (e->prof_stats) {
         unsigned long long st[sxk::kRasterStats];
         SXH_HIP(hipMemcpy(st, e->rstats.p, sizeof(st), hipMemcpyDeviceToHost));

@@ -29,6 +29,7 @@
 
 #include "sx_dev.h"
 #include "sx_kernels.h"
+#include "sx_loss.h"
 #include "sx_order.h"
 
 namespace sxk {
@@ -963,7 +964,9 @@ __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const i
                                                               int32_t* __restrict__ long_list,
                                                               int32_t* __restrict__ long_count,
                                                               const int64_t* __restrict__ count_dev,
-                                                              int inline_long) {
+                                                              int inline_long, StepLoss L) {
+    // the first workgroup (one wave) also reduces the step's loss, before its ranges (L.out null: none)
+    if (L.out && blockIdx.x == 0) loss_final_wave(L);
     __shared__ float s_rec[kGatherStage][kPartFloats];  // odd row stride: lanes on different rows, different banks
     __shared__ int32_t s_off[kGatherWave];              // each lane's first staged entry
     __shared__ int32_t s_src[kGatherWave];              // each lane's first entry in `part`
@@ -1073,11 +1076,11 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part, const uint32_t* stamp,
                          const uint8_t* touched, float4* grads, int32_t* long_list, int32_t* long_count,
-                         hipStream_t s, const int64_t* count_dev, bool inline_long) {
+                         hipStream_t s, const int64_t* count_dev, bool inline_long, const StepLoss* loss) {
     if (count <= 0) return;
     hipLaunchKernelGGL(k_gather_grads, dim3((count + kGatherWave - 1) / kGatherWave), dim3(kGatherWave), 0, s, count,
                        order, cum, part, stamp, touched, grads, long_list, long_count, count_dev,
-                       inline_long ? 1 : 0);
+                       inline_long ? 1 : 0, loss ? *loss : StepLoss{});
     if (!inline_long)
         hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, stamp, grads,
                            long_list, long_count);

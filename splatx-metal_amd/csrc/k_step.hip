@@ -1,7 +1,8 @@
 // k_step.hip — fused kernels of the device-resident training step (gfx950).
 //
 // The reference step (MetalBackend.cpp:1696-2264) runs ~95 launches; here the per-Gaussian work
-// is two kernels:
+// is two kernels, which a training step runs as one launch per step (the previous step's
+// postprocess fused with this step's preprocess, k_postprocess<NC, true>):
 //   preprocess  = train_exp + train_sigmoid + projection fwd + AA product + prep_sh + SH fwd (reading
 //                 sh0/shN directly, no coeffs assembly) + SH post-op + isect count, and the zeroing
 //                 of this Gaussian's gradient record;
@@ -15,6 +16,7 @@
 #include <stdexcept>
 
 #include "sx_dev_bwd.h"
+#include "sx_loss.h"
 #include "sx_philox.h"
 #include "sx_step.h"
 
@@ -57,78 +59,79 @@ __device__ __forceinline__ float adam_update(float* __restrict__ p, float* __res
 }
 
 
-// NC = the arena's SH coefficient count (1, 4, 9 or 16): the coefficients of a visible Gaussian are
-// loaded into registers in one burst before the evaluation
+// The preprocess of row i from its parameters (means, quaternion, log scales, logit): projection, colour
+// and tile count; stores the splat record and the radii, returns the tile count (0 for a row that is not
+// visible; vis = visible). co: the row's SH coefficients when co_ready, else loaded here for a visible
+// row (NC = the arena's coefficient count, 1, 4, 9 or 16, a compile-time bound that keeps them in
+// registers).
 template <int NC>
-__global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, float4* __restrict__ splats,
-                                                       int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
-                                                       uint32_t* __restrict__ vis_part, StepClear clr) {
-    __shared__ uint32_t s_vis[kBlock / 64], s_isect[kBlock / 64], s_emit[kBlock / 64];
-    uint32_t n_tiles_sum = 0;  // this lane's tile count; summed per block below
-    const int i = blockIdx.x * kBlock + threadIdx.x;
-    bool vis = false;
-    if (i < c.count) {
-        const size_t R = static_cast<size_t>(A.rows);
-        const float mw[3] = {A.p[0][i], A.p[0][R + i], A.p[0][2 * R + i]};
-        const float q[4] = {A.p[1][i], A.p[1][R + i], A.p[1][2 * R + i], A.p[1][3 * R + i]};
-        const float s[3] = {sxm::expf_(A.p[2][i]), sxm::expf_(A.p[2][R + i]), sxm::expf_(A.p[2][2 * R + i])};
-        const float opac = sigmoid_ref(A.p[3][i]);
-        float Cw[9];
-        sxd::quat_scale_to_covar_ref(q, s, Cw);
-        const sxd::Cam cam = sxd::make_cam(c.vm, c.K, c.width, c.height);
-        const sxd::ProjCfg cfg{c.eps2d, c.near_plane, c.far_plane, c.radius_clip, c.aa, 1};
-        const sxd::ProjOut o = sxd::project_one(cam, mw, Cw, opac, cfg);
-        radii[2 * i] = o.alive ? o.rx : 0;
-        radii[2 * i + 1] = o.alive ? o.ry : 0;
-        int32_t cnt = 0;
-        uint32_t meta = 0;
-        if (o.alive) {
-            vis = true;
-            const float op_used = c.aa ? opac * o.comp : opac;
-            float cp[3];
-            campos_of(c.vm, cp);
-            const float dx = mw[0] - cp[0], dy = mw[1] - cp[1], dz = mw[2] - cp[2];
-            float col[3];
-            meta = 1u;
-            const int nb = (static_cast<int>(c.degree) + 1) * (static_cast<int>(c.degree) + 1);
-            float co[NC][3];
+__device__ __forceinline__ int32_t preprocess_row(const StepConst& c, const Arena& A, int i, const float (&mw)[3],
+                                                  const float (&q)[4], const float (&sl)[3], float logit,
+                                                  float (&co)[NC][3], bool co_ready, float4* splats, int32_t* radii,
+                                                  bool& vis) {
+    const size_t R = static_cast<size_t>(A.rows);
+    const float s[3] = {sxm::expf_(sl[0]), sxm::expf_(sl[1]), sxm::expf_(sl[2])};
+    const float opac = sigmoid_ref(logit);
+    float Cw[9];
+    sxd::quat_scale_to_covar_ref(q, s, Cw);
+    const sxd::Cam cam = sxd::make_cam(c.vm, c.K, c.width, c.height);
+    const sxd::ProjCfg cfg{c.eps2d, c.near_plane, c.far_plane, c.radius_clip, c.aa, 1};
+    const sxd::ProjOut o = sxd::project_one(cam, mw, Cw, opac, cfg);
+    radii[2 * i] = o.alive ? o.rx : 0;
+    radii[2 * i + 1] = o.alive ? o.ry : 0;
+    int32_t cnt = 0;
+    vis = o.alive;
+    if (o.alive) {
+        const float op_used = c.aa ? opac * o.comp : opac;
+        float cp[3];
+        campos_of(c.vm, cp);
+        const float dx = mw[0] - cp[0], dy = mw[1] - cp[1], dz = mw[2] - cp[2];
+        float col[3];
+        uint32_t meta = 1u;
+        const int nb = (static_cast<int>(c.degree) + 1) * (static_cast<int>(c.degree) + 1);
+        if (!co_ready) {
 #pragma unroll
             for (int k = 0; k < NC; k++)
 #pragma unroll
                 for (int ch = 0; ch < 3; ch++)
                     co[k][ch] = k >= nb ? 0.0f : k == 0 ? A.p[4][ch * R + i] : A.p[5][((k - 1) * 3 + ch) * R + i];
-#pragma unroll
-            for (int ch = 0; ch < 3; ch++) {
-                const float raw = sxd::sh_color(c.degree, dx, dy, dz, [&](int k) { return co[k][ch]; });
-                const float pre = raw + 0.5f;
-                if (pre > 0.0f) meta |= 2u << ch;
-                col[ch] = (pre < 0.0f) ? 0.0f : pre;
-            }
-            if (c.accutile) {
-                cnt = static_cast<int32_t>(sxd::accutile<false>(o.ca, o.cb, o.cc, op_used, o.m2x, o.m2y, 16.0f,
-                                                                c.tile_width, c.tile_height, [](int32_t) {}));
-            } else {
-                const sxd::TileRect r = sxd::aabb_rect(o.m2x, o.m2y, static_cast<float>(o.rx),
-                                                       static_cast<float>(o.ry), 16.0f, c.tile_width, c.tile_height);
-                cnt = (r.max_y - r.min_y) * (r.max_x - r.min_x);
-            }
-            splats[3 * (size_t)i] = make_float4(o.m2x, o.m2y, op_used, o.depth);
-            splats[3 * (size_t)i + 1] = make_float4(o.ca, o.cb, o.cc, o.comp);
-            splats[3 * (size_t)i + 2] = make_float4(col[0], col[1], col[2], __uint_as_float(meta));
-        } else {
-            splats[3 * (size_t)i + 2] = make_float4(0.f, 0.f, 0.f, __uint_as_float(0u));
         }
-        tiles[i] = cnt;
-        n_tiles_sum = static_cast<uint32_t>(cnt);
-        if (clr.touched) clr.touched[i] = 0;
+#pragma unroll
+        for (int ch = 0; ch < 3; ch++) {
+            const float raw = sxd::sh_color(c.degree, dx, dy, dz, [&](int k) { return co[k][ch]; });
+            const float pre = raw + 0.5f;
+            if (pre > 0.0f) meta |= 2u << ch;
+            col[ch] = (pre < 0.0f) ? 0.0f : pre;
+        }
+        if (c.accutile) {
+            cnt = static_cast<int32_t>(sxd::accutile<false>(o.ca, o.cb, o.cc, op_used, o.m2x, o.m2y, 16.0f,
+                                                            c.tile_width, c.tile_height, [](int32_t) {}));
+        } else {
+            const sxd::TileRect r = sxd::aabb_rect(o.m2x, o.m2y, static_cast<float>(o.rx),
+                                                   static_cast<float>(o.ry), 16.0f, c.tile_width, c.tile_height);
+            cnt = (r.max_y - r.min_y) * (r.max_x - r.min_x);
+        }
+        splats[3 * (size_t)i] = make_float4(o.m2x, o.m2y, op_used, o.depth);
+        splats[3 * (size_t)i + 1] = make_float4(o.ca, o.cb, o.cc, o.comp);
+        splats[3 * (size_t)i + 2] = make_float4(col[0], col[1], col[2], __uint_as_float(meta));
+    } else {
+        splats[3 * (size_t)i + 2] = make_float4(0.f, 0.f, 0.f, __uint_as_float(0u));
     }
+    return cnt;
+}
+
+// The end of a preprocess workgroup (every thread calls it): the step's clears by the first thread of
+// the grid, and the block's visible count, tile count and count of Gaussians with tiles (plain stores;
+// a single global counter would serialize every wave).
+__device__ __forceinline__ void preprocess_block_end(bool vis, uint32_t n_tiles_sum, uint32_t* vis_part,
+                                                     const StepClear& clr) {
+    __shared__ uint32_t s_vis[kBlock / 64], s_isect[kBlock / 64], s_emit[kBlock / 64];
     if (clr.stamp && blockIdx.x == 0 && threadIdx.x == 0) {
+        if (clr.long_prev) *clr.long_prev = *clr.long_count;
         *clr.long_count = 0;
         const uint32_t next = *clr.stamp + 1u;
         *clr.stamp = next ? next : 1u;  // never 0: zeroed entries hold 0
     }
-    // visible count, tile count and count of Gaussians with tiles per block (plain stores; a single
-    // global counter would serialize every wave)
     const unsigned long long bal = __ballot(vis);
     const unsigned long long bal_emit = __ballot(n_tiles_sum > 0u);
 #pragma unroll
@@ -152,10 +155,25 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
     }
 }
 
-// a store into mapped host memory, at system scope (no GPU cache keeps it from the host)
-template <class T>
-__device__ __forceinline__ void store_host(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+template <int NC>
+__global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, float4* __restrict__ splats,
+                                                       int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
+                                                       uint32_t* __restrict__ vis_part, StepClear clr) {
+    uint32_t n_tiles_sum = 0;  // this lane's tile count; summed per block
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    bool vis = false;
+    if (i < c.count) {
+        const size_t R = static_cast<size_t>(A.rows);
+        const float mw[3] = {A.p[0][i], A.p[0][R + i], A.p[0][2 * R + i]};
+        const float q[4] = {A.p[1][i], A.p[1][R + i], A.p[1][2 * R + i], A.p[1][3 * R + i]};
+        const float sl[3] = {A.p[2][i], A.p[2][R + i], A.p[2][2 * R + i]};
+        float co[NC][3];
+        const int32_t cnt = preprocess_row<NC>(c, A, i, mw, q, sl, A.p[3][i], co, false, splats, radii, vis);
+        tiles[i] = cnt;
+        n_tiles_sum = static_cast<uint32_t>(cnt);
+        if (clr.touched) clr.touched[i] = 0;
+    }
+    preprocess_block_end(vis, n_tiles_sum, vis_part, clr);
 }
 
 // One workgroup over the preprocess blocks' {visible, tiles, Gaussians with tiles} counts: the totals
@@ -547,86 +565,60 @@ __global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ k
     off[t] = static_cast<int32_t>(lo);
 }
 
-__device__ double block_sum_fixed(const double* __restrict__ p, int n, double* s_red) {
-    double acc = 0.0;
-    int k = threadIdx.x;
-    // eight independent loads in flight, summed in the same (ascending) order as the plain loop
-    for (; k + 7 * kBlock < n; k += 8 * kBlock) {
-        double v[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = p[k + j * kBlock];
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc += v[j];
-    }
-    for (; k < n; k += kBlock) acc += p[k];
-    s_red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int o = kBlock / 2; o > 0; o >>= 1) {
-        if (threadIdx.x < o) s_red[threadIdx.x] += s_red[threadIdx.x + o];
-        __syncthreads();
-    }
-    const double r = s_red[0];
-    __syncthreads();
-    return r;
-}
-
-// The step's loss from the per-block partial sums, by a whole workgroup: loss = (1-lam) * float(l1_sum /
-// n_px) + lam * (1 - float(ssim_sum / M)) (or the L1 alone); thread 0 stores it and, with rb.host set,
-// the loss and rb's words into mapped host memory.
-__device__ void loss_final(const StepLoss& L, double* s_red) {
-    const double l1s = block_sum_fixed(L.l1p, L.n_l1, s_red);
-    const double sss = L.use_ssim ? block_sum_fixed(L.ssp, L.n_ss, s_red) : 0.0;
-    if (threadIdx.x == 0) {
-        const float l1 = static_cast<float>(l1s / L.n_px);
-        const float loss =
-            L.use_ssim ? (1.0f - L.lam) * l1 + L.lam * (1.0f - static_cast<float>(sss / L.M)) : l1;
-        L.out[0] = loss;
-        if (L.rb.host) {
-            store_host(&L.rb.host[0], __float_as_uint(loss));
-            store_host(&L.rb.host[1], *L.rb.sort_err);
-            store_host(&L.rb.host[2], *L.rb.max_tile);
-            store_host(&L.rb.host[3], L.rb.long_count ? static_cast<uint32_t>(*L.rb.long_count) : 0u);
-            __hip_atomic_store(L.rb.seq_host, L.rb.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
-    }
-}
-
-// NC = the arena's SH coefficient count (1, 4, 9 or 16), a compile-time bound so that the SH basis and
-// its partials stay in registers
-template <int NC>
-__global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, const float4* __restrict__ splats,
-                                                        const float4* __restrict__ grads,
-                                                        const uint8_t* __restrict__ touched,
-                                                        const unsigned long long* __restrict__ skip, StepLoss L) {
-    __shared__ double s_red[kBlock];
-    // the first workgroup also reduces the loss (every thread of it, before any leaves)
-    if (L.out && blockIdx.x == 0) loss_final(L, s_red);
-    // the step overflowed its buffers and runs again, or the tile sort gave up (its lists, and every
-    // gradient rasterised from them, are wrong; the host reports the error): leave the arena as it was
-    if (skip && *skip) return;
-    if (L.rb.sort_err && *L.rb.sort_err) return;
+// The parameter update of a training step (constants c; NC = the arena's SH coefficient count, 1, 4, 9 or
+// 16, a compile-time bound so that the SH basis and its partials stay in registers), per row: relu mask,
+// SH backward fused with the Adam of sh0/shN, AA chain, projection backward, gradient chains and
+// regularisers, Adam of the geometry; then, with c.inject_noise, the MCMC position noise. The arena is
+// left as it was when the step overflowed its buffers and runs again (skip), or when the tile sort gave
+// up (sort_err: its lists, and every gradient rasterised from them, are wrong; the host reports the
+// error).
+// FUSED: the next step's preprocess too (constants cn, the same rows), from the row's updated values
+// still in registers instead of a second read of the arena — the same results as this update followed
+// by k_preprocess; the row's touched flag (read by the update) is then cleared for the new step when
+// clr.touched is set.
+template <int NC, bool FUSED>
+__global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, float4* splats,
+                                                        const float4* __restrict__ grads, uint8_t* touched,
+                                                        const unsigned long long* __restrict__ skip,
+                                                        const uint32_t* __restrict__ sort_err, StepConst cn,
+                                                        int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
+                                                        uint32_t* __restrict__ vis_part, StepClear clr) {
+    const bool apply = !(skip && *skip) && !(sort_err && *sort_err);  // uniform
+    if (!FUSED && !apply) return;
     const int i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= c.count) return;
+    if (!FUSED && i >= c.count) return;
+    const bool row = i < c.count;
     const size_t R = static_cast<size_t>(A.rows);
-    const uint32_t meta = __float_as_uint(splats[3 * (size_t)i + 2].w);
+    const uint32_t meta = row ? __float_as_uint(splats[3 * (size_t)i + 2].w) : 0u;
     const bool live = meta & 1u;
     // A wave with a visible row takes its culled rows along (loaded and stored back unchanged): the
     // columns are SoA, so skipping them would leave every line partially written (a read-modify-write
     // in the memory system). A wave of culled rows with no noise has nothing to read or write.
     const bool wave_live = __any(live);
-    if (!wave_live && !c.inject_noise) return;
-    float mw[3] = {ld_stream(&A.p[0][i]), ld_stream(&A.p[0][R + i]), ld_stream(&A.p[0][2 * R + i])};
-    float q[4] = {ld_stream(&A.p[1][i]), ld_stream(&A.p[1][R + i]), ld_stream(&A.p[1][2 * R + i]),
-                  ld_stream(&A.p[1][3 * R + i])};
-    float sl[3] = {ld_stream(&A.p[2][i]), ld_stream(&A.p[2][R + i]), ld_stream(&A.p[2][2 * R + i])};
-    float logit = ld_stream(&A.p[3][i]);
-    if (wave_live) {
+    if (!FUSED && !wave_live && !c.inject_noise) return;
+    float mw[3], q[4], sl[3], logit = 0.f;
+    if (row) {
+        mw[0] = ld_stream(&A.p[0][i]);
+        mw[1] = ld_stream(&A.p[0][R + i]);
+        mw[2] = ld_stream(&A.p[0][2 * R + i]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) q[k] = ld_stream(&A.p[1][k * R + i]);
+#pragma unroll
+        for (int k = 0; k < 3; k++) sl[k] = ld_stream(&A.p[2][k * R + i]);
+        logit = ld_stream(&A.p[3][i]);
+    }
+    float co[NC][3];  // FUSED: the updated SH coefficients when co_ready
+    bool co_ready = false;
+    if (row && apply && wave_live) {
         // rows no tile reached have no gradient record this step: zeros
-        const bool has_g = live && touched[i];
-        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 g0 = has_g ? grads[3 * (size_t)i] : z4;
-        const float4 g1 = has_g ? grads[3 * (size_t)i + 1] : z4;
-        const float4 g2 = has_g ? grads[3 * (size_t)i + 2] : z4;
+        // (a branch around the loads: as selects between a load and a zero vector, the compiler can turn
+        // them into one load through a select of two pointers, one to a zero vector in scratch memory)
+        float4 g0 = make_float4(0.f, 0.f, 0.f, 0.f), g1 = g0, g2 = g0;
+        if (live && touched[i]) {
+            g0 = grads[3 * (size_t)i];
+            g1 = grads[3 * (size_t)i + 1];
+            g2 = grads[3 * (size_t)i + 2];
+        }
         const float4 s1 = splats[3 * (size_t)i + 1];
         // relu mask (train_relu_mask_apply)
         const float vrgb[3] = {(meta & 2u) ? g2.x : 0.0f, (meta & 4u) ? g2.y : 0.0f, (meta & 8u) ? g2.z : 0.0f};
@@ -653,7 +645,6 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         sxd::ShBasis b;
         sxd::sh_basis(c.degree, mw[0] - cp[0], mw[1] - cp[1], mw[2] - cp[2], b);
         const int nb = (static_cast<int>(c.degree) + 1) * (static_cast<int>(c.degree) + 1);
-        float co[NC][3];
 #pragma unroll
         for (int k = 0; k < NC; k++)
 #pragma unroll
@@ -694,8 +685,8 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
                     const int grp = k == 0 ? 4 : 5;
                     const size_t idx = (k == 0 ? (size_t)ch : (size_t)((k - 1) * 3 + ch)) * R + i;
                     const float g = k < nb ? b.Y[k] * vrgb[ch] : 0.0f;
-                    adam_update(A.p[grp], A.m[grp], A.v[grp], idx, co[k][ch], mm[dk][ch], vv[dk][ch], g, c.lr[grp],
-                                c.b1, c.b2, c.eps, live);
+                    co[k][ch] = adam_update(A.p[grp], A.m[grp], A.v[grp], idx, co[k][ch], mm[dk][ch], vv[dk][ch], g,
+                                            c.lr[grp], c.b1, c.b2, c.eps, live);
                 }
         }
         float vdir[3] = {0.f, 0.f, 0.f};
@@ -729,9 +720,9 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         }
         float vlog = v_op * (opac * (1.0f - opac));
         if (c.opacity_reg_w > 0.0f) vlog += c.opacity_reg_w * opac * (1.0f - opac);
-        // Adam of means, quats, scales, opacities
+        // Adam of means, quats, scales, opacities (the updated values stay in registers for the noise
+        // step and the next preprocess)
 #pragma unroll
-        // (the updated values stay in registers for the noise step below)
         for (int k = 0; k < 3; k++)
             mw[k] = adam_update(A.p[0], A.m[0], A.v[0], k * R + i, mw[k], m0[k], v0[k], vm_[k], c.lr[0], c.b1, c.b2,
                                 c.eps, live);
@@ -744,8 +735,9 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
             sl[k] = adam_update(A.p[2], A.m[2], A.v[2], k * R + i, sl[k], m2[k], v2[k], vsl[k], c.lr[2], c.b1, c.b2,
                                 c.eps, live);
         logit = adam_update(A.p[3], A.m[3], A.v[3], i, logit, m3, v3, vlog, c.lr[3], c.b1, c.b2, c.eps, live);
+        co_ready = true;
     }
-    if (c.inject_noise) {
+    if (row && apply && c.inject_noise) {
         // normals 3i..3i+2 of the Philox stream (seed, offset): blocks t = n / 4
         const uint32_t n0 = 3u * static_cast<uint32_t>(i);
         const uint32_t t0 = n0 >> 2, t1 = (n0 + 2u) >> 2;
@@ -765,6 +757,17 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, co
         sxd::perturb_one(mw, q, sl, logit, nz, c.noise_scale, 0.005f, 100.0f);
 #pragma unroll
         for (int k = 0; k < 3; k++) A.p[0][k * R + i] = mw[k];
+    }
+    if constexpr (FUSED) {
+        uint32_t n_tiles_sum = 0;
+        bool vis = false;
+        if (row) {
+            const int32_t cnt = preprocess_row<NC>(cn, A, i, mw, q, sl, logit, co, co_ready, splats, radii, vis);
+            tiles[i] = cnt;
+            n_tiles_sum = static_cast<uint32_t>(cnt);
+            if (clr.touched) touched[i] = 0;
+        }
+        preprocess_block_end(vis, n_tiles_sum, vis_part, clr);
     }
 }
 
@@ -890,18 +893,51 @@ void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* of
     launch_tile_offsets(keys, n, n_tiles, offsets, s, n_dev);
 }
 
+void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena& A, float4* splats, const float4* grads,
+                            uint8_t* touched, const unsigned long long* skip, const uint32_t* sort_err, int32_t* radii,
+                            int32_t* tiles, uint32_t* vis_part, unsigned long long* n_visible,
+                            unsigned long long* block_base, unsigned long long isect_cap, unsigned long long* host_counts,
+                            unsigned long long seq, const StepClear& clr, hipStream_t s) {
+    if (c.count <= 0) return;
+    if (cu.count != c.count || cu.n_coeffs != c.n_coeffs)
+        throw std::invalid_argument("update_preprocess: both steps must cover the same rows");
+    if (clr.touched && clr.touched != touched)
+        throw std::invalid_argument("update_preprocess: the touched flags cleared must be the ones read");
+    const dim3 grid(grid_for(c.count)), block(kBlock);
+#define SX_UPD(NC)                                                                                              \
+    hipLaunchKernelGGL((k_postprocess<NC, true>), grid, block, 0, s, cu, A, splats, grads, touched, skip, sort_err, c, \
+                       radii, tiles, vis_part, clr)
+    switch (c.n_coeffs) {
+        case 1: SX_UPD(1); break;
+        case 4: SX_UPD(4); break;
+        case 9: SX_UPD(9); break;
+        case 16: SX_UPD(16); break;
+        default: throw std::invalid_argument("update_preprocess: SH coefficient count must be 1, 4, 9 or 16");
+    }
+#undef SX_UPD
+    hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
+                       static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts, seq);
+}
+
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
                       const uint8_t* touched, hipStream_t s, const unsigned long long* skip,
-                      const StepLoss& loss) {
+                      const uint32_t* sort_err) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
+    // (the splat records and touched flags are only read: the launch shares the fused variant's signature)
+    float4* sp = const_cast<float4*>(splats);
+    uint8_t* tch = const_cast<uint8_t*>(touched);
+#define SX_PP(NC)                                                                                                \
+    hipLaunchKernelGGL((k_postprocess<NC, false>), grid, block, 0, s, c, A, sp, grads, tch, skip, sort_err, c, \
+                       nullptr, nullptr, nullptr, StepClear{})
     switch (c.n_coeffs) {
-        case 1: hipLaunchKernelGGL(k_postprocess<1>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
-        case 4: hipLaunchKernelGGL(k_postprocess<4>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
-        case 9: hipLaunchKernelGGL(k_postprocess<9>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
-        case 16: hipLaunchKernelGGL(k_postprocess<16>, grid, block, 0, s, c, A, splats, grads, touched, skip, loss); break;
+        case 1: SX_PP(1); break;
+        case 4: SX_PP(4); break;
+        case 9: SX_PP(9); break;
+        case 16: SX_PP(16); break;
         default: throw std::invalid_argument("postprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
+#undef SX_PP
 }
 
 int step_l1_blocks(int64_t n) { return static_cast<int>(std::min<int64_t>(1024, grid_for(n))); }

@@ -99,6 +99,12 @@ struct sxh_executor {
     // sets the sort's error word, as a sort that gave up would; every kernel still runs to its end
     bool debug_sort_error = false;
     int isect_order = SXH_ISECT_ORDER_AUTO;
+    // The last training step's parameter update is deferred: the next training step applies it in its
+    // preprocess, row by row in the same pass over the arena (step_update_preprocess); anything else that
+    // reads or writes the arena applies it first (sxh_detail::flush_update). pending_c: that step's
+    // constants.
+    bool update_pending = false;
+    sxk::StepConst pending_c{};
     int64_t last_max_tile = -1;      // the largest tile's entry count in the previous step (-1: none yet)
     int64_t last_long = -1;          // the previous training step's gather ranges past kLongRange (-1: none yet)
     sxh::DevBuf<uint32_t> max_tile;  // written by the step's tile order
@@ -188,4 +194,7 @@ namespace sxh_detail {
 // One training (or forward-only) step of the executor; render_to_dev, when not null, receives a
 // device copy of the render. Defined in executor.cpp.
 void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out, float* render_to_dev);
+// The deferred parameter update of the last training step, if one is pending, as its own launch on the
+// executor's stream (ordered before whatever is queued after it). Defined in executor.cpp.
+void flush_update(sxh_executor* e);
 }  // namespace sxh_detail

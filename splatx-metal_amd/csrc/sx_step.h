@@ -58,6 +58,7 @@ struct StepClear {
     uint8_t* touched = nullptr;
     uint32_t* stamp = nullptr;
     int32_t* long_count = nullptr;
+    int32_t* long_prev = nullptr;  // (when set) receives the previous step's long-range count first
 };
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
@@ -101,8 +102,8 @@ struct StepReadback {
     unsigned long long* seq_host = nullptr;
     unsigned long long seq = 0;
 };
-// A training step's loss, reduced by the postprocess's first workgroup from the per-block partial sums
-// (fixed order): loss = (1-lam) * float(l1_sum / n_px) + lam * (1 - float(ssim_sum / M)) (or the L1
+// A training step's loss, reduced by one wave (the gather's first workgroup) from the per-block partial
+// sums (fixed order): loss = (1-lam) * float(l1_sum / n_px) + lam * (1 - float(ssim_sum / M)) (or the L1
 // alone) into out[0]; with rb.host set, the loss and rb's words also go to the host. Null out: none.
 struct StepLoss {
     const double* l1p = nullptr;
@@ -115,12 +116,20 @@ struct StepLoss {
     float* out = nullptr;
     StepReadback rb{};
 };
-// skip (when set): a device word; nonzero leaves the arena untouched (the overflow word of out_vis);
-// loss: the step's loss (computed whatever skip holds)
+// The parameter update of a training step with constants c. skip, sort_err (when set): device words;
+// either nonzero leaves the arena untouched (the overflow word of out_vis, the tile sort's error word).
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
                       const uint8_t* touched, hipStream_t s, const unsigned long long* skip = nullptr,
-                      const StepLoss& loss = {});
-// Noise only (the forward-only path never calls it; a training step fuses it into postprocess).
+                      const uint32_t* sort_err = nullptr);
+// A training step's parameter update (constants cu, its skip and sort error words) and the next step's
+// preprocess (constants c, the same rows; then the block scan, as step_preprocess) in one pass over the
+// arena: the same results as step_postprocess followed by step_preprocess. touched: the update's
+// touched flags, cleared for the new step when clr.touched (which must be the same buffer) is set.
+void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena& A, float4* splats, const float4* grads,
+                            uint8_t* touched, const unsigned long long* skip, const uint32_t* sort_err, int32_t* radii,
+                            int32_t* tiles, uint32_t* vis_part, unsigned long long* out_vis,
+                            unsigned long long* block_base, unsigned long long isect_cap, unsigned long long* host_counts,
+                            unsigned long long seq, const StepClear& clr, hipStream_t s);
 // L1 gradient without SSIM: v_render = sign(render - gt) / n, per-block f64 sums of |render - gt|.
 void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_render, double* partials,
                   int n_blocks, hipStream_t s);

@@ -145,9 +145,9 @@ def test_steps_returning_at_the_loss_match_fully_synced_steps(gpu):
 
 def test_gather_long_ranges_inline_match_queued(gpu, oracle):
     """The gather reduces a Gaussian's entries past 64 tiles either queued (a wave each, in a second
-    launch) or inline (the gather's own waves, after its short ranges), chosen from the previous
-    step's count of such ranges: the first step of an executor queues them, the next one (with few)
-    reduces them inline. Both must give the same sums: with b1 = 0 the first moment after a step is
+    launch) or inline (the gather's own waves, after its short ranges), chosen from the count of such
+    ranges the previous step reported (its predecessor's: 0 before any): the first step of an executor
+    queues them, the next one reduces them inline. Both must give the same sums: with b1 = 0 the first moment after a step is
     exactly its gradient, and with frozen parameters (learning rates 0) and the same pose the two
     steps' gradients must agree bit for bit. Large splats in a 512x384 image give ranges past 64."""
     sc = scene.make_scene(n=3000, sh_degree=1, width=512, height=384, fx=400.0, seed=21,
