@@ -225,7 +225,9 @@ def load_traffic(kernel: str, cfg: int):
         return None
     with open(path) as f:
         rec = json.load(f)
-    k = rec.get("configs", {}).get(str(cfg), {}).get("kernels", {}).get(kernel)
+    # the counter tables label kernels by what they run; bench.py's event intervals by step stage
+    label = {"update_preprocess": "update + preprocess"}.get(kernel, kernel)
+    k = rec.get("configs", {}).get(str(cfg), {}).get("kernels", {}).get(label)
     if k is None:
         return None
     return round(k["hbm_bytes"] / max(1, k["dispatches"]))
@@ -299,6 +301,8 @@ def main():
                     help="only time the VALU yardstick kernels (issue rate per instruction class) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run device copies of MIB MiB (yardstick for the HBM byte counters) and exit")
+    ap.add_argument("--row-order", choices=("auto", "original", "spatial"), default="auto",
+                    help="how the executor keeps the rows in HBM (sxh_exec_set_row_order; the same results)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the step has no multi-GPU "
@@ -329,6 +333,8 @@ def main():
     b = sh.Backend(0)
     ex = b.make_train_step_executor(arena_rows=arena, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
                                     antialiased=aa, isect_mode=isect)
+    ex.set_row_order({"auto": sh.SXH_ROW_ORDER_SPATIAL_AUTO, "original": sh.SXH_ROW_ORDER_ORIGINAL,
+                      "spatial": sh.SXH_ROW_ORDER_SPATIAL}[args.row_order])
     # targets: the second scene rendered from every pose into the device GT cache
     ex.set_gt_cache(np.zeros((n_poses, sc.height, sc.width, 3), np.float32))
     tp, tm, tv = scene.copy_state(tgt)
@@ -466,7 +472,8 @@ def main():
         "config": {"workload": f"config {args.config}: N={sc.n}, SH{sc.sh_degree}, {sc.width}x{sc.height}, "
                                f"fx=fy={cfg['fx']}, {cfg['isect']} isect, ssim_weight={cfg['ssim']}, "
                                f"pose jittered per step", "gaussians": sc.n, "width": sc.width,
-                   "height": sc.height, "sh_degree": sc.sh_degree, "parallelism": "single GPU"},
+                   "height": sc.height, "sh_degree": sc.sh_degree, "parallelism": "single GPU",
+                   "row_order": args.row_order},
         "ms_p50": round(float(np.percentile(step_ms, 50)), 4),
         "ms_p90": round(float(np.percentile(step_ms, 90)), 4),
         "gaussians_per_s": round(sc.n / (ms_per_step / 1e3), 1),

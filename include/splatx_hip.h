@@ -682,6 +682,19 @@ int32_t sxh_exec_set_graph(sxh_executor* e, int32_t enable);
 #define SXH_ISECT_ORDER_DEPTH_FIRST 1
 #define SXH_ISECT_ORDER_INDEX_FIRST 2
 int32_t sxh_exec_set_isect_order(sxh_executor* e, int32_t mode);
+/* The order in which the executor keeps the live rows in HBM. SXH_ROW_ORDER_SPATIAL_AUTO (default):
+ * from the second training step after the last call that exchanged rows with the caller (upload,
+ * download, refine, checkpoint, export), for clouds of at least 65536 rows, along a Morton curve over
+ * the means, so that the rows a camera culls fill whole waves that the parameter update skips;
+ * SXH_ROW_ORDER_ORIGINAL: always the caller's order; SXH_ROW_ORDER_SPATIAL: along the curve from the
+ * next training step on, at any size. Every result is the same bit for bit in every mode (the
+ * intersections are emitted, and the MCMC noise drawn, by original row; every call that exchanges
+ * rows restores the caller's order first). No counterpart in the reference (a layout choice of this
+ * backend). */
+#define SXH_ROW_ORDER_SPATIAL_AUTO 0
+#define SXH_ROW_ORDER_ORIGINAL 1
+#define SXH_ROW_ORDER_SPATIAL 2
+int32_t sxh_exec_set_row_order(sxh_executor* e, int32_t mode);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -111,7 +111,7 @@ static void sync_params(sxh_executor* e, const sxh_param_sync* s, bool up) {
     if (!s) invalid("TrainStepExecutor", "null sync");
     if (s->rows < 0 || s->rows > e->rows) invalid("TrainStepExecutor", "sync rows out of [0, arena_rows]");
     const int rows = static_cast<int>(s->rows);
-    sxh_detail::flush_update(e);  // (an upload overwrites rows the pending update would write later)
+    sxh_detail::canonicalize(e);  // rows in the caller's order, the pending update applied
     if (rows == 0) return;
     hipStream_t st = e->b->stream;
     for (int g = 0; g < 6; g++) {
@@ -206,6 +206,17 @@ int32_t sxh_exec_set_isect_order(sxh_executor* e, int32_t mode) {
     });
 }
 
+int32_t sxh_exec_set_row_order(sxh_executor* e, int32_t mode) {
+    return guarded([&] {
+        if (!e) invalid("TrainStepExecutor", "null executor");
+        if (mode < SXH_ROW_ORDER_SPATIAL_AUTO || mode > SXH_ROW_ORDER_SPATIAL)
+            invalid("TrainStepExecutor", "unknown row order");
+        SXH_HIP(hipSetDevice(e->b->device));
+        if (mode == SXH_ROW_ORDER_ORIGINAL && e->permuted) sxh_detail::canonicalize(e);
+        e->row_order = mode;
+    });
+}
+
 int32_t sxh_exec_get_timing(sxh_executor* e, sxh_exec_timing* out) {
     return guarded([&] {
         if (!e || !out) invalid("TrainStepExecutor", "null argument");
@@ -240,8 +251,42 @@ void sxh_detail::flush_update(sxh_executor* e) {
     e->update_pending = false;
     // gated like the fused launch: the pending step's overflow word (n_vis word 4) and sort error word
     sxk::step_postprocess(e->pending_c, e->arena(), e->splats.p, e->grads.p, e->touched.p, e->b->stream, e->n_vis.p + 4,
-                          e->sort_scratch.p ? sxk::sort_error_flag(e->sort_scratch.p) : nullptr);
+                          e->sort_scratch.p ? sxk::sort_error_flag(e->sort_scratch.p) : nullptr,
+                          e->permuted ? e->row_orig.p : nullptr);
     SXH_HIP(hipGetLastError());
+}
+
+void sxh_detail::canonicalize(sxh_executor* e) {
+    flush_update(e);
+    e->steps_since_exchange = 0;
+    if (!e->permuted) return;
+    // original row o takes internal row row_int[o]
+    sxk::arena_permute_rows(e->arena(), e->dims, e->perm_count, e->row_int.p, e->staging.p, e->b->stream);
+    SXH_HIP(hipGetLastError());
+    e->permuted = false;
+}
+
+// The live rows [0, count) along a Morton curve over their means (the arena in original order, no
+// update pending): keys and a stable sort of them, then every parameter and moment column reordered.
+static void spatial_order(sxh_executor* e, int count) {
+    hipStream_t s = e->b->stream;
+    if (e->row_orig.n < static_cast<size_t>(e->rows)) {
+        e->row_orig.alloc(static_cast<size_t>(e->rows));
+        e->row_int.alloc(static_cast<size_t>(e->rows));
+    }
+    const size_t sf = sxk::arena_morton_scratch_floats(count);
+    if (e->perm_scratch.n < sf) e->perm_scratch.alloc(sf);
+    const sxk::Arena A = e->arena();
+    sxk::arena_morton_keys(A, count, e->perm_scratch.p, e->dkey_a.p, e->order_a.p, s);
+    const int w = sxk::radix_sort(e->dkey_a.p, e->order_a.p, e->dkey_b.p, e->order_b.p, count, 30, e->sort_scratch.p, s,
+                                  true, nullptr, true);
+    if (w < 0) throw std::runtime_error("TrainStepExecutor: spatial order sort failed");
+    const int32_t* src = w ? e->order_b.p : e->order_a.p;
+    sxk::arena_permute_rows(A, e->dims, count, src, e->staging.p, s);
+    sxk::perm_maps(src, count, e->row_orig.p, e->row_int.p, s);
+    SXH_HIP(hipGetLastError());
+    e->permuted = true;
+    e->perm_count = count;
 }
 
 // The step proper. `render_to_dev` (device), when not null, receives a copy of the render.
@@ -302,6 +347,18 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     c.noise_offset = in->noise_offset;
     c.noise_scale = in->noise_scale;
     const sxk::Arena A = e->arena();
+    // the live rows' order: spatial ones cover this step's rows; a cloud that stayed on the device for a
+    // step since it last exchanged rows with the caller goes into spatial order (at most a few ms, once)
+    constexpr int kSpatialMinRows = 1 << 16;
+    if (e->permuted && e->perm_count != c.count) sxh_detail::canonicalize(e);
+    if (!fwd_only && !e->permuted &&
+        ((e->row_order == SXH_ROW_ORDER_SPATIAL) ||
+         (e->row_order == SXH_ROW_ORDER_SPATIAL_AUTO && c.count >= kSpatialMinRows && e->steps_since_exchange >= 2))) {
+        sxh_detail::flush_update(e);
+        spatial_order(e, c.count);
+    }
+    const int32_t* const row_orig = e->permuted ? e->row_orig.p : nullptr;
+    const int32_t* const row_int = e->permuted ? e->row_int.p : nullptr;
     // the last training step's deferred update rides on this step's preprocess when both cover the same
     // rows; a forward-only step (or another row count) applies it first
     if (e->update_pending && (fwd_only || e->pending_c.count != c.count)) sxh_detail::flush_update(e);
@@ -330,11 +387,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             sxk::step_update_preprocess(e->pending_c, c, A, e->splats.p, e->grads.p, e->touched.p, e->n_vis.p + 4,
                                         sxk::sort_error_flag(e->sort_scratch.p), e->radii.p, e->tiles.p,
                                         e->vis_part.p, e->n_vis.p, e->blk_base.p, cap,
-                                        static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s);
+                                        static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s, row_orig,
+                                        row_int);
             e->mark("update_preprocess");
         } else {
             sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
-                                 cap, static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s);
+                                 cap, static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s, row_int);
             e->mark("preprocess");
         }
     };
@@ -371,7 +429,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         // positions of the emit: the Gaussians with tiles (*n_emit of them), compacted in index order
         const unsigned long long* n_emit = e->n_vis.p + 2;
         const int64_t* n_emit_i = reinterpret_cast<const int64_t*>(n_emit);
-        sxk::step_emit_compact(c, e->tiles.p, e->blk_base.p, e->emit_list.p, index_first ? e->cum.p : nullptr, s);
+        sxk::step_emit_compact(c, e->tiles.p, e->blk_base.p, e->emit_list.p, index_first ? e->cum.p : nullptr, s,
+                               row_int);
         const int32_t* order = e->emit_list.p;
         if (!index_first) {
             sxk::step_depth_keys(c, e->splats.p, e->emit_list.p, n_emit, e->dkey_a.p, e->order_a.p, s);
@@ -588,6 +647,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     if (!fwd_only) {  // segment B is queued: its update is this step's pending one
         e->update_pending = true;
         e->pending_c = c;
+        e->steps_since_exchange++;
     }
     out->n_isects = n_isects;
     out->sort_key_bits = 32 + c.tile_n_bits;

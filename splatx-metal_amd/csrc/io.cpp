@@ -287,7 +287,7 @@ int32_t sxh_exec_export_ply(sxh_executor* e, int64_t count, float min_opacity, u
         if (!e || !path) invalid(what, "null executor/path");
         if (count < 0 || count > e->rows) invalid(what, "count out of [0, arena_rows]");
         SXH_HIP(hipSetDevice(e->b->device));
-        sxh_detail::flush_update(e);
+        sxh_detail::canonicalize(e);
         hipStream_t s = e->b->stream;
         const int N = static_cast<int>(count);
         const int K = e->n_coeffs - 1;
@@ -381,7 +381,7 @@ int32_t sxh_exec_save_checkpoint(sxh_executor* e, const sxh_checkpoint_config* c
         if (cfg->sh_degree != e->d.sh_degree) invalid(what, "cloud/config sh_degree mismatch");
         if (iter < 0) invalid("Trainer::make_checkpoint", "iter must be >= 0");
         SXH_HIP(hipSetDevice(e->b->device));
-        sxh_detail::flush_update(e);
+        sxh_detail::canonicalize(e);
         const std::string rng = rng_state ? rng_state : "";
         const std::string tmp = std::string(path) + ".tmp";
         try {
@@ -460,7 +460,7 @@ int32_t sxh_exec_load_checkpoint(sxh_executor* e, const char* path, const sxh_ch
             std::memcpy(rng_state, rng.c_str(), rng.size() + 1);
         }
         SXH_HIP(hipSetDevice(e->b->device));
-        sxh_detail::flush_update(e);  // (the loaded rows then replace the updated ones)
+        sxh_detail::canonicalize(e);  // (the loaded rows then replace the updated ones)
         hipStream_t s = e->b->stream;
         const int n = static_cast<int>(h.alive_count);
         const int mode = h.fp16 ? sxk::kCkptF16 : sxk::kCkptF32;

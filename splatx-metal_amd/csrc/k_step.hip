@@ -176,6 +176,24 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
     preprocess_block_end(vis, n_tiles_sum, vis_part, clr);
 }
 
+// With the arena in spatial order (row_int[o] = the internal row of original row o): the preprocess's
+// per-block counts again, over blocks of 256 original rows, from each row's tile count and visible bit
+// (the splat record's meta word), so that the compaction below runs in the original order.
+__global__ void __launch_bounds__(kBlock) k_orig_block_counts(const int32_t* __restrict__ row_int, int count,
+                                                              const int32_t* __restrict__ tiles,
+                                                              const float4* __restrict__ splats,
+                                                              uint32_t* __restrict__ vis_part) {
+    const int o = blockIdx.x * kBlock + threadIdx.x;
+    uint32_t t = 0u;
+    bool vis = false;
+    if (o < count) {
+        const int g = row_int[o];
+        t = static_cast<uint32_t>(tiles[g]);
+        vis = __float_as_uint(splats[3 * (size_t)g + 2].w) & 1u;
+    }
+    preprocess_block_end(vis, t, vis_part, StepClear{});
+}
+
 // One workgroup over the preprocess blocks' {visible, tiles, Gaussians with tiles} counts: the totals
 // (out = {u64 visible, u64 intersections, u64 Gaussians with tiles, u64 intersections, u64 overflow})
 // and, per block b, the intersections and the Gaussians with tiles of the blocks before it (base[2 b],
@@ -266,14 +284,17 @@ __global__ void __launch_bounds__(kScanBlock) k_block_scan(const uint4* __restri
 // The Gaussians with tiles, in index order, compacted: position j = base[2 b + 1] + (its rank among
 // block b's) gets list[j] = the Gaussian and (cum set) cum[j] = the inclusive sum of the tile counts
 // up to it (base[2 b] + the block's running sum): the emit ranges of the index-first order, and the
-// list the depth-first order sorts.
+// list the depth-first order sorts. row_int (the arena in spatial order): i runs over original rows,
+// the list holds internal rows.
 __global__ void __launch_bounds__(kBlock) k_emit_compact(const int32_t* __restrict__ tiles, int count,
                                                          const unsigned long long* __restrict__ base,
-                                                         int32_t* __restrict__ list, int64_t* __restrict__ cum) {
+                                                         int32_t* __restrict__ list, int64_t* __restrict__ cum,
+                                                         const int32_t* __restrict__ row_int) {
     __shared__ uint32_t s_n[kBlock / 64], s_t[kBlock / 64];
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t t = i < count ? static_cast<uint32_t>(tiles[i]) : 0u;
+    const int g = (row_int && i < count) ? row_int[i] : i;
+    const uint32_t t = i < count ? static_cast<uint32_t>(tiles[g]) : 0u;
     const unsigned long long bal = __ballot(t > 0u);
     const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
@@ -297,7 +318,7 @@ __global__ void __launch_bounds__(kBlock) k_emit_compact(const int32_t* __restri
         }
     if (t > 0u) {
         const unsigned long long j = base[2 * (size_t)blockIdx.x + 1] + pn + rank;
-        list[j] = i;
+        list[j] = g;
         if (cum) cum[j] = static_cast<int64_t>(base[2 * (size_t)blockIdx.x] + pt + incl);
     }
 }
@@ -582,7 +603,8 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, fl
                                                         const unsigned long long* __restrict__ skip,
                                                         const uint32_t* __restrict__ sort_err, StepConst cn,
                                                         int32_t* __restrict__ radii, int32_t* __restrict__ tiles,
-                                                        uint32_t* __restrict__ vis_part, StepClear clr) {
+                                                        uint32_t* __restrict__ vis_part, StepClear clr,
+                                                        const int32_t* __restrict__ row_orig) {
     const bool apply = !(skip && *skip) && !(sort_err && *sort_err);  // uniform
     if (!FUSED && !apply) return;
     const int i = blockIdx.x * kBlock + threadIdx.x;
@@ -738,8 +760,8 @@ __global__ void __launch_bounds__(kBlock) k_postprocess(StepConst c, Arena A, fl
         co_ready = true;
     }
     if (row && apply && c.inject_noise) {
-        // normals 3i..3i+2 of the Philox stream (seed, offset): blocks t = n / 4
-        const uint32_t n0 = 3u * static_cast<uint32_t>(i);
+        // normals 3i..3i+2 of the Philox stream (seed, offset), i the original row: blocks t = n / 4
+        const uint32_t n0 = 3u * static_cast<uint32_t>(row_orig ? row_orig[i] : i);
         const uint32_t t0 = n0 >> 2, t1 = (n0 + 2u) >> 2;
         float z0[4], z1[4];
         sx::philox_normals4(t0, c.noise_seed, c.noise_offset, z0);
@@ -821,7 +843,7 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* n_visible, unsigned long long* block_base,
                      unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
-                     const StepClear& clr, hipStream_t s) {
+                     const StepClear& clr, hipStream_t s, const int32_t* row_int) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
@@ -831,15 +853,17 @@ void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t
         case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part, clr); break;
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
+    if (row_int)  // the block counts in original order
+        hipLaunchKernelGGL(k_orig_block_counts, grid, block, 0, s, row_int, c.count, tiles, splats, vis_part);
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
                        static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts, seq);
 }
 
 void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
-                       int64_t* cum, hipStream_t s) {
+                       int64_t* cum, hipStream_t s, const int32_t* row_int) {
     if (c.count <= 0) return;
     hipLaunchKernelGGL(k_emit_compact, dim3(grid_for(c.count)), dim3(kBlock), 0, s, tiles, c.count, block_base, list,
-                       cum);
+                       cum, row_int);
 }
 
 int step_preprocess_blocks(int64_t count) { return grid_for(count); }
@@ -897,7 +921,8 @@ void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena
                             uint8_t* touched, const unsigned long long* skip, const uint32_t* sort_err, int32_t* radii,
                             int32_t* tiles, uint32_t* vis_part, unsigned long long* n_visible,
                             unsigned long long* block_base, unsigned long long isect_cap, unsigned long long* host_counts,
-                            unsigned long long seq, const StepClear& clr, hipStream_t s) {
+                            unsigned long long seq, const StepClear& clr, hipStream_t s, const int32_t* row_orig,
+                            const int32_t* row_int) {
     if (c.count <= 0) return;
     if (cu.count != c.count || cu.n_coeffs != c.n_coeffs)
         throw std::invalid_argument("update_preprocess: both steps must cover the same rows");
@@ -906,7 +931,7 @@ void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena
     const dim3 grid(grid_for(c.count)), block(kBlock);
 #define SX_UPD(NC)                                                                                              \
     hipLaunchKernelGGL((k_postprocess<NC, true>), grid, block, 0, s, cu, A, splats, grads, touched, skip, sort_err, c, \
-                       radii, tiles, vis_part, clr)
+                       radii, tiles, vis_part, clr, row_orig)
     switch (c.n_coeffs) {
         case 1: SX_UPD(1); break;
         case 4: SX_UPD(4); break;
@@ -915,13 +940,15 @@ void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena
         default: throw std::invalid_argument("update_preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
 #undef SX_UPD
+    if (row_int)  // the block counts in original order
+        hipLaunchKernelGGL(k_orig_block_counts, grid, block, 0, s, row_int, c.count, tiles, splats, vis_part);
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
                        static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts, seq);
 }
 
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
                       const uint8_t* touched, hipStream_t s, const unsigned long long* skip,
-                      const uint32_t* sort_err) {
+                      const uint32_t* sort_err, const int32_t* row_orig) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     // (the splat records and touched flags are only read: the launch shares the fused variant's signature)
@@ -929,7 +956,7 @@ void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, 
     uint8_t* tch = const_cast<uint8_t*>(touched);
 #define SX_PP(NC)                                                                                                \
     hipLaunchKernelGGL((k_postprocess<NC, false>), grid, block, 0, s, c, A, sp, grads, tch, skip, sort_err, c, \
-                       nullptr, nullptr, nullptr, StepClear{})
+                       nullptr, nullptr, nullptr, StepClear{}, row_orig)
     switch (c.n_coeffs) {
         case 1: SX_PP(1); break;
         case 4: SX_PP(4); break;

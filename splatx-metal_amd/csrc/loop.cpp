@@ -187,7 +187,7 @@ double eval_psnr(sxh_executor* e, const sxh_train_loop_args& a, int64_t count, L
 
 // filter_cloud_for_export (min opacity 0.005) of the live rows into host arrays, raw domain
 int64_t filtered_rows(sxh_executor* e, int64_t count, std::vector<float> (&host)[6]) {
-    sxh_detail::flush_update(e);
+    sxh_detail::canonicalize(e);
     hipStream_t s = e->b->stream;
     const int N = static_cast<int>(count);
     DevBuf<unsigned long long> removed(2);

@@ -188,7 +188,7 @@ int32_t sxh_exec_mcmc_refine(sxh_executor* e, const sxh_refine_inputs* in, sxh_r
         if (!in->rng || in->rng->p > kMtWords) invalid(what, "null or malformed rng state");
         if (out->capacity < 0) invalid(what, "negative capacity");
         SXH_HIP(hipSetDevice(e->b->device));
-        sxh_detail::flush_update(e);  // the refine reads the step's updated rows
+        sxh_detail::canonicalize(e);  // the refine reads the step's updated rows, in the caller's order
         ensure_refine_buffers(e, in->n_max);
         hipStream_t s = e->b->stream;
         Ctx c{e, s, static_cast<Readback*>(e->host_small.p), e->arena()};

@@ -105,6 +105,16 @@ struct sxh_executor {
     // constants.
     bool update_pending = false;
     sxk::StepConst pending_c{};
+    // The live rows' order in HBM (sxh_exec_set_row_order, k_perm.hip). With `permuted`, internal row k
+    // of the live rows [0, perm_count) holds original row row_orig[k], and row_int is the inverse;
+    // steps_since_exchange counts the training steps since the last call that exchanged rows with the
+    // caller (which restores the original order: sxh_detail::canonicalize).
+    int row_order = SXH_ROW_ORDER_SPATIAL_AUTO;
+    bool permuted = false;
+    int perm_count = 0;
+    int64_t steps_since_exchange = 0;
+    sxh::DevBuf<int32_t> row_orig, row_int;
+    sxh::DevBuf<float> perm_scratch;
     int64_t last_max_tile = -1;      // the largest tile's entry count in the previous step (-1: none yet)
     int64_t last_long = -1;          // the previous training step's gather ranges past kLongRange (-1: none yet)
     sxh::DevBuf<uint32_t> max_tile;  // written by the step's tile order
@@ -197,4 +207,7 @@ void run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_outputs* out,
 // The deferred parameter update of the last training step, if one is pending, as its own launch on the
 // executor's stream (ordered before whatever is queued after it). Defined in executor.cpp.
 void flush_update(sxh_executor* e);
+// Before a call exchanges rows with the caller: flush_update, then the arena back in the caller's row
+// order if it is in spatial order. Defined in executor.cpp.
+void canonicalize(sxh_executor* e);
 }  // namespace sxh_detail

@@ -15,18 +15,20 @@ __device__ __forceinline__ void store_host(T* p, T v) {
 }
 
 // Sum of p[0, n) by one 64-lane wave in a fixed order: lane l adds p[l], p[l + 64], ... in ascending order
-// (eight loads in flight), then the 64 lane sums are added in a fixed butterfly, after which every lane
-// holds the same total (a + b and b + a are the same double).
+// (sixteen loads in flight: a single wave's sum is bound by its round trips to memory), then the 64 lane
+// sums are added in a fixed butterfly, after which every lane holds the same total (a + b and b + a are
+// the same double).
 __device__ __forceinline__ double wave_sum_fixed(const double* __restrict__ p, int n) {
+    constexpr int kBatch = 16;
     const int lane = threadIdx.x & 63;
     double acc = 0.0;
     int k = lane;
-    for (; k + 7 * 64 < n; k += 8 * 64) {
-        double v[8];
+    for (; k + (kBatch - 1) * 64 < n; k += kBatch * 64) {
+        double v[kBatch];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = p[k + j * 64];
+        for (int j = 0; j < kBatch; j++) v[j] = p[k + j * 64];
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc += v[j];
+        for (int j = 0; j < kBatch; j++) acc += v[j];
     }
     for (; k < n; k += 64) acc += p[k];
 #pragma unroll

@@ -60,16 +60,19 @@ struct StepClear {
     int32_t* long_count = nullptr;
     int32_t* long_prev = nullptr;  // (when set) receives the previous step's long-range count first
 };
+// row_int (when set): the arena is in spatial order, row_int[o] the internal row of original row o; the
+// per-block counts the block scan reads are then taken again over original rows (for the compaction).
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
                      unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
-                     const StepClear& clr, hipStream_t s);
+                     const StepClear& clr, hipStream_t s, const int32_t* row_int = nullptr);
 // number of blocks of step_preprocess
 int step_preprocess_blocks(int64_t count);
 // The Gaussians with tiles in index order (list[j], j below out_vis[2]) and (cum set) cum[j], the
-// inclusive sum of their tile counts: the positions of the index-first emit.
+// inclusive sum of their tile counts: the positions of the index-first emit. row_int (the arena in
+// spatial order): the list runs in original order and holds internal rows.
 void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
-                       int64_t* cum, hipStream_t s);
+                       int64_t* cum, hipStream_t s, const int32_t* row_int = nullptr);
 // depth-first intersections: depth keys of the listed Gaussians (values = index) for a stable 32-bit
 // sort of *n_list keys; then, over that order, each Gaussian's tile ids at [cum[j-1], cum[j]) (cum =
 // inclusive scan of the tile counts gathered through the order); after a stable sort of the tile ids,
@@ -120,7 +123,7 @@ struct StepLoss {
 // either nonzero leaves the arena untouched (the overflow word of out_vis, the tile sort's error word).
 void step_postprocess(const StepConst& c, const Arena& A, const float4* splats, const float4* grads,
                       const uint8_t* touched, hipStream_t s, const unsigned long long* skip = nullptr,
-                      const uint32_t* sort_err = nullptr);
+                      const uint32_t* sort_err = nullptr, const int32_t* row_orig = nullptr);
 // A training step's parameter update (constants cu, its skip and sort error words) and the next step's
 // preprocess (constants c, the same rows; then the block scan, as step_preprocess) in one pass over the
 // arena: the same results as step_postprocess followed by step_preprocess. touched: the update's
@@ -129,7 +132,17 @@ void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena
                             uint8_t* touched, const unsigned long long* skip, const uint32_t* sort_err, int32_t* radii,
                             int32_t* tiles, uint32_t* vis_part, unsigned long long* out_vis,
                             unsigned long long* block_base, unsigned long long isect_cap, unsigned long long* host_counts,
-                            unsigned long long seq, const StepClear& clr, hipStream_t s);
+                            unsigned long long seq, const StepClear& clr, hipStream_t s,
+                            const int32_t* row_orig = nullptr, const int32_t* row_int = nullptr);
+// The arena's spatial order (row_orig[k]: the original row of internal row k; row_int its inverse;
+// nothing is reordered past the live rows [0, count)). arena_morton_keys: keys[i] = the 30-bit Morton
+// code of row i's mean in the means' bounding box, vals[i] = i (scratch: arena_morton_scratch_floats).
+// arena_permute_rows: internal row k of every parameter and moment column takes row src[k] (tmp:
+// 45 * count floats at least). perm_maps: the maps of src read as internal row k <- original row src[k].
+void arena_morton_keys(const Arena& A, int count, float* scratch, uint32_t* keys, int32_t* vals, hipStream_t s);
+size_t arena_morton_scratch_floats(int count);
+void arena_permute_rows(const Arena& A, const int dims[6], int count, const int32_t* src, float* tmp, hipStream_t s);
+void perm_maps(const int32_t* src, int count, int32_t* row_orig, int32_t* row_int, hipStream_t s);
 // L1 gradient without SSIM: v_render = sign(render - gt) / n, per-block f64 sums of |render - gt|.
 void step_l1_grad(const float* render, const float* gt, int64_t n, float* v_render, double* partials,
                   int n_blocks, hipStream_t s);

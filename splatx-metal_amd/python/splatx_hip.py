@@ -31,6 +31,9 @@ SXH_ISECT_AABB = 1
 SXH_ISECT_ORDER_AUTO = 0
 SXH_ISECT_ORDER_DEPTH_FIRST = 1
 SXH_ISECT_ORDER_INDEX_FIRST = 2
+SXH_ROW_ORDER_SPATIAL_AUTO = 0
+SXH_ROW_ORDER_ORIGINAL = 1
+SXH_ROW_ORDER_SPATIAL = 2
 
 
 class SxInvalidArgument(ValueError):
@@ -768,7 +771,7 @@ class Executor:
         self.h = h
         for n in ("sxh_exec_upload", "sxh_exec_download", "sxh_exec_step", "sxh_exec_set_gt_cache",
                   "sxh_exec_render_to_gt_cache", "sxh_exec_set_profiling", "sxh_exec_get_timing", "sxh_exec_set_graph",
-                  "sxh_exec_set_isect_order", "sxh_exec_mcmc_refine", "sxh_exec_sync"):
+                  "sxh_exec_set_isect_order", "sxh_exec_set_row_order", "sxh_exec_mcmc_refine", "sxh_exec_sync"):
             getattr(self.lib, n).restype = C.c_int32
         self.lib.sxh_exec_destroy.argtypes = [C.c_void_p]
 
@@ -980,6 +983,11 @@ class Executor:
         """SXH_ISECT_ORDER_AUTO (default), _DEPTH_FIRST or _INDEX_FIRST: how the step
         builds each tile's (depth, index)-ordered intersection list (the same lists either way)."""
         self._check(self.lib.sxh_exec_set_isect_order(self.h, int(mode)))
+
+    def set_row_order(self, mode: int):
+        """SXH_ROW_ORDER_SPATIAL_AUTO (default), _ORIGINAL or _SPATIAL: the order in which the executor keeps
+        the live rows in HBM (the same results in every mode)."""
+        self._check(self.lib.sxh_exec_set_row_order(self.h, int(mode)))
 
     def get_timing(self):
         t = ExecTiming()

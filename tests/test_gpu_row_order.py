@@ -1,0 +1,133 @@
+"""The executor may keep the live rows in HBM along a Morton curve over their means (so that the rows
+a camera culls fill whole waves, which the parameter update skips), with maps to the caller's rows.
+Every result must be the caller's-order result bit for bit: an executor forced into spatial order
+(SXH_ROW_ORDER_SPATIAL) and one kept in the caller's order (SXH_ROW_ORDER_ORIGINAL) must return the
+same losses and renders and, downloaded, the same parameters and moments, through steps with learning
+rates on, the MCMC position noise (drawn by original row), equal depths (the stable sorts' ties go by
+original row), both intersection orders, a change of the row count, uploads, checkpoints, PLY exports
+and refines in between (each restores the caller's order; the next steps sort again)."""
+import math
+
+import numpy as np
+import pytest
+
+import inputs
+import scene
+import splatx_hip as sh
+
+pytestmark = pytest.mark.gpu
+
+
+def roty(deg):
+    a = math.radians(deg)
+    v = scene.identity_view()
+    v[0, 0], v[0, 2], v[2, 0], v[2, 2] = math.cos(a), math.sin(a), -math.sin(a), math.cos(a)
+    return v
+
+
+def same_state(a, b):
+    return all(np.array_equal(np.asarray(x).view(np.uint32), np.asarray(y).view(np.uint32))
+               for ga, gb in zip(a, b) for x, y in zip(ga, gb))
+
+
+def make(gpu, sc, order, isect_order=sh.SXH_ISECT_ORDER_AUTO, antialiased=False):
+    ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=0.2,
+                                      isect_mode=sh.SXH_ISECT_ACCUTILE, antialiased=antialiased)
+    ex.set_row_order(order)
+    ex.set_isect_order(isect_order)
+    ex.upload_params(*scene.copy_state(sc), sc.n)
+    return ex
+
+
+@pytest.mark.parametrize("isect_order", [sh.SXH_ISECT_ORDER_INDEX_FIRST, sh.SXH_ISECT_ORDER_DEPTH_FIRST])
+def test_spatial_order_matches_original(gpu, isect_order):
+    # a tenth of the means at one depth: ties in every tile's depth order
+    sc = scene.make_scene(n=30000, sh_degree=3, width=256, height=192, fx=220.0, seed=41,
+                          log_scale_mu=math.log(0.04), tie_frac=0.1)
+    noise = dict(inject_noise=True, noise_seed=9, noise_offset=5, noise_scale=0.01)
+    runs = []
+    for order in (sh.SXH_ROW_ORDER_ORIGINAL, sh.SXH_ROW_ORDER_SPATIAL):
+        print(f"row order {order}, isect order {isect_order}", flush=True)
+        ex = make(gpu, sc, order, isect_order, antialiased=True)
+        out = []
+        for k, a in enumerate((0.0, 4.0, -3.0, 2.0, 1.0)):
+            kw = dict(scene.step_kwargs(sc), viewmat=roty(a), gt_rgb=sc.gt, **(noise if k % 2 else {}))
+            r = ex.step(want_render=True, **kw)
+            out.append((r["loss"], r["n_isects"], r["n_visible"], r["render_colors"].copy()))
+        state = scene.copy_state(sc)
+        ex.download_params(*state, sc.n)
+        ex.close()
+        runs.append((out, state))
+    (oa, sa), (ob, sb) = runs
+    for k, (x, y) in enumerate(zip(oa, ob)):
+        assert x[:3] == y[:3], (k, x[:3], y[:3])
+        assert np.array_equal(x[3].view(np.uint32), y[3].view(np.uint32)), k
+    assert same_state(sa, sb)
+    assert not same_state(sa, scene.copy_state(sc))
+
+
+def test_spatial_order_through_exchanges(gpu, tmp_path):
+    """Uploads, downloads, a checkpoint and a PLY export between steps (each restores the caller's
+    order), a step over fewer rows, then steps again in spatial order."""
+    sc = scene.make_scene(n=30000, sh_degree=1, width=256, height=192, fx=220.0, seed=42,
+                          log_scale_mu=math.log(0.04))
+    cfg = sh.CkptConfig.make(sh_degree=sc.sh_degree, total_iters=100)
+    res = []
+    for order in (sh.SXH_ROW_ORDER_ORIGINAL, sh.SXH_ROW_ORDER_SPATIAL):
+        print(f"exchanges, row order {order}", flush=True)
+        ex = make(gpu, sc, order)
+        losses = []
+        kw = dict(scene.step_kwargs(sc), gt_rgb=sc.gt)
+        for a in (0.0, 2.0):
+            losses.append(ex.step(**dict(kw, viewmat=roty(a)))["loss"])
+        ckpt = tmp_path / f"c{order}.sxck"
+        ply = tmp_path / f"p{order}.ply"
+        ex.save_checkpoint(cfg, 2, sc.n, str(ckpt))
+        ex.export_ply(sc.n, str(ply))
+        state = scene.copy_state(sc)
+        ex.download_params(*state, sc.n)
+        ex.upload_params(*state, sc.n)
+        losses.append(ex.step(**dict(kw, viewmat=roty(1.0), count=sc.n - 7000))["loss"])
+        for a in (-1.0, 3.0, 0.5):
+            losses.append(ex.step(**dict(kw, viewmat=roty(a)))["loss"])
+        final = scene.copy_state(sc)
+        ex.download_params(*final, sc.n)
+        ex.close()
+        res.append((losses, ckpt.read_bytes(), ply.read_bytes(), final))
+    (la, ca, pa, fa), (lb, cb, pb, fb) = res
+    assert la == lb, (la, lb)
+    assert ca == cb and pa == pb
+    assert same_state(fa, fb)
+
+
+def test_spatial_order_with_refine(gpu, oracle):
+    """Steps in spatial order, then an MCMC refine (which runs in the caller's order), then steps again:
+    the same lists, counts and arena as in the caller's order."""
+    n, cap, deg = 30000, 36000, 1
+    p, m, v = inputs.make_cloud(n, cap, deg, 13, -1.0, 3.0)
+    sc = scene.make_scene(n=n, sh_degree=deg, width=256, height=192, fx=220.0, seed=43)
+    binoms = oracle.make_binoms_lut(51)
+    res = []
+    for order in (sh.SXH_ROW_ORDER_ORIGINAL, sh.SXH_ROW_ORDER_SPATIAL):
+        print(f"refine, row order {order}", flush=True)
+        ex = gpu.make_train_step_executor(arena_rows=cap, sh_degree=deg, ssim_weight=0.2,
+                                          isect_mode=sh.SXH_ISECT_ACCUTILE)
+        ex.set_row_order(order)
+        ex.upload_params([x.copy() for x in p], [x.copy() for x in m], [x.copy() for x in v], cap)
+        kw = dict(scene.step_kwargs(sc), gt_rgb=sc.gt, count=n)
+        losses = [ex.step(**dict(kw, viewmat=roty(a)))["loss"] for a in (0.0, 2.0, -1.0)]
+        rng = gpu.mt64_seed(5)
+        r = ex.mcmc_refine(n, cap, rng, binoms, want_lists=True)
+        cnt = r["count"]
+        losses += [ex.step(**dict(kw, viewmat=roty(a), count=cnt))["loss"] for a in (1.0, -2.0, 0.5)]
+        state = [np.zeros_like(x) for x in p], [np.zeros_like(x) for x in m], [np.zeros_like(x) for x in v]
+        ex.download_params(*state, cap)
+        ex.close()
+        res.append((losses, r, state))
+    (la, ra, sa), (lb, rb, sb) = res
+    assert la == lb, (la, lb)
+    for key in ("count", "n_relocated", "n_added"):
+        assert ra[key] == rb[key], key
+    for key in ("relocated_dead", "relocation_src", "added_src"):
+        assert np.array_equal(ra[key], rb[key]), key
+    assert same_state(sa, sb)
