@@ -273,6 +273,7 @@ static void spatial_order(sxh_executor* e, int count) {
     if (e->row_orig.n < static_cast<size_t>(e->rows)) {
         e->row_orig.alloc(static_cast<size_t>(e->rows));
         e->row_int.alloc(static_cast<size_t>(e->rows));
+        e->tiles_o.alloc(static_cast<size_t>(e->rows));
     }
     const size_t sf = sxk::arena_morton_scratch_floats(count);
     if (e->perm_scratch.n < sf) e->perm_scratch.alloc(sf);
@@ -388,11 +389,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
                                         sxk::sort_error_flag(e->sort_scratch.p), e->radii.p, e->tiles.p,
                                         e->vis_part.p, e->n_vis.p, e->blk_base.p, cap,
                                         static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s, row_orig,
-                                        row_int);
+                                        row_int, e->tiles_o.p);
             e->mark("update_preprocess");
         } else {
             sxk::step_preprocess(c, A, e->splats.p, e->radii.p, e->tiles.p, e->vis_part.p, e->n_vis.p, e->blk_base.p,
-                                 cap, static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s, row_int);
+                                 cap, static_cast<unsigned long long*>(e->step_rb.dev), seq, clr, s, row_int,
+                                 e->tiles_o.p);
             e->mark("preprocess");
         }
     };
@@ -429,8 +431,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         // positions of the emit: the Gaussians with tiles (*n_emit of them), compacted in index order
         const unsigned long long* n_emit = e->n_vis.p + 2;
         const int64_t* n_emit_i = reinterpret_cast<const int64_t*>(n_emit);
-        sxk::step_emit_compact(c, e->tiles.p, e->blk_base.p, e->emit_list.p, index_first ? e->cum.p : nullptr, s,
-                               row_int);
+        sxk::step_emit_compact(c, row_int ? e->tiles_o.p : e->tiles.p, e->blk_base.p, e->emit_list.p,
+                               index_first ? e->cum.p : nullptr, s, row_int);
         const int32_t* order = e->emit_list.p;
         if (!index_first) {
             sxk::step_depth_keys(c, e->splats.p, e->emit_list.p, n_emit, e->dkey_a.p, e->order_a.p, s);

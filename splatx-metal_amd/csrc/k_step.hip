@@ -176,22 +176,41 @@ __global__ void __launch_bounds__(kBlock) k_preprocess(StepConst c, Arena A, flo
     preprocess_block_end(vis, n_tiles_sum, vis_part, clr);
 }
 
-// With the arena in spatial order (row_int[o] = the internal row of original row o): the preprocess's
-// per-block counts again, over blocks of 256 original rows, from each row's tile count and visible bit
-// (the splat record's meta word), so that the compaction below runs in the original order.
+// With the arena in spatial order (row_int[o] = the internal row of original row o): the tile counts in
+// original order (tiles_o[o], read by the compaction in sequence) and the per-block counts again, over
+// blocks of 256 original rows, so that the compaction below runs in the original order. The visible
+// count of block b stays the preprocess's (only its total is read).
 __global__ void __launch_bounds__(kBlock) k_orig_block_counts(const int32_t* __restrict__ row_int, int count,
                                                               const int32_t* __restrict__ tiles,
-                                                              const float4* __restrict__ splats,
+                                                              int32_t* __restrict__ tiles_o,
                                                               uint32_t* __restrict__ vis_part) {
+    __shared__ uint32_t s_t[kBlock / 64], s_e[kBlock / 64];
     const int o = blockIdx.x * kBlock + threadIdx.x;
     uint32_t t = 0u;
-    bool vis = false;
     if (o < count) {
-        const int g = row_int[o];
-        t = static_cast<uint32_t>(tiles[g]);
-        vis = __float_as_uint(splats[3 * (size_t)g + 2].w) & 1u;
+        t = static_cast<uint32_t>(tiles[row_int[o]]);
+        tiles_o[o] = static_cast<int32_t>(t);
     }
-    preprocess_block_end(vis, t, vis_part, StepClear{});
+    const unsigned long long bal = __ballot(t > 0u);
+    uint32_t sum = t;
+#pragma unroll
+    for (int k = 32; k > 0; k >>= 1) sum += static_cast<uint32_t>(__shfl_xor(static_cast<int>(sum), k, 64));
+    if (sxd::lane_id() == 0) {
+        s_t[threadIdx.x >> 6] = sum;
+        s_e[threadIdx.x >> 6] = static_cast<uint32_t>(__popcll(bal));
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t isect = 0u, emit = 0u;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; w++) {
+            isect += s_t[w];
+            emit += s_e[w];
+        }
+        uint4* vp = reinterpret_cast<uint4*>(vis_part) + blockIdx.x;
+        const uint32_t vis = vp->x;  // the preprocess's (internal block b)
+        *vp = make_uint4(vis, isect, emit, 0u);
+    }
 }
 
 // One workgroup over the preprocess blocks' {visible, tiles, Gaussians with tiles} counts: the totals
@@ -293,8 +312,8 @@ __global__ void __launch_bounds__(kBlock) k_emit_compact(const int32_t* __restri
     __shared__ uint32_t s_n[kBlock / 64], s_t[kBlock / 64];
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int g = (row_int && i < count) ? row_int[i] : i;
-    const uint32_t t = i < count ? static_cast<uint32_t>(tiles[g]) : 0u;
+    const int g = (row_int && i < count) ? row_int[i] : i;  // (with row_int, `tiles` is in original order)
+    const uint32_t t = i < count ? static_cast<uint32_t>(tiles[i]) : 0u;
     const unsigned long long bal = __ballot(t > 0u);
     const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
@@ -843,7 +862,7 @@ __global__ void __launch_bounds__(kBlock) k_soa_to_aos(const float* __restrict__
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* n_visible, unsigned long long* block_base,
                      unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
-                     const StepClear& clr, hipStream_t s, const int32_t* row_int) {
+                     const StepClear& clr, hipStream_t s, const int32_t* row_int, int32_t* tiles_o) {
     if (c.count <= 0) return;
     const dim3 grid(grid_for(c.count)), block(kBlock);
     switch (c.n_coeffs) {
@@ -853,8 +872,8 @@ void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t
         case 16: hipLaunchKernelGGL(k_preprocess<16>, grid, block, 0, s, c, A, splats, radii, tiles, vis_part, clr); break;
         default: throw std::invalid_argument("preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
-    if (row_int)  // the block counts in original order
-        hipLaunchKernelGGL(k_orig_block_counts, grid, block, 0, s, row_int, c.count, tiles, splats, vis_part);
+    if (row_int)  // the tile counts and the block counts in original order
+        hipLaunchKernelGGL(k_orig_block_counts, grid, block, 0, s, row_int, c.count, tiles, tiles_o, vis_part);
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
                        static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts, seq);
 }
@@ -922,7 +941,7 @@ void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena
                             int32_t* tiles, uint32_t* vis_part, unsigned long long* n_visible,
                             unsigned long long* block_base, unsigned long long isect_cap, unsigned long long* host_counts,
                             unsigned long long seq, const StepClear& clr, hipStream_t s, const int32_t* row_orig,
-                            const int32_t* row_int) {
+                            const int32_t* row_int, int32_t* tiles_o) {
     if (c.count <= 0) return;
     if (cu.count != c.count || cu.n_coeffs != c.n_coeffs)
         throw std::invalid_argument("update_preprocess: both steps must cover the same rows");
@@ -940,8 +959,8 @@ void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena
         default: throw std::invalid_argument("update_preprocess: SH coefficient count must be 1, 4, 9 or 16");
     }
 #undef SX_UPD
-    if (row_int)  // the block counts in original order
-        hipLaunchKernelGGL(k_orig_block_counts, grid, block, 0, s, row_int, c.count, tiles, splats, vis_part);
+    if (row_int)  // the tile counts and the block counts in original order
+        hipLaunchKernelGGL(k_orig_block_counts, grid, block, 0, s, row_int, c.count, tiles, tiles_o, vis_part);
     hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(kScanBlock), 0, s, reinterpret_cast<const uint4*>(vis_part),
                        static_cast<int>(grid.x), n_visible, block_base, isect_cap, host_counts, seq);
 }

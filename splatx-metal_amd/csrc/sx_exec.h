@@ -113,7 +113,7 @@ struct sxh_executor {
     bool permuted = false;
     int perm_count = 0;
     int64_t steps_since_exchange = 0;
-    sxh::DevBuf<int32_t> row_orig, row_int;
+    sxh::DevBuf<int32_t> row_orig, row_int, tiles_o;  // tiles_o: the tile counts in original order
     sxh::DevBuf<float> perm_scratch;
     int64_t last_max_tile = -1;      // the largest tile's entry count in the previous step (-1: none yet)
     int64_t last_long = -1;          // the previous training step's gather ranges past kLongRange (-1: none yet)

@@ -61,16 +61,19 @@ struct StepClear {
     int32_t* long_prev = nullptr;  // (when set) receives the previous step's long-range count first
 };
 // row_int (when set): the arena is in spatial order, row_int[o] the internal row of original row o; the
-// per-block counts the block scan reads are then taken again over original rows (for the compaction).
+// tile counts are then also written in original order into tiles_o, and the per-block counts the block
+// scan reads are taken again over original rows (for the compaction, which then reads tiles_o).
 void step_preprocess(const StepConst& c, const Arena& A, float4* splats, int32_t* radii, int32_t* tiles,
                      uint32_t* vis_part, unsigned long long* out_vis, unsigned long long* block_base,
                      unsigned long long isect_cap, unsigned long long* host_counts, unsigned long long seq,
-                     const StepClear& clr, hipStream_t s, const int32_t* row_int = nullptr);
+                     const StepClear& clr, hipStream_t s, const int32_t* row_int = nullptr,
+                     int32_t* tiles_o = nullptr);
 // number of blocks of step_preprocess
 int step_preprocess_blocks(int64_t count);
 // The Gaussians with tiles in index order (list[j], j below out_vis[2]) and (cum set) cum[j], the
 // inclusive sum of their tile counts: the positions of the index-first emit. row_int (the arena in
-// spatial order): the list runs in original order and holds internal rows.
+// spatial order): the list runs in original order and holds internal rows, and `tiles` must be the tile
+// counts in original order (the preprocess's tiles_o).
 void step_emit_compact(const StepConst& c, const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
                        int64_t* cum, hipStream_t s, const int32_t* row_int = nullptr);
 // depth-first intersections: depth keys of the listed Gaussians (values = index) for a stable 32-bit
@@ -133,7 +136,8 @@ void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena
                             int32_t* tiles, uint32_t* vis_part, unsigned long long* out_vis,
                             unsigned long long* block_base, unsigned long long isect_cap, unsigned long long* host_counts,
                             unsigned long long seq, const StepClear& clr, hipStream_t s,
-                            const int32_t* row_orig = nullptr, const int32_t* row_int = nullptr);
+                            const int32_t* row_orig = nullptr, const int32_t* row_int = nullptr,
+                            int32_t* tiles_o = nullptr);
 // The arena's spatial order (row_orig[k]: the original row of internal row k; row_int its inverse;
 // nothing is reordered past the live rows [0, count)). arena_morton_keys: keys[i] = the 30-bit Morton
 // code of row i's mean in the means' bounding box, vals[i] = i (scratch: arena_morton_scratch_floats).
