@@ -71,6 +71,7 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->stamp.alloc(1);
             e->max_tile.alloc(1);
             SXH_HIP(hipMemsetAsync(e->stamp.p, 0, sizeof(uint32_t), b->stream));
+            e->tie_count.alloc(1);
             e->touched.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
             e->dkey_a.alloc(R);
@@ -358,8 +359,17 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         sxh_detail::flush_update(e);
         spatial_order(e, c.count);
     }
+    // index-first sorts each tile's list by depth in one workgroup: fast while the tiles stay small
+    // (up to 2048 entries in LDS, larger ones through global scratch, correct at any size)
+    constexpr int64_t kIndexFirstMaxTile = 4096;
+    const bool index_first = e->isect_order == SXH_ISECT_ORDER_INDEX_FIRST ||
+                             (e->isect_order == SXH_ISECT_ORDER_AUTO && e->last_max_tile >= 0 &&
+                              e->last_max_tile <= kIndexFirstMaxTile);
+    // rows in spatial order: depth first compacts the visible rows in original order (its depth sort's
+    // ties then go by original row); index first compacts them in internal order, and the per-tile
+    // depth sort orders equal depths by original row
     const int32_t* const row_orig = e->permuted ? e->row_orig.p : nullptr;
-    const int32_t* const row_int = e->permuted ? e->row_int.p : nullptr;
+    const int32_t* const row_int = (e->permuted && !index_first) ? e->row_int.p : nullptr;
     // the last training step's deferred update rides on this step's preprocess when both cover the same
     // rows; a forward-only step (or another row count) applies it first
     if (e->update_pending && (fwd_only || e->pending_c.count != c.count)) sxh_detail::flush_update(e);
@@ -413,12 +423,6 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
     const int64_t* n_isects_dev = reinterpret_cast<const int64_t*>(e->n_vis.p) + 3;
     int n_l1 = 0, n_ss = 0;
     int32_t* flat = e->vals_a.p;
-    // index-first sorts each tile's list by depth in one workgroup: fast while the tiles stay small
-    // (up to 2048 entries in LDS, larger ones through global scratch, correct at any size)
-    constexpr int64_t kIndexFirstMaxTile = 4096;
-    const bool index_first = e->isect_order == SXH_ISECT_ORDER_INDEX_FIRST ||
-                             (e->isect_order == SXH_ISECT_ORDER_AUTO && e->last_max_tile >= 0 &&
-                              e->last_max_tile <= kIndexFirstMaxTile);
 
     // ---- segment B: everything after the count. With n_dev the launches read the intersection count on
     // the device (grids sized for the capacity), so they can be captured before the count is known.
@@ -453,6 +457,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         uint32_t* const edepth_b =
             index_first ? reinterpret_cast<uint32_t*>(e->keys_a.p) + e->isect_cap : nullptr;
         int which = 0;
+        // (index first with rows in spatial order: the offsets launch clears the depth sort's tie count)
+        uint32_t* const tie_zero = (index_first && row_orig) ? e->tie_count.p : nullptr;
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
             uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
@@ -461,7 +467,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);
             e->mark("sort");
-            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
+            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev, tie_zero);
         } else {
             uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
             uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
@@ -470,7 +476,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);
             e->mark("sort");
-            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
+            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev, tie_zero);
         }
         if (which < 0) throw std::runtime_error(std::string(what) + ": intersection capacity too large for a device count");
         if (e->debug_sort_error) sxk::step_set_word(sxk::sort_error_flag(e->sort_scratch.p), 1u, s);
@@ -480,9 +486,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             // the sorted tile keys are spent (the offsets are built): both key buffers and the other
             // value buffer are the scratch of tiles too large for LDS. The rasterisers' tile order comes
             // from one more workgroup of the same launch.
+            // (rows in spatial order: the emit ran in that order, and equal depths go by original row)
+            const sxk::TieOrder ties{e->tie_list.p, e->tie_count.p, e->emit_gid.p, row_orig, e->splats.p};
             sxk::tile_depth_sort(e->offsets.p, n_tiles, n_host, n_dev, nullptr, flat, which ? edepth_b : edepth,
                                  reinterpret_cast<uint32_t*>(e->keys_a.p), reinterpret_cast<uint32_t*>(e->keys_b.p),
-                                 which ? e->vals_a.p : e->vals_b.p, s, e->tile_order.p, e->max_tile.p);
+                                 which ? e->vals_a.p : e->vals_b.p, s, e->tile_order.p, e->max_tile.p,
+                                 row_orig ? &ties : nullptr);
             e->mark("tile_depth_sort");
         } else {
             sxk::raster_tile_order(e->offsets.p, n_tiles, n_host, e->tile_order.p, s, n_dev, e->max_tile.p);

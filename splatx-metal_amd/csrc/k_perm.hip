@@ -5,9 +5,10 @@
 // over every line, so each step streams the whole arena. Kept in the order of a Morton curve over the
 // means instead, the culled rows fill whole waves, which the update skips: the executor may hold the
 // live rows [0, count) in that order, with the maps between its internal rows and the caller's
-// (original) rows. Every result stays the caller's: the emit runs in original order (so do the stable
-// sorts' ties), the MCMC noise is drawn by original row, and every entry point that exchanges rows
-// with the caller restores the original order first.
+// (original) rows. Every result stays the caller's: depth first, the emit runs in original order (so
+// the stable depth sort's ties go by original row); index first, it runs in internal order and the
+// per-tile depth sort puts equal depths in original-row order; the MCMC noise is drawn by original row,
+// and every entry point that exchanges rows with the caller restores the original order first.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>

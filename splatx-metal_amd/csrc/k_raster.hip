@@ -1011,18 +1011,28 @@ __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const i
     for (int k = 0; k < kPartFloats; k++) v[k] = 0.f;
     for (int base = 0; base < total; base += kGatherStage) {  // uniform
         const int cnt = min(kGatherStage, total - base);
-        for (int i = lane; i < cnt; i += kGatherWave) {
+        // the round's entries, kGatherStage / kGatherWave per lane, loaded together (the lanes past the
+        // round's end load its last entry again) and then staged
+        constexpr int kPerLane = kGatherStage / kGatherWave;
+        float e[kPerLane][kPartFloats];
+        bool on[kPerLane];
+#pragma unroll
+        for (int u = 0; u < kPerLane; u++) {
             // the staged entry's owner: the last lane whose first staged entry is at or before it (lanes
             // that stage nothing share the next lane's offset, and the search passes over them)
-            const int k = base + i;
+            const int k = base + min(lane + u * kGatherWave, cnt - 1);
             int lo = 0;
 #pragma unroll
             for (int step = kGatherWave / 2; step > 0; step >>= 1)
                 if (s_off[lo + step] <= k) lo += step;
-            float e[kPartFloats];
-            const bool on = load_entry(part, s_src[lo] + (k - s_off[lo]), stamp, e);
+            on[u] = load_entry(part, s_src[lo] + (k - s_off[lo]), stamp, e[u]);
+        }
 #pragma unroll
-            for (int c = 0; c < kPartFloats; c++) s_rec[i][c] = on ? e[c] : 0.f;
+        for (int u = 0; u < kPerLane; u++) {
+            const int i = lane + u * kGatherWave;
+            if (i < cnt)
+#pragma unroll
+                for (int c = 0; c < kPartFloats; c++) s_rec[i][c] = on[u] ? e[u][c] : 0.f;
         }
         __syncthreads();
         const int a = max(off, base), b = min(off + n, base + cnt);

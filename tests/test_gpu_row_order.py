@@ -4,7 +4,7 @@ Every result must be the caller's-order result bit for bit: an executor forced i
 (SXH_ROW_ORDER_SPATIAL) and one kept in the caller's order (SXH_ROW_ORDER_ORIGINAL) must return the
 same losses and renders and, downloaded, the same parameters and moments, through steps with learning
 rates on, the MCMC position noise (drawn by original row), equal depths (the stable sorts' ties go by
-original row), both intersection orders, a change of the row count, uploads, checkpoints, PLY exports
+original row; index first, the per-tile depth sort puts them in that order), both intersection orders, a change of the row count, uploads, checkpoints, PLY exports
 and refines in between (each restores the caller's order; the next steps sort again)."""
 import math
 
@@ -64,6 +64,46 @@ def test_spatial_order_matches_original(gpu, isect_order):
         assert np.array_equal(x[3].view(np.uint32), y[3].view(np.uint32)), k
     assert same_state(sa, sb)
     assert not same_state(sa, scene.copy_state(sc))
+
+
+# index first, tiles of every size: ~16 k-entry tiles (the per-tile sort's global-scratch path) with a
+# fifth of the depths equal, one shared depth in large and in small tiles (the sort's all-equal case)
+TIE_CASES = {
+    "big_tiles_ties": (dict(n=20000, sh_degree=0, tie_frac=0.2, xy=0.6, log_scale_mu=math.log(0.1)), (64, 64, 60.0)),
+    "one_depth_big": (dict(n=20000, sh_degree=0, tie_frac=1.0, xy=0.6, log_scale_mu=math.log(0.1)), (64, 64, 60.0)),
+    "one_depth_small": (dict(n=3000, sh_degree=0, tie_frac=1.0), (96, 64, 90.0)),
+}
+
+
+@pytest.mark.parametrize("case", list(TIE_CASES))
+def test_spatial_order_index_first_ties(gpu, case):
+    """Index first, the visible rows are emitted in the internal (spatial) order: the per-tile depth sort
+    orders equal depths by original row, so the lists, renders and updates match the caller's order."""
+    skw, (w, h, fx) = TIE_CASES[case]
+    skw = dict(skw)
+    n, deg = skw.pop("n"), skw.pop("sh_degree")
+    sc = scene.make_scene(n=n, sh_degree=deg, width=w, height=h, fx=fx, seed=44, **skw)
+    runs = []
+    for order in (sh.SXH_ROW_ORDER_ORIGINAL, sh.SXH_ROW_ORDER_SPATIAL):
+        print(f"{case}, row order {order}", flush=True)
+        ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=0.2,
+                                          isect_mode=sh.SXH_ISECT_AABB)
+        ex.set_row_order(order)
+        ex.set_isect_order(sh.SXH_ISECT_ORDER_INDEX_FIRST)
+        ex.upload_params(*scene.copy_state(sc), sc.n)
+        out = []
+        for a in (0.0, 1.5, -1.0):
+            r = ex.step(want_render=True, **dict(scene.step_kwargs(sc), viewmat=roty(a), gt_rgb=sc.gt))
+            out.append((r["loss"], r["n_isects"], r["render_colors"].copy()))
+        state = scene.copy_state(sc)
+        ex.download_params(*state, sc.n)
+        ex.close()
+        runs.append((out, state))
+    (oa, sa), (ob, sb) = runs
+    for k, (x, y) in enumerate(zip(oa, ob)):
+        assert x[:2] == y[:2] and x[1] > 0, (case, k, x[:2], y[:2])
+        assert np.array_equal(x[2].view(np.uint32), y[2].view(np.uint32)), (case, k)
+    assert same_state(sa, sb), case
 
 
 def test_spatial_order_through_exchanges(gpu, tmp_path):
