@@ -78,7 +78,8 @@ TIE_CASES = {
 @pytest.mark.parametrize("case", list(TIE_CASES))
 def test_spatial_order_index_first_ties(gpu, case):
     """Index first, the visible rows are emitted in the internal (spatial) order: the per-tile depth sort
-    orders equal depths by original row, so the lists, renders and updates match the caller's order."""
+    orders equal depths by original row, so the lists, renders (a forward-only one among them) and updates
+    match the caller's order."""
     skw, (w, h, fx) = TIE_CASES[case]
     skw = dict(skw)
     n, deg = skw.pop("n"), skw.pop("sh_degree")
@@ -95,6 +96,11 @@ def test_spatial_order_index_first_ties(gpu, case):
         for a in (0.0, 1.5, -1.0):
             r = ex.step(want_render=True, **dict(scene.step_kwargs(sc), viewmat=roty(a), gt_rgb=sc.gt))
             out.append((r["loss"], r["n_isects"], r["render_colors"].copy()))
+        # a forward-only render in between (the rows stay in spatial order; the pending update applied)
+        r = ex.step(want_render=True, forward_only=True, **dict(scene.step_kwargs(sc), viewmat=roty(0.5)))
+        out.append((0.0, r["n_isects"], r["render_colors"].copy()))
+        r = ex.step(want_render=True, **dict(scene.step_kwargs(sc), viewmat=roty(2.0), gt_rgb=sc.gt))
+        out.append((r["loss"], r["n_isects"], r["render_colors"].copy()))
         state = scene.copy_state(sc)
         ex.download_params(*state, sc.n)
         ex.close()
