@@ -688,8 +688,8 @@ int32_t sxh_exec_set_isect_order(sxh_executor* e, int32_t mode);
  * the means, so that the rows a camera culls fill whole waves that the parameter update skips;
  * SXH_ROW_ORDER_ORIGINAL: always the caller's order; SXH_ROW_ORDER_SPATIAL: along the curve from the
  * next training step on, at any size. Every result is the same bit for bit in every mode (the
- * intersections are emitted, and the MCMC noise drawn, by original row; every call that exchanges
- * rows restores the caller's order first). No counterpart in the reference (a layout choice of this
+ * intersection lists order equal depths, and the MCMC noise is drawn, by original row; every call that
+ * exchanges rows restores the caller's order first). No counterpart in the reference (a layout choice of this
  * backend). */
 #define SXH_ROW_ORDER_SPATIAL_AUTO 0
 #define SXH_ROW_ORDER_ORIGINAL 1
