@@ -71,7 +71,6 @@ int32_t sxh_exec_create(sxh_backend* b, const sxh_exec_desc* desc, sxh_executor*
             e->stamp.alloc(1);
             e->max_tile.alloc(1);
             SXH_HIP(hipMemsetAsync(e->stamp.p, 0, sizeof(uint32_t), b->stream));
-            e->tie_count.alloc(1);
             e->touched.alloc(R);
             e->scan_scratch.alloc(sxk::scan_scratch_bytes(static_cast<int64_t>(R)));
             e->dkey_a.alloc(R);
@@ -457,8 +456,6 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         uint32_t* const edepth_b =
             index_first ? reinterpret_cast<uint32_t*>(e->keys_a.p) + e->isect_cap : nullptr;
         int which = 0;
-        // (index first with rows in spatial order: the offsets launch clears the depth sort's tie count)
-        uint32_t* const tie_zero = (index_first && row_orig) ? e->tie_count.p : nullptr;
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
             uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
@@ -467,7 +464,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);
             e->mark("sort");
-            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev, tie_zero);
+            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         } else {
             uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
             uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
@@ -476,7 +473,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);
             e->mark("sort");
-            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev, tie_zero);
+            sxk::step_tile_offsets(which ? kb : ka, n_host, n_tiles, e->offsets.p, s, n_dev);
         }
         if (which < 0) throw std::runtime_error(std::string(what) + ": intersection capacity too large for a device count");
         if (e->debug_sort_error) sxk::step_set_word(sxk::sort_error_flag(e->sort_scratch.p), 1u, s);
@@ -487,7 +484,7 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             // value buffer are the scratch of tiles too large for LDS. The rasterisers' tile order comes
             // from one more workgroup of the same launch.
             // (rows in spatial order: the emit ran in that order, and equal depths go by original row)
-            const sxk::TieOrder ties{e->tie_list.p, e->tie_count.p, e->emit_gid.p, row_orig, e->splats.p};
+            const sxk::TieOrder ties{e->emit_gid.p, row_orig, e->splats.p};
             sxk::tile_depth_sort(e->offsets.p, n_tiles, n_host, n_dev, nullptr, flat, which ? edepth_b : edepth,
                                  reinterpret_cast<uint32_t*>(e->keys_a.p), reinterpret_cast<uint32_t*>(e->keys_b.p),
                                  which ? e->vals_a.p : e->vals_b.p, s, e->tile_order.p, e->max_tile.p,

@@ -1044,7 +1044,7 @@ __device__ __forceinline__ uint32_t wave_starts(uint32_t (*s_woff)[kBins], uint3
     return run;
 }
 
-// equal depths: runs up to this long are ordered by the sort's own threads, longer ones by k_tile_tie_order
+// equal depths: runs up to this long are put in order in place, a tile with a longer one is sorted again
 constexpr int kTieRun = 32;
 
 // The run of keys equal to keys[i] that starts at i when one does (the key before differs, the next one
@@ -1066,13 +1066,17 @@ __device__ __forceinline__ int32_t tie_run_end(const uint32_t* keys, int32_t i, 
 // order_out (optional): workgroup 0 writes the rasterisers' tile order there instead (and the largest
 // tile's count into *max_count), beside the sorting workgroups, which then take tile blockIdx.x - 1: the
 // per-tile sorts gain nothing from running heaviest first, and the order costs no launch of its own.
-// tie_list (optional, with tie_count, id_of and row_orig): the lists are in an internal row order whose
-// equal depths must go by original row (row_orig[id_of[value]]). After the depth sort, equal depths are
-// runs of adjacent entries: a run of up to kTieRun entries is put in that order by the thread at its
-// start (an insertion sort in LDS, or in global scratch for the large tiles); a tile with a longer run
-// is appended to tie_list for k_tile_tie_order. One compare per entry for tiles without equal depths.
+// row_orig (optional, with id_of and splats): the lists are in an internal row order whose equal depths
+// must go by original row (row_orig[id_of[value]]). After the depth sort, equal depths are runs of
+// adjacent entries: a run of up to kTieRun entries is put in that order by the thread at its start (an
+// insertion sort in LDS, or in global scratch for the large tiles); a tile with a longer run, or with
+// one depth, is sorted again through global scratch, LSD by its original rows' varying bytes, then by
+// its depth bytes (an entry's depth is word 3 of its Gaussian's splat record, splats[3 id_of[value]].w,
+// the key the emit wrote). One compare per entry for tiles without equal depths. (The occupancy target
+// of 7 waves per SIMD, which the LDS allows, keeps the register allocation of the tie work within it:
+// without it 75 VGPRs, 6 waves.)
 template <int RMAX>
-__global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles,
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7))) k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles,
                                                               int32_t n_isects, const int64_t* __restrict__ n_dev,
                                                               const int32_t* __restrict__ tile_order,
                                                               int32_t* __restrict__ vals,
@@ -1080,10 +1084,9 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
                                                               uint32_t* __restrict__ sk0, uint32_t* __restrict__ sk1,
                                                               int32_t* __restrict__ sv, int32_t* __restrict__ order_out,
                                                               uint32_t* __restrict__ max_count,
-                                                              int32_t* __restrict__ tie_list,
-                                                              uint32_t* __restrict__ tie_count,
                                                               const int32_t* __restrict__ id_of,
-                                                              const int32_t* __restrict__ row_orig) {
+                                                              const int32_t* __restrict__ row_orig,
+                                                              const float4* __restrict__ splats) {
     constexpr int kCap = kWaves * 64 * RMAX;
     __shared__ uint32_t s_key[kCap];
     __shared__ int32_t s_val[kCap];
@@ -1105,7 +1108,13 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
     const int32_t nt = (t + 1 < n_tiles ? offsets[t + 1] : n_all) - start;
     if (nt <= 1) return;  // uniform
     int32_t* const seg = vals + start;
+    const bool by_orig = row_orig != nullptr;
     auto orig_of = [&](int32_t v) -> uint32_t { return static_cast<uint32_t>(row_orig[id_of[v]]); };
+    auto depth_of = [&](int32_t v) -> uint32_t { return __float_as_uint(splats[3 * (size_t)id_of[v]].w); };
+    // with row_orig, a tile with a run of equal depths longer than kTieRun (or with one depth) is sorted
+    // again through global scratch (the large tiles' path): stage 1 by its original rows, stage 2 by its
+    // depth bits
+    int stage = 0;
     uint32_t key[RMAX];
     int32_t val[RMAX];
     uint32_t off[RMAX];
@@ -1131,10 +1140,8 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
             }
         }
         const uint32_t diff = block_key_diff(a, o, s_and, s_or);
-        if (diff == 0u) {  // one depth: the index order stands
-            if (tie_list && tid == 0) tie_list[atomicAdd(tie_count, 1u)] = t;  // (one run: the tie launch's)
-            return;
-        }
+        if (diff == 0u && !by_orig) return;  // one depth: the index order stands
+        if (diff == 0u) stage = 1;  // (one run: by original row alone)
         for (int p = 0; p < 4; p++) {
             const int shift = 8 * p;
             if (((diff >> shift) & 255u) == 0u) continue;  // uniform: every key has this byte
@@ -1170,7 +1177,7 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
             }
             __syncthreads();
         }
-        if (tie_list) {
+        if (by_orig && stage == 0) {
             // equal depths are adjacent now: each key against the one before it, from the lane below (DPP
             // wave shift) or, for lane 0, the wave's previous round
             int tie = 0;
@@ -1199,7 +1206,7 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
                     }
                 }
                 if (__syncthreads_or(long_run)) {
-                    if (tid == 0) tie_list[atomicAdd(tie_count, 1u)] = t;
+                    stage = 1;  // (the whole tile again, from the values as loaded: any order will do)
                 } else {
                     // the thread at a run's start replaces its keys (all equal) with the entries' original
                     // rows and sorts them with the values
@@ -1230,166 +1237,54 @@ __global__ void __launch_bounds__(kThreads) k_tile_depth_sort(const int32_t* __r
                 }
             }
         }
+        if (stage == 0) {
 #pragma unroll
-        for (int r = 0; r < RMAX; r++) {
-            const int i = wb + r * 64 + lane;
-            if (r < R && i < nt) seg[i] = val[r];
+            for (int r = 0; r < RMAX; r++) {
+                const int i = wb + r * 64 + lane;
+                if (r < R && i < nt) seg[i] = val[r];
+            }
+            return;
         }
-        return;
     }
     {
-        // a tile of more than kCap entries: the keys go to sk0, then each pass moves (key, value) between
-        // (sk0, vals) and (sk1, sv) over the tile's range, chunk by chunk in list order
-        uint32_t a = ~0u, o = 0u;
-        for (int32_t i = tid; i < nt; i += kThreads) {
-            const uint32_t k = sdepth[start + i];
-            sk0[start + i] = k;
-            a &= k;
-            o |= k;
-        }
-        const uint32_t diff = block_key_diff(a, o, s_and, s_or);  // (its barrier also orders the sk0 stores)
-        const uint32_t* src_k = sk0 + start;
-        const int32_t* src_v = seg;
-        uint32_t* dst_k = sk1 + start;
-        int32_t* dst_v = sv + start;
-        constexpr int kPerWave = kCap / kWaves;
-        for (int p = 0; p < 4; p++) {
-            const int shift = 8 * p;
-            if (((diff >> shift) & 255u) == 0u) continue;  // uniform
-            s_base[tid] = 0;
-            __syncthreads();
-            for (int32_t i = tid; i < nt; i += kThreads) atomicAdd(&s_base[(src_k[i] >> shift) & 255u], 1u);
-            __syncthreads();
-            {
-                uint32_t all = 0;
-                const uint32_t b = block_excl_scan_u32(s_base[tid], s_wave, &all);
-                s_base[tid] = b;  // every thread has read its own digit's count above
-            }
-            __syncthreads();
-            for (int32_t c0 = 0; c0 < nt; c0 += kCap) {  // uniform
-                const int cn = static_cast<int>(min<int32_t>(kCap, nt - c0));
-                const int wb = wave * kPerWave;
-#pragma unroll
-                for (int r = 0; r < RMAX; r++) {
-                    const int i = wb + r * 64 + lane;
-                    key[r] = i < cn ? src_k[c0 + i] : 0u;
-                    val[r] = i < cn ? src_v[c0 + i] : 0;
-                }
-#pragma unroll
-                for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
-                __syncthreads();
-                wave_rank_byte<RMAX>(key, RMAX, wb, cn, shift, s_woff[wave], off);
-                __syncthreads();
-                s_base[tid] = wave_starts(s_woff, s_base[tid]);
-                __syncthreads();
-#pragma unroll
-                for (int r = 0; r < RMAX; r++) {
-                    if (wb + r * 64 + lane < cn) {
-                        const uint32_t pos = s_woff[wave][(key[r] >> shift) & 255u] + off[r];
-                        dst_k[pos] = key[r];
-                        dst_v[pos] = val[r];
-                    }
-                }
-                __syncthreads();  // s_woff is cleared for the next chunk; the next pass reads these stores
-            }
-            const uint32_t* tk = src_k;
-            src_k = dst_k;
-            dst_k = const_cast<uint32_t*>(tk);
-            const int32_t* tv = src_v;
-            src_v = dst_v;
-            dst_v = const_cast<int32_t*>(tv);
-        }
-        if (tie_list) {
-            // as in LDS: runs of up to kTieRun fixed by the thread at their start (the original rows in
-            // dst_k, the keys in src_k left for the other threads' run search), longer ones listed (one run
-            // of the whole tile when no byte differs)
-            int tie = 0, long_run = diff == 0u;
-            if (!long_run) {
-                for (int32_t i = tid; i < nt; i += kThreads) {
-                    const int32_t len = tie_run_end(src_k, i, nt) - i;
-                    tie |= len > 0;
-                    long_run |= len > kTieRun;
-                }
-            }
-            if (__syncthreads_or(long_run)) {
-                if (tid == 0) tie_list[atomicAdd(tie_count, 1u)] = t;
-            } else if (__syncthreads_or(tie)) {
-                int32_t* const v = const_cast<int32_t*>(src_v);
-                for (int32_t i = tid; i < nt; i += kThreads) {
-                    const int32_t e = tie_run_end(src_k, i, nt);
-                    for (int32_t m = i; m < e; m++) dst_k[m] = orig_of(v[m]);
-                    for (int32_t m = i + 1; m < e; m++) {
-                        const uint32_t km = dst_k[m];
-                        const int32_t vm = v[m];
-                        int32_t q = m;
-                        for (; q > i && dst_k[q - 1] > km; q--) {
-                            dst_k[q] = dst_k[q - 1];
-                            v[q] = v[q - 1];
-                        }
-                        dst_k[q] = km;
-                        v[q] = vm;
-                    }
-                }
-                __syncthreads();  // the copy below reads other threads' runs
-            }
-        }
-        if (src_v != seg)
-            for (int32_t i = tid; i < nt; i += kThreads) seg[i] = src_v[i];
-    }
-}
-
-// Equal depths by original row for the tiles k_tile_depth_sort listed (a run of equal depths longer
-// than kTieRun; the lists sorted by depth, equal depths in the order of the arena's internal rows), one
-// workgroup per tile in turn: each tile is sorted again through global memory, LSD, by its original rows'
-// varying bytes (row_orig[id_of[value]]), then by the depth bytes (an entry's depth is word 3 of its
-// Gaussian's splat record, splats[3 id_of[value]].w, the emit's key), the passes moving (key, value)
-// between (sk0, vals) and (sk1, sv). *tie_count: the list's length.
-template <int RMAX>
-__global__ void __launch_bounds__(kThreads) k_tile_tie_order(const int32_t* __restrict__ offsets, int n_tiles,
-                                                             int32_t n_isects, const int64_t* __restrict__ n_dev,
-                                                             int32_t* __restrict__ vals, uint32_t* __restrict__ sk0,
-                                                             uint32_t* __restrict__ sk1, int32_t* __restrict__ sv,
-                                                             const int32_t* __restrict__ tie_list,
-                                                             const uint32_t* __restrict__ tie_count,
-                                                             const int32_t* __restrict__ id_of,
-                                                             const int32_t* __restrict__ row_orig,
-                                                             const float4* __restrict__ splats) {
-    constexpr int kCap = kWaves * 64 * RMAX;
-    constexpr int kPerWave = kCap / kWaves;
-    __shared__ uint32_t s_woff[kWaves][kBins];
-    __shared__ uint32_t s_base[kBins];
-    __shared__ uint32_t s_wave[kWaves];
-    __shared__ uint32_t s_and[kWaves], s_or[kWaves];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int32_t n_all = n_dev ? static_cast<int32_t>(*n_dev) : n_isects;
-    const uint32_t n_list = *tie_count;
-    auto orig_of = [&](int32_t v) -> uint32_t { return static_cast<uint32_t>(row_orig[id_of[v]]); };
-    auto depth_of = [&](int32_t v) -> uint32_t { return __float_as_uint(splats[3 * (size_t)id_of[v]].w); };
-    uint32_t key[RMAX];
-    int32_t val[RMAX];
-    uint32_t off[RMAX];
-    for (uint32_t q = blockIdx.x; q < n_list; q += gridDim.x) {  // uniform
-        const int t = tie_list[q];
-        const int32_t start = offsets[t];
-        const int32_t nt = (t + 1 < n_tiles ? offsets[t + 1] : n_all) - start;
-        int32_t* const seg = vals + start;
-        // the whole tile again: keys = the original rows, sorted; keys = the depth bits, sorted
+        // a tile of more than kCap entries (or one sorted again by original row): the keys go to sk0, then
+        // each pass moves (key, value) between (sk0, vals) and (sk1, sv) over the tile's range, chunk by
+        // chunk in list order
         uint32_t* src_k = sk0 + start;
         int32_t* src_v = seg;
         uint32_t* dst_k = sk1 + start;
         int32_t* dst_v = sv + start;
-        for (int stage = 0; stage < 2; stage++) {
+        uint32_t todo = 0u;
+        if (stage == 0) {
             uint32_t a = ~0u, o = 0u;
             for (int32_t i = tid; i < nt; i += kThreads) {
-                const uint32_t k = stage == 0 ? orig_of(src_v[i]) : depth_of(src_v[i]);
-                src_k[i] = k;
+                const uint32_t k = sdepth[start + i];
+                sk0[start + i] = k;
                 a &= k;
                 o |= k;
             }
-            const uint32_t diff = block_key_diff(a, o, s_and, s_or);  // (orders the key stores)
+            todo = block_key_diff(a, o, s_and, s_or);  // (its barrier also orders the sk0 stores)
+            if (todo == 0u && by_orig) stage = 1;
+        }
+        // (chunks of half the LDS path's rounds: this path's registers stay within the LDS path's)
+        constexpr int kRG = RMAX / 2 > 0 ? RMAX / 2 : 1;
+        constexpr int kChunk = kWaves * 64 * kRG;
+        constexpr int kPerWave = kChunk / kWaves;
+        for (;;) {
+            if (stage > 0) {
+                // the keys (scratch) replaced: 1 the entries' original rows, 2 their depth bits again
+                uint32_t a = ~0u, o = 0u;
+                for (int32_t i = tid; i < nt; i += kThreads) {
+                    const uint32_t k = stage == 1 ? orig_of(src_v[i]) : depth_of(src_v[i]);
+                    src_k[i] = k;
+                    a &= k;
+                    o |= k;
+                }
+                todo = block_key_diff(a, o, s_and, s_or);  // (orders the key stores)
+            }
             for (int p = 0; p < 4; p++) {
                 const int shift = 8 * p;
-                if (((diff >> shift) & 255u) == 0u) continue;  // uniform
+                if (((todo >> shift) & 255u) == 0u) continue;  // uniform
                 s_base[tid] = 0;
                 __syncthreads();
                 for (int32_t i = tid; i < nt; i += kThreads) atomicAdd(&s_base[(src_k[i] >> shift) & 255u], 1u);
@@ -1397,14 +1292,14 @@ __global__ void __launch_bounds__(kThreads) k_tile_tie_order(const int32_t* __re
                 {
                     uint32_t all = 0;
                     const uint32_t b = block_excl_scan_u32(s_base[tid], s_wave, &all);
-                    s_base[tid] = b;
+                    s_base[tid] = b;  // every thread has read its own digit's count above
                 }
                 __syncthreads();
-                for (int32_t c0 = 0; c0 < nt; c0 += kCap) {  // uniform
-                    const int cn = static_cast<int>(min<int32_t>(kCap, nt - c0));
+                for (int32_t c0 = 0; c0 < nt; c0 += kChunk) {  // uniform
+                    const int cn = static_cast<int>(min<int32_t>(kChunk, nt - c0));
                     const int wb = wave * kPerWave;
 #pragma unroll
-                    for (int r = 0; r < RMAX; r++) {
+                    for (int r = 0; r < kRG; r++) {
                         const int i = wb + r * 64 + lane;
                         key[r] = i < cn ? src_k[c0 + i] : 0u;
                         val[r] = i < cn ? src_v[c0 + i] : 0;
@@ -1412,19 +1307,19 @@ __global__ void __launch_bounds__(kThreads) k_tile_tie_order(const int32_t* __re
 #pragma unroll
                     for (int w = 0; w < kWaves; w++) s_woff[w][tid] = 0;
                     __syncthreads();
-                    wave_rank_byte<RMAX>(key, RMAX, wb, cn, shift, s_woff[wave], off);
+                    wave_rank_byte<kRG>(key, kRG, wb, cn, shift, s_woff[wave], off);
                     __syncthreads();
                     s_base[tid] = wave_starts(s_woff, s_base[tid]);
                     __syncthreads();
 #pragma unroll
-                    for (int r = 0; r < RMAX; r++) {
+                    for (int r = 0; r < kRG; r++) {
                         if (wb + r * 64 + lane < cn) {
                             const uint32_t pos = s_woff[wave][(key[r] >> shift) & 255u] + off[r];
                             dst_k[pos] = key[r];
                             dst_v[pos] = val[r];
                         }
                     }
-                    __syncthreads();
+                    __syncthreads();  // s_woff is cleared for the next chunk; the next pass reads these stores
                 }
                 uint32_t* tk = src_k;
                 src_k = dst_k;
@@ -1433,10 +1328,45 @@ __global__ void __launch_bounds__(kThreads) k_tile_tie_order(const int32_t* __re
                 src_v = dst_v;
                 dst_v = tv;
             }
+            if (!by_orig || stage == 2) break;
+            if (stage == 1) {
+                stage = 2;
+                continue;
+            }
+            // stage 0, as in LDS: runs of up to kTieRun fixed by the thread at their start (the original rows
+            // in dst_k, the keys in src_k left for the other threads' run search), longer ones sorted again
+            int tie = 0, long_run = 0;
+            for (int32_t i = tid; i < nt; i += kThreads) {
+                const int32_t len = tie_run_end(src_k, i, nt) - i;
+                tie |= len > 0;
+                long_run |= len > kTieRun;
+            }
+            if (__syncthreads_or(long_run)) {
+                stage = 1;
+                continue;
+            }
+            if (__syncthreads_or(tie)) {
+                for (int32_t i = tid; i < nt; i += kThreads) {
+                    const int32_t e = tie_run_end(src_k, i, nt);
+                    for (int32_t m = i; m < e; m++) dst_k[m] = orig_of(src_v[m]);
+                    for (int32_t m = i + 1; m < e; m++) {
+                        const uint32_t km = dst_k[m];
+                        const int32_t vm = src_v[m];
+                        int32_t q = m;
+                        for (; q > i && dst_k[q - 1] > km; q--) {
+                            dst_k[q] = dst_k[q - 1];
+                            src_v[q] = src_v[q - 1];
+                        }
+                        dst_k[q] = km;
+                        src_v[q] = vm;
+                    }
+                }
+                __syncthreads();  // the copy below reads other threads' runs
+            }
+            break;
         }
         if (src_v != seg)
             for (int32_t i = tid; i < nt; i += kThreads) seg[i] = src_v[i];
-        __syncthreads();
     }
 }
 
@@ -1482,25 +1412,18 @@ int radix_sort_positions(uint32_t* keys_a, int32_t* vals_a, uint32_t* keys_b, in
 }
 
 constexpr int kDepthSortRounds = 8;
-constexpr int kTieGrid = 64;
 
 void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
                      const int32_t* tile_order, int32_t* vals, const uint32_t* sdepth, uint32_t* scratch_k0,
                      uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s, int32_t* order_out,
                      uint32_t* max_count, const TieOrder* ties) {
     if (n_tiles <= 0 || (!order_out && !n_dev && n_isects <= 1)) return;
-    if (ties && (!ties->list || !ties->count || !ties->id_of || !ties->row_orig || !ties->splats))
+    if (ties && (!ties->id_of || !ties->row_orig || !ties->splats))
         throw std::invalid_argument("tile_depth_sort: incomplete tie order arguments");
     hipLaunchKernelGGL(k_tile_depth_sort<kDepthSortRounds>, dim3(n_tiles + (order_out ? 1 : 0)), dim3(kThreads), 0,
                        s, offsets, n_tiles, static_cast<int32_t>(n_isects), n_dev, tile_order, vals, sdepth,
-                       scratch_k0, scratch_k1, scratch_v, order_out, max_count, ties ? ties->list : nullptr,
-                       ties ? ties->count : nullptr, ties ? ties->id_of : nullptr, ties ? ties->row_orig : nullptr);
-    if (!ties) return;
-    // the tiles with equal depths, a few per launch: a small grid takes them in turn
-    const int grid = std::min(n_tiles, kTieGrid);
-    hipLaunchKernelGGL(k_tile_tie_order<kDepthSortRounds>, dim3(grid), dim3(kThreads), 0, s, offsets, n_tiles,
-                       static_cast<int32_t>(n_isects), n_dev, vals, scratch_k0, scratch_k1, scratch_v, ties->list,
-                       ties->count, ties->id_of, ties->row_orig, ties->splats);
+                       scratch_k0, scratch_k1, scratch_v, order_out, max_count, ties ? ties->id_of : nullptr,
+                       ties ? ties->row_orig : nullptr, ties ? ties->splats : nullptr);
 }
 
 void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_out, int32_t* vals_out,

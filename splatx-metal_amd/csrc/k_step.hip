@@ -575,9 +575,7 @@ constexpr int kOffPer = 8;  // positions per thread of the pass
 template <class K>
 __global__ void __launch_bounds__(kBlock) k_tile_offsets_pass(const K* __restrict__ keys, int64_t n, int n_tiles,
                                                               int32_t* __restrict__ off,
-                                                              const int64_t* __restrict__ n_dev,
-                                                              uint32_t* __restrict__ zero_word) {
-    if (zero_word && blockIdx.x == 0 && threadIdx.x == 0) *zero_word = 0u;
+                                                              const int64_t* __restrict__ n_dev) {
     if (n_dev) n = *n_dev;
     const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * kOffPer;
     if (i0 > n) return;
@@ -594,10 +592,8 @@ __global__ void __launch_bounds__(kBlock) k_tile_offsets_pass(const K* __restric
 
 template <class K>
 __global__ void __launch_bounds__(kBlock) k_tile_offsets(const K* __restrict__ keys, int64_t n, int n_tiles,
-                                                         int32_t* __restrict__ off, const int64_t* __restrict__ n_dev,
-                                                         uint32_t* __restrict__ zero_word) {
+                                                         int32_t* __restrict__ off, const int64_t* __restrict__ n_dev) {
     const int t = blockIdx.x * kBlock + threadIdx.x;
-    if (zero_word && t == 0) *zero_word = 0u;
     if (t >= n_tiles) return;
     if (n_dev) n = *n_dev;
     int64_t lo = 0, hi = n;
@@ -918,26 +914,26 @@ void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* r
 constexpr int64_t kOffPassMax = int64_t{1} << 25;
 template <class K>
 static void launch_tile_offsets(const K* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
-                                const int64_t* n_dev, uint32_t* zero_word) {
+                                const int64_t* n_dev) {
     if (n_tiles <= 0) return;
     if (n <= kOffPassMax) {
         const int64_t threads = n / kOffPer + 1;  // positions 0..n
         hipLaunchKernelGGL(k_tile_offsets_pass<K>, dim3(grid_for(threads)), dim3(kBlock), 0, s, keys, n, n_tiles,
-                           offsets, n_dev, zero_word);
+                           offsets, n_dev);
     } else {
         hipLaunchKernelGGL(k_tile_offsets<K>, dim3(grid_for(n_tiles)), dim3(kBlock), 0, s, keys, n, n_tiles, offsets,
-                           n_dev, zero_word);
+                           n_dev);
     }
 }
 
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
-                       const int64_t* n_dev, uint32_t* zero_word) {
-    launch_tile_offsets(keys, n, n_tiles, offsets, s, n_dev, zero_word);
+                       const int64_t* n_dev) {
+    launch_tile_offsets(keys, n, n_tiles, offsets, s, n_dev);
 }
 
 void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
-                       const int64_t* n_dev, uint32_t* zero_word) {
-    launch_tile_offsets(keys, n, n_tiles, offsets, s, n_dev, zero_word);
+                       const int64_t* n_dev) {
+    launch_tile_offsets(keys, n, n_tiles, offsets, s, n_dev);
 }
 
 void step_update_preprocess(const StepConst& cu, const StepConst& c, const Arena& A, float4* splats, const float4* grads,

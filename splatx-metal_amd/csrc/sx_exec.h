@@ -73,8 +73,6 @@ struct sxh_executor {
     // image-sized buffers
     size_t img_px = 0, img_tiles = 0, img_map = 0;
     sxh::DevBuf<int32_t> offsets, last_ids, tile_order, mask_end;
-    sxh::DevBuf<int32_t> tie_list;  // index first, rows in spatial order: the tiles with equal depths
-    sxh::DevBuf<uint32_t> tie_count;  // their count (zeroed by the step's tile offsets launch)
     sxh::DevBuf<float> render, alpha, v_render, v_alpha_zero, gt_stage;
     sxh::DevBuf<float> cmu, csg, ccr;  // SSIM coefficient maps (the map itself is only summed)
     sxh::DevBuf<double> ssim_part, l1_part;
@@ -186,7 +184,6 @@ struct sxh_executor {
         if (tiles_n > img_tiles) {
             offsets.alloc(tiles_n);
             tile_order.alloc(tiles_n);
-            tie_list.alloc(tiles_n);
             mask_end.alloc(tiles_n);
             img_tiles = tiles_n;
         }

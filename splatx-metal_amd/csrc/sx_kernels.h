@@ -109,12 +109,9 @@ void radix_sort_into(const uint64_t* keys, const int32_t* vals, uint64_t* keys_o
 // what the sorts before it left, so several sorts in a row can be checked with one read.
 uint32_t* sort_error_flag(void* scratch);
 // Equal depths by original row in index-first lists whose Gaussians are numbered in an internal row
-// order: list (one int32 per tile) and *count (zero when the sort starts) are the sort's own state; the
-// order of equal depths is row_orig[id_of[value]], and an entry's depth is word 3 of its Gaussian's
-// splat record, splats[3 id_of[value]].w (the emit's key).
+// order: the order of equal depths is row_orig[id_of[value]], and an entry's depth is word 3 of its
+// Gaussian's splat record, splats[3 id_of[value]].w (the emit's key).
 struct TieOrder {
-    int32_t* list;
-    uint32_t* count;
     const int32_t* id_of;
     const int32_t* row_orig;
     const float4* splats;
@@ -128,8 +125,7 @@ struct TieOrder {
 // the count long; none of them may overlap sdepth). order_out (optional): the launch also writes the
 // rasterisers' tile order (raster_tile_order's, from the same offsets) there and the largest tile's
 // count into *max_count, from one extra workgroup; the tiles are then sorted in index order. ties
-// (optional): equal depths go by original row instead of index (a second launch puts the tiles that
-// have equal depths in that order).
+// (optional): equal depths go by original row instead of index (work only tiles with equal depths do).
 void tile_depth_sort(const int32_t* offsets, int n_tiles, int64_t n_isects, const int64_t* n_dev,
                      const int32_t* tile_order, int32_t* vals, const uint32_t* sdepth, uint32_t* scratch_k0,
                      uint32_t* scratch_k1, int32_t* scratch_v, hipStream_t s, int32_t* order_out = nullptr,

@@ -91,12 +91,11 @@ void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* r
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
                       const int64_t* cum, const unsigned long long* n_pos, uint32_t* keys, int32_t* vals,
                       hipStream_t s, uint32_t* edepth = nullptr);
-// n_dev: the key count on the device, read instead of n. zero_word (optional): set to 0 by the launch
-// (the per-tile depth sort's tie count, which must be zero when that sort starts)
+// n_dev: the key count on the device, read instead of n
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
-                       const int64_t* n_dev = nullptr, uint32_t* zero_word = nullptr);
+                       const int64_t* n_dev = nullptr);
 void step_tile_offsets(const uint32_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
-                       const int64_t* n_dev = nullptr, uint32_t* zero_word = nullptr);
+                       const int64_t* n_dev = nullptr);
 // The words a step reports to the host, stored straight into mapped host memory (host: 4 u32, the loss
 // bits, the sort's error flag, the largest tile's entry count, the gather's long-range count (0 when
 // long_count is null)) instead of one copy each, then `seq` into *seq_host (release order: a host that
