@@ -40,14 +40,11 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
     pd = 3 + 4 + 3 + 1 + 3 + (sh_k - 1) * 3  # parameter floats per Gaussian (59 at SH3)
     kb = shape["key_b"]
     if shape.get("index_first"):
-        if name == "scan":
-            # the compaction: every Gaussian's tile count (4 B) in, the list of those with tiles (4 B) and
-            # their inclusive offsets (8 B) out
-            return 4.0 * n + 12.0 * v
         if name == "emit":
-            # list (4 B) and offset (8 B) per Gaussian, its 32-B conic/mean record; per entry the tile id,
-            # the Gaussian (4 B) and its depth bits (4 B) out
-            return v * (12.0 + 32.0) + i * (kb + 8.0)
+            # the compaction in the same launch: every Gaussian's tile count (4 B) in, the list of those with
+            # tiles (4 B) and their inclusive offsets (8 B) out; their 32-B conic/mean record; per entry the
+            # tile id, the Gaussian (4 B) and its depth bits (4 B) out
+            return 4.0 * n + v * (12.0 + 32.0) + i * (kb + 8.0)
         if name == "tile_depth_sort":
             # per entry: the emit position in and out (8 B), its depth bits (4 B, carried by the tile sort)
             return 12.0 * i

@@ -434,8 +434,10 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         // positions of the emit: the Gaussians with tiles (*n_emit of them), compacted in index order
         const unsigned long long* n_emit = e->n_vis.p + 2;
         const int64_t* n_emit_i = reinterpret_cast<const int64_t*>(n_emit);
-        sxk::step_emit_compact(c, row_int ? e->tiles_o.p : e->tiles.p, e->blk_base.p, e->emit_list.p,
-                               index_first ? e->cum.p : nullptr, s, row_int);
+        // (index first, the compaction runs inside the emit's launch, below)
+        if (!index_first)
+            sxk::step_emit_compact(c, row_int ? e->tiles_o.p : e->tiles.p, e->blk_base.p, e->emit_list.p, nullptr, s,
+                                   row_int);
         const int32_t* order = e->emit_list.p;
         if (!index_first) {
             sxk::step_depth_keys(c, e->splats.p, e->emit_list.p, n_emit, e->dkey_a.p, e->order_a.p, s);
@@ -446,8 +448,8 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
             order = wd ? e->order_b.p : e->order_a.p;
             e->mark("depth_sort");
             sxk::scan_i32_i64(e->tiles.p, e->cum.p, c.count, e->scan_scratch.p, s, order, n_emit_i);
+            e->mark("scan");
         }
-        e->mark("scan");
         // index first: the emit also writes each entry's depth bits, into the upper half of keys_b (u64
         // words; the tile sort's keys and the large tiles' scratch use the lower half of each key buffer);
         // the tile sort carries them with the keys, between there and the upper half of keys_a
@@ -459,7 +461,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         if (c.tile_n_bits <= 16) {
             uint16_t* ka = reinterpret_cast<uint16_t*>(e->keys_a.p);
             uint16_t* kb = reinterpret_cast<uint16_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
+            if (index_first)
+                sxk::step_emit_compact_sorted(c, e->splats.p, e->radii.p, e->tiles.p, e->blk_base.p, e->emit_list.p,
+                                              e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
+            else
+                sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s,
+                                      edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);
@@ -468,7 +475,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         } else {
             uint32_t* ka = reinterpret_cast<uint32_t*>(e->keys_a.p);
             uint32_t* kb = reinterpret_cast<uint32_t*>(e->keys_b.p);
-            sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
+            if (index_first)
+                sxk::step_emit_compact_sorted(c, e->splats.p, e->radii.p, e->tiles.p, e->blk_base.p, e->emit_list.p,
+                                              e->cum.p, n_emit, ka, e->emit_gid.p, s, edepth);
+            else
+                sxk::step_emit_sorted(c, e->splats.p, e->radii.p, order, e->cum.p, n_emit, ka, e->emit_gid.p, s,
+                                      edepth);
             e->mark("emit");
             which = sxk::radix_sort_positions(ka, e->vals_a.p, kb, e->vals_b.p, n_host, c.tile_n_bits,
                                               e->sort_scratch.p, s, index_first, n_dev, edepth, edepth_b, true);

@@ -419,13 +419,20 @@ __device__ __forceinline__ sxd::F2 line_upper_cut(const sxd::AccuSweep& sw, int 
     return sxd::accutile_start(sw);
 }
 
-template <class K>
+// COMPACT (index order): the workgroup takes the 256 rows of preprocess block b instead of 256 emit
+// positions, and compacts them first as k_emit_compact does (tiles: the rows' tile counts, base: the block
+// scan's bases), writing the list and the offsets (list, cum_out) for the later kernels; a lane's
+// Gaussian is then its own row, its output range known without reading them back.
+template <class K, bool COMPACT>
 __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float4* __restrict__ splats,
                                                         const int32_t* __restrict__ radii,
                                                         const int32_t* __restrict__ order,
                                                         const int64_t* __restrict__ cum, K* __restrict__ keys,
                                                         int32_t* __restrict__ vals, uint32_t* __restrict__ edepth,
-                                                        const unsigned long long* __restrict__ n_pos) {
+                                                        const unsigned long long* __restrict__ n_pos,
+                                                        const int32_t* __restrict__ tiles,
+                                                        const unsigned long long* __restrict__ base,
+                                                        int32_t* __restrict__ list, int64_t* __restrict__ cum_out) {
     __shared__ EmitWave s_w[kBlock / 64];
     const int j = blockIdx.x * kBlock + threadIdx.x;
     const int lane = threadIdx.x & 63;
@@ -436,11 +443,50 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
     int g = 0, n_lines = 0;
     uint32_t dbits = 0;
     sxd::AccuSweep sw = {};
-    if (j < c.count && static_cast<unsigned long long>(j) < *n_pos) {
+    bool have = false;
+    if constexpr (COMPACT) {
+        __shared__ uint32_t s_n[kBlock / 64], s_t[kBlock / 64];
+        const int wave = threadIdx.x >> 6;
+        const uint32_t t = j < c.count ? static_cast<uint32_t>(tiles[j]) : 0u;
+        const unsigned long long bal = __ballot(t > 0u);
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
+        uint32_t incl = t;  // the block's tile counts are 32-bit (256 Gaussians x at most 2^23 tiles)
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), o, 64));
+            if (lane >= o) incl += y;
+        }
+        if (lane == 63) {
+            s_n[wave] = static_cast<uint32_t>(__popcll(bal));
+            s_t[wave] = incl;
+        }
+        __syncthreads();
+        uint32_t pn = 0, pt = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; w++)
+            if (w < wave) {
+                pn += s_n[w];
+                pt += s_t[w];
+            }
+        const unsigned long long jj = base[2 * (size_t)blockIdx.x + 1] + pn + rank;
+        if (t > 0u && jj < *n_pos) {  // (n_pos reads 0 after an overflow: nothing is written)
+            const int64_t end = static_cast<int64_t>(base[2 * (size_t)blockIdx.x] + pt + incl);
+            list[jj] = j;
+            cum_out[jj] = end;
+            my0 = end - t;
+            cnt = t;
+            g = j;
+            have = true;
+        }
+    } else if (j < c.count && static_cast<unsigned long long>(j) < *n_pos) {
         my0 = j == 0 ? 0 : cum[j - 1];
         cnt = cum[j] - my0;
+        g = cnt > 0 && order ? order[j] : j;
+        have = true;
+    }
+    if (have) {
         if (cnt > 0 && cnt <= kEmitLaneMax) {
-            g = order ? order[j] : j;
             const float4 s0 = splats[3 * (size_t)g];
             dbits = __float_as_uint(s0.w);
             int64_t cur = my0;
@@ -462,7 +508,6 @@ __global__ void __launch_bounds__(kBlock) k_emit_sorted(StepConst c, const float
                 for (int32_t y = r.min_y; y < r.max_y; y++) line(y, r.min_x, r.max_x, true);
             }
         } else if (cnt > 0) {
-            g = order ? order[j] : j;
             const float4 s0 = splats[3 * (size_t)g];
             dbits = __float_as_uint(s0.w);
             if (c.accutile) {
@@ -898,16 +943,40 @@ void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* r
                       const int64_t* cum, const unsigned long long* n_pos, uint16_t* keys, int32_t* vals,
                       hipStream_t s, uint32_t* edepth) {
     if (c.count <= 0) return;
-    hipLaunchKernelGGL(k_emit_sorted<uint16_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
-                       cum, keys, vals, edepth, n_pos);
+    hipLaunchKernelGGL((k_emit_sorted<uint16_t, false>), dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii,
+                       order, cum, keys, vals, edepth, n_pos, nullptr, nullptr, nullptr, nullptr);
 }
 
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
                       const int64_t* cum, const unsigned long long* n_pos, uint32_t* keys, int32_t* vals,
                       hipStream_t s, uint32_t* edepth) {
     if (c.count <= 0) return;
-    hipLaunchKernelGGL(k_emit_sorted<uint32_t>, dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii, order,
-                       cum, keys, vals, edepth, n_pos);
+    hipLaunchKernelGGL((k_emit_sorted<uint32_t, false>), dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii,
+                       order, cum, keys, vals, edepth, n_pos, nullptr, nullptr, nullptr, nullptr);
+}
+
+template <class K>
+static void launch_emit_compact_sorted(const StepConst& c, const float4* splats, const int32_t* radii,
+                                       const int32_t* tiles, const unsigned long long* block_base, int32_t* list,
+                                       int64_t* cum, const unsigned long long* n_pos, K* keys, int32_t* vals,
+                                       hipStream_t s, uint32_t* edepth) {
+    if (c.count <= 0) return;
+    hipLaunchKernelGGL((k_emit_sorted<K, true>), dim3(grid_for(c.count)), dim3(kBlock), 0, s, c, splats, radii,
+                       nullptr, nullptr, keys, vals, edepth, n_pos, tiles, block_base, list, cum);
+}
+
+void step_emit_compact_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* tiles,
+                              const unsigned long long* block_base, int32_t* list, int64_t* cum,
+                              const unsigned long long* n_pos, uint16_t* keys, int32_t* vals, hipStream_t s,
+                              uint32_t* edepth) {
+    launch_emit_compact_sorted(c, splats, radii, tiles, block_base, list, cum, n_pos, keys, vals, s, edepth);
+}
+
+void step_emit_compact_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* tiles,
+                              const unsigned long long* block_base, int32_t* list, int64_t* cum,
+                              const unsigned long long* n_pos, uint32_t* keys, int32_t* vals, hipStream_t s,
+                              uint32_t* edepth) {
+    launch_emit_compact_sorted(c, splats, radii, tiles, block_base, list, cum, n_pos, keys, vals, s, edepth);
 }
 
 // n (the count, or with n_dev its upper bound) picks the way: the pass up to 2^25 ids

@@ -91,6 +91,18 @@ void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* r
 void step_emit_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* order,
                       const int64_t* cum, const unsigned long long* n_pos, uint32_t* keys, int32_t* vals,
                       hipStream_t s, uint32_t* edepth = nullptr);
+// Index first in one launch: step_emit_compact (without row_int) and step_emit_sorted over its list
+// (order = the list): each workgroup compacts the 256 rows of one preprocess block, writes their list
+// entries and offsets (list, cum: for the gather) and emits their tile ids; *n_pos (the count of
+// Gaussians with tiles, 0 after an overflow) bounds the positions as in step_emit_sorted.
+void step_emit_compact_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* tiles,
+                              const unsigned long long* block_base, int32_t* list, int64_t* cum,
+                              const unsigned long long* n_pos, uint16_t* keys, int32_t* vals, hipStream_t s,
+                              uint32_t* edepth);
+void step_emit_compact_sorted(const StepConst& c, const float4* splats, const int32_t* radii, const int32_t* tiles,
+                              const unsigned long long* block_base, int32_t* list, int64_t* cum,
+                              const unsigned long long* n_pos, uint32_t* keys, int32_t* vals, hipStream_t s,
+                              uint32_t* edepth);
 // n_dev: the key count on the device, read instead of n
 void step_tile_offsets(const uint16_t* keys, int64_t n, int n_tiles, int32_t* offsets, hipStream_t s,
                        const int64_t* n_dev = nullptr);
