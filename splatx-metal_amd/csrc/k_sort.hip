@@ -1076,17 +1076,13 @@ __device__ __forceinline__ int32_t tie_run_end(const uint32_t* keys, int32_t i, 
 // of 7 waves per SIMD, which the LDS allows, keeps the register allocation of the tie work within it:
 // without it 75 VGPRs, 6 waves.)
 template <int RMAX>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7))) k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles,
-                                                              int32_t n_isects, const int64_t* __restrict__ n_dev,
-                                                              const int32_t* __restrict__ tile_order,
-                                                              int32_t* __restrict__ vals,
-                                                              const uint32_t* __restrict__ sdepth,
-                                                              uint32_t* __restrict__ sk0, uint32_t* __restrict__ sk1,
-                                                              int32_t* __restrict__ sv, int32_t* __restrict__ order_out,
-                                                              uint32_t* __restrict__ max_count,
-                                                              const int32_t* __restrict__ id_of,
-                                                              const int32_t* __restrict__ row_orig,
-                                                              const float4* __restrict__ splats) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(7)))
+k_tile_depth_sort(const int32_t* __restrict__ offsets, int n_tiles, int32_t n_isects, const int64_t* __restrict__ n_dev,
+                  const int32_t* __restrict__ tile_order, int32_t* __restrict__ vals,
+                  const uint32_t* __restrict__ sdepth, uint32_t* __restrict__ sk0, uint32_t* __restrict__ sk1,
+                  int32_t* __restrict__ sv, int32_t* __restrict__ order_out, uint32_t* __restrict__ max_count,
+                  const int32_t* __restrict__ id_of, const int32_t* __restrict__ row_orig,
+                  const float4* __restrict__ splats) {
     constexpr int kCap = kWaves * 64 * RMAX;
     __shared__ uint32_t s_key[kCap];
     __shared__ int32_t s_val[kCap];
