@@ -112,6 +112,39 @@ def test_spatial_order_index_first_ties(gpu, case):
     assert same_state(sa, sb), case
 
 
+def test_spatial_order_capacity_growth(gpu):
+    """Index first in spatial order through steps that overflow the intersection buffers (the step runs
+    again on grown buffers) and a step without any intersection: the same results as in the caller's
+    order."""
+    sc = scene.make_scene(n=60000, sh_degree=1, width=256, height=192, fx=200.0, seed=45,
+                          log_scale_mu=math.log(0.03), tie_frac=0.05)
+    away = scene.identity_view()
+    away[2, 3] = -20.0  # every mean behind the camera
+    views = [roty(30), away, roty(28), scene.identity_view(), roty(-5), roty(10)]
+    runs = []
+    for order in (sh.SXH_ROW_ORDER_ORIGINAL, sh.SXH_ROW_ORDER_SPATIAL):
+        print(f"capacity growth, row order {order}", flush=True)
+        ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=0.2,
+                                          isect_mode=sh.SXH_ISECT_ACCUTILE)
+        ex.set_row_order(order)
+        ex.set_isect_order(sh.SXH_ISECT_ORDER_INDEX_FIRST)
+        ex.upload_params(*scene.copy_state(sc), sc.n)
+        out = []
+        for vm in views:
+            r = ex.step(want_render=True, **dict(scene.step_kwargs(sc), viewmat=vm, gt_rgb=sc.gt))
+            out.append((r["loss"], r["n_isects"], r["render_colors"].copy()))
+        state = scene.copy_state(sc)
+        ex.download_params(*state, sc.n)
+        ex.close()
+        runs.append((out, state))
+    (oa, sa), (ob, sb) = runs
+    assert oa[1][1] == 0 and max(x[1] for x in oa) > (1 << 16) + (1 << 15)  # none, and past the first capacity
+    for k, (x, y) in enumerate(zip(oa, ob)):
+        assert x[:2] == y[:2], (k, x[:2], y[:2])
+        assert np.array_equal(x[2].view(np.uint32), y[2].view(np.uint32)), k
+    assert same_state(sa, sb)
+
+
 def test_spatial_order_through_exchanges(gpu, tmp_path):
     """Uploads, downloads, a checkpoint and a PLY export between steps (each restores the caller's
     order), a step over fewer rows, then steps again in spatial order."""
