@@ -145,6 +145,37 @@ def test_spatial_order_capacity_growth(gpu):
     assert same_state(sa, sb)
 
 
+def test_spatial_order_config3_steps(gpu):
+    """The headline workload (N = 1M, 1297x840, SH3, AccuTile, SSIM 0.2, jittered poses): five training
+    steps with the executor's default row order (spatial from the third step on, index first from the
+    second) and five in the caller's order give the same losses, counts, last render and arena, bit for
+    bit."""
+    sc, cfg = scene.config_scene(3)
+    rng = np.random.Generator(np.random.PCG64(7))
+    gt = rng.uniform(0.0, 1.0, (sc.height, sc.width, 3)).astype(np.float32)
+    views = [scene.jittered_view(rng) for _ in range(5)]
+    runs = []
+    for order in (sh.SXH_ROW_ORDER_ORIGINAL, sh.SXH_ROW_ORDER_SPATIAL_AUTO):
+        print(f"config 3, row order {order}", flush=True)
+        ex = gpu.make_train_step_executor(arena_rows=sc.n, sh_degree=sc.sh_degree, ssim_weight=cfg["ssim"],
+                                          isect_mode=sh.SXH_ISECT_ACCUTILE)
+        ex.set_row_order(order)
+        ex.upload_params(*scene.copy_state(sc), sc.n)
+        out = []
+        for k, vm in enumerate(views):
+            r = ex.step(want_render=k == len(views) - 1, gt_rgb=gt, **dict(scene.step_kwargs(sc), viewmat=vm))
+            out.append((r["loss"], r["n_isects"], r["n_visible"]))
+        render = r["render_colors"].copy()
+        state = scene.copy_state(sc)
+        ex.download_params(*state, sc.n)
+        ex.close()
+        runs.append((out, render, state))
+    (oa, ra, sa), (ob, rb, sb) = runs
+    assert oa == ob, (oa, ob)
+    assert np.array_equal(ra.view(np.uint32), rb.view(np.uint32))
+    assert same_state(sa, sb)
+
+
 def test_spatial_order_through_exchanges(gpu, tmp_path):
     """Uploads, downloads, a checkpoint and a PLY export between steps (each restores the caller's
     order), a step over fewer rows, then steps again in spatial order."""
