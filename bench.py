@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 
 
 def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, shape: dict) -> float:
-    """Minimum HBM bytes one launch of `name` must move (per-unit figures stated in DESIGN.md). shape:
+    """Minimum HBM bytes one launch of `name` must move (the per-unit figures of each case below). shape:
     index_first (the step's intersection order: emit in index order, then per-tile depth sorts; else
     depth first), depth_passes / tile_passes (radix passes of the depth sort over the Gaussians with tiles
     and of the tile sort over the i intersections) and key_b (bytes of a tile id: 2 up to 2^16 tiles,
@@ -65,11 +65,11 @@ def algorithmic_bytes(name: str, n: int, v: int, i: int, px: int, sh_k: int, sha
         # preprocess reads nothing again
         return algorithmic_bytes("postprocess", n, v, i, px, sh_k, shape) + 12.0 * n + 48.0 * v
     if name == "raster_fwd":
-        # the survey's per-unit figures: 40 B read per intersection (its sorted id and the splat's record),
+        # the measurement plan's per-unit figures: 40 B read per intersection (its sorted id and the splat's record),
         # 20 B written per pixel (colour, alpha, last id)
         return i * 40.0 + px * 20.0
     if name == "raster_bwd":
-        # the survey's per-unit figures: 40 B read and 36 B of gradient sums scattered per intersection,
+        # the measurement plan's per-unit figures: 40 B read and 36 B of gradient sums scattered per intersection,
         # 20 B read per pixel (alpha, last id, v_render)
         return i * (40.0 + 36.0) + px * 20.0
     if name == "gather":
