@@ -574,8 +574,12 @@ void sxh_detail::run_step(sxh_executor* e, const sxh_step_inputs* in, sxh_step_o
         // config 5); either way the same sums
         constexpr int64_t kInlineLongMax = 1024;
         const bool inline_long = e->last_long >= 0 && e->last_long <= kInlineLongMax;
+        // 32 positions per wave where the emit order puts Gaussians of one size together (the rows in
+        // spatial order, or the depth order): its waves of large Gaussians take half the staging rounds
+        // (config 3 in spatial order 43.6 -> 34.7 us); 64 in the caller's order (33.9 against 39.1 us)
+        const int gather_positions = (e->permuted || !index_first) ? 32 : 64;
         sxk::raster_gather_grads(c.count, order, e->cum.p, e->part.p, e->stamp.p, e->touched.p, e->grads.p,
-                                 e->long_list.p, e->long_count.p, s, n_emit_i, inline_long, &loss);
+                                 e->long_list.p, e->long_count.p, s, n_emit_i, inline_long, &loss, gather_positions);
         e->mark("gather");
         // (the step's parameter update waits for the next step's preprocess, or a flush)
     };

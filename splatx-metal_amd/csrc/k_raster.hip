@@ -938,10 +938,11 @@ __device__ __forceinline__ void reduce_long_range(const float* __restrict__ part
     }
 }
 
-constexpr int kGatherWave = 64;    // emit positions per gather workgroup (one wave)
+constexpr int kGatherWave = 64;    // lanes of a gather workgroup (one wave)
 constexpr int kGatherStage = 256;  // entries staged in LDS per round
 
-// One wave per 64 consecutive positions j of the emit order, for Gaussian order[j]: the sums of its
+// One wave per `npos` (32 or 64) consecutive positions j of the emit order, for Gaussian order[j] (lane l
+// takes position l; lanes past npos only stage entries): the sums of its
 // (tile, Gaussian) entries, which the emit placed at [cum[j-1], cum[j]), in emit order (its tiles in
 // the order the intersection emit visits them), into its gradient record {v_x, v_y, v_opacity, 0 |
 // v_conic a, b, c, 0 | v_r, v_g, v_b, 0}. The wave's ranges lie back to back in `part`, so the wave
@@ -964,20 +965,20 @@ __global__ void __launch_bounds__(kGatherWave) k_gather_grads(int count, const i
                                                               int32_t* __restrict__ long_list,
                                                               int32_t* __restrict__ long_count,
                                                               const int64_t* __restrict__ count_dev,
-                                                              int inline_long, StepLoss L) {
+                                                              int inline_long, int npos, StepLoss L) {
     // the first workgroup (one wave) also reduces the step's loss, before its ranges (L.out null: none)
     if (L.out && blockIdx.x == 0) loss_final_wave(L);
     __shared__ float s_rec[kGatherStage][kPartFloats];  // odd row stride: lanes on different rows, different banks
     __shared__ int32_t s_off[kGatherWave];              // each lane's first staged entry
     __shared__ int32_t s_src[kGatherWave];              // each lane's first entry in `part`
     const int lane = threadIdx.x;
-    const int j = blockIdx.x * kGatherWave + lane;
+    const int j = blockIdx.x * npos + lane;
     const int n_pos = count_dev ? static_cast<int>(*count_dev) : count;
     const uint32_t stamp = *stamp_p;
     int32_t p0 = 0, p1 = 0, n = 0;
     int g = 0;
     bool is_long = false;
-    if (j < n_pos) {
+    if (lane < npos && j < n_pos) {
         p1 = static_cast<int32_t>(cum[j]);
         p0 = j > 0 ? static_cast<int32_t>(cum[j - 1]) : 0;
         g = order ? order[j] : j;
@@ -1086,11 +1087,14 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part, const uint32_t* stamp,
                          const uint8_t* touched, float4* grads, int32_t* long_list, int32_t* long_count,
-                         hipStream_t s, const int64_t* count_dev, bool inline_long, const StepLoss* loss) {
+                         hipStream_t s, const int64_t* count_dev, bool inline_long, const StepLoss* loss,
+                         int positions_per_wave) {
     if (count <= 0) return;
-    hipLaunchKernelGGL(k_gather_grads, dim3((count + kGatherWave - 1) / kGatherWave), dim3(kGatherWave), 0, s, count,
-                       order, cum, part, stamp, touched, grads, long_list, long_count, count_dev,
-                       inline_long ? 1 : 0, loss ? *loss : StepLoss{});
+    if (positions_per_wave != 32 && positions_per_wave != 64)
+        throw std::invalid_argument("raster_gather_grads: positions_per_wave must be 32 or 64");
+    hipLaunchKernelGGL(k_gather_grads, dim3((count + positions_per_wave - 1) / positions_per_wave), dim3(kGatherWave),
+                       0, s, count, order, cum, part, stamp, touched, grads, long_list, long_count, count_dev,
+                       inline_long ? 1 : 0, positions_per_wave, loss ? *loss : StepLoss{});
     if (!inline_long)
         hipLaunchKernelGGL(k_gather_long, dim3(1024), dim3(kThreads), 0, s, order, cum, part, stamp, grads,
                            long_list, long_count);

@@ -225,11 +225,15 @@ void raster_bwd_begin(uint32_t* stamp, uint8_t* touched, int rows, int32_t* long
 // instead of queueing them for a second launch (same sums; fast while they are few).
 // loss (optional): the training step's loss, reduced by the gather's first workgroup (one wave) before
 // its own ranges, and the step's host words (see StepLoss)
+// positions_per_wave (32 or 64): the positions each one-wave workgroup takes; every lane stages entries,
+// the first positions_per_wave lanes own a position each. 32 halves the rounds of the waves whose
+// positions hold many entries (Gaussians of one size sit together when the rows are in spatial order);
+// the sums are the same either way.
 struct StepLoss;
 void raster_gather_grads(int count, const int32_t* order, const int64_t* cum, const float* part,
                          const uint32_t* stamp, const uint8_t* touched, float4* grads, int32_t* long_list,
                          int32_t* long_count, hipStream_t s, const int64_t* count_dev = nullptr,
-                         bool inline_long = false, const StepLoss* loss = nullptr);
+                         bool inline_long = false, const StepLoss* loss = nullptr, int positions_per_wave = 64);
 void raster_bwd(const RasterArgs& a, const float* render_alphas, const int32_t* last_ids,
                 const float* v_render_colors, const float* v_render_alphas, const RasterBwdGrads& g,
                 hipStream_t s);
