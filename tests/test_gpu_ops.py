@@ -175,8 +175,9 @@ def _run_keys(n, key_bits, seed):
 
 # Keys laid out in runs (an emit's tile ids along a row, repeated keys): the digit counts add a thread's
 # runs of equal digits at once, and the passes see runs of consecutive digits wrapping past the last
-# digit, for digit ranges from 16 (the last pass of 36 bits) to 256.
-@pytest.mark.parametrize("n,bits", [(1_048_577, 13), (1_048_576, 36), (2_000_003, 45), (1_100_000, 64)])
+# digit, for digit ranges from 16 (the first pass of 9 bits: 4 + 5) to 256.
+@pytest.mark.parametrize("n,bits", [(1_048_577, 9), (1_048_577, 13), (1_048_576, 36), (2_000_003, 45),
+                                    (1_100_000, 64)])
 def test_sort_reduce_then_scan_runs(gpu, n, bits):
     keys, vals = _run_keys(n, bits, seed=n + bits)
     ks, vs = gpu.sort_isect(keys, vals, bits)
